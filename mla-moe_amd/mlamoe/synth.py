@@ -1,0 +1,79 @@
+"""Seeded synthetic inputs for the mla-moe hot path (DeepSeek-V2-Lite shapes).
+
+Weights are bf16 stored as uint16, produced from float32 N(0, std) samples by
+truncation, which is the reference's own fp32 -> bf16 rule (include/tensor.h:16-20).
+Activations are float32 N(0, 1).  The generator is numpy's PCG64
+`default_rng(seed)`, so host-side inputs are identical on every machine that
+runs this image.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# DeepSeek-V2-Lite MoE / MLA geometry.
+DSV2 = dict(H=2048, E=64, K=6, I=1408, n_shared=2, NH=16, QKN=128, QKR=64, KVL=512, VHD=128)
+
+
+def bf16_from_f32(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 by truncation (include/tensor.h:16-20)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return (a.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(u: np.ndarray) -> np.ndarray:
+    """bf16 -> fp32 by a 16-bit shift (include/tensor.h:9-14)."""
+    u = np.ascontiguousarray(u, dtype=np.uint16)
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def normal_f32(rng: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
+    x = rng.standard_normal(size=shape, dtype=np.float32)
+    if std != 1.0:
+        x *= np.float32(std)
+    return x
+
+
+def normal_bf16(rng: np.random.Generator, shape, std: float = 0.02) -> np.ndarray:
+    return bf16_from_f32(normal_f32(rng, shape, std))
+
+
+def moe_layer(seed: int, H: int, E: int, I: int, n_shared: int, std: float = 0.02,
+              gate_bias: bool = False) -> dict:
+    """One MoE layer's bf16 weights: router [E,H], experts gate/up [E,I,H],
+    down [E,H,I], shared gate/up [S,H], down [H,S] with S = n_shared*I."""
+    rng = np.random.default_rng(seed)
+    S = n_shared * I
+    w = dict(
+        moe_gate=normal_bf16(rng, (E, H), std),
+        eg=normal_bf16(rng, (E, I, H), std),
+        eu=normal_bf16(rng, (E, I, H), std),
+        ed=normal_bf16(rng, (E, H, I), std),
+        sg=normal_bf16(rng, (S, H), std),
+        su=normal_bf16(rng, (S, H), std),
+        sd=normal_bf16(rng, (H, S), std),
+    )
+    w["moe_gate_bias"] = normal_f32(rng, (E,), 0.1) if gate_bias else None
+    return w
+
+
+def activations(seed: int, T: int, H: int) -> np.ndarray:
+    return normal_f32(np.random.default_rng(seed), (T, H))
+
+
+def zipf_prior(seed: int, E: int, s: float = 1.1) -> np.ndarray:
+    """Per-expert logit prior z_e = -s * ln(1 + pi(e)), pi a seeded permutation:
+    expert pi^-1(r) gets the prior of Zipf rank r+1, which skews the load."""
+    perm = np.random.default_rng(seed).permutation(E)
+    return (-np.float64(s) * np.log1p(perm.astype(np.float64))).astype(np.float32)
+
+
+def uniform_logits(seed: int, T: int, E: int) -> np.ndarray:
+    return np.random.default_rng(seed).random((T, E), dtype=np.float32)
+
+
+def checksum_u16(a: np.ndarray) -> int:
+    """Order-sensitive 64-bit checksum of a uint16 array, used to assert that a
+    regenerated weight tensor equals the one a golden vector was made from."""
+    v = np.ascontiguousarray(a, dtype=np.uint16).ravel().astype(np.uint64)
+    pos = np.arange(v.size, dtype=np.uint64)
+    return int((v * (pos % np.uint64(65521) + np.uint64(1))).sum(dtype=np.uint64))

@@ -1,0 +1,324 @@
+"""ctypes bindings for the CPU oracle (liboracle.so) and, where it is built,
+the reference's own compiled hot path (_ref/libref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.  The
+product library never loads it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libref.so")
+
+_f32p = C.POINTER(C.c_float)
+_u16p = C.POINTER(C.c_uint16)
+_i8p = C.POINTER(C.c_int8)
+_i32p = C.POINTER(C.c_int32)
+_ip = C.POINTER(C.c_int)
+
+
+def build(ref: bool = False) -> None:
+    """Compile liboracle.so (and _ref/libref.so when `ref` and the reference
+    tree exists)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    if ref and os.path.isdir("/root/reference/src"):
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+def _p(a, t):
+    if a is None:
+        return None
+    return a.ctypes.data_as(t)
+
+
+class MoeCfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_routed_experts", C.c_int),
+                ("n_shared_experts", C.c_int), ("n_experts_per_tok", C.c_int),
+                ("moe_inter_size", C.c_int), ("router_sigmoid", C.c_int),
+                ("norm_topk", C.c_int), ("routed_scaling", C.c_float)]
+
+
+class MoeWeights(C.Structure):
+    _fields_ = [("moe_gate", _u16p), ("moe_gate_bias", _f32p), ("eg", _u16p),
+                ("eu", _u16p), ("ed", _u16p), ("sg", _u16p), ("su", _u16p),
+                ("sd", _u16p)]
+
+
+class MoeI8Weights(C.Structure):
+    _fields_ = [("qg", _i8p), ("qu", _i8p), ("sg", _f32p), ("su", _f32p),
+                ("qd", _i8p), ("sd", _f32p), ("qsg", _i8p), ("qsu", _i8p),
+                ("ssg", _f32p), ("ssu", _f32p), ("qsd", _i8p), ("ssd", _f32p)]
+
+
+class I8Debug(C.Structure):
+    _fields_ = [("qx", _i8p), ("sx", _f32p), ("acc_gu", _i32p), ("qh", _i8p),
+                ("sh", _f32p), ("acc_d", _i32p), ("qhs", _i8p), ("shs", _f32p)]
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.or_bf16_to_f32.restype = C.c_float
+        L.or_bf16_to_f32.argtypes = [C.c_uint16]
+        L.or_f32_to_bf16.restype = C.c_uint16
+        L.or_f32_to_bf16.argtypes = [C.c_float]
+        L.or_silu.restype = C.c_float
+        L.or_silu.argtypes = [C.c_float]
+        L.or_matmul.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_int]
+        L.or_matmul_rows.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_int, C.c_int]
+        L.or_swiglu.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, C.c_int, C.c_int,
+                                _f32p, _f32p]
+        L.or_softmax.argtypes = [_f32p, C.c_int]
+        L.or_route.argtypes = [C.POINTER(MoeCfg), _f32p, _f32p, _ip, _f32p]
+        L.or_ffn_compute.argtypes = [C.POINTER(MoeCfg), C.POINTER(MoeWeights), _f32p,
+                                     _f32p, _ip, _f32p, _f32p]
+        L.or_ffn_compute_rows.argtypes = [C.POINTER(MoeCfg), C.POINTER(MoeWeights),
+                                          C.c_int, _f32p, _f32p, _f32p, _ip, _f32p, _f32p]
+        L.or_quant_row_i8.argtypes = [_f32p, C.c_int, _i8p, _f32p]
+        L.or_quant_rows_i8.argtypes = [_f32p, C.c_int, C.c_int, _i8p, _f32p]
+        L.or_quant_weight_i8.argtypes = [_u16p, C.c_int, C.c_int, _i8p, _f32p]
+        L.or_gemm_i8.argtypes = [_i8p, _i8p, _i32p, C.c_int, C.c_int, C.c_int]
+        L.or_dequant_row.argtypes = [_i32p, C.c_float, _f32p, C.c_int, _f32p]
+        L.or_ffn_i8.argtypes = [C.POINTER(MoeCfg), _u16p, _f32p, C.POINTER(MoeI8Weights),
+                                C.c_int, _f32p, _f32p, _f32p, _ip, _f32p, _f32p,
+                                C.POINTER(I8Debug)]
+        L.or_absorbed_head.argtypes = [_f32p, _f32p, _u16p, _u16p, _f32p, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_int, C.c_float, _f32p, _f32p,
+                                       _f32p, _f32p]
+        L.or_absorbed_decode.argtypes = [_f32p, _u16p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                         C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.c_float, _f32p, _f32p, _f32p, _f32p]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    """The reference's own compiled run.c (only in the build container)."""
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        R.ref_matmul.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_int]
+        R.ref_silu.restype = C.c_float
+        R.ref_silu.argtypes = [C.c_float]
+        R.ref_softmax.argtypes = [_f32p, C.c_int]
+        R.ref_swiglu.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, C.c_int, C.c_int,
+                                 _f32p, _f32p]
+        R.ref_ffn_compute.argtypes = [C.c_int] * 7 + [C.c_float] + [_u16p, _f32p] + \
+            [_u16p] * 6 + [_f32p, _f32p, _ip, _f32p, _f32p]
+        R.ref_absorbed_decode.restype = C.c_int
+        R.ref_absorbed_decode.argtypes = [C.c_int] * 9 + [C.c_float, _f32p] + [_u16p] * 13 + \
+            [_f32p, C.c_char_p, _f32p]
+        _ref = R
+    return _ref
+
+
+# ---------------------------------------------------------------------------
+# numpy-level helpers
+# ---------------------------------------------------------------------------
+
+def c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def matmul(x, w):
+    """run.c:30 matmul for each row of x ([T, n_in] or [n_in]); w bf16 [d_out, n_in]."""
+    x = c32(x)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    d_out, n_in = w.shape
+    x2 = x.reshape(-1, n_in)
+    y = np.empty((x2.shape[0], d_out), np.float32)
+    lib().or_matmul_rows(_p(y, _f32p), _p(x2, _f32p), _p(w, _u16p), x2.shape[0], d_out, n_in)
+    return y.reshape(x.shape[:-1] + (d_out,))
+
+
+def softmax(x):
+    x = c32(x).copy()
+    lib().or_softmax(_p(x, _f32p), x.size)
+    return x
+
+
+def moe_cfg(H, E, n_shared, K, I, router_sigmoid=0, norm_topk=0, routed_scaling=1.0):
+    return MoeCfg(H, E, n_shared, K, I, router_sigmoid, norm_topk, routed_scaling)
+
+
+def _weights_struct(w):
+    return MoeWeights(_p(w["moe_gate"], _u16p), _p(w.get("moe_gate_bias"), _f32p),
+                      _p(w["eg"], _u16p), _p(w["eu"], _u16p), _p(w["ed"], _u16p),
+                      _p(w["sg"], _u16p), _p(w["su"], _u16p), _p(w["sd"], _u16p))
+
+
+def route(cfg, logits, bias=None):
+    """Router on one token's logits; returns (probs, idx, w)."""
+    s = c32(logits).copy()
+    K = cfg.n_experts_per_tok
+    idx = np.empty(K, np.int32)
+    w = np.empty(K, np.float32)
+    lib().or_route(C.byref(cfg), _p(s, _f32p), _p(c32(bias) if bias is not None else None, _f32p),
+                   _p(idx, _ip), _p(w, _f32p))
+    return s, idx, w
+
+
+def ffn_compute_rows(cfg, w, xn, logits=None):
+    """T tokens through the reference MoE FFN; returns out, idx, w, probs."""
+    xn = c32(xn)
+    T = xn.shape[0]
+    H, E, K = cfg.hidden, cfg.n_routed_experts, cfg.n_experts_per_tok
+    out = np.empty((T, H), np.float32)
+    idx = np.empty((T, K), np.int32)
+    wt = np.empty((T, K), np.float32)
+    probs = np.empty((T, E), np.float32)
+    ws = _weights_struct(w)
+    lg = c32(logits) if logits is not None else None
+    lib().or_ffn_compute_rows(C.byref(cfg), C.byref(ws), T, _p(xn, _f32p), _p(lg, _f32p),
+                              _p(out, _f32p), _p(idx, _ip), _p(wt, _f32p), _p(probs, _f32p))
+    return out, idx, wt, probs
+
+
+def quant_rows(x):
+    x = c32(x)
+    rows, n = x.reshape(-1, x.shape[-1]).shape
+    q = np.empty((rows, n), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().or_quant_rows_i8(_p(x, _f32p), rows, n, _p(q, _i8p), _p(s, _f32p))
+    return q, s
+
+
+def quant_weight(w):
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    N, K = w.shape[-2], w.shape[-1]
+    rows = w.size // K
+    q = np.empty(w.shape, np.int8)
+    s = np.empty(w.shape[:-1], np.float32)
+    lib().or_quant_weight_i8(_p(w, _u16p), rows, K, _p(q, _i8p), _p(s, _f32p))
+    return q, s
+
+
+def gemm_i8(a, b):
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    M, K = a.shape
+    N = b.shape[0]
+    c = np.empty((M, N), np.int32)
+    lib().or_gemm_i8(_p(a, _i8p), _p(b, _i8p), _p(c, _i32p), M, N, K)
+    return c
+
+
+def quantize_moe_weights(w):
+    """Per-output-channel int8 quantisation of every expert matrix."""
+    q = {}
+    for k in ("eg", "eu", "ed", "sg", "su", "sd"):
+        q["q" + k], q["s" + k] = quant_weight(w[k])
+    return q
+
+
+def ffn_i8(cfg, w, qw, xn, logits=None, debug=False):
+    """T tokens through the int8 MoE layer (or_ffn_i8)."""
+    xn = c32(xn)
+    T = xn.shape[0]
+    H, E, K, I = cfg.hidden, cfg.n_routed_experts, cfg.n_experts_per_tok, cfg.moe_inter_size
+    S = cfg.n_shared_experts * I
+    out = np.empty((T, H), np.float32)
+    idx = np.empty((T, K), np.int32)
+    wt = np.empty((T, K), np.float32)
+    probs = np.empty((T, E), np.float32)
+    ws = MoeI8Weights(_p(qw["qeg"], _i8p), _p(qw["qeu"], _i8p), _p(qw["seg"], _f32p),
+                      _p(qw["seu"], _f32p), _p(qw["qed"], _i8p), _p(qw["sed"], _f32p),
+                      _p(qw["qsg"], _i8p), _p(qw["qsu"], _i8p), _p(qw["ssg"], _f32p),
+                      _p(qw["ssu"], _f32p), _p(qw["qsd"], _i8p), _p(qw["ssd"], _f32p))
+    dbg = None
+    d = {}
+    if debug:
+        d = dict(qx=np.empty((T, H), np.int8), sx=np.empty(T, np.float32),
+                 acc_gu=np.empty((T, K, 2, I), np.int32), qh=np.empty((T, K, I), np.int8),
+                 sh=np.empty((T, K), np.float32), acc_d=np.empty((T, K, H), np.int32),
+                 qhs=np.empty((T, max(S, 1)), np.int8), shs=np.empty(T, np.float32))
+        dbg = I8Debug(_p(d["qx"], _i8p), _p(d["sx"], _f32p), _p(d["acc_gu"], _i32p),
+                      _p(d["qh"], _i8p), _p(d["sh"], _f32p), _p(d["acc_d"], _i32p),
+                      _p(d["qhs"], _i8p), _p(d["shs"], _f32p))
+    lg = c32(logits) if logits is not None else None
+    bias = w.get("moe_gate_bias")
+    lib().or_ffn_i8(C.byref(cfg), _p(w["moe_gate"], _u16p),
+                    _p(c32(bias) if bias is not None else None, _f32p), C.byref(ws), T,
+                    _p(xn, _f32p), _p(lg, _f32p), _p(out, _f32p), _p(idx, _ip),
+                    _p(wt, _f32p), _p(probs, _f32p), C.byref(dbg) if dbg else None)
+    return out, idx, wt, probs, d
+
+
+def absorbed_decode(q, kv_b, cache, kv_len, NH, QKN, QKR, KVL, VHD, scale=None,
+                    seq_stride=None):
+    """B sequences x NH heads of the absorbed chain.  cache: [B, L, KVL+QKR]
+    uint16 (bf16) or float32.  Returns ctx, qabs, probs, clat."""
+    q = c32(q)
+    B = q.shape[0]
+    kv_b = np.ascontiguousarray(kv_b, dtype=np.uint16)
+    is_bf16 = cache.dtype == np.uint16
+    cache = np.ascontiguousarray(cache)
+    L = cache.shape[1] if seq_stride is None else seq_stride
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(QKN + QKR)))
+    ctx = np.empty((B, NH * VHD), np.float32)
+    qabs = np.empty((B, NH, KVL), np.float32)
+    probs = np.empty((B, NH, kv_len), np.float32)
+    clat = np.empty((B, NH, KVL), np.float32)
+    lib().or_absorbed_decode(_p(q, _f32p), _p(kv_b, _u16p), cache.ctypes.data_as(C.c_void_p),
+                             int(is_bf16), B, NH, QKN, QKR, KVL, VHD, kv_len, L,
+                             C.c_float(scale), _p(ctx, _f32p), _p(qabs, _f32p),
+                             _p(probs, _f32p), _p(clat, _f32p))
+    return ctx, qabs, probs, clat
+
+
+# ---------------------------------------------------------------------------
+# reference-library helpers (build container only)
+# ---------------------------------------------------------------------------
+
+def ref_matmul(x, w):
+    x = c32(x)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    d_out, n_in = w.shape
+    y = np.empty(d_out, np.float32)
+    ref().ref_matmul(_p(y, _f32p), _p(x, _f32p), _p(w, _u16p), d_out, n_in)
+    return y
+
+
+def ref_softmax(x):
+    x = c32(x).copy()
+    ref().ref_softmax(_p(x, _f32p), x.size)
+    return x
+
+
+def ref_ffn_compute(cfg, w, xn):
+    """One token through the reference's own ffn_compute."""
+    xn = c32(xn)
+    H, E, K = cfg.hidden, cfg.n_routed_experts, cfg.n_experts_per_tok
+    out = np.empty(H, np.float32)
+    idx = np.empty(K, np.int32)
+    wt = np.empty(K, np.float32)
+    probs = np.empty(E, np.float32)
+    bias = w.get("moe_gate_bias")
+    ref().ref_ffn_compute(cfg.hidden, E, cfg.n_shared_experts, K, cfg.moe_inter_size,
+                          cfg.router_sigmoid, cfg.norm_topk, C.c_float(cfg.routed_scaling),
+                          _p(w["moe_gate"], _u16p),
+                          _p(c32(bias) if bias is not None else None, _f32p),
+                          _p(w["eg"], _u16p), _p(w["eu"], _u16p), _p(w["ed"], _u16p),
+                          _p(w["sg"], _u16p), _p(w["su"], _u16p), _p(w["sd"], _u16p),
+                          _p(xn, _f32p), _p(out, _f32p), _p(idx, _ip), _p(wt, _f32p),
+                          _p(probs, _f32p))
+    return out, idx, wt, probs

@@ -1,0 +1,195 @@
+"""Write the golden vectors under tests/golden/ from the reference's own code.
+
+Runs only in the build container, where /root/reference exists: it calls the
+reference's src/run.c compiled from its own sources into oracle/_ref/libref.so
+(`make -C oracle ref`) and stores inputs and outputs as .npz fixtures
+(numpy, no pickles).  Large weight tensors are not stored; they are
+regenerated from the recorded seed with mlamoe.synth, and a checksum of each
+regenerated tensor is stored so a test can prove it rebuilt the same bytes.
+
+    python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import sys
+import tempfile
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.join(ROOT, "mla-moe_amd"))
+
+import pyoracle as O  # noqa: E402
+from mlamoe import synth  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _p(a, t):
+    return None if a is None else a.ctypes.data_as(t)
+
+
+def gen_matmul():
+    rng = np.random.default_rng(101)
+    d = {}
+    for name, (d_out, n_in) in dict(tiny=(7, 13), odd=(5, 129)).items():
+        x = synth.normal_f32(rng, (n_in,))
+        w = synth.normal_bf16(rng, (d_out, n_in), 0.02)
+        d[f"{name}_x"], d[f"{name}_w"], d[f"{name}_y"] = x, w, O.ref_matmul(x, w)
+    # router-shaped [64, 2048] and expert-shaped [1408, 2048], by seed
+    for name, (seed, d_out, n_in) in dict(router=(102, 64, 2048),
+                                          expert=(103, 1408, 2048)).items():
+        r = np.random.default_rng(seed)
+        w = synth.normal_bf16(r, (d_out, n_in), 0.02)
+        x = synth.normal_f32(r, (n_in,))
+        d[f"{name}_seed"] = np.int64(seed)
+        d[f"{name}_shape"] = np.array([d_out, n_in], np.int64)
+        d[f"{name}_wsum"] = np.uint64(synth.checksum_u16(w))
+        d[f"{name}_y"] = O.ref_matmul(x, w)
+    np.savez_compressed(os.path.join(OUT, "matmul.npz"), **d)
+
+
+def gen_softmax_silu():
+    rng = np.random.default_rng(201)
+    d = {}
+    cases = {
+        "router": synth.normal_f32(rng, (64,)),
+        "ctx": synth.normal_f32(rng, (4096,), 3.0),
+        "masked": np.where(rng.random(33) < 0.3, -np.inf, synth.normal_f32(rng, (33,))),
+        "equal": np.full(64, 0.25, np.float32),
+    }
+    for k, v in cases.items():
+        v = v.astype(np.float32)
+        d[f"softmax_{k}_in"] = v
+        d[f"softmax_{k}_out"] = O.ref_softmax(v)
+    xs = np.concatenate([synth.normal_f32(rng, (256,), 4.0),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 87.0, -87.0,
+                                   100.0, -100.0], np.float32)]).astype(np.float32)
+    d["silu_in"] = xs
+    d["silu_out"] = np.array([O.ref().ref_silu(C.c_float(float(v))) for v in xs], np.float32)
+    np.savez_compressed(os.path.join(OUT, "softmax_silu.npz"), **d)
+
+
+def gen_ffn_tiny():
+    """ffn_compute on tiny layers, three router flavours, 5 tokens each."""
+    H, E, K, I, NS, T = 64, 8, 3, 24, 2, 5
+    d = {}
+    flavours = {
+        "dsv2": dict(sig=0, norm=0, scale=1.0, bias=False, zero_gate=False),
+        "glm": dict(sig=1, norm=1, scale=1.8, bias=True, zero_gate=False),
+        "tie": dict(sig=0, norm=0, scale=1.0, bias=False, zero_gate=True),
+    }
+    for i, (name, f) in enumerate(flavours.items()):
+        w = synth.moe_layer(300 + i, H, E, I, NS, gate_bias=f["bias"])
+        if f["zero_gate"]:
+            w["moe_gate"] = np.zeros_like(w["moe_gate"])
+        x = synth.activations(310 + i, T, H)
+        cfg = O.moe_cfg(H, E, NS, K, I, f["sig"], f["norm"], f["scale"])
+        outs = [O.ref_ffn_compute(cfg, w, x[t]) for t in range(T)]
+        for k in ("moe_gate", "eg", "eu", "ed", "sg", "su", "sd"):
+            d[f"{name}_{k}"] = w[k]
+        if w["moe_gate_bias"] is not None:
+            d[f"{name}_bias"] = w["moe_gate_bias"]
+        d[f"{name}_cfg"] = np.array([H, E, NS, K, I, f["sig"], f["norm"]], np.int64)
+        d[f"{name}_scale"] = np.float32(f["scale"])
+        d[f"{name}_x"] = x
+        d[f"{name}_out"] = np.stack([o[0] for o in outs])
+        d[f"{name}_idx"] = np.stack([o[1] for o in outs])
+        d[f"{name}_w"] = np.stack([o[2] for o in outs])
+        d[f"{name}_probs"] = np.stack([o[3] for o in outs])
+    np.savez_compressed(os.path.join(OUT, "ffn_tiny.npz"), **d)
+
+
+def gen_ffn_dsv2():
+    """One DeepSeek-V2-Lite-shaped MoE layer (config 1), two tokens, by seed."""
+    g = synth.DSV2
+    seed, xseed, T = 401, 402, 2
+    w = synth.moe_layer(seed, g["H"], g["E"], g["I"], g["n_shared"])
+    x = synth.activations(xseed, T, g["H"])
+    cfg = O.moe_cfg(g["H"], g["E"], g["n_shared"], g["K"], g["I"])
+    outs = [O.ref_ffn_compute(cfg, w, x[t]) for t in range(T)]
+    d = dict(seed=np.int64(seed), xseed=np.int64(xseed), T=np.int64(T),
+             out=np.stack([o[0] for o in outs]), idx=np.stack([o[1] for o in outs]),
+             w=np.stack([o[2] for o in outs]), probs=np.stack([o[3] for o in outs]))
+    for k in ("moe_gate", "eg", "eu", "ed", "sg", "su", "sd"):
+        d[f"sum_{k}"] = np.uint64(synth.checksum_u16(w[k]))
+    np.savez_compressed(os.path.join(OUT, "ffn_dsv2.npz"), **d)
+
+
+def _absorbed_case(name, NH, QKN, QKR, KVL, VHD, pos, seed, store_kvb):
+    H = NH * VHD                    # so that an identity o_proj returns ctx exactly
+    KVD, QHD = KVL + QKR, QKN + QKR
+    DI, V = 4, 2
+    r = np.random.default_rng(seed)
+    kv_b = synth.normal_bf16(np.random.default_rng(seed + 1), (NH * (QKN + VHD), KVL), 0.02)
+    one = np.uint16(0x3F80)                                      # bf16 1.0
+    embed = synth.normal_bf16(r, (V, H), 1.0)
+    in_norm = np.full(H, one, np.uint16)
+    q_proj = synth.normal_bf16(r, (NH * QHD, H), 0.02)
+    kv_a = synth.normal_bf16(r, (KVD, H), 0.02)
+    kv_a_norm = np.full(KVL, one, np.uint16)
+    o_proj = np.zeros((H, NH * VHD), np.uint16)
+    o_proj[np.arange(H), np.arange(H)] = one
+    post_norm = np.full(H, one, np.uint16)
+    dg = synth.normal_bf16(r, (DI, H), 0.02)
+    du = synth.normal_bf16(r, (DI, H), 0.02)
+    dd = synth.normal_bf16(r, (H, DI), 0.02)
+    final_norm = np.full(H, one, np.uint16)
+    lm_head = synth.normal_bf16(r, (V, H), 0.02)
+    # earlier cache rows: bf16-representable values, as a bf16 cache would hold
+    cache_in = synth.bf16_to_f32(synth.normal_bf16(r, (pos, KVD), 1.0))
+    inv_freq = (1.0 / (10000.0 ** (np.arange(0, QKR, 2, dtype=np.float64) / QKR))).astype(np.float32)
+    q = np.empty(NH * QHD, np.float32)
+    f32p, u16p = C.POINTER(C.c_float), C.POINTER(C.c_uint16)
+    with tempfile.TemporaryDirectory() as td:
+        rc = O.ref().ref_absorbed_decode(
+            NH, QKN, QKR, KVL, VHD, H, DI, V, pos, C.c_float(1e-6), _p(inv_freq, f32p),
+            _p(embed, u16p), _p(in_norm, u16p), _p(q_proj, u16p), _p(kv_a, u16p),
+            _p(kv_a_norm, u16p), _p(kv_b, u16p), _p(o_proj, u16p), _p(post_norm, u16p),
+            _p(dg, u16p), _p(du, u16p), _p(dd, u16p), _p(final_norm, u16p), _p(lm_head, u16p),
+            _p(np.ascontiguousarray(cache_in), f32p), td.encode(), _p(q, f32p))
+        assert rc == 0
+
+        def rd(n):
+            return np.fromfile(os.path.join(td, f"decode_layer0_{n}.bin"), np.float32)
+        kv_len = pos + 1
+        ckv = rd("c_kv_cache").reshape(kv_len, KVL)
+        kpe = rd("k_pe_cache").reshape(kv_len, QKR)
+        d = {
+            f"{name}_dims": np.array([NH, QKN, QKR, KVL, VHD, kv_len], np.int64),
+            f"{name}_q": q.reshape(NH, QHD),
+            f"{name}_cache": np.concatenate([ckv, kpe], axis=1),
+            f"{name}_qabs": rd("q_absorbed").reshape(NH, KVL),
+            f"{name}_probs": rd("attn_weights").reshape(NH, kv_len),
+            f"{name}_clat": rd("ctx_latent").reshape(NH, KVL),
+            f"{name}_ctx": rd("attn_out").reshape(NH, VHD),
+            f"{name}_kvb_seed": np.int64(seed + 1),
+            f"{name}_kvb_sum": np.uint64(synth.checksum_u16(kv_b)),
+        }
+        assert np.array_equal(d[f"{name}_cache"][:pos], cache_in)
+        if store_kvb:
+            d[f"{name}_kvb"] = kv_b
+        return d
+
+
+def gen_absorbed():
+    d = {}
+    d.update(_absorbed_case("tiny", 2, 16, 8, 32, 16, 6, 501, True))
+    d.update(_absorbed_case("dsv2", 16, 128, 64, 512, 128, 40, 511, False))
+    np.savez_compressed(os.path.join(OUT, "absorbed.npz"), **d)
+
+
+if __name__ == "__main__":
+    if not O.ref_available():
+        O.build(ref=True)
+    gen_matmul()
+    gen_softmax_silu()
+    gen_ffn_tiny()
+    gen_absorbed()
+    gen_ffn_dsv2()
+    for f in sorted(os.listdir(OUT)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(OUT, f)))

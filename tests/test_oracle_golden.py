@@ -1,0 +1,137 @@
+"""The CPU oracle against golden vectors written by the reference's own
+compiled src/run.c (tests/golden/make_golden.py), bit for bit, and against
+the compiled reference itself on fresh random inputs where it is built."""
+import numpy as np
+import pytest
+
+from conftest import load_golden
+from mlamoe import synth
+
+
+def test_bf16_conversions(oracle):
+    # include/tensor.h:9-20: shift up, truncate down (no round-to-nearest)
+    L = oracle.lib()
+    assert L.or_bf16_to_f32(0x3F80) == 1.0
+    assert L.or_bf16_to_f32(0xC000) == -2.0
+    assert L.or_f32_to_bf16(1.0) == 0x3F80
+    # 1 + 2^-8 + 2^-9 would round up to 0x3F81 under RNE; truncation keeps 0x3F80
+    assert L.or_f32_to_bf16(1.0 + 2 ** -8 + 2 ** -9) == 0x3F80
+    assert L.or_f32_to_bf16(-1.0 - 2 ** -8 - 2 ** -9) == 0xBF80
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(1000).astype(np.float32)
+    u = synth.bf16_from_f32(x)
+    assert all(L.or_f32_to_bf16(float(v)) == b for v, b in zip(x[:100], u[:100]))
+    back = synth.bf16_to_f32(u)
+    assert np.all(np.abs(back) <= np.abs(x)) and np.all(np.sign(back) == np.sign(x))
+
+
+def test_matmul_golden(oracle):
+    g = load_golden("matmul.npz")
+    for name in ("tiny", "odd"):
+        y = oracle.matmul(g[f"{name}_x"], g[f"{name}_w"])
+        assert np.array_equal(y.view(np.uint32), g[f"{name}_y"].view(np.uint32)), name
+    for name in ("router", "expert"):
+        r = np.random.default_rng(int(g[f"{name}_seed"]))
+        d_out, n_in = (int(v) for v in g[f"{name}_shape"])
+        w = synth.normal_bf16(r, (d_out, n_in), 0.02)
+        x = synth.normal_f32(r, (n_in,))
+        assert synth.checksum_u16(w) == int(g[f"{name}_wsum"])
+        y = oracle.matmul(x, w)
+        assert np.array_equal(y.view(np.uint32), g[f"{name}_y"].view(np.uint32)), name
+
+
+def test_softmax_silu_golden(oracle):
+    g = load_golden("softmax_silu.npz")
+    for k in ("router", "ctx", "masked", "equal"):
+        y = oracle.softmax(g[f"softmax_{k}_in"])
+        assert np.array_equal(y.view(np.uint32), g[f"softmax_{k}_out"].view(np.uint32)), k
+    L = oracle.lib()
+    s = np.array([L.or_silu(float(v)) for v in g["silu_in"]], np.float32)
+    assert np.array_equal(s.view(np.uint32), g["silu_out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("flavour", ["dsv2", "glm", "tie"])
+def test_ffn_tiny_golden(oracle, flavour):
+    g = load_golden("ffn_tiny.npz")
+    H, E, NS, K, I, sig, norm = (int(v) for v in g[f"{flavour}_cfg"])
+    cfg = oracle.moe_cfg(H, E, NS, K, I, sig, norm, float(g[f"{flavour}_scale"]))
+    w = {k: g[f"{flavour}_{k}"] for k in ("moe_gate", "eg", "eu", "ed", "sg", "su", "sd")}
+    w["moe_gate_bias"] = g.get(f"{flavour}_bias")
+    out, idx, wt, probs = oracle.ffn_compute_rows(cfg, w, g[f"{flavour}_x"])
+    assert np.array_equal(idx, g[f"{flavour}_idx"])
+    for a, b in ((out, "out"), (wt, "w"), (probs, "probs")):
+        assert np.array_equal(a.view(np.uint32), g[f"{flavour}_{b}"].view(np.uint32)), b
+    if flavour == "tie":
+        # all logits equal: strict '>' keeps the lowest index (run.c:140)
+        assert np.all(idx == np.arange(K))
+        assert np.all(probs == np.float32(1.0 / E))
+
+
+def test_ffn_dsv2_golden(oracle):
+    """Config-1 layer (H=2048, 64 experts, I=1408, top-6, 2 shared), regenerated
+    from its seed; output, routing and scores bit-identical to the reference."""
+    g = load_golden("ffn_dsv2.npz")
+    d = synth.DSV2
+    w = synth.moe_layer(int(g["seed"]), d["H"], d["E"], d["I"], d["n_shared"])
+    for k in ("moe_gate", "eg", "eu", "ed", "sg", "su", "sd"):
+        assert synth.checksum_u16(w[k]) == int(g[f"sum_{k}"]), k
+    x = synth.activations(int(g["xseed"]), int(g["T"]), d["H"])
+    cfg = oracle.moe_cfg(d["H"], d["E"], d["n_shared"], d["K"], d["I"])
+    out, idx, wt, probs = oracle.ffn_compute_rows(cfg, w, x)
+    assert np.array_equal(idx, g["idx"])
+    assert np.array_equal(out.view(np.uint32), g["out"].view(np.uint32))
+    assert np.array_equal(wt.view(np.uint32), g["w"].view(np.uint32))
+    assert np.array_equal(probs.view(np.uint32), g["probs"].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["tiny", "dsv2"])
+def test_absorbed_golden(oracle, case):
+    """The absorbed per-head chain against the reference forward_absorbed's
+    own layer-0 dumps (run.c:430-490)."""
+    g = load_golden("absorbed.npz")
+    NH, QKN, QKR, KVL, VHD, kv_len = (int(v) for v in g[f"{case}_dims"])
+    if f"{case}_kvb" in g:
+        kv_b = g[f"{case}_kvb"]
+    else:
+        kv_b = synth.normal_bf16(np.random.default_rng(int(g[f"{case}_kvb_seed"])),
+                                 (NH * (QKN + VHD), KVL), 0.02)
+    assert synth.checksum_u16(kv_b) == int(g[f"{case}_kvb_sum"])
+    q = g[f"{case}_q"][None]
+    cache = g[f"{case}_cache"][None].astype(np.float32)
+    ctx, qabs, probs, clat = oracle.absorbed_decode(q, kv_b, cache, kv_len, NH, QKN, QKR,
+                                                    KVL, VHD)
+    for a, b in ((qabs[0], "qabs"), (probs[0], "probs"), (clat[0], "clat"),
+                 (ctx[0].reshape(NH, VHD), "ctx")):
+        assert np.array_equal(a.view(np.uint32), g[f"{case}_{b}"].view(np.uint32)), b
+
+
+needs_ref = pytest.mark.skipif(
+    not __import__("pyoracle").ref_available(),
+    reason="oracle/_ref/libref.so is built only where /root/reference exists")
+
+
+@needs_ref
+def test_matmul_vs_reference_random(oracle):
+    rng = np.random.default_rng(7)
+    for d_out, n_in in ((3, 1), (17, 255), (64, 2048), (2048, 1408)):
+        x = synth.normal_f32(rng, (n_in,))
+        w = synth.normal_bf16(rng, (d_out, n_in), 0.05)
+        a, b = oracle.matmul(x, w), oracle.ref_matmul(x, w)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_ffn_vs_reference_random(oracle, seed):
+    H, E, K, I, NS = 128, 16, 4, 40, 1
+    sig = seed % 2
+    w = synth.moe_layer(seed, H, E, I, NS, gate_bias=bool(sig))
+    cfg = oracle.moe_cfg(H, E, NS, K, I, sig, sig, 1.0 + 0.4 * sig)
+    x = synth.activations(seed + 100, 3, H)
+    out, idx, wt, probs = oracle.ffn_compute_rows(cfg, w, x)
+    for t in range(3):
+        ro, ri, rw, rp = oracle.ref_ffn_compute(cfg, w, x[t])
+        assert np.array_equal(idx[t], ri)
+        assert np.array_equal(out[t].view(np.uint32), ro.view(np.uint32))
+        assert np.array_equal(wt[t].view(np.uint32), rw.view(np.uint32))
+        assert np.array_equal(probs[t].view(np.uint32), rp.view(np.uint32))
