@@ -1,0 +1,148 @@
+/* mlamoe.h -- C-ABI of the MI355X (gfx950) mla-moe matmul hot path.
+ *
+ * A drop-in for the reference engine's CPU hot path:
+ *   - the MoE FFN, ffn_compute (src/run.c:116-162), batched over T tokens,
+ *     with bf16 weights (GEMV, T small) or int8 weights (MFMA, any T);
+ *   - (declared as they are implemented) the dense bf16 matmul
+ *     (src/run.c:29-37) and the MLA absorbed-decode chain (src/run.c:430-460).
+ *
+ * Conventions
+ *   - Plain C types only; every function returns an int status (0 = MM_OK)
+ *     and never exits the process.  mm_last_error() describes the last
+ *     failure on the calling thread.  The reference calls exit() instead
+ *     (src/model_load.c:15-22, src/kernels/utils.h:9-19).
+ *   - A context (mm_ctx) owns one HIP stream on one device plus all
+ *     device-side weights it was given; it is used by one host thread at a
+ *     time.  The reference keeps this state in a process-global GpuContext
+ *     (src/getp_run.hip:26, src/kernels/getp_state.h:57-96).
+ *   - Functions named *_dev take device pointers and are asynchronous on the
+ *     context stream; the mm_ffn_compute* mirrors take host pointers and
+ *     return with the result in host memory, like the reference functions.
+ *   - Weights are uploaded (and quantised, for int8) once per layer, outside
+ *     any timed region, like the reference's warm_up (src/getp_run.hip:703-880).
+ */
+#ifndef MLAMOE_H
+#define MLAMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Every entry point below is exported from libmlamoe.so; nothing else is. */
+#define MM_API __attribute__((visibility("default")))
+
+/* ---- status ------------------------------------------------------------ */
+#define MM_OK 0
+#define MM_ERR_INVALID (-1)     /* bad argument or shape */
+#define MM_ERR_UNSUPPORTED (-2) /* valid request this build cannot serve */
+#define MM_ERR_HIP (-3)         /* HIP runtime error */
+#define MM_ERR_NOMEM (-4)       /* device or host allocation failed */
+#define MM_ERR_STATE (-5)       /* call order (e.g. layer not loaded) */
+
+/* Message for the last failed call on this thread ("" if none). */
+MM_API const char *mm_last_error(void);
+
+/* ---- context ----------------------------------------------------------- */
+typedef struct mm_ctx mm_ctx;
+
+/* Create a context on HIP device `device`: loads the gfx950 code objects and
+ * creates the context's stream (default priority). */
+MM_API int mm_ctx_create(int device, mm_ctx **out);
+MM_API void mm_ctx_destroy(mm_ctx *ctx);
+/* The context's hipStream_t, as an opaque pointer. */
+MM_API void *mm_ctx_stream(mm_ctx *ctx);
+/* Wait for all work queued on the context stream. */
+MM_API int mm_ctx_sync(mm_ctx *ctx);
+
+/* ---- device memory and timing helpers ------------------------------------ */
+MM_API int mm_dev_alloc(mm_ctx *ctx, size_t bytes, void **dptr);
+MM_API int mm_dev_free(mm_ctx *ctx, void *dptr);
+/* Synchronous copies (ordered after the context stream's queued work). */
+MM_API int mm_h2d(mm_ctx *ctx, void *dst, const void *src, size_t bytes);
+MM_API int mm_d2h(mm_ctx *ctx, void *dst, const void *src, size_t bytes);
+MM_API int mm_d2d(mm_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+#define MM_FILL_BF16_NORMAL 0   /* uint16 bf16, N(0, std), truncated */
+#define MM_FILL_F32_NORMAL 1    /* float N(0, std) */
+#define MM_FILL_F32_UNIFORM 2   /* float U[0, 1) */
+/* Fill n elements with seeded synthetic data on the device (asynchronous). */
+MM_API int mm_fill_synthetic(mm_ctx *ctx, void *dst, size_t n, int kind, uint64_t seed, float stdev);
+
+/* HIP events on the context stream: mm_timer_start, queue work,
+ * mm_timer_stop -> elapsed milliseconds (synchronises). */
+MM_API int mm_timer_start(mm_ctx *ctx);
+MM_API int mm_timer_stop(mm_ctx *ctx, float *ms);
+
+/* Per-kernel timing: while enabled, every kernel this context launches is
+ * bracketed by HIP events on its stream.  mm_prof_query synchronises and
+ * returns the summed duration and launch count of kernels named `kernel`. */
+MM_API int mm_prof_enable(mm_ctx *ctx, int on);
+MM_API int mm_prof_reset(mm_ctx *ctx);
+MM_API int mm_prof_query(mm_ctx *ctx, const char *kernel, double *total_ms, long long *launches);
+
+/* ---- MoE FFN ----------------------------------------------------------- */
+
+/* The MoE fields of the reference Config (include/model.h:12-42). */
+typedef struct {
+    int hidden_size;        /* H */
+    int n_routed_experts;   /* E (<= 256) */
+    int n_shared_experts;   /* shared MLP width = n_shared_experts * moe_inter_size */
+    int n_experts_per_tok;  /* K (<= 16) */
+    int moe_inter_size;     /* I */
+    int router_sigmoid;     /* 0: softmax scores (dsv2), 1: sigmoid (GLM noaux_tc) */
+    int norm_topk;          /* normalise the top-k weights */
+    float routed_scaling;   /* multiply the routed weights */
+} mm_moe_config;
+
+/* One MoE layer's weights, as the reference's ModelWeights holds them
+ * (include/model.h:84-96): bf16 row-major, one pointer per expert. */
+typedef struct {
+    const uint16_t *moe_gate;              /* [E, H] */
+    const float *moe_gate_bias;            /* [E] or NULL (GLM e_score_correction_bias) */
+    const uint16_t *const *expert_gate;    /* E pointers to [I, H] */
+    const uint16_t *const *expert_up;      /* E pointers to [I, H] */
+    const uint16_t *const *expert_down;    /* E pointers to [H, I] */
+    const uint16_t *shared_gate;           /* [S, H], S = n_shared_experts * I */
+    const uint16_t *shared_up;             /* [S, H] */
+    const uint16_t *shared_down;           /* [H, S] */
+} mm_moe_layer_weights;
+
+/* Configure the MoE geometry for `n_layers` layers (once per context). */
+MM_API int mm_moe_init(mm_ctx *ctx, const mm_moe_config *cfg, int n_layers);
+
+#define MM_LOAD_BF16 1u          /* keep bf16 expert weights (GEMV path) */
+#define MM_LOAD_INT8 2u          /* keep int8 per-output-channel weights (MFMA path) */
+#define MM_LOAD_DEVICE_PTRS 4u   /* the weight pointers are device pointers */
+/* Upload one layer's weights (synchronous). */
+MM_API int mm_moe_load_layer(mm_ctx *ctx, int layer, const mm_moe_layer_weights *w, unsigned flags);
+
+#define MM_FWD_BF16 0u           /* bf16 weights, fp32 activations */
+#define MM_FWD_INT8 1u           /* int8 weights, per-token int8 activations */
+#define MM_FWD_ACCUMULATE 2u     /* out += ffn(x) (residual fused) instead of out = */
+
+/* T tokens through MoE layer `layer` (ffn_compute, src/run.c:116-162, per
+ * token; the prefill loop of src/run.c:291-313).  Device pointers, queued on
+ * the context stream:
+ *   xn      [T, H] fp32 input (post-attention-norm hidden)
+ *   out     [T, H] fp32 output (overwritten, or accumulated with
+ *           MM_FWD_ACCUMULATE; may alias xn only with MM_FWD_INT8)
+ *   logits  [T, E] fp32 router logits to route instead of computing them
+ *           from xn, or NULL
+ *   topk_idx/topk_w [T, K] selected experts / weights out, or NULL
+ *   probs   [T, E] router scores out (s->moe_logits after the call), or NULL */
+MM_API int mm_moe_forward_dev(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
+                       const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
+                       unsigned flags);
+
+/* Host-pointer mirror of ffn_compute (src/run.c:116-117) for one token:
+ * out [H] overwritten; topk_idx/topk_w [K] may be NULL. Synchronous. */
+MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, int *topk_idx,
+                   float *topk_w, unsigned flags);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MLAMOE_H */

@@ -1,0 +1,18 @@
+/* embed.S -- the gfx950 code objects built from csrc/kernels/*.hip, linked
+ * into libmlamoe.so as read-only data and loaded with hipModuleLoadData.
+ * The assembler finds the .hsaco files through -I<build dir>. */
+    .section .rodata.mm_code_objects, "a", @progbits
+
+    .balign 4096
+    .globl mm_co_moe_bf16
+    .type mm_co_moe_bf16, @object
+mm_co_moe_bf16:
+    .incbin "moe_bf16.hsaco"
+
+    .balign 4096
+    .globl mm_co_util
+    .type mm_co_util, @object
+mm_co_util:
+    .incbin "util.hsaco"
+
+    .section .note.GNU-stack, "", @progbits

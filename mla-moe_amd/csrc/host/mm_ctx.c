@@ -1,0 +1,293 @@
+/* mm_ctx.c -- context, code-object loading, launches, memory and timing.
+ *
+ * The gfx950 kernels are compiled to code objects (hipcc --genco) that are
+ * embedded in this library (embed.S) and loaded with hipModuleLoadData when
+ * a context is created; kernels are launched with hipModuleLaunchKernel.
+ * The host side therefore stays plain C11 over the HIP runtime API.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "mm_internal.h"
+
+/* ---- embedded code objects (embed.S) ------------------------------------ */
+extern const unsigned char mm_co_moe_bf16[];
+extern const unsigned char mm_co_util[];
+
+enum { MOD_MOE_BF16, MOD_UTIL, MOD_COUNT };
+static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util};
+
+static const struct {
+    const char *name;
+    int module;
+} kinfo[K_COUNT] = {
+    [K_ROUTER] = {"mm_router", MOD_MOE_BF16},
+    [K_MOE_BF16_S1] = {"mm_moe_bf16_stage1", MOD_MOE_BF16},
+    [K_MOE_BF16_S2] = {"mm_moe_bf16_stage2", MOD_MOE_BF16},
+    [K_MOE_BF16_S3] = {"mm_moe_bf16_stage3", MOD_MOE_BF16},
+    [K_FILL] = {"mm_fill", MOD_UTIL},
+    [K_QUANT_W] = {"mm_quant_weight", MOD_UTIL},
+    [K_TRANSPOSE_GATE] = {"mm_transpose_gate", MOD_UTIL},
+};
+
+/* ---- errors ------------------------------------------------------------- */
+static _Thread_local char g_err[512];
+
+const char *mm_last_error(void) { return g_err; }
+
+int mm_fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int mm_hip_fail(hipError_t e, const char *what) {
+    return mm_fail(e == hipErrorOutOfMemory ? MM_ERR_NOMEM : MM_ERR_HIP, "%s: %s (%d)", what,
+                   hipGetErrorString(e), (int)e);
+}
+
+int mm_set_device(mm_ctx *ctx) {
+    MM_HIP(hipSetDevice(ctx->device));
+    return MM_OK;
+}
+
+/* ---- context ------------------------------------------------------------ */
+int mm_ctx_create(int device, mm_ctx **out) {
+    if (!out) return mm_fail(MM_ERR_INVALID, "mm_ctx_create: out is NULL");
+    *out = NULL;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return mm_fail(MM_ERR_HIP, "mm_ctx_create: no HIP device");
+    if (device < 0 || device >= n)
+        return mm_fail(MM_ERR_INVALID, "mm_ctx_create: device %d out of range [0,%d)", device, n);
+    hipDeviceProp_t prop;
+    MM_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_ctx_create: device %d is %s, this build is gfx950",
+                       device, prop.gcnArchName);
+    if (prop.warpSize != 64)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_ctx_create: wave64 required");
+
+    mm_ctx *c = calloc(1, sizeof(*c));
+    if (!c) return mm_fail(MM_ERR_NOMEM, "mm_ctx_create: calloc");
+    c->device = device;
+    int st = MM_OK;
+    if ((e = hipSetDevice(device)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreate(&c->t0)) != hipSuccess || (e = hipEventCreate(&c->t1)) != hipSuccess) {
+        st = mm_hip_fail(e, "mm_ctx_create");
+        goto fail;
+    }
+    c->modules = calloc(MOD_COUNT, sizeof(hipModule_t));
+    if (!c->modules) {
+        st = mm_fail(MM_ERR_NOMEM, "mm_ctx_create: calloc");
+        goto fail;
+    }
+    for (int m = 0; m < MOD_COUNT; m++) {
+        if ((e = hipModuleLoadData(&c->modules[m], mod_blob[m])) != hipSuccess) {
+            st = mm_hip_fail(e, "hipModuleLoadData");
+            goto fail;
+        }
+        c->n_modules = m + 1;
+    }
+    for (int k = 0; k < K_COUNT; k++) {
+        if ((e = hipModuleGetFunction(&c->fn[k], c->modules[kinfo[k].module], kinfo[k].name)) !=
+            hipSuccess) {
+            st = mm_fail(MM_ERR_HIP, "hipModuleGetFunction(%s): %s", kinfo[k].name,
+                         hipGetErrorString(e));
+            goto fail;
+        }
+    }
+    *out = c;
+    return MM_OK;
+fail:
+    mm_ctx_destroy(c);
+    return st;
+}
+
+void mm_ctx_destroy(mm_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    mm_moe_release(c);
+    if (c->ws) hipFree(c->ws);
+    for (size_t i = 0; i < c->ev_pool_n; i++) hipEventDestroy(c->ev_pool[i]);
+    free(c->ev_pool);
+    free(c->prof);
+    for (int m = 0; m < c->n_modules; m++) hipModuleUnload(c->modules[m]);
+    free(c->modules);
+    if (c->t0) hipEventDestroy(c->t0);
+    if (c->t1) hipEventDestroy(c->t1);
+    if (c->stream) hipStreamDestroy(c->stream);
+    free(c);
+}
+
+void *mm_ctx_stream(mm_ctx *c) { return c ? (void *)c->stream : NULL; }
+
+int mm_ctx_sync(mm_ctx *c) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_ctx_sync: NULL context");
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipStreamSynchronize(c->stream));
+    return MM_OK;
+}
+
+/* ---- launches and per-kernel timing ------------------------------------- */
+/* Event `i` of the profiling pool (record r uses events 2r and 2r+1). */
+static int pool_event(mm_ctx *c, size_t i, hipEvent_t *ev) {
+    while (i >= c->ev_pool_n) {
+        if (c->ev_pool_n == c->ev_pool_cap) {
+            size_t cap = c->ev_pool_cap ? 2 * c->ev_pool_cap : 256;
+            hipEvent_t *p = realloc(c->ev_pool, cap * sizeof(*p));
+            if (!p) return mm_fail(MM_ERR_NOMEM, "profiler events");
+            c->ev_pool = p;
+            c->ev_pool_cap = cap;
+        }
+        MM_HIP(hipEventCreate(&c->ev_pool[c->ev_pool_n]));
+        c->ev_pool_n++;
+    }
+    *ev = c->ev_pool[i];
+    return MM_OK;
+}
+
+int mm_launch(mm_ctx *c, mm_kernel_id id, unsigned gx, unsigned gy, unsigned gz,
+              unsigned block, size_t shmem, void *args) {
+    if (gx == 0 || gy == 0 || gz == 0) return MM_OK;
+    void *params[1] = {args};
+    mm_prof_rec rec = {id, {0, 0}};
+    if (c->prof_on) {
+        if (c->prof_n == c->prof_cap) {
+            size_t cap = c->prof_cap ? 2 * c->prof_cap : 128;
+            mm_prof_rec *p = realloc(c->prof, cap * sizeof(*p));
+            if (!p) return mm_fail(MM_ERR_NOMEM, "profiler records");
+            c->prof = p;
+            c->prof_cap = cap;
+        }
+        int st = pool_event(c, 2 * c->prof_n, &rec.ev[0]);
+        if (!st) st = pool_event(c, 2 * c->prof_n + 1, &rec.ev[1]);
+        if (st) return st;
+        MM_HIP(hipEventRecord(rec.ev[0], c->stream));
+    }
+    hipError_t e = hipModuleLaunchKernel(c->fn[id], gx, gy, gz, block, 1, 1, (unsigned)shmem,
+                                         c->stream, params, NULL);
+    if (e != hipSuccess)
+        return mm_fail(MM_ERR_HIP, "launch %s: %s", kinfo[id].name, hipGetErrorString(e));
+    if (c->prof_on) {
+        MM_HIP(hipEventRecord(rec.ev[1], c->stream));
+        c->prof[c->prof_n++] = rec;
+    }
+    return MM_OK;
+}
+
+int mm_prof_enable(mm_ctx *c, int on) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_prof_enable: NULL context");
+    c->prof_on = on != 0;
+    return MM_OK;
+}
+
+int mm_prof_reset(mm_ctx *c) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_prof_reset: NULL context");
+    int st = mm_ctx_sync(c);
+    c->prof_n = 0;
+    return st;
+}
+
+int mm_prof_query(mm_ctx *c, const char *kernel, double *total_ms, long long *launches) {
+    if (!c || !kernel) return mm_fail(MM_ERR_INVALID, "mm_prof_query: bad argument");
+    int st = mm_ctx_sync(c);
+    if (st) return st;
+    double tot = 0.0;
+    long long n = 0;
+    for (size_t i = 0; i < c->prof_n; i++) {
+        if (strcmp(kinfo[c->prof[i].id].name, kernel) != 0) continue;
+        float ms = 0.0f;
+        MM_HIP(hipEventElapsedTime(&ms, c->prof[i].ev[0], c->prof[i].ev[1]));
+        tot += ms;
+        n++;
+    }
+    if (total_ms) *total_ms = tot;
+    if (launches) *launches = n;
+    return MM_OK;
+}
+
+int mm_timer_start(mm_ctx *c) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_timer_start: NULL context");
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipEventRecord(c->t0, c->stream));
+    return MM_OK;
+}
+
+int mm_timer_stop(mm_ctx *c, float *ms) {
+    if (!c || !ms) return mm_fail(MM_ERR_INVALID, "mm_timer_stop: bad argument");
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipEventRecord(c->t1, c->stream));
+    MM_HIP(hipEventSynchronize(c->t1));
+    MM_HIP(hipEventElapsedTime(ms, c->t0, c->t1));
+    return MM_OK;
+}
+
+/* ---- memory --------------------------------------------------------------- */
+int mm_dev_alloc(mm_ctx *c, size_t bytes, void **dptr) {
+    if (!c || !dptr) return mm_fail(MM_ERR_INVALID, "mm_dev_alloc: bad argument");
+    *dptr = NULL;
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+    return MM_OK;
+}
+
+int mm_dev_free(mm_ctx *c, void *dptr) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_dev_free: NULL context");
+    if (!dptr) return MM_OK;
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipStreamSynchronize(c->stream));
+    MM_HIP(hipFree(dptr));
+    return MM_OK;
+}
+
+static int copy(mm_ctx *c, void *dst, const void *src, size_t bytes, hipMemcpyKind k) {
+    if (!c || (bytes && (!dst || !src))) return mm_fail(MM_ERR_INVALID, "copy: bad argument");
+    if (!bytes) return MM_OK;
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipMemcpyAsync(dst, src, bytes, k, c->stream));
+    MM_HIP(hipStreamSynchronize(c->stream));
+    return MM_OK;
+}
+
+int mm_h2d(mm_ctx *c, void *dst, const void *src, size_t bytes) {
+    return copy(c, dst, src, bytes, hipMemcpyHostToDevice);
+}
+int mm_d2h(mm_ctx *c, void *dst, const void *src, size_t bytes) {
+    return copy(c, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+int mm_d2d(mm_ctx *c, void *dst, const void *src, size_t bytes) {
+    return copy(c, dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+int mm_workspace(mm_ctx *c, size_t bytes, void **out) {
+    if (bytes > c->ws_bytes) {
+        MM_HIP(hipStreamSynchronize(c->stream));
+        if (c->ws) MM_HIP(hipFree(c->ws));
+        c->ws = NULL;
+        c->ws_bytes = 0;
+        size_t nb = bytes + bytes / 4;
+        MM_HIP(hipMalloc(&c->ws, nb));
+        c->ws_bytes = nb;
+    }
+    *out = c->ws;
+    return MM_OK;
+}
+
+int mm_fill_synthetic(mm_ctx *c, void *dst, size_t n, int kind, uint64_t seed, float stdev) {
+    if (!c || (n && !dst) || kind < 0 || kind > 2)
+        return mm_fail(MM_ERR_INVALID, "mm_fill_synthetic: bad argument");
+    int st = mm_set_device(c);
+    if (st) return st;
+    mm_fill_args a = {dst, (uint64_t)n, seed, stdev, kind};
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    return mm_launch(c, K_FILL, (unsigned)blocks, 1, 1, 256, 0, &a);
+}

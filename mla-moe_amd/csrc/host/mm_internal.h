@@ -1,0 +1,82 @@
+/* mm_internal.h -- private state of the C11 host library. */
+#ifndef MLAMOE_INTERNAL_H
+#define MLAMOE_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../kernel_params.h"
+#include "mlamoe.h"
+
+/* Kernels, one entry per extern "C" __global__ in csrc/kernels. */
+typedef enum {
+    K_ROUTER,
+    K_MOE_BF16_S1,
+    K_MOE_BF16_S2,
+    K_MOE_BF16_S3,
+    K_FILL,
+    K_QUANT_W,
+    K_TRANSPOSE_GATE,
+    K_COUNT
+} mm_kernel_id;
+
+typedef struct {
+    int id;
+    hipEvent_t ev[2];
+} mm_prof_rec;
+
+typedef struct {
+    int loaded;
+    unsigned formats;
+    float *wgT;                 /* [H, E] fp32 router weight, transposed */
+    float *bias;                /* [E] or NULL */
+    uint16_t *bf16_pool;        /* one allocation holding the six bf16 families */
+    uint16_t *eg, *eu, *ed, *sg, *su, *sd;
+} mm_moe_layer;
+
+struct mm_ctx {
+    int device;
+    hipStream_t stream;
+    hipModule_t *modules;
+    int n_modules;
+    hipFunction_t fn[K_COUNT];
+    hipEvent_t t0, t1;
+
+    int prof_on;
+    mm_prof_rec *prof;
+    size_t prof_n, prof_cap;
+    hipEvent_t *ev_pool;
+    size_t ev_pool_n, ev_pool_cap;
+
+    /* MoE */
+    int moe_ready;
+    mm_moe_config moe;
+    int n_layers;
+    mm_moe_layer *layers;
+
+    /* growable device workspace */
+    void *ws;
+    size_t ws_bytes;
+};
+
+/* error reporting (thread-local message) */
+int mm_fail(int status, const char *fmt, ...);
+int mm_hip_fail(hipError_t e, const char *what);
+#define MM_HIP(call)                                              \
+    do {                                                          \
+        hipError_t mm_e_ = (call);                                \
+        if (mm_e_ != hipSuccess) return mm_hip_fail(mm_e_, #call); \
+    } while (0)
+
+int mm_set_device(mm_ctx *ctx);
+/* Launch kernel `id` with its argument block `args` (the struct is copied). */
+int mm_launch(mm_ctx *ctx, mm_kernel_id id, unsigned gx, unsigned gy, unsigned gz,
+              unsigned block, size_t shmem, void *args);
+/* Device workspace of at least `bytes`, reallocated (after a stream sync)
+ * when too small. */
+int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
+
+void mm_moe_release(mm_ctx *ctx);
+
+#endif

@@ -1,0 +1,135 @@
+/* moe_bf16.hip -- MoE expert FFN with bf16 weights and fp32 activations for
+ * small token counts (T=1 decode), as three GEMV stages.
+ *
+ * Reference semantics: ffn_compute (src/run.c:116-162).  Weights are
+ * row-major [rows, K] bf16 exactly as the reference stores them; every GEMV
+ * reads a weight row once with 128-bit loads, 64 lanes covering 1 KB
+ * contiguous per instruction, and accumulates in fp32.
+ *
+ *   stage 1  blocks [0, n_router_blocks): router (router.h)
+ *            other blocks: shared-expert gate/up rows for all T tokens,
+ *            SwiGLU, written to hcat[t, K*I + j]
+ *   stage 2  routed gate/up for every (token, slot) route, SwiGLU scaled by
+ *            the route weight, written to hcat[t, r*I + j]
+ *   stage 3  out[t, d] = sum over the K routed segments and the shared
+ *            segment of down_seg[d, :] . hcat[t, seg]
+ *
+ * The router and the shared expert do not depend on each other, so they run
+ * in one launch: the router's dependent add chains overlap the shared
+ * expert's weight stream.  The route weight is folded into the hidden row
+ * (w_r * silu(g) * u) so the combine of run.c:151-160 becomes a single dot
+ * product over the concatenated hidden rows.
+ */
+#include "router.h"
+
+#define GU_THREADS 256
+#define GU_WAVES (GU_THREADS / MM_WAVE)
+#define NT_MAX 8
+
+/* Gate/up rows [row0, row0+nrows) against T tokens xs [T, H] (global memory;
+ * every wave of a block reads the same activations, so they stay in L1/L2).
+ * Writes h[t*hstride + hoff + j] = wt[t] * silu(g) * u. */
+__device__ __forceinline__ void gu_rows(const uint16_t *__restrict__ gate, const uint16_t *__restrict__ up,
+                        const float *xs, int T, int H, int row0, int nrows,
+                        float *__restrict__ h, size_t hstride, int hoff, const float *wt) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = threadIdx.x / MM_WAVE;
+    const int nch = H >> 3;
+    for (int rr = wave; rr < nrows; rr += GU_WAVES) {
+        const int row = row0 + rr;
+        const u32x4 *gp = (const u32x4 *)(gate + (size_t)row * H);
+        const u32x4 *up_ = (const u32x4 *)(up + (size_t)row * H);
+        float ag[NT_MAX], au[NT_MAX];
+#pragma unroll
+        for (int t = 0; t < NT_MAX; t++) { ag[t] = 0.0f; au[t] = 0.0f; }
+#pragma unroll 4
+        for (int c = lane; c < nch; c += MM_WAVE) {
+            u32x4 gv = __builtin_nontemporal_load(gp + c);
+            u32x4 uv = __builtin_nontemporal_load(up_ + c);
+#pragma unroll
+            for (int t = 0; t < NT_MAX; t++) {
+                if (t < T) {
+                    const float *xv = xs + (size_t)t * H + 8 * c;
+                    ag[t] = dot8_bf16(gv, xv, ag[t]);
+                    au[t] = dot8_bf16(uv, xv, au[t]);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NT_MAX; t++) {
+            if (t < T) {
+                float g = wave_sum(ag[t]);
+                float u = wave_sum(au[t]);
+                if (lane == 0) h[(size_t)t * hstride + hoff + row] = wt[t] * swiglu_f(g, u);
+            }
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_router(mm_router_args a) {
+    router_block(a, blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_gu_bf16_args a) {
+    if ((int)blockIdx.x < a.r.n_router_blocks) {
+        router_block(a.r, blockIdx.x);
+        return;
+    }
+    const int b = blockIdx.x - a.r.n_router_blocks;
+    const int row0 = b * a.rows_per_block;
+    const int nrows = min(a.rows_per_block, a.S - row0);
+    if (nrows <= 0) return;
+    float one[NT_MAX];
+#pragma unroll
+    for (int t = 0; t < NT_MAX; t++) one[t] = 1.0f;
+    gu_rows(a.gate, a.up, a.x, a.T, a.H, row0, nrows, a.hcat, (size_t)a.K * a.I + a.S,
+            a.K * a.I, one);
+}
+
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_gu_bf16_args a) {
+    const int route = blockIdx.y;               /* t*K + r */
+    const int t = route / a.K, r = route % a.K;
+    const int row0 = blockIdx.x * a.rows_per_block;
+    const int nrows = min(a.rows_per_block, a.I - row0);
+    if (nrows <= 0) return;
+    const int e = min(max(a.r.topk_idx[route], 0), a.r.E - 1);
+    const float wr = a.r.topk_w[route];
+    const size_t off = (size_t)e * a.I * a.H;
+    gu_rows(a.gate + off, a.up + off, a.x + (size_t)t * a.H, 1, a.H, row0, nrows,
+            a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), 0, r * a.I, &wr);
+}
+
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_down_bf16_args a) {
+    const int t = blockIdx.y;
+    const float *hs = a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S);
+
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = threadIdx.x / MM_WAVE;
+    const int d0 = blockIdx.x * a.rows_per_block;
+    const int nrows = min(a.rows_per_block, a.H - d0);
+    const int nci = a.I >> 3, ncs = a.S >> 3;
+    for (int rr = wave; rr < nrows; rr += GU_WAVES) {
+        const int d = d0 + rr;
+        float acc = 0.0f;
+        for (int r = 0; r < a.K; r++) {
+            const int e = min(max(a.topk_idx[(size_t)t * a.K + r], 0), a.E - 1);
+            const u32x4 *p = (const u32x4 *)(a.down + ((size_t)e * a.H + d) * a.I);
+            const float *hseg = hs + r * a.I;
+#pragma unroll 2
+            for (int c = lane; c < nci; c += MM_WAVE)
+                acc = dot8_bf16(__builtin_nontemporal_load(p + c), hseg + 8 * c, acc);
+        }
+        if (a.S > 0) {
+            const u32x4 *p = (const u32x4 *)(a.sdown + (size_t)d * a.S);
+            const float *hseg = hs + a.K * a.I;
+#pragma unroll 2
+            for (int c = lane; c < ncs; c += MM_WAVE)
+                acc = dot8_bf16(__builtin_nontemporal_load(p + c), hseg + 8 * c, acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            float *o = a.out + (size_t)t * a.H + d;
+            *o = a.accumulate ? *o + acc : acc;
+        }
+    }
+}

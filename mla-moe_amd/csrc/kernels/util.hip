@@ -1,0 +1,66 @@
+/* util.hip -- device-side data preparation: synthetic inputs, the int8
+ * per-output-channel weight quantiser and the router-weight transpose. */
+#include "common.h"
+
+/* Counter-based generator: splitmix64 of (seed, index), so any element can be
+ * produced independently.  Normal samples use Box-Muller on two 32-bit
+ * uniforms.  Used for large synthetic benchmark inputs only. */
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float gen_normal(uint64_t seed, uint64_t i) {
+    uint64_t h = splitmix64(seed * 0x2545F4914F6CDD1Dull ^ splitmix64(i));
+    float u1 = ((float)(uint32_t)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);   /* (0, 1] */
+    float u2 = (float)(uint32_t)(h & 0xFFFFFFu) * (1.0f / 16777216.0f);      /* [0, 1) */
+    return sqrtf(-2.0f * __logf(u1)) * __cosf(6.28318530718f * u2);
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_fill(mm_fill_args a) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+        if (a.kind == 0) {
+            float v = gen_normal(a.seed, i) * a.std;
+            ((uint16_t *)a.dst)[i] = (uint16_t)(__float_as_uint(v) >> 16);   /* truncation */
+        } else if (a.kind == 1) {
+            ((float *)a.dst)[i] = gen_normal(a.seed, i) * a.std;
+        } else {
+            uint64_t h = splitmix64(a.seed * 0x2545F4914F6CDD1Dull ^ splitmix64(i));
+            ((float *)a.dst)[i] = (float)(uint32_t)(h >> 40) * (1.0f / 16777216.0f);
+        }
+    }
+}
+
+/* One wave per row: s = max|w| / 127, q = clamp(rint(w / s), -127, 127),
+ * with IEEE fp32 division and round-half-even, bit-identical to the CPU
+ * quantiser; s == 0 gives an all-zero row. */
+extern "C" __global__ __launch_bounds__(256) void mm_quant_weight(mm_quant_w_args a) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int row = blockIdx.x * (blockDim.x / MM_WAVE) + threadIdx.x / MM_WAVE;
+    if (row >= a.rows) return;
+    const uint16_t *w = a.w + (size_t)row * a.K;
+    int8_t *q = a.q + (size_t)row * a.K;
+    float amax = 0.0f;
+    for (int i = lane; i < a.K; i += MM_WAVE) amax = fmaxf(amax, fabsf(bf16_f32(w[i])));
+    amax = wave_max(amax);
+    const float s = amax / 127.0f;
+    if (lane == 0) a.s[row] = s;
+    for (int i = lane; i < a.K; i += MM_WAVE) {
+        float v = 0.0f;
+        if (s != 0.0f) v = fminf(fmaxf(rintf(bf16_f32(w[i]) / s), -127.0f), 127.0f);
+        q[i] = (int8_t)(int)v;
+    }
+}
+
+/* [E, H] bf16 -> [H, E] fp32 */
+extern "C" __global__ __launch_bounds__(256) void mm_transpose_gate(mm_transpose_gate_args a) {
+    const size_t n = (size_t)a.E * a.H;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        size_t h = i / a.E, e = i % a.E;
+        a.dst[i] = bf16_f32(a.src[e * a.H + h]);
+    }
+}

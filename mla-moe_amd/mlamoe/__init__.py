@@ -1,0 +1,265 @@
+"""Python mirror of the libmlamoe C-ABI (include/mlamoe.h), over ctypes.
+
+This is the host-side interface the tests and the benchmark drive; it keeps
+the reference's names and argument meanings (ffn_compute, matmul, the
+absorbed-decode chain).  Errors are raised as MMError carrying the library's
+message.  The HIP library is required: importing works without it, but
+creating a Context fails loudly when libmlamoe.so is missing or no gfx950
+device is present.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libmlamoe.so")
+HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "mlamoe.h")
+
+MM_LOAD_BF16, MM_LOAD_INT8, MM_LOAD_DEVICE_PTRS = 1, 2, 4
+MM_FWD_BF16, MM_FWD_INT8, MM_FWD_ACCUMULATE = 0, 1, 2
+MM_FILL_BF16_NORMAL, MM_FILL_F32_NORMAL, MM_FILL_F32_UNIFORM = 0, 1, 2
+
+_vp = C.c_void_p
+
+
+class MMError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"mlamoe status {status}: {msg}")
+        self.status = status
+
+
+class MoeConfig(C.Structure):
+    """Mirror of mm_moe_config (the MoE fields of the reference Config)."""
+    _fields_ = [("hidden_size", C.c_int), ("n_routed_experts", C.c_int),
+                ("n_shared_experts", C.c_int), ("n_experts_per_tok", C.c_int),
+                ("moe_inter_size", C.c_int), ("router_sigmoid", C.c_int),
+                ("norm_topk", C.c_int), ("routed_scaling", C.c_float)]
+
+
+class MoeLayerWeights(C.Structure):
+    _fields_ = [("moe_gate", _vp), ("moe_gate_bias", _vp), ("expert_gate", C.POINTER(_vp)),
+                ("expert_up", C.POINTER(_vp)), ("expert_down", C.POINTER(_vp)),
+                ("shared_gate", _vp), ("shared_up", _vp), ("shared_down", _vp)]
+
+
+_lib = None
+
+
+def header_functions():
+    """Names of the functions include/mlamoe.h declares."""
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(mm_\w+)\s*\(", src, flags=re.M)))
+
+
+def lib():
+    """Load libmlamoe.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MMError(-2, f"{LIB_PATH} not built; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        L.mm_last_error.restype = C.c_char_p
+        L.mm_ctx_create.argtypes = [C.c_int, C.POINTER(_vp)]
+        L.mm_ctx_destroy.argtypes = [_vp]
+        L.mm_ctx_destroy.restype = None
+        L.mm_ctx_stream.argtypes = [_vp]
+        L.mm_ctx_stream.restype = _vp
+        L.mm_ctx_sync.argtypes = [_vp]
+        L.mm_dev_alloc.argtypes = [_vp, C.c_size_t, C.POINTER(_vp)]
+        L.mm_dev_free.argtypes = [_vp, _vp]
+        for f in (L.mm_h2d, L.mm_d2h, L.mm_d2d):
+            f.argtypes = [_vp, _vp, _vp, C.c_size_t]
+        L.mm_fill_synthetic.argtypes = [_vp, _vp, C.c_size_t, C.c_int, C.c_uint64, C.c_float]
+        L.mm_timer_start.argtypes = [_vp]
+        L.mm_timer_stop.argtypes = [_vp, C.POINTER(C.c_float)]
+        L.mm_prof_enable.argtypes = [_vp, C.c_int]
+        L.mm_prof_reset.argtypes = [_vp]
+        L.mm_prof_query.argtypes = [_vp, C.c_char_p, C.POINTER(C.c_double),
+                                    C.POINTER(C.c_longlong)]
+        L.mm_moe_init.argtypes = [_vp, C.POINTER(MoeConfig), C.c_int]
+        L.mm_moe_load_layer.argtypes = [_vp, C.c_int, C.POINTER(MoeLayerWeights), C.c_uint]
+        L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         C.c_uint]
+        L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        _lib = L
+    return _lib
+
+
+def _check(st):
+    if st != 0:
+        raise MMError(st, lib().mm_last_error().decode())
+
+
+class DevBuf:
+    """A device allocation owned by a Context."""
+
+    def __init__(self, ctx, nbytes, dtype=np.uint8, shape=None):
+        self.ctx, self.nbytes, self.dtype = ctx, int(nbytes), np.dtype(dtype)
+        self.shape = shape if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = _vp()
+        _check(lib().mm_dev_alloc(ctx.h, self.nbytes, C.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            _check(lib().mm_dev_free(self.ctx.h, self.ptr))
+            self.ptr = None
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _check(lib().mm_h2d(self.ctx.h, self.ptr, a.ctypes.data, a.nbytes))
+        return self
+
+    def download(self, dtype=None, shape=None):
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        shp = shape if shape is not None else self.shape
+        out = np.empty(shp, dt)
+        _check(lib().mm_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+
+class Context:
+    """One mm_ctx: a device, its stream and the weights it holds."""
+
+    def __init__(self, device=0):
+        h = _vp()
+        _check(lib().mm_ctx_create(device, C.byref(h)))
+        self.h = h.value
+        self._bufs = []
+        self._moe_cfg = None
+
+    def close(self):
+        if self.h:
+            for b in self._bufs:
+                b.free()
+            self._bufs = []
+            lib().mm_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # memory --------------------------------------------------------------
+    def alloc(self, nbytes, dtype=np.uint8, shape=None, keep=True):
+        b = DevBuf(self, nbytes, dtype, shape)
+        if keep:
+            self._bufs.append(b)
+        return b
+
+    def to_device(self, a):
+        a = np.ascontiguousarray(a)
+        return self.alloc(max(a.nbytes, 1), a.dtype, a.shape).upload(a)
+
+    def empty(self, shape, dtype):
+        dt = np.dtype(dtype)
+        n = int(np.prod(shape)) * dt.itemsize
+        return self.alloc(max(n, 1), dt, tuple(shape))
+
+    def fill(self, buf, n, kind, seed, std=1.0):
+        _check(lib().mm_fill_synthetic(self.h, buf.ptr, n, kind, seed, std))
+
+    def sync(self):
+        _check(lib().mm_ctx_sync(self.h))
+
+    # timing --------------------------------------------------------------
+    def timer_start(self):
+        _check(lib().mm_timer_start(self.h))
+
+    def timer_stop(self):
+        ms = C.c_float()
+        _check(lib().mm_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
+    def prof_enable(self, on=True):
+        _check(lib().mm_prof_enable(self.h, int(on)))
+
+    def prof_reset(self):
+        _check(lib().mm_prof_reset(self.h))
+
+    def prof_query(self, kernel):
+        t = C.c_double()
+        n = C.c_longlong()
+        _check(lib().mm_prof_query(self.h, kernel.encode(), C.byref(t), C.byref(n)))
+        return t.value, n.value
+
+    # MoE FFN ---------------------------------------------------------------
+    def moe_init(self, H, E, n_shared, K, I, router_sigmoid=0, norm_topk=0,
+                 routed_scaling=1.0, n_layers=1):
+        cfg = MoeConfig(H, E, n_shared, K, I, router_sigmoid, norm_topk, routed_scaling)
+        _check(lib().mm_moe_init(self.h, C.byref(cfg), n_layers))
+        self._moe_cfg = cfg
+
+    def moe_load_layer(self, layer, w, flags=MM_LOAD_BF16):
+        """w: dict of numpy arrays as mlamoe.synth.moe_layer returns (host
+        pointers), or of DevBufs with flags | MM_LOAD_DEVICE_PTRS."""
+        cfg = self._moe_cfg
+        E, I, H = cfg.n_routed_experts, cfg.moe_inter_size, cfg.hidden_size
+        dev = bool(flags & MM_LOAD_DEVICE_PTRS)
+        keep = []
+
+        def base(a):
+            if a is None:
+                return None
+            if dev:
+                return a.ptr
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+            return a.ctypes.data
+
+        def per_expert(a, rows, cols):
+            b = base(a)
+            step = rows * cols * 2
+            return (_vp * E)(*[b + e * step for e in range(E)])
+        eg, eu, ed = per_expert(w["eg"], I, H), per_expert(w["eu"], I, H), per_expert(w["ed"], H, I)
+        lw = MoeLayerWeights(base(w["moe_gate"]), base(w.get("moe_gate_bias")), eg, eu, ed,
+                             base(w["sg"]), base(w["su"]), base(w["sd"]))
+        _check(lib().mm_moe_load_layer(self.h, layer, C.byref(lw), flags))
+
+    def moe_forward_dev(self, layer, T, xn, out, logits=None, topk_idx=None, topk_w=None,
+                        probs=None, flags=MM_FWD_BF16):
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        _check(lib().mm_moe_forward_dev(self.h, layer, T, p(xn), p(out), p(logits),
+                                        p(topk_idx), p(topk_w), p(probs), flags))
+
+    def moe_forward(self, layer, xn, logits=None, flags=MM_FWD_BF16):
+        """Host arrays in and out: returns out, topk_idx, topk_w, probs."""
+        cfg = self._moe_cfg
+        xn = np.ascontiguousarray(xn, np.float32)
+        T = xn.shape[0]
+        E, K, H = cfg.n_routed_experts, cfg.n_experts_per_tok, cfg.hidden_size
+        dx = self.alloc(xn.nbytes, keep=False).upload(xn)
+        dout = self.alloc(T * H * 4, keep=False)
+        didx = self.alloc(T * K * 4, keep=False)
+        dw = self.alloc(T * K * 4, keep=False)
+        dp = self.alloc(T * E * 4, keep=False)
+        dl = None
+        if logits is not None:
+            dl = self.alloc(T * E * 4, keep=False).upload(np.ascontiguousarray(logits, np.float32))
+        try:
+            self.moe_forward_dev(layer, T, dx, dout, dl, didx, dw, dp, flags)
+            return (dout.download(np.float32, (T, H)), didx.download(np.int32, (T, K)),
+                    dw.download(np.float32, (T, K)), dp.download(np.float32, (T, E)))
+        finally:
+            for b in (dx, dout, didx, dw, dp, dl):
+                if b is not None:
+                    b.free()
+
+    def ffn_compute(self, layer, xn, flags=MM_FWD_BF16):
+        """Mirror of the reference ffn_compute (src/run.c:116) for one token."""
+        cfg = self._moe_cfg
+        xn = np.ascontiguousarray(xn, np.float32)
+        out = np.empty(cfg.hidden_size, np.float32)
+        idx = np.empty(cfg.n_experts_per_tok, np.int32)
+        w = np.empty(cfg.n_experts_per_tok, np.float32)
+        _check(lib().mm_ffn_compute(self.h, layer, xn.ctypes.data, out.ctypes.data,
+                                    idx.ctypes.data, w.ctypes.data, flags))
+        return out, idx, w
