@@ -137,6 +137,37 @@ MM_API int mm_moe_forward_dev(mm_ctx *ctx, int layer, int T, const float *xn, fl
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags);
 
+/* Intermediates of the int8 path, for parity checking (no reference
+ * counterpart: the reference has no int8 path).  Device pointers; any may be
+ * NULL.  R = T * K routed rows, row t*K + r is token t's slot r.
+ *   qx [T, H] int8, sx [T]        per-token quantised input
+ *   acc_gu [R, 2, I] int32        raw gate (0) and up (1) accumulators
+ *   h [R, I]                      SwiGLU output, fp32
+ *   qh [R, I] int8, sh [R]        its per-row quantisation
+ *   acc_d [R, H] int32            raw down-projection accumulators
+ *   y [R, H]                      dequantised expert outputs (before the route weight)
+ *   hs, qhs [T, S], shs [T], ys [T, H]   the same for the shared expert */
+typedef struct {
+    int8_t *qx;
+    float *sx;
+    int32_t *acc_gu;
+    float *h;
+    int8_t *qh;
+    float *sh;
+    int32_t *acc_d;
+    float *y;
+    float *hs;
+    int8_t *qhs;
+    float *shs;
+    float *ys;
+} mm_moe_i8_debug;
+
+/* mm_moe_forward_dev with MM_FWD_INT8, also filling the debug intermediates. */
+MM_API int mm_moe_forward_i8_debug_dev(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
+                                       const float *logits, int32_t *topk_idx, float *topk_w,
+                                       float *probs, unsigned flags,
+                                       const mm_moe_i8_debug *dbg);
+
 /* Host-pointer mirror of ffn_compute (src/run.c:116-117) for one token:
  * out [H] overwritten; topk_idx/topk_w [K] may be NULL. Synchronous. */
 MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, int *topk_idx,

@@ -15,4 +15,10 @@ mm_co_moe_bf16:
 mm_co_util:
     .incbin "util.hsaco"
 
+    .balign 4096
+    .globl mm_co_moe_i8
+    .type mm_co_moe_i8, @object
+mm_co_moe_i8:
+    .incbin "moe_i8.hsaco"
+
     .section .note.GNU-stack, "", @progbits

@@ -16,9 +16,11 @@
 /* ---- embedded code objects (embed.S) ------------------------------------ */
 extern const unsigned char mm_co_moe_bf16[];
 extern const unsigned char mm_co_util[];
+extern const unsigned char mm_co_moe_i8[];
 
-enum { MOD_MOE_BF16, MOD_UTIL, MOD_COUNT };
-static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util};
+enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_COUNT };
+static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util,
+                                                          mm_co_moe_i8};
 
 static const struct {
     const char *name;
@@ -31,6 +33,12 @@ static const struct {
     [K_FILL] = {"mm_fill", MOD_UTIL},
     [K_QUANT_W] = {"mm_quant_weight", MOD_UTIL},
     [K_TRANSPOSE_GATE] = {"mm_transpose_gate", MOD_UTIL},
+    [K_I8_ROUTE] = {"mm_i8_route", MOD_MOE_I8},
+    [K_I8_GU] = {"mm_i8_gu", MOD_MOE_I8},
+    [K_I8_QUANT_H] = {"mm_i8_quant_h", MOD_MOE_I8},
+    [K_I8_DOWN] = {"mm_i8_down", MOD_MOE_I8},
+    [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
+    [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
 };
 
 /* ---- errors ------------------------------------------------------------- */

@@ -18,6 +18,12 @@ typedef enum {
     K_FILL,
     K_QUANT_W,
     K_TRANSPOSE_GATE,
+    K_I8_ROUTE,
+    K_I8_GU,
+    K_I8_QUANT_H,
+    K_I8_DOWN,
+    K_I8_COMBINE,
+    K_PACK_I8,
     K_COUNT
 } mm_kernel_id;
 
@@ -33,6 +39,9 @@ typedef struct {
     float *bias;                /* [E] or NULL */
     uint16_t *bf16_pool;        /* one allocation holding the six bf16 families */
     uint16_t *eg, *eu, *ed, *sg, *su, *sd;
+    int8_t *i8_pool;            /* packed int8 fragments (kernel_params.h) */
+    float *i8_scales;
+    mm_i8_weights i8;
 } mm_moe_layer;
 
 struct mm_ctx {
@@ -54,6 +63,7 @@ struct mm_ctx {
     mm_moe_config moe;
     int n_layers;
     mm_moe_layer *layers;
+    int32_t *moe_cnt;           /* [E] per-expert row counters, zero between calls */
 
     /* growable device workspace */
     void *ws;

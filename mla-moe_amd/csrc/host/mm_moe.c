@@ -23,9 +23,13 @@ void mm_moe_release(mm_ctx *c) {
         if (L->wgT) hipFree(L->wgT);
         if (L->bias) hipFree(L->bias);
         if (L->bf16_pool) hipFree(L->bf16_pool);
+        if (L->i8_pool) hipFree(L->i8_pool);
+        if (L->i8_scales) hipFree(L->i8_scales);
     }
     free(c->layers);
     c->layers = NULL;
+    if (c->moe_cnt) hipFree(c->moe_cnt);
+    c->moe_cnt = NULL;
     c->moe_ready = 0;
 }
 
@@ -41,6 +45,11 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     if (E > 256) return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_init: E > 256 experts");
     if (H % 8 || I % 8)
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_init: hidden and moe_inter must be multiples of 8");
+    int st = mm_set_device(c);
+    if (st) return st;
+    MM_HIP(hipMalloc((void **)&c->moe_cnt, (size_t)E * sizeof(int32_t)));
+    MM_HIP(hipMemsetAsync(c->moe_cnt, 0, (size_t)E * sizeof(int32_t), c->stream));
+    MM_HIP(hipStreamSynchronize(c->stream));
     c->layers = calloc((size_t)n_layers, sizeof(mm_moe_layer));
     if (!c->layers) return mm_fail(MM_ERR_NOMEM, "mm_moe_init: calloc");
     c->moe = *cfg;
@@ -56,6 +65,106 @@ static int upload(mm_ctx *c, void *dst, const void *src, size_t bytes, int dev) 
     return MM_OK;
 }
 
+/* ---- int8 weights -------------------------------------------------------- */
+
+/* Device copy of one expert family (E matrices of n elements). */
+static int gather_family(mm_ctx *c, uint16_t *dst, const uint16_t *const *src, size_t E,
+                         size_t n, int dev) {
+    for (size_t e = 0; e < E; e++) {
+        int st = upload(c, dst + e * n, src[e], n * 2, dev);
+        if (st) return st;
+    }
+    return MM_OK;
+}
+
+static int quant_rows_dev(mm_ctx *c, const uint16_t *src, size_t rows, size_t K, int8_t *q,
+                          float *s) {
+    mm_quant_w_args a = {src, q, s, (int)rows, (int)K};
+    return mm_launch(c, K_QUANT_W, (unsigned)((rows + 3) / 4), 1, 1, 256, 0, &a);
+}
+
+static int pack_dev(mm_ctx *c, const int8_t *s0, const int8_t *s1, int8_t *dst, size_t N, size_t K) {
+    mm_pack_i8_args a = {s0, s1, dst, (int)N, (int)K};
+    size_t threads = (N / 16) * (s1 ? 2 : 1) * (K / 64) * 64;
+    size_t blocks = (threads + 255) / 256;
+    if (blocks > 65535) blocks = 65535;
+    return mm_launch(c, K_PACK_I8, (unsigned)blocks, 1, 1, 256, 0, &a);
+}
+
+/* Quantise every expert matrix per output channel (s = max|w|/127) and pack
+ * it into MFMA fragment order (kernel_params.h, mm_i8_weights). */
+static int load_int8(mm_ctx *c, mm_moe_layer *L, const mm_moe_layer_weights *w, int dev) {
+    const mm_moe_config *g = &c->moe;
+    const size_t H = g->hidden_size, E = g->n_routed_experts, I = g->moe_inter_size;
+    const size_t S = (size_t)g->n_shared_experts * I;
+    const size_t ne = I * H;
+    const size_t gu_b = 2 * E * ne, d_b = E * ne, sgu_b = 2 * S * H, sd_b = S * H;
+    const size_t nsc = 2 * E * I + E * H + 2 * S + H;
+    int st = MM_OK;
+    MM_HIP(hipMalloc((void **)&L->i8_pool, gu_b + d_b + sgu_b + sd_b));
+    MM_HIP(hipMalloc((void **)&L->i8_scales, nsc * sizeof(float)));
+    mm_i8_weights *q = &L->i8;
+    q->gu = L->i8_pool;
+    q->d = q->gu + gu_b;
+    q->sgu = q->d + d_b;
+    q->sdn = q->sgu + sgu_b;
+    float *sc = L->i8_scales;
+    q->s_g = sc;
+    q->s_u = sc + E * I;
+    q->s_d = sc + 2 * E * I;
+    q->ss_g = sc + 2 * E * I + E * H;
+    q->ss_u = q->ss_g + S;
+    q->ss_d = q->ss_u + S;
+
+    const size_t fam = E * ne > S * H ? E * ne : S * H;
+    uint16_t *tb = NULL;
+    int8_t *t0 = NULL, *t1 = NULL;
+    if (hipMalloc((void **)&tb, fam * 2) != hipSuccess || hipMalloc((void **)&t0, fam) != hipSuccess ||
+        hipMalloc((void **)&t1, fam) != hipSuccess) {
+        st = mm_fail(MM_ERR_NOMEM, "mm_moe_load_layer: int8 staging buffers");
+        goto out;
+    }
+    /* routed gate / up: [E*I, H] rows, interleaved per 16-row block */
+    const uint16_t *src;
+    if (L->eg) src = L->eg;
+    else if (!(st = gather_family(c, tb, w->expert_gate, E, ne, dev))) src = tb;
+    if (st || (st = quant_rows_dev(c, src, E * I, H, t0, (float *)q->s_g))) goto out;
+    if (L->eu) src = L->eu;
+    else if (!(st = gather_family(c, tb, w->expert_up, E, ne, dev))) src = tb;
+    if (st || (st = quant_rows_dev(c, src, E * I, H, t1, (float *)q->s_u))) goto out;
+    for (size_t e = 0; e < E && !st; e++)
+        st = pack_dev(c, t0 + e * ne, t1 + e * ne, (int8_t *)q->gu + e * 2 * ne, I, H);
+    if (st) goto out;
+    /* routed down: [E*H, I] */
+    if (L->ed) src = L->ed;
+    else if (!(st = gather_family(c, tb, w->expert_down, E, ne, dev))) src = tb;
+    if (st || (st = quant_rows_dev(c, src, E * H, I, t0, (float *)q->s_d))) goto out;
+    for (size_t e = 0; e < E && !st; e++)
+        st = pack_dev(c, t0 + e * ne, NULL, (int8_t *)q->d + e * ne, H, I);
+    if (st) goto out;
+    /* shared expert */
+    if (S) {
+        if (L->sg) src = L->sg;
+        else if (!(st = upload(c, tb, w->shared_gate, S * H * 2, dev))) src = tb;
+        if (st || (st = quant_rows_dev(c, src, S, H, t0, (float *)q->ss_g))) goto out;
+        if (L->su) src = L->su;
+        else if (!(st = upload(c, tb, w->shared_up, S * H * 2, dev))) src = tb;
+        if (st || (st = quant_rows_dev(c, src, S, H, t1, (float *)q->ss_u))) goto out;
+        if ((st = pack_dev(c, t0, t1, (int8_t *)q->sgu, S, H))) goto out;
+        if (L->sd) src = L->sd;
+        else if (!(st = upload(c, tb, w->shared_down, S * H * 2, dev))) src = tb;
+        if (st || (st = quant_rows_dev(c, src, H, S, t0, (float *)q->ss_d))) goto out;
+        if ((st = pack_dev(c, t0, NULL, (int8_t *)q->sdn, H, S))) goto out;
+    }
+out:;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (tb) hipFree(tb);
+    if (t0) hipFree(t0);
+    if (t1) hipFree(t1);
+    if (!st && e != hipSuccess) st = mm_hip_fail(e, "mm_moe_load_layer(int8)");
+    return st;
+}
+
 int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsigned flags) {
     if (!c || !w) return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: NULL argument");
     if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer: call mm_moe_init first");
@@ -63,8 +172,10 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: layer %d out of range", layer);
     if (!(flags & (MM_LOAD_BF16 | MM_LOAD_INT8)))
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: no weight format requested");
-    if (flags & MM_LOAD_INT8)
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_load_layer: int8 format not built yet");
+    if ((flags & MM_LOAD_INT8) &&
+        (c->moe.hidden_size % 64 || c->moe.moe_inter_size % 64))
+        return mm_fail(MM_ERR_UNSUPPORTED,
+                       "mm_moe_load_layer: int8 format needs hidden and moe_inter multiples of 64");
     if (!w->moe_gate || !w->expert_gate || !w->expert_up || !w->expert_down)
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: NULL weight pointer");
     int st = mm_set_device(c);
@@ -114,6 +225,9 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
         }
         if (st) goto out;
     }
+    if (flags & MM_LOAD_INT8) {
+        if ((st = load_int8(c, L, w, dev))) goto out;
+    }
     L->formats = flags & (MM_LOAD_BF16 | MM_LOAD_INT8);
     L->loaded = 1;
 out:;
@@ -123,6 +237,21 @@ out:;
     return st;
 }
 
+/* ---- workspace planning --------------------------------------------------- */
+
+typedef struct {
+    size_t off;
+} mm_plan;
+
+/* Reserve `bytes` (256-byte aligned) in the plan; returns the offset. */
+static size_t plan_take(mm_plan *p, size_t bytes) {
+    size_t o = p->off;
+    p->off = (o + bytes + 255) & ~(size_t)255;
+    return o;
+}
+
+/* ---- bf16 forward ------------------------------------------------------------ */
+
 /* bf16 weights, GEMV stages (kernels/moe_bf16.hip), BF16_NT_MAX tokens per pass. */
 static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc) {
@@ -130,10 +259,16 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const int H = g->hidden_size, E = g->n_routed_experts, K = g->n_experts_per_tok;
     const int I = g->moe_inter_size, S = g->n_shared_experts * I;
     const size_t hw = (size_t)K * I + S;
-    void *ws;
-    int st = mm_workspace(c, (size_t)BF16_NT_MAX * hw * sizeof(float), &ws);
+    mm_plan p = {0};
+    const size_t o_h = plan_take(&p, (size_t)BF16_NT_MAX * hw * sizeof(float));
+    const size_t o_i = plan_take(&p, (size_t)T * K * sizeof(int32_t));
+    const size_t o_w = plan_take(&p, (size_t)T * K * sizeof(float));
+    char *ws;
+    int st = mm_workspace(c, p.off, (void **)&ws);
     if (st) return st;
-    float *hcat = ws;
+    float *hcat = (float *)(ws + o_h);
+    if (!idx) idx = (int32_t *)(ws + o_i);
+    if (!wts) wts = (float *)(ws + o_w);
     for (int t0 = 0; t0 < T; t0 += BF16_NT_MAX) {
         const int Tc = T - t0 < BF16_NT_MAX ? T - t0 : BF16_NT_MAX;
         mm_gu_bf16_args a;
@@ -181,47 +316,156 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     return MM_OK;
 }
 
-/* Device scratch for the routing results the caller did not ask for. */
-static int routing_scratch(mm_ctx *c, int T, int32_t **idx, float **w) {
-    const int K = c->moe.n_experts_per_tok, H = c->moe.hidden_size;
-    const int I = c->moe.moe_inter_size, S = c->moe.n_shared_experts * I;
-    const size_t hbytes = (size_t)BF16_NT_MAX * ((size_t)K * I + S) * sizeof(float);
-    const size_t rbytes = (size_t)T * K * (sizeof(int32_t) + sizeof(float));
-    (void)H;
-    void *ws;
-    int st = mm_workspace(c, hbytes + rbytes, &ws);
+/* ---- int8 forward ----------------------------------------------------------- */
+
+static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
+                        const float *logits, int32_t *idx, float *wts, float *probs, int acc,
+                        const mm_moe_i8_debug *dbg) {
+    const mm_moe_config *g = &c->moe;
+    const size_t H = g->hidden_size, E = g->n_routed_experts, K = g->n_experts_per_tok;
+    const size_t I = g->moe_inter_size, S = (size_t)g->n_shared_experts * I;
+    const size_t R = (size_t)T * K;   /* routed rows */
+    mm_plan p = {0};
+    const size_t o_rows = plan_take(&p, E * T * 4), o_qx = plan_take(&p, (size_t)T * H);
+    const size_t o_sx = plan_take(&p, (size_t)T * 4), o_h = plan_take(&p, R * I * 4);
+    const size_t o_hs = plan_take(&p, (size_t)T * S * 4), o_qh = plan_take(&p, R * I);
+    const size_t o_sh = plan_take(&p, R * 4), o_qhs = plan_take(&p, (size_t)T * S);
+    const size_t o_shs = plan_take(&p, (size_t)T * 4), o_y = plan_take(&p, R * H * 4);
+    const size_t o_ys = plan_take(&p, (size_t)T * H * 4), o_i = plan_take(&p, R * 4);
+    const size_t o_w = plan_take(&p, R * 4);
+    char *ws;
+    int st = mm_workspace(c, p.off, (void **)&ws);
     if (st) return st;
-    char *p = (char *)ws + hbytes;
-    if (!*idx) *idx = (int32_t *)p;
-    if (!*w) *w = (float *)(p + (size_t)T * K * sizeof(int32_t));
+    if (!idx) idx = (int32_t *)(ws + o_i);
+    if (!wts) wts = (float *)(ws + o_w);
+    int32_t *rows = (int32_t *)(ws + o_rows);
+    int8_t *qx = (int8_t *)(ws + o_qx), *qh = (int8_t *)(ws + o_qh), *qhs = (int8_t *)(ws + o_qhs);
+    float *sx = (float *)(ws + o_sx), *h = (float *)(ws + o_h), *hs = (float *)(ws + o_hs);
+    float *sh = (float *)(ws + o_sh), *shs = (float *)(ws + o_shs);
+    float *y = (float *)(ws + o_y), *ys = (float *)(ws + o_ys);
+
+    mm_i8_route_args ra;
+    memset(&ra, 0, sizeof(ra));
+    ra.r.x = xn;
+    ra.r.wgT = L->wgT;
+    ra.r.logits_in = logits;
+    ra.r.bias = L->bias;
+    ra.r.probs = probs;
+    ra.r.topk_idx = idx;
+    ra.r.topk_w = wts;
+    ra.r.T = T;
+    ra.r.H = (int)H;
+    ra.r.E = (int)E;
+    ra.r.K = (int)K;
+    ra.r.sigmoid = g->router_sigmoid;
+    ra.r.norm_topk = g->norm_topk;
+    ra.r.scale = g->routed_scaling;
+    ra.cnt = c->moe_cnt;
+    ra.rows = rows;
+    ra.x = xn;
+    ra.qx = qx;
+    ra.sx = sx;
+    if ((st = mm_launch(c, K_I8_ROUTE, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK,
+                        1, 1, 256, 0, &ra)))
+        return st;
+
+    mm_i8_gemm_args ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.w = L->i8;
+    ga.cnt = c->moe_cnt;
+    ga.rows = rows;
+    ga.a = qx;
+    ga.sa = sx;
+    ga.h = h;
+    ga.hs = hs;
+    ga.dbg_acc = dbg ? dbg->acc_gu : NULL;
+    ga.T = T;
+    ga.H = (int)H;
+    ga.I = (int)I;
+    ga.S = (int)S;
+    ga.E = (int)E;
+    ga.K = (int)K;
+    ga.wg_per_expert = (int)((I + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+    unsigned nb = (unsigned)(E * ga.wg_per_expert + (S + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+    if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 256, 0, &ga))) return st;
+
+    mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
+                                S ? T : 0, (int)S};
+    if ((st = mm_launch(c, K_I8_QUANT_H, (unsigned)((R + (S ? T : 0) + 3) / 4), 1, 1, 256, 0, &qa)))
+        return st;
+
+    ga.a = qh;
+    ga.sa = sh;
+    ga.a_sh = qhs;
+    ga.sa_sh = shs;
+    ga.y = y;
+    ga.ys = ys;
+    ga.dbg_acc = dbg ? dbg->acc_d : NULL;
+    ga.wg_per_expert = (int)((H + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+    nb = (unsigned)(E * ga.wg_per_expert + (S ? ga.wg_per_expert : 0));
+    if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 256, 0, &ga))) return st;
+
+    mm_i8_combine_args ca = {y, ys, wts, out, c->moe_cnt, T, (int)H, (int)K, (int)E, acc, S > 0};
+    if ((st = mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca))) return st;
+
+    if (dbg) {
+        struct {
+            void *dst;
+            const void *src;
+            size_t n;
+        } cp[] = {{dbg->qx, qx, (size_t)T * H},       {dbg->sx, sx, (size_t)T * 4},
+                  {dbg->h, h, R * I * 4},             {dbg->qh, qh, R * I},
+                  {dbg->sh, sh, R * 4},               {dbg->y, y, R * H * 4},
+                  {dbg->hs, hs, (size_t)T * S * 4},   {dbg->qhs, qhs, (size_t)T * S},
+                  {dbg->shs, shs, (size_t)T * 4},     {dbg->ys, ys, (size_t)T * H * 4}};
+        for (size_t i = 0; i < sizeof(cp) / sizeof(cp[0]); i++)
+            if (cp[i].dst && cp[i].n)
+                MM_HIP(hipMemcpyAsync(cp[i].dst, cp[i].src, cp[i].n, hipMemcpyDeviceToDevice,
+                                      c->stream));
+    }
     return MM_OK;
+}
+
+static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, const float *logits,
+                   int32_t *topk_idx, float *topk_w, float *probs, unsigned flags,
+                   const mm_moe_i8_debug *dbg) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: NULL context");
+    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_forward: call mm_moe_init first");
+    if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded)
+        return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d not loaded", layer);
+    if (T < 0 || !out || (!xn && T > 0))
+        return mm_fail(MM_ERR_INVALID, "mm_moe_forward: bad arguments");
+    if (T == 0) return MM_OK;
+    if ((uintptr_t)xn % 16 || (uintptr_t)out % 16)
+        return mm_fail(MM_ERR_INVALID, "mm_moe_forward: xn/out must be 16-byte aligned");
+    const mm_moe_layer *L = &c->layers[layer];
+    int st = mm_set_device(c);
+    if (st) return st;
+    const int acc = (flags & MM_FWD_ACCUMULATE) != 0;
+    if (flags & MM_FWD_INT8) {
+        if (!(L->formats & MM_LOAD_INT8))
+            return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no int8 weights", layer);
+        return forward_int8(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc, dbg);
+    }
+    if (dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: debug outputs need MM_FWD_INT8");
+    if (!(L->formats & MM_LOAD_BF16))
+        return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no bf16 weights", layer);
+    if (xn == out) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: bf16 path needs out != xn");
+    return forward_bf16(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc);
 }
 
 int mm_moe_forward_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags) {
-    if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward_dev: NULL context");
-    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_forward_dev: call mm_moe_init first");
-    if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded)
-        return mm_fail(MM_ERR_STATE, "mm_moe_forward_dev: layer %d not loaded", layer);
-    if (T < 0 || !out || (!xn && T > 0))
-        return mm_fail(MM_ERR_INVALID, "mm_moe_forward_dev: bad arguments");
-    if (T == 0) return MM_OK;
-    if ((uintptr_t)xn % 16 || (uintptr_t)out % 16)
-        return mm_fail(MM_ERR_INVALID, "mm_moe_forward_dev: xn/out must be 16-byte aligned");
-    const mm_moe_layer *L = &c->layers[layer];
-    int st = mm_set_device(c);
-    if (st) return st;
-    const int acc = (flags & MM_FWD_ACCUMULATE) != 0;
-    if (flags & MM_FWD_INT8)
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_forward_dev: int8 path not built yet");
-    if (!(L->formats & MM_LOAD_BF16))
-        return mm_fail(MM_ERR_STATE, "mm_moe_forward_dev: layer %d has no bf16 weights", layer);
-    if (xn == out) return mm_fail(MM_ERR_INVALID, "mm_moe_forward_dev: bf16 path needs out != xn");
-    int32_t *idx = topk_idx;
-    float *w = topk_w;
-    if ((st = routing_scratch(c, T, &idx, &w))) return st;
-    return forward_bf16(c, L, T, xn, out, logits, idx, w, probs, acc);
+    return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags, NULL);
+}
+
+int mm_moe_forward_i8_debug_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,
+                                const float *logits, int32_t *topk_idx, float *topk_w,
+                                float *probs, unsigned flags, const mm_moe_i8_debug *dbg) {
+    if (!dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward_i8_debug_dev: NULL debug block");
+    return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags | MM_FWD_INT8,
+                   dbg);
 }
 
 int mm_ffn_compute(mm_ctx *c, int layer, const float *xn, float *out, int *topk_idx,

@@ -74,3 +74,83 @@ typedef struct {
 } mm_transpose_gate_args;
 
 #endif
+
+/* ---- int8 MoE path ------------------------------------------------------ */
+
+/* Per-layer int8 weights in MFMA fragment order.  A "fragment" is the
+ * 16-row x 64-column int8 block one v_mfma_i32_16x16x64_i8 consumes as its
+ * B operand: 1 KB, lane l holding row (l % 16), columns 16*(l/16) .. +15.
+ *   gu   [E][I/16][2][H/64] fragments: gate rows then up rows of each
+ *        16-row block (the SwiGLU pair of an output column block)
+ *   d    [E][H/16][I/64] fragments of the down projection
+ *   sgu  [S/16][2][H/64], sd_ [H/16][S/64] for the shared expert */
+typedef struct {
+    const int8_t *gu, *d, *sgu, *sdn;
+    const float *s_g, *s_u, *s_d;       /* [E, I], [E, I], [E, H] */
+    const float *ss_g, *ss_u, *ss_d;    /* [S], [S], [H] */
+} mm_i8_weights;
+
+/* Routing + per-token activation quantisation. */
+typedef struct {
+    mm_router_args r;
+    int32_t *cnt;            /* [E] rows per expert (zero on entry) */
+    int32_t *rows;           /* [E, T] route ids (t*K + r) per expert */
+    const float *x;          /* [T, H] */
+    int8_t *qx;              /* [T, H] */
+    float *sx;               /* [T] */
+} mm_i8_route_args;
+
+/* Grouped int8 GEMM over experts 0..E-1 (routed) and the shared expert. */
+typedef struct {
+    mm_i8_weights w;
+    const int32_t *cnt;      /* [E] */
+    const int32_t *rows;     /* [E, T] */
+    const int8_t *a;         /* gate/up: qx [T, H];  down: qh [T*K, I] */
+    const float *sa;         /* gate/up: sx [T];     down: sh [T*K] */
+    const int8_t *a_sh;      /* down: shared qhs [T, S] */
+    const float *sa_sh;      /* down: shared shs [T] */
+    float *h;                /* gate/up out: routed [T*K, I] */
+    float *hs;               /* gate/up out: shared [T, S] */
+    float *y;                /* down out: routed [T*K, H] */
+    float *ys;               /* down out: shared [T, H] */
+    int32_t *dbg_acc;        /* debug: raw accumulators, gate/up [T*K, 2, I], down [T*K, H], or 0 */
+    int T, H, I, S, E, K;
+    int wg_per_expert;       /* blocks per routed expert */
+} mm_i8_gemm_args;
+
+/* Per-row quantisation of the SwiGLU output. */
+typedef struct {
+    const float *h;          /* [rows, n] */
+    int8_t *q;
+    float *s;
+    int rows, n;
+    const float *h2;         /* second region (shared expert) or 0 */
+    int8_t *q2;
+    float *s2;
+    int rows2, n2;
+} mm_i8_quant_rows_args;
+
+/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]; also re-zeroes cnt. */
+typedef struct {
+    const float *y, *ys;
+    const float *topk_w;
+    float *out;
+    int32_t *cnt;
+    int T, H, K, E;
+    int accumulate;
+    int has_shared;
+} mm_i8_combine_args;
+
+/* Pack a row-major int8 [N, K] matrix into 16x64 fragments, optionally
+ * interleaving two matrices per 16-row block (gate/up). */
+typedef struct {
+    const int8_t *src0, *src1;   /* src1 = 0: no interleave */
+    int8_t *dst;
+    int N, K;
+} mm_pack_i8_args;
+
+/* Launch geometry shared by the int8 GEMM kernels and the host: 4 waves per
+ * block, 2 sixteen-column blocks per wave. */
+#define MM_I8_WAVES 4
+#define MM_I8_NBW 2
+#define MM_I8_COLS_PER_WG (MM_I8_WAVES * MM_I8_NBW * 16)

@@ -1,0 +1,304 @@
+/* moe_i8.hip -- MoE expert FFN with int8 weights and int8 activations on
+ * v_mfma_i32_16x16x64_i8 (int32 accumulation).
+ *
+ * Semantics follow ffn_compute (src/run.c:116-162) with each expert matmul
+ * replaced by: per-token int8 activations (s = max|x|/127, q = rint(x/s)),
+ * per-output-channel int8 weights (same rule), exact int32 dot products,
+ * dequantisation ((float)acc * s_a) * s_w, SwiGLU in fp32, per-route int8
+ * quantisation of the hidden row, int8 down projection, and the combine of
+ * run.c:151-160 in slot order with the shared expert last.
+ *
+ * Kernels, in launch order:
+ *   mm_i8_route    router (router.h), per-expert row lists built with one
+ *                  atomic slot per route, per-token quantisation of x
+ *   mm_i8_gu       grouped gate/up GEMM + SwiGLU epilogue -> h (fp32)
+ *   mm_i8_quant_h  per-row quantisation of h -> qh, sh
+ *   mm_i8_down     grouped down GEMM -> y per route (fp32)
+ *   mm_i8_combine  out[t] = sum_r w_r * y[t, r] + y_shared[t]
+ *
+ * The order of rows inside an expert's list depends on atomic timing, but
+ * every row is computed independently and written to its own route slot,
+ * so results do not depend on it.
+ *
+ * MFMA operand layout (16x16x64 i8): lane l supplies row (l % 16) of the
+ * A operand and column (l % 16) of the B operand, bytes 16*(l/16) .. +15 of
+ * the 64-wide K step, for both; the int32 result element i of lane l is
+ * D[4*(l/16) + i][l % 16].  Weights are pre-packed so that a wave's B
+ * operand for one K step is one contiguous 1 KB block (kernel_params.h).
+ */
+#include "router.h"
+
+#define I8_WAVES MM_I8_WAVES
+#define I8_NBW MM_I8_NBW
+#define I8_MT 4        /* 16-row tiles per pass (64 rows) */
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4i ldg16(const int8_t *p) {
+    return __builtin_nontemporal_load((const v4i *)p);
+}
+
+/* ---- routing + activation quantisation ----------------------------------- */
+
+/* s = max|x| / 127; q = clamp(rint(x / s), -127, 127), IEEE division and
+ * round-half-even, identical to the CPU quantiser.  One wave, n % 4 == 0. */
+__device__ __forceinline__ void quant_row_wave(const float *x, int n, int8_t *q, float *s) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    float amax = 0.0f;
+    for (int i = lane * 4; i < n; i += MM_WAVE * 4) {
+        f32x4 v = *(const f32x4 *)(x + i);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    amax = wave_max(amax);
+    const float sc = amax / 127.0f;
+    if (lane == 0) *s = sc;
+    for (int i = lane * 4; i < n; i += MM_WAVE * 4) {
+        f32x4 v = *(const f32x4 *)(x + i);
+        int b[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(v[j] / sc), -127.0f), 127.0f);
+            b[j] = (int)r & 0xff;
+        }
+        *(uint32_t *)(q + i) = (uint32_t)(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_route(mm_i8_route_args a) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    router_block(a.r, blockIdx.x, [&](int tok, const int *idx, const float *) {
+        int e = 0;
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (lane == r) e = idx[r];
+        if (lane < a.r.K) {
+            int pos = atomicAdd(&a.cnt[e], 1);
+            if (pos < a.r.T) a.rows[(size_t)e * a.r.T + pos] = tok * a.r.K + lane;
+        }
+        quant_row_wave(a.x + (size_t)tok * a.r.H, a.r.H, a.qx + (size_t)tok * a.r.H,
+                       a.sx + tok);
+    });
+}
+
+/* ---- grouped GEMM ---------------------------------------------------------- */
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+/* One pass of up to I8_MT*16 rows against this wave's I8_NBW column blocks.
+ * GU: gate/up pair per column block (B fragments interleaved), SwiGLU
+ * epilogue; otherwise a plain GEMM with a dequantising epilogue.
+ *   arow(m) -> pointer to row m of A (int8, K bytes), only called for m < M
+ *   epi(m, col, acc0, acc1) consumes the int32 results of row m, column col */
+template <bool GU, class ARow, class Epi>
+__device__ __forceinline__ void gemm_pass(const int8_t *bbase, int nb0, int nbl, int KB, int m0,
+                                          int M, ARow arow, Epi epi) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int NB_STRIDE = (GU ? 2 : 1) * KB * 1024;
+    const int nmt = min(I8_MT, (M - m0 + 15) >> 4);
+    const int8_t *ap[I8_MT];
+    bool av[I8_MT];
+#pragma unroll
+    for (int mi = 0; mi < I8_MT; mi++) {
+        const int m = m0 + mi * 16 + (lane & 15);
+        av[mi] = mi < nmt && m < M;
+        ap[mi] = (av[mi] ? arow(m) : arow(m0)) + 16 * (lane >> 4);
+    }
+    const int8_t *bp[I8_NBW];
+#pragma unroll
+    for (int j = 0; j < I8_NBW; j++)
+        bp[j] = bbase + (size_t)min(nb0 + j, nbl - 1) * NB_STRIDE + lane * 16;
+
+    v4i acc0[I8_MT][I8_NBW], acc1[I8_MT][I8_NBW];
+#pragma unroll
+    for (int mi = 0; mi < I8_MT; mi++)
+#pragma unroll
+        for (int j = 0; j < I8_NBW; j++) {
+            acc0[mi][j] = (v4i){0, 0, 0, 0};
+            acc1[mi][j] = (v4i){0, 0, 0, 0};
+        }
+
+#pragma unroll 2
+    for (int kb = 0; kb < KB; kb++) {
+        v4i b0[I8_NBW], b1[I8_NBW], av_[I8_MT];
+#pragma unroll
+        for (int j = 0; j < I8_NBW; j++) {
+            b0[j] = ldg16(bp[j] + kb * 1024);
+            if (GU) b1[j] = ldg16(bp[j] + (KB + kb) * 1024);
+        }
+#pragma unroll
+        for (int mi = 0; mi < I8_MT; mi++) {
+            if (mi < nmt) {
+                av_[mi] = *(const v4i *)(ap[mi] + kb * 64);
+                if (!av[mi]) av_[mi] = (v4i){0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < I8_MT; mi++) {
+            if (mi < nmt) {
+#pragma unroll
+                for (int j = 0; j < I8_NBW; j++) {
+                    acc0[mi][j] = mfma_i8(av_[mi], b0[j], acc0[mi][j]);
+                    if (GU) acc1[mi][j] = mfma_i8(av_[mi], b1[j], acc1[mi][j]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < I8_MT; mi++) {
+        if (mi < nmt) {
+#pragma unroll
+            for (int j = 0; j < I8_NBW; j++) {
+                if (nb0 + j < nbl) {
+                    const int col = (nb0 + j) * 16 + (lane & 15);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
+                        if (m < M) epi(m, col, acc0[mi][j][i], acc1[mi][j][i]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int KB = a.H / 64;
+    const int routed_blocks = a.E * a.wg_per_expert;
+    const int b = blockIdx.x;
+    if (b < routed_blocks) {
+        const int e = b / a.wg_per_expert, wgi = b % a.wg_per_expert;
+        const int M = min(a.cnt[e], a.T);
+        const int nbl = a.I / 16;
+        const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
+        if (M == 0 || nb0 >= nbl) return;
+        const int32_t *rows = a.rows + (size_t)e * a.T;
+        const int8_t *bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
+        const float *sg = a.w.s_g + (size_t)e * a.I, *su = a.w.s_u + (size_t)e * a.I;
+        for (int m0 = 0; m0 < M; m0 += I8_MT * 16) {
+            gemm_pass<true>(
+                bbase, nb0, nbl, KB, m0, M,
+                [&](int m) { return a.a + (size_t)(rows[m] / a.K) * a.H; },
+                [&](int m, int col, int32_t ag, int32_t au) {
+                    const int rid = rows[m];
+                    const float sx = a.sa[rid / a.K];
+                    const float g = ((float)ag * sx) * sg[col];
+                    const float u = ((float)au * sx) * su[col];
+                    a.h[(size_t)rid * a.I + col] = silu_mul(g, u);
+                    if (a.dbg_acc) {
+                        a.dbg_acc[((size_t)rid * 2) * a.I + col] = ag;
+                        a.dbg_acc[((size_t)rid * 2 + 1) * a.I + col] = au;
+                    }
+                });
+        }
+    } else {
+        const int sb = b - routed_blocks;
+        const int nbl = a.S / 16;
+        const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
+        if (nb0 >= nbl) return;
+        for (int m0 = 0; m0 < a.T; m0 += I8_MT * 16) {
+            gemm_pass<true>(
+                a.w.sgu, nb0, nbl, KB, m0, a.T,
+                [&](int m) { return a.a + (size_t)m * a.H; },
+                [&](int m, int col, int32_t ag, int32_t au) {
+                    const float sx = a.sa[m];
+                    const float g = ((float)ag * sx) * a.w.ss_g[col];
+                    const float u = ((float)au * sx) * a.w.ss_u[col];
+                    a.hs[(size_t)m * a.S + col] = silu_mul(g, u);
+                });
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int routed_blocks = a.E * a.wg_per_expert;
+    const int nbl = a.H / 16;
+    const int b = blockIdx.x;
+    if (b < routed_blocks) {
+        const int e = b / a.wg_per_expert, wgi = b % a.wg_per_expert;
+        const int M = min(a.cnt[e], a.T);
+        const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
+        if (M == 0 || nb0 >= nbl) return;
+        const int KB = a.I / 64;
+        const int32_t *rows = a.rows + (size_t)e * a.T;
+        const int8_t *bbase = a.w.d + (size_t)e * nbl * KB * 1024;
+        const float *sd = a.w.s_d + (size_t)e * a.H;
+        for (int m0 = 0; m0 < M; m0 += I8_MT * 16) {
+            gemm_pass<false>(
+                bbase, nb0, nbl, KB, m0, M,
+                [&](int m) { return a.a + (size_t)rows[m] * a.I; },
+                [&](int m, int col, int32_t acc, int32_t) {
+                    const int rid = rows[m];
+                    a.y[(size_t)rid * a.H + col] = ((float)acc * a.sa[rid]) * sd[col];
+                    if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.H + col] = acc;
+                });
+        }
+    } else {
+        const int sb = b - routed_blocks;
+        const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
+        if (nb0 >= nbl) return;
+        const int KB = a.S / 64;
+        for (int m0 = 0; m0 < a.T; m0 += I8_MT * 16) {
+            gemm_pass<false>(
+                a.w.sdn, nb0, nbl, KB, m0, a.T,
+                [&](int m) { return a.a_sh + (size_t)m * a.S; },
+                [&](int m, int col, int32_t acc, int32_t) {
+                    a.ys[(size_t)m * a.H + col] = ((float)acc * a.sa_sh[m]) * a.w.ss_d[col];
+                });
+        }
+    }
+}
+
+/* ---- hidden-row quantisation and combine ------------------------------------- */
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_quant_h(mm_i8_quant_rows_args a) {
+    const int row = blockIdx.x * (blockDim.x / MM_WAVE) + threadIdx.x / MM_WAVE;
+    if (row < a.rows)
+        quant_row_wave(a.h + (size_t)row * a.n, a.n, a.q + (size_t)row * a.n, a.s + row);
+    else if (row - a.rows < a.rows2) {
+        const int r = row - a.rows;
+        quant_row_wave(a.h2 + (size_t)r * a.n2, a.n2, a.q2 + (size_t)r * a.n2, a.s2 + r);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_args a) {
+    const int t = blockIdx.x;
+    const float *w = a.topk_w + (size_t)t * a.K;
+    for (int n = threadIdx.x * 4; n < a.H; n += blockDim.x * 4) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < a.K; r++) {
+            const f32x4 y = *(const f32x4 *)(a.y + ((size_t)t * a.K + r) * a.H + n);
+            acc += w[r] * y;
+        }
+        if (a.has_shared) acc += *(const f32x4 *)(a.ys + (size_t)t * a.H + n);
+        f32x4 *o = (f32x4 *)(a.out + (size_t)t * a.H + n);
+        *o = a.accumulate ? *o + acc : acc;
+    }
+    if (t == 0)
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
+}
+
+/* ---- weight packing ----------------------------------------------------------- */
+
+/* One thread per 16-byte lane slice of a fragment. */
+extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) {
+    const int KB = a.K / 64, NB = a.N / 16, NS = a.src1 ? 2 : 1;
+    const size_t total = (size_t)NB * NS * KB * 64;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i & 63);
+        const size_t f = i >> 6;
+        const int kb = (int)(f % KB);
+        const int which = (int)((f / KB) % NS);
+        const int nb = (int)(f / ((size_t)KB * NS));
+        const int8_t *src = which ? a.src1 : a.src0;
+        const size_t row = (size_t)nb * 16 + (lane & 15);
+        const size_t col = (size_t)kb * 64 + 16 * (lane >> 4);
+        *(v4i *)(a.dst + i * 16) = *(const v4i *)(src + row * a.K + col);
+    }
+}

@@ -23,8 +23,15 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-template <int EJ, int TPW>
-__device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id) {
+struct router_no_post {
+    __device__ void operator()(int, const int *, const float *) const {}
+};
+
+/* Routes tokens [wave_id*TPW, wave_id*TPW + TPW) and then calls
+ * post(token, idx, w) with the wave-uniform selection of each token. */
+template <int EJ, int TPW, class Post = router_no_post>
+__device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id,
+                                            Post post = Post()) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int t0 = wave_id * TPW;
     if (t0 >= a.T) return;
@@ -176,6 +183,7 @@ __device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id
                     a.topk_w[(size_t)tok * K + r] = w[r];
                 }
         }
+        post(tok, idx, w);
     }
 }
 
@@ -183,13 +191,15 @@ __device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id
 #define MM_ROUTER_WAVES 4
 
 /* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_WAVES * TPW tokens. */
-__device__ __forceinline__ void router_block(const mm_router_args &a, int block) {
+template <class Post = router_no_post>
+__device__ __forceinline__ void router_block(const mm_router_args &a, int block,
+                                             Post post = Post()) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int wid = block * MM_ROUTER_WAVES + wave;
     if (a.E <= 64)
-        router_wave<1, MM_ROUTER_TPW>(a, wid);
+        router_wave<1, MM_ROUTER_TPW>(a, wid, post);
     else if (a.E <= 128)
-        router_wave<2, MM_ROUTER_TPW>(a, wid);
+        router_wave<2, MM_ROUTER_TPW>(a, wid, post);
     else
-        router_wave<4, MM_ROUTER_TPW>(a, wid);
+        router_wave<4, MM_ROUTER_TPW>(a, wid, post);
 }

@@ -46,6 +46,11 @@ class MoeLayerWeights(C.Structure):
                 ("shared_gate", _vp), ("shared_up", _vp), ("shared_down", _vp)]
 
 
+class MoeI8Debug(C.Structure):
+    _fields_ = [(n, _vp) for n in ("qx", "sx", "acc_gu", "h", "qh", "sh", "acc_d", "y", "hs",
+                                   "qhs", "shs", "ys")]
+
+
 _lib = None
 
 
@@ -86,6 +91,8 @@ def lib():
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
         L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_moe_forward_i8_debug_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
+                                                  _vp, _vp, C.c_uint, C.POINTER(MoeI8Debug)]
         _lib = L
     return _lib
 
@@ -252,6 +259,39 @@ class Context:
             for b in (dx, dout, didx, dw, dp, dl):
                 if b is not None:
                     b.free()
+
+    def moe_forward_i8_debug(self, layer, xn, logits=None, flags=MM_FWD_INT8):
+        """int8 forward returning (out, idx, w, probs, intermediates dict)."""
+        cfg = self._moe_cfg
+        xn = np.ascontiguousarray(xn, np.float32)
+        T = xn.shape[0]
+        E, K, H = cfg.n_routed_experts, cfg.n_experts_per_tok, cfg.hidden_size
+        I = cfg.moe_inter_size
+        S = cfg.n_shared_experts * I
+        R = T * K
+        shapes = dict(qx=((T, H), np.int8), sx=((T,), np.float32),
+                      acc_gu=((R, 2, I), np.int32), h=((R, I), np.float32),
+                      qh=((R, I), np.int8), sh=((R,), np.float32), acc_d=((R, H), np.int32),
+                      y=((R, H), np.float32), hs=((T, max(S, 1)), np.float32),
+                      qhs=((T, max(S, 1)), np.int8), shs=((T,), np.float32),
+                      ys=((T, H), np.float32))
+        bufs = {k: self.empty(shp, dt) for k, (shp, dt) in shapes.items()}
+        dbg = MoeI8Debug(*[bufs[n].ptr for n, _ in MoeI8Debug._fields_])
+        dx = self.to_device(xn)
+        dout = self.empty((T, H), np.float32)
+        didx = self.empty((T, K), np.int32)
+        dw = self.empty((T, K), np.float32)
+        dp = self.empty((T, E), np.float32)
+        dl = self.to_device(np.ascontiguousarray(logits, np.float32)) if logits is not None else None
+        _check(lib().mm_moe_forward_i8_debug_dev(self.h, layer, T, dx.ptr, dout.ptr,
+                                                 dl.ptr if dl else None, didx.ptr, dw.ptr,
+                                                 dp.ptr, flags, C.byref(dbg)))
+        res = {k: b.download() for k, b in bufs.items()}
+        out = (dout.download(), didx.download(), dw.download(), dp.download(), res)
+        for b in list(bufs.values()) + [dx, dout, didx, dw, dp] + ([dl] if dl else []):
+            b.free()
+            self._bufs.remove(b)
+        return out
 
     def ffn_compute(self, layer, xn, flags=MM_FWD_BF16):
         """Mirror of the reference ffn_compute (src/run.c:116) for one token."""

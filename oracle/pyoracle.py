@@ -203,10 +203,13 @@ def quant_rows(x):
 
 def quant_weight(w):
     w = np.ascontiguousarray(w, dtype=np.uint16)
-    N, K = w.shape[-2], w.shape[-1]
-    rows = w.size // K
+    K = w.shape[-1]
     q = np.empty(w.shape, np.int8)
     s = np.empty(w.shape[:-1], np.float32)
+    if w.size == 0:
+        s[...] = 0
+        return q, s
+    rows = w.size // K
     lib().or_quant_weight_i8(_p(w, _u16p), rows, K, _p(q, _i8p), _p(s, _f32p))
     return q, s
 
