@@ -1,0 +1,330 @@
+"""Benchmark of the MI355X mla-moe hot path (one JSON line on stdout).
+
+Default workload: batched decode, B=64 tokens through a
+26-layer stack of DeepSeek-V2-Lite-shaped MoE FFN layers with int8
+per-output-channel weights (from bf16 N(0, 0.02)), uniform-random fp32 router
+logits per layer, residual carried through the stack (x += ffn(x)), weights
+resident in HBM.  A step is one pass of the 64 tokens through the 26 layers.
+
+The same line carries, under "extra", the other MoE configurations measured
+in the same run: config 3 (prefill T=2048, int8, Zipf-skewed routing, router
+GEMV included) and config 1 (T=1 decode layer, bf16 weights).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mla-moe_amd"))
+
+import mlamoe  # noqa: E402
+from mlamoe import synth  # noqa: E402
+
+METRIC = "MoE FFN tok/s; decode HBM GB/s & prefill int8 TOPS vs MI355X roofline"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5033.0        # MI355X dense int8 MFMA (no sparsity)
+G = synth.DSV2                 # H=2048, E=64, K=6, I=1408, n_shared=2
+H, E, K, I, NS = G["H"], G["E"], G["K"], G["I"], G["n_shared"]
+S = NS * I
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def fill_layer_bf16(ctx, bufs, seed):
+    for i, (k, b) in enumerate(bufs.items()):
+        ctx.fill(b, int(np.prod(b.shape)), mlamoe.MM_FILL_BF16_NORMAL, seed * 16 + i, 0.02)
+
+
+def bf16_buffers(ctx):
+    shapes = dict(moe_gate=(E, H), eg=(E, I, H), eu=(E, I, H), ed=(E, H, I), sg=(S, H),
+                  su=(S, H), sd=(H, S))
+    return {k: ctx.empty(v, np.uint16) for k, v in shapes.items()}
+
+
+def load_layers(ctx, n_layers, seed0, flags):
+    """Synthetic bf16 weights generated on the device, then loaded (and
+    quantised for int8) layer by layer through the C-ABI."""
+    ctx.moe_init(H, E, NS, K, I, n_layers=n_layers)
+    bufs = bf16_buffers(ctx)
+    w = dict(bufs)
+    w["moe_gate_bias"] = None
+    for l in range(n_layers):
+        fill_layer_bf16(ctx, bufs, seed0 + l)
+        ctx.moe_load_layer(l, w, flags | mlamoe.MM_LOAD_DEVICE_PTRS)
+    for b in bufs.values():
+        b.free()
+        ctx._bufs.remove(b)
+
+
+def i8_gu_bytes(touched, T, R):
+    """Algorithmic HBM bytes of one mm_i8_gu launch: int8 gate/up weights of
+    the touched experts and the shared expert, their scales, the quantised
+    activations, and the fp32 SwiGLU rows written."""
+    w = touched * 2 * I * H + 2 * S * H
+    sc = touched * 2 * I * 4 + 2 * S * 4
+    act = T * H + T * 4
+    out = R * I * 4 + T * S * 4
+    return w + sc + act + out
+
+
+def i8_layer_bytes(touched, T, R):
+    """Algorithmic HBM bytes of a whole int8 MoE layer (all kernels): every
+    touched expert's int8 weights and scales read once, activations in and
+    out, and the intermediate rows each written and read once."""
+    w = touched * 3 * I * H + 3 * S * H
+    sc = touched * (2 * I + H) * 4 + (2 * S + H) * 4
+    io = 2 * T * H * 4 + T * E * 4
+    inter = (R * I * 4) * 2 + R * I + (T * S * 4) * 2 + T * S + (R * H * 4) * 2 + (T * H * 4) * 2
+    return w + sc + io + inter
+
+
+def kernel_avg_ms(ctx, name):
+    tot, n = ctx.prof_query(name)
+    return tot / max(n, 1), n
+
+
+def timed(ctx, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    ctx.sync()                                    # barrier + synchronize (N = 1)
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for _ in range(steps):
+        fn()
+    ms = ctx.timer_stop()                         # HIP events on the context stream
+    ctx.sync()
+    wall = (time.perf_counter() - t0) * 1e3
+    return ms / steps, wall / steps
+
+
+def profile_kernels(ctx, fn, steps, names):
+    ctx.prof_enable(True)
+    ctx.prof_reset()
+    for _ in range(steps):
+        fn()
+    res = {n: kernel_avg_ms(ctx, n) for n in names}
+    ctx.prof_enable(False)
+    ctx.prof_reset()
+    return res
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+# ---------------------------------------------------------------------------
+
+def bench_decode_i8(ctx, steps, warmup, B=64, L=26):
+    """Config 4: B tokens through L int8 MoE layers, residual carried."""
+    log(f"[decode_i8] loading {L} int8 layers")
+    load_layers(ctx, L, 1000, mlamoe.MM_LOAD_INT8)
+    x0 = ctx.empty((B, H), np.float32)
+    ctx.fill(x0, B * H, mlamoe.MM_FILL_F32_NORMAL, 7, 1.0)
+    x = ctx.empty((B, H), np.float32)
+    logits = [ctx.empty((B, E), np.float32) for _ in range(L)]
+    for l, lg in enumerate(logits):
+        ctx.fill(lg, B * E, mlamoe.MM_FILL_F32_UNIFORM, 500 + l)
+    idx = [ctx.empty((B, K), np.int32) for _ in range(L)]
+    wts = ctx.empty((B, K), np.float32)
+    flags = mlamoe.MM_FWD_INT8 | mlamoe.MM_FWD_ACCUMULATE
+    lib, h = mlamoe.lib(), ctx.h
+
+    def step():
+        mlamoe._check(lib.mm_d2d(h, x.ptr, x0.ptr, B * H * 4))
+        for l in range(L):
+            mlamoe._check(lib.mm_moe_forward_dev(h, l, B, x.ptr, x.ptr, logits[l].ptr,
+                                                 idx[l].ptr, wts.ptr, None, flags))
+    log("[decode_i8] timing")
+    ms, wall = timed(ctx, step, steps, warmup)
+    touched = [len(np.unique(i.download())) for i in idx]
+    R = B * K
+    names = ["mm_i8_route", "mm_i8_gu", "mm_i8_quant_h", "mm_i8_down", "mm_i8_combine"]
+    prof = profile_kernels(ctx, step, max(2, steps // 4), names)
+    gu_ms = prof["mm_i8_gu"][0]
+    gu_bytes = float(np.mean([i8_gu_bytes(t, B, R) for t in touched]))
+    step_bytes = float(sum(i8_layer_bytes(t, B, R) for t in touched))
+    res = dict(
+        ms_per_step=ms, wall_ms_per_step=wall, tok_s=B / (ms * 1e-3),
+        step_gbs=step_bytes / (ms * 1e-3) / 1e9, step_bytes=step_bytes,
+        touched_experts_per_layer=float(np.mean(touched)),
+        kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()},
+        roofline=dict(bound="hbm", kernel="mm_i8_gu",
+                      achieved=gu_bytes / (gu_ms * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
+                      unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=gu_ms * 1e3))
+    res["roofline"]["frac"] = res["roofline"]["achieved"] / HBM_PEAK_GBS
+    res["roofline"]["traffic"] = traffic_from_profiles("mm_i8_gu", "decode_i8")
+    return res
+
+
+def bench_prefill_i8(ctx, steps, warmup, T=2048):
+    """Config 3: T tokens through one int8 layer, router logits W_g x plus a
+    Zipf(1.1) prior computed inside the step."""
+    log("[prefill_i8] loading int8 layer")
+    load_layers(ctx, 1, 3000, mlamoe.MM_LOAD_INT8)
+    x = ctx.empty((T, H), np.float32)
+    ctx.fill(x, T * H, mlamoe.MM_FILL_F32_NORMAL, 11, 1.0)
+    prior = ctx.to_device(synth.zipf_prior(12, E, 1.1))
+    logits = ctx.empty((T, E), np.float32)
+    out = ctx.empty((T, H), np.float32)
+    idx = ctx.empty((T, K), np.int32)
+    wts = ctx.empty((T, K), np.float32)
+    lib, h = mlamoe.lib(), ctx.h
+
+    def step():
+        mlamoe._check(lib.mm_moe_router_logits_dev(h, 0, T, x.ptr, prior.ptr, logits.ptr))
+        mlamoe._check(lib.mm_moe_forward_dev(h, 0, T, x.ptr, out.ptr, logits.ptr, idx.ptr,
+                                             wts.ptr, None, mlamoe.MM_FWD_INT8))
+    log("[prefill_i8] timing")
+    ms, wall = timed(ctx, step, steps, warmup)
+    ii = idx.download()
+    counts = np.bincount(ii.ravel(), minlength=E)
+    names = ["mm_router", "mm_i8_route", "mm_i8_gu", "mm_i8_quant_h", "mm_i8_down",
+             "mm_i8_combine"]
+    prof = profile_kernels(ctx, step, max(2, steps // 4), names)
+    R = T * K
+    gu_ops = 2.0 * R * 2 * I * H + 2.0 * T * 2 * S * H
+    dn_ops = 2.0 * R * H * I + 2.0 * T * H * S
+    gemm_ms = prof["mm_i8_gu"][0] + prof["mm_i8_down"][0]
+    res = dict(
+        ms_per_step=ms, wall_ms_per_step=wall, tok_s=T / (ms * 1e-3),
+        layer_tops=(gu_ops + dn_ops) / (ms * 1e-3) / 1e12,
+        gemm_tops=(gu_ops + dn_ops) / (gemm_ms * 1e-3) / 1e12,
+        expert_rows_max=int(counts.max()), expert_rows_min=int(counts.min()),
+        experts_touched=int((counts > 0).sum()),
+        kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()},
+        roofline=dict(bound="mfma", kernel="mm_i8_gu",
+                      achieved=gu_ops / (prof["mm_i8_gu"][0] * 1e-3) / 1e12,
+                      peak=INT8_PEAK_TOPS, unit="TOPS", ops_per_launch=gu_ops,
+                      avg_launch_us=prof["mm_i8_gu"][0] * 1e3))
+    res["roofline"]["frac"] = res["roofline"]["achieved"] / INT8_PEAK_TOPS
+    res["roofline"]["traffic"] = traffic_from_profiles("mm_i8_gu", "prefill_i8")
+    return res
+
+
+def bench_decode_bf16(ctx, steps, warmup):
+    """Config 1: one T=1 decode token through a bf16 MoE layer (router GEMV
+    from x, top-6 softmax, 2 shared experts)."""
+    log("[decode_bf16] loading bf16 layer")
+    load_layers(ctx, 1, 5000, mlamoe.MM_LOAD_BF16)
+    x = ctx.empty((1, H), np.float32)
+    ctx.fill(x, H, mlamoe.MM_FILL_F32_NORMAL, 13, 1.0)
+    out = ctx.empty((1, H), np.float32)
+    idx = ctx.empty((1, K), np.int32)
+    wts = ctx.empty((1, K), np.float32)
+    lib, h = mlamoe.lib(), ctx.h
+
+    def step():
+        mlamoe._check(lib.mm_moe_forward_dev(h, 0, 1, x.ptr, out.ptr, None, idx.ptr, wts.ptr,
+                                             None, mlamoe.MM_FWD_BF16))
+    ms, wall = timed(ctx, step, steps * 20, warmup * 5)
+    names = ["mm_moe_bf16_stage1", "mm_moe_bf16_stage2", "mm_moe_bf16_stage3"]
+    prof = profile_kernels(ctx, step, 50, names)
+    nbytes = 262144 + 103809024 + 34603008      # router + 6 experts + shared (bf16)
+    return dict(ms_per_step=ms, tok_s=1.0 / (ms * 1e-3), layer_gbs=nbytes / (ms * 1e-3) / 1e9,
+                frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()})
+
+
+# ---------------------------------------------------------------------------
+
+def cpu_baseline_decode(B=64, seconds_hint=True):
+    """Reference CPU path (ffn_compute on bf16 experts, the oracle's
+    restatement, bit-identical to the reference's golden vectors), single
+    thread, on a bounded sample: all B tokens through ONE of the 26 layers;
+    the step time is that times 26."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    log("[cpu_baseline] generating one host layer")
+    w = synth.moe_layer(9001, H, E, I, NS)
+    rng = np.random.default_rng(9002)
+    x = synth.normal_f32(rng, (B, H))
+    lg = synth.uniform_logits(9003, B, E)
+    cfg = pyoracle.moe_cfg(H, E, NS, K, I)
+    pyoracle.ffn_compute_rows(cfg, w, x[:1], lg[:1])          # warm-up (page in)
+    log("[cpu_baseline] timing")
+    t0 = time.perf_counter()
+    pyoracle.ffn_compute_rows(cfg, w, x, lg)
+    dt = time.perf_counter() - t0
+    step_s = dt * 26
+    return dict(value=B / step_s, unit="tok/s", cores=1, kind="port",
+                sample=f"{B} tokens x 1 of 26 layers ({dt:.1f} s single-threaded, "
+                       f"x26 for a step); oracle ffn_compute on bf16 experts",
+                cpu=_cpu_name(), nproc=os.cpu_count())
+
+
+def _cpu_name():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding plan is design-only (DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    extra = {}
+    with mlamoe.Context(0) as ctx:
+        dec = bench_decode_i8(ctx, args.steps, args.warmup)
+    if not args.no_extra:
+        with mlamoe.Context(0) as ctx:
+            extra["prefill_i8_config3"] = bench_prefill_i8(ctx, args.steps, args.warmup)
+        with mlamoe.Context(0) as ctx:
+            extra["decode_bf16_config1"] = bench_decode_bf16(ctx, args.steps, args.warmup)
+    roof = dec.pop("roofline")
+    cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
+    line = {
+        "metric": METRIC,
+        "value": round(dec["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded device RNG; bf16 N(0,0.02) weights quantised to int8, "
+                "U(0,1) router logits, N(0,1) activations)",
+        "config": {"workload": "config4: MoE decode B=64 x 26 layers, int8 weights, "
+                               "DeepSeek-V2-Lite shapes",
+                   "batch": 64, "layers": 26, "hidden": H, "experts": E, "top_k": K,
+                   "moe_inter": I, "shared_experts": NS, "parallelism": "single-gpu"},
+        "roofline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in roof.items()},
+        "cpu_baseline": cpu,
+        "decode_detail": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in dec.items()},
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -137,6 +137,14 @@ MM_API int mm_moe_forward_dev(mm_ctx *ctx, int layer, int T, const float *xn, fl
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags);
 
+/* Router logits alone: logits[t, e] = sum_i xn[t, i] * moe_gate[e, i] in the
+ * reference's sequential fp32 order (the matmul at src/run.c:124), plus
+ * logit_bias[e] when logit_bias != NULL (a per-expert prior; not in the
+ * reference, used to build skewed synthetic workloads).  Device pointers,
+ * asynchronous.  The result can be passed as `logits` to mm_moe_forward_dev. */
+MM_API int mm_moe_router_logits_dev(mm_ctx *ctx, int layer, int T, const float *xn,
+                                    const float *logit_bias, float *logits);
+
 /* Intermediates of the int8 path, for parity checking (no reference
  * counterpart: the reference has no int8 path).  Device pointers; any may be
  * NULL.  R = T * K routed rows, row t*K + r is token t's slot r.

@@ -454,6 +454,32 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
     return forward_bf16(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc);
 }
 
+int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
+                             const float *logit_bias, float *logits) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_router_logits_dev: NULL context");
+    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_router_logits_dev: call mm_moe_init first");
+    if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded)
+        return mm_fail(MM_ERR_STATE, "mm_moe_router_logits_dev: layer %d not loaded", layer);
+    if (T < 0 || (T > 0 && (!xn || !logits)))
+        return mm_fail(MM_ERR_INVALID, "mm_moe_router_logits_dev: bad arguments");
+    if (T == 0) return MM_OK;
+    int st = mm_set_device(c);
+    if (st) return st;
+    const mm_moe_layer *L = &c->layers[layer];
+    mm_router_args a;
+    memset(&a, 0, sizeof(a));
+    a.x = xn;
+    a.wgT = L->wgT;
+    a.logit_bias = logit_bias;
+    a.logits_out = logits;
+    a.T = T;
+    a.H = c->moe.hidden_size;
+    a.E = c->moe.n_routed_experts;
+    a.K = c->moe.n_experts_per_tok;
+    return mm_launch(c, K_ROUTER, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK, 1, 1,
+                     256, 0, &a);
+}
+
 int mm_moe_forward_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags) {

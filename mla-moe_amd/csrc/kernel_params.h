@@ -14,7 +14,9 @@ typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */
     const float *wgT;        /* [H, E] router weight, fp32, transposed */
     const float *logits_in;  /* [T, E] or 0 */
-    const float *bias;       /* [E] or 0 */
+    const float *bias;       /* [E] selection bias (GLM e_score correction) or 0 */
+    const float *logit_bias; /* [E] added to computed logits (logits-only mode) or 0 */
+    float *logits_out;       /* [T, E]: write the logits and stop, or 0 */
     float *probs;            /* [T, E] scores out, or 0 */
     int32_t *topk_idx;       /* [T, K] */
     float *topk_w;           /* [T, K] */

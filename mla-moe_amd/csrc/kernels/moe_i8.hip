@@ -68,9 +68,10 @@ __device__ __forceinline__ void quant_row_wave(const float *x, int n, int8_t *q,
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_i8_route(mm_i8_route_args a) {
+extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_i8_route(mm_i8_route_args a) {
+    __shared__ float lds[2 * MM_ROUTER_CHUNK_FLOATS];
     const int lane = threadIdx.x & (MM_WAVE - 1);
-    router_block(a.r, blockIdx.x, [&](int tok, const int *idx, const float *) {
+    router_block(a.r, blockIdx.x, lds, [&](int tok, const int *idx, const float *) {
         int e = 0;
 #pragma unroll
         for (int r = 0; r < MM_KMAX; r++)

@@ -4,8 +4,11 @@
  * experts are identical to the CPU reference:
  *   - logits: y[e] = sum_i x[i] * W[e, i] accumulated in fp32 in ascending i
  *     with a separate multiply and add (run.c:29-37).  One lane owns one
- *     expert's dependent add chain; the router weight is stored transposed
- *     ([H, E], fp32) so a wave's 64 experts load as one coalesced row.
+ *     (token, expert) dependent add chain.  The router weight is kept
+ *     transposed ([H, E], fp32); the block streams it through LDS in
+ *     double-buffered chunks that all its waves share, and each wave reads
+ *     its tokens' x through scalar loads, so the add chains never wait on
+ *     HBM.
  *   - softmax (run.c:95-105): max, e^(x - max) (-inf -> 0), sum in ascending
  *     expert order, divide; or sigmoid 1 / (1 + e^-x) (run.c:125-127).
  *   - top-k (run.c:132-143): K passes; each picks the unused expert with the
@@ -18,6 +21,11 @@
 #include "common.h"
 
 #define MM_KMAX 16
+#define MM_ROUTER_TPW 2
+#define MM_ROUTER_WAVES 4
+#define MM_ROUTER_THREADS (MM_ROUTER_WAVES * MM_WAVE)
+#define MM_ROUTER_CHUNK_FLOATS 8192   /* one LDS buffer: HC rows x E experts */
+#define MM_ROUTER_LDS_BYTES (2 * MM_ROUTER_CHUNK_FLOATS * 4)
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -27,61 +35,96 @@ struct router_no_post {
     __device__ void operator()(int, const int *, const float *) const {}
 };
 
-/* Routes tokens [wave_id*TPW, wave_id*TPW + TPW) and then calls
- * post(token, idx, w) with the wave-uniform selection of each token. */
-template <int EJ, int TPW, class Post = router_no_post>
-__device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id,
-                                            Post post = Post()) {
+/* Block-cooperative logits for the block's MM_ROUTER_WAVES * TPW tokens.
+ * Every thread of the block must call this (it synchronises).  On return
+ * lg[t][j] holds the logit of token (wave's t0 + t), expert lane + 64 j. */
+template <int EJ, int TPW>
+__device__ __forceinline__ void router_logits_block(const mm_router_args &a, int t0,
+                                                    float (&lg)[TPW][EJ], float *lds) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int t0 = wave_id * TPW;
-    if (t0 >= a.T) return;
-    const int E = a.E, H = a.H, K = a.K, T = a.T;
-
-    float lg[TPW][EJ];
-    if (a.logits_in) {
+    const int E = a.E, H = a.H, T = a.T;
+    const int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* rows per chunk */
+    const int CH = HC * E;                                     /* floats per chunk */
+    const bool active = t0 < T;
+    const float *xr[TPW];
 #pragma unroll
-        for (int t = 0; t < TPW; t++)
+    for (int t = 0; t < TPW; t++) {
+        xr[t] = a.x + (size_t)min(t0 + t, T - 1) * H;
 #pragma unroll
-            for (int j = 0; j < EJ; j++) {
-                int e = lane + MM_WAVE * j, tt = min(t0 + t, T - 1);
-                lg[t][j] = e < E ? a.logits_in[(size_t)tt * E + e] : 0.0f;
-            }
-    } else {
-#pragma clang fp contract(off)
-        const float *xr[TPW];
+        for (int j = 0; j < EJ; j++) lg[t][j] = 0.0f;
+    }
+    /* register staging of the next chunk: CH/4 float4 spread over the block */
+    constexpr int PER = MM_ROUTER_CHUNK_FLOATS / 4 / MM_ROUTER_THREADS;
+    f32x4 stage[PER];
+    auto fetch = [&](int c0) {
+        const f32x4 *src = (const f32x4 *)(a.wgT + (size_t)c0 * E);
+        const int n4 = (min(HC, H - c0) * E) >> 2;
 #pragma unroll
-        for (int t = 0; t < TPW; t++) {
-            xr[t] = a.x + (size_t)min(t0 + t, T - 1) * H;
-#pragma unroll
-            for (int j = 0; j < EJ; j++) lg[t][j] = 0.0f;
+        for (int k = 0; k < PER; k++) {
+            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
+            stage[k] = i < n4 ? src[i] : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         }
-        const float *wp = a.wgT + lane;
-        for (int i0 = 0; i0 < H; i0 += 8) {
-            float w[8][EJ];
+    };
+    auto store = [&](float *buf) {
 #pragma unroll
-            for (int u = 0; u < 8; u++)
+        for (int k = 0; k < PER; k++) {
+            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
+            if (i * 4 < CH) *(f32x4 *)(buf + i * 4) = stage[k];
+        }
+    };
+    fetch(0);
+    store(lds);
+    __syncthreads();
+    int cur = 0;
+    for (int c0 = 0; c0 < H; c0 += HC) {
+        const bool more = c0 + HC < H;
+        if (more) fetch(c0 + HC);
+        if (active) {
+#pragma clang fp contract(off)
+            const float *buf = lds + cur * MM_ROUTER_CHUNK_FLOATS + lane;
+            const int n = min(HC, H - c0);
+            for (int i0 = 0; i0 < n; i0 += 8) {
+                float w[8][EJ];
 #pragma unroll
-                for (int j = 0; j < EJ; j++) {
-                    int e = lane + MM_WAVE * j;
-                    w[u][j] = (e < E && i0 + u < H) ? wp[(size_t)(i0 + u) * E + MM_WAVE * j] : 0.0f;
-                }
+                for (int u = 0; u < 8; u++)
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (i0 + u < H) {
+                    for (int j = 0; j < EJ; j++) w[u][j] = buf[(i0 + u) * E + MM_WAVE * j];
 #pragma unroll
-                    for (int t = 0; t < TPW; t++) {
-                        float xv = xr[t][i0 + u];
+                for (int u = 0; u < 8; u++) {
+                    if (i0 + u < n) {
 #pragma unroll
-                        for (int j = 0; j < EJ; j++) {
-                            float prod = xv * w[u][j];
-                            lg[t][j] = lg[t][j] + prod;
+                        for (int t = 0; t < TPW; t++) {
+                            const float xv = xr[t][c0 + i0 + u];
+#pragma unroll
+                            for (int j = 0; j < EJ; j++) {
+                                const float prod = xv * w[u][j];
+                                lg[t][j] = lg[t][j] + prod;
+                            }
                         }
                     }
                 }
             }
         }
+        if (more) {
+            store(lds + (cur ^ 1) * MM_ROUTER_CHUNK_FLOATS);
+            __syncthreads();
+            cur ^= 1;
+        }
     }
+#pragma unroll
+    for (int j = 0; j < EJ; j++)
+        if (lane + MM_WAVE * j >= E)
+#pragma unroll
+            for (int t = 0; t < TPW; t++) lg[t][j] = 0.0f;
+}
 
+/* Scores and top-k of one wave's tokens from their logits; calls
+ * post(token, idx, w) with the wave-uniform selection of each token. */
+template <int EJ, int TPW, class Post>
+__device__ __forceinline__ void router_select_wave(const mm_router_args &a, int t0,
+                                                   float (&lg)[TPW][EJ], Post post) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int E = a.E, K = a.K, T = a.T;
 #pragma unroll
     for (int t = 0; t < TPW; t++) {
         const int tok = t0 + t;
@@ -187,19 +230,55 @@ __device__ __forceinline__ void router_wave(const mm_router_args &a, int wave_id
     }
 }
 
-#define MM_ROUTER_TPW 2
-#define MM_ROUTER_WAVES 4
-
-/* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_WAVES * TPW tokens. */
-template <class Post = router_no_post>
-__device__ __forceinline__ void router_block(const mm_router_args &a, int block,
-                                             Post post = Post()) {
+template <int EJ, class Post>
+__device__ __forceinline__ void router_block_t(const mm_router_args &a, int block, float *lds,
+                                               Post post) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
-    const int wid = block * MM_ROUTER_WAVES + wave;
+    const int t0 = (block * MM_ROUTER_WAVES + wave) * MM_ROUTER_TPW;
+    float lg[MM_ROUTER_TPW][EJ];
+    if (a.logits_in) {
+#pragma unroll
+        for (int t = 0; t < MM_ROUTER_TPW; t++)
+#pragma unroll
+            for (int j = 0; j < EJ; j++) {
+                const int e = lane + MM_WAVE * j, tt = min(t0 + t, a.T - 1);
+                lg[t][j] = e < a.E ? a.logits_in[(size_t)tt * a.E + e] : 0.0f;
+            }
+    } else {
+        router_logits_block<EJ, MM_ROUTER_TPW>(a, t0, lg, lds);
+        if (a.logit_bias) {
+#pragma unroll
+            for (int t = 0; t < MM_ROUTER_TPW; t++)
+#pragma unroll
+                for (int j = 0; j < EJ; j++) {
+                    const int e = lane + MM_WAVE * j;
+                    if (e < a.E) lg[t][j] += a.logit_bias[e];
+                }
+        }
+    }
+    if (a.logits_out) {
+#pragma unroll
+        for (int t = 0; t < MM_ROUTER_TPW; t++)
+#pragma unroll
+            for (int j = 0; j < EJ; j++) {
+                const int e = lane + MM_WAVE * j;
+                if (t0 + t < a.T && e < a.E) a.logits_out[(size_t)(t0 + t) * a.E + e] = lg[t][j];
+            }
+        return;
+    }
+    router_select_wave<EJ, MM_ROUTER_TPW>(a, t0, lg, post);
+}
+
+/* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_WAVES * TPW tokens.
+ * All threads of the block must call it; `lds` holds MM_ROUTER_LDS_BYTES. */
+template <class Post = router_no_post>
+__device__ __forceinline__ void router_block(const mm_router_args &a, int block, float *lds,
+                                             Post post = Post()) {
     if (a.E <= 64)
-        router_wave<1, MM_ROUTER_TPW>(a, wid, post);
+        router_block_t<1>(a, block, lds, post);
     else if (a.E <= 128)
-        router_wave<2, MM_ROUTER_TPW>(a, wid, post);
+        router_block_t<2>(a, block, lds, post);
     else
-        router_wave<4, MM_ROUTER_TPW>(a, wid, post);
+        router_block_t<4>(a, block, lds, post);
 }

@@ -91,6 +91,7 @@ def lib():
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
         L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_moe_router_logits_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp]
         L.mm_moe_forward_i8_debug_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
                                                   _vp, _vp, C.c_uint, C.POINTER(MoeI8Debug)]
         _lib = L
@@ -259,6 +260,26 @@ class Context:
             for b in (dx, dout, didx, dw, dp, dl):
                 if b is not None:
                     b.free()
+
+    def router_logits_dev(self, layer, T, xn, logits, logit_bias=None):
+        _check(lib().mm_moe_router_logits_dev(self.h, layer, T, xn.ptr,
+                                              logit_bias.ptr if logit_bias is not None else None,
+                                              logits.ptr))
+
+    def router_logits(self, layer, xn, logit_bias=None):
+        xn = np.ascontiguousarray(xn, np.float32)
+        T = xn.shape[0]
+        E = self._moe_cfg.n_routed_experts
+        dx = self.to_device(xn)
+        dl = self.empty((T, E), np.float32)
+        db = self.to_device(np.ascontiguousarray(logit_bias, np.float32)) \
+            if logit_bias is not None else None
+        self.router_logits_dev(layer, T, dx, dl, db)
+        out = dl.download()
+        for b in [dx, dl] + ([db] if db is not None else []):
+            b.free()
+            self._bufs.remove(b)
+        return out
 
     def moe_forward_i8_debug(self, layer, xn, logits=None, flags=MM_FWD_INT8):
         """int8 forward returning (out, idx, w, probs, intermediates dict)."""

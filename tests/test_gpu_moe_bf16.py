@@ -139,3 +139,25 @@ def test_rejects_bad_shapes(ctx):
     ctx.moe_init(64, 8, 1, 2, 16)
     with pytest.raises(mlamoe.MMError):        # layer not loaded
         ctx.moe_forward(0, np.zeros((1, 64), np.float32))
+
+
+@pytest.mark.parametrize("H,E", [(2048, 64), (1000, 40), (256, 160)])
+def test_router_logits_bit_exact(ctx, oracle, H, E):
+    """Logits-only router: bit-identical to the reference matmul (run.c:29-37,
+    sequential fp32, no FMA), for a partial last LDS chunk (H=1000) and more
+    than 64 experts per wave (E=160); the optional prior is a plain fp32 add."""
+    print(f"router logits H={H} E={E}", flush=True)
+    K, I, T = 4, 8, 29
+    w = synth.moe_layer(55 + E, H, E, I, 0)
+    _layer_ctx(ctx, w, H, E, 0, K, I)
+    x = synth.activations(56, T, H)
+    ref = oracle.matmul(x, w["moe_gate"])
+    got = ctx.router_logits(0, x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    z = synth.zipf_prior(57, E)
+    got2 = ctx.router_logits(0, x, z)
+    assert np.array_equal(got2.view(np.uint32), (ref + z).view(np.uint32))
+    # routing from those logits equals routing from x
+    out_a, idx_a, *_ = ctx.moe_forward(0, x)
+    out_b, idx_b, *_ = ctx.moe_forward(0, x, logits=got)
+    assert np.array_equal(idx_a, idx_b) and np.array_equal(out_a, out_b)
