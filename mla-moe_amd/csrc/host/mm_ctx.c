@@ -39,6 +39,7 @@ static const struct {
     [K_I8_DOWN] = {"mm_i8_down", MOD_MOE_I8},
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
+    [K_I8_TILED] = {"mm_i8_gemm_tiled", MOD_MOE_I8},
 };
 
 /* ---- errors ------------------------------------------------------------- */
@@ -111,6 +112,11 @@ int mm_ctx_create(int device, mm_ctx **out) {
             goto fail;
         }
     }
+    /* MLAMOE_I8_TILED_MIN_T overrides the token count from which the int8
+     * path switches to the tiled GEMM (for measuring the crossover). */
+    c->i8_tiled_min_t = 256;
+    const char *ev = getenv("MLAMOE_I8_TILED_MIN_T");
+    if (ev && *ev) c->i8_tiled_min_t = atoi(ev);
     *out = c;
     return MM_OK;
 fail:

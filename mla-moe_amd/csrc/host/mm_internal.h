@@ -24,6 +24,7 @@ typedef enum {
     K_I8_DOWN,
     K_I8_COMBINE,
     K_PACK_I8,
+    K_I8_TILED,
     K_COUNT
 } mm_kernel_id;
 
@@ -64,6 +65,8 @@ struct mm_ctx {
     int n_layers;
     mm_moe_layer *layers;
     int32_t *moe_cnt;           /* [E] per-expert row counters, zero between calls */
+
+    int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
 
     /* growable device workspace */
     void *ws;

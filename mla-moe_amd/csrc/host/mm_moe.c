@@ -369,6 +369,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                         1, 1, 256, 0, &ra)))
         return st;
 
+    const int tiled = T >= c->i8_tiled_min_t;
     mm_i8_gemm_args ga;
     memset(&ga, 0, sizeof(ga));
     ga.w = L->i8;
@@ -385,25 +386,59 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ga.S = (int)S;
     ga.E = (int)E;
     ga.K = (int)K;
-    ga.wg_per_expert = (int)((I + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-    unsigned nb = (unsigned)(E * ga.wg_per_expert + (S + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-    if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 256, 0, &ga))) return st;
+    const unsigned mt_routed = (unsigned)((R + MM_I8T_BM - 1) / MM_I8T_BM + E);
+    const unsigned mt_shared = (unsigned)((T + MM_I8T_BM - 1) / MM_I8T_BM);
+    if (tiled) {
+        /* routed experts, then the shared expert as one dense GEMM */
+        mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
+                               rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
+                               (int)E, (int)I, (int)H, 1, (int)mt_routed};
+        if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * I / 16 + 7) / 8), mt_routed, 1, 256, 0,
+                            &ta)))
+            return st;
+        if (S) {
+            mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
+                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, (int)mt_shared};
+            if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * S / 16 + 7) / 8), mt_shared, 1,
+                                256, 0, &ts)))
+                return st;
+        }
+    } else {
+        ga.wg_per_expert = (int)((I + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+        unsigned nb = (unsigned)(E * ga.wg_per_expert + (S + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 256, 0, &ga))) return st;
+    }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
                                 S ? T : 0, (int)S};
     if ((st = mm_launch(c, K_I8_QUANT_H, (unsigned)((R + (S ? T : 0) + 3) / 4), 1, 1, 256, 0, &qa)))
         return st;
 
-    ga.a = qh;
-    ga.sa = sh;
-    ga.a_sh = qhs;
-    ga.sa_sh = shs;
-    ga.y = y;
-    ga.ys = ys;
-    ga.dbg_acc = dbg ? dbg->acc_d : NULL;
-    ga.wg_per_expert = (int)((H + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-    nb = (unsigned)(E * ga.wg_per_expert + (S ? ga.wg_per_expert : 0));
-    if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 256, 0, &ga))) return st;
+    if (tiled) {
+        mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
+                               1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
+                               0, (int)mt_routed};
+        if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_routed, 1, 256, 0, &td)))
+            return st;
+        if (S) {
+            mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
+                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, (int)mt_shared};
+            if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_shared, 1, 256, 0,
+                                &tsd)))
+                return st;
+        }
+    } else {
+        ga.a = qh;
+        ga.sa = sh;
+        ga.a_sh = qhs;
+        ga.sa_sh = shs;
+        ga.y = y;
+        ga.ys = ys;
+        ga.dbg_acc = dbg ? dbg->acc_d : NULL;
+        ga.wg_per_expert = (int)((H + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+        unsigned nb = (unsigned)(E * ga.wg_per_expert + (S ? ga.wg_per_expert : 0));
+        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 256, 0, &ga))) return st;
+    }
 
     mm_i8_combine_args ca = {y, ys, wts, out, c->moe_cnt, T, (int)H, (int)K, (int)E, acc, S > 0};
     if ((st = mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca))) return st;

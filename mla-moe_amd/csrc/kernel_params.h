@@ -156,3 +156,26 @@ typedef struct {
 #define MM_I8_WAVES 4
 #define MM_I8_NBW 2
 #define MM_I8_COLS_PER_WG (MM_I8_WAVES * MM_I8_NBW * 16)
+
+/* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
+ * the routed experts' row lists (or all T rows for the shared expert). */
+#define MM_I8T_BM 128
+#define MM_I8T_BN 128
+typedef struct {
+    const int8_t *b;         /* packed fragments of expert 0 */
+    size_t b_expert_stride;  /* bytes between experts' fragment sets */
+    const float *sb0, *sb1;  /* per-column weight scales (gate, up) of expert 0 */
+    int sb_expert_stride;    /* floats between experts' scale vectors */
+    const int32_t *cnt;      /* [E] rows per expert, or 0: one expert with T rows */
+    const int32_t *rows;     /* [E, T] route ids, or 0: identity rows */
+    const int8_t *a;         /* A rows (int8), indexed by token (gate/up) or route id (down) */
+    const float *sa;         /* A row scales, same index as a */
+    int a_by_route;          /* 1: A row = route id; 0: A row = route id / K (token) */
+    float *out;              /* [rows, N_out] by route id (or token for identity rows) */
+    int32_t *dbg_acc;        /* raw accumulators (routed gate/up: [R,2,I]; down: [R,H]) or 0 */
+    int T, K, E;             /* tokens, top-k, experts (E = 1 for the shared expert) */
+    int N;                   /* output columns (I or S for gate/up, H for down) */
+    int Kd;                  /* reduction length (H for gate/up, I or S for down) */
+    int gu;                  /* 1: gate/up with SwiGLU epilogue, 0: plain dequantising GEMM */
+    int max_mtiles;          /* grid.y bound */
+} mm_i8_tiled_args;

@@ -67,12 +67,12 @@ __device__ __forceinline__ void gu_rows(const uint16_t *__restrict__ gate, const
 }
 
 extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_router_args a) {
-    __shared__ float lds[2 * MM_ROUTER_CHUNK_FLOATS];
+    __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     router_block(a, blockIdx.x, lds);
 }
 
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_gu_bf16_args a) {
-    __shared__ float lds[2 * MM_ROUTER_CHUNK_FLOATS];
+    __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     if ((int)blockIdx.x < a.r.n_router_blocks) {
         router_block(a.r, blockIdx.x, lds);
         return;

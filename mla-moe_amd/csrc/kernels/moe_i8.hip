@@ -69,7 +69,7 @@ __device__ __forceinline__ void quant_row_wave(const float *x, int n, int8_t *q,
 }
 
 extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_i8_route(mm_i8_route_args a) {
-    __shared__ float lds[2 * MM_ROUTER_CHUNK_FLOATS];
+    __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     const int lane = threadIdx.x & (MM_WAVE - 1);
     router_block(a.r, blockIdx.x, lds, [&](int tok, const int *idx, const float *) {
         int e = 0;
@@ -301,5 +301,188 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
         const size_t row = (size_t)nb * 16 + (lane & 15);
         const size_t col = (size_t)kb * 64 + 16 * (lane >> 4);
         *(v4i *)(a.dst + i * 16) = *(const v4i *)(src + row * a.K + col);
+    }
+}
+
+/* ---- tiled grouped GEMM (prefill) ------------------------------------------- */
+
+/* Block tile: MM_I8T_BM rows x 8 B fragments (gate/up: 4 column blocks of
+ * 16 with their gate and up fragments = 64 output columns; plain: 8 column
+ * blocks = 128 output columns), K step 64.  Four waves in a 2 x 2 grid, each
+ * a 64-row x 4-fragment tile: 16 v_mfma_i32_16x16x64_i8 per K step.
+ * A (gathered rows) and B (packed fragments) are staged through two LDS
+ * buffers of 16 KB in MFMA operand order; the next K step's global loads are
+ * issued before the current step's MFMAs.  grid.x = column tile, grid.y =
+ * row tile over all experts (prefix of ceil(rows_e / 128)). */
+#define T_FRAGS 8
+
+/* Expert and first row of row-tile `tile` (all threads of the block get the
+ * same answer); returns false when the tile is past the last expert. */
+__device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, int *e_out,
+                                           int *m0_out, int *M_out) {
+    __shared__ int s_e, s_m0, s_M;
+    if (threadIdx.x < MM_WAVE) {
+        const int lane = threadIdx.x;
+        int found = -1, m0 = 0, Mf = 0;
+        if (!a.cnt) {
+            if (tile * MM_I8T_BM < a.T) { found = 0; m0 = tile * MM_I8T_BM; Mf = a.T; }
+        } else {
+            int base = 0;   /* tiles before this group of 64 experts */
+            for (int e0 = 0; e0 < a.E && found < 0; e0 += MM_WAVE) {
+                const int e = e0 + lane;
+                const int M = e < a.E ? min(a.cnt[e], a.T) : 0;
+                const int nt = (M + MM_I8T_BM - 1) / MM_I8T_BM;
+                int incl = nt;   /* inclusive wave prefix sum */
+#pragma unroll
+                for (int off = 1; off < MM_WAVE; off <<= 1) {
+                    int v = __shfl_up(incl, off, MM_WAVE);
+                    if (lane >= off) incl += v;
+                }
+                const int excl = base + incl - nt;
+                const bool mine = tile >= excl && tile < excl + nt;
+                const unsigned long long bal = __ballot(mine);
+                if (bal) {
+                    const int src = __ffsll((long long)bal) - 1;
+                    found = e0 + src;
+                    m0 = (tile - __shfl(excl, src, MM_WAVE)) * MM_I8T_BM;
+                    Mf = __shfl(M, src, MM_WAVE);
+                }
+                base += __shfl(incl, MM_WAVE - 1, MM_WAVE);
+            }
+        }
+        if (lane == 0) { s_e = found; s_m0 = m0; s_M = Mf; }
+    }
+    __syncthreads();
+    *e_out = s_e;
+    *m0_out = s_m0;
+    *M_out = s_M;
+    return s_e >= 0;
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[2][2 * T_FRAGS * 1024];
+    int e, m0, M;
+    if (!tile_owner(a, blockIdx.y, &e, &m0, &M)) return;
+    const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int KB = a.Kd / 64;
+    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
+    const int fr0 = blockIdx.x * T_FRAGS;
+    if (fr0 >= nfr_total) return;   /* uniform per block */
+    const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
+    const int8_t *bexp = a.b + (size_t)e * a.b_expert_stride;
+
+    /* this thread's two A rows and two B fragments (fixed over K) */
+    const int part = tid & 3;
+    const int8_t *asrc[2];
+    bool aval[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int r = (tid >> 2) + 64 * h, m = m0 + r;
+        aval[h] = m < M;
+        int arow = 0;
+        if (aval[h]) {
+            const int rid = rows ? rows[m] : m;
+            arow = (a.a_by_route || !rows) ? rid : rid / a.K;
+        }
+        asrc[h] = a.a + (size_t)arow * a.Kd + part * 16;
+    }
+    const int8_t *bsrc[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int f = (tid >> 6) + 4 * h;
+        bsrc[h] = bexp + (size_t)min(fr0 + f, nfr_total - 1) * KB * 1024 + lane * 16;
+    }
+    /* LDS destinations of those chunks */
+    int adst[2], bdst[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int r = (tid >> 2) + 64 * h;
+        adst[h] = (r >> 4) * 1024 + ((r & 15) + 16 * part) * 16;
+        bdst[h] = T_FRAGS * 1024 + ((tid >> 6) + 4 * h) * 1024 + lane * 16;
+    }
+    v4i ra[2], rb[2];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            ra[h] = aval[h] ? *(const v4i *)(asrc[h] + kb * 64) : (v4i){0, 0, 0, 0};
+            rb[h] = ldg16(bsrc[h] + kb * 1024);
+        }
+    };
+    auto lstore = [&](int s) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *(v4i *)(&lds[s][adst[h]]) = ra[h];
+            *(v4i *)(&lds[s][bdst[h]]) = rb[h];
+        }
+    };
+
+    v4i acc[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+        for (int f = 0; f < 4; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < KB; kb++) {
+        const int s = kb & 1;
+        if (kb + 1 < KB) gload(kb + 1);
+        v4i av[4], bv[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; mi++)
+            av[mi] = *(const v4i *)(&lds[s][(wm * 4 + mi) * 1024 + lane * 16]);
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+            bv[f] = *(const v4i *)(&lds[s][T_FRAGS * 1024 + (wn * 4 + f) * 1024 + lane * 16]);
+#pragma unroll
+        for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+            for (int f = 0; f < 4; f++) acc[mi][f] = mfma_i8(av[mi], bv[f], acc[mi][f]);
+        if (kb + 1 < KB) lstore(s ^ 1);
+        __syncthreads();
+    }
+
+    /* epilogue */
+    const float *sb0 = a.sb0 + (size_t)e * a.sb_expert_stride;
+    const float *sb1 = a.sb1 ? a.sb1 + (size_t)e * a.sb_expert_stride : nullptr;
+#pragma unroll
+    for (int mi = 0; mi < 4; mi++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + wm * 64 + mi * 16 + 4 * (lane >> 4) + i;
+            if (m >= M) continue;
+            const int rid = rows ? rows[m] : m;
+            const int arow = (a.a_by_route || !rows) ? rid : rid / a.K;
+            const float sa = a.sa[arow];
+            if (a.gu) {
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const int nb = (fr0 >> 1) + wn * 2 + k;
+                    if (nb * 16 >= a.N) continue;
+                    const int col = nb * 16 + (lane & 15);
+                    const int32_t ag = acc[mi][2 * k][i], au = acc[mi][2 * k + 1][i];
+                    const float g = ((float)ag * sa) * sb0[col];
+                    const float u = ((float)au * sa) * sb1[col];
+                    a.out[(size_t)rid * a.N + col] = silu_mul(g, u);
+                    if (a.dbg_acc) {
+                        a.dbg_acc[((size_t)rid * 2) * a.N + col] = ag;
+                        a.dbg_acc[((size_t)rid * 2 + 1) * a.N + col] = au;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int f = 0; f < 4; f++) {
+                    const int nb = fr0 + wn * 4 + f;
+                    if (nb * 16 >= a.N) continue;
+                    const int col = nb * 16 + (lane & 15);
+                    const int32_t ac = acc[mi][f][i];
+                    a.out[(size_t)rid * a.N + col] = ((float)ac * sa) * sb0[col];
+                    if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.N + col] = ac;
+                }
+            }
+        }
     }
 }

@@ -24,8 +24,11 @@
 #define MM_ROUTER_TPW 2
 #define MM_ROUTER_WAVES 4
 #define MM_ROUTER_THREADS (MM_ROUTER_WAVES * MM_WAVE)
-#define MM_ROUTER_CHUNK_FLOATS 8192   /* one LDS buffer: HC rows x E experts */
-#define MM_ROUTER_LDS_BYTES (2 * MM_ROUTER_CHUNK_FLOATS * 4)
+#define MM_ROUTER_CHUNK_FLOATS 8192   /* router-weight chunk: HC rows x E experts */
+#define MM_ROUTER_TOKENS (MM_ROUTER_WAVES * MM_ROUTER_TPW)
+#define MM_ROUTER_XCHUNK_FLOATS (MM_ROUTER_TOKENS * (MM_ROUTER_CHUNK_FLOATS / MM_WAVE))
+#define MM_ROUTER_BUF_FLOATS (MM_ROUTER_CHUNK_FLOATS + MM_ROUTER_XCHUNK_FLOATS)
+#define MM_ROUTER_LDS_FLOATS (2 * MM_ROUTER_BUF_FLOATS)
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -35,27 +38,30 @@ struct router_no_post {
     __device__ void operator()(int, const int *, const float *) const {}
 };
 
-/* Block-cooperative logits for the block's MM_ROUTER_WAVES * TPW tokens.
- * Every thread of the block must call this (it synchronises).  On return
- * lg[t][j] holds the logit of token (wave's t0 + t), expert lane + 64 j. */
+/* Block-cooperative logits for the block's MM_ROUTER_TOKENS tokens.  Every
+ * thread of the block must call this (it synchronises).  Each LDS buffer
+ * holds a chunk of HC router-weight rows ([HC][E]) and the same HC columns
+ * of the block's token rows ([tokens][HC]); the next chunk is fetched into
+ * registers while the current one is consumed.  Inside a chunk the lanes'
+ * add chains run on operands already in LDS, read one group of 8 ahead.
+ * On return lg[t][j] is the logit of token t0 + t, expert lane + 64 j. */
 template <int EJ, int TPW>
-__device__ __forceinline__ void router_logits_block(const mm_router_args &a, int t0,
+__device__ __forceinline__ void router_logits_block(const mm_router_args &a, int tb0, int t0,
                                                     float (&lg)[TPW][EJ], float *lds) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int E = a.E, H = a.H, T = a.T;
-    const int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* rows per chunk */
-    const int CH = HC * E;                                     /* floats per chunk */
+    constexpr int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* rows per chunk */
+    const int CH = HC * E;
     const bool active = t0 < T;
-    const float *xr[TPW];
+    const int tw = t0 - tb0;                                       /* wave's first row in x chunk */
 #pragma unroll
-    for (int t = 0; t < TPW; t++) {
-        xr[t] = a.x + (size_t)min(t0 + t, T - 1) * H;
+    for (int t = 0; t < TPW; t++)
 #pragma unroll
         for (int j = 0; j < EJ; j++) lg[t][j] = 0.0f;
-    }
-    /* register staging of the next chunk: CH/4 float4 spread over the block */
+
     constexpr int PER = MM_ROUTER_CHUNK_FLOATS / 4 / MM_ROUTER_THREADS;
-    f32x4 stage[PER];
+    constexpr int XPER = (MM_ROUTER_TOKENS * HC / 4 + MM_ROUTER_THREADS - 1) / MM_ROUTER_THREADS;
+    f32x4 stage[PER], xstage[XPER];
     auto fetch = [&](int c0) {
         const f32x4 *src = (const f32x4 *)(a.wgT + (size_t)c0 * E);
         const int n4 = (min(HC, H - c0) * E) >> 2;
@@ -64,12 +70,27 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;
             stage[k] = i < n4 ? src[i] : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         }
+#pragma unroll
+        for (int k = 0; k < XPER; k++) {
+            const int i = threadIdx.x + k * MM_ROUTER_THREADS;   /* float4 index in [tokens][HC] */
+            const int row = i / (HC / 4), col = (i % (HC / 4)) * 4;
+            const int tok = min(tb0 + row, T - 1);
+            xstage[k] = (row < MM_ROUTER_TOKENS && c0 + col < H)
+                            ? *(const f32x4 *)(a.x + (size_t)tok * H + c0 + col)
+                            : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
     };
     auto store = [&](float *buf) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;
             if (i * 4 < CH) *(f32x4 *)(buf + i * 4) = stage[k];
+        }
+#pragma unroll
+        for (int k = 0; k < XPER; k++) {
+            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
+            if (i < MM_ROUTER_TOKENS * HC / 4)
+                *(f32x4 *)(buf + MM_ROUTER_CHUNK_FLOATS + i * 4) = xstage[k];
         }
     };
     fetch(0);
@@ -81,32 +102,53 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
         if (more) fetch(c0 + HC);
         if (active) {
 #pragma clang fp contract(off)
-            const float *buf = lds + cur * MM_ROUTER_CHUNK_FLOATS + lane;
-            const int n = min(HC, H - c0);
-            for (int i0 = 0; i0 < n; i0 += 8) {
-                float w[8][EJ];
+            /* Rows of the chunk past H were fetched as zeros: x*w = +0 and
+             * acc + (+0) = acc exactly (acc starts at +0 and never becomes -0
+             * under round-to-nearest), so the whole chunk is consumed with a
+             * constant trip count and the result is bit-identical. */
+            const float *wb = lds + cur * MM_ROUTER_BUF_FLOATS + lane;
+            const float *xb = lds + cur * MM_ROUTER_BUF_FLOATS + MM_ROUTER_CHUNK_FLOATS + tw * HC;
+            float w[2][8][EJ], xv[2][TPW][8];
+            auto load = [&](int s, int i0) {
 #pragma unroll
                 for (int u = 0; u < 8; u++)
 #pragma unroll
-                    for (int j = 0; j < EJ; j++) w[u][j] = buf[(i0 + u) * E + MM_WAVE * j];
+                    for (int j = 0; j < EJ; j++) w[s][u][j] = wb[(i0 + u) * E + MM_WAVE * j];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    if (i0 + u < n) {
-#pragma unroll
-                        for (int t = 0; t < TPW; t++) {
-                            const float xv = xr[t][c0 + i0 + u];
-#pragma unroll
-                            for (int j = 0; j < EJ; j++) {
-                                const float prod = xv * w[u][j];
-                                lg[t][j] = lg[t][j] + prod;
-                            }
-                        }
-                    }
+                for (int t = 0; t < TPW; t++) {
+                    const f32x4 lo = *(const f32x4 *)(xb + t * HC + i0);
+                    const f32x4 hi = *(const f32x4 *)(xb + t * HC + i0 + 4);
+                    xv[s][t][0] = lo.x; xv[s][t][1] = lo.y; xv[s][t][2] = lo.z; xv[s][t][3] = lo.w;
+                    xv[s][t][4] = hi.x; xv[s][t][5] = hi.y; xv[s][t][6] = hi.z; xv[s][t][7] = hi.w;
                 }
+            };
+            /* products first (independent), then the ordered adds, so the
+             * only serial dependency left is each accumulator's add chain */
+            auto compute = [&](int s) {
+                float prod[8][TPW][EJ];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int t = 0; t < TPW; t++)
+#pragma unroll
+                        for (int j = 0; j < EJ; j++) prod[u][t][j] = xv[s][t][u] * w[s][u][j];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int t = 0; t < TPW; t++)
+#pragma unroll
+                        for (int j = 0; j < EJ; j++) lg[t][j] = lg[t][j] + prod[u][t][j];
+            };
+            /* two register stages, statically indexed: one group of 8 ahead */
+            load(0, 0);
+#pragma unroll
+            for (int g = 0; g < HC / 8; g++) {
+                if (g + 1 < HC / 8) load((g + 1) & 1, (g + 1) * 8);
+                compute(g & 1);
             }
         }
         if (more) {
-            store(lds + (cur ^ 1) * MM_ROUTER_CHUNK_FLOATS);
+            store(lds + (cur ^ 1) * MM_ROUTER_BUF_FLOATS);
             __syncthreads();
             cur ^= 1;
         }
@@ -246,7 +288,7 @@ __device__ __forceinline__ void router_block_t(const mm_router_args &a, int bloc
                 lg[t][j] = e < a.E ? a.logits_in[(size_t)tt * a.E + e] : 0.0f;
             }
     } else {
-        router_logits_block<EJ, MM_ROUTER_TPW>(a, t0, lg, lds);
+        router_logits_block<EJ, MM_ROUTER_TPW>(a, block * MM_ROUTER_TOKENS, t0, lg, lds);
         if (a.logit_bias) {
 #pragma unroll
             for (int t = 0; t < MM_ROUTER_TPW; t++)
@@ -270,8 +312,8 @@ __device__ __forceinline__ void router_block_t(const mm_router_args &a, int bloc
     router_select_wave<EJ, MM_ROUTER_TPW>(a, t0, lg, post);
 }
 
-/* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_WAVES * TPW tokens.
- * All threads of the block must call it; `lds` holds MM_ROUTER_LDS_BYTES. */
+/* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_TOKENS tokens.  All
+ * threads of the block must call it; `lds` holds MM_ROUTER_LDS_FLOATS. */
 template <class Post = router_no_post>
 __device__ __forceinline__ void router_block(const mm_router_args &a, int block, float *lds,
                                              Post post = Post()) {

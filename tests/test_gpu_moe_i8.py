@@ -19,8 +19,12 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.fixture
-def ctx():
+@pytest.fixture(params=["decode", "tiled"])
+def ctx(request, monkeypatch):
+    """A context whose int8 GEMMs take the decode-shaped path or the tiled
+    (prefill) path for every T."""
+    monkeypatch.setenv("MLAMOE_I8_TILED_MIN_T", "1" if request.param == "tiled" else "1000000000")
+    print(f"int8 GEMM path: {request.param}", flush=True)
     c = mlamoe.Context(0)
     yield c
     c.close()
@@ -115,7 +119,8 @@ def test_i8_no_shared_expert(ctx, oracle):
 
 def test_i8_dsv2_decode_batch(ctx, oracle):
     """DeepSeek-V2-Lite shape, batched decode with given uniform logits
-    (config 4's routing), T = 16."""
+    (config 4's routing), T = 16 (routed and shared accumulators checked on
+    the tiled path's larger tiles too)."""
     d = synth.DSV2
     T = 16
     lg = synth.uniform_logits(70, T, d["E"])
@@ -170,3 +175,33 @@ def test_i8_vs_bf16_drift_reported(ctx, oracle):
     drift = max_abs_rel(o8, ro)
     print(f"int8 vs bf16 reference drift (max-abs-rel): {drift:.3e}")
     assert drift < 5e-2
+
+
+def test_i8_dsv2_prefill_skewed(ctx, oracle):
+    """Config-3 routing on a shorter prompt: DeepSeek-V2-Lite shapes, T=300,
+    router logits W_g x plus the Zipf(1.1) prior, so some experts get more
+    than one 128-row tile and others none."""
+    d = synth.DSV2
+    H, E, K, I, NS, T = d["H"], d["E"], d["K"], d["I"], d["n_shared"], 300
+    w = synth.moe_layer(120, H, E, I, NS)
+    ctx.moe_init(H, E, NS, K, I)
+    ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8)
+    x = synth.activations(121, T, H)
+    z = synth.zipf_prior(122, E)
+    lg = ctx.router_logits(0, x, z)
+    assert np.array_equal(lg.view(np.uint32), (oracle.matmul(x, w["moe_gate"]) + z).view(np.uint32))
+    out, idx, wt, probs, dd = ctx.moe_forward_i8_debug(0, x, lg)
+    cfg = oracle.moe_cfg(H, E, NS, K, I)
+    qw = oracle.quantize_moe_weights(w)
+    ro, ri, *_ = oracle.ffn_i8(cfg, w, qw, x, lg)
+    assert np.array_equal(idx, ri)
+    counts = np.bincount(idx.ravel(), minlength=E)
+    assert counts.max() > 128
+    # spot-check int32 accumulators of the busiest expert's rows
+    e = int(counts.argmax())
+    rids = [t * K + r for t in range(T) for r in range(K) if idx[t, r] == e][:40]
+    for rid in rids:
+        t = rid // K
+        assert np.array_equal(dd["acc_gu"][rid, 0], _dot_exact(dd["qx"][t:t + 1], qw["qeg"][e])[0])
+        assert np.array_equal(dd["acc_d"][rid], _dot_exact(dd["qh"][rid:rid + 1], qw["qed"][e])[0])
+    assert max_abs_rel(out, ro) < TOL
