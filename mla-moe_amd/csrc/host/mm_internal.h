@@ -25,6 +25,8 @@ typedef enum {
     K_I8_COMBINE,
     K_PACK_I8,
     K_I8_TILED,
+    K_I8_GU_S,
+    K_I8_DOWN_S,
     K_COUNT
 } mm_kernel_id;
 

@@ -15,6 +15,7 @@
 #define GU_ROWS_PER_BLOCK 4   /* one gate/up row pair per wave */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
 #define ROUTER_TOKENS_PER_BLOCK 8
+#define I8T_MGROUP 1          /* 128-row tiles per block in the tiled int8 GEMM */
 
 void mm_moe_release(mm_ctx *c) {
     if (!c->layers) return;
@@ -386,19 +387,21 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ga.S = (int)S;
     ga.E = (int)E;
     ga.K = (int)K;
-    const unsigned mt_routed = (unsigned)((R + MM_I8T_BM - 1) / MM_I8T_BM + E);
-    const unsigned mt_shared = (unsigned)((T + MM_I8T_BM - 1) / MM_I8T_BM);
+    /* row groups of I8T_MGROUP tiles: upper bound over any routing */
+    const size_t GR = (size_t)MM_I8T_BM * I8T_MGROUP;
+    const unsigned mt_routed = (unsigned)((R + GR - 1) / GR + E);
+    const unsigned mt_shared = (unsigned)((T + GR - 1) / GR);
     if (tiled) {
         /* routed experts, then the shared expert as one dense GEMM */
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
-                               (int)E, (int)I, (int)H, 1, (int)mt_routed};
+                               (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed};
         if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * I / 16 + 7) / 8), mt_routed, 1, 256, 0,
                             &ta)))
             return st;
         if (S) {
             mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
-                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, (int)mt_shared};
+                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared};
             if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * S / 16 + 7) / 8), mt_shared, 1,
                                 256, 0, &ts)))
                 return st;
@@ -406,6 +409,9 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     } else {
         ga.wg_per_expert = (int)((I + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
         unsigned nb = (unsigned)(E * ga.wg_per_expert + (S + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
+        /* experts with <= 16 rows, then the rest and the shared expert */
+        if ((st = mm_launch(c, K_I8_GU_S, (unsigned)(E * ga.wg_per_expert), 1, 1, 256, 0, &ga)))
+            return st;
         if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 256, 0, &ga))) return st;
     }
 
@@ -417,12 +423,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     if (tiled) {
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
-                               0, (int)mt_routed};
+                               0, I8T_MGROUP, (int)mt_routed};
         if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_routed, 1, 256, 0, &td)))
             return st;
         if (S) {
             mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
-                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, (int)mt_shared};
+                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared};
             if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_shared, 1, 256, 0,
                                 &tsd)))
                 return st;
@@ -437,6 +443,8 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
         ga.wg_per_expert = (int)((H + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
         unsigned nb = (unsigned)(E * ga.wg_per_expert + (S ? ga.wg_per_expert : 0));
+        if ((st = mm_launch(c, K_I8_DOWN_S, (unsigned)(E * ga.wg_per_expert), 1, 1, 256, 0, &ga)))
+            return st;
         if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 256, 0, &ga))) return st;
     }
 

@@ -177,5 +177,6 @@ typedef struct {
     int N;                   /* output columns (I or S for gate/up, H for down) */
     int Kd;                  /* reduction length (H for gate/up, I or S for down) */
     int gu;                  /* 1: gate/up with SwiGLU epilogue, 0: plain dequantising GEMM */
-    int max_mtiles;          /* grid.y bound */
+    int mgroup;              /* consecutive 128-row tiles one block walks (weight reuse) */
+    int max_groups;          /* grid.y bound */
 } mm_i8_tiled_args;

@@ -89,21 +89,23 @@ extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_i8_route(mm_i
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-/* One pass of up to I8_MT*16 rows against this wave's I8_NBW column blocks.
+/* One pass of up to MT*16 rows against this wave's I8_NBW column blocks.
  * GU: gate/up pair per column block (B fragments interleaved), SwiGLU
- * epilogue; otherwise a plain GEMM with a dequantising epilogue.
+ * epilogue; otherwise a plain GEMM with a dequantising epilogue.  The K loop
+ * is unrolled UNR deep so that UNR * I8_NBW * (GU ? 2 : 1) weight fragments
+ * are in flight per wave.
  *   arow(m) -> pointer to row m of A (int8, K bytes), only called for m < M
  *   epi(m, col, acc0, acc1) consumes the int32 results of row m, column col */
-template <bool GU, class ARow, class Epi>
+template <bool GU, int MT, int UNR, class ARow, class Epi>
 __device__ __forceinline__ void gemm_pass(const int8_t *bbase, int nb0, int nbl, int KB, int m0,
                                           int M, ARow arow, Epi epi) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int NB_STRIDE = (GU ? 2 : 1) * KB * 1024;
-    const int nmt = min(I8_MT, (M - m0 + 15) >> 4);
-    const int8_t *ap[I8_MT];
-    bool av[I8_MT];
+    const int nmt = min(MT, (M - m0 + 15) >> 4);
+    const int8_t *ap[MT];
+    bool av[MT];
 #pragma unroll
-    for (int mi = 0; mi < I8_MT; mi++) {
+    for (int mi = 0; mi < MT; mi++) {
         const int m = m0 + mi * 16 + (lane & 15);
         av[mi] = mi < nmt && m < M;
         ap[mi] = (av[mi] ? arow(m) : arow(m0)) + 16 * (lane >> 4);
@@ -113,43 +115,59 @@ __device__ __forceinline__ void gemm_pass(const int8_t *bbase, int nb0, int nbl,
     for (int j = 0; j < I8_NBW; j++)
         bp[j] = bbase + (size_t)min(nb0 + j, nbl - 1) * NB_STRIDE + lane * 16;
 
-    v4i acc0[I8_MT][I8_NBW], acc1[I8_MT][I8_NBW];
+    v4i acc0[MT][I8_NBW], acc1[MT][I8_NBW];
 #pragma unroll
-    for (int mi = 0; mi < I8_MT; mi++)
+    for (int mi = 0; mi < MT; mi++)
 #pragma unroll
         for (int j = 0; j < I8_NBW; j++) {
             acc0[mi][j] = (v4i){0, 0, 0, 0};
             acc1[mi][j] = (v4i){0, 0, 0, 0};
         }
 
-#pragma unroll 2
-    for (int kb = 0; kb < KB; kb++) {
-        v4i b0[I8_NBW], b1[I8_NBW], av_[I8_MT];
+    auto step = [&](int kb, const v4i *b0, const v4i *b1) {
+        v4i a_[MT];
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            if (mi < nmt) {
+                a_[mi] = *(const v4i *)(ap[mi] + kb * 64);
+                if (!av[mi]) a_[mi] = (v4i){0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++) {
+            if (mi < nmt) {
+#pragma unroll
+                for (int j = 0; j < I8_NBW; j++) {
+                    acc0[mi][j] = mfma_i8(a_[mi], b0[j], acc0[mi][j]);
+                    if (GU) acc1[mi][j] = mfma_i8(a_[mi], b1[j], acc1[mi][j]);
+                }
+            }
+        }
+    };
+    int kb = 0;
+    for (; kb + UNR <= KB; kb += UNR) {
+        v4i b0[UNR][I8_NBW], b1[UNR][I8_NBW];
+#pragma unroll
+        for (int u = 0; u < UNR; u++)
+#pragma unroll
+            for (int j = 0; j < I8_NBW; j++) {
+                b0[u][j] = ldg16(bp[j] + (kb + u) * 1024);
+                if (GU) b1[u][j] = ldg16(bp[j] + (KB + kb + u) * 1024);
+            }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) step(kb + u, b0[u], b1[u]);
+    }
+    for (; kb < KB; kb++) {
+        v4i b0[I8_NBW], b1[I8_NBW];
 #pragma unroll
         for (int j = 0; j < I8_NBW; j++) {
             b0[j] = ldg16(bp[j] + kb * 1024);
             if (GU) b1[j] = ldg16(bp[j] + (KB + kb) * 1024);
         }
-#pragma unroll
-        for (int mi = 0; mi < I8_MT; mi++) {
-            if (mi < nmt) {
-                av_[mi] = *(const v4i *)(ap[mi] + kb * 64);
-                if (!av[mi]) av_[mi] = (v4i){0, 0, 0, 0};
-            }
-        }
-#pragma unroll
-        for (int mi = 0; mi < I8_MT; mi++) {
-            if (mi < nmt) {
-#pragma unroll
-                for (int j = 0; j < I8_NBW; j++) {
-                    acc0[mi][j] = mfma_i8(av_[mi], b0[j], acc0[mi][j]);
-                    if (GU) acc1[mi][j] = mfma_i8(av_[mi], b1[j], acc1[mi][j]);
-                }
-            }
-        }
+        step(kb, b0, b1);
     }
 #pragma unroll
-    for (int mi = 0; mi < I8_MT; mi++) {
+    for (int mi = 0; mi < MT; mi++) {
         if (mi < nmt) {
 #pragma unroll
             for (int j = 0; j < I8_NBW; j++) {
@@ -166,7 +184,15 @@ __device__ __forceinline__ void gemm_pass(const int8_t *bbase, int nb0, int nbl,
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
+/* Decode-shaped grouped GEMMs: one block per (expert, 128-column slab), every
+ * row of the expert against the slab, weights streamed once.  SMALL = true
+ * serves the routed experts with at most 16 rows (one 16-row tile, deep K
+ * unroll, low register use); SMALL = false serves the rest and the shared
+ * expert (four 16-row tiles per pass).  Both are launched; each block exits
+ * when its expert belongs to the other variant. */
+template <bool SMALL>
+__device__ __forceinline__ void i8_gu_decode(const mm_i8_gemm_args &a) {
+    constexpr int MT = SMALL ? 1 : I8_MT, UNR = SMALL ? 4 : 2;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int KB = a.H / 64;
     const int routed_blocks = a.E * a.wg_per_expert;
@@ -176,12 +202,12 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
         const int M = min(a.cnt[e], a.T);
         const int nbl = a.I / 16;
         const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
-        if (M == 0 || nb0 >= nbl) return;
+        if (M == 0 || nb0 >= nbl || (SMALL != (M <= 16))) return;
         const int32_t *rows = a.rows + (size_t)e * a.T;
         const int8_t *bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
         const float *sg = a.w.s_g + (size_t)e * a.I, *su = a.w.s_u + (size_t)e * a.I;
-        for (int m0 = 0; m0 < M; m0 += I8_MT * 16) {
-            gemm_pass<true>(
+        for (int m0 = 0; m0 < M; m0 += MT * 16) {
+            gemm_pass<true, MT, UNR>(
                 bbase, nb0, nbl, KB, m0, M,
                 [&](int m) { return a.a + (size_t)(rows[m] / a.K) * a.H; },
                 [&](int m, int col, int32_t ag, int32_t au) {
@@ -196,13 +222,13 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
                     }
                 });
         }
-    } else {
+    } else if (!SMALL) {
         const int sb = b - routed_blocks;
         const int nbl = a.S / 16;
         const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
         if (nb0 >= nbl) return;
-        for (int m0 = 0; m0 < a.T; m0 += I8_MT * 16) {
-            gemm_pass<true>(
+        for (int m0 = 0; m0 < a.T; m0 += MT * 16) {
+            gemm_pass<true, MT, UNR>(
                 a.w.sgu, nb0, nbl, KB, m0, a.T,
                 [&](int m) { return a.a + (size_t)m * a.H; },
                 [&](int m, int col, int32_t ag, int32_t au) {
@@ -215,7 +241,9 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) {
+template <bool SMALL>
+__device__ __forceinline__ void i8_down_decode(const mm_i8_gemm_args &a) {
+    constexpr int MT = SMALL ? 1 : I8_MT, UNR = SMALL ? 4 : 2;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int routed_blocks = a.E * a.wg_per_expert;
     const int nbl = a.H / 16;
@@ -224,13 +252,13 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) 
         const int e = b / a.wg_per_expert, wgi = b % a.wg_per_expert;
         const int M = min(a.cnt[e], a.T);
         const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
-        if (M == 0 || nb0 >= nbl) return;
+        if (M == 0 || nb0 >= nbl || (SMALL != (M <= 16))) return;
         const int KB = a.I / 64;
         const int32_t *rows = a.rows + (size_t)e * a.T;
         const int8_t *bbase = a.w.d + (size_t)e * nbl * KB * 1024;
         const float *sd = a.w.s_d + (size_t)e * a.H;
-        for (int m0 = 0; m0 < M; m0 += I8_MT * 16) {
-            gemm_pass<false>(
+        for (int m0 = 0; m0 < M; m0 += MT * 16) {
+            gemm_pass<false, MT, UNR>(
                 bbase, nb0, nbl, KB, m0, M,
                 [&](int m) { return a.a + (size_t)rows[m] * a.I; },
                 [&](int m, int col, int32_t acc, int32_t) {
@@ -239,13 +267,13 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) 
                     if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.H + col] = acc;
                 });
         }
-    } else {
+    } else if (!SMALL) {
         const int sb = b - routed_blocks;
         const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
         if (nb0 >= nbl) return;
         const int KB = a.S / 64;
-        for (int m0 = 0; m0 < a.T; m0 += I8_MT * 16) {
-            gemm_pass<false>(
+        for (int m0 = 0; m0 < a.T; m0 += MT * 16) {
+            gemm_pass<false, MT, UNR>(
                 a.w.sdn, nb0, nbl, KB, m0, a.T,
                 [&](int m) { return a.a_sh + (size_t)m * a.S; },
                 [&](int m, int col, int32_t acc, int32_t) {
@@ -253,6 +281,19 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) 
                 });
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_i8_gu_s(mm_i8_gemm_args a) {
+    i8_gu_decode<true>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
+    i8_gu_decode<false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void mm_i8_down_s(mm_i8_gemm_args a) {
+    i8_down_decode<true>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) {
+    i8_down_decode<false>(a);
 }
 
 /* ---- hidden-row quantisation and combine ------------------------------------- */
@@ -316,22 +357,24 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
  * row tile over all experts (prefix of ceil(rows_e / 128)). */
 #define T_FRAGS 8
 
-/* Expert and first row of row-tile `tile` (all threads of the block get the
- * same answer); returns false when the tile is past the last expert. */
+/* Expert, first row and row count of row-group `tile` (a group is up to
+ * a.mgroup consecutive 128-row tiles of one expert); all threads of the
+ * block get the same answer; false when the group is past the last expert. */
 __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, int *e_out,
                                            int *m0_out, int *M_out) {
     __shared__ int s_e, s_m0, s_M;
     if (threadIdx.x < MM_WAVE) {
         const int lane = threadIdx.x;
         int found = -1, m0 = 0, Mf = 0;
+        const int GR = MM_I8T_BM * a.mgroup;   /* rows per group */
         if (!a.cnt) {
-            if (tile * MM_I8T_BM < a.T) { found = 0; m0 = tile * MM_I8T_BM; Mf = a.T; }
+            if (tile * GR < a.T) { found = 0; m0 = tile * GR; Mf = a.T; }
         } else {
             int base = 0;   /* tiles before this group of 64 experts */
             for (int e0 = 0; e0 < a.E && found < 0; e0 += MM_WAVE) {
                 const int e = e0 + lane;
                 const int M = e < a.E ? min(a.cnt[e], a.T) : 0;
-                const int nt = (M + MM_I8T_BM - 1) / MM_I8T_BM;
+                const int nt = (M + GR - 1) / GR;
                 int incl = nt;   /* inclusive wave prefix sum */
 #pragma unroll
                 for (int off = 1; off < MM_WAVE; off <<= 1) {
@@ -344,7 +387,7 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
                 if (bal) {
                     const int src = __ffsll((long long)bal) - 1;
                     found = e0 + src;
-                    m0 = (tile - __shfl(excl, src, MM_WAVE)) * MM_I8T_BM;
+                    m0 = (tile - __shfl(excl, src, MM_WAVE)) * GR;
                     Mf = __shfl(M, src, MM_WAVE);
                 }
                 base += __shfl(incl, MM_WAVE - 1, MM_WAVE);
@@ -359,62 +402,76 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
     return s_e >= 0;
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[2][2 * T_FRAGS * 1024];
-    int e, m0, M;
-    if (!tile_owner(a, blockIdx.y, &e, &m0, &M)) return;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+/* 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (direct
+ * global -> LDS load, no VGPR staging). */
+__device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
+}
+
+/* LDS byte address of a __shared__ location. */
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
+}
+
+/* ds_read_b128 issued as inline assembly: the compiler's conservative
+ * "wait for every outstanding direct-to-LDS load before any LDS read" would
+ * otherwise drain the whole load ring every K step.  The caller orders the
+ * reads with explicit vmcnt waits and a barrier, and must follow them with
+ * lds_wait_regs() before using the results. */
+__device__ __forceinline__ v4i ds_read16(uint32_t addr) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+
+/* s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima). */
+#define VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
+#define T_STAGES 4
+#define T_STAGE_BYTES (2 * T_FRAGS * 1024)
+
+/* One 128-row x 8-fragment tile starting at row m0 of expert e (M rows). */
+__device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_STAGE_BYTES],
+                                           int e, int m0, int M) {
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
     const int wm = wave >> 1, wn = wave & 1;
     const int KB = a.Kd / 64;
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
     const int fr0 = blockIdx.x * T_FRAGS;
-    if (fr0 >= nfr_total) return;   /* uniform per block */
     const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
     const int8_t *bexp = a.b + (size_t)e * a.b_expert_stride;
 
-    /* this thread's two A rows and two B fragments (fixed over K) */
-    const int part = tid & 3;
+    /* Wave w loads A fragments 2w, 2w+1 (rows 32w .. 32w+31 of the tile) and
+     * B fragments 2w, 2w+1 of every K step.  Lane L of an A fragment carries
+     * row (L % 16), bytes 16 * (L / 16) of the 64-byte K step. */
     const int8_t *asrc[2];
-    bool aval[2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        const int r = (tid >> 2) + 64 * h, m = m0 + r;
-        aval[h] = m < M;
+        const int m = m0 + (2 * wave + h) * 16 + (lane & 15);
         int arow = 0;
-        if (aval[h]) {
+        if (m < M) {
             const int rid = rows ? rows[m] : m;
             arow = (a.a_by_route || !rows) ? rid : rid / a.K;
+        } else {
+            const int rid = rows ? rows[m0] : m0;   /* any valid row; result discarded */
+            arow = (a.a_by_route || !rows) ? rid : rid / a.K;
         }
-        asrc[h] = a.a + (size_t)arow * a.Kd + part * 16;
+        asrc[h] = a.a + (size_t)arow * a.Kd + (lane >> 4) * 16;
     }
     const int8_t *bsrc[2];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int f = (tid >> 6) + 4 * h;
-        bsrc[h] = bexp + (size_t)min(fr0 + f, nfr_total - 1) * KB * 1024 + lane * 16;
-    }
-    /* LDS destinations of those chunks */
-    int adst[2], bdst[2];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int r = (tid >> 2) + 64 * h;
-        adst[h] = (r >> 4) * 1024 + ((r & 15) + 16 * part) * 16;
-        bdst[h] = T_FRAGS * 1024 + ((tid >> 6) + 4 * h) * 1024 + lane * 16;
-    }
-    v4i ra[2], rb[2];
-    auto gload = [&](int kb) {
+    for (int h = 0; h < 2; h++)
+        bsrc[h] = bexp + (size_t)min(fr0 + 2 * wave + h, nfr_total - 1) * KB * 1024 + lane * 16;
+    auto issue = [&](int kb) {
+        int8_t *st = lds[kb % T_STAGES];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            ra[h] = aval[h] ? *(const v4i *)(asrc[h] + kb * 64) : (v4i){0, 0, 0, 0};
-            rb[h] = ldg16(bsrc[h] + kb * 1024);
-        }
-    };
-    auto lstore = [&](int s) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            *(v4i *)(&lds[s][adst[h]]) = ra[h];
-            *(v4i *)(&lds[s][bdst[h]]) = rb[h];
+            lds_dma16(asrc[h] + kb * 64, st + (2 * wave + h) * 1024);
+            lds_dma16(bsrc[h] + (size_t)kb * 1024, st + T_FRAGS * 1024 + (2 * wave + h) * 1024);
         }
     };
 
@@ -424,25 +481,32 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_a
 #pragma unroll
         for (int f = 0; f < 4; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < T_STAGES - 1; s++)
+        if (s < KB) issue(s);
     for (int kb = 0; kb < KB; kb++) {
-        const int s = kb & 1;
-        if (kb + 1 < KB) gload(kb + 1);
+        /* this wave's loads for step kb are done once at most 4 * (number of
+         * later steps already issued) of its loads are outstanding */
+        const int later = min(T_STAGES - 2, KB - 1 - kb);
+        if (later >= 2) VMCNT_WAIT(8);
+        else if (later == 1) VMCNT_WAIT(4);
+        else VMCNT_WAIT(0);
+        __builtin_amdgcn_s_barrier();   /* every wave's part of stage kb has landed,
+                                           and stage kb-1 is no longer being read */
+        if (kb + T_STAGES - 1 < KB) issue(kb + T_STAGES - 1);
+        const uint32_t st = lds_addr(lds[kb % T_STAGES]) + lane * 16;
         v4i av[4], bv[4];
 #pragma unroll
-        for (int mi = 0; mi < 4; mi++)
-            av[mi] = *(const v4i *)(&lds[s][(wm * 4 + mi) * 1024 + lane * 16]);
+        for (int mi = 0; mi < 4; mi++) av[mi] = ds_read16(st + (wm * 4 + mi) * 1024);
 #pragma unroll
-        for (int f = 0; f < 4; f++)
-            bv[f] = *(const v4i *)(&lds[s][T_FRAGS * 1024 + (wn * 4 + f) * 1024 + lane * 16]);
+        for (int f = 0; f < 4; f++) bv[f] = ds_read16(st + T_FRAGS * 1024 + (wn * 4 + f) * 1024);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]),
+                       "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]));
 #pragma unroll
         for (int mi = 0; mi < 4; mi++)
 #pragma unroll
             for (int f = 0; f < 4; f++) acc[mi][f] = mfma_i8(av[mi], bv[f], acc[mi][f]);
-        if (kb + 1 < KB) lstore(s ^ 1);
-        __syncthreads();
     }
 
     /* epilogue */
@@ -484,5 +548,21 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_a
                 }
             }
         }
+    }
+}
+
+/* grid.x = 8-fragment column slab, grid.y = row group.  A block walks the
+ * group's 128-row tiles in order, so the slab's weights (K x 128 bytes) come
+ * from HBM once and from this CU's L2 for the group's later tiles. */
+extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[T_STAGES][T_STAGE_BYTES];
+    int e, g0, M;
+    if (!tile_owner(a, blockIdx.y, &e, &g0, &M)) return;
+    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
+    if ((int)blockIdx.x * T_FRAGS >= nfr_total) return;   /* uniform per block */
+    const int g1 = min(M, g0 + a.mgroup * MM_I8T_BM);
+    for (int m0 = g0; m0 < g1; m0 += MM_I8T_BM) {
+        tiled_tile(a, lds, e, m0, M);
+        __builtin_amdgcn_s_barrier();   /* the LDS ring is refilled by the next tile */
     }
 }

@@ -12,7 +12,8 @@
  *   - softmax (run.c:95-105): max, e^(x - max) (-inf -> 0), sum in ascending
  *     expert order, divide; or sigmoid 1 / (1 + e^-x) (run.c:125-127).
  *   - top-k (run.c:132-143): K passes; each picks the unused expert with the
- *     largest score + bias, lowest index on a tie (the CPU's strict '>').
+ *     largest score + bias, lowest index on a tie (the CPU's strict '>'),
+ *     computed as each expert's rank in that order.
  *   - weight = raw score; optional normalisation seeded with 1e-20; times
  *     routed_scaling (run.c:144-149).
  * A wave routes TPW tokens; lane l holds experts l, l+64, ... (EJ of them).
@@ -203,13 +204,31 @@ __device__ __forceinline__ void router_select_wave(const mm_router_args &a, int 
             }
         }
 
-        bool used[EJ];
+        /* Greedy top-k of run.c:132-143 as ranks: the expert chosen in pass
+         * r is the one with exactly r others ahead of it in the order
+         * (score + bias descending, index ascending), which is the order the
+         * CPU's strict '>' scan picks them in.  One readlane sweep computes
+         * every expert's rank; no cross-lane shuffles. */
         float sel[EJ];
+        int rank[EJ];
 #pragma unroll
         for (int j = 0; j < EJ; j++) {
-            int e = lane + MM_WAVE * j;
-            used[j] = e >= E;
+            const int e = lane + MM_WAVE * j;
             sel[j] = p[j] + (a.bias && e < E ? a.bias[e] : 0.0f);
+            rank[j] = 0;
+        }
+#pragma unroll
+        for (int jo = 0; jo < EJ; jo++) {
+            const int n = min(MM_WAVE, E - MM_WAVE * jo);
+            for (int l = 0; l < n; l++) {
+                const float so = readlane_f(sel[jo], l);
+                const int eo = l + MM_WAVE * jo;
+#pragma unroll
+                for (int j = 0; j < EJ; j++) {
+                    const int e = lane + MM_WAVE * j;
+                    rank[j] += (so > sel[j] || (so == sel[j] && eo < e)) ? 1 : 0;
+                }
+            }
         }
         int idx[MM_KMAX];
         float w[MM_KMAX];
@@ -218,35 +237,16 @@ __device__ __forceinline__ void router_select_wave(const mm_router_args &a, int 
             idx[r] = 0;
             w[r] = 0.0f;
             if (r >= K) continue;
-            float bv = -INFINITY;
-            int bi = 0x7fffffff;
 #pragma unroll
-            for (int j = 0; j < EJ; j++)
-                if (!used[j] && (bi == 0x7fffffff || sel[j] > bv)) {
-                    bv = sel[j];
-                    bi = lane + MM_WAVE * j;
-                }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                float ov = __shfl_xor(bv, off, MM_WAVE);
-                int oi = __shfl_xor(bi, off, MM_WAVE);
-                if (oi != 0x7fffffff &&
-                    (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
+            for (int j = 0; j < EJ; j++) {
+                const unsigned long long m =
+                    __ballot(lane + MM_WAVE * j < E && rank[j] == r);
+                if (m) {
+                    const int l = __ffsll((long long)m) - 1;
+                    idx[r] = l + MM_WAVE * j;
+                    w[r] = readlane_f(p[j], l);
                 }
             }
-            bi = __builtin_amdgcn_readfirstlane(bi);
-            const int owner = bi & (MM_WAVE - 1), jj = bi / MM_WAVE;
-            float pw = 0.0f;
-#pragma unroll
-            for (int j = 0; j < EJ; j++)
-                if (j == jj) {
-                    pw = readlane_f(p[j], owner);
-                    if (lane == owner) used[j] = true;
-                }
-            idx[r] = bi;
-            w[r] = pw;
         }
         if (a.norm_topk) {
             float s = 1e-20f;
