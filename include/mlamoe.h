@@ -181,6 +181,41 @@ MM_API int mm_moe_forward_i8_debug_dev(mm_ctx *ctx, int layer, int T, const floa
 MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, int *topk_idx,
                    float *topk_w, unsigned flags);
 
+/* ---- MLA absorbed decode --------------------------------------------------- */
+
+/* The attention fields of the reference Config (include/model.h:12-42). */
+typedef struct {
+    int n_heads;            /* NH */
+    int qk_nope_head_dim;   /* QKN */
+    int qk_rope_head_dim;   /* QKR (64) */
+    int kv_lora_rank;       /* KVL (512) */
+    int v_head_dim;         /* VHD */
+    float softmax_scale;    /* (QKN + QKR)^-0.5 (src/model_load.c:270) */
+} mm_mla_config;
+
+/* Configure MLA for `n_layers` layers; kv_lora_rank 512 and qk_rope_head_dim
+ * 64 are served (DeepSeek-V2-Lite, GLM-4.7-Flash). */
+MM_API int mm_mla_init(mm_ctx *ctx, const mm_mla_config *cfg, int n_layers);
+
+/* Upload one layer's kv_b_proj weight, [NH * (QKN + VHD), KVL] bf16,
+ * head-interleaved [W_UK_h | W_UV_h] per head as the reference splits it
+ * (src/model_load.c:80-86; include/model.h:56-65).  Synchronous. */
+MM_API int mm_mla_load_layer(mm_ctx *ctx, int layer, const uint16_t *kv_b, unsigned flags);
+
+/* The absorbed per-head decode chain of forward_absorbed (src/run.c:430-460)
+ * for B sequences.  Device pointers, asynchronous:
+ *   q      [B, NH, QKN + QKR] fp32, q_nope | q_pe (RoPE applied)
+ *   cache  [B, seq_stride, KVL + QKR] bf16 latent cache (c_kv | k_pe), the
+ *          first kv_len (or kv_lens[b]) rows of each sequence attended
+ *   kv_lens [B] per-sequence lengths <= kv_len, or NULL (all kv_len)
+ *   ctx    [B, NH * VHD] fp32 output (ctx_h of run.c:460, heads concatenated)
+ *   qabs   [B, NH, KVL], probs [B, NH, kv_len], clat [B, NH, KVL]: the
+ *          q_absorbed, softmax weights and latent context, or NULL */
+MM_API int mm_mla_absorbed_decode_dev(mm_ctx *ctx, int layer, int B, const float *q,
+                                      const uint16_t *cache, int seq_stride,
+                                      const int32_t *kv_lens, int kv_len, float *ctx_out,
+                                      float *qabs, float *probs, float *clat);
+
 #ifdef __cplusplus
 }
 #endif

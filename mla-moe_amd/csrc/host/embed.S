@@ -5,20 +5,30 @@
 
     .balign 4096
     .globl mm_co_moe_bf16
+    .hidden mm_co_moe_bf16
     .type mm_co_moe_bf16, @object
 mm_co_moe_bf16:
     .incbin "moe_bf16.hsaco"
 
     .balign 4096
     .globl mm_co_util
+    .hidden mm_co_util
     .type mm_co_util, @object
 mm_co_util:
     .incbin "util.hsaco"
 
     .balign 4096
     .globl mm_co_moe_i8
+    .hidden mm_co_moe_i8
     .type mm_co_moe_i8, @object
 mm_co_moe_i8:
     .incbin "moe_i8.hsaco"
+
+    .balign 4096
+    .globl mm_co_mla
+    .hidden mm_co_mla
+    .type mm_co_mla, @object
+mm_co_mla:
+    .incbin "mla.hsaco"
 
     .section .note.GNU-stack, "", @progbits

@@ -17,10 +17,11 @@
 extern const unsigned char mm_co_moe_bf16[];
 extern const unsigned char mm_co_util[];
 extern const unsigned char mm_co_moe_i8[];
+extern const unsigned char mm_co_mla[];
 
-enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_COUNT };
+enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_COUNT };
 static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util,
-                                                          mm_co_moe_i8};
+                                                          mm_co_moe_i8, mm_co_mla};
 
 static const struct {
     const char *name;
@@ -42,6 +43,9 @@ static const struct {
     [K_I8_TILED] = {"mm_i8_gemm_tiled", MOD_MOE_I8},
     [K_I8_GU_S] = {"mm_i8_gu_s", MOD_MOE_I8},
     [K_I8_DOWN_S] = {"mm_i8_down_s", MOD_MOE_I8},
+    [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
+    [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
+    [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
 };
 
 /* ---- errors ------------------------------------------------------------- */
@@ -131,6 +135,7 @@ void mm_ctx_destroy(mm_ctx *c) {
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
     mm_moe_release(c);
+    mm_mla_release(c);
     if (c->ws) hipFree(c->ws);
     for (size_t i = 0; i < c->ev_pool_n; i++) hipEventDestroy(c->ev_pool[i]);
     free(c->ev_pool);

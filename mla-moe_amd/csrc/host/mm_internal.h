@@ -27,6 +27,9 @@ typedef enum {
     K_I8_TILED,
     K_I8_GU_S,
     K_I8_DOWN_S,
+    K_MLA_QPREP,
+    K_MLA_ATTN,
+    K_MLA_COMBINE,
     K_COUNT
 } mm_kernel_id;
 
@@ -68,6 +71,12 @@ struct mm_ctx {
     mm_moe_layer *layers;
     int32_t *moe_cnt;           /* [E] per-expert row counters, zero between calls */
 
+    /* MLA */
+    int mla_ready;
+    mm_mla_config mla;
+    int mla_layers;
+    uint16_t **mla_kvb;         /* [layers] device kv_b_proj weights */
+
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
 
     /* growable device workspace */
@@ -93,5 +102,6 @@ int mm_launch(mm_ctx *ctx, mm_kernel_id id, unsigned gx, unsigned gy, unsigned g
 int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
 
 void mm_moe_release(mm_ctx *ctx);
+void mm_mla_release(mm_ctx *ctx);
 
 #endif

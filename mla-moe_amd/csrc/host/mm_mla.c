@@ -1,0 +1,100 @@
+/* mm_mla.c -- MLA absorbed decode (host side).
+ *
+ * Replaces the absorbed per-head loop of forward_absorbed (src/run.c:430-460)
+ * for B sequences at once.  kv_b is the reference's kv_b_proj weight,
+ * head-interleaved [W_UK_h | W_UV_h] per head (src/model_load.c:80-86).
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "mm_internal.h"
+
+void mm_mla_release(mm_ctx *c) {
+    if (!c->mla_kvb) return;
+    for (int l = 0; l < c->mla_layers; l++)
+        if (c->mla_kvb[l]) hipFree(c->mla_kvb[l]);
+    free(c->mla_kvb);
+    c->mla_kvb = NULL;
+    c->mla_ready = 0;
+}
+
+int mm_mla_init(mm_ctx *c, const mm_mla_config *cfg, int n_layers) {
+    if (!c || !cfg) return mm_fail(MM_ERR_INVALID, "mm_mla_init: NULL argument");
+    if (c->mla_ready) return mm_fail(MM_ERR_STATE, "mm_mla_init: already initialised");
+    if (n_layers <= 0 || cfg->n_heads <= 0 || cfg->qk_nope_head_dim <= 0 || cfg->v_head_dim <= 0)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_init: non-positive dimension");
+    if (cfg->kv_lora_rank != MM_MLA_KVL || cfg->qk_rope_head_dim != MM_MLA_QKR)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_init: kernels serve kv_lora_rank %d and "
+                       "qk_rope_head_dim %d", MM_MLA_KVL, MM_MLA_QKR);
+    c->mla_kvb = calloc((size_t)n_layers, sizeof(uint16_t *));
+    if (!c->mla_kvb) return mm_fail(MM_ERR_NOMEM, "mm_mla_init: calloc");
+    c->mla = *cfg;
+    c->mla_layers = n_layers;
+    c->mla_ready = 1;
+    return MM_OK;
+}
+
+int mm_mla_load_layer(mm_ctx *c, int layer, const uint16_t *kv_b, unsigned flags) {
+    if (!c || !kv_b) return mm_fail(MM_ERR_INVALID, "mm_mla_load_layer: NULL argument");
+    if (!c->mla_ready) return mm_fail(MM_ERR_STATE, "mm_mla_load_layer: call mm_mla_init first");
+    if (layer < 0 || layer >= c->mla_layers)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_load_layer: layer %d out of range", layer);
+    if (c->mla_kvb[layer]) return mm_fail(MM_ERR_STATE, "mm_mla_load_layer: layer %d loaded", layer);
+    int st = mm_set_device(c);
+    if (st) return st;
+    const mm_mla_config *g = &c->mla;
+    const size_t n = (size_t)g->n_heads * (g->qk_nope_head_dim + g->v_head_dim) * g->kv_lora_rank;
+    MM_HIP(hipMalloc((void **)&c->mla_kvb[layer], n * 2));
+    MM_HIP(hipMemcpyAsync(c->mla_kvb[layer], kv_b, n * 2,
+                          (flags & MM_LOAD_DEVICE_PTRS) ? hipMemcpyDeviceToDevice
+                                                        : hipMemcpyHostToDevice,
+                          c->stream));
+    MM_HIP(hipStreamSynchronize(c->stream));
+    return MM_OK;
+}
+
+int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
+                               const uint16_t *cache, int seq_stride, const int32_t *kv_lens,
+                               int kv_len, float *ctx_out, float *qabs, float *probs,
+                               float *clat) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
+    if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
+        return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
+    if (B < 0 || (B > 0 && (!q || !cache || !ctx_out)))
+        return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL argument");
+    if (B == 0) return MM_OK;
+    if (kv_len < 1 || seq_stride < kv_len)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: need 1 <= kv_len <= seq_stride");
+    const int nchunks = (kv_len + MM_MLA_CHUNK - 1) / MM_MLA_CHUNK;
+    if (nchunks > 64)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_absorbed_decode_dev: kv_len > %d",
+                       64 * MM_MLA_CHUNK);
+    if ((uintptr_t)cache % 16)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: cache must be 16-byte aligned");
+    int st = mm_set_device(c);
+    if (st) return st;
+    const mm_mla_config *g = &c->mla;
+    const int NH = g->n_heads, HG = (NH + 15) / 16;
+    const size_t qf_b = (size_t)B * HG * 2 * MM_MLA_KC * 64 * 8 * 2;
+    const size_t qa_b = qabs ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
+    const size_t ml_b = (size_t)B * HG * nchunks * 32 * 4;
+    const size_t po_b = (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
+    char *ws;
+    const size_t a1 = (qf_b + 255) & ~(size_t)255, a2 = (qa_b + 255) & ~(size_t)255;
+    const size_t a3 = (ml_b + 255) & ~(size_t)255;
+    if ((st = mm_workspace(c, a1 + a2 + a3 + po_b, (void **)&ws))) return st;
+    uint16_t *qfrag = (uint16_t *)ws;
+    if (!qabs) qabs = (float *)(ws + a1);
+    float *part_ml = (float *)(ws + a1 + a2), *part_o = (float *)(ws + a1 + a2 + a3);
+
+    mm_mla_qprep_args qa = {q, c->mla_kvb[layer], qabs, qfrag, B, NH, g->qk_nope_head_dim,
+                            g->v_head_dim, HG};
+    if ((st = mm_launch(c, K_MLA_QPREP, (unsigned)(HG * 16), (unsigned)B, 1, 256, 0, &qa))) return st;
+    mm_mla_attn_args aa = {qfrag, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
+                           part_o, probs, kv_len, NH, HG, nchunks};
+    if ((st = mm_launch(c, K_MLA_ATTN, (unsigned)nchunks, (unsigned)B, (unsigned)HG, 128, 0, &aa)))
+        return st;
+    mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
+                              probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks};
+    return mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, 1, 256, 0, &ca);
+}

@@ -180,3 +180,48 @@ typedef struct {
     int mgroup;              /* consecutive 128-row tiles one block walks (weight reuse) */
     int max_groups;          /* grid.y bound */
 } mm_i8_tiled_args;
+
+/* ---- MLA absorbed decode ----------------------------------------------------- */
+#define MM_MLA_KVL 512            /* kv_lora_rank served by the kernels */
+#define MM_MLA_QKR 64             /* qk_rope_head_dim served by the kernels */
+#define MM_MLA_KVD (MM_MLA_KVL + MM_MLA_QKR)
+#define MM_MLA_KC (MM_MLA_KVD / 32) /* 32-wide latent chunks of one cache row */
+#define MM_MLA_CHUNK 512          /* keys per attention block (2 waves x 256) */
+
+/* qabs = q_nope . W_UK per head, plus the bf16 hi/lo halves of
+ * [qabs | q_pe] in MFMA A-operand order for the score MFMA. */
+typedef struct {
+    const float *q;           /* [B, NH, QKN + QKR] */
+    const uint16_t *kv_b;     /* [NH * (QKN + VHD), KVL] bf16, head-interleaved */
+    float *qabs;              /* [B, NH, KVL] */
+    uint16_t *qfrag;          /* [B, HG, 2 (hi/lo), KC, 64 lanes, 8] bf16 */
+    int B, NH, QKN, VHD, HG;
+} mm_mla_qprep_args;
+
+/* Flash-decoding partials: block (chunk, b, head group). */
+typedef struct {
+    const uint16_t *qfrag;    /* as above */
+    const uint16_t *cache;    /* [B, seq_stride, KVD] bf16 */
+    const int32_t *kv_lens;   /* [B] or 0 */
+    int kv_len;               /* used when kv_lens == 0 */
+    int seq_stride;
+    float scale;
+    float *part_ml;           /* [B, HG, nchunks, 2, 16]: running max, sum */
+    float *part_o;            /* [B, HG, nchunks, 16, KVL] unnormalised */
+    float *scores;            /* [B, NH, probs_stride] scaled scores (debug) or 0 */
+    int probs_stride;
+    int NH, HG, nchunks;
+} mm_mla_attn_args;
+
+/* Merge the chunk partials, normalise (clat), apply W_UV -> ctx. */
+typedef struct {
+    const float *part_ml, *part_o;
+    const uint16_t *kv_b;
+    const int32_t *kv_lens;
+    int kv_len;
+    float *ctx;               /* [B, NH * VHD] */
+    float *clat;              /* [B, NH, KVL] or 0 */
+    float *probs;             /* [B, NH, probs_stride]: scores in, probabilities out, or 0 */
+    int probs_stride;
+    int B, NH, QKN, VHD, HG, nchunks;
+} mm_mla_combine_args;

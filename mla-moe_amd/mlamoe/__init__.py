@@ -46,6 +46,13 @@ class MoeLayerWeights(C.Structure):
                 ("shared_gate", _vp), ("shared_up", _vp), ("shared_down", _vp)]
 
 
+class MlaConfig(C.Structure):
+    """Mirror of mm_mla_config (the attention fields of the reference Config)."""
+    _fields_ = [("n_heads", C.c_int), ("qk_nope_head_dim", C.c_int),
+                ("qk_rope_head_dim", C.c_int), ("kv_lora_rank", C.c_int),
+                ("v_head_dim", C.c_int), ("softmax_scale", C.c_float)]
+
+
 class MoeI8Debug(C.Structure):
     _fields_ = [(n, _vp) for n in ("qx", "sx", "acc_gu", "h", "qh", "sh", "acc_d", "y", "hs",
                                    "qhs", "shs", "ys")]
@@ -91,6 +98,10 @@ def lib():
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
         L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_mla_init.argtypes = [_vp, C.POINTER(MlaConfig), C.c_int]
+        L.mm_mla_load_layer.argtypes = [_vp, C.c_int, _vp, C.c_uint]
+        L.mm_mla_absorbed_decode_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
+                                                 C.c_int, _vp, _vp, _vp, _vp]
         L.mm_moe_router_logits_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp]
         L.mm_moe_forward_i8_debug_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
                                                   _vp, _vp, C.c_uint, C.POINTER(MoeI8Debug)]
@@ -310,6 +321,51 @@ class Context:
         res = {k: b.download() for k, b in bufs.items()}
         out = (dout.download(), didx.download(), dw.download(), dp.download(), res)
         for b in list(bufs.values()) + [dx, dout, didx, dw, dp] + ([dl] if dl else []):
+            b.free()
+            self._bufs.remove(b)
+        return out
+
+    # MLA absorbed decode -------------------------------------------------------
+    def mla_init(self, NH, QKN=128, QKR=64, KVL=512, VHD=128, scale=None, n_layers=1):
+        if scale is None:
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(QKN + QKR)))
+        cfg = MlaConfig(NH, QKN, QKR, KVL, VHD, scale)
+        _check(lib().mm_mla_init(self.h, C.byref(cfg), n_layers))
+        self._mla_cfg = cfg
+
+    def mla_load_layer(self, layer, kv_b, flags=0):
+        if flags & MM_LOAD_DEVICE_PTRS:
+            _check(lib().mm_mla_load_layer(self.h, layer, kv_b.ptr, flags))
+        else:
+            kv_b = np.ascontiguousarray(kv_b, np.uint16)
+            _check(lib().mm_mla_load_layer(self.h, layer, kv_b.ctypes.data, flags))
+
+    def mla_absorbed_decode_dev(self, layer, B, q, cache, seq_stride, kv_len, ctx_out,
+                                kv_lens=None, qabs=None, probs=None, clat=None):
+        p = lambda b: None if b is None else b.ptr  # noqa: E731
+        _check(lib().mm_mla_absorbed_decode_dev(self.h, layer, B, q.ptr, cache.ptr, seq_stride,
+                                                p(kv_lens), kv_len, ctx_out.ptr, p(qabs),
+                                                p(probs), p(clat)))
+
+    def mla_absorbed_decode(self, layer, q, cache, kv_len, kv_lens=None):
+        """Host arrays: q [B, NH, QKN+QKR] fp32, cache [B, L, KVL+QKR] bf16
+        (uint16).  Returns ctx [B, NH*VHD], qabs, probs, clat."""
+        cfg = self._mla_cfg
+        q = np.ascontiguousarray(q, np.float32)
+        cache = np.ascontiguousarray(cache, np.uint16)
+        B, L = cache.shape[0], cache.shape[1]
+        NH, KVL, VHD = cfg.n_heads, cfg.kv_lora_rank, cfg.v_head_dim
+        bufs = dict(q=self.to_device(q), cache=self.to_device(cache),
+                    ctx=self.empty((B, NH * VHD), np.float32),
+                    qabs=self.empty((B, NH, KVL), np.float32),
+                    probs=self.empty((B, NH, kv_len), np.float32),
+                    clat=self.empty((B, NH, KVL), np.float32))
+        if kv_lens is not None:
+            bufs["lens"] = self.to_device(np.ascontiguousarray(kv_lens, np.int32))
+        self.mla_absorbed_decode_dev(layer, B, bufs["q"], bufs["cache"], L, kv_len, bufs["ctx"],
+                                     bufs.get("lens"), bufs["qabs"], bufs["probs"], bufs["clat"])
+        out = tuple(bufs[k].download() for k in ("ctx", "qabs", "probs", "clat"))
+        for b in bufs.values():
             b.free()
             self._bufs.remove(b)
         return out
