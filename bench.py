@@ -243,6 +243,37 @@ def bench_decode_bf16(ctx, steps, warmup):
                 kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()})
 
 
+def bench_mla_decode(ctx, steps, warmup, B=32, NH=16, L=4096):
+    """Config 5: MLA absorbed decode, B sequences x NH heads over a bf16
+    latent cache of L positions."""
+    log("[mla_decode] setup")
+    QKN, QKR, KVL, VHD = 128, 64, 512, 128
+    ctx.mla_init(NH, QKN, QKR, KVL, VHD)
+    kvb = ctx.empty((NH * (QKN + VHD), KVL), np.uint16)
+    ctx.fill(kvb, NH * (QKN + VHD) * KVL, mlamoe.MM_FILL_BF16_NORMAL, 21, 0.02)
+    ctx.mla_load_layer(0, kvb, mlamoe.MM_LOAD_DEVICE_PTRS)
+    cache = ctx.empty((B, L, KVL + QKR), np.uint16)
+    ctx.fill(cache, B * L * (KVL + QKR), mlamoe.MM_FILL_BF16_NORMAL, 22, 1.0)
+    q = ctx.empty((B, NH, QKN + QKR), np.float32)
+    ctx.fill(q, B * NH * (QKN + QKR), mlamoe.MM_FILL_F32_NORMAL, 23, 1.0)
+    out = ctx.empty((B, NH * VHD), np.float32)
+    lib, h = mlamoe.lib(), ctx.h
+
+    def step():
+        mlamoe._check(lib.mm_mla_absorbed_decode_dev(h, 0, B, q.ptr, cache.ptr, L, None, L,
+                                                     out.ptr, None, None, None))
+    ms, wall = timed(ctx, step, steps * 5, warmup)
+    names = ["mm_mla_qprep", "mm_mla_attn", "mm_mla_combine"]
+    prof = profile_kernels(ctx, step, 20, names)
+    nbytes = B * L * (KVL + QKR) * 2 + 2 * NH * QKN * KVL * 2   # cache + W_UK + W_UV
+    attn_bytes = B * L * (KVL + QKR) * 2
+    at_ms = prof["mm_mla_attn"][0]
+    return dict(ms_per_step=ms, seq_per_s=B / (ms * 1e-3), gbs=nbytes / (ms * 1e-3) / 1e9,
+                frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                attn_kernel_gbs=attn_bytes / (at_ms * 1e-3) / 1e9,
+                kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()})
+
+
 # ---------------------------------------------------------------------------
 
 def cpu_baseline_decode(B=64, seconds_hint=True):
@@ -301,6 +332,8 @@ def main():
             extra["prefill_i8_config3"] = bench_prefill_i8(ctx, args.steps, args.warmup)
         with mlamoe.Context(0) as ctx:
             extra["decode_bf16_config1"] = bench_decode_bf16(ctx, args.steps, args.warmup)
+        with mlamoe.Context(0) as ctx:
+            extra["mla_decode_config5"] = bench_mla_decode(ctx, args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
     line = {

@@ -181,6 +181,19 @@ MM_API int mm_moe_forward_i8_debug_dev(mm_ctx *ctx, int layer, int T, const floa
 MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, int *topk_idx,
                    float *topk_w, unsigned flags);
 
+/* ---- dense bf16 matmul ------------------------------------------------------ */
+
+#define MM_MATMUL_X_BF16 1u       /* cast x to bf16 (truncation, include/tensor.h:16-20) */
+#define MM_MATMUL_ACCUMULATE 2u   /* y += x . W^T (the GPU gemv "add" variant) */
+
+/* matmul (src/run.c:29-37) over T rows: y[t, d] = sum_i x[t, i] * W[d, i],
+ * W bf16 row-major [d_out, n_in] (nn.Linear layout), x/y fp32.  Without
+ * MM_MATMUL_X_BF16 the fp32 x is carried as a bf16 hi/lo pair (two MFMAs),
+ * tracking the fp32 reference to ~1e-5.  n_in % 8 == 0.  Device pointers,
+ * asynchronous. */
+MM_API int mm_matmul_bf16_dev(mm_ctx *ctx, float *y, const float *x, const uint16_t *w,
+                              int d_out, int n_in, int T, unsigned flags);
+
 /* ---- MLA absorbed decode --------------------------------------------------- */
 
 /* The attention fields of the reference Config (include/model.h:12-42). */

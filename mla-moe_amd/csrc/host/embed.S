@@ -31,4 +31,11 @@ mm_co_moe_i8:
 mm_co_mla:
     .incbin "mla.hsaco"
 
+    .balign 4096
+    .globl mm_co_gemm_bf16
+    .hidden mm_co_gemm_bf16
+    .type mm_co_gemm_bf16, @object
+mm_co_gemm_bf16:
+    .incbin "gemm_bf16.hsaco"
+
     .section .note.GNU-stack, "", @progbits

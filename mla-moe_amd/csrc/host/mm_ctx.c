@@ -18,10 +18,12 @@ extern const unsigned char mm_co_moe_bf16[];
 extern const unsigned char mm_co_util[];
 extern const unsigned char mm_co_moe_i8[];
 extern const unsigned char mm_co_mla[];
+extern const unsigned char mm_co_gemm_bf16[];
 
-enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_COUNT };
+enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_GEMM_BF16, MOD_COUNT };
 static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util,
-                                                          mm_co_moe_i8, mm_co_mla};
+                                                          mm_co_moe_i8, mm_co_mla,
+                                                          mm_co_gemm_bf16};
 
 static const struct {
     const char *name;
@@ -46,6 +48,7 @@ static const struct {
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
+    [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
 };
 
 /* ---- errors ------------------------------------------------------------- */

@@ -30,6 +30,7 @@ typedef enum {
     K_MLA_QPREP,
     K_MLA_ATTN,
     K_MLA_COMBINE,
+    K_GEMM_BF16,
     K_COUNT
 } mm_kernel_id;
 

@@ -225,3 +225,14 @@ typedef struct {
     int probs_stride;
     int B, NH, QKN, VHD, HG, nchunks;
 } mm_mla_combine_args;
+
+/* ---- dense bf16 matmul --------------------------------------------------------- */
+/* y[t, d] (=|+=) sum_i x[t, i] * W[d, i]; W bf16 row-major [d_out, n_in]. */
+typedef struct {
+    const float *x;          /* [T, n_in] */
+    const uint16_t *w;       /* [d_out, n_in] */
+    float *y;                /* [T, d_out] */
+    int T, d_out, n_in;
+    int x_bf16;              /* 1: x truncated to bf16 (one MFMA); 0: hi/lo split */
+    int accumulate;
+} mm_gemm_bf16_args;

@@ -22,6 +22,7 @@ HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "mlamoe.h")
 MM_LOAD_BF16, MM_LOAD_INT8, MM_LOAD_DEVICE_PTRS = 1, 2, 4
 MM_FWD_BF16, MM_FWD_INT8, MM_FWD_ACCUMULATE = 0, 1, 2
 MM_FILL_BF16_NORMAL, MM_FILL_F32_NORMAL, MM_FILL_F32_UNIFORM = 0, 1, 2
+MM_MATMUL_X_BF16, MM_MATMUL_ACCUMULATE = 1, 2
 
 _vp = C.c_void_p
 
@@ -98,6 +99,7 @@ def lib():
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
         L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_matmul_bf16_dev.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
         L.mm_mla_init.argtypes = [_vp, C.POINTER(MlaConfig), C.c_int]
         L.mm_mla_load_layer.argtypes = [_vp, C.c_int, _vp, C.c_uint]
         L.mm_mla_absorbed_decode_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
@@ -324,6 +326,25 @@ class Context:
             b.free()
             self._bufs.remove(b)
         return out
+
+    # dense bf16 matmul ----------------------------------------------------------
+    def matmul_dev(self, y, x, w, d_out, n_in, T, flags=0):
+        _check(lib().mm_matmul_bf16_dev(self.h, y.ptr, x.ptr, w.ptr, d_out, n_in, T, flags))
+
+    def matmul(self, x, w, flags=0, y0=None):
+        """Mirror of the reference matmul (src/run.c:30) over the rows of x."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, np.shape(w)[1])
+        w = np.ascontiguousarray(w, np.uint16)
+        T, (d_out, n_in) = x.shape[0], w.shape
+        dx, dw = self.to_device(x), self.to_device(w)
+        dy = self.to_device(np.ascontiguousarray(y0, np.float32)) if y0 is not None else \
+            self.empty((T, d_out), np.float32)
+        self.matmul_dev(dy, dx, dw, d_out, n_in, T, flags)
+        y = dy.download()
+        for b in (dx, dw, dy):
+            b.free()
+            self._bufs.remove(b)
+        return y
 
     # MLA absorbed decode -------------------------------------------------------
     def mla_init(self, NH, QKN=128, QKR=64, KVL=512, VHD=128, scale=None, n_layers=1):

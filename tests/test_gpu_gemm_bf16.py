@@ -1,0 +1,63 @@
+"""GPU parity of the dense bf16 matmul (run.c:29-37 over T rows) against the
+oracle's matmul: max-abs-rel 2e-3 (fp32 accumulation in MFMA order)."""
+import numpy as np
+import pytest
+
+import mlamoe
+from conftest import load_golden, max_abs_rel
+from mlamoe import synth
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture
+def ctx():
+    c = mlamoe.Context(0)
+    yield c
+    c.close()
+
+
+def test_matmul_golden(ctx, oracle):
+    """Against the reference matmul's own outputs (tests/golden/matmul.npz);
+    the tiny shapes have n_in not a multiple of 8, which this build rejects."""
+    g = load_golden("matmul.npz")
+    for name in ("router", "expert"):
+        r = np.random.default_rng(int(g[f"{name}_seed"]))
+        d_out, n_in = (int(v) for v in g[f"{name}_shape"])
+        w = synth.normal_bf16(r, (d_out, n_in), 0.02)
+        x = synth.normal_f32(r, (n_in,))
+        y = ctx.matmul(x[None], w)[0]
+        assert max_abs_rel(y, g[f"{name}_y"]) < 1e-5, name
+    with pytest.raises(mlamoe.MMError):
+        ctx.matmul(g["tiny_x"][None], g["tiny_w"])
+
+
+@pytest.mark.parametrize("T,d_out,n_in", [(1, 64, 2048), (37, 100, 264), (512, 576, 2048),
+                                          (512, 4096, 512), (70, 3072, 2048)])
+def test_matmul_shapes(ctx, oracle, T, d_out, n_in):
+    print(f"matmul T={T} d_out={d_out} n_in={n_in}", flush=True)
+    rng = np.random.default_rng(T + d_out)
+    w = synth.normal_bf16(rng, (d_out, n_in), 0.02)
+    x = synth.normal_f32(rng, (T, n_in))
+    ref = oracle.matmul(x, w)
+    assert max_abs_rel(ctx.matmul(x, w), ref) < 1e-5      # fp32 x as a bf16 hi/lo pair
+    xb = synth.bf16_to_f32(synth.bf16_from_f32(x))         # the config-2 input cast
+    ref_b = oracle.matmul(xb, w)
+    got_b = ctx.matmul(x, w, mlamoe.MM_MATMUL_X_BF16)
+    assert max_abs_rel(got_b, ref_b) < TOL
+    # accumulate: y += x . W^T
+    y0 = synth.normal_f32(rng, (T, d_out))
+    got_acc = ctx.matmul(x, w, mlamoe.MM_MATMUL_ACCUMULATE, y0=y0)
+    assert max_abs_rel(got_acc - y0, ref) < 1e-5
+
+
+def test_matmul_integer_exact(ctx):
+    """Integer-valued operands with sums < 2^24: every order gives the exact
+    integer result, so the GPU must match it bit for bit."""
+    rng = np.random.default_rng(3)
+    w = rng.integers(-8, 9, size=(96, 256)).astype(np.float32)
+    x = rng.integers(-8, 9, size=(33, 256)).astype(np.float32)
+    exact = (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    got = ctx.matmul(x, synth.bf16_from_f32(w), mlamoe.MM_MATMUL_X_BF16)
+    assert np.array_equal(got, exact)
