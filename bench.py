@@ -274,6 +274,33 @@ def bench_mla_decode(ctx, steps, warmup, B=32, NH=16, L=4096):
                 kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()})
 
 
+def bench_dense_bf16(ctx, steps, warmup, T=512):
+    """Config 2: the four MLA projection GEMMs at prefill T=512, activations
+    cast to bf16 on the input side, fp32 accumulation."""
+    log("[dense_bf16] setup")
+    shapes = dict(q_proj=(3072, 2048), kv_a=(576, 2048), kv_b=(4096, 512), o_proj=(2048, 2048))
+    bufs = {}
+    for i, (k, (d, n)) in enumerate(shapes.items()):
+        w = ctx.empty((d, n), np.uint16)
+        ctx.fill(w, d * n, mlamoe.MM_FILL_BF16_NORMAL, 31 + i, 0.02)
+        x = ctx.empty((T, n), np.float32)
+        ctx.fill(x, T * n, mlamoe.MM_FILL_F32_NORMAL, 41 + i, 1.0)
+        y = ctx.empty((T, d), np.float32)
+        bufs[k] = (w, x, y, d, n)
+    lib, h = mlamoe.lib(), ctx.h
+
+    def step():
+        for w, x, y, d, n in bufs.values():
+            mlamoe._check(lib.mm_matmul_bf16_dev(h, y.ptr, x.ptr, w.ptr, d, n, T,
+                                                 mlamoe.MM_MATMUL_X_BF16))
+    ms, wall = timed(ctx, step, steps * 5, warmup)
+    prof = profile_kernels(ctx, step, 20, ["mm_gemm_bf16"])
+    flops = sum(2.0 * T * d * n for _, _, _, d, n in bufs.values())
+    return dict(ms_per_step=ms, tflops=flops / (ms * 1e-3) / 1e12,
+                frac_bf16_peak=flops / (ms * 1e-3) / 1e12 / 2516.6,
+                kernel_avg_us=round(prof["mm_gemm_bf16"][0] * 1e3, 2), gflop=flops / 1e9)
+
+
 # ---------------------------------------------------------------------------
 
 def cpu_baseline_decode(B=64, seconds_hint=True):
@@ -318,11 +345,35 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", choices=["decode_i8", "prefill_i8", "decode_bf16", "mla", "dense",
+                                       "calib"],
+                    help="run one workload and print its result dict (profiling runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first copy 1 GiB device-to-device (reference kernel for the "
+                         "FETCH_SIZE/WRITE_SIZE counter scale)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the multi-GPU sharding plan is design-only (DESIGN.md).", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        with mlamoe.Context(0) as ctx:
+            n = 1 << 30
+            src, dst = ctx.alloc(n, keep=True), ctx.alloc(n, keep=True)
+            ctx.fill(src, n // 4, mlamoe.MM_FILL_F32_UNIFORM, 1)
+            for _ in range(3):
+                mlamoe._check(mlamoe.lib().mm_d2d(ctx.h, dst.ptr, src.ptr, n))
+            log(f"[calibrate] copied {n} bytes x3 device-to-device")
+    if args.only == "calib":
+        return
+    if args.only:
+        fn = dict(decode_i8=bench_decode_i8, prefill_i8=bench_prefill_i8,
+                  decode_bf16=bench_decode_bf16, mla=bench_mla_decode,
+                  dense=bench_dense_bf16)[args.only]
+        with mlamoe.Context(0) as ctx:
+            print(json.dumps({args.only: fn(ctx, args.steps, args.warmup)}, default=float), flush=True)
+        return
 
     extra = {}
     with mlamoe.Context(0) as ctx:
@@ -334,6 +385,8 @@ def main():
             extra["decode_bf16_config1"] = bench_decode_bf16(ctx, args.steps, args.warmup)
         with mlamoe.Context(0) as ctx:
             extra["mla_decode_config5"] = bench_mla_decode(ctx, args.steps, args.warmup)
+        with mlamoe.Context(0) as ctx:
+            extra["dense_bf16_config2"] = bench_dense_bf16(ctx, args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
     line = {
