@@ -153,12 +153,10 @@ def bench_decode_i8(ctx, steps, warmup, B=64, L=26):
     ms, wall = timed(ctx, step, steps, warmup)
     touched = [len(np.unique(i.download())) for i in idx]
     R = B * K
-    names = ["mm_i8_route", "mm_i8_gu_s", "mm_i8_gu", "mm_i8_quant_h", "mm_i8_down_s",
-             "mm_i8_down", "mm_i8_combine"]
+    names = ["mm_i8_route", "mm_i8_gu", "mm_i8_quant_h", "mm_i8_down", "mm_i8_combine"]
     prof = profile_kernels(ctx, step, max(2, steps // 4), names)
-    # gate/up runs as two launches per layer: experts with <= 16 rows, then
-    # the larger ones and the shared expert; their sum is the gate/up GEMM
-    gu_ms = prof["mm_i8_gu_s"][0] + prof["mm_i8_gu"][0]
+    # one gate/up launch per layer covers the routed and the shared expert
+    gu_ms = prof["mm_i8_gu"][0]
     gu_bytes = float(np.mean([i8_gu_bytes(t, B, R) for t in touched]))
     step_bytes = float(sum(i8_layer_bytes(t, B, R) for t in touched))
     res = dict(
@@ -166,7 +164,7 @@ def bench_decode_i8(ctx, steps, warmup, B=64, L=26):
         step_gbs=step_bytes / (ms * 1e-3) / 1e9, step_bytes=step_bytes,
         touched_experts_per_layer=float(np.mean(touched)),
         kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()},
-        roofline=dict(bound="hbm", kernel="mm_i8_gu_s + mm_i8_gu (gate/up GEMM)",
+        roofline=dict(bound="hbm", kernel="mm_i8_gu (gate/up GEMM, routed + shared)",
                       achieved=gu_bytes / (gu_ms * 1e-3) / 1e9, peak=HBM_PEAK_GBS,
                       unit="GB/s", bytes_per_launch=gu_bytes, avg_launch_us=gu_ms * 1e3))
     res["roofline"]["frac"] = res["roofline"]["achieved"] / HBM_PEAK_GBS

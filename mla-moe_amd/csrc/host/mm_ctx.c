@@ -43,8 +43,6 @@ static const struct {
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
     [K_I8_TILED] = {"mm_i8_gemm_tiled", MOD_MOE_I8},
-    [K_I8_GU_S] = {"mm_i8_gu_s", MOD_MOE_I8},
-    [K_I8_DOWN_S] = {"mm_i8_down_s", MOD_MOE_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},

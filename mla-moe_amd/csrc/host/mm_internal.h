@@ -25,8 +25,6 @@ typedef enum {
     K_I8_COMBINE,
     K_PACK_I8,
     K_I8_TILED,
-    K_I8_GU_S,
-    K_I8_DOWN_S,
     K_MLA_QPREP,
     K_MLA_ATTN,
     K_MLA_COMBINE,

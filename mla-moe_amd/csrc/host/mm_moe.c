@@ -407,12 +407,10 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                 return st;
         }
     } else {
-        ga.wg_per_expert = (int)((I + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-        unsigned nb = (unsigned)(E * ga.wg_per_expert + (S + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-        /* experts with <= 16 rows, then the rest and the shared expert */
-        if ((st = mm_launch(c, K_I8_GU_S, (unsigned)(E * ga.wg_per_expert), 1, 1, 256, 0, &ga)))
-            return st;
-        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 256, 0, &ga))) return st;
+        /* shared-expert blocks, then every routed expert's blocks */
+        const size_t cu = 16 * MM_I8S_NBW_GU, per_e = (I / cu + MM_I8S_WAVES - 1) / MM_I8S_WAVES;
+        const unsigned nb = (unsigned)(S / cu + E * per_e);
+        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_WAVES, 0, &ga))) return st;
     }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
@@ -441,11 +439,9 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.y = y;
         ga.ys = ys;
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
-        ga.wg_per_expert = (int)((H + MM_I8_COLS_PER_WG - 1) / MM_I8_COLS_PER_WG);
-        unsigned nb = (unsigned)(E * ga.wg_per_expert + (S ? ga.wg_per_expert : 0));
-        if ((st = mm_launch(c, K_I8_DOWN_S, (unsigned)(E * ga.wg_per_expert), 1, 1, 256, 0, &ga)))
-            return st;
-        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 256, 0, &ga))) return st;
+        const size_t cd = 16 * MM_I8S_NBW_DOWN, per_e = (H / cd + MM_I8S_WAVES - 1) / MM_I8S_WAVES;
+        const unsigned nb = (unsigned)((S ? H / cd : 0) + E * per_e);
+        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_WAVES, 0, &ga))) return st;
     }
 
     mm_i8_combine_args ca = {y, ys, wts, out, c->moe_cnt, T, (int)H, (int)K, (int)E, acc, S > 0};

@@ -117,7 +117,6 @@ typedef struct {
     float *ys;               /* down out: shared [T, H] */
     int32_t *dbg_acc;        /* debug: raw accumulators, gate/up [T*K, 2, I], down [T*K, H], or 0 */
     int T, H, I, S, E, K;
-    int wg_per_expert;       /* blocks per routed expert */
 } mm_i8_gemm_args;
 
 /* Per-row quantisation of the SwiGLU output. */
@@ -153,9 +152,12 @@ typedef struct {
 
 /* Launch geometry shared by the int8 GEMM kernels and the host: 4 waves per
  * block, 2 sixteen-column blocks per wave. */
-#define MM_I8_WAVES 4
-#define MM_I8_NBW 2
-#define MM_I8_COLS_PER_WG (MM_I8_WAVES * MM_I8_NBW * 16)
+/* Decode-shaped GEMMs: blocks of MM_I8S_WAVES waves, each wave one unit of
+ * MM_I8S_NBW_* 16-column blocks.  H / 16 and (n_shared * I) / 16 must be
+ * multiples of the NBW values. */
+#define MM_I8S_WAVES 4
+#define MM_I8S_NBW_GU 1
+#define MM_I8S_NBW_DOWN 2
 
 /* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
  * the routed experts' row lists (or all T rows for the shared expert). */

@@ -11,9 +11,11 @@
  * Kernels, in launch order:
  *   mm_i8_route    router (router.h), per-expert row lists built with one
  *                  atomic slot per route, per-token quantisation of x
- *   mm_i8_gu       grouped gate/up GEMM + SwiGLU epilogue -> h (fp32)
+ *   mm_i8_gu       grouped gate/up GEMM + SwiGLU epilogue -> h (fp32),
+ *                  routed and shared experts in one launch (decode sizes)
  *   mm_i8_quant_h  per-row quantisation of h -> qh, sh
  *   mm_i8_down     grouped down GEMM -> y per route (fp32)
+ *   mm_i8_gemm_tiled  block-tiled variant of both GEMMs for prefill sizes
  *   mm_i8_combine  out[t] = sum_r w_r * y[t, r] + y_shared[t]
  *
  * The order of rows inside an expert's list depends on atomic timing, but
@@ -27,10 +29,6 @@
  * operand for one K step is one contiguous 1 KB block (kernel_params.h).
  */
 #include "router.h"
-
-#define I8_WAVES MM_I8_WAVES
-#define I8_NBW MM_I8_NBW
-#define I8_MT 4        /* 16-row tiles per pass (64 rows) */
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 
@@ -85,215 +83,291 @@ extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_i8_route(mm_i
     });
 }
 
-/* ---- grouped GEMM ---------------------------------------------------------- */
+/* ---- streaming grouped GEMM (decode) ------------------------------------------- */
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-/* One pass of up to MT*16 rows against this wave's I8_NBW column blocks.
- * GU: gate/up pair per column block (B fragments interleaved), SwiGLU
- * epilogue; otherwise a plain GEMM with a dequantising epilogue.  The K loop
- * is unrolled UNR deep so that UNR * I8_NBW * (GU ? 2 : 1) weight fragments
- * are in flight per wave.
- *   arow(m) -> pointer to row m of A (int8, K bytes), only called for m < M
- *   epi(m, col, acc0, acc1) consumes the int32 results of row m, column col */
-template <bool GU, int MT, int UNR, class ARow, class Epi>
-__device__ __forceinline__ void gemm_pass(const int8_t *bbase, int nb0, int nbl, int KB, int m0,
-                                          int M, ARow arow, Epi epi) {
-    const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int NB_STRIDE = (GU ? 2 : 1) * KB * 1024;
-    const int nmt = min(MT, (M - m0 + 15) >> 4);
-    const int8_t *ap[MT];
-    bool av[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; mi++) {
-        const int m = m0 + mi * 16 + (lane & 15);
-        av[mi] = mi < nmt && m < M;
-        ap[mi] = (av[mi] ? arow(m) : arow(m0)) + 16 * (lane >> 4);
-    }
-    const int8_t *bp[I8_NBW];
-#pragma unroll
-    for (int j = 0; j < I8_NBW; j++)
-        bp[j] = bbase + (size_t)min(nb0 + j, nbl - 1) * NB_STRIDE + lane * 16;
-
-    v4i acc0[MT][I8_NBW], acc1[MT][I8_NBW];
+/* One work unit = one wave = NF weight fragment columns (16 output columns
+ * each; for gate/up the gate and the up fragment of one column block) of one
+ * expert over the whole K, against MT 16-row tiles of that expert's rows.
+ *
+ * Weights stream once from HBM with non-temporal loads through a D-deep
+ * register ring: the loads of K step kb + D are issued as soon as step kb's
+ * MFMAs have been issued, so every wave keeps D steps of fragments in flight
+ * and never drains its queue inside the K loop.  The A rows (a few KB, read
+ * by every unit of the expert) come through the caches.
+ *
+ * Rows are independent in D = A * B, so lanes whose row is past M read any
+ * valid row and their results are discarded by the epilogue.
+ *   bp[f]  : lane's 16-byte slice of fragment column f at K step 0
+ *   ap[mi] : lane's 16-byte slice of A row tile mi at K step 0
+ * On return acc[mi][f] holds D[4*(lane/16) + i][lane % 16] of tile mi,
+ * fragment column f. */
+template <int NF, int MT, int D>
+__device__ __forceinline__ void stream_k(const int8_t *const (&bp)[NF], const int8_t *const (&ap)[MT],
+                                         int KB, v4i (&acc)[MT][NF]) {
+    v4i bq[D][NF], aq[D][MT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++)
 #pragma unroll
-        for (int j = 0; j < I8_NBW; j++) {
-            acc0[mi][j] = (v4i){0, 0, 0, 0};
-            acc1[mi][j] = (v4i){0, 0, 0, 0};
-        }
-
-    auto step = [&](int kb, const v4i *b0, const v4i *b1) {
-        v4i a_[MT];
+        for (int f = 0; f < NF; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
+    /* The scheduling barriers keep the loads in slot order, which is what
+     * lets the inserted waits stay partial (vmcnt counts in issue order). */
+    auto load = [&](int slot, int kb) {
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++) {
-            if (mi < nmt) {
-                a_[mi] = *(const v4i *)(ap[mi] + kb * 64);
-                if (!av[mi]) a_[mi] = (v4i){0, 0, 0, 0};
-            }
-        }
+        for (int f = 0; f < NF; f++) bq[slot][f] = ldg16(bp[f] + (size_t)kb * 1024);
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++) {
-            if (mi < nmt) {
-#pragma unroll
-                for (int j = 0; j < I8_NBW; j++) {
-                    acc0[mi][j] = mfma_i8(a_[mi], b0[j], acc0[mi][j]);
-                    if (GU) acc1[mi][j] = mfma_i8(a_[mi], b1[j], acc1[mi][j]);
-                }
-            }
-        }
+        for (int mi = 0; mi < MT; mi++) aq[slot][mi] = *(const v4i *)(ap[mi] + kb * 64);
+        __builtin_amdgcn_sched_barrier(0);
     };
-    int kb = 0;
-    for (; kb + UNR <= KB; kb += UNR) {
-        v4i b0[UNR][I8_NBW], b1[UNR][I8_NBW];
+    auto consume = [&](int slot) {
 #pragma unroll
-        for (int u = 0; u < UNR; u++)
+        for (int mi = 0; mi < MT; mi++)
 #pragma unroll
-            for (int j = 0; j < I8_NBW; j++) {
-                b0[u][j] = ldg16(bp[j] + (kb + u) * 1024);
-                if (GU) b1[u][j] = ldg16(bp[j] + (KB + kb + u) * 1024);
-            }
+            for (int f = 0; f < NF; f++) acc[mi][f] = mfma_i8(aq[slot][mi], bq[slot][f], acc[mi][f]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    /* unconditional (clamped) so that the loop is entered with a known
+     * number of loads in flight and the waits inside it stay partial */
 #pragma unroll
-        for (int u = 0; u < UNR; u++) step(kb + u, b0[u], b1[u]);
-    }
-    for (; kb < KB; kb++) {
-        v4i b0[I8_NBW], b1[I8_NBW];
+    for (int d = 0; d < D; d++) load(d, min(d, KB - 1));
+    int kb0 = 0;
+    /* steady state: every slot is refilled D steps ahead, unconditionally */
+    for (; kb0 + 2 * D <= KB; kb0 += D) {
 #pragma unroll
-        for (int j = 0; j < I8_NBW; j++) {
-            b0[j] = ldg16(bp[j] + kb * 1024);
-            if (GU) b1[j] = ldg16(bp[j] + (KB + kb) * 1024);
+        for (int d = 0; d < D; d++) {
+            consume(d);
+            load(d, kb0 + d + D);
         }
-        step(kb, b0, b1);
     }
+    /* last D .. 2D-1 steps */
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+        if (kb0 + d < KB) consume(d);
+        if (kb0 + d + D < KB) load(d, kb0 + d + D);
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (kb0 + D + d < KB) consume(d);
+}
+
+/* Row ids of a 16-row tile for the epilogue: lane l's results are rows
+ * 4*(l/16) + i; the A-side row id of tile row r sits in lane r. */
+__device__ __forceinline__ int tile_row_id(int a_side_id, int i) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    return __shfl(a_side_id, 4 * (lane >> 4) + i, MM_WAVE);
+}
+
+/* Gate/up + SwiGLU for one unit: rows m0 .. min(M, m0 + 16*MT) - 1 of an
+ * expert (or of the shared expert), column blocks nb0 .. nb0 + NBW - 1.
+ * rid_of(m): route id of row m (the row of h written); tok_of(rid): row of qx. */
+template <int NBW, int MT, int D, class RidOf, class TokOf>
+__device__ __forceinline__ void gu_unit(const mm_i8_gemm_args &a, const int8_t *bbase, int KB,
+                                        int nb0, int m0, int M, const float *sg, const float *su,
+                                        float *hout, int ncols, int32_t *dbg, RidOf rid_of,
+                                        TokOf tok_of) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int8_t *bp[2 * NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; j++) {
+        bp[2 * j] = bbase + (size_t)(nb0 + j) * 2 * KB * 1024 + lane * 16;
+        bp[2 * j + 1] = bp[2 * j] + (size_t)KB * 1024;
+    }
+    int rid_a[MT];
+    float sx_a[MT];
+    const int8_t *ap[MT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
-        if (mi < nmt) {
+        const int m = min(m0 + mi * 16 + (lane & 15), M - 1);
+        rid_a[mi] = rid_of(m);
+        const int t = tok_of(rid_a[mi]);
+        sx_a[mi] = a.sa[t];
+        ap[mi] = a.a + (size_t)t * a.H + 16 * (lane >> 4);
+    }
+    float cg[NBW], cu[NBW];
 #pragma unroll
-            for (int j = 0; j < I8_NBW; j++) {
-                if (nb0 + j < nbl) {
-                    const int col = (nb0 + j) * 16 + (lane & 15);
+    for (int j = 0; j < NBW; j++) {
+        const int col = (nb0 + j) * 16 + (lane & 15);
+        cg[j] = sg[col];
+        cu[j] = su[col];
+    }
+    v4i acc[MT][2 * NBW];
+    stream_k<2 * NBW, MT, D>(bp, ap, KB, acc);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
-                        if (m < M) epi(m, col, acc0[mi][j][i], acc1[mi][j][i]);
-                    }
+    for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
+            const int rid = tile_row_id(rid_a[mi], i);
+            const float sx = __shfl(sx_a[mi], 4 * (lane >> 4) + i, MM_WAVE);
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < NBW; j++) {
+                const int col = (nb0 + j) * 16 + (lane & 15);
+                const int32_t ag = acc[mi][2 * j][i], au = acc[mi][2 * j + 1][i];
+                const float g = ((float)ag * sx) * cg[j];
+                const float u = ((float)au * sx) * cu[j];
+                hout[(size_t)rid * ncols + col] = silu_mul(g, u);
+                if (dbg) {
+                    dbg[((size_t)rid * 2) * ncols + col] = ag;
+                    dbg[((size_t)rid * 2 + 1) * ncols + col] = au;
                 }
             }
         }
-    }
 }
 
-/* Decode-shaped grouped GEMMs: one block per (expert, 128-column slab), every
- * row of the expert against the slab, weights streamed once.  SMALL = true
- * serves the routed experts with at most 16 rows (one 16-row tile, deep K
- * unroll, low register use); SMALL = false serves the rest and the shared
- * expert (four 16-row tiles per pass).  Both are launched; each block exits
- * when its expert belongs to the other variant. */
-template <bool SMALL>
-__device__ __forceinline__ void i8_gu_decode(const mm_i8_gemm_args &a) {
-    constexpr int MT = SMALL ? 1 : I8_MT, UNR = SMALL ? 4 : 2;
+/* Down projection for one unit; y[rid] = dequantised A row rid times W_d. */
+template <int NBW, int MT, int D, class RidOf>
+__device__ __forceinline__ void down_unit(const int8_t *abase, const float *sa, int Kd,
+                                          const int8_t *bbase, int nb0, int m0, int M,
+                                          const float *sd, float *yout, int ncols, int32_t *dbg,
+                                          RidOf rid_of) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int KB = Kd / 64;
+    const int8_t *bp[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; j++) bp[j] = bbase + (size_t)(nb0 + j) * KB * 1024 + lane * 16;
+    int rid_a[MT];
+    float sa_a[MT];
+    const int8_t *ap[MT];
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++) {
+        const int m = min(m0 + mi * 16 + (lane & 15), M - 1);
+        rid_a[mi] = rid_of(m);
+        sa_a[mi] = sa[rid_a[mi]];
+        ap[mi] = abase + (size_t)rid_a[mi] * Kd + 16 * (lane >> 4);
+    }
+    float cd[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; j++) cd[j] = sd[(nb0 + j) * 16 + (lane & 15)];
+    v4i acc[MT][NBW];
+    stream_k<NBW, MT, D>(bp, ap, KB, acc);
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
+            const int rid = tile_row_id(rid_a[mi], i);
+            const float s = __shfl(sa_a[mi], 4 * (lane >> 4) + i, MM_WAVE);
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < NBW; j++) {
+                const int col = (nb0 + j) * 16 + (lane & 15);
+                const int32_t ac = acc[mi][j][i];
+                yout[(size_t)rid * ncols + col] = ((float)ac * s) * cd[j];
+                if (dbg) dbg[(size_t)rid * ncols + col] = ac;
+            }
+        }
+}
+
+#define GU_NBW MM_I8S_NBW_GU
+#define DN_NBW MM_I8S_NBW_DOWN
+#define S_WAVES MM_I8S_WAVES
+
+/* Decode-shaped gate/up.  Block = S_WAVES waves.  Blocks [0, S/16/GU_NBW)
+ * serve the shared expert: one column unit per block, wave w taking the
+ * 16-row tiles w, w + S_WAVES, ... of the T rows, so the block's waves
+ * stream the same weight fragments at the same time and all but the first
+ * read of each is a cache hit.  The remaining blocks serve the routed
+ * experts: S_WAVES consecutive column units of one expert per block, every
+ * wave all of the expert's rows (16 at a time).  Shared blocks come first so
+ * their longer work starts early; a routed block of an expert with no rows
+ * exits at once. */
+extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int KB = a.H / 64;
-    const int routed_blocks = a.E * a.wg_per_expert;
+    const int n_sh = a.S / (16 * GU_NBW);
     const int b = blockIdx.x;
-    if (b < routed_blocks) {
-        const int e = b / a.wg_per_expert, wgi = b % a.wg_per_expert;
-        const int M = min(a.cnt[e], a.T);
+    /* one call site for both kinds of block (a single copy of the unit) */
+    const int8_t *bbase;
+    const float *sg, *su;
+    const int32_t *rows;
+    float *hout;
+    int32_t *dbg;
+    int nb0, M, m0, mstep, ncols, kdiv;
+    if (b < n_sh) {
+        bbase = a.w.sgu;
+        sg = a.w.ss_g;
+        su = a.w.ss_u;
+        rows = nullptr;
+        hout = a.hs;
+        dbg = nullptr;
+        nb0 = b * GU_NBW;
+        M = a.T;
+        m0 = wave * 16;
+        mstep = 16 * S_WAVES;
+        ncols = a.S;
+        kdiv = 1;
+    } else {
         const int nbl = a.I / 16;
-        const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
-        if (M == 0 || nb0 >= nbl || (SMALL != (M <= 16))) return;
-        const int32_t *rows = a.rows + (size_t)e * a.T;
-        const int8_t *bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
-        const float *sg = a.w.s_g + (size_t)e * a.I, *su = a.w.s_u + (size_t)e * a.I;
-        for (int m0 = 0; m0 < M; m0 += MT * 16) {
-            gemm_pass<true, MT, UNR>(
-                bbase, nb0, nbl, KB, m0, M,
-                [&](int m) { return a.a + (size_t)(rows[m] / a.K) * a.H; },
-                [&](int m, int col, int32_t ag, int32_t au) {
-                    const int rid = rows[m];
-                    const float sx = a.sa[rid / a.K];
-                    const float g = ((float)ag * sx) * sg[col];
-                    const float u = ((float)au * sx) * su[col];
-                    a.h[(size_t)rid * a.I + col] = silu_mul(g, u);
-                    if (a.dbg_acc) {
-                        a.dbg_acc[((size_t)rid * 2) * a.I + col] = ag;
-                        a.dbg_acc[((size_t)rid * 2 + 1) * a.I + col] = au;
-                    }
-                });
-        }
-    } else if (!SMALL) {
-        const int sb = b - routed_blocks;
-        const int nbl = a.S / 16;
-        const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
-        if (nb0 >= nbl) return;
-        for (int m0 = 0; m0 < a.T; m0 += MT * 16) {
-            gemm_pass<true, MT, UNR>(
-                a.w.sgu, nb0, nbl, KB, m0, a.T,
-                [&](int m) { return a.a + (size_t)m * a.H; },
-                [&](int m, int col, int32_t ag, int32_t au) {
-                    const float sx = a.sa[m];
-                    const float g = ((float)ag * sx) * a.w.ss_g[col];
-                    const float u = ((float)au * sx) * a.w.ss_u[col];
-                    a.hs[(size_t)m * a.S + col] = silu_mul(g, u);
-                });
-        }
+        const int per_e = (nbl + S_WAVES * GU_NBW - 1) / (S_WAVES * GU_NBW);
+        const int v = b - n_sh, e = v / per_e;
+        nb0 = ((v % per_e) * S_WAVES + wave) * GU_NBW;
+        M = min(a.cnt[e], a.T);
+        if (M == 0 || nb0 >= nbl) return;
+        bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
+        sg = a.w.s_g + (size_t)e * a.I;
+        su = a.w.s_u + (size_t)e * a.I;
+        rows = a.rows + (size_t)e * a.T;
+        hout = a.h;
+        dbg = a.dbg_acc;
+        m0 = 0;
+        mstep = 16;
+        ncols = a.I;
+        kdiv = a.K;
     }
+    for (; m0 < M; m0 += mstep)
+        gu_unit<GU_NBW, 1, 4>(a, bbase, KB, nb0, m0, M, sg, su, hout, ncols, dbg,
+                              [&](int m) { return rows ? rows[m] : m; },
+                              [&](int r) { return r / kdiv; });
 }
 
-template <bool SMALL>
-__device__ __forceinline__ void i8_down_decode(const mm_i8_gemm_args &a) {
-    constexpr int MT = SMALL ? 1 : I8_MT, UNR = SMALL ? 4 : 2;
+/* Decode-shaped down projection, same block layout: H/16/DN_NBW shared
+ * blocks (when there is a shared expert), then the routed experts'. */
+extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_down(mm_i8_gemm_args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
-    const int routed_blocks = a.E * a.wg_per_expert;
     const int nbl = a.H / 16;
+    const int n_sh = a.S ? nbl / DN_NBW : 0;
     const int b = blockIdx.x;
-    if (b < routed_blocks) {
-        const int e = b / a.wg_per_expert, wgi = b % a.wg_per_expert;
-        const int M = min(a.cnt[e], a.T);
-        const int nb0 = (wgi * I8_WAVES + wave) * I8_NBW;
-        if (M == 0 || nb0 >= nbl || (SMALL != (M <= 16))) return;
-        const int KB = a.I / 64;
-        const int32_t *rows = a.rows + (size_t)e * a.T;
-        const int8_t *bbase = a.w.d + (size_t)e * nbl * KB * 1024;
-        const float *sd = a.w.s_d + (size_t)e * a.H;
-        for (int m0 = 0; m0 < M; m0 += MT * 16) {
-            gemm_pass<false, MT, UNR>(
-                bbase, nb0, nbl, KB, m0, M,
-                [&](int m) { return a.a + (size_t)rows[m] * a.I; },
-                [&](int m, int col, int32_t acc, int32_t) {
-                    const int rid = rows[m];
-                    a.y[(size_t)rid * a.H + col] = ((float)acc * a.sa[rid]) * sd[col];
-                    if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.H + col] = acc;
-                });
-        }
-    } else if (!SMALL) {
-        const int sb = b - routed_blocks;
-        const int nb0 = (sb * I8_WAVES + wave) * I8_NBW;
-        if (nb0 >= nbl) return;
-        const int KB = a.S / 64;
-        for (int m0 = 0; m0 < a.T; m0 += MT * 16) {
-            gemm_pass<false, MT, UNR>(
-                a.w.sdn, nb0, nbl, KB, m0, a.T,
-                [&](int m) { return a.a_sh + (size_t)m * a.S; },
-                [&](int m, int col, int32_t acc, int32_t) {
-                    a.ys[(size_t)m * a.H + col] = ((float)acc * a.sa_sh[m]) * a.w.ss_d[col];
-                });
-        }
+    const int8_t *abase, *bbase;
+    const float *sa, *sd;
+    const int32_t *rows;
+    float *yout;
+    int32_t *dbg;
+    int nb0, M, m0, mstep, Kd;
+    if (b < n_sh) {
+        abase = a.a_sh;
+        sa = a.sa_sh;
+        Kd = a.S;
+        bbase = a.w.sdn;
+        sd = a.w.ss_d;
+        rows = nullptr;
+        yout = a.ys;
+        dbg = nullptr;
+        nb0 = b * DN_NBW;
+        M = a.T;
+        m0 = wave * 16;
+        mstep = 16 * S_WAVES;
+    } else {
+        const int per_e = (nbl + S_WAVES * DN_NBW - 1) / (S_WAVES * DN_NBW);
+        const int v = b - n_sh, e = v / per_e;
+        nb0 = ((v % per_e) * S_WAVES + wave) * DN_NBW;
+        M = min(a.cnt[e], a.T);
+        if (M == 0 || nb0 >= nbl) return;
+        abase = a.a;
+        sa = a.sa;
+        Kd = a.I;
+        bbase = a.w.d + (size_t)e * nbl * (a.I / 64) * 1024;
+        sd = a.w.s_d + (size_t)e * a.H;
+        rows = a.rows + (size_t)e * a.T;
+        yout = a.y;
+        dbg = a.dbg_acc;
+        m0 = 0;
+        mstep = 16;
     }
-}
-
-extern "C" __global__ __launch_bounds__(256) void mm_i8_gu_s(mm_i8_gemm_args a) {
-    i8_gu_decode<true>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mm_i8_gu(mm_i8_gemm_args a) {
-    i8_gu_decode<false>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mm_i8_down_s(mm_i8_gemm_args a) {
-    i8_down_decode<true>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mm_i8_down(mm_i8_gemm_args a) {
-    i8_down_decode<false>(a);
+    for (; m0 < M; m0 += mstep)
+        down_unit<DN_NBW, 1, 4>(abase, sa, Kd, bbase, nb0, m0, M, sd, yout, a.H, dbg,
+                                [&](int m) { return rows ? rows[m] : m; });
 }
 
 /* ---- hidden-row quantisation and combine ------------------------------------- */
