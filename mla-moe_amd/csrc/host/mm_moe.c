@@ -319,6 +319,14 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
 
 /* ---- int8 forward ----------------------------------------------------------- */
 
+/* Blocks of a decode GEMM that serve the shared expert's `groups` column
+ * groups: MM_I8S_RT row-tile waves each, dealt in sets of MM_I8S_XCD. */
+static size_t sh_blocks(size_t groups) {
+    return (groups + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT;
+}
+
+static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
                         const mm_moe_i8_debug *dbg) {
@@ -333,7 +341,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const size_t o_sh = plan_take(&p, R * 4), o_qhs = plan_take(&p, (size_t)T * S);
     const size_t o_shs = plan_take(&p, (size_t)T * 4), o_y = plan_take(&p, R * H * 4);
     const size_t o_ys = plan_take(&p, (size_t)T * H * 4), o_i = plan_take(&p, R * 4);
-    const size_t o_w = plan_take(&p, R * 4);
+    const size_t o_w = plan_take(&p, R * 4), o_lg = plan_take(&p, logits ? 0 : (size_t)T * E * 4);
     char *ws;
     int st = mm_workspace(c, p.off, (void **)&ws);
     if (st) return st;
@@ -345,6 +353,22 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     float *sh = (float *)(ws + o_sh), *shs = (float *)(ws + o_shs);
     float *y = (float *)(ws + o_y), *ys = (float *)(ws + o_ys);
 
+    if (!logits) {
+        /* router logits in the reference's order, then routing from them */
+        mm_router_args la;
+        memset(&la, 0, sizeof(la));
+        la.x = xn;
+        la.wgT = L->wgT;
+        la.logits_out = (float *)(ws + o_lg);
+        la.T = T;
+        la.H = (int)H;
+        la.E = (int)E;
+        la.K = (int)K;
+        if ((st = mm_launch(c, K_ROUTER, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK,
+                            1, 1, 256, 0, &la)))
+            return st;
+        logits = la.logits_out;
+    }
     mm_i8_route_args ra;
     memset(&ra, 0, sizeof(ra));
     ra.r.x = xn;
@@ -366,11 +390,11 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ra.x = xn;
     ra.qx = qx;
     ra.sx = sx;
-    if ((st = mm_launch(c, K_I8_ROUTE, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK,
-                        1, 1, 256, 0, &ra)))
+    const int tiled = T >= c->i8_tiled_min_t;
+    if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
+                        64 * MM_I8_RT_WAVES, 0, &ra)))
         return st;
 
-    const int tiled = T >= c->i8_tiled_min_t;
     mm_i8_gemm_args ga;
     memset(&ga, 0, sizeof(ga));
     ga.w = L->i8;
@@ -407,10 +431,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                 return st;
         }
     } else {
-        /* shared-expert blocks, then every routed expert's blocks */
-        const size_t cu = 16 * MM_I8S_NBW_GU, per_e = (I / cu + MM_I8S_WAVES - 1) / MM_I8S_WAVES;
-        const unsigned nb = (unsigned)(S / cu + E * per_e);
-        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_WAVES, 0, &ga))) return st;
+        /* shared-expert blocks (row-tile waves), then every routed unit */
+        const size_t per_blk = (size_t)MM_I8S_W * MM_I8S_SEG;
+        const unsigned nb = (unsigned)((S ? sh_blocks(ceil_div(S / 16, per_blk)) : 0) +
+                                       E * ceil_div(I / 16, per_blk));
+        /* dynamic LDS: the 16-row A tile, 16 * K bytes */
+        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H, &ga))) return st;
     }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
@@ -439,9 +465,10 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.y = y;
         ga.ys = ys;
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
-        const size_t cd = 16 * MM_I8S_NBW_DOWN, per_e = (H / cd + MM_I8S_WAVES - 1) / MM_I8S_WAVES;
-        const unsigned nb = (unsigned)((S ? H / cd : 0) + E * per_e);
-        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_WAVES, 0, &ga))) return st;
+        const size_t gpe = ceil_div(H / 16, (size_t)MM_I8S_W * MM_I8S_SEG);
+        const unsigned nb = (unsigned)((S ? sh_blocks(gpe) : 0) + E * gpe);
+        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W, 16 * (S > I ? S : I), &ga)))
+            return st;
     }
 
     mm_i8_combine_args ca = {y, ys, wts, out, c->moe_cnt, T, (int)H, (int)K, (int)E, acc, S > 0};

@@ -82,17 +82,21 @@ typedef struct {
 /* Per-layer int8 weights in MFMA fragment order.  A "fragment" is the
  * 16-row x 64-column int8 block one v_mfma_i32_16x16x64_i8 consumes as its
  * B operand: 1 KB, lane l holding row (l % 16), columns 16*(l/16) .. +15.
- *   gu   [E][I/16][2][H/64] fragments: gate rows then up rows of each
- *        16-row block (the SwiGLU pair of an output column block)
+ *   gu   [E][I/16][H/64][2] fragments: for each 16-row block and K step, the
+ *        gate fragment then the up fragment (the SwiGLU pair), so that one
+ *        column block's whole K range is one contiguous 2*H*16-byte stream
  *   d    [E][H/16][I/64] fragments of the down projection
- *   sgu  [S/16][2][H/64], sd_ [H/16][S/64] for the shared expert */
+ *   sgu  [S/16][H/64][2], sdn [H/16][S/64] for the shared expert */
 typedef struct {
     const int8_t *gu, *d, *sgu, *sdn;
     const float *s_g, *s_u, *s_d;       /* [E, I], [E, I], [E, H] */
     const float *ss_g, *ss_u, *ss_d;    /* [S], [S], [H] */
 } mm_i8_weights;
 
-/* Routing + per-token activation quantisation. */
+/* Routing + per-token activation quantisation (logits given). */
+#define MM_I8_RT_WAVES 4
+#define MM_I8_RT_TOKENS 4        /* tokens per block: one per wave */
+#define MM_EMAX 256
 typedef struct {
     mm_router_args r;
     int32_t *cnt;            /* [E] rows per expert (zero on entry) */
@@ -150,14 +154,25 @@ typedef struct {
     int N, K;
 } mm_pack_i8_args;
 
-/* Launch geometry shared by the int8 GEMM kernels and the host: 4 waves per
- * block, 2 sixteen-column blocks per wave. */
-/* Decode-shaped GEMMs: blocks of MM_I8S_WAVES waves, each wave one unit of
- * MM_I8S_NBW_* 16-column blocks.  H / 16 and (n_shared * I) / 16 must be
- * multiples of the NBW values. */
-#define MM_I8S_WAVES 4
-#define MM_I8S_NBW_GU 1
-#define MM_I8S_NBW_DOWN 2
+/* Decode-shaped GEMMs: a block of MM_I8S_W waves serves one 16-row tile of
+ * one expert (A tile staged once in LDS); each wave streams MM_I8S_SEG
+ * consecutive 16-column blocks of the expert's weights (one contiguous run of
+ * fragments), the waves of a block taking column units G apart, G being the
+ * number of blocks per expert.  The shared expert's row tiles go to
+ * MM_I8S_RT blocks 8 block ids apart (one XCD), so that their identical
+ * weight reads meet in that XCD's L2. */
+#ifndef MM_I8S_W
+#define MM_I8S_W 8                 /* waves per block */
+#endif
+#ifndef MM_I8S_SEG
+#define MM_I8S_SEG 1               /* column blocks per wave (<= 4) */
+#endif
+#ifndef MM_I8S_DEPTH_GU
+#define MM_I8S_DEPTH_GU 4          /* K steps of weight fragments in flight per wave */
+#define MM_I8S_DEPTH_DOWN 8
+#endif
+#define MM_I8S_RT 4                /* row-tile blocks per shared-expert column group */
+#define MM_I8S_XCD 8               /* blocks are dealt to XCDs round robin */
 
 /* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
  * the routed experts' row lists (or all T rows for the shared expert). */

@@ -43,268 +43,431 @@ __device__ __forceinline__ v4i ldg16(const int8_t *p) {
 /* ---- routing + activation quantisation ----------------------------------- */
 
 /* s = max|x| / 127; q = clamp(rint(x / s), -127, 127), IEEE division and
- * round-half-even, identical to the CPU quantiser.  One wave, n % 4 == 0. */
-__device__ __forceinline__ void quant_row_wave(const float *x, int n, int8_t *q, float *s) {
+ * round-half-even, identical to the CPU quantiser.  One wave, n % 4 == 0.
+ * Loads are issued QC float4 per lane at a time (one round trip per 256*QC
+ * floats); rows of at most 256*QC floats stay in registers between the max
+ * and the quantisation. */
+#define QC 8
+__device__ __forceinline__ void quant_row_load(const float *x, int n, int base, f32x4 (&v)[QC]) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
+#pragma unroll
+    for (int c = 0; c < QC; c++) {
+        const int i = base + (c * MM_WAVE + lane) * 4;
+        v[c] = i < n ? *(const f32x4 *)(x + i) : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+/* v: the row's first chunk, already loaded by quant_row_load(x, n, 0, v). */
+__device__ __forceinline__ void quant_row_wave_pre(const float *x, int n, int8_t *q, float *s,
+                                                   f32x4 (&v)[QC]) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    auto load = [&](int base) { quant_row_load(x, n, base, v); };
     float amax = 0.0f;
-    for (int i = lane * 4; i < n; i += MM_WAVE * 4) {
-        f32x4 v = *(const f32x4 *)(x + i);
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    for (int base = 0; base < n; base += QC * MM_WAVE * 4) {
+        if (base) load(base);
+#pragma unroll
+        for (int c = 0; c < QC; c++)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)),
+                                     fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
     }
     amax = wave_max(amax);
     const float sc = amax / 127.0f;
     if (lane == 0) *s = sc;
-    for (int i = lane * 4; i < n; i += MM_WAVE * 4) {
-        f32x4 v = *(const f32x4 *)(x + i);
-        int b[4];
+    for (int base = 0; base < n; base += QC * MM_WAVE * 4) {
+        if (n > QC * MM_WAVE * 4) load(base);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(v[j] / sc), -127.0f), 127.0f);
-            b[j] = (int)r & 0xff;
+        for (int c = 0; c < QC; c++) {
+            const int i = base + (c * MM_WAVE + lane) * 4;
+            if (i >= n) continue;
+            int b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(v[c][j] / sc), -127.0f), 127.0f);
+                b[j] = (int)r & 0xff;
+            }
+            *(uint32_t *)(q + i) = (uint32_t)(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
         }
-        *(uint32_t *)(q + i) = (uint32_t)(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
     }
 }
 
-extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_i8_route(mm_i8_route_args a) {
-    __shared__ float lds[MM_ROUTER_LDS_FLOATS];
+__device__ __forceinline__ void quant_row_wave(const float *x, int n, int8_t *q, float *s) {
+    f32x4 v[QC];
+    quant_row_load(x, n, 0, v);
+    quant_row_wave_pre(x, n, q, s, v);
+}
+
+/* ---- routing ------------------------------------------------------------------- */
+
+#define RT_TPW 1                             /* tokens per wave */
+#define RT_TOKENS (RT_TPW * MM_I8_RT_WAVES)  /* tokens per block */
+static_assert(RT_TOKENS == MM_I8_RT_TOKENS, "route block size");
+
+/* Scores, top-k and weights of one token from its logits (lane holds experts
+ * lane + 64 j), following run.c:124-149 exactly:
+ *   softmax: max, e^(x - max) (-inf -> 0), sum in ascending expert order,
+ *   divide; or sigmoid 1 / (1 + e^-x);
+ *   top-k: the expert picked in pass r of the CPU's strict '>' scan is the
+ *   one with exactly r others ahead of it in the order (score + bias
+ *   descending, index ascending), so every lane computes its expert's rank
+ *   against all scores (broadcast LDS reads) and ranks < K are the slots;
+ *   weight = raw score, optional normalisation seeded with 1e-20 summed in
+ *   slot order, times routed_scaling.
+ * On return lanes r < K hold slot r's expert (*e_out) and weight (*w_out).
+ * `ws` is this wave's LDS scratch of 2 * MM_EMAX + 2 * MM_KMAX words. */
+template <int EJ>
+__device__ __forceinline__ void route_token(const mm_router_args &a, int tok, const float (&lg)[EJ],
+                                            float *ws, int *e_out, float *w_out) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
-    router_block(a.r, blockIdx.x, lds, [&](int tok, const int *idx, const float *) {
-        int e = 0;
+    const int E = a.E, K = a.K;
+    float *sp = ws, *ss = ws + MM_EMAX;
+    int *slot_e = (int *)(ws + 2 * MM_EMAX);
+    float *slot_w = ws + 2 * MM_EMAX + MM_KMAX;
+    float p[EJ];
+    if (a.sigmoid) {
 #pragma unroll
-        for (int r = 0; r < MM_KMAX; r++)
-            if (lane == r) e = idx[r];
-        if (lane < a.r.K) {
-            int pos = atomicAdd(&a.cnt[e], 1);
-            if (pos < a.r.T) a.rows[(size_t)e * a.r.T + pos] = tok * a.r.K + lane;
+        for (int j = 0; j < EJ; j++) p[j] = 1.0f / (1.0f + exp_cr(-lg[j]));
+    } else {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < EJ; j++)
+            if (lane + MM_WAVE * j < E) mx = fmaxf(mx, lg[j]);
+        mx = wave_max(mx);
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            const int e = lane + MM_WAVE * j;
+            p[j] = (e < E && lg[j] != -INFINITY) ? exp_cr(lg[j] - mx) : 0.0f;
+            if (e < E) sp[e] = p[j];
         }
-        quant_row_wave(a.x + (size_t)tok * a.r.H, a.r.H, a.qx + (size_t)tok * a.r.H,
-                       a.sx + tok);
-    });
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        float sum = 0.0f;   /* ascending expert order, as the CPU sums */
+        for (int e = 0; e < E; e += 4) {
+            const f32x4 v = *(const f32x4 *)(sp + e);
+            sum += v.x;
+            if (e + 1 < E) sum += v.y;
+            if (e + 2 < E) sum += v.z;
+            if (e + 3 < E) sum += v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < EJ; j++) p[j] = p[j] / sum;
+    }
+    if (a.probs) {
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            const int e = lane + MM_WAVE * j;
+            if (e < E) a.probs[(size_t)tok * E + e] = p[j];
+        }
+    }
+    float sel[EJ];
+    int rank[EJ];
+#pragma unroll
+    for (int j = 0; j < EJ; j++) {
+        const int e = lane + MM_WAVE * j;
+        sel[j] = p[j] + (a.bias && e < E ? a.bias[e] : 0.0f);
+        rank[j] = 0;
+        if (e < E) ss[e] = sel[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    for (int e0 = 0; e0 < E; e0 += 4) {
+        const f32x4 v = *(const f32x4 *)(ss + e0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int eo = e0 + k;
+#pragma unroll
+            for (int j = 0; j < EJ; j++) {
+                const int e = lane + MM_WAVE * j;
+                rank[j] += (eo < E && (v[k] > sel[j] || (v[k] == sel[j] && eo < e))) ? 1 : 0;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < EJ; j++) {
+        const int e = lane + MM_WAVE * j;
+        if (e < E && rank[j] < K) {
+            slot_e[rank[j]] = e;
+            slot_w[rank[j]] = p[j];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float norm = 1.0f;
+    if (a.norm_topk) {
+        float sw = 1e-20f;
+        for (int r = 0; r < K; r++) sw += slot_w[r];
+        norm = sw;
+    }
+    const int r = min(lane, K - 1);
+    float w = slot_w[r];
+    if (a.norm_topk) w /= norm;
+    *w_out = w * a.scale;
+    *e_out = slot_e[r];
+}
+
+/* Routing, per-expert row lists and per-token quantisation of x.  Block =
+ * MM_I8_RT_WAVES waves x RT_TPW tokens.  Row-list slots are claimed per
+ * block: LDS counters give each route its place among the block's routes to
+ * the same expert, then one global atomic per (block, expert) reserves the
+ * block's range of the expert's list.  Logits come from logits_in. */
+template <int EJ>
+__device__ __forceinline__ void i8_route(const mm_i8_route_args &a) {
+    __shared__ int lcnt[MM_EMAX];
+    __shared__ float wsc[MM_I8_RT_WAVES][2 * MM_EMAX + 2 * MM_KMAX];
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const mm_router_args &r = a.r;
+    const int T = r.T, E = r.E, K = r.K;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) lcnt[e] = 0;
+    const int t0 = blockIdx.x * RT_TOKENS + wave * RT_TPW;
+    /* the x rows' first chunks are fetched now, consumed after the routing */
+    f32x4 xv[RT_TPW][QC];
+#pragma unroll
+    for (int t = 0; t < RT_TPW; t++)
+        quant_row_load(a.x + (size_t)min(t0 + t, T - 1) * r.H, r.H, 0, xv[t]);
+    float lg[RT_TPW][EJ];
+#pragma unroll
+    for (int t = 0; t < RT_TPW; t++)
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            const int e = lane + MM_WAVE * j, tt = min(t0 + t, T - 1);
+            lg[t][j] = e < E ? r.logits_in[(size_t)tt * E + e] : -INFINITY;
+        }
+    __syncthreads();
+    int my_e[RT_TPW], my_pos[RT_TPW];
+#pragma unroll
+    for (int t = 0; t < RT_TPW; t++) {
+        my_e[t] = -1;
+        const int tok = t0 + t;
+        if (tok >= T) continue;
+        int e;
+        float w;
+        route_token<EJ>(r, tok, lg[t], wsc[wave], &e, &w);
+        if (lane < K) {
+            r.topk_idx[(size_t)tok * K + lane] = e;
+            r.topk_w[(size_t)tok * K + lane] = w;
+            my_e[t] = e;
+            my_pos[t] = atomicAdd(&lcnt[e], 1);
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        const int n = lcnt[e];
+        lcnt[e] = n ? atomicAdd(&a.cnt[e], n) : 0;   /* now the block's base */
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < RT_TPW; t++) {
+        const int e = my_e[t];
+        if (e >= 0) {
+            const int pos = lcnt[e] + my_pos[t];
+            if (pos < T) a.rows[(size_t)e * T + pos] = (t0 + t) * K + lane;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < RT_TPW; t++) {
+        const int tok = t0 + t;
+        if (tok < T)
+            quant_row_wave_pre(a.x + (size_t)tok * r.H, r.H, a.qx + (size_t)tok * r.H, a.sx + tok,
+                               xv[t]);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MM_I8_RT_WAVES * MM_WAVE) void mm_i8_route(mm_i8_route_args a) {
+    if (a.r.E <= 64)
+        i8_route<1>(a);
+    else if (a.r.E <= 128)
+        i8_route<2>(a);
+    else
+        i8_route<4>(a);
 }
 
 /* ---- streaming grouped GEMM (decode) ------------------------------------------- */
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+/* 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (direct
+ * global -> LDS load, no VGPR staging). */
+__device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
+}
+
+/* LDS byte address of a __shared__ location. */
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
+}
+
+/* ds_read_b128 issued as inline assembly: the compiler's conservative
+ * "wait for every outstanding direct-to-LDS load before any LDS read" would
+ * otherwise drain the whole load ring every K step.  The caller orders the
+ * reads with explicit vmcnt waits and a barrier, and must follow them with
+ * lds_wait_regs() before using the results. */
+__device__ __forceinline__ v4i ds_read16(uint32_t addr) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+
+
+
+/* s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima). */
+#define VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-/* One work unit = one wave = NF weight fragment columns (16 output columns
- * each; for gate/up the gate and the up fragment of one column block) of one
- * expert over the whole K, against MT 16-row tiles of that expert's rows.
+/* Decode-shaped grouped GEMMs.
  *
- * Weights stream once from HBM with non-temporal loads through a D-deep
- * register ring: the loads of K step kb + D are issued as soon as step kb's
- * MFMAs have been issued, so every wave keeps D steps of fragments in flight
- * and never drains its queue inside the K loop.  The A rows (a few KB, read
- * by every unit of the expert) come through the caches.
+ * A block of MM_I8S_W waves serves one 16-row tile of one expert (or of the
+ * shared expert).  The tile's A rows (16 x K int8) are staged once into LDS
+ * in MFMA operand order, [K step][lane][16 B], and every wave reads them
+ * from there.  Each wave streams its own MM_I8S_SEG consecutive 16-column
+ * blocks of the expert's weights -- one contiguous run of fragments
+ * (gate/up: [gate|up] 2 KB per K step, down: 1 KB per K step) -- and the
+ * waves of a block take column units G apart (G = blocks per expert), so
+ * that no two waves of a block stream neighbouring memory.
  *
- * Rows are independent in D = A * B, so lanes whose row is past M read any
- * valid row and their results are discarded by the epilogue.
- *   bp[f]  : lane's 16-byte slice of fragment column f at K step 0
- *   ap[mi] : lane's 16-byte slice of A row tile mi at K step 0
- * On return acc[mi][f] holds D[4*(lane/16) + i][lane % 16] of tile mi,
- * fragment column f. */
-template <int NF, int MT, int D>
-__device__ __forceinline__ void stream_k(const int8_t *const (&bp)[NF], const int8_t *const (&ap)[MT],
-                                         int KB, v4i (&acc)[MT][NF]) {
-    v4i bq[D][NF], aq[D][MT];
+ * Weights stream from HBM with non-temporal loads through a D-deep register
+ * ring: the loads of step s + D go out right after step s's MFMAs, across
+ * column-block boundaries, so each wave keeps D steps in flight from its
+ * first load to its last.  The first D steps' loads are issued before the
+ * A tile is staged (they only depend on the block index).  At the end of
+ * each column block the epilogue runs on that block's accumulators while
+ * the next block's fragments are arriving.
+ *
+ * Rows past M are staged as zeros; their results are never stored. */
+template <bool GU, int D, class Epi>
+__device__ __forceinline__ void stream_lds(const int8_t *bp, int KB, int nseg, uint32_t lds_a,
+                                           bool prologue_issued, v4i (&bq)[D][GU ? 2 : 1], Epi epi) {
+    constexpr int NF = GU ? 2 : 1;
+    constexpr int BSTEP = NF * 1024;
+    const int total = KB * nseg;
+    auto load_b = [&](int slot, int st) {
 #pragma unroll
-    for (int mi = 0; mi < MT; mi++)
-#pragma unroll
-        for (int f = 0; f < NF; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
-    /* The scheduling barriers keep the loads in slot order, which is what
-     * lets the inserted waits stay partial (vmcnt counts in issue order). */
-    auto load = [&](int slot, int kb) {
-#pragma unroll
-        for (int f = 0; f < NF; f++) bq[slot][f] = ldg16(bp[f] + (size_t)kb * 1024);
-#pragma unroll
-        for (int mi = 0; mi < MT; mi++) aq[slot][mi] = *(const v4i *)(ap[mi] + kb * 64);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int f = 0; f < NF; f++)
+            bq[slot][f] = ldg16(bp + (size_t)min(st, total - 1) * BSTEP + f * 1024);
     };
-    auto consume = [&](int slot) {
+    if (!prologue_issued) {
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++)
-#pragma unroll
-            for (int f = 0; f < NF; f++) acc[mi][f] = mfma_i8(aq[slot][mi], bq[slot][f], acc[mi][f]);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    /* unconditional (clamped) so that the loop is entered with a known
-     * number of loads in flight and the waits inside it stay partial */
-#pragma unroll
-    for (int d = 0; d < D; d++) load(d, min(d, KB - 1));
-    int kb0 = 0;
-    /* steady state: every slot is refilled D steps ahead, unconditionally */
-    for (; kb0 + 2 * D <= KB; kb0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; d++) {
-            consume(d);
-            load(d, kb0 + d + D);
-        }
+        for (int d = 0; d < D; d++) load_b(d, d);
     }
-    /* last D .. 2D-1 steps */
+    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    int ck = 0, seg = 0;   /* K step and column block of the next consume */
+    auto step = [&](int slot, int st) {
+        v4i av = ds_read16(lds_a + ck * 1024);
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av));
+        acc0 = mfma_i8(av, bq[slot][0], acc0);
+        if (GU) acc1 = mfma_i8(av, bq[slot][NF - 1], acc1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(slot, st + D);
+        __builtin_amdgcn_sched_barrier(0);
+        if (++ck == KB) {
+            epi(seg, acc0, acc1);
+            acc0 = (v4i){0, 0, 0, 0};
+            acc1 = (v4i){0, 0, 0, 0};
+            ck = 0;
+            ++seg;
+        }
+    };
+    /* full ring turns (unconditional body), then the last partial turn */
+    int s0 = 0;
+    for (; s0 + D <= total; s0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; d++) {
-        if (kb0 + d < KB) consume(d);
-        if (kb0 + d + D < KB) load(d, kb0 + d + D);
+        for (int d = 0; d < D; d++) step(d, s0 + d);
     }
 #pragma unroll
     for (int d = 0; d < D; d++)
-        if (kb0 + D + d < KB) consume(d);
+        if (s0 + d < total) step(d, s0 + d);
 }
 
-/* Row ids of a 16-row tile for the epilogue: lane l's results are rows
- * 4*(l/16) + i; the A-side row id of tile row r sits in lane r. */
-__device__ __forceinline__ int tile_row_id(int a_side_id, int i) {
-    const int lane = threadIdx.x & (MM_WAVE - 1);
-    return __shfl(a_side_id, 4 * (lane >> 4) + i, MM_WAVE);
-}
-
-/* Gate/up + SwiGLU for one unit: rows m0 .. min(M, m0 + 16*MT) - 1 of an
- * expert (or of the shared expert), column blocks nb0 .. nb0 + NBW - 1.
- * rid_of(m): route id of row m (the row of h written); tok_of(rid): row of qx. */
-template <int NBW, int MT, int D, class RidOf, class TokOf>
-__device__ __forceinline__ void gu_unit(const mm_i8_gemm_args &a, const int8_t *bbase, int KB,
-                                        int nb0, int m0, int M, const float *sg, const float *su,
-                                        float *hout, int ncols, int32_t *dbg, RidOf rid_of,
-                                        TokOf tok_of) {
-    const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int8_t *bp[2 * NBW];
+/* Stage the 16-row A tile into LDS ([K step][lane][16 B], 1 KB per step):
+ * thread t copies the 16-byte pieces of tile row (t % 16) it is responsible
+ * for.  arow: that row's K bytes, or nullptr for rows past M (zeros). */
+#define STAGE_BATCH 4
+__device__ __forceinline__ void stage_a(int8_t *lds, const int8_t *arow, int KB, const int8_t *any) {
+    constexpr int NTHR = MM_I8S_W * MM_WAVE;
+    const int tid = threadIdx.x;
+    const int part = (tid & (MM_WAVE - 1)) >> 4;   /* 16-byte column of the 64-byte step */
+    const int n = KB * MM_WAVE;                    /* 16-byte pieces */
+    const int8_t *src = arow ? arow : any;         /* rows past M: any valid row, zeroed */
+    for (int i0 = 0; i0 < n; i0 += STAGE_BATCH * NTHR) {
+        /* all of a batch's loads are issued (unconditionally) before its stores */
+        v4i v[STAGE_BATCH];
 #pragma unroll
-    for (int j = 0; j < NBW; j++) {
-        bp[2 * j] = bbase + (size_t)(nb0 + j) * 2 * KB * 1024 + lane * 16;
-        bp[2 * j + 1] = bp[2 * j] + (size_t)KB * 1024;
-    }
-    int rid_a[MT];
-    float sx_a[MT];
-    const int8_t *ap[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; mi++) {
-        const int m = min(m0 + mi * 16 + (lane & 15), M - 1);
-        rid_a[mi] = rid_of(m);
-        const int t = tok_of(rid_a[mi]);
-        sx_a[mi] = a.sa[t];
-        ap[mi] = a.a + (size_t)t * a.H + 16 * (lane >> 4);
-    }
-    float cg[NBW], cu[NBW];
-#pragma unroll
-    for (int j = 0; j < NBW; j++) {
-        const int col = (nb0 + j) * 16 + (lane & 15);
-        cg[j] = sg[col];
-        cu[j] = su[col];
-    }
-    v4i acc[MT][2 * NBW];
-    stream_k<2 * NBW, MT, D>(bp, ap, KB, acc);
-#pragma unroll
-    for (int mi = 0; mi < MT; mi++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
-            const int rid = tile_row_id(rid_a[mi], i);
-            const float sx = __shfl(sx_a[mi], 4 * (lane >> 4) + i, MM_WAVE);
-            if (m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < NBW; j++) {
-                const int col = (nb0 + j) * 16 + (lane & 15);
-                const int32_t ag = acc[mi][2 * j][i], au = acc[mi][2 * j + 1][i];
-                const float g = ((float)ag * sx) * cg[j];
-                const float u = ((float)au * sx) * cu[j];
-                hout[(size_t)rid * ncols + col] = silu_mul(g, u);
-                if (dbg) {
-                    dbg[((size_t)rid * 2) * ncols + col] = ag;
-                    dbg[((size_t)rid * 2 + 1) * ncols + col] = au;
-                }
-            }
+        for (int j = 0; j < STAGE_BATCH; j++) {
+            const int i = min(i0 + j * NTHR + tid, n - 1);
+            v[j] = *(const v4i *)(src + (i / MM_WAVE) * 64 + part * 16);
         }
-}
-
-/* Down projection for one unit; y[rid] = dequantised A row rid times W_d. */
-template <int NBW, int MT, int D, class RidOf>
-__device__ __forceinline__ void down_unit(const int8_t *abase, const float *sa, int Kd,
-                                          const int8_t *bbase, int nb0, int m0, int M,
-                                          const float *sd, float *yout, int ncols, int32_t *dbg,
-                                          RidOf rid_of) {
-    const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int KB = Kd / 64;
-    const int8_t *bp[NBW];
 #pragma unroll
-    for (int j = 0; j < NBW; j++) bp[j] = bbase + (size_t)(nb0 + j) * KB * 1024 + lane * 16;
-    int rid_a[MT];
-    float sa_a[MT];
-    const int8_t *ap[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; mi++) {
-        const int m = min(m0 + mi * 16 + (lane & 15), M - 1);
-        rid_a[mi] = rid_of(m);
-        sa_a[mi] = sa[rid_a[mi]];
-        ap[mi] = abase + (size_t)rid_a[mi] * Kd + 16 * (lane >> 4);
-    }
-    float cd[NBW];
-#pragma unroll
-    for (int j = 0; j < NBW; j++) cd[j] = sd[(nb0 + j) * 16 + (lane & 15)];
-    v4i acc[MT][NBW];
-    stream_k<NBW, MT, D>(bp, ap, KB, acc);
-#pragma unroll
-    for (int mi = 0; mi < MT; mi++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + mi * 16 + 4 * (lane >> 4) + i;
-            const int rid = tile_row_id(rid_a[mi], i);
-            const float s = __shfl(sa_a[mi], 4 * (lane >> 4) + i, MM_WAVE);
-            if (m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < NBW; j++) {
-                const int col = (nb0 + j) * 16 + (lane & 15);
-                const int32_t ac = acc[mi][j][i];
-                yout[(size_t)rid * ncols + col] = ((float)ac * s) * cd[j];
-                if (dbg) dbg[(size_t)rid * ncols + col] = ac;
-            }
+        for (int j = 0; j < STAGE_BATCH; j++) {
+            const int i = i0 + j * NTHR + tid;
+            if (i < n) *(v4i *)(lds + (size_t)i * 16) = arow ? v[j] : (v4i){0, 0, 0, 0};
         }
+    }
 }
 
-#define GU_NBW MM_I8S_NBW_GU
-#define DN_NBW MM_I8S_NBW_DOWN
-#define S_WAVES MM_I8S_WAVES
+__device__ __forceinline__ int tile_row_i(int a_side, int i) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    return __shfl(a_side, 4 * (lane >> 4) + i, MM_WAVE);
+}
+__device__ __forceinline__ float tile_row_f(float a_side, int i) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    return __shfl(a_side, 4 * (lane >> 4) + i, MM_WAVE);
+}
 
-/* Decode-shaped gate/up.  Block = S_WAVES waves.  Blocks [0, S/16/GU_NBW)
- * serve the shared expert: one column unit per block, wave w taking the
- * 16-row tiles w, w + S_WAVES, ... of the T rows, so the block's waves
- * stream the same weight fragments at the same time and all but the first
- * read of each is a cache hit.  The remaining blocks serve the routed
- * experts: S_WAVES consecutive column units of one expert per block, every
- * wave all of the expert's rows (16 at a time).  Shared blocks come first so
- * their longer work starts early; a routed block of an expert with no rows
- * exits at once. */
-extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
+/* Shared-expert block b of a decode GEMM: column group and row tile, with
+ * the MM_I8S_RT blocks of a column group 8 block ids apart (one XCD, so
+ * their identical weight reads meet in that XCD's L2). */
+__device__ __forceinline__ void shared_block(int b, int *group, int *rt) {
+    constexpr int G = MM_I8S_XCD * MM_I8S_RT;
+    *group = (b / G) * MM_I8S_XCD + b % MM_I8S_XCD;
+    *rt = (b / MM_I8S_XCD) % MM_I8S_RT;
+}
+
+/* Column blocks per wave and blocks per expert of a decode GEMM over nbl
+ * 16-column blocks. */
+__device__ __forceinline__ int units_per_wave_group(int nbl) {
+    return (nbl + MM_I8S_W * MM_I8S_SEG - 1) / (MM_I8S_W * MM_I8S_SEG);
+}
+
+/* Decode-shaped gate/up + SwiGLU.  Blocks [0, n_sh): the shared expert
+ * (column group g, row tile rt + MM_I8S_RT * k); the rest: routed expert e,
+ * column group g, all of e's rows 16 at a time.  Shared blocks come first so
+ * that their work starts early; a routed block of an expert with no rows
+ * exits at once.  Dynamic LDS: 16 * H bytes (the A tile). */
+extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds_a[];
+    const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int KB = a.H / 64;
-    const int n_sh = a.S / (16 * GU_NBW);
+    const int gs = units_per_wave_group(a.S / 16);
+    const int n_sh = a.S ? (gs + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT : 0;
     const int b = blockIdx.x;
-    /* one call site for both kinds of block (a single copy of the unit) */
     const int8_t *bbase;
     const float *sg, *su;
     const int32_t *rows;
     float *hout;
     int32_t *dbg;
-    int nb0, M, m0, mstep, ncols, kdiv;
+    int nbl, G, g, M, m0, mstep, kdiv;
     if (b < n_sh) {
+        int rt;
+        shared_block(b, &g, &rt);
+        if (g >= gs) return;
+        nbl = a.S / 16;
+        G = gs;
         bbase = a.w.sgu;
         sg = a.w.ss_g;
         su = a.w.ss_u;
         rows = nullptr;
         hout = a.hs;
         dbg = nullptr;
-        nb0 = b * GU_NBW;
         M = a.T;
-        m0 = wave * 16;
-        mstep = 16 * S_WAVES;
-        ncols = a.S;
+        m0 = rt * 16;
+        mstep = 16 * MM_I8S_RT;
         kdiv = 1;
     } else {
-        const int nbl = a.I / 16;
-        const int per_e = (nbl + S_WAVES * GU_NBW - 1) / (S_WAVES * GU_NBW);
-        const int v = b - n_sh, e = v / per_e;
-        nb0 = ((v % per_e) * S_WAVES + wave) * GU_NBW;
+        nbl = a.I / 16;
+        G = units_per_wave_group(nbl);
+        const int v = b - n_sh, e = v / G;
+        g = v % G;
         M = min(a.cnt[e], a.T);
-        if (M == 0 || nb0 >= nbl) return;
+        if (M == 0) return;
         bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
         sg = a.w.s_g + (size_t)e * a.I;
         su = a.w.s_u + (size_t)e * a.I;
@@ -313,29 +476,82 @@ extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_gu(mm
         dbg = a.dbg_acc;
         m0 = 0;
         mstep = 16;
-        ncols = a.I;
         kdiv = a.K;
     }
-    for (; m0 < M; m0 += mstep)
-        gu_unit<GU_NBW, 1, 4>(a, bbase, KB, nb0, m0, M, sg, su, hout, ncols, dbg,
-                              [&](int m) { return rows ? rows[m] : m; },
-                              [&](int r) { return r / kdiv; });
+    if (m0 >= M) return;   /* whole block: a shared row tile past T */
+    const int ncols = nbl * 16;
+    const int nb0 = (g + G * wave) * MM_I8S_SEG;   /* this wave's first column block */
+    const int nseg = max(0, min(MM_I8S_SEG, nbl - nb0));
+    /* per-column scales: lane l holds column l % 16 of block nb0 + l / 16 */
+    const int scol = (min(nb0 + min(lane >> 4, MM_I8S_SEG - 1), nbl - 1)) * 16 + (lane & 15);
+    const float cg_all = sg[scol], cu_all = su[scol];
+    const int8_t *bp = bbase + (size_t)min(nb0, nbl - 1) * 2 * KB * 1024 + lane * 16;
+    v4i bq[MM_I8S_DEPTH_GU][2];
+    for (; m0 < M; m0 += mstep) {
+        /* row of this thread's A piece (tile row lane % 16) */
+        /* row lookup first, then the first ring turn (it does not depend on
+         * the rows), then the A tile; all unconditional so that the waits
+         * stay partial */
+        const int m = m0 + (lane & 15);
+        const int rl = rows ? rows[min(m, M - 1)] : min(m, M - 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < MM_I8S_DEPTH_GU; d++)
+#pragma unroll
+            for (int f = 0; f < 2; f++)
+                bq[d][f] = ldg16(bp + (size_t)min(d, KB * max(nseg, 1) - 1) * 2048 + f * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+        const int rid_a = m < M ? rl : -1;
+        const int t = rid_a >= 0 ? rid_a / kdiv : 0;
+        const float sx_a = rid_a >= 0 ? a.sa[t] : 0.0f;
+        __syncthreads();   /* the previous tile's LDS reads are done */
+        stage_a(lds_a, rid_a >= 0 ? a.a + (size_t)t * a.H : nullptr, KB, a.a);
+        __syncthreads();
+        if (nseg == 0) continue;
+        stream_lds<true, MM_I8S_DEPTH_GU>(
+            bp, KB, nseg, lds_addr(lds_a) + lane * 16, true, bq,
+            [&](int seg, v4i ag, v4i au) {
+                const int col = (nb0 + seg) * 16 + (lane & 15);
+                const float cg = __shfl(cg_all, seg * 16 + (lane & 15), MM_WAVE);
+                const float cu = __shfl(cu_all, seg * 16 + (lane & 15), MM_WAVE);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int rid = tile_row_i(rid_a, i);
+                    const float sx = tile_row_f(sx_a, i);
+                    const float gv = ((float)ag[i] * sx) * cg;
+                    const float uv = ((float)au[i] * sx) * cu;
+                    if (rid < 0) continue;
+                    hout[(size_t)rid * ncols + col] = silu_mul(gv, uv);
+                    if (dbg) {
+                        dbg[((size_t)rid * 2) * ncols + col] = ag[i];
+                        dbg[((size_t)rid * 2 + 1) * ncols + col] = au[i];
+                    }
+                }
+            });
+    }
 }
 
-/* Decode-shaped down projection, same block layout: H/16/DN_NBW shared
- * blocks (when there is a shared expert), then the routed experts'. */
-extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_down(mm_i8_gemm_args a) {
+/* Decode-shaped down projection, same block layout (shared blocks over the
+ * H/16 column blocks, then the routed experts').  Dynamic LDS:
+ * 16 * max(I, S) bytes. */
+extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i8_gemm_args a) {
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds_a[];
+    const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int nbl = a.H / 16;
-    const int n_sh = a.S ? nbl / DN_NBW : 0;
+    const int G = units_per_wave_group(nbl);
+    const int n_sh = a.S ? (G + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT : 0;
     const int b = blockIdx.x;
     const int8_t *abase, *bbase;
     const float *sa, *sd;
     const int32_t *rows;
     float *yout;
     int32_t *dbg;
-    int nb0, M, m0, mstep, Kd;
+    int g, M, m0, mstep, Kd;
     if (b < n_sh) {
+        int rt;
+        shared_block(b, &g, &rt);
+        if (g >= G) return;
         abase = a.a_sh;
         sa = a.sa_sh;
         Kd = a.S;
@@ -344,16 +560,14 @@ extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_down(
         rows = nullptr;
         yout = a.ys;
         dbg = nullptr;
-        nb0 = b * DN_NBW;
         M = a.T;
-        m0 = wave * 16;
-        mstep = 16 * S_WAVES;
+        m0 = rt * 16;
+        mstep = 16 * MM_I8S_RT;
     } else {
-        const int per_e = (nbl + S_WAVES * DN_NBW - 1) / (S_WAVES * DN_NBW);
-        const int v = b - n_sh, e = v / per_e;
-        nb0 = ((v % per_e) * S_WAVES + wave) * DN_NBW;
+        const int v = b - n_sh, e = v / G;
+        g = v % G;
         M = min(a.cnt[e], a.T);
-        if (M == 0 || nb0 >= nbl) return;
+        if (M == 0) return;
         abase = a.a;
         sa = a.sa;
         Kd = a.I;
@@ -365,9 +579,42 @@ extern "C" __global__ __launch_bounds__(MM_I8S_WAVES * MM_WAVE) void mm_i8_down(
         m0 = 0;
         mstep = 16;
     }
-    for (; m0 < M; m0 += mstep)
-        down_unit<DN_NBW, 1, 4>(abase, sa, Kd, bbase, nb0, m0, M, sd, yout, a.H, dbg,
-                                [&](int m) { return rows ? rows[m] : m; });
+    if (m0 >= M) return;
+    const int KB = Kd / 64;
+    const int nb0 = (g + G * wave) * MM_I8S_SEG;
+    const int nseg = max(0, min(MM_I8S_SEG, nbl - nb0));
+    const float cd_all = sd[(min(nb0 + min(lane >> 4, MM_I8S_SEG - 1), nbl - 1)) * 16 + (lane & 15)];
+    const int8_t *bp = bbase + (size_t)min(nb0, nbl - 1) * KB * 1024 + lane * 16;
+    v4i bq[MM_I8S_DEPTH_DOWN][1];
+    for (; m0 < M; m0 += mstep) {
+        const int m = m0 + (lane & 15);
+        const int rl = rows ? rows[min(m, M - 1)] : min(m, M - 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < MM_I8S_DEPTH_DOWN; d++)
+            bq[d][0] = ldg16(bp + (size_t)min(d, KB * max(nseg, 1) - 1) * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+        const int rid_a = m < M ? rl : -1;
+        const float sa_a = rid_a >= 0 ? sa[rid_a] : 0.0f;
+        __syncthreads();
+        stage_a(lds_a, rid_a >= 0 ? abase + (size_t)rid_a * Kd : nullptr, KB, abase);
+        __syncthreads();
+        if (nseg == 0) continue;
+        stream_lds<false, MM_I8S_DEPTH_DOWN>(
+            bp, KB, nseg, lds_addr(lds_a) + lane * 16, true, bq,
+            [&](int seg, v4i ac, v4i) {
+                const int col = (nb0 + seg) * 16 + (lane & 15);
+                const float cd = __shfl(cd_all, seg * 16 + (lane & 15), MM_WAVE);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int rid = tile_row_i(rid_a, i);
+                    const float sv = tile_row_f(sa_a, i);
+                    if (rid < 0) continue;
+                    yout[(size_t)rid * a.H + col] = ((float)ac[i] * sv) * cd;
+                    if (dbg) dbg[(size_t)rid * a.H + col] = ac[i];
+                }
+            });
+    }
 }
 
 /* ---- hidden-row quantisation and combine ------------------------------------- */
@@ -382,18 +629,29 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_quant_h(mm_i8_quant_rows
     }
 }
 
+/* out[t] (=|+=) sum_r w_r * y[t*K + r] (slot order) + ys[t].  All of a
+ * thread's loads are issued before the sums (one round trip). */
 extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_args a) {
     const int t = blockIdx.x;
     const float *w = a.topk_w + (size_t)t * a.K;
     for (int n = threadIdx.x * 4; n < a.H; n += blockDim.x * 4) {
+        f32x4 y[MM_KMAX], ys = {0.0f, 0.0f, 0.0f, 0.0f}, o = {0.0f, 0.0f, 0.0f, 0.0f};
+        float wr[MM_KMAX];
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < a.K) {
+                y[r] = *(const f32x4 *)(a.y + ((size_t)t * a.K + r) * a.H + n);
+                wr[r] = w[r];
+            }
+        if (a.has_shared) ys = *(const f32x4 *)(a.ys + (size_t)t * a.H + n);
+        f32x4 *op = (f32x4 *)(a.out + (size_t)t * a.H + n);
+        if (a.accumulate) o = *op;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int r = 0; r < a.K; r++) {
-            const f32x4 y = *(const f32x4 *)(a.y + ((size_t)t * a.K + r) * a.H + n);
-            acc += w[r] * y;
-        }
-        if (a.has_shared) acc += *(const f32x4 *)(a.ys + (size_t)t * a.H + n);
-        f32x4 *o = (f32x4 *)(a.out + (size_t)t * a.H + n);
-        *o = a.accumulate ? *o + acc : acc;
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < a.K) acc += wr[r] * y[r];
+        if (a.has_shared) acc += ys;
+        *op = a.accumulate ? o + acc : acc;
     }
     if (t == 0)
         for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
@@ -409,8 +667,8 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
          i += (size_t)gridDim.x * blockDim.x) {
         const int lane = (int)(i & 63);
         const size_t f = i >> 6;
-        const int kb = (int)(f % KB);
-        const int which = (int)((f / KB) % NS);
+        const int which = (int)(f % NS);
+        const int kb = (int)((f / NS) % KB);
         const int nb = (int)(f / ((size_t)KB * NS));
         const int8_t *src = which ? a.src1 : a.src0;
         const size_t row = (size_t)nb * 16 + (lane & 15);
@@ -476,34 +734,6 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
     return s_e >= 0;
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-/* 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (direct
- * global -> LDS load, no VGPR staging). */
-__device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
-    __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
-}
-
-/* LDS byte address of a __shared__ location. */
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
-}
-
-/* ds_read_b128 issued as inline assembly: the compiler's conservative
- * "wait for every outstanding direct-to-LDS load before any LDS read" would
- * otherwise drain the whole load ring every K step.  The caller orders the
- * reads with explicit vmcnt waits and a barrier, and must follow them with
- * lds_wait_regs() before using the results. */
-__device__ __forceinline__ v4i ds_read16(uint32_t addr) {
-    v4i r;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
-    return r;
-}
-
-/* s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima). */
-#define VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
-
 #define T_STAGES 4
 #define T_STAGE_BYTES (2 * T_FRAGS * 1024)
 
@@ -536,16 +766,23 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
         }
         asrc[h] = a.a + (size_t)arow * a.Kd + (lane >> 4) * 16;
     }
+    /* fragment column fr at K step kb: gate/up [nb][kb][gate|up] (fr = 2 nb +
+     * gate|up), plain [nb][kb] */
+    const int bstep = a.gu ? 2048 : 1024;
     const int8_t *bsrc[2];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
-        bsrc[h] = bexp + (size_t)min(fr0 + 2 * wave + h, nfr_total - 1) * KB * 1024 + lane * 16;
+    for (int h = 0; h < 2; h++) {
+        const int fr = min(fr0 + 2 * wave + h, nfr_total - 1);
+        const size_t off = a.gu ? ((size_t)(fr >> 1) * 2 * KB + (fr & 1)) * 1024
+                                : (size_t)fr * KB * 1024;
+        bsrc[h] = bexp + off + lane * 16;
+    }
     auto issue = [&](int kb) {
         int8_t *st = lds[kb % T_STAGES];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             lds_dma16(asrc[h] + kb * 64, st + (2 * wave + h) * 1024);
-            lds_dma16(bsrc[h] + (size_t)kb * 1024, st + T_FRAGS * 1024 + (2 * wave + h) * 1024);
+            lds_dma16(bsrc[h] + (size_t)kb * bstep, st + T_FRAGS * 1024 + (2 * wave + h) * 1024);
         }
     };
 

@@ -16,7 +16,7 @@ import re
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "libmlamoe.so")
+LIB_PATH = os.environ.get("MLAMOE_LIB") or os.path.join(PKG_DIR, "libmlamoe.so")
 HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "mlamoe.h")
 
 MM_LOAD_BF16, MM_LOAD_INT8, MM_LOAD_DEVICE_PTRS = 1, 2, 4
