@@ -385,12 +385,17 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ra.r.sigmoid = g->router_sigmoid;
     ra.r.norm_topk = g->norm_topk;
     ra.r.scale = g->routed_scaling;
-    ra.cnt = c->moe_cnt;
-    ra.rows = rows;
+    /* decode-shaped GEMMs stage a 16-row A tile (16 * K bytes) and a row list
+     * (T ints) in LDS; shapes beyond 64 KB of it take the tiled GEMMs */
+    const size_t lds_dec = 16 * (H > (I > S ? I : S) ? H : (I > S ? I : S)) + 4 * (size_t)T;
+    const int tiled = T >= c->i8_tiled_min_t || lds_dec > 65536;
+    /* per-expert row lists only for the tiled path; the decode-shaped GEMMs
+     * build theirs from the routing */
+    ra.cnt = tiled ? c->moe_cnt : NULL;
+    ra.rows = tiled ? rows : NULL;
     ra.x = xn;
     ra.qx = qx;
     ra.sx = sx;
-    const int tiled = T >= c->i8_tiled_min_t;
     if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
                         64 * MM_I8_RT_WAVES, 0, &ra)))
         return st;
@@ -400,6 +405,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ga.w = L->i8;
     ga.cnt = c->moe_cnt;
     ga.rows = rows;
+    ga.topk = idx;
     ga.a = qx;
     ga.sa = sx;
     ga.h = h;
@@ -436,7 +442,8 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         const unsigned nb = (unsigned)((S ? sh_blocks(ceil_div(S / 16, per_blk)) : 0) +
                                        E * ceil_div(I / 16, per_blk));
         /* dynamic LDS: the 16-row A tile, 16 * K bytes */
-        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H, &ga))) return st;
+        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H + 4 * (size_t)T, &ga)))
+            return st;
     }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
@@ -467,7 +474,8 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
         const size_t gpe = ceil_div(H / 16, (size_t)MM_I8S_W * MM_I8S_SEG);
         const unsigned nb = (unsigned)((S ? sh_blocks(gpe) : 0) + E * gpe);
-        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W, 16 * (S > I ? S : I), &ga)))
+        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W,
+                            16 * (S > I ? S : I) + 4 * (size_t)T, &ga)))
             return st;
     }
 

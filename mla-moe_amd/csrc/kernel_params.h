@@ -99,8 +99,8 @@ typedef struct {
 #define MM_EMAX 256
 typedef struct {
     mm_router_args r;
-    int32_t *cnt;            /* [E] rows per expert (zero on entry) */
-    int32_t *rows;           /* [E, T] route ids (t*K + r) per expert */
+    int32_t *cnt;            /* [E] rows per expert (zero on entry), or 0 */
+    int32_t *rows;           /* [E, T] route ids (t*K + r) per expert, or 0 (no lists) */
     const float *x;          /* [T, H] */
     int8_t *qx;              /* [T, H] */
     float *sx;               /* [T] */
@@ -109,8 +109,9 @@ typedef struct {
 /* Grouped int8 GEMM over experts 0..E-1 (routed) and the shared expert. */
 typedef struct {
     mm_i8_weights w;
-    const int32_t *cnt;      /* [E] */
-    const int32_t *rows;     /* [E, T] */
+    const int32_t *cnt;      /* [E] (tiled path) */
+    const int32_t *rows;     /* [E, T] (tiled path) */
+    const int32_t *topk;     /* [T, K] expert ids (decode path builds its row lists) */
     const int8_t *a;         /* gate/up: qx [T, H];  down: qh [T*K, I] */
     const float *sa;         /* gate/up: sx [T];     down: sh [T*K] */
     const int8_t *a_sh;      /* down: shared qhs [T, S] */

@@ -243,21 +243,23 @@ __device__ __forceinline__ void i8_route(const mm_i8_route_args &a) {
             r.topk_idx[(size_t)tok * K + lane] = e;
             r.topk_w[(size_t)tok * K + lane] = w;
             my_e[t] = e;
-            my_pos[t] = atomicAdd(&lcnt[e], 1);
+            if (a.rows) my_pos[t] = atomicAdd(&lcnt[e], 1);
         }
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int n = lcnt[e];
-        lcnt[e] = n ? atomicAdd(&a.cnt[e], n) : 0;   /* now the block's base */
-    }
-    __syncthreads();
+    if (a.rows) {   /* per-expert row lists (block-uniform) */
+        __syncthreads();
+        for (int e = threadIdx.x; e < E; e += blockDim.x) {
+            const int n = lcnt[e];
+            lcnt[e] = n ? atomicAdd(&a.cnt[e], n) : 0;   /* now the block's base */
+        }
+        __syncthreads();
 #pragma unroll
-    for (int t = 0; t < RT_TPW; t++) {
-        const int e = my_e[t];
-        if (e >= 0) {
-            const int pos = lcnt[e] + my_pos[t];
-            if (pos < T) a.rows[(size_t)e * T + pos] = (t0 + t) * K + lane;
+        for (int t = 0; t < RT_TPW; t++) {
+            const int e = my_e[t];
+            if (e >= 0) {
+                const int pos = lcnt[e] + my_pos[t];
+                if (pos < T) a.rows[(size_t)e * T + pos] = (t0 + t) * K + lane;
+            }
         }
     }
 #pragma unroll
@@ -411,6 +413,37 @@ __device__ __forceinline__ float tile_row_f(float a_side, int i) {
     return __shfl(a_side, 4 * (lane >> 4) + i, MM_WAVE);
 }
 
+/* Row list of routed expert e, built by the whole block from the routing
+ * (topk [R] expert ids): the route ids with topk[rid] == e in ascending
+ * order, into LDS `list` (at most T entries; a token picks an expert at most
+ * once).  Returns the count (block-uniform).  No atomics: each wave ballots
+ * its hits and places them after the hits of the waves before it. */
+__device__ __forceinline__ int expert_rows(const int32_t *topk, int R, int e, int *list) {
+    __shared__ int wsum[MM_I8S_W];
+    constexpr int NTHR = MM_I8S_W * MM_WAVE;
+    const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
+    int total = 0;
+    for (int base = 0; base < R; base += NTHR) {
+        const int i = base + tid;
+        const bool hit = i < R && topk[i] == e;
+        const unsigned long long bal = __ballot(hit);
+        if (lane == 0) wsum[wave] = __popcll(bal);
+        __syncthreads();
+        int off = total, all = 0;
+#pragma unroll
+        for (int w = 0; w < MM_I8S_W; w++) {
+            const int c = wsum[w];
+            off += w < wave ? c : 0;
+            all += c;
+        }
+        if (hit) list[off + __popcll(bal & ((1ull << lane) - 1ull))] = i;
+        __syncthreads();
+        total += all;
+    }
+    return total;
+}
+
 /* Shared-expert block b of a decode GEMM: column group and row tile, with
  * the MM_I8S_RT blocks of a column group 8 block ids apart (one XCD, so
  * their identical weight reads meet in that XCD's L2). */
@@ -430,7 +463,8 @@ __device__ __forceinline__ int units_per_wave_group(int nbl) {
  * (column group g, row tile rt + MM_I8S_RT * k); the rest: routed expert e,
  * column group g, all of e's rows 16 at a time.  Shared blocks come first so
  * that their work starts early; a routed block of an expert with no rows
- * exits at once.  Dynamic LDS: 16 * H bytes (the A tile). */
+ * exits at once.  Dynamic LDS: 16 * H bytes (the A tile), then T ints (the
+ * expert's row list). */
 extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds_a[];
     const int lane = threadIdx.x & (MM_WAVE - 1);
@@ -441,7 +475,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
     const int b = blockIdx.x;
     const int8_t *bbase;
     const float *sg, *su;
-    const int32_t *rows;
+    const int *rows;
     float *hout;
     int32_t *dbg;
     int nbl, G, g, M, m0, mstep, kdiv;
@@ -466,12 +500,13 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         G = units_per_wave_group(nbl);
         const int v = b - n_sh, e = v / G;
         g = v % G;
-        M = min(a.cnt[e], a.T);
+        int *list = (int *)(lds_a + 16 * a.H);
+        M = expert_rows(a.topk, a.T * a.K, e, list);
         if (M == 0) return;
         bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
         sg = a.w.s_g + (size_t)e * a.I;
         su = a.w.s_u + (size_t)e * a.I;
-        rows = a.rows + (size_t)e * a.T;
+        rows = list;
         hout = a.h;
         dbg = a.dbg_acc;
         m0 = 0;
@@ -533,7 +568,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
 
 /* Decode-shaped down projection, same block layout (shared blocks over the
  * H/16 column blocks, then the routed experts').  Dynamic LDS:
- * 16 * max(I, S) bytes. */
+ * 16 * max(I, S) bytes, then T ints. */
 extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i8_gemm_args a) {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds_a[];
     const int lane = threadIdx.x & (MM_WAVE - 1);
@@ -544,7 +579,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i
     const int b = blockIdx.x;
     const int8_t *abase, *bbase;
     const float *sa, *sd;
-    const int32_t *rows;
+    const int *rows;
     float *yout;
     int32_t *dbg;
     int g, M, m0, mstep, Kd;
@@ -566,14 +601,15 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i
     } else {
         const int v = b - n_sh, e = v / G;
         g = v % G;
-        M = min(a.cnt[e], a.T);
+        int *list = (int *)(lds_a + 16 * (a.S > a.I ? a.S : a.I));
+        M = expert_rows(a.topk, a.T * a.K, e, list);
         if (M == 0) return;
         abase = a.a;
         sa = a.sa;
         Kd = a.I;
         bbase = a.w.d + (size_t)e * nbl * (a.I / 64) * 1024;
         sd = a.w.s_d + (size_t)e * a.H;
-        rows = a.rows + (size_t)e * a.T;
+        rows = list;
         yout = a.y;
         dbg = a.dbg_acc;
         m0 = 0;
