@@ -35,7 +35,6 @@ static const struct {
     [K_MOE_BF16_S3] = {"mm_moe_bf16_stage3", MOD_MOE_BF16},
     [K_FILL] = {"mm_fill", MOD_UTIL},
     [K_QUANT_W] = {"mm_quant_weight", MOD_UTIL},
-    [K_TRANSPOSE_GATE] = {"mm_transpose_gate", MOD_UTIL},
     [K_I8_ROUTE] = {"mm_i8_route", MOD_MOE_I8},
     [K_I8_GU] = {"mm_i8_gu", MOD_MOE_I8},
     [K_I8_QUANT_H] = {"mm_i8_quant_h", MOD_MOE_I8},

@@ -17,7 +17,6 @@ typedef enum {
     K_MOE_BF16_S3,
     K_FILL,
     K_QUANT_W,
-    K_TRANSPOSE_GATE,
     K_I8_ROUTE,
     K_I8_GU,
     K_I8_QUANT_H,
@@ -40,7 +39,7 @@ typedef struct {
 typedef struct {
     int loaded;
     unsigned formats;
-    float *wgT;                 /* [H, E] fp32 router weight, transposed */
+    uint16_t *wg;               /* [E, H] bf16 router weight */
     float *bias;                /* [E] or NULL */
     uint16_t *bf16_pool;        /* one allocation holding the six bf16 families */
     uint16_t *eg, *eu, *ed, *sg, *su, *sd;

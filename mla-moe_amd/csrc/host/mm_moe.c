@@ -3,8 +3,8 @@
  * Mirrors the reference's ffn_compute (src/run.c:116-162) over T tokens.
  * Weight upload replaces the reference GPU driver's warm_up packing
  * (src/getp_run.hip:58-113, 781-808): every layer owns one device pool per
- * weight format, and the router weight is kept transposed in fp32 for the
- * sequential-order router.
+ * weight format; the router weight is kept as the checkpoint's bf16 [E, H]
+ * for the sequential-order router.
  */
 #include <stdlib.h>
 #include <string.h>
@@ -21,7 +21,7 @@ void mm_moe_release(mm_ctx *c) {
     if (!c->layers) return;
     for (int l = 0; l < c->n_layers; l++) {
         mm_moe_layer *L = &c->layers[l];
-        if (L->wgT) hipFree(L->wgT);
+        if (L->wg) hipFree(L->wg);
         if (L->bias) hipFree(L->bias);
         if (L->bf16_pool) hipFree(L->bf16_pool);
         if (L->i8_pool) hipFree(L->i8_pool);
@@ -188,12 +188,9 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
     mm_moe_layer *L = &c->layers[layer];
     if (L->loaded) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer: layer %d already loaded", layer);
 
-    uint16_t *gate_tmp = NULL;
-    MM_HIP(hipMalloc((void **)&L->wgT, H * E * sizeof(float)));
-    MM_HIP(hipMalloc((void **)&gate_tmp, H * E * sizeof(uint16_t)));
-    if ((st = upload(c, gate_tmp, w->moe_gate, H * E * 2, dev))) goto out;
-    mm_transpose_gate_args ta = {gate_tmp, L->wgT, (int)E, (int)H};
-    if ((st = mm_launch(c, K_TRANSPOSE_GATE, 1024, 1, 1, 256, 0, &ta))) goto out;
+    /* router weight in its checkpoint layout [E, H] bf16 */
+    MM_HIP(hipMalloc((void **)&L->wg, H * E * sizeof(uint16_t)));
+    if ((st = upload(c, L->wg, w->moe_gate, H * E * 2, dev))) goto out;
     if (w->moe_gate_bias) {
         if (hipMalloc((void **)&L->bias, E * sizeof(float)) != hipSuccess) {
             st = mm_fail(MM_ERR_NOMEM, "mm_moe_load_layer: bias");
@@ -233,7 +230,6 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
     L->loaded = 1;
 out:;
     hipError_t e = hipStreamSynchronize(c->stream);
-    if (gate_tmp) hipFree(gate_tmp);
     if (!st && e != hipSuccess) st = mm_hip_fail(e, "mm_moe_load_layer");
     return st;
 }
@@ -275,7 +271,7 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_gu_bf16_args a;
         memset(&a, 0, sizeof(a));
         a.r.x = xn + (size_t)t0 * H;
-        a.r.wgT = L->wgT;
+        a.r.wg = L->wg;
         a.r.logits_in = logits ? logits + (size_t)t0 * E : NULL;
         a.r.bias = L->bias;
         a.r.probs = probs ? probs + (size_t)t0 * E : NULL;
@@ -327,6 +323,15 @@ static size_t sh_blocks(size_t groups) {
 
 static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
 
+/* 1-D grid of the tiled GEMM: every (column slab, run of 8 row groups) pair
+ * gets 8 blocks on one XCD; the count is padded to a multiple of 64 so that
+ * the kernel's block -> (slab, row group) map covers every pair once (blocks
+ * past the last row group exit). */
+static unsigned tiled_blocks(unsigned nslab, unsigned groups) {
+    const size_t runs = (size_t)nslab * ceil_div(groups, MM_I8S_XCD);
+    return (unsigned)(ceil_div(runs, MM_I8S_XCD) * MM_I8S_XCD * MM_I8S_XCD);
+}
+
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
                         const mm_moe_i8_debug *dbg) {
@@ -358,7 +363,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_router_args la;
         memset(&la, 0, sizeof(la));
         la.x = xn;
-        la.wgT = L->wgT;
+        la.wg = L->wg;
         la.logits_out = (float *)(ws + o_lg);
         la.T = T;
         la.H = (int)H;
@@ -372,7 +377,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     mm_i8_route_args ra;
     memset(&ra, 0, sizeof(ra));
     ra.r.x = xn;
-    ra.r.wgT = L->wgT;
+    ra.r.wg = L->wg;
     ra.r.logits_in = logits;
     ra.r.bias = L->bias;
     ra.r.probs = probs;
@@ -426,13 +431,13 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
                                (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * I / 16 + 7) / 8), mt_routed, 1, 256, 0,
+        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((2 * I / 16 + 7) / 8), mt_routed), 1, 1, 256, 0,
                             &ta)))
             return st;
         if (S) {
             mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
                                    hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, (unsigned)((2 * S / 16 + 7) / 8), mt_shared, 1,
+            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((2 * S / 16 + 7) / 8), mt_shared), 1, 1,
                                 256, 0, &ts)))
                 return st;
         }
@@ -455,12 +460,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
                                0, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_routed, 1, 256, 0, &td)))
+        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((H / 16 + 7) / 8), mt_routed), 1, 1, 256, 0, &td)))
             return st;
         if (S) {
             mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
                                     NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, (unsigned)((H / 16 + 7) / 8), mt_shared, 1, 256, 0,
+            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((H / 16 + 7) / 8), mt_shared), 1, 1, 256, 0,
                                 &tsd)))
                 return st;
         }
@@ -543,7 +548,7 @@ int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
     mm_router_args a;
     memset(&a, 0, sizeof(a));
     a.x = xn;
-    a.wgT = L->wgT;
+    a.wg = L->wg;
     a.logit_bias = logit_bias;
     a.logits_out = logits;
     a.T = T;

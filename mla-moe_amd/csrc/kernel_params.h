@@ -12,7 +12,7 @@
  * rule, optional normalisation and scaling. */
 typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */
-    const float *wgT;        /* [H, E] router weight, fp32, transposed */
+    const uint16_t *wg;      /* [E, H] router weight, bf16 (checkpoint layout) */
     const float *logits_in;  /* [T, E] or 0 */
     const float *bias;       /* [E] selection bias (GLM e_score correction) or 0 */
     const float *logit_bias; /* [E] added to computed logits (logits-only mode) or 0 */
@@ -69,11 +69,6 @@ typedef struct {
     int rows, K;
 } mm_quant_w_args;
 
-typedef struct {
-    const uint16_t *src;     /* [E, H] bf16 */
-    float *dst;              /* [H, E] fp32 */
-    int E, H;
-} mm_transpose_gate_args;
 
 #endif
 

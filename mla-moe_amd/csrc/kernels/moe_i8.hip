@@ -775,13 +775,13 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
 
 /* One 128-row x 8-fragment tile starting at row m0 of expert e (M rows). */
 __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_STAGE_BYTES],
-                                           int e, int m0, int M) {
+                                           int e, int m0, int M, int slab) {
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
     const int wm = wave >> 1, wn = wave & 1;
     const int KB = a.Kd / 64;
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int fr0 = blockIdx.x * T_FRAGS;
+    const int fr0 = slab * T_FRAGS;
     const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
     const int8_t *bexp = a.b + (size_t)e * a.b_expert_stride;
 
@@ -901,15 +901,27 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
 /* grid.x = 8-fragment column slab, grid.y = row group.  A block walks the
  * group's 128-row tiles in order, so the slab's weights (K x 128 bytes) come
  * from HBM once and from this CU's L2 for the group's later tiles. */
+/* 1-D grid (a multiple of 64 blocks, see the host).  Blocks are dealt to
+ * the 8 XCDs round robin (block b runs on XCD b % 8); b is mapped to (column
+ * slab, row group) so that each XCD receives runs of 8 consecutive row
+ * groups of ONE slab: the slab's weights then come from HBM once per run
+ * and from that XCD's L2 for the other row groups (the tiles of a hot
+ * expert are consecutive row groups). */
 extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[T_STAGES][T_STAGE_BYTES];
-    int e, g0, M;
-    if (!tile_owner(a, blockIdx.y, &e, &g0, &M)) return;
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    if ((int)blockIdx.x * T_FRAGS >= nfr_total) return;   /* uniform per block */
+    const int nslab = (nfr_total + T_FRAGS - 1) / T_FRAGS;
+    const int b = blockIdx.x;
+    const int xcd = b % MM_I8S_XCD, j = b / MM_I8S_XCD;
+    const int q = (j / MM_I8S_XCD) * MM_I8S_XCD + xcd;   /* (slab, row-group run) index */
+    const int slab = q % nslab;
+    const int grp = (q / nslab) * MM_I8S_XCD + j % MM_I8S_XCD;
+    if (grp >= a.max_groups) return;                      /* uniform per block */
+    int e, g0, M;
+    if (!tile_owner(a, grp, &e, &g0, &M)) return;
     const int g1 = min(M, g0 + a.mgroup * MM_I8T_BM);
     for (int m0 = g0; m0 < g1; m0 += MM_I8T_BM) {
-        tiled_tile(a, lds, e, m0, M);
+        tiled_tile(a, lds, e, m0, M, slab);
         __builtin_amdgcn_s_barrier();   /* the LDS ring is refilled by the next tile */
     }
 }

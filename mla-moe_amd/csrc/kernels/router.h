@@ -4,11 +4,10 @@
  * experts are identical to the CPU reference:
  *   - logits: y[e] = sum_i x[i] * W[e, i] accumulated in fp32 in ascending i
  *     with a separate multiply and add (run.c:29-37).  One lane owns one
- *     (token, expert) dependent add chain.  The router weight is kept
- *     transposed ([H, E], fp32); the block streams it through LDS in
- *     double-buffered chunks that all its waves share, and each wave reads
- *     its tokens' x through scalar loads, so the add chains never wait on
- *     HBM.
+ *     (token, expert) dependent add chain.  The block streams the bf16
+ *     router weight ([E, H], its checkpoint layout) and the tokens' x
+ *     through LDS in chunks that all its waves share, prefetched several
+ *     chunks ahead, so the add chains rarely wait on memory.
  *   - softmax (run.c:95-105): max, e^(x - max) (-inf -> 0), sum in ascending
  *     expert order, divide; or sigmoid 1 / (1 + e^-x) (run.c:125-127).
  *   - top-k (run.c:132-143): K passes; each picks the unused expert with the
@@ -19,6 +18,7 @@
  * A wave routes TPW tokens; lane l holds experts l, l+64, ... (EJ of them).
  */
 #pragma once
+#include <type_traits>
 #include "common.h"
 
 #define MM_KMAX 16
@@ -40,19 +40,36 @@ struct router_no_post {
 };
 
 /* Block-cooperative logits for the block's MM_ROUTER_TOKENS tokens.  Every
- * thread of the block must call this (it synchronises).  Each LDS buffer
- * holds a chunk of HC router-weight rows ([HC][E]) and the same HC columns
- * of the block's token rows ([tokens][HC]); the next chunk is fetched into
- * registers while the current one is consumed.  Inside a chunk the lanes'
- * add chains run on operands already in LDS, read one group of 8 ahead.
+ * thread of the block must call this (it synchronises).
+ *
+ * The router weight is used in its checkpoint layout, W [E][H] bf16 (its
+ * fp32 values are exact).  It is consumed in chunks of HC hidden indices:
+ * the chunk's [E][HC] block of W (16 KB) goes to LDS expert-major with rows
+ * padded by 16 bytes, so that a lane reads the next 8 weights of its expert
+ * with one conflict-free 16-byte read; the same HC columns of the block's
+ * token rows ([tokens][HC] fp32) go beside it.  Chunks are loaded into
+ * registers RL_PF chunks ahead of their use and written to one of two LDS
+ * buffers when their turn comes, so the serial add chains (one add per
+ * hidden index, in the reference's ascending order) rarely wait for memory.
  * On return lg[t][j] is the logit of token t0 + t, expert lane + 64 j. */
+#define RL_PF 3                                    /* chunks in flight in registers */
+#define RL_WBYTES (MM_ROUTER_CHUNK_FLOATS * 2)      /* bf16 weight bytes per chunk */
 template <int EJ, int TPW>
 __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int tb0, int t0,
                                                     float (&lg)[TPW][EJ], float *lds) {
+    static_assert(TPW <= 2, "tail handling assumes at most two tokens per wave");
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int E = a.E, H = a.H, T = a.T;
-    constexpr int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* rows per chunk */
-    const int CH = HC * E;
+    constexpr int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* hidden indices per chunk */
+    constexpr int RS = HC + 8;                                    /* padded LDS row, bf16 */
+    constexpr int WLDS = MM_WAVE * EJ * RS * 2;                   /* weight bytes in LDS */
+    constexpr int XB = MM_ROUTER_TOKENS * HC * 4;                 /* x bytes per chunk */
+    constexpr int BUF = WLDS + XB;                                /* LDS bytes per buffer */
+    static_assert(2 * BUF <= MM_ROUTER_LDS_FLOATS * 4, "router LDS");
+    constexpr int PPE = HC / 8;                                   /* 16-byte pieces per expert row */
+    constexpr int WP = RL_WBYTES / 16 / MM_ROUTER_THREADS;        /* weight pieces per thread */
+    constexpr int XP = (XB / 16 + MM_ROUTER_THREADS - 1) / MM_ROUTER_THREADS;
+    const int nch = (H + HC - 1) / HC;
     const bool active = t0 < T;
     const int tw = t0 - tb0;                                       /* wave's first row in x chunk */
 #pragma unroll
@@ -60,98 +77,121 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
 #pragma unroll
         for (int j = 0; j < EJ; j++) lg[t][j] = 0.0f;
 
-    constexpr int PER = MM_ROUTER_CHUNK_FLOATS / 4 / MM_ROUTER_THREADS;
-    constexpr int XPER = (MM_ROUTER_TOKENS * HC / 4 + MM_ROUTER_THREADS - 1) / MM_ROUTER_THREADS;
-    f32x4 stage[PER], xstage[XPER];
-    auto fetch = [&](int c0) {
-        const f32x4 *src = (const f32x4 *)(a.wgT + (size_t)c0 * E);
-        const int n4 = (min(HC, H - c0) * E) >> 2;
+    /* register slots for chunks c+1 .. c+PF (statically indexed: the chunk
+     * loop below is unrolled by PF) */
+    u32x4 wr[RL_PF][WP], xr[RL_PF][XP];
+    auto fetch = [&](int slot, int c) {
+        const int c0 = c * HC;
+        /* every load is unconditional (addresses clamped into range, the
+         * value zeroed afterwards) so that the waits for a chunk stay
+         * partial */
 #pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
-            stage[k] = i < n4 ? src[i] : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < WP; k++) {
+            const int i = threadIdx.x + k * MM_ROUTER_THREADS;   /* piece: expert i / PPE */
+            const int e = i / PPE, o = (i % PPE) * 8;
+            const bool ok = c < nch && e < E && c0 + o < H;
+            const u32x4 v = *(const u32x4 *)(a.wg + (size_t)min(e, E - 1) * H + min(c0 + o, H - 8));
+            wr[slot][k] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int k = 0; k < XPER; k++) {
+        for (int k = 0; k < XP; k++) {
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;   /* float4 index in [tokens][HC] */
             const int row = i / (HC / 4), col = (i % (HC / 4)) * 4;
             const int tok = min(tb0 + row, T - 1);
-            xstage[k] = (row < MM_ROUTER_TOKENS && c0 + col < H)
-                            ? *(const f32x4 *)(a.x + (size_t)tok * H + c0 + col)
-                            : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            const bool ok = c < nch && row < MM_ROUTER_TOKENS && c0 + col < H;
+            const u32x4 v = *(const u32x4 *)(a.x + (size_t)tok * H + min(c0 + col, H - 4));
+            xr[slot][k] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
         }
     };
-    auto store = [&](float *buf) {
+    auto store = [&](int slot, uint8_t *buf) {
 #pragma unroll
-        for (int k = 0; k < PER; k++) {
+        for (int k = 0; k < WP; k++) {
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;
-            if (i * 4 < CH) *(f32x4 *)(buf + i * 4) = stage[k];
+            const int e = i / PPE, o = (i % PPE) * 8;
+            *(u32x4 *)(buf + ((size_t)e * RS + o) * 2) = wr[slot][k];
         }
 #pragma unroll
-        for (int k = 0; k < XPER; k++) {
+        for (int k = 0; k < XP; k++) {
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;
-            if (i < MM_ROUTER_TOKENS * HC / 4)
-                *(f32x4 *)(buf + MM_ROUTER_CHUNK_FLOATS + i * 4) = xstage[k];
+            if (i < XB / 16) *(u32x4 *)(buf + WLDS + (size_t)i * 16) = xr[slot][k];
         }
     };
-    fetch(0);
-    store(lds);
-    __syncthreads();
-    int cur = 0;
-    for (int c0 = 0; c0 < H; c0 += HC) {
-        const bool more = c0 + HC < H;
-        if (more) fetch(c0 + HC);
-        if (active) {
+    auto compute = [&](const uint8_t *buf) {
 #pragma clang fp contract(off)
-            /* Rows of the chunk past H were fetched as zeros: x*w = +0 and
-             * acc + (+0) = acc exactly (acc starts at +0 and never becomes -0
-             * under round-to-nearest), so the whole chunk is consumed with a
-             * constant trip count and the result is bit-identical. */
-            const float *wb = lds + cur * MM_ROUTER_BUF_FLOATS + lane;
-            const float *xb = lds + cur * MM_ROUTER_BUF_FLOATS + MM_ROUTER_CHUNK_FLOATS + tw * HC;
-            float w[2][8][EJ], xv[2][TPW][8];
-            auto load = [&](int s, int i0) {
+        if (!active) return;
+        /* Indices of the chunk past H were fetched as zeros: x*w = +0 and
+         * acc + (+0) = acc exactly (acc starts at +0 and never becomes -0
+         * under round-to-nearest), so the whole chunk is consumed with a
+         * constant trip count and the result is bit-identical. */
+        const uint8_t *wb = buf + (size_t)lane * RS * 2;
+        const float *xb = (const float *)(buf + WLDS) + tw * HC;
+        u32x4 wq[2][EJ];
+        float xv[2][TPW][8];
+        auto load = [&](int s, int i0) {
 #pragma unroll
-                for (int u = 0; u < 8; u++)
+            for (int j = 0; j < EJ; j++)
+                wq[s][j] = *(const u32x4 *)(wb + ((size_t)j * MM_WAVE * RS + i0) * 2);
 #pragma unroll
-                    for (int j = 0; j < EJ; j++) w[s][u][j] = wb[(i0 + u) * E + MM_WAVE * j];
+            for (int t = 0; t < TPW; t++) {
+                const f32x4 lo = *(const f32x4 *)(xb + t * HC + i0);
+                const f32x4 hi = *(const f32x4 *)(xb + t * HC + i0 + 4);
+                xv[s][t][0] = lo.x; xv[s][t][1] = lo.y; xv[s][t][2] = lo.z; xv[s][t][3] = lo.w;
+                xv[s][t][4] = hi.x; xv[s][t][5] = hi.y; xv[s][t][6] = hi.z; xv[s][t][7] = hi.w;
+            }
+        };
+        /* products first (independent), then the ordered adds, so the only
+         * serial dependency left is each accumulator's add chain; NT token
+         * chains (the wave's tokens inside T) */
+        auto comp = [&](int s, auto nt) {
+            constexpr int NT = decltype(nt)::value;
+            float prod[8][NT][EJ];
 #pragma unroll
-                for (int t = 0; t < TPW; t++) {
-                    const f32x4 lo = *(const f32x4 *)(xb + t * HC + i0);
-                    const f32x4 hi = *(const f32x4 *)(xb + t * HC + i0 + 4);
-                    xv[s][t][0] = lo.x; xv[s][t][1] = lo.y; xv[s][t][2] = lo.z; xv[s][t][3] = lo.w;
-                    xv[s][t][4] = hi.x; xv[s][t][5] = hi.y; xv[s][t][6] = hi.z; xv[s][t][7] = hi.w;
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int j = 0; j < EJ; j++) {
+                    const uint32_t d = wq[s][j][u >> 1];
+                    const float w = __uint_as_float((u & 1) ? (d & 0xffff0000u) : (d << 16));
+#pragma unroll
+                    for (int t = 0; t < NT; t++) prod[u][t][j] = xv[s][t][u] * w;
                 }
-            };
-            /* products first (independent), then the ordered adds, so the
-             * only serial dependency left is each accumulator's add chain */
-            auto compute = [&](int s) {
-                float prod[8][TPW][EJ];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
+            for (int u = 0; u < 8; u++)
 #pragma unroll
-                    for (int t = 0; t < TPW; t++)
+                for (int t = 0; t < NT; t++)
 #pragma unroll
-                        for (int j = 0; j < EJ; j++) prod[u][t][j] = xv[s][t][u] * w[s][u][j];
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-#pragma unroll
-                    for (int t = 0; t < TPW; t++)
-#pragma unroll
-                        for (int j = 0; j < EJ; j++) lg[t][j] = lg[t][j] + prod[u][t][j];
-            };
-            /* two register stages, statically indexed: one group of 8 ahead */
+                    for (int j = 0; j < EJ; j++) lg[t][j] = lg[t][j] + prod[u][t][j];
+        };
+        auto run = [&](auto nt) {
             load(0, 0);
 #pragma unroll
             for (int g = 0; g < HC / 8; g++) {
                 if (g + 1 < HC / 8) load((g + 1) & 1, (g + 1) * 8);
-                compute(g & 1);
+                comp(g & 1, nt);
             }
-        }
-        if (more) {
-            store(lds + (cur ^ 1) * MM_ROUTER_BUF_FLOATS);
-            __syncthreads();
-            cur ^= 1;
+        };
+        if (TPW == 1 || t0 + TPW <= T)
+            run(std::integral_constant<int, TPW>());
+        else
+            run(std::integral_constant<int, 1>());   /* TPW = 2 at the tail: one chain */
+    };
+    uint8_t *lbuf = (uint8_t *)lds;
+#pragma unroll
+    for (int k = 0; k < RL_PF; k++) fetch(k, k);
+    /* chunk c: slot c % PF -> LDS buffer c % 2, barrier, refill the slot with
+     * chunk c + PF, consume the buffer.  One barrier per chunk suffices: the
+     * buffer written for chunk c was last read for chunk c - 2, which every
+     * wave finished before the barrier of chunk c - 1. */
+    for (int c0 = 0; c0 < nch; c0 += RL_PF) {
+#pragma unroll
+        for (int k = 0; k < RL_PF; k++) {
+            const int c = c0 + k;
+            if (c < nch) {   /* block-uniform */
+                uint8_t *buf = lbuf + (c & 1) * BUF;
+                store(k, buf);
+                __syncthreads();
+                fetch(k, c + RL_PF);
+                compute(buf);
+            }
         }
     }
 #pragma unroll

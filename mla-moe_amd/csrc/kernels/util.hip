@@ -1,5 +1,5 @@
-/* util.hip -- device-side data preparation: synthetic inputs, the int8
- * per-output-channel weight quantiser and the router-weight transpose. */
+/* util.hip -- device-side data preparation: synthetic inputs and the int8
+ * per-output-channel weight quantiser. */
 #include "common.h"
 
 /* Counter-based generator: splitmix64 of (seed, index), so any element can be
@@ -55,12 +55,3 @@ extern "C" __global__ __launch_bounds__(256) void mm_quant_weight(mm_quant_w_arg
     }
 }
 
-/* [E, H] bf16 -> [H, E] fp32 */
-extern "C" __global__ __launch_bounds__(256) void mm_transpose_gate(mm_transpose_gate_args a) {
-    const size_t n = (size_t)a.E * a.H;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
-        size_t h = i / a.E, e = i % a.E;
-        a.dst[i] = bf16_f32(a.src[e * a.H + h]);
-    }
-}
