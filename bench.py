@@ -261,7 +261,7 @@ def bench_mla_decode(ctx, steps, warmup, B=32, NH=16, L=4096):
         mlamoe._check(lib.mm_mla_absorbed_decode_dev(h, 0, B, q.ptr, cache.ptr, L, None, L,
                                                      out.ptr, None, None, None))
     ms, wall = timed(ctx, step, steps * 5, warmup)
-    names = ["mm_mla_qprep", "mm_mla_attn", "mm_mla_combine"]
+    names = ["mm_mla_qprep", "mm_mla_attn", "mm_mla_combine", "mm_mla_uv"]
     prof = profile_kernels(ctx, step, 20, names)
     nbytes = B * L * (KVL + QKR) * 2 + 2 * NH * QKN * KVL * 2   # cache + W_UK + W_UV
     attn_bytes = B * L * (KVL + QKR) * 2

@@ -45,6 +45,8 @@ static const struct {
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
+    [K_MLA_UV] = {"mm_mla_uv", MOD_MLA},
+    [K_MLA_WPREP] = {"mm_mla_wprep", MOD_MLA},
     [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
 };
 

@@ -27,6 +27,8 @@ typedef enum {
     K_MLA_QPREP,
     K_MLA_ATTN,
     K_MLA_COMBINE,
+    K_MLA_UV,
+    K_MLA_WPREP,
     K_GEMM_BF16,
     K_COUNT
 } mm_kernel_id;

@@ -23,6 +23,8 @@ int mm_mla_init(mm_ctx *c, const mm_mla_config *cfg, int n_layers) {
     if (c->mla_ready) return mm_fail(MM_ERR_STATE, "mm_mla_init: already initialised");
     if (n_layers <= 0 || cfg->n_heads <= 0 || cfg->qk_nope_head_dim <= 0 || cfg->v_head_dim <= 0)
         return mm_fail(MM_ERR_INVALID, "mm_mla_init: non-positive dimension");
+    if (cfg->qk_nope_head_dim % 32)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_init: qk_nope_head_dim must be a multiple of 32");
     if (cfg->kv_lora_rank != MM_MLA_KVL || cfg->qk_rope_head_dim != MM_MLA_QKR)
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_init: kernels serve kv_lora_rank %d and "
                        "qk_rope_head_dim %d", MM_MLA_KVL, MM_MLA_QKR);
@@ -43,12 +45,17 @@ int mm_mla_load_layer(mm_ctx *c, int layer, const uint16_t *kv_b, unsigned flags
     int st = mm_set_device(c);
     if (st) return st;
     const mm_mla_config *g = &c->mla;
+    /* one pool per layer: kv_b as given, then W_UK^T per head [NH][KVL][QKN] */
     const size_t n = (size_t)g->n_heads * (g->qk_nope_head_dim + g->v_head_dim) * g->kv_lora_rank;
-    MM_HIP(hipMalloc((void **)&c->mla_kvb[layer], n * 2));
+    const size_t nt = (size_t)g->n_heads * g->kv_lora_rank * g->qk_nope_head_dim;
+    MM_HIP(hipMalloc((void **)&c->mla_kvb[layer], (n + nt) * 2));
     MM_HIP(hipMemcpyAsync(c->mla_kvb[layer], kv_b, n * 2,
                           (flags & MM_LOAD_DEVICE_PTRS) ? hipMemcpyDeviceToDevice
                                                         : hipMemcpyHostToDevice,
                           c->stream));
+    mm_mla_wprep_args wa = {c->mla_kvb[layer], c->mla_kvb[layer] + n, g->n_heads,
+                            g->qk_nope_head_dim, g->v_head_dim};
+    if ((st = mm_launch(c, K_MLA_WPREP, 1024, 1, 1, 256, 0, &wa))) return st;
     MM_HIP(hipStreamSynchronize(c->stream));
     return MM_OK;
 }
@@ -79,22 +86,29 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
     const size_t qa_b = qabs ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
     const size_t ml_b = (size_t)B * HG * nchunks * 32 * 4;
     const size_t po_b = (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
+    const size_t cl_b = clat ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
     char *ws;
     const size_t a1 = (qf_b + 255) & ~(size_t)255, a2 = (qa_b + 255) & ~(size_t)255;
-    const size_t a3 = (ml_b + 255) & ~(size_t)255;
-    if ((st = mm_workspace(c, a1 + a2 + a3 + po_b, (void **)&ws))) return st;
+    const size_t a3 = (ml_b + 255) & ~(size_t)255, a4 = (po_b + 255) & ~(size_t)255;
+    if ((st = mm_workspace(c, a1 + a2 + a3 + a4 + cl_b, (void **)&ws))) return st;
     uint16_t *qfrag = (uint16_t *)ws;
     if (!qabs) qabs = (float *)(ws + a1);
     float *part_ml = (float *)(ws + a1 + a2), *part_o = (float *)(ws + a1 + a2 + a3);
+    if (!clat) clat = (float *)(ws + a1 + a2 + a3 + a4);
 
-    mm_mla_qprep_args qa = {q, c->mla_kvb[layer], qabs, qfrag, B, NH, g->qk_nope_head_dim,
-                            g->v_head_dim, HG};
-    if ((st = mm_launch(c, K_MLA_QPREP, (unsigned)(HG * 16), (unsigned)B, 1, 256, 0, &qa))) return st;
+    const int QKN = g->qk_nope_head_dim;
+    const size_t nkvb = (size_t)NH * (QKN + g->v_head_dim) * MM_MLA_KVL;
+    mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, qfrag, B, NH, QKN, g->v_head_dim, HG};
+    if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVD / 64, (unsigned)(HG * 16),
+                        (unsigned)((B + 31) / 32), 256, 0, &qa)))
+        return st;
     mm_mla_attn_args aa = {qfrag, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
                            part_o, probs, kv_len, NH, HG, nchunks};
     if ((st = mm_launch(c, K_MLA_ATTN, (unsigned)nchunks, (unsigned)B, (unsigned)HG, 128, 0, &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks};
-    return mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, 1, 256, 0, &ca);
+    if ((st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, 1, 256, 0, &ca))) return st;
+    return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,
+                     (unsigned)((B + 31) / 32), 256, 0, &ca);
 }

@@ -205,11 +205,18 @@ typedef struct {
  * [qabs | q_pe] in MFMA A-operand order for the score MFMA. */
 typedef struct {
     const float *q;           /* [B, NH, QKN + QKR] */
-    const uint16_t *kv_b;     /* [NH * (QKN + VHD), KVL] bf16, head-interleaved */
+    const uint16_t *wukT;     /* [NH, KVL, QKN] bf16: W_UK per head, transposed */
     float *qabs;              /* [B, NH, KVL] */
     uint16_t *qfrag;          /* [B, HG, 2 (hi/lo), KC, 64 lanes, 8] bf16 */
     int B, NH, QKN, VHD, HG;
 } mm_mla_qprep_args;
+
+/* Load-time preparation of W_UK^T from the head-interleaved kv_b. */
+typedef struct {
+    const uint16_t *kv_b;
+    uint16_t *wukT;
+    int NH, QKN, VHD;
+} mm_mla_wprep_args;
 
 /* Flash-decoding partials: block (chunk, b, head group). */
 typedef struct {
@@ -226,14 +233,14 @@ typedef struct {
     int NH, HG, nchunks;
 } mm_mla_attn_args;
 
-/* Merge the chunk partials, normalise (clat), apply W_UV -> ctx. */
+/* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */
 typedef struct {
     const float *part_ml, *part_o;
     const uint16_t *kv_b;
     const int32_t *kv_lens;
     int kv_len;
     float *ctx;               /* [B, NH * VHD] */
-    float *clat;              /* [B, NH, KVL] or 0 */
+    float *clat;              /* [B, NH, KVL] (written by the merge, read by the W_UV product) */
     float *probs;             /* [B, NH, probs_stride]: scores in, probabilities out, or 0 */
     int probs_stride;
     int B, NH, QKN, VHD, HG, nchunks;

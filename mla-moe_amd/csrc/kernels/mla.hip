@@ -45,31 +45,113 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t *hi, uint16_t *lo) 
     *lo = bf16_rne(x - bf16_f32(h));
 }
 
-/* grid (HG * 16 head slots, B), 256 threads.  Head slots >= NH write zero
- * operands so a partial head group contributes nothing. */
-extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
-    const int hs = blockIdx.x, b = blockIdx.y;
-    const int hg = hs >> 4, hl = hs & 15;
-    const int QKR = MM_MLA_QKR;
-    const bool real = hs < a.NH;
-    const float *q = a.q + ((size_t)b * a.NH + (real ? hs : 0)) * (a.QKN + QKR);
-    const uint16_t *wuk = a.kv_b + (size_t)(real ? hs : 0) * (a.QKN + a.VHD) * KVL;
-    uint16_t *qf = a.qfrag + (size_t)(b * a.HG + hg) * 2 * KC * 64 * 8;
-    for (int e = threadIdx.x; e < KVD; e += blockDim.x) {
-        float v = 0.0f;
-        if (real) {
-            if (e < KVL) {
-                for (int d = 0; d < a.QKN; d++) v = __builtin_fmaf(q[d], bf16_f32(wuk[(size_t)d * KVL + e]), v);
-                a.qabs[((size_t)b * a.NH + hs) * KVL + e] = v;
-            } else {
-                v = q[a.QKN + (e - KVL)];
+/* One wave's share of a per-head GEMM on bf16 MFMA, Y[m, n] = sum_k
+ * X[m, k] W[n, k]: 32 rows of X (fp32, split into bf16 hi + lo so that the
+ * products carry fp32-level precision) against 16 rows of W (bf16, K
+ * contiguous).  Operand fragments come straight from memory: lane l holds
+ * row (l % 16), K values 8 (l / 16) .. +7 of a 32-wide K step.  Rows of X
+ * at or past mrows read row 0 (their results are not stored).  On return
+ * acc[t][i] = Y[16 t + 4 (l / 16) + i][l % 16]. */
+__device__ __forceinline__ void hl_gemm_32x16(const float *X, size_t xs, int mrows,
+                                              const uint16_t *W, size_t ws, int k_begin, int k_end,
+                                              f32x4 (&acc)[2]) {
+    constexpr int GB = 4;   /* K steps whose loads are issued together */
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int r16 = lane & 15, kq = 8 * (lane >> 4);
+    acc[0] = acc[1] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const float *xr[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int m = 16 * t + r16;
+        xr[t] = X + (size_t)(m < mrows ? m : 0) * xs + kq;
+    }
+    const uint16_t *wr = W + (size_t)r16 * ws + kq;
+    for (int k0 = k_begin; k0 < k_end; k0 += 32 * GB) {
+        u16x8 bw[GB];
+        f32x4 xv[GB][2][2];
+#pragma unroll
+        for (int g = 0; g < GB; g++) {
+            const int k = min(k0 + 32 * g, k_end - 32);   /* steps past the end: not used */
+            bw[g] = *(const u16x8 *)(wr + k);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                xv[g][t][0] = *(const f32x4 *)(xr[t] + k);
+                xv[g][t][1] = *(const f32x4 *)(xr[t] + k + 4);
             }
         }
-        uint16_t hi, lo;
-        split_bf16(v, &hi, &lo);
-        const int c = e >> 5, L = hl + 16 * ((e & 31) >> 3), j = e & 7;
-        qf[((size_t)(0 * KC + c) * 64 + L) * 8 + j] = hi;
-        qf[((size_t)(1 * KC + c) * 64 + L) * 8 + j] = lo;
+#pragma unroll
+        for (int g = 0; g < GB; g++) {
+            if (k0 + 32 * g >= k_end) break;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                u16x8 hi, lo;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint16_t h16, l16;
+                    split_bf16(xv[g][t][j >> 2][j & 3], &h16, &l16);
+                    hi[j] = h16;
+                    lo[j] = l16;
+                }
+                const bf16x8 b8 = __builtin_bit_cast(bf16x8, bw[g]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hi), b8, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lo), b8, acc[t], 0, 0, 0);
+            }
+        }
+    }
+}
+
+/* Absorbed queries, qabs[b, h, r] = sum_d q_nope[b, h, d] W_UK_h[d, r], as a
+ * per-head GEMM with W_UK_h kept transposed ([r][d], prepared at load
+ * time); then the bf16 hi/lo halves of [qabs | q_pe] in MFMA A-operand
+ * order for the score MFMA.  grid (KVD / 64 column slabs, HG * 16 head
+ * slots, ceil(B / 32)), 4 waves of 16 columns.  The last slab is q_pe (no
+ * product); head slots >= NH write zero operands so a partial head group
+ * contributes nothing. */
+extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
+    const int slab = blockIdx.x, hs = blockIdx.y, b0 = blockIdx.z * 32;
+    const int hg = hs >> 4, hl = hs & 15;
+    const int QKR = MM_MLA_QKR, QKN = a.QKN;
+    const bool real = hs < a.NH;
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int e = slab * 64 + 16 * wave + (lane & 15);     /* latent index of this lane */
+    const int mrows = min(32, a.B - b0);
+    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    if (real && slab < KVL / 64)
+        hl_gemm_32x16(a.q + ((size_t)b0 * a.NH + hs) * (QKN + QKR), (size_t)a.NH * (QKN + QKR), mrows,
+                      a.wukT + ((size_t)hs * KVL + slab * 64 + 16 * wave) * QKN, QKN, 0, QKN, acc);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int bb = 16 * t + 4 * (lane >> 4) + i;
+            if (bb >= mrows) continue;
+            const int b = b0 + bb;
+            float v = 0.0f;
+            if (real) {
+                if (e < KVL) {
+                    v = acc[t][i];
+                    a.qabs[((size_t)b * a.NH + hs) * KVL + e] = v;
+                } else {
+                    v = a.q[((size_t)b * a.NH + hs) * (QKN + QKR) + QKN + (e - KVL)];
+                }
+            }
+            uint16_t hi, lo;
+            split_bf16(v, &hi, &lo);
+            uint16_t *qf = a.qfrag + (size_t)(b * a.HG + hg) * 2 * KC * 64 * 8;
+            const int c = e >> 5, L = hl + 16 * ((e & 31) >> 3), j = e & 7;
+            qf[((size_t)(0 * KC + c) * 64 + L) * 8 + j] = hi;
+            qf[((size_t)(1 * KC + c) * 64 + L) * 8 + j] = lo;
+        }
+}
+
+/* Load-time: W_UK_h transposed, wukT[h][r][d] = kv_b[h (QKN + VHD) + d][r]. */
+extern "C" __global__ __launch_bounds__(256) void mm_mla_wprep(mm_mla_wprep_args a) {
+    const size_t n = (size_t)a.NH * KVL * a.QKN;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t d = i % a.QKN, r = (i / a.QKN) % KVL, h = i / ((size_t)a.QKN * KVL);
+        a.wukT[i] = a.kv_b[(h * (a.QKN + a.VHD) + d) * KVL + r];
     }
 }
 
@@ -220,50 +302,79 @@ extern "C" __global__ __launch_bounds__(128) void mm_mla_attn(mm_mla_attn_args a
     }
 }
 
-/* grid (NH, B), 256 threads. */
+/* Merge the chunk partials of (head h, sequence b): clat = sum_c w_c O_c / l
+ * with w_c = e^(m_c - m); also turns the debug scores into probabilities.
+ * grid (NH, B), 256 threads. */
 extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_args a) {
-    __shared__ float cl[KVL];
     __shared__ float wch[64];
     __shared__ float stat[2];
     const int h = blockIdx.x, b = blockIdx.y;
     const int hg = h >> 4, hl = h & 15;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
     const size_t pbase = (size_t)(b * a.HG + hg) * a.nchunks;
-    if (tid == 0) {
-        float mx = -INFINITY;
-        for (int c = 0; c < a.nchunks; c++) mx = fmaxf(mx, a.part_ml[(pbase + c) * 32 + hl]);
-        float ls = 0.0f;
-        for (int c = 0; c < a.nchunks; c++) {
-            const float mc = a.part_ml[(pbase + c) * 32 + hl];
-            const float wc = mc == -INFINITY ? 0.0f : __expf(mc - mx);
-            wch[c] = wc;
-            ls += a.part_ml[(pbase + c) * 32 + 16 + hl] * wc;
+    if (tid < MM_WAVE) {
+        /* chunk maxima and sums, one lane per chunk (nchunks <= 64) */
+        const bool ok = tid < a.nchunks;
+        const float mc = ok ? a.part_ml[(pbase + tid) * 32 + hl] : -INFINITY;
+        const float lc = ok ? a.part_ml[(pbase + tid) * 32 + 16 + hl] : 0.0f;
+        const float mx = wave_max(mc);
+        const float wc = mc == -INFINITY ? 0.0f : __expf(mc - mx);
+        const float ls = wave_sum(lc * wc);
+        if (ok) wch[tid] = wc;
+        if (tid == 0) {
+            stat[0] = mx;
+            stat[1] = ls;
         }
-        stat[0] = mx;
-        stat[1] = ls;
     }
     __syncthreads();
     const float mx = stat[0], inv = 1.0f / stat[1];
+    float *cl = a.clat + ((size_t)b * a.NH + h) * KVL;
     for (int r = tid; r < KVL; r += blockDim.x) {
         float o = 0.0f;
         for (int c = 0; c < a.nchunks; c++)
             o += wch[c] * a.part_o[((pbase + c) * 16 + hl) * KVL + r];
-        o *= inv;
-        cl[r] = o;
-        if (a.clat) a.clat[((size_t)b * a.NH + h) * KVL + r] = o;
+        cl[r] = o * inv;
     }
     if (a.probs) {
         float *pr = a.probs + ((size_t)b * a.NH + h) * a.probs_stride;
         for (int k = tid; k < L; k += blockDim.x) pr[k] = __expf(pr[k] - mx) * inv;
     }
-    __syncthreads();
-    const uint16_t *wuv = a.kv_b + ((size_t)h * (a.QKN + a.VHD) + a.QKN) * KVL;
-    for (int dv = wave; dv < a.VHD; dv += blockDim.x / 64) {
-        const uint16_t *row = wuv + (size_t)dv * KVL;
-        float acc = 0.0f;
-        for (int r = lane; r < KVL; r += 64) acc = __builtin_fmaf(cl[r], bf16_f32(row[r]), acc);
-        acc = wave_sum(acc);
-        if (lane == 0) a.ctx[((size_t)b * a.NH + h) * a.VHD + dv] = acc;
+}
+
+/* ctx[b, h, v] = sum_r W_UV_h[v, r] clat[b, h, r], a per-head GEMM on bf16
+ * MFMA (clat split hi/lo).  grid (ceil(VHD / 16), NH, ceil(B / 32)), 4 waves
+ * splitting K = KVL; the partial sums meet in LDS. */
+extern "C" __global__ __launch_bounds__(256) void mm_mla_uv(mm_mla_combine_args a) {
+    __shared__ f32x4 red[3][2][MM_WAVE];
+    const int vw = blockIdx.x * 16, h = blockIdx.y, b0 = blockIdx.z * 32;
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int mrows = min(32, a.B - b0);
+    const int nv = min(16, a.VHD - vw);
+    const uint16_t *wuv = a.kv_b + ((size_t)h * (a.QKN + a.VHD) + a.QKN + vw) * KVL;
+    f32x4 acc[2];
+    /* rows of W_UV past VHD: read row vw instead (results not stored) */
+    hl_gemm_32x16(a.clat + ((size_t)b0 * a.NH + h) * KVL, (size_t)a.NH * KVL, mrows,
+                  (lane & 15) < nv ? wuv : wuv - (size_t)(lane & 15) * KVL, KVL,
+                  wave * (KVL / 4), (wave + 1) * (KVL / 4), acc);
+    if (wave > 0) {
+        red[wave - 1][0][lane] = acc[0];
+        red[wave - 1][1][lane] = acc[1];
     }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; w++) {
+        acc[0] += red[w][0][lane];
+        acc[1] += red[w][1][lane];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int bb = 16 * t + 4 * (lane >> 4) + i;
+            if (bb < mrows && (lane & 15) < nv)
+                a.ctx[((size_t)(b0 + bb) * a.NH + h) * a.VHD + vw + (lane & 15)] = acc[t][i];
+        }
 }
