@@ -62,3 +62,35 @@ __device__ __forceinline__ float swiglu_f(float g, float u) {
  * ~2^-29 relative of a rounding boundary can differ from a correctly rounded
  * libm expf. */
 __device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+
+/* ---- direct-to-LDS loads and LDS reads the compiler does not track ---- */
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+/* 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (direct
+ * global -> LDS load, no VGPR staging). */
+__device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
+}
+
+/* LDS byte address of a __shared__ location. */
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
+}
+
+/* ds_read_b128 issued as inline assembly: the compiler's conservative
+ * "wait for every outstanding direct-to-LDS load before any LDS read" would
+ * otherwise drain the whole load ring every K step.  The caller orders the
+ * reads with explicit vmcnt waits and a barrier, and must follow them with
+ * lds_wait_regs() before using the results. */
+__device__ __forceinline__ i32x4 ds_read16(uint32_t addr) {
+    i32x4 r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+
+
+
+/* s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima). */
+#define VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))

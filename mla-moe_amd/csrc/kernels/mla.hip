@@ -10,15 +10,10 @@
  * sequence for all heads:
  *   mm_mla_qprep    qabs (fp32) and [qabs | q_pe] as a bf16 hi/lo pair in
  *                   MFMA operand order (x = hi + lo to ~2^-17 relative)
- *   mm_mla_attn     flash decoding over 512-key chunks: the 16 heads of a
- *                   head group are the M dimension of the MFMAs.  Per 16-key
- *                   sub-tile: S = Q . C^T on v_mfma_f32_16x16x32_bf16 (cache
- *                   rows loaded straight into B operands), online softmax in
- *                   registers, O += P . C_kv on v_mfma_f32_16x16x16bf16_1k
- *                   with the key-major B operand built by a per-wave LDS
- *                   transpose of the same cache rows.  Two waves per block,
- *                   merged in LDS into one partial per chunk.
- *   mm_mla_combine  merge the chunk partials, clat = O / l, ctx = W_UV . clat
+ *   mm_mla_attn     flash decoding over 512-key chunks, all 16 heads of a
+ *                   head group per MFMA (see the kernel)
+ *   mm_mla_combine  merge the chunk partials, clat = O / l
+ *   mm_mla_uv       ctx = W_UV . clat
  */
 #include "common.h"
 
@@ -29,8 +24,6 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 #define KVL MM_MLA_KVL
 #define KVD MM_MLA_KVD
 #define KC MM_MLA_KC
-#define SUB 16                    /* keys per sub-tile */
-#define CT_ROW 20                 /* u16 per transposed row: 16 keys + pad (conflict-free reads) */
 
 __device__ __forceinline__ uint16_t bf16_rne(float x) {
     uint32_t u = __float_as_uint(x);
@@ -166,139 +159,226 @@ __device__ __forceinline__ float grp16_sum(float v) {
     return v;
 }
 
-/* grid (nchunks, B, HG), 128 threads (2 waves); wave w handles keys
- * [chunk*512 + w*256, +256). */
-extern "C" __global__ __launch_bounds__(128) void mm_mla_attn(mm_mla_attn_args a) {
-    __shared__ __attribute__((aligned(16))) uint16_t qlds[2 * KC * 64 * 8];          /* 36 KB */
-    __shared__ __attribute__((aligned(16))) uint16_t ctlds[2][KVL * CT_ROW];        /* 40 KB */
-    __shared__ __attribute__((aligned(16))) uint16_t plds[2][2][16 * 16];           /* 2 KB */
-    __shared__ float mlds[2][32];
+/* Transposing LDS read (ds_read_b64_tr_b16) as inline assembly (the
+ * compiler does not track it; callers wait with lgkmcnt): within each
+ * 16-lane group, lane 4k + c supplies the address of 4 consecutive 16-bit
+ * values of row k (k, c = 0..3); lane i receives column i of the 4 rows,
+ * i.e. a row-major [4][16] block read as the B operand of
+ * v_mfma_f32_16x16x16bf16_1k. */
+__device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr) {
+    s16x4 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
 
+#define AW 4                      /* waves per attention block */
+#define KPW (MM_MLA_CHUNK / AW)   /* keys per wave */
+#define CROW_B 1056               /* bytes per LDS c_kv row: 1024 + 32 pad */
+#define TILE_B (16 * CROW_B + 16 * 128)   /* 16 keys: c_kv rows, then the k_pe parts */
+
+/* grid (nchunks, B, HG), AW waves; wave w handles keys [chunk * 512 + w * KPW,
+ * + KPW) in 16-key sub-tiles, each staged into LDS by direct global -> LDS
+ * loads one sub-tile ahead of its use (two LDS stages per wave):
+ *   S^T[key][head] = C[key] . Q[head]^T on v_mfma_f32_16x16x32_bf16 with the
+ *     cache rows as the A operand and Q (hi and lo halves, in registers) as
+ *     B, so lane (head = l % 16, l / 16) holds the scores of keys
+ *     4 (l / 16) .. +3;
+ *   online softmax per head (in-lane and across the 4 lane groups);
+ *   P[head][keys] is then already in A-operand order for
+ *   O[head][r] += P . C_kv on v_mfma_f32_16x16x16bf16_1k, whose B operand
+ *   ([keys][r] row-major) comes from the same LDS rows by transposing reads.
+ * The AW waves' partial states merge in LDS into one partial per chunk.
+ * Dynamic LDS: AW * 2 * TILE_B bytes. */
+extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_attn_args a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
     const int chunk = blockIdx.x, b = blockIdx.y, hg = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, kl = lane & 15;
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
+    uint8_t *wt0 = alds + (size_t)w * 2 * TILE_B;     /* this wave's two stages */
 
-    {   /* Q operands for this (b, head group) into LDS */
+    /* Q operands (hi, lo) in registers */
+    bf16x8 qh[KC], ql[KC];
+    {
         const u16x8 *src = (const u16x8 *)(a.qfrag + (size_t)(b * a.HG + hg) * 2 * KC * 64 * 8);
-        u16x8 *dst = (u16x8 *)qlds;
-        for (int i = tid; i < 2 * KC * 64; i += 128) dst[i] = src[i];
-    }
-    __syncthreads();
-
-    float m[4], l[4];
-    f32x4 O[KVL / 16];
 #pragma unroll
-    for (int i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
+        for (int c = 0; c < KC; c++) {
+            qh[c] = __builtin_bit_cast(bf16x8, src[(0 * KC + c) * 64 + lane]);
+            ql[c] = __builtin_bit_cast(bf16x8, src[(1 * KC + c) * 64 + lane]);
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;        /* softmax state of head kl */
+    f32x4 O[KVL / 16];
 #pragma unroll
     for (int nb = 0; nb < KVL / 16; nb++) O[nb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    uint16_t *ct = ctlds[w];
-    const int kbeg = chunk * MM_MLA_CHUNK + w * (MM_MLA_CHUNK / 2);
-    const int kend = min(kbeg + MM_MLA_CHUNK / 2, L);
-    const uint16_t *cseq = a.cache + (size_t)b * a.seq_stride * KVD;
-    for (int k0 = kbeg; k0 < kend; k0 += SUB) {
-        const int key = k0 + kl;
-        const bool valid = key < L;
-        const uint16_t *rp = cseq + (size_t)(valid ? key : k0) * KVD + 8 * g;
-        bf16x8 bfr[KC];
+    const int kbeg = chunk * MM_MLA_CHUNK + w * KPW;
+    const int kend = min(kbeg + KPW, L);
+    const uint8_t *cseq = (const uint8_t *)(a.cache + (size_t)b * a.seq_stride * KVD);
+    /* sub-tile at key k0 -> stage st: row p's c_kv (1 KB, one load per lane
+     * of 16 B) at p * CROW_B; the k_pe parts (128 B per row) of rows 0..7 and
+     * 8..15 as two 1 KB pieces after the c_kv rows.  Rows past L load row
+     * L - 1 (masked in the softmax). */
+    auto issue = [&](int st, int k0) {
+        uint8_t *t = wt0 + st * TILE_B;
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            u16x8 v = *(const u16x8 *)(rp + 32 * c);
-            if (!valid) v = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-            bfr[c] = __builtin_bit_cast(bf16x8, v);
+        for (int p = 0; p < 16; p++) {
+            const int key = min(k0 + p, L - 1);
+            lds_dma16(cseq + (size_t)key * KVD * 2 + lane * 16, t + p * CROW_B);
         }
-        /* S[head 4g+i][key kl] */
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int key = min(k0 + 8 * p + (lane >> 3), L - 1);
+            lds_dma16(cseq + (size_t)key * KVD * 2 + KVL * 2 + (lane & 7) * 16,
+                      t + 16 * CROW_B + p * 1024);
+        }
+    };
+
+    auto process = [&](int st, int k0) {
+        const uint32_t t = lds_addr(wt0 + st * TILE_B);
+        /* S^T[key 4g+i][head kl]: A = cache row kl, latent 32 c + 8 g .. +7 */
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const bf16x8 qh = __builtin_bit_cast(bf16x8, *(const u16x8 *)&qlds[((0 * KC + c) * 64 + lane) * 8]);
-            const bf16x8 ql = __builtin_bit_cast(bf16x8, *(const u16x8 *)&qlds[((1 * KC + c) * 64 + lane) * 8]);
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, bfr[c], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql, bfr[c], s, 0, 0, 0);
+        for (int c0 = 0; c0 < KC; c0 += 6) {
+            i32x4 af[6];
+#pragma unroll
+            for (int c = c0; c < c0 + 6; c++)
+                af[c - c0] = c < KVL / 32 ? ds_read16(t + kl * CROW_B + (32 * c + 8 * g) * 2)
+                                          : ds_read16(t + 16 * CROW_B + kl * 128 + (32 * (c - KVL / 32) + 8 * g) * 2);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]),
+                         "+v"(af[4]), "+v"(af[5]));
+#pragma unroll
+            for (int c = c0; c < c0 + 6; c++) {
+                const bf16x8 ab = __builtin_bit_cast(bf16x8, af[c - c0]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[c], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[c], s, 0, 0, 0);
+            }
         }
-        float p[4], cr[4];
+        const int head = hg * 16 + kl;
+        float sv[4];
+        float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float sv = valid ? s[i] * a.scale : -INFINITY;
-            const int head = hg * 16 + 4 * g + i;
-            if (a.scores && valid && head < a.NH)
-                a.scores[((size_t)b * a.NH + head) * a.probs_stride + key] = sv;
-            const float mnew = fmaxf(m[i], grp16_max(sv));
-            cr[i] = m[i] == -INFINITY ? 0.0f : __expf(m[i] - mnew);
-            p[i] = sv == -INFINITY ? 0.0f : __expf(sv - mnew);
-            l[i] = l[i] * cr[i] + grp16_sum(p[i]);
-            m[i] = mnew;
+            const int key = k0 + 4 * g + i;
+            sv[i] = key < kend ? s[i] * a.scale : -INFINITY;
+            if (a.scores && key < kend && head < a.NH)
+                a.scores[((size_t)b * a.NH + head) * a.probs_stride + key] = sv[i];
+            mx = fmaxf(mx, sv[i]);
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, MM_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, MM_WAVE));
+        const float mnew = fmaxf(m, mx);
+        const float cr = m == -INFINITY ? 0.0f : __expf(m - mnew);
+        float p[4], ps = 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < KVL / 16; nb++)
+        for (int i = 0; i < 4; i++) {
+            p[i] = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - mnew);
+            ps += p[i];
+        }
+        ps += __shfl_xor(ps, 16, MM_WAVE);
+        ps += __shfl_xor(ps, 32, MM_WAVE);
+        l = l * cr + ps;
+        m = mnew;
+        /* rescale O rows: lane (r, g) holds heads 4g + i, whose factor sits
+         * in lane 4g + i */
 #pragma unroll
-            for (int i = 0; i < 4; i++) O[nb][i] *= cr[i];
-        /* P (hi/lo) as [head][key]; the sub-tile's c_kv transposed [r][key] */
+        for (int i = 0; i < 4; i++) {
+            const float ci = __shfl(cr, 4 * g + i, MM_WAVE);
+#pragma unroll
+            for (int nb = 0; nb < KVL / 16; nb++) O[nb][i] *= ci;
+        }
+        /* P[head kl][keys 4g .. 4g+3] as bf16 hi/lo A operands */
+        s16x4 ph, pl;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             uint16_t hi, lo;
             split_bf16(p[i], &hi, &lo);
-            plds[w][0][(4 * g + i) * 16 + kl] = hi;
-            plds[w][1][(4 * g + i) * 16 + kl] = lo;
+            ph[i] = (short)hi;
+            pl[i] = (short)lo;
         }
+        /* O[head][r] += P . C_kv; transposing reads: lane 4k + c of group g
+         * reads row 4g + k, columns 16 nb + 4c .. +3 */
+        const uint32_t tb = t + (4 * g + (kl >> 2)) * CROW_B + 8 * (kl & 3);
 #pragma unroll
-        for (int c = 0; c < KVL / 32; c++) {
-            const u16x8 v = __builtin_bit_cast(u16x8, bfr[c]);
+        for (int nb0 = 0; nb0 < KVL / 16; nb0 += 8) {
+            s16x4 bv[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) ct[(32 * c + 8 * g + j) * CT_ROW + kl] = v[j];
+            for (int j = 0; j < 8; j++) bv[j] = ds_read_tr16(tb + 32 * (nb0 + j));
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]),
+                         "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]), "+v"(bv[7]));
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                O[nb0 + j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, bv[j], O[nb0 + j], 0, 0, 0);
+                O[nb0 + j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, bv[j], O[nb0 + j], 0, 0, 0);
+            }
         }
-        /* O[head][r] += P[head][keys] . C[keys][r]  (K = 16 keys, 4 per lane) */
-        const s16x4 ph = *(const s16x4 *)&plds[w][0][kl * 16 + 4 * g];
-        const s16x4 pl = *(const s16x4 *)&plds[w][1][kl * 16 + 4 * g];
+    };
+    if (kbeg < kend) {
+        issue(0, kbeg);
+        int st = 0;
+        for (int k0 = kbeg; k0 < kend; k0 += 16, st ^= 1) {
+            VMCNT_WAIT(0);                      /* this sub-tile's rows are in LDS */
+            __builtin_amdgcn_sched_barrier(0);
+            if (k0 + 16 < kend) issue(st ^ 1, k0 + 16);   /* the other stage's reads are done */
+            __builtin_amdgcn_sched_barrier(0);
+            process(st, k0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    VMCNT_WAIT(0);
+
+    /* merge the waves: waves 1.. park O, m, l in LDS (over the staging area,
+     * free after the barrier); wave 0 merges */
+    __syncthreads();
+    float *ob = (float *)alds;                       /* [AW-1][16 heads][KVL] */
+    float *mlb = ob + (AW - 1) * 16 * KVL;           /* [AW-1][2][16] */
+    if (w > 0) {
+        float *o = ob + (size_t)(w - 1) * 16 * KVL;
+#pragma unroll
+        for (int nb = 0; nb < KVL / 16; nb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[(4 * g + i) * KVL + nb * 16 + kl] = O[nb][i];
+        if (g == 0) {
+            mlb[(w - 1) * 32 + kl] = m;
+            mlb[(w - 1) * 32 + 16 + kl] = l;
+        }
+    }
+    __syncthreads();
+    if (w != 0) return;
+    /* per head (lane kl): merged max and each part's weight */
+    float mm = m;
+#pragma unroll
+    for (int j = 0; j < AW - 1; j++) mm = fmaxf(mm, mlb[j * 32 + kl]);
+    float wt[AW];
+    wt[0] = m == -INFINITY ? 0.0f : __expf(m - mm);
+    float lsum = l * wt[0];
+#pragma unroll
+    for (int j = 0; j < AW - 1; j++) {
+        const float mj = mlb[j * 32 + kl];
+        wt[j + 1] = mj == -INFINITY ? 0.0f : __expf(mj - mm);
+        lsum += mlb[j * 32 + 16 + kl] * wt[j + 1];
+    }
+    const size_t pidx = ((size_t)(b * a.HG + hg) * a.nchunks + chunk);
+    if (g == 0) {
+        a.part_ml[pidx * 32 + kl] = mm;
+        a.part_ml[pidx * 32 + 16 + kl] = lsum;
+    }
+    float *po = a.part_o + pidx * 16 * KVL;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float wi[AW];
+#pragma unroll
+        for (int j = 0; j < AW; j++) wi[j] = __shfl(wt[j], 4 * g + i, MM_WAVE);
 #pragma unroll
         for (int nb = 0; nb < KVL / 16; nb++) {
-            const s16x4 bv = *(const s16x4 *)&ct[(nb * 16 + kl) * CT_ROW + 4 * g];
-            O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, bv, O[nb], 0, 0, 0);
-            O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, bv, O[nb], 0, 0, 0);
+            const int idx = (4 * g + i) * KVL + nb * 16 + kl;
+            float v = O[nb][i] * wi[0];
+#pragma unroll
+            for (int j = 0; j < AW - 1; j++) v += ob[(size_t)j * 16 * KVL + idx] * wi[j + 1];
+            po[idx] = v;
         }
-    }
-
-    /* merge the two waves: wave 1 parks its state in LDS, wave 0 merges */
-    __syncthreads();
-    float *ob = (float *)ctlds;   /* 16 x 512 fp32 = 32 KB fits in the 40 KB transpose area */
-    if (w == 1) {
-#pragma unroll
-        for (int nb = 0; nb < KVL / 16; nb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) ob[(4 * g + i) * KVL + nb * 16 + kl] = O[nb][i];
-        if (kl == 0)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                mlds[0][4 * g + i] = m[i];
-                mlds[1][4 * g + i] = l[i];
-            }
-    }
-    __syncthreads();
-    if (w == 0) {
-        const size_t pidx = ((size_t)(b * a.HG + hg) * a.nchunks + chunk);
-        float *po = a.part_o + pidx * 16 * KVL;
-        float w0[4], w1[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hrow = 4 * g + i;
-            const float m1 = mlds[0][hrow], l1 = mlds[1][hrow];
-            const float mm = fmaxf(m[i], m1);
-            w0[i] = m[i] == -INFINITY ? 0.0f : __expf(m[i] - mm);
-            w1[i] = m1 == -INFINITY ? 0.0f : __expf(m1 - mm);
-            if (kl == 0) {
-                a.part_ml[pidx * 32 + hrow] = mm;
-                a.part_ml[pidx * 32 + 16 + hrow] = l[i] * w0[i] + l1 * w1[i];
-            }
-        }
-#pragma unroll
-        for (int nb = 0; nb < KVL / 16; nb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int idx = (4 * g + i) * KVL + nb * 16 + kl;
-                po[idx] = O[nb][i] * w0[i] + ob[idx] * w1[i];
-            }
     }
 }
 

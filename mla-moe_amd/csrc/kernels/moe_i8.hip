@@ -30,7 +30,7 @@
  */
 #include "router.h"
 
-typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef i32x4 v4i;
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -282,35 +282,6 @@ extern "C" __global__ __launch_bounds__(MM_I8_RT_WAVES * MM_WAVE) void mm_i8_rou
 
 /* ---- streaming grouped GEMM (decode) ------------------------------------------- */
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-/* 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (direct
- * global -> LDS load, no VGPR staging). */
-__device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
-    __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
-}
-
-/* LDS byte address of a __shared__ location. */
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const lds_void_t *)p;
-}
-
-/* ds_read_b128 issued as inline assembly: the compiler's conservative
- * "wait for every outstanding direct-to-LDS load before any LDS read" would
- * otherwise drain the whole load ring every K step.  The caller orders the
- * reads with explicit vmcnt waits and a barrier, and must follow them with
- * lds_wait_regs() before using the results. */
-__device__ __forceinline__ v4i ds_read16(uint32_t addr) {
-    v4i r;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
-    return r;
-}
-
-
-
-/* s_waitcnt vmcnt(n) only (expcnt and lgkmcnt left at their maxima). */
-#define VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
