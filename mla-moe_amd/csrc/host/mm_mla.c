@@ -82,28 +82,26 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
     if (st) return st;
     const mm_mla_config *g = &c->mla;
     const int NH = g->n_heads, HG = (NH + 15) / 16;
-    const size_t qf_b = (size_t)B * HG * 2 * MM_MLA_KC * 64 * 8 * 2;
     const size_t qa_b = qabs ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
     const size_t ml_b = (size_t)B * HG * nchunks * 32 * 4;
     const size_t po_b = (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
     const size_t cl_b = clat ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
     char *ws;
-    const size_t a1 = (qf_b + 255) & ~(size_t)255, a2 = (qa_b + 255) & ~(size_t)255;
+    const size_t a1 = 0, a2 = (qa_b + 255) & ~(size_t)255;
     const size_t a3 = (ml_b + 255) & ~(size_t)255, a4 = (po_b + 255) & ~(size_t)255;
     if ((st = mm_workspace(c, a1 + a2 + a3 + a4 + cl_b, (void **)&ws))) return st;
-    uint16_t *qfrag = (uint16_t *)ws;
     if (!qabs) qabs = (float *)(ws + a1);
     float *part_ml = (float *)(ws + a1 + a2), *part_o = (float *)(ws + a1 + a2 + a3);
     if (!clat) clat = (float *)(ws + a1 + a2 + a3 + a4);
 
     const int QKN = g->qk_nope_head_dim;
     const size_t nkvb = (size_t)NH * (QKN + g->v_head_dim) * MM_MLA_KVL;
-    mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, qfrag, B, NH, QKN, g->v_head_dim, HG};
-    if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVD / 64, (unsigned)(HG * 16),
-                        (unsigned)((B + 31) / 32), 256, 0, &qa)))
+    mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, B, NH, QKN};
+    if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVL / 64, (unsigned)NH, (unsigned)((B + 31) / 32), 256,
+                        0, &qa)))
         return st;
-    mm_mla_attn_args aa = {qfrag, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
-                           part_o, probs, kv_len, NH, HG, nchunks};
+    mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
+                           part_o, probs, kv_len, NH, HG, nchunks, QKN};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)4 * 2 * (16 * 1056 + 16 * 128);

@@ -201,14 +201,12 @@ typedef struct {
 #define MM_MLA_KC (MM_MLA_KVD / 32) /* 32-wide latent chunks of one cache row */
 #define MM_MLA_CHUNK 512          /* keys per attention block (2 waves x 256) */
 
-/* qabs = q_nope . W_UK per head, plus the bf16 hi/lo halves of
- * [qabs | q_pe] in MFMA A-operand order for the score MFMA. */
+/* qabs = q_nope . W_UK per head. */
 typedef struct {
     const float *q;           /* [B, NH, QKN + QKR] */
     const uint16_t *wukT;     /* [NH, KVL, QKN] bf16: W_UK per head, transposed */
     float *qabs;              /* [B, NH, KVL] */
-    uint16_t *qfrag;          /* [B, HG, 2 (hi/lo), KC, 64 lanes, 8] bf16 */
-    int B, NH, QKN, VHD, HG;
+    int B, NH, QKN;
 } mm_mla_qprep_args;
 
 /* Load-time preparation of W_UK^T from the head-interleaved kv_b. */
@@ -220,7 +218,8 @@ typedef struct {
 
 /* Flash-decoding partials: block (chunk, b, head group). */
 typedef struct {
-    const uint16_t *qfrag;    /* as above */
+    const float *qabs;        /* [B, NH, KVL] */
+    const float *q;           /* [B, NH, QKN + QKR] (the q_pe part) */
     const uint16_t *cache;    /* [B, seq_stride, KVD] bf16 */
     const int32_t *kv_lens;   /* [B] or 0 */
     int kv_len;               /* used when kv_lens == 0 */
@@ -230,7 +229,7 @@ typedef struct {
     float *part_o;            /* [B, HG, nchunks, 16, KVL] unnormalised */
     float *scores;            /* [B, NH, probs_stride] scaled scores (debug) or 0 */
     int probs_stride;
-    int NH, HG, nchunks;
+    int NH, HG, nchunks, QKN;
 } mm_mla_attn_args;
 
 /* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */

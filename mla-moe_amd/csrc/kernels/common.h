@@ -89,6 +89,13 @@ __device__ __forceinline__ i32x4 ds_read16(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
     return r;
 }
+/* As ds_read16 at addr + off, with off (a constant after unrolling,
+ * < 65536) in the instruction's offset field. */
+__device__ __forceinline__ i32x4 ds_read16(uint32_t addr, int off) {
+    i32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off));
+    return r;
+}
 
 
 

@@ -8,8 +8,9 @@
  *   ctx      = W_UV . clat                                     (run.c:460)
  * Here the latent cache (bf16, [B, L, 576] = c_kv | k_pe) is read once per
  * sequence for all heads:
- *   mm_mla_qprep    qabs (fp32) and [qabs | q_pe] as a bf16 hi/lo pair in
- *                   MFMA operand order (x = hi + lo to ~2^-17 relative)
+ *   mm_mla_qprep    qabs (fp32), a per-head GEMM on bf16 MFMA; q is split
+ *                   into bf16 hi + lo halves (x = hi + lo to ~2^-17 relative)
+ *                   wherever an fp32 operand meets a bf16 MFMA
  *   mm_mla_attn     flash decoding over 512-key chunks, all 16 heads of a
  *                   head group per MFMA (see the kernel)
  *   mm_mla_combine  merge the chunk partials, clat = O / l
@@ -95,46 +96,24 @@ __device__ __forceinline__ void hl_gemm_32x16(const float *X, size_t xs, int mro
 
 /* Absorbed queries, qabs[b, h, r] = sum_d q_nope[b, h, d] W_UK_h[d, r], as a
  * per-head GEMM with W_UK_h kept transposed ([r][d], prepared at load
- * time); then the bf16 hi/lo halves of [qabs | q_pe] in MFMA A-operand
- * order for the score MFMA.  grid (KVD / 64 column slabs, HG * 16 head
- * slots, ceil(B / 32)), 4 waves of 16 columns.  The last slab is q_pe (no
- * product); head slots >= NH write zero operands so a partial head group
- * contributes nothing. */
+ * time).  grid (KVL / 64 column slabs, NH, ceil(B / 32)), 4 waves of 16
+ * columns. */
 extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
-    const int slab = blockIdx.x, hs = blockIdx.y, b0 = blockIdx.z * 32;
-    const int hg = hs >> 4, hl = hs & 15;
+    const int slab = blockIdx.x, h = blockIdx.y, b0 = blockIdx.z * 32;
     const int QKR = MM_MLA_QKR, QKN = a.QKN;
-    const bool real = hs < a.NH;
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int e = slab * 64 + 16 * wave + (lane & 15);     /* latent index of this lane */
     const int mrows = min(32, a.B - b0);
-    f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    if (real && slab < KVL / 64)
-        hl_gemm_32x16(a.q + ((size_t)b0 * a.NH + hs) * (QKN + QKR), (size_t)a.NH * (QKN + QKR), mrows,
-                      a.wukT + ((size_t)hs * KVL + slab * 64 + 16 * wave) * QKN, QKN, 0, QKN, acc);
+    f32x4 acc[2];
+    hl_gemm_32x16(a.q + ((size_t)b0 * a.NH + h) * (QKN + QKR), (size_t)a.NH * (QKN + QKR), mrows,
+                  a.wukT + ((size_t)h * KVL + slab * 64 + 16 * wave) * QKN, QKN, 0, QKN, acc);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int bb = 16 * t + 4 * (lane >> 4) + i;
-            if (bb >= mrows) continue;
-            const int b = b0 + bb;
-            float v = 0.0f;
-            if (real) {
-                if (e < KVL) {
-                    v = acc[t][i];
-                    a.qabs[((size_t)b * a.NH + hs) * KVL + e] = v;
-                } else {
-                    v = a.q[((size_t)b * a.NH + hs) * (QKN + QKR) + QKN + (e - KVL)];
-                }
-            }
-            uint16_t hi, lo;
-            split_bf16(v, &hi, &lo);
-            uint16_t *qf = a.qfrag + (size_t)(b * a.HG + hg) * 2 * KC * 64 * 8;
-            const int c = e >> 5, L = hl + 16 * ((e & 31) >> 3), j = e & 7;
-            qf[((size_t)(0 * KC + c) * 64 + L) * 8 + j] = hi;
-            qf[((size_t)(1 * KC + c) * 64 + L) * 8 + j] = lo;
+            if (bb < mrows) a.qabs[((size_t)(b0 + bb) * a.NH + h) * KVL + e] = acc[t][i];
         }
 }
 
@@ -159,15 +138,16 @@ __device__ __forceinline__ float grp16_sum(float v) {
     return v;
 }
 
-/* Transposing LDS read (ds_read_b64_tr_b16) as inline assembly (the
- * compiler does not track it; callers wait with lgkmcnt): within each
+/* Transposing LDS read (ds_read_b64_tr_b16) at addr + off (off a constant
+ * after unrolling) as inline assembly (the compiler does not track it;
+ * callers wait with lgkmcnt): within each
  * 16-lane group, lane 4k + c supplies the address of 4 consecutive 16-bit
  * values of row k (k, c = 0..3); lane i receives column i of the 4 rows,
  * i.e. a row-major [4][16] block read as the B operand of
  * v_mfma_f32_16x16x16bf16_1k. */
-__device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr) {
+__device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr, int off) {
     s16x4 r;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off));
     return r;
 }
 
@@ -175,6 +155,14 @@ __device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr) {
 #define KPW (MM_MLA_CHUNK / AW)   /* keys per wave */
 #define CROW_B 1056               /* bytes per LDS c_kv row: 1024 + 32 pad */
 #define TILE_B (16 * CROW_B + 16 * 128)   /* 16 keys: c_kv rows, then the k_pe parts */
+#define OROW (KVL + 4)            /* floats per head row of the merge buffer */
+/* Rescaling is lazy: a head's running maximum m moves only when a score
+ * exceeds it by more than RESCALE_TAU, so exp(s - m) <= e^RESCALE_TAU and the
+ * accumulator is rescaled on few sub-tiles.  The final O / l is the same
+ * quantity for any m. */
+#define RESCALE_TAU 8.0f
+static_assert((AW * 16 * OROW + AW * 32) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
+static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
 /* grid (nchunks, B, HG), AW waves; wave w handles keys [chunk * 512 + w * KPW,
  * + KPW) in 16-key sub-tiles, each staged into LDS by direct global -> LDS
@@ -183,12 +171,13 @@ __device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr) {
  *     cache rows as the A operand and Q (hi and lo halves, in registers) as
  *     B, so lane (head = l % 16, l / 16) holds the scores of keys
  *     4 (l / 16) .. +3;
- *   online softmax per head (in-lane and across the 4 lane groups);
+ *   online softmax per head with lazy rescaling; the sums l stay per lane
+ *     (4 keys each) until the merge;
  *   P[head][keys] is then already in A-operand order for
  *   O[head][r] += P . C_kv on v_mfma_f32_16x16x16bf16_1k, whose B operand
  *   ([keys][r] row-major) comes from the same LDS rows by transposing reads.
  * The AW waves' partial states merge in LDS into one partial per chunk.
- * Dynamic LDS: AW * 2 * TILE_B bytes. */
+ * Dynamic LDS: AW * 2 * TILE_B bytes (the merge reuses it). */
 extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_attn_args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
     const int chunk = blockIdx.x, b = blockIdx.y, hg = blockIdx.z;
@@ -197,22 +186,6 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
     const int g = lane >> 4, kl = lane & 15;
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
     uint8_t *wt0 = alds + (size_t)w * 2 * TILE_B;     /* this wave's two stages */
-
-    /* Q operands (hi, lo) in registers */
-    bf16x8 qh[KC], ql[KC];
-    {
-        const u16x8 *src = (const u16x8 *)(a.qfrag + (size_t)(b * a.HG + hg) * 2 * KC * 64 * 8);
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            qh[c] = __builtin_bit_cast(bf16x8, src[(0 * KC + c) * 64 + lane]);
-            ql[c] = __builtin_bit_cast(bf16x8, src[(1 * KC + c) * 64 + lane]);
-        }
-    }
-
-    float m = -INFINITY, l = 0.0f;        /* softmax state of head kl */
-    f32x4 O[KVL / 16];
-#pragma unroll
-    for (int nb = 0; nb < KVL / 16; nb++) O[nb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
     const int kbeg = chunk * MM_MLA_CHUNK + w * KPW;
     const int kend = min(kbeg + KPW, L);
@@ -225,61 +198,156 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
         uint8_t *t = wt0 + st * TILE_B;
 #pragma unroll
         for (int p = 0; p < 16; p++) {
-            const int key = min(k0 + p, L - 1);
-            lds_dma16(cseq + (size_t)key * KVD * 2 + lane * 16, t + p * CROW_B);
+            const int key = __builtin_amdgcn_readfirstlane(min(k0 + p, L - 1));
+            lds_dma16(cseq + (uint32_t)(key * KVD * 2) + lane * 16, t + p * CROW_B);
         }
 #pragma unroll
         for (int p = 0; p < 2; p++) {
             const int key = min(k0 + 8 * p + (lane >> 3), L - 1);
-            lds_dma16(cseq + (size_t)key * KVD * 2 + KVL * 2 + (lane & 7) * 16,
+            lds_dma16(cseq + (uint32_t)(key * KVD * 2 + KVL * 2 + (lane & 7) * 16),
                       t + 16 * CROW_B + p * 1024);
         }
     };
+    if (kbeg < kend) issue(0, kbeg);
 
-    auto process = [&](int st, int k0) {
-        const uint32_t t = lds_addr(wt0 + st * TILE_B);
-        /* S^T[key 4g+i][head kl]: A = cache row kl, latent 32 c + 8 g .. +7 */
+    /* Q operands in registers: lane (head kl, g) holds [qabs | q_pe] of its
+     * head, latent 32 c + 8 g .. +7, split into bf16 hi + lo; head slots
+     * past NH are zero */
+    bf16x8 qh[KC], ql[KC];
+    {
+        const int qhd = hg * 16 + kl;
+        const bool real = qhd < a.NH;
+        const float *qa = a.qabs + ((size_t)b * a.NH + (real ? qhd : 0)) * KVL;
+        const float *qp = a.q + ((size_t)b * a.NH + (real ? qhd : 0)) * (a.QKN + MM_MLA_QKR) + a.QKN;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const float *src = c < KVL / 32 ? qa + 32 * c + 8 * g : qp + 32 * (c - KVL / 32) + 8 * g;
+            const f32x4 x0 = *(const f32x4 *)src, x1 = *(const f32x4 *)(src + 4);
+            u16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint16_t h16, l16;
+                split_bf16(real ? (j < 4 ? x0[j & 3] : x1[j & 3]) : 0.0f, &h16, &l16);
+                hi[j] = h16;
+                lo[j] = l16;
+            }
+            qh[c] = __builtin_bit_cast(bf16x8, hi);
+            ql[c] = __builtin_bit_cast(bf16x8, lo);
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;        /* head kl: running max; this lane's share of the sum */
+    f32x4 O[KVL / 16];
+#pragma unroll
+    for (int nb = 0; nb < KVL / 16; nb++) O[nb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto read_a = [&](uint32_t t, int c) -> i32x4 {
+        return c < KVL / 32 ? ds_read16(t + kl * CROW_B + 16 * g, 64 * c)
+                            : ds_read16(t + 16 * CROW_B + kl * 128 + 16 * g, 64 * (c - KVL / 32));
+    };
+
+    /* S^T[key 4g+i][head kl] for the sub-tile at LDS address t: A = cache
+     * row kl, latent 32 c + 8 g .. +7; LDS reads run one batch of 6 ahead of
+     * the MFMAs.  Returns the scaled scores, -inf past kend. */
+    auto score = [&](uint32_t t, int k0, float *sv) {
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+        i32x4 af[2][6];
 #pragma unroll
-        for (int c0 = 0; c0 < KC; c0 += 6) {
-            i32x4 af[6];
+        for (int c = 0; c < 6; c++) af[0][c] = read_a(t, c);
 #pragma unroll
-            for (int c = c0; c < c0 + 6; c++)
-                af[c - c0] = c < KVL / 32 ? ds_read16(t + kl * CROW_B + (32 * c + 8 * g) * 2)
-                                          : ds_read16(t + 16 * CROW_B + kl * 128 + (32 * (c - KVL / 32) + 8 * g) * 2);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]),
-                         "+v"(af[4]), "+v"(af[5]));
+        for (int bt = 0; bt < KC / 6; bt++) {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[bt & 1][0]), "+v"(af[bt & 1][1]), "+v"(af[bt & 1][2]),
+                         "+v"(af[bt & 1][3]), "+v"(af[bt & 1][4]), "+v"(af[bt & 1][5]));
+            if (bt + 1 < KC / 6) {
 #pragma unroll
-            for (int c = c0; c < c0 + 6; c++) {
-                const bf16x8 ab = __builtin_bit_cast(bf16x8, af[c - c0]);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[c], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[c], s, 0, 0, 0);
+                for (int c = 0; c < 6; c++) af[(bt + 1) & 1][c] = read_a(t, 6 * (bt + 1) + c);
+            }
+#pragma unroll
+            for (int c = 0; c < 6; c++) {
+                const bf16x8 ab = __builtin_bit_cast(bf16x8, af[bt & 1][c]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[6 * bt + c], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[6 * bt + c], s, 0, 0, 0);
             }
         }
         const int head = hg * 16 + kl;
-        float sv[4];
-        float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int key = k0 + 4 * g + i;
             sv[i] = key < kend ? s[i] * a.scale : -INFINITY;
             if (a.scores && key < kend && head < a.NH)
                 a.scores[((size_t)b * a.NH + head) * a.probs_stride + key] = sv[i];
-            mx = fmaxf(mx, sv[i]);
         }
+    };
+    /* P = e^(s - m) into the sums and O[head][r] += P . C_kv.  P[head kl][keys
+     * 4g .. 4g+3] is a bf16 hi/lo pair of A operands; the B operands come by
+     * transposing reads (lane 4k + c of group g reads row 4g + k, columns
+     * 16 nb + 4c .. +3), one batch of 8 ahead of the MFMAs. */
+    auto accumulate = [&](uint32_t t, const float *sv) {
+        const uint32_t tb = t + (4 * g + (kl >> 2)) * CROW_B + 8 * (kl & 3);
+        s16x4 bv[2][8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) bv[0][j] = ds_read_tr16(tb, 32 * j);
+        s16x4 ph, pl;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float p = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - m);
+            l += p;
+            uint16_t hi, lo;
+            split_bf16(p, &hi, &lo);
+            ph[i] = (short)hi;
+            pl[i] = (short)lo;
+        }
+#pragma unroll
+        for (int bt = 0; bt < KVL / 128; bt++) {
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(bv[bt & 1][0]), "+v"(bv[bt & 1][1]), "+v"(bv[bt & 1][2]), "+v"(bv[bt & 1][3]),
+                           "+v"(bv[bt & 1][4]), "+v"(bv[bt & 1][5]), "+v"(bv[bt & 1][6]), "+v"(bv[bt & 1][7]));
+            if (bt + 1 < KVL / 128) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) bv[(bt + 1) & 1][j] = ds_read_tr16(tb, 32 * (8 * (bt + 1) + j));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int nb = 8 * bt + j;
+                O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, bv[bt & 1][j], O[nb], 0, 0, 0);
+                O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, bv[bt & 1][j], O[nb], 0, 0, 0);
+            }
+        }
+    };
+    /* The inner loop touches O only through MFMAs (it stays in accumulation
+     * registers); a sub-tile that needs a rescale leaves it, and the outer
+     * loop rescales and accumulates that sub-tile. */
+    int k0 = kbeg, st = 0;
+    while (k0 < kend) {
+        float sv[4];
+        bool moved = false;
+        for (;;) {
+            VMCNT_WAIT(0);                      /* this sub-tile's rows are in LDS */
+            __builtin_amdgcn_sched_barrier(0);
+            if (k0 + 16 < kend) issue(st ^ 1, k0 + 16);   /* the other stage's reads are done */
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t t = lds_addr(wt0 + st * TILE_B);
+            score(t, k0, sv);
+            const float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_TAU)) {
+                moved = true;
+                break;
+            }
+            accumulate(t, sv);
+            __builtin_amdgcn_sched_barrier(0);
+            k0 += 16;
+            st ^= 1;
+            if (k0 >= kend) break;
+        }
+        if (!moved) break;
+        /* some head's maximum moved: new m = the head's max over the
+         * sub-tile (across the 4 lane groups) */
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16, MM_WAVE));
         mx = fmaxf(mx, __shfl_xor(mx, 32, MM_WAVE));
         const float mnew = fmaxf(m, mx);
         const float cr = m == -INFINITY ? 0.0f : __expf(m - mnew);
-        float p[4], ps = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            p[i] = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - mnew);
-            ps += p[i];
-        }
-        ps += __shfl_xor(ps, 16, MM_WAVE);
-        ps += __shfl_xor(ps, 32, MM_WAVE);
-        l = l * cr + ps;
+        l *= cr;
         m = mnew;
         /* rescale O rows: lane (r, g) holds heads 4g + i, whose factor sits
          * in lane 4g + i */
@@ -289,96 +357,60 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
 #pragma unroll
             for (int nb = 0; nb < KVL / 16; nb++) O[nb][i] *= ci;
         }
-        /* P[head kl][keys 4g .. 4g+3] as bf16 hi/lo A operands */
-        s16x4 ph, pl;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint16_t hi, lo;
-            split_bf16(p[i], &hi, &lo);
-            ph[i] = (short)hi;
-            pl[i] = (short)lo;
-        }
-        /* O[head][r] += P . C_kv; transposing reads: lane 4k + c of group g
-         * reads row 4g + k, columns 16 nb + 4c .. +3 */
-        const uint32_t tb = t + (4 * g + (kl >> 2)) * CROW_B + 8 * (kl & 3);
-#pragma unroll
-        for (int nb0 = 0; nb0 < KVL / 16; nb0 += 8) {
-            s16x4 bv[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) bv[j] = ds_read_tr16(tb + 32 * (nb0 + j));
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]),
-                         "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]), "+v"(bv[7]));
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                O[nb0 + j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, bv[j], O[nb0 + j], 0, 0, 0);
-                O[nb0 + j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, bv[j], O[nb0 + j], 0, 0, 0);
-            }
-        }
-    };
-    if (kbeg < kend) {
-        issue(0, kbeg);
-        int st = 0;
-        for (int k0 = kbeg; k0 < kend; k0 += 16, st ^= 1) {
-            VMCNT_WAIT(0);                      /* this sub-tile's rows are in LDS */
-            __builtin_amdgcn_sched_barrier(0);
-            if (k0 + 16 < kend) issue(st ^ 1, k0 + 16);   /* the other stage's reads are done */
-            __builtin_amdgcn_sched_barrier(0);
-            process(st, k0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        accumulate(lds_addr(wt0 + st * TILE_B), sv);
+        __builtin_amdgcn_sched_barrier(0);
+        k0 += 16;
+        st ^= 1;
     }
     VMCNT_WAIT(0);
 
-    /* merge the waves: waves 1.. park O, m, l in LDS (over the staging area,
-     * free after the barrier); wave 0 merges */
+    /* merge the waves (LDS of the stages is free after the barrier):
+     * per head, mm = max over waves of m, each wave's weight e^(m_w - mm);
+     * every wave parks its weighted O; all threads then sum the AW parts */
+    l += __shfl_xor(l, 16, MM_WAVE);
+    l += __shfl_xor(l, 32, MM_WAVE);
     __syncthreads();
-    float *ob = (float *)alds;                       /* [AW-1][16 heads][KVL] */
-    float *mlb = ob + (AW - 1) * 16 * KVL;           /* [AW-1][2][16] */
-    if (w > 0) {
-        float *o = ob + (size_t)(w - 1) * 16 * KVL;
+    float *ob = (float *)alds;                       /* [AW][16 heads][OROW] */
+    float *mlb = ob + AW * 16 * OROW;                /* [AW][2][16] */
+    if (g == 0) {
+        mlb[w * 32 + kl] = m;
+        mlb[w * 32 + 16 + kl] = l;
+    }
+    __syncthreads();
+    float mm = -INFINITY;
 #pragma unroll
-        for (int nb = 0; nb < KVL / 16; nb++)
+    for (int j = 0; j < AW; j++) mm = fmaxf(mm, mlb[j * 32 + kl]);
+    const float wself = m == -INFINITY ? 0.0f : __expf(m - mm);
+    {
+        float *o = ob + (size_t)w * 16 * OROW;
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[(4 * g + i) * KVL + nb * 16 + kl] = O[nb][i];
-        if (g == 0) {
-            mlb[(w - 1) * 32 + kl] = m;
-            mlb[(w - 1) * 32 + 16 + kl] = l;
+        for (int i = 0; i < 4; i++) {
+            const float wi = __shfl(wself, 4 * g + i, MM_WAVE);
+#pragma unroll
+            for (int nb = 0; nb < KVL / 16; nb++) o[(4 * g + i) * OROW + nb * 16 + kl] = O[nb][i] * wi;
         }
     }
-    __syncthreads();
-    if (w != 0) return;
-    /* per head (lane kl): merged max and each part's weight */
-    float mm = m;
-#pragma unroll
-    for (int j = 0; j < AW - 1; j++) mm = fmaxf(mm, mlb[j * 32 + kl]);
-    float wt[AW];
-    wt[0] = m == -INFINITY ? 0.0f : __expf(m - mm);
-    float lsum = l * wt[0];
-#pragma unroll
-    for (int j = 0; j < AW - 1; j++) {
-        const float mj = mlb[j * 32 + kl];
-        wt[j + 1] = mj == -INFINITY ? 0.0f : __expf(mj - mm);
-        lsum += mlb[j * 32 + 16 + kl] * wt[j + 1];
-    }
     const size_t pidx = ((size_t)(b * a.HG + hg) * a.nchunks + chunk);
-    if (g == 0) {
+    if (w == 0 && g == 0) {
+        float lsum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < AW; j++) {
+            const float mj = mlb[j * 32 + kl];
+            lsum += mj == -INFINITY ? 0.0f : mlb[j * 32 + 16 + kl] * __expf(mj - mm);
+        }
         a.part_ml[pidx * 32 + kl] = mm;
         a.part_ml[pidx * 32 + 16 + kl] = lsum;
     }
+    __syncthreads();
     float *po = a.part_o + pidx * 16 * KVL;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float wi[AW];
+    for (int j = 0; j < 16 * KVL / (4 * AW * MM_WAVE); j++) {
+        const int e = 4 * (tid + j * AW * MM_WAVE);
+        const int hh = e / KVL, col = e % KVL;
+        f32x4 v = *(const f32x4 *)(ob + hh * OROW + col);
 #pragma unroll
-        for (int j = 0; j < AW; j++) wi[j] = __shfl(wt[j], 4 * g + i, MM_WAVE);
-#pragma unroll
-        for (int nb = 0; nb < KVL / 16; nb++) {
-            const int idx = (4 * g + i) * KVL + nb * 16 + kl;
-            float v = O[nb][i] * wi[0];
-#pragma unroll
-            for (int j = 0; j < AW - 1; j++) v += ob[(size_t)j * 16 * KVL + idx] * wi[j + 1];
-            po[idx] = v;
-        }
+        for (int k = 1; k < AW; k++) v += *(const f32x4 *)(ob + (size_t)k * 16 * OROW + hh * OROW + col);
+        *(f32x4 *)(po + e) = v;
     }
 }
 
