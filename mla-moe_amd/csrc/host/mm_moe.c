@@ -431,13 +431,13 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
                                (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((2 * I / 16 + 7) / 8), mt_routed), 1, 1, 256, 0,
+        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(2 * I / 16, MM_I8T_FR), mt_routed), 1, 1, 256, 0,
                             &ta)))
             return st;
         if (S) {
             mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
                                    hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((2 * S / 16 + 7) / 8), mt_shared), 1, 1,
+            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(2 * S / 16, MM_I8T_FR), mt_shared), 1, 1,
                                 256, 0, &ts)))
                 return st;
         }
@@ -460,12 +460,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
                                0, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((H / 16 + 7) / 8), mt_routed), 1, 1, 256, 0, &td)))
+        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(H / 16, MM_I8T_FR), mt_routed), 1, 1, 256, 0, &td)))
             return st;
         if (S) {
             mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
                                     NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)((H / 16 + 7) / 8), mt_shared), 1, 1, 256, 0,
+            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(H / 16, MM_I8T_FR), mt_shared), 1, 1, 256, 0,
                                 &tsd)))
                 return st;
         }

@@ -172,8 +172,8 @@ typedef struct {
 
 /* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
  * the routed experts' row lists (or all T rows for the shared expert). */
-#define MM_I8T_BM 128
-#define MM_I8T_BN 128
+#define MM_I8T_BM 128     /* rows per tile */
+#define MM_I8T_FR 16      /* B fragments (16 packed columns each) per column slab */
 typedef struct {
     const int8_t *b;         /* packed fragments of expert 0 */
     size_t b_expert_stride;  /* bytes between experts' fragment sets */

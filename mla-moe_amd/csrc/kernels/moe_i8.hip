@@ -686,15 +686,18 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
 
 /* ---- tiled grouped GEMM (prefill) ------------------------------------------- */
 
-/* Block tile: MM_I8T_BM rows x 8 B fragments (gate/up: 4 column blocks of
- * 16 with their gate and up fragments = 64 output columns; plain: 8 column
- * blocks = 128 output columns), K step 64.  Four waves in a 2 x 2 grid, each
- * a 64-row x 4-fragment tile: 16 v_mfma_i32_16x16x64_i8 per K step.
- * A (gathered rows) and B (packed fragments) are staged through two LDS
- * buffers of 16 KB in MFMA operand order; the next K step's global loads are
- * issued before the current step's MFMAs.  grid.x = column tile, grid.y =
- * row tile over all experts (prefix of ceil(rows_e / 128)). */
-#define T_FRAGS 8
+/* Block tile: MM_I8T_BM = 128 rows x MM_I8T_FR = 16 B fragments (gate/up: 8
+ * column blocks of 16 with their gate and up fragments = 128 output columns;
+ * plain: 16 column blocks = 256 output columns), K step 64.  The four waves
+ * split the fragments (4 each) and share the rows: the gathered A rows of a
+ * K step (8 fragments of 16 rows) are staged through LDS by direct global ->
+ * LDS loads, and every wave streams its own B fragments straight into a
+ * register ring.  A wave tile is 128 x 4 fragments = 32
+ * v_mfma_i32_16x16x64_i8 per K step; 2 blocks fit a CU. */
+#define T_WF 4                    /* B fragments per wave */
+#define T_D 2                     /* K steps issued ahead (A and B) */
+#define T_NS (T_D + 1)            /* A stages in LDS = B register slots */
+#define T_ASTAGE (8 * 1024)       /* one K step of A: 8 fragments of 16 rows x 64 B */
 
 /* Expert, first row and row count of row-group `tile` (a group is up to
  * a.mgroup consecutive 128-row tiles of one expert); all threads of the
@@ -741,108 +744,117 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
     return s_e >= 0;
 }
 
-#define T_STAGES 4
-#define T_STAGE_BYTES (2 * T_FRAGS * 1024)
-
-/* One 128-row x 8-fragment tile starting at row m0 of expert e (M rows). */
-__device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_STAGE_BYTES],
+/* One 128-row x 16-fragment tile starting at row m0 of expert e (M rows). */
+__device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_ASTAGE],
+                                           int32_t *s_arow, float *s_sa, int32_t *s_rid,
                                            int e, int m0, int M, int slab) {
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
-    const int wm = wave >> 1, wn = wave & 1;
     const int KB = a.Kd / 64;
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int fr0 = slab * T_FRAGS;
+    const int fr0 = slab * MM_I8T_FR + wave * T_WF;   /* this wave's first fragment */
     const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
     const int8_t *bexp = a.b + (size_t)e * a.b_expert_stride;
 
-    /* Wave w loads A fragments 2w, 2w+1 (rows 32w .. 32w+31 of the tile) and
-     * B fragments 2w, 2w+1 of every K step.  Lane L of an A fragment carries
-     * row (L % 16), bytes 16 * (L / 16) of the 64-byte K step. */
+    /* the tile's rows: route id, A row and A scale (rows past M repeat row m0;
+     * their results are discarded) */
+    if (tid < MM_I8T_BM) {
+        const int m = m0 + tid < M ? m0 + tid : m0;
+        const int rid = rows ? rows[m] : m;
+        const int arow = (a.a_by_route || !rows) ? rid : rid / a.K;
+        s_rid[tid] = m0 + tid < M ? rid : -1;
+        s_arow[tid] = arow;
+        s_sa[tid] = a.sa[arow];
+    }
+    __syncthreads();
+
+    /* A: wave w loads fragments 2w, 2w+1 (rows 32w .. 32w+31) of every K step;
+     * lane L of a fragment carries row L % 16, bytes 16 (L / 16) of the step */
     const int8_t *asrc[2];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int m = m0 + (2 * wave + h) * 16 + (lane & 15);
-        int arow = 0;
-        if (m < M) {
-            const int rid = rows ? rows[m] : m;
-            arow = (a.a_by_route || !rows) ? rid : rid / a.K;
-        } else {
-            const int rid = rows ? rows[m0] : m0;   /* any valid row; result discarded */
-            arow = (a.a_by_route || !rows) ? rid : rid / a.K;
-        }
-        asrc[h] = a.a + (size_t)arow * a.Kd + (lane >> 4) * 16;
-    }
-    /* fragment column fr at K step kb: gate/up [nb][kb][gate|up] (fr = 2 nb +
-     * gate|up), plain [nb][kb] */
+    for (int h = 0; h < 2; h++)
+        asrc[h] = a.a + (size_t)s_arow[(2 * wave + h) * 16 + (lane & 15)] * a.Kd + (lane >> 4) * 16;
+    /* B: fragment fr at K step kb is 1 KB at gate/up [nb][kb][gate|up]
+     * (fr = 2 nb + gate|up) or plain [nb][kb]; fragments past the last are
+     * clamped (results discarded).  Plain (cached) loads: the other row
+     * tiles of the expert read the same fragments from L2. */
     const int bstep = a.gu ? 2048 : 1024;
-    const int8_t *bsrc[2];
+    const int8_t *bsrc[T_WF];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int fr = min(fr0 + 2 * wave + h, nfr_total - 1);
-        const size_t off = a.gu ? ((size_t)(fr >> 1) * 2 * KB + (fr & 1)) * 1024
-                                : (size_t)fr * KB * 1024;
-        bsrc[h] = bexp + off + lane * 16;
+    for (int f = 0; f < T_WF; f++) {
+        const int fr = min(fr0 + f, nfr_total - 1);
+        const size_t off = a.gu ? ((size_t)(fr >> 1) * 2 * KB + (fr & 1)) * 1024 : (size_t)fr * KB * 1024;
+        bsrc[f] = bexp + off + lane * 16;
     }
-    auto issue = [&](int kb) {
-        int8_t *st = lds[kb % T_STAGES];
+
+    v4i bq[T_NS][T_WF];
+    auto issue = [&](int kb, int slot) {
+        int8_t *st = lds[slot];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            lds_dma16(asrc[h] + kb * 64, st + (2 * wave + h) * 1024);
-            lds_dma16(bsrc[h] + (size_t)kb * bstep, st + T_FRAGS * 1024 + (2 * wave + h) * 1024);
-        }
+        for (int h = 0; h < 2; h++) lds_dma16(asrc[h] + kb * 64, st + (2 * wave + h) * 1024);
+#pragma unroll
+        for (int f = 0; f < T_WF; f++) bq[slot][f] = *(const v4i *)(bsrc[f] + (size_t)kb * bstep);
     };
 
-    v4i acc[4][4];
+    v4i acc[8][T_WF];
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-        for (int f = 0; f < 4; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
+        for (int f = 0; f < T_WF; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
 
+    /* every K step issues one group of loads (2 A + T_WF B), steps past the
+     * end re-load the last step (unconditional, so that the wait counts are
+     * static) into a stage / slot nobody reads again */
 #pragma unroll
-    for (int s = 0; s < T_STAGES - 1; s++)
-        if (s < KB) issue(s);
-    for (int kb = 0; kb < KB; kb++) {
-        /* this wave's loads for step kb are done once at most 4 * (number of
-         * later steps already issued) of its loads are outstanding */
-        const int later = min(T_STAGES - 2, KB - 1 - kb);
-        if (later >= 2) VMCNT_WAIT(8);
-        else if (later == 1) VMCNT_WAIT(4);
-        else VMCNT_WAIT(0);
-        __builtin_amdgcn_s_barrier();   /* every wave's part of stage kb has landed,
-                                           and stage kb-1 is no longer being read */
-        if (kb + T_STAGES - 1 < KB) issue(kb + T_STAGES - 1);
-        const uint32_t st = lds_addr(lds[kb % T_STAGES]) + lane * 16;
-        v4i av[4], bv[4];
+    for (int s = 0; s < T_D; s++) issue(min(s, KB - 1), s);
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kb, int j) {   /* j = kb % T_NS */
+        VMCNT_WAIT((2 + T_WF) * (T_D - 1));   /* this wave's step-kb group has landed */
+        __builtin_amdgcn_s_barrier();   /* every wave's A part of step kb has landed,
+                                           and step kb-1's stage is no longer read */
+        __builtin_amdgcn_sched_barrier(0);
+        issue(min(kb + T_D, KB - 1), (j + T_D) % T_NS);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t st = lds_addr(lds[j]) + lane * 16;
+        v4i av[8];
 #pragma unroll
-        for (int mi = 0; mi < 4; mi++) av[mi] = ds_read16(st + (wm * 4 + mi) * 1024);
-#pragma unroll
-        for (int f = 0; f < 4; f++) bv[f] = ds_read16(st + T_FRAGS * 1024 + (wn * 4 + f) * 1024);
+        for (int mi = 0; mi < 8; mi++) av[mi] = ds_read16(st, mi * 1024);
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]),
-                       "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]));
+                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(av[4]), "+v"(av[5]),
+                       "+v"(av[6]), "+v"(av[7]));
 #pragma unroll
-        for (int mi = 0; mi < 4; mi++)
+        for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-            for (int f = 0; f < 4; f++) acc[mi][f] = mfma_i8(av[mi], bv[f], acc[mi][f]);
+            for (int f = 0; f < T_WF; f++) acc[mi][f] = mfma_i8(av[mi], bq[j][f], acc[mi][f]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    /* rounds of T_NS steps keep the ring indices compile-time */
+    int k0 = 0;
+    for (; k0 + T_NS <= KB; k0 += T_NS) {
+#pragma unroll
+        for (int j = 0; j < T_NS; j++) step(k0 + j, j);
     }
+#pragma unroll
+    for (int j = 0; j < T_NS - 1; j++)
+        if (k0 + j < KB) step(k0 + j, j);
+    VMCNT_WAIT(0);   /* the trailing groups land before the next tile reuses the stages */
 
-    /* epilogue */
+    /* epilogue: lane holds rows 16 mi + 4 (lane / 16) + i of column
+     * (lane % 16) of each of its fragments */
     const float *sb0 = a.sb0 + (size_t)e * a.sb_expert_stride;
     const float *sb1 = a.sb1 ? a.sb1 + (size_t)e * a.sb_expert_stride : nullptr;
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++) {
+    for (int mi = 0; mi < 8; mi++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int m = m0 + wm * 64 + mi * 16 + 4 * (lane >> 4) + i;
-            if (m >= M) continue;
-            const int rid = rows ? rows[m] : m;
-            const int arow = (a.a_by_route || !rows) ? rid : rid / a.K;
-            const float sa = a.sa[arow];
+            const int r = mi * 16 + 4 * (lane >> 4) + i;
+            const int rid = s_rid[r];
+            if (rid < 0) continue;
+            const float sa = s_sa[r];
             if (a.gu) {
 #pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    const int nb = (fr0 >> 1) + wn * 2 + k;
+                for (int k = 0; k < T_WF / 2; k++) {
+                    const int nb = (fr0 >> 1) + k;
                     if (nb * 16 >= a.N) continue;
                     const int col = nb * 16 + (lane & 15);
                     const int32_t ag = acc[mi][2 * k][i], au = acc[mi][2 * k + 1][i];
@@ -856,8 +868,8 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
                 }
             } else {
 #pragma unroll
-                for (int f = 0; f < 4; f++) {
-                    const int nb = fr0 + wn * 4 + f;
+                for (int f = 0; f < T_WF; f++) {
+                    const int nb = fr0 + f;
                     if (nb * 16 >= a.N) continue;
                     const int col = nb * 16 + (lane & 15);
                     const int32_t ac = acc[mi][f][i];
@@ -869,19 +881,18 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
     }
 }
 
-/* grid.x = 8-fragment column slab, grid.y = row group.  A block walks the
- * group's 128-row tiles in order, so the slab's weights (K x 128 bytes) come
- * from HBM once and from this CU's L2 for the group's later tiles. */
 /* 1-D grid (a multiple of 64 blocks, see the host).  Blocks are dealt to
  * the 8 XCDs round robin (block b runs on XCD b % 8); b is mapped to (column
  * slab, row group) so that each XCD receives runs of 8 consecutive row
  * groups of ONE slab: the slab's weights then come from HBM once per run
  * and from that XCD's L2 for the other row groups (the tiles of a hot
  * expert are consecutive row groups). */
-extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[T_STAGES][T_STAGE_BYTES];
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[T_NS][T_ASTAGE];
+    __shared__ int32_t s_arow[MM_I8T_BM], s_rid[MM_I8T_BM];
+    __shared__ float s_sa[MM_I8T_BM];
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int nslab = (nfr_total + T_FRAGS - 1) / T_FRAGS;
+    const int nslab = (nfr_total + MM_I8T_FR - 1) / MM_I8T_FR;
     const int b = blockIdx.x;
     const int xcd = b % MM_I8S_XCD, j = b / MM_I8S_XCD;
     const int q = (j / MM_I8S_XCD) * MM_I8S_XCD + xcd;   /* (slab, row-group run) index */
@@ -892,7 +903,7 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_gemm_tiled(mm_i8_tiled_a
     if (!tile_owner(a, grp, &e, &g0, &M)) return;
     const int g1 = min(M, g0 + a.mgroup * MM_I8T_BM);
     for (int m0 = g0; m0 < g1; m0 += MM_I8T_BM) {
-        tiled_tile(a, lds, e, m0, M, slab);
-        __builtin_amdgcn_s_barrier();   /* the LDS ring is refilled by the next tile */
+        tiled_tile(a, lds, s_arow, s_sa, s_rid, e, m0, M, slab);
+        __syncthreads();   /* the LDS ring and row tables are refilled by the next tile */
     }
 }
