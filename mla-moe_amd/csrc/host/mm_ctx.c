@@ -48,6 +48,7 @@ static const struct {
     [K_MLA_UV] = {"mm_mla_uv", MOD_MLA},
     [K_MLA_WPREP] = {"mm_mla_wprep", MOD_MLA},
     [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
+    [K_CVT_BF16] = {"mm_cvt_bf16", MOD_GEMM_BF16},
 };
 
 /* ---- errors ------------------------------------------------------------- */

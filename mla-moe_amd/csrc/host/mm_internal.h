@@ -30,6 +30,7 @@ typedef enum {
     K_MLA_UV,
     K_MLA_WPREP,
     K_GEMM_BF16,
+    K_CVT_BF16,
     K_COUNT
 } mm_kernel_id;
 

@@ -246,12 +246,21 @@ typedef struct {
 } mm_mla_combine_args;
 
 /* ---- dense bf16 matmul --------------------------------------------------------- */
-/* y[t, d] (=|+=) sum_i x[t, i] * W[d, i]; W bf16 row-major [d_out, n_in]. */
+/* y[t, d] (=|+=) sum_i x[t, i] * W[d, i]; W bf16 row-major [d_out, n_in].  x
+ * is first converted to bf16 rows of a padded stride kp (a multiple of 64,
+ * zeros past n_in): truncated, or split into hi + lo halves. */
 typedef struct {
     const float *x;          /* [T, n_in] */
+    uint16_t *xh, *xl;       /* [T, kp]; xl only for the split */
+    int T, n_in, kp;
+    int split;               /* 1: hi/lo split (RNE); 0: truncation */
+} mm_cvt_bf16_args;
+
+typedef struct {
+    const uint16_t *xh, *xl; /* [T, kp] converted x (xl: split mode) */
     const uint16_t *w;       /* [d_out, n_in] */
     float *y;                /* [T, d_out] */
-    int T, d_out, n_in;
-    int x_bf16;              /* 1: x truncated to bf16 (one MFMA); 0: hi/lo split */
+    int T, d_out, n_in, kp;
+    int split;               /* 1: two MFMAs per product (x = hi + lo) */
     int accumulate;
 } mm_gemm_bf16_args;

@@ -4,17 +4,27 @@
  * W is bf16 row-major [d_out, n_in] exactly as the reference stores it: a B
  * operand fragment (16 output columns x 32 inputs, lane l holding column
  * l % 16 and inputs 8*(l/16) .. +7) is 16 contiguous bytes of one weight row
- * per lane.  x is fp32: either truncated to bf16 (the config that casts
- * activations on the input side, include/tensor.h:16-20) or split into a
- * bf16 hi/lo pair (two MFMAs, ~2^-17 relative) so the result tracks the fp32
- * reference.  Block tile 64 x 64, four waves of 32 x 32, K step 32; operands
- * are read from L1/L2 directly (the GEMMs of this path are small enough that
- * the block grid, not LDS reuse, is what fills the machine).
+ * per lane, so B stages into LDS by direct global -> LDS loads in operand
+ * order.  x is fp32: mm_cvt_bf16 first writes it as bf16 rows, either
+ * truncated (the config that casts activations on the input side,
+ * include/tensor.h:16-20) or split into a bf16 hi/lo pair (two MFMAs, ~2^-17
+ * relative) so the result tracks the fp32 reference; A then stages exactly
+ * like B.
+ *
+ * Block tile 128 x 128, K step 64; four waves in a 2 x 2 grid, each a 64 x
+ * 64 tile (16 MFMAs per 32 of K).  Both operands stage through an LDS ring
+ * (4 stages, 3 for the split) by direct loads issued three (two) steps
+ * ahead of the MFMAs.
  */
 #include "common.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+#define GB_BM 128
+#define GB_BN 128
+#define GB_BK 64
+#define GB_COPY (128 * 128)             /* one operand of one stage: 128 rows x 128 B */
 
 __device__ __forceinline__ uint16_t rne16(float x) {
     uint32_t u = __float_as_uint(x);
@@ -22,78 +32,184 @@ __device__ __forceinline__ uint16_t rne16(float x) {
     return (uint16_t)(u >> 16);
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args a) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int g = lane >> 4, r16 = lane & 15;
-    const int m0 = blockIdx.y * 64 + wm * 32, n0 = blockIdx.x * 64 + wn * 32;
-    const int K = a.n_in;
-
-    const float *xr[2];
-    const uint16_t *wr[2];
-    bool mv[2], nv[2];
+/* x -> bf16 rows of stride kp (zeros past n_in), 8 values per thread:
+ * truncation (the reference's cast, include/tensor.h:16-20) or the RNE
+ * hi/lo split. */
+extern "C" __global__ __launch_bounds__(256) void mm_cvt_bf16(mm_cvt_bf16_args a) {
+    const size_t i8 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   /* 8-value chunk */
+    const int cpr = a.kp / 8;
+    if (i8 >= (size_t)a.T * cpr) return;
+    const int t = (int)(i8 / cpr), k = (int)(i8 % cpr) * 8;
+    u16x8 hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (k < a.n_in) {   /* n_in is a multiple of 8 */
+        const float *p = a.x + (size_t)t * a.n_in + k;
+        const f32x4 x0 = *(const f32x4 *)p, x1 = *(const f32x4 *)(p + 4);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int m = m0 + i * 16 + r16, n = n0 + i * 16 + r16;
-        mv[i] = m < a.T;
-        nv[i] = n < a.d_out;
-        xr[i] = a.x + (size_t)(mv[i] ? m : 0) * K + 8 * g;
-        wr[i] = a.w + (size_t)(nv[i] ? n : 0) * K + 8 * g;
-    }
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int k0 = 0; k0 < K; k0 += 32) {
-        const bool kv = k0 + 8 * g < K;   /* K is a multiple of 8 */
-        bf16x8 ah[2], al[2], bw[2];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            u16x8 hi = {0, 0, 0, 0, 0, 0, 0, 0}, lo = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (mv[i] && kv) {
-                const f32x4 x0 = *(const f32x4 *)(xr[i] + k0), x1 = *(const f32x4 *)(xr[i] + k0 + 4);
-                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (a.x_bf16) {
-                        hi[j] = (uint16_t)(__float_as_uint(xs[j]) >> 16);   /* truncation */
-                    } else {
-                        const uint16_t h = rne16(xs[j]);
-                        hi[j] = h;
-                        lo[j] = rne16(xs[j] - bf16_f32(h));
-                    }
-                }
+        for (int e = 0; e < 8; e++) {
+            const float v = e < 4 ? x0[e] : x1[e - 4];
+            if (a.split) {
+                const uint16_t h16 = rne16(v);
+                hi[e] = h16;
+                lo[e] = rne16(v - bf16_f32(h16));
+            } else {
+                hi[e] = (uint16_t)(__float_as_uint(v) >> 16);
             }
-            ah[i] = __builtin_bit_cast(bf16x8, hi);
-            al[i] = __builtin_bit_cast(bf16x8, lo);
-            u16x8 wv = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (nv[i] && kv) wv = *(const u16x8 *)(wr[i] + k0);
-            bw[i] = __builtin_bit_cast(bf16x8, wv);
         }
+    }
+    *(u16x8 *)(a.xh + i8 * 8) = hi;
+    if (a.split) *(u16x8 *)(a.xl + i8 * 8) = lo;
+}
+
+/* Stage layout: [A hi][A lo (split mode)][B], each 128 rows (A) or output
+ * columns (B) x 64 K = 16 KB.  A load instruction moves 8 rows x 128 B
+ * (whole cache lines; half-line accesses measured ~2.6x slower): lane l
+ * carries row 8 i + l / 8 and stores at position p = l % 8 of that row's
+ * 128 B the 16 B chunk q = p ^ s(row), s(R) = (R / 2) % 8.  The XOR swizzle
+ * makes the operand reads below (16 rows, one chunk each) conflict-free. */
+__device__ __forceinline__ int gb_swz(int R) { return (R >> 1) & 7; }
+
+template <bool HL>
+__device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *lds) {
+    constexpr int NCOPY = HL ? 3 : 2;
+    constexpr int SB = NCOPY * GB_COPY;          /* stage bytes */
+    constexpr int BOFF = (NCOPY - 1) * GB_COPY;
+    constexpr int NS = HL ? 3 : 4;               /* stages */
+    constexpr int D = NS - 1;                    /* steps issued ahead */
+    constexpr int G = 4 * NCOPY;                 /* transfers per wave per step */
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    /* 1-D grid: blocks are dealt to the 8 XCDs round robin (block b -> XCD
+     * b % 8).  XCD x takes the column blocks x, x + 8, ... for every row
+     * block: its weight columns are fetched into its L2 once and reused by
+     * all row blocks, and the x rows (small) are shared by its tiles */
+    const int nbx = (a.d_out + GB_BN - 1) / GB_BN, nby = (a.T + GB_BM - 1) / GB_BM;
+    const int b = blockIdx.x, slot = b / 8;
+    const int cb = b % 8 + 8 * (slot / nby), rb = slot % nby;
+    if (cb >= nbx) return;
+    const int m0 = rb * GB_BM, n0 = cb * GB_BN;
+    const int K = a.n_in, KB = a.kp / GB_BK;
+
+    /* wave w issues instructions 4 w .. 4 w + 3 (rows 32 w .. 32 w + 31) of A
+     * (hi, lo) and of B; rows past T / columns past d_out read the last one
+     * (results discarded); B chunks past n_in re-read chunk 0 of the row (A
+     * is zero there) */
+    const uint16_t *ah_src[4], *al_src[4], *b_src[4];
+    int bq[4];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+    for (int h = 0; h < 4; h++) {
+        const int R = 8 * (4 * wave + h) + (lane >> 3);
+        const int kq = 8 * ((lane & 7) ^ gb_swz(R));      /* element offset in the step */
+        const int m = min(m0 + R, a.T - 1);
+        const int n = min(n0 + R, a.d_out - 1);
+        ah_src[h] = a.xh + (size_t)m * a.kp + kq;
+        al_src[h] = HL ? a.xl + (size_t)m * a.kp + kq : nullptr;
+        b_src[h] = a.w + (size_t)n * K;
+        bq[h] = kq;
+    }
+    auto issue = [&](int kb, int st) {
+        uint8_t *s0 = lds + st * SB;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
-                if (!a.x_bf16)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+        for (int h = 0; h < 4; h++) {
+            const int i = 4 * wave + h;
+            lds_dma16(ah_src[h] + kb * GB_BK, s0 + i * 1024);
+            if (HL) lds_dma16(al_src[h] + kb * GB_BK, s0 + GB_COPY + i * 1024);
+            const int k = kb * GB_BK + bq[h];
+            lds_dma16(b_src[h] + (k < K ? k : 0), s0 + BOFF + i * 1024);
+        }
+    };
+    /* operand read of lane (c = l % 16, g = l / 16) for fragment row block r
+     * and K half kh: row 16 r + c, chunk q = 4 kh + g, at (16 r + c) * 128 +
+     * 16 (q ^ s(c)); the r part is a compile-time offset */
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const uint32_t rd0 = c16 * 128 + 16 * ((0 + g4) ^ gb_swz(c16));
+    const uint32_t rd1 = c16 * 128 + 16 * ((4 + g4) ^ gb_swz(c16));
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[r][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    /* every step issues one group (steps past the end re-load the last, so
+     * that the wait counts are static) */
+#pragma unroll
+    for (int s = 0; s < D; s++) issue(min(s, KB - 1), s);
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kb, int j) {   /* j = kb % NS */
+        VMCNT_WAIT(G * (D - 1));       /* this wave's step-kb group has landed */
+        __builtin_amdgcn_s_barrier();  /* ... every wave's, and stage kb-1 is free */
+        __builtin_amdgcn_sched_barrier(0);
+        issue(min(kb + D, KB - 1), (j + D) % NS);
+        __builtin_amdgcn_sched_barrier(0);
+        /* this wave's A rows 64 wm .. and B columns 64 wn .. */
+        const uint32_t st0 = lds_addr(lds + j * SB);
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            const uint32_t sa = st0 + (kh ? rd1 : rd0) + wm * 64 * 128;
+            const uint32_t sb = st0 + BOFF + (kh ? rd1 : rd0) + wn * 64 * 128;
+            i32x4 ah[4], al[4], bw[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                ah[r] = ds_read16(sa, r * 2048);
+                if (HL) al[r] = ds_read16(sa, GB_COPY + r * 2048);
             }
+#pragma unroll
+            for (int c = 0; c < 4; c++) bw[c] = ds_read16(sb, c * 2048);
+            if (HL)
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(al[0]), "+v"(al[1]),
+                               "+v"(al[2]), "+v"(al[3]), "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]));
+            else
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(bw[0]), "+v"(bw[1]),
+                               "+v"(bw[2]), "+v"(bw[3]));
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const bf16x8 bb = __builtin_bit_cast(bf16x8, bw[c]);
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[r]), bb,
+                                                                        acc[r][c], 0, 0, 0);
+                    if (HL)
+                        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al[r]), bb,
+                                                                            acc[r][c], 0, 0, 0);
+                }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int k0 = 0;
+    for (; k0 + NS <= KB; k0 += NS) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) step(k0 + j, j);
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int j = 0; j < NS - 1; j++)
+        if (k0 + j < KB) step(k0 + j, j);
+    VMCNT_WAIT(0);
+
+    /* lane holds D[4 (l / 16) + i][l % 16] of each 16 x 16 tile */
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + j * 16 + r16;
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int n = n0 + 64 * wn + 16 * c + (lane & 15);
             if (n >= a.d_out) continue;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + i * 16 + 4 * g + e;
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 64 * wm + 16 * r + 4 * (lane >> 4) + i;
                 if (m >= a.T) continue;
                 float *o = a.y + (size_t)m * a.d_out + n;
-                *o = a.accumulate ? *o + acc[i][j][e] : acc[i][j][e];
+                *o = a.accumulate ? *o + acc[r][c][i] : acc[r][c][i];
             }
         }
+}
+
+/* 1-D grid of 8 * ceil(ceil(d_out / 128) / 8) * ceil(T / 128) blocks, 256
+ * threads, dynamic LDS: 4 stages x 32 KB (truncated x) or
+ * 3 x 48 KB (hi/lo x). */
+extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t glds[];
+    if (a.split) gemm_block<true>(a, glds);
+    else gemm_block<false>(a, glds);
 }
