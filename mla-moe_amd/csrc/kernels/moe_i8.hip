@@ -626,13 +626,48 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i
 
 /* ---- hidden-row quantisation and combine ------------------------------------- */
 
+/* One wave per row.  Rows of up to QH_MAXF4 * 256 values are held in
+ * registers whole (every load issued before the max: one round trip);
+ * longer rows take the chunked quantiser.  Same formula either way. */
+#define QH_MAXF4 12
+__device__ __forceinline__ void quant_row_regs(const float *x, int n, int8_t *q, float *s) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    if ((n / 4 + MM_WAVE - 1) / MM_WAVE > QH_MAXF4) {
+        quant_row_wave(x, n, q, s);
+        return;
+    }
+    f32x4 v[QH_MAXF4];
+#pragma unroll
+    for (int c = 0; c < QH_MAXF4; c++) v[c] = *(const f32x4 *)(x + min((c * MM_WAVE + lane) * 4, n - 4));
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < QH_MAXF4; c++)
+        if ((c * MM_WAVE + lane) * 4 < n)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+    amax = wave_max(amax);
+    const float sc = amax / 127.0f;
+    if (lane == 0) *s = sc;
+#pragma unroll
+    for (int c = 0; c < QH_MAXF4; c++) {
+        const int i = (c * MM_WAVE + lane) * 4;
+        if (i >= n) continue;
+        int b[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float r = sc == 0.0f ? 0.0f : fminf(fmaxf(rintf(v[c][j] / sc), -127.0f), 127.0f);
+            b[j] = (int)r & 0xff;
+        }
+        *(uint32_t *)(q + i) = (uint32_t)(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void mm_i8_quant_h(mm_i8_quant_rows_args a) {
     const int row = blockIdx.x * (blockDim.x / MM_WAVE) + threadIdx.x / MM_WAVE;
     if (row < a.rows)
-        quant_row_wave(a.h + (size_t)row * a.n, a.n, a.q + (size_t)row * a.n, a.s + row);
+        quant_row_regs(a.h + (size_t)row * a.n, a.n, a.q + (size_t)row * a.n, a.s + row);
     else if (row - a.rows < a.rows2) {
         const int r = row - a.rows;
-        quant_row_wave(a.h2 + (size_t)r * a.n2, a.n2, a.q2 + (size_t)r * a.n2, a.s2 + r);
+        quant_row_regs(a.h2 + (size_t)r * a.n2, a.n2, a.q2 + (size_t)r * a.n2, a.s2 + r);
     }
 }
 
