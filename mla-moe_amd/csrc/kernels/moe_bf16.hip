@@ -101,6 +101,13 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_g
             a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), 0, r * a.I, &wr);
 }
 
+/* Down rows: a wave's row d takes, per lane, chunks c = lane, lane + 64, ...
+ * of each routed segment in slot order, then of the shared segment -- the
+ * accumulation order of the sequential loops.  The loads of up to DN_BATCH
+ * chunks are issued before any is used (chunks past a segment's end load
+ * chunk 0 of it and are skipped), so a row costs ceil(chunks / DN_BATCH)
+ * round trips instead of one per segment. */
+#define DN_BATCH 24
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_down_bf16_args a) {
     const int t = blockIdx.y;
     const float *hs = a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S);
@@ -110,23 +117,41 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_d
     const int d0 = blockIdx.x * a.rows_per_block;
     const int nrows = min(a.rows_per_block, a.H - d0);
     const int nci = a.I >> 3, ncs = a.S >> 3;
+    const int cpl = (nci + MM_WAVE - 1) / MM_WAVE;        /* chunk slots per routed segment */
+    const int cps = (ncs + MM_WAVE - 1) / MM_WAVE;        /* ... of the shared segment */
+    const int nf = a.K * cpl + (a.S > 0 ? cps : 0);
     for (int rr = wave; rr < nrows; rr += GU_WAVES) {
         const int d = d0 + rr;
         float acc = 0.0f;
-        for (int r = 0; r < a.K; r++) {
-            const int e = min(max(a.topk_idx[(size_t)t * a.K + r], 0), a.E - 1);
-            const u32x4 *p = (const u32x4 *)(a.down + ((size_t)e * a.H + d) * a.I);
-            const float *hseg = hs + r * a.I;
-#pragma unroll 2
-            for (int c = lane; c < nci; c += MM_WAVE)
-                acc = dot8_bf16(__builtin_nontemporal_load(p + c), hseg + 8 * c, acc);
-        }
-        if (a.S > 0) {
-            const u32x4 *p = (const u32x4 *)(a.sdown + (size_t)d * a.S);
-            const float *hseg = hs + a.K * a.I;
-#pragma unroll 2
-            for (int c = lane; c < ncs; c += MM_WAVE)
-                acc = dot8_bf16(__builtin_nontemporal_load(p + c), hseg + 8 * c, acc);
+        for (int f0 = 0; f0 < nf; f0 += DN_BATCH) {
+            u32x4 wv[DN_BATCH];
+            const float *hv[DN_BATCH];
+            bool ok[DN_BATCH];
+#pragma unroll
+            for (int b = 0; b < DN_BATCH; b++) {
+                const int f = min(f0 + b, nf - 1);
+                const u32x4 *p;
+                int c;
+                if (f < a.K * cpl) {
+                    const int r = f / cpl;
+                    c = lane + MM_WAVE * (f % cpl);
+                    ok[b] = f0 + b < nf && c < nci;
+                    const int e = min(max(a.topk_idx[(size_t)t * a.K + r], 0), a.E - 1);
+                    p = (const u32x4 *)(a.down + ((size_t)e * a.H + d) * a.I);
+                    hv[b] = hs + r * a.I;
+                } else {
+                    c = lane + MM_WAVE * (f - a.K * cpl);
+                    ok[b] = f0 + b < nf && c < ncs;
+                    p = (const u32x4 *)(a.sdown + (size_t)d * a.S);
+                    hv[b] = hs + a.K * a.I;
+                }
+                if (!ok[b]) c = 0;
+                wv[b] = __builtin_nontemporal_load(p + c);
+                hv[b] += 8 * c;
+            }
+#pragma unroll
+            for (int b = 0; b < DN_BATCH; b++)
+                if (ok[b]) acc = dot8_bf16(wv[b], hv[b], acc);
         }
         acc = wave_sum(acc);
         if (lane == 0) {

@@ -723,16 +723,22 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
 
 /* Block tile: MM_I8T_BM = 128 rows x MM_I8T_FR = 16 B fragments (gate/up: 8
  * column blocks of 16 with their gate and up fragments = 128 output columns;
- * plain: 16 column blocks = 256 output columns), K step 64.  The four waves
- * split the fragments (4 each) and share the rows: the gathered A rows of a
- * K step (8 fragments of 16 rows) are staged through LDS by direct global ->
- * LDS loads, and every wave streams its own B fragments straight into a
- * register ring.  A wave tile is 128 x 4 fragments = 32
- * v_mfma_i32_16x16x64_i8 per K step; 2 blocks fit a CU. */
+ * plain: 16 column blocks = 256 output columns), K step 128 (two MFMA K
+ * halves of 64).  The four waves split the fragments (4 each) and share the
+ * rows.  The gathered A rows of a K step are staged through a 3-stage LDS
+ * ring by direct global -> LDS loads of whole cache lines (8 rows x 128 B per
+ * instruction: half-line accesses measured ~2.6x slower), XOR-swizzled so
+ * that the operand reads are conflict-free, two steps ahead.  Every wave
+ * streams its own B fragments (packed, 1 KB contiguous) with buffer loads
+ * (scalar base and step offset, one lane-offset register) into a ring of
+ * three 64-byte K halves, two halves ahead.  A wave tile is 128 x 4
+ * fragments = 32 v_mfma_i32_16x16x64_i8 per K half; 2 blocks fit a CU. */
 #define T_WF 4                    /* B fragments per wave */
-#define T_D 2                     /* K steps issued ahead (A and B) */
-#define T_NS (T_D + 1)            /* A stages in LDS = B register slots */
-#define T_ASTAGE (8 * 1024)       /* one K step of A: 8 fragments of 16 rows x 64 B */
+#define T_NSA 3                   /* A stages (issued 2 steps ahead) */
+#define T_ASTAGE (128 * 128)      /* one K step of A: 128 rows x 128 B */
+
+/* position of 16 B chunk q of tile row R within the row's 128 B in LDS */
+__device__ __forceinline__ int t_swz(int R) { return (R >> 1) & 7; }
 
 /* Expert, first row and row count of row-group `tile` (a group is up to
  * a.mgroup consecutive 128-row tiles of one expert); all threads of the
@@ -785,11 +791,13 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
                                            int e, int m0, int M, int slab) {
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
-    const int KB = a.Kd / 64;
+    const int KB = (a.Kd + 127) / 128;                /* K steps; Kd % 128 == 64 leaves the
+                                                         last step half (its second half
+                                                         is skipped) */
+    const int KH = a.Kd / 64;                         /* 64-byte K halves */
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
     const int fr0 = slab * MM_I8T_FR + wave * T_WF;   /* this wave's first fragment */
     const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
-    const int8_t *bexp = a.b + (size_t)e * a.b_expert_stride;
 
     /* the tile's rows: route id, A row and A scale (rows past M repeat row m0;
      * their results are discarded) */
@@ -803,32 +811,53 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
     }
     __syncthreads();
 
-    /* A: wave w loads fragments 2w, 2w+1 (rows 32w .. 32w+31) of every K step;
-     * lane L of a fragment carries row L % 16, bytes 16 (L / 16) of the step */
-    const int8_t *asrc[2];
+    /* A: wave w issues instructions 4 w .. 4 w + 3 of a step (rows 32 w ..
+     * 32 w + 31); lane l carries row R = 8 i + l / 8 and stores at position
+     * l % 8 of the row's 128 B the chunk (l % 8) ^ swz(R).  32-bit offsets
+     * from a.a (rows x Kd < 2^31). */
+    uint32_t arow_off[4];
+    int aq[4];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
-        asrc[h] = a.a + (size_t)s_arow[(2 * wave + h) * 16 + (lane & 15)] * a.Kd + (lane >> 4) * 16;
-    /* B: fragment fr at K step kb is 1 KB at gate/up [nb][kb][gate|up]
-     * (fr = 2 nb + gate|up) or plain [nb][kb]; fragments past the last are
-     * clamped (results discarded).  Plain (cached) loads: the other row
-     * tiles of the expert read the same fragments from L2. */
+    for (int h = 0; h < 4; h++) {
+        const int R = 8 * (4 * wave + h) + (lane >> 3);
+        arow_off[h] = (uint32_t)s_arow[R] * (uint32_t)a.Kd;
+        aq[h] = 16 * ((lane & 7) ^ t_swz(R));
+    }
+    /* B: fragment fr at K half k is 1 KB at gate/up [nb][k][gate|up]
+     * (fr = 2 nb + gate|up) or plain [nb][k]; fragments past the last are
+     * clamped (results discarded).  Buffer loads over the expert's fragments
+     * (cached: the other row tiles of the expert read them from L2). */
     const int bstep = a.gu ? 2048 : 1024;
-    const int8_t *bsrc[T_WF];
+    const uint32_t bytes_e = (uint32_t)(nfr_total * KH) * 1024u;
+    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.b + (size_t)e * a.b_expert_stride), 0, (int)bytes_e, 0x00020000);
+    int bfo[T_WF];   /* wave-uniform fragment offsets */
 #pragma unroll
     for (int f = 0; f < T_WF; f++) {
-        const int fr = min(fr0 + f, nfr_total - 1);
-        const size_t off = a.gu ? ((size_t)(fr >> 1) * 2 * KB + (fr & 1)) * 1024 : (size_t)fr * KB * 1024;
-        bsrc[f] = bexp + off + lane * 16;
+        const int fr = __builtin_amdgcn_readfirstlane(min(fr0 + f, nfr_total - 1));
+        bfo[f] = a.gu ? ((fr >> 1) * 2 * KH + (fr & 1)) * 1024 : fr * KH * 1024;
     }
+    const int lane16 = lane * 16;
+    /* operand read of lane (c = l % 16, g = l / 16) for 16-row block mi and
+     * K half ks: row 16 mi + c, chunk 4 ks + g; the mi part is a compile-time
+     * offset */
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const uint32_t rd0 = c16 * 128 + 16 * ((0 + g4) ^ t_swz(c16));
+    const uint32_t rd1 = c16 * 128 + 16 * ((4 + g4) ^ t_swz(c16));
 
-    v4i bq[T_NS][T_WF];
-    auto issue = [&](int kb, int slot) {
-        int8_t *st = lds[slot];
+    v4i bq[3][T_WF];   /* B of three 64-byte K halves */
+    auto issue_a = [&](int kb, int st) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) lds_dma16(asrc[h] + kb * 64, st + (2 * wave + h) * 1024);
+        for (int h = 0; h < 4; h++) {
+            const int k = kb * 128 + aq[h];   /* past Kd (a half last step): any valid chunk */
+            lds_dma16(a.a + (arow_off[h] + (uint32_t)(k < a.Kd ? k : k - 64)), lds[st] + (4 * wave + h) * 1024);
+        }
+    };
+    auto issue_b = [&](int hs, int slot) {   /* K half hs (clamped) */
+        const int so = __builtin_amdgcn_readfirstlane(min(hs, KH - 1) * bstep);
 #pragma unroll
-        for (int f = 0; f < T_WF; f++) bq[slot][f] = *(const v4i *)(bsrc[f] + (size_t)kb * bstep);
+        for (int f = 0; f < T_WF; f++)
+            bq[slot][f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(brs, lane16, bfo[f] + so, 0));
     };
 
     v4i acc[8][T_WF];
@@ -837,40 +866,57 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
 #pragma unroll
         for (int f = 0; f < T_WF; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
 
-    /* every K step issues one group of loads (2 A + T_WF B), steps past the
-     * end re-load the last step (unconditional, so that the wait counts are
-     * static) into a stage / slot nobody reads again */
-#pragma unroll
-    for (int s = 0; s < T_D; s++) issue(min(s, KB - 1), s);
+    /* Issue order: A(0), B(0), A(1), B(1); then step kb issues B(2kb+2),
+     * A(kb+2) at its start and B(2kb+3) after its first half.  At the top
+     * of step kb the groups after B(2kb) and A(kb) are A(kb+1) and B(2kb+1):
+     * 8 transfers.  Steps past the end re-load the last (unconditional loads
+     * keep the wait counts static). */
+    issue_a(0, 0);
+    issue_b(0, 0);
+    issue_a(min(1, KB - 1), 1);
+    issue_b(1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    auto step = [&](int kb, int j) {   /* j = kb % T_NS */
-        VMCNT_WAIT((2 + T_WF) * (T_D - 1));   /* this wave's step-kb group has landed */
-        __builtin_amdgcn_s_barrier();   /* every wave's A part of step kb has landed,
-                                           and step kb-1's stage is no longer read */
+    auto half = [&](uint32_t sa, int slot, int bmask) {   /* bmask 0: a half past Kd adds nothing */
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            v4i av[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) av[mi] = ds_read16(sa, (2 * h + mi) * 2048);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[0]), "+v"(av[1]));
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int f = 0; f < T_WF; f++)
+                    acc[2 * h + mi][f] = mfma_i8(av[mi], bq[slot][f] & bmask, acc[2 * h + mi][f]);
+        }
+    };
+    auto step = [&](int kb, int j) {   /* j = kb % 6: A stage j % 3, B slots (2j) % 3, (2j+1) % 3 */
+        VMCNT_WAIT(8);                 /* A(kb) and B(2kb) of this wave have landed */
+        __builtin_amdgcn_s_barrier();  /* every wave's A part of step kb has landed,
+                                          and step kb-1's stage is no longer read */
         __builtin_amdgcn_sched_barrier(0);
-        issue(min(kb + T_D, KB - 1), (j + T_D) % T_NS);
+        issue_b(2 * kb + 2, (2 * j + 2) % 3);
+        issue_a(min(kb + 2, KB - 1), (j + 2) % 3);
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t st = lds_addr(lds[j]) + lane * 16;
-        v4i av[8];
-#pragma unroll
-        for (int mi = 0; mi < 8; mi++) av[mi] = ds_read16(st, mi * 1024);
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(av[4]), "+v"(av[5]),
-                       "+v"(av[6]), "+v"(av[7]));
-#pragma unroll
-        for (int mi = 0; mi < 8; mi++)
-#pragma unroll
-            for (int f = 0; f < T_WF; f++) acc[mi][f] = mfma_i8(av[mi], bq[j][f], acc[mi][f]);
+        const uint32_t st = lds_addr(lds[j % 3]);
+        half(st + rd0, (2 * j) % 3, -1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_b(2 * kb + 3, (2 * j) % 3);
+        __builtin_amdgcn_sched_barrier(0);
+        VMCNT_WAIT(12);                /* B(2kb+1): three groups were issued after it */
+        /* a half last step (Kd % 128 == 64): the second half's B is zeroed
+         * (no branch, which would cost registers) */
+        half(st + rd1, (2 * j + 1) % 3, __builtin_amdgcn_readfirstlane(2 * kb + 1 < KH ? -1 : 0));
         __builtin_amdgcn_sched_barrier(0);
     };
-    /* rounds of T_NS steps keep the ring indices compile-time */
+    /* rounds of 6 steps keep the slot and stage indices compile-time */
     int k0 = 0;
-    for (; k0 + T_NS <= KB; k0 += T_NS) {
+    for (; k0 + 6 <= KB; k0 += 6) {
 #pragma unroll
-        for (int j = 0; j < T_NS; j++) step(k0 + j, j);
+        for (int j = 0; j < 6; j++) step(k0 + j, j);
     }
 #pragma unroll
-    for (int j = 0; j < T_NS - 1; j++)
+    for (int j = 0; j < 5; j++)
         if (k0 + j < KB) step(k0 + j, j);
     VMCNT_WAIT(0);   /* the trailing groups land before the next tile reuses the stages */
 
@@ -923,16 +969,21 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
  * and from that XCD's L2 for the other row groups (the tiles of a hot
  * expert are consecutive row groups). */
 extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[T_NS][T_ASTAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t lds[T_NSA][T_ASTAGE];
     __shared__ int32_t s_arow[MM_I8T_BM], s_rid[MM_I8T_BM];
     __shared__ float s_sa[MM_I8T_BM];
     const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
     const int nslab = (nfr_total + MM_I8T_FR - 1) / MM_I8T_FR;
     const int b = blockIdx.x;
     const int xcd = b % MM_I8S_XCD, j = b / MM_I8S_XCD;
+#ifdef T_MAP_SLAB_MINOR
+    const int slab = j % nslab;
+    const int grp = (j / nslab) * MM_I8S_XCD + xcd;
+#else
     const int q = (j / MM_I8S_XCD) * MM_I8S_XCD + xcd;   /* (slab, row-group run) index */
     const int slab = q % nslab;
     const int grp = (q / nslab) * MM_I8S_XCD + j % MM_I8S_XCD;
+#endif
     if (grp >= a.max_groups) return;                      /* uniform per block */
     int e, g0, M;
     if (!tile_owner(a, grp, &e, &g0, &M)) return;
