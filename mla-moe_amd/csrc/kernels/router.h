@@ -28,7 +28,9 @@
 #define MM_ROUTER_CHUNK_FLOATS 8192   /* router-weight chunk: HC rows x E experts */
 #define MM_ROUTER_TOKENS (MM_ROUTER_WAVES * MM_ROUTER_TPW)
 #define MM_ROUTER_XCHUNK_FLOATS (MM_ROUTER_TOKENS * (MM_ROUTER_CHUNK_FLOATS / MM_WAVE))
-#define MM_ROUTER_BUF_FLOATS (MM_ROUTER_CHUNK_FLOATS + MM_ROUTER_XCHUNK_FLOATS)
+/* weight chunk widened to fp32 with 4 pad floats per expert row (at most 256
+ * rows), then the token columns */
+#define MM_ROUTER_BUF_FLOATS (MM_ROUTER_CHUNK_FLOATS + 4 * 256 + MM_ROUTER_XCHUNK_FLOATS)
 #define MM_ROUTER_LDS_FLOATS (2 * MM_ROUTER_BUF_FLOATS)
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
@@ -44,10 +46,10 @@ struct router_no_post {
  *
  * The router weight is used in its checkpoint layout, W [E][H] bf16 (its
  * fp32 values are exact).  It is consumed in chunks of HC hidden indices:
- * the chunk's [E][HC] block of W (16 KB) goes to LDS expert-major with rows
- * padded by 16 bytes, so that a lane reads the next 8 weights of its expert
- * with one conflict-free 16-byte read; the same HC columns of the block's
- * token rows ([tokens][HC] fp32) go beside it.  Chunks are loaded into
+ * the chunk's [E][HC] block of W (16 KB of bf16) goes to LDS widened to
+ * fp32, expert-major with rows padded by 16 bytes, so that a lane reads the
+ * next 4 weights of its expert with one conflict-free 16-byte read; the same
+ * HC columns of the block's token rows ([tokens][HC] fp32) go beside it.  Chunks are loaded into
  * registers RL_PF chunks ahead of their use and written to one of two LDS
  * buffers when their turn comes, so the serial add chains (one add per
  * hidden index, in the reference's ascending order) rarely wait for memory.
@@ -61,8 +63,8 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int E = a.E, H = a.H, T = a.T;
     constexpr int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* hidden indices per chunk */
-    constexpr int RS = HC + 8;                                    /* padded LDS row, bf16 */
-    constexpr int WLDS = MM_WAVE * EJ * RS * 2;                   /* weight bytes in LDS */
+    constexpr int RS = HC + 4;                                    /* padded LDS row, fp32 */
+    constexpr int WLDS = MM_WAVE * EJ * RS * 4;                   /* weight bytes in LDS */
     constexpr int XB = MM_ROUTER_TOKENS * HC * 4;                 /* x bytes per chunk */
     constexpr int BUF = WLDS + XB;                                /* LDS bytes per buffer */
     static_assert(2 * BUF <= MM_ROUTER_LDS_FLOATS * 4, "router LDS");
@@ -106,9 +108,17 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
     auto store = [&](int slot, uint8_t *buf) {
 #pragma unroll
         for (int k = 0; k < WP; k++) {
+            /* the bf16 weights widened to fp32 once here (exact), so the
+             * serial compute below spends no instruction on unpacking */
             const int i = threadIdx.x + k * MM_ROUTER_THREADS;
             const int e = i / PPE, o = (i % PPE) * 8;
-            *(u32x4 *)(buf + ((size_t)e * RS + o) * 2) = wr[slot][k];
+            const u32x4 d = wr[slot][k];
+            const f32x4 lo = {__uint_as_float(d.x << 16), __uint_as_float(d.x & 0xffff0000u),
+                              __uint_as_float(d.y << 16), __uint_as_float(d.y & 0xffff0000u)};
+            const f32x4 hi = {__uint_as_float(d.z << 16), __uint_as_float(d.z & 0xffff0000u),
+                              __uint_as_float(d.w << 16), __uint_as_float(d.w & 0xffff0000u)};
+            *(f32x4 *)(buf + ((size_t)e * RS + o) * 4) = lo;
+            *(f32x4 *)(buf + ((size_t)e * RS + o + 4) * 4) = hi;
         }
 #pragma unroll
         for (int k = 0; k < XP; k++) {
@@ -123,14 +133,16 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
          * acc + (+0) = acc exactly (acc starts at +0 and never becomes -0
          * under round-to-nearest), so the whole chunk is consumed with a
          * constant trip count and the result is bit-identical. */
-        const uint8_t *wb = buf + (size_t)lane * RS * 2;
+        const float *wb = (const float *)buf + (size_t)lane * RS;
         const float *xb = (const float *)(buf + WLDS) + tw * HC;
-        u32x4 wq[2][EJ];
-        float xv[2][TPW][8];
+        f32x4 wq[3][EJ][2];
+        float xv[3][TPW][8];
         auto load = [&](int s, int i0) {
 #pragma unroll
-            for (int j = 0; j < EJ; j++)
-                wq[s][j] = *(const u32x4 *)(wb + ((size_t)j * MM_WAVE * RS + i0) * 2);
+            for (int j = 0; j < EJ; j++) {
+                wq[s][j][0] = *(const f32x4 *)(wb + (size_t)j * MM_WAVE * RS + i0);
+                wq[s][j][1] = *(const f32x4 *)(wb + (size_t)j * MM_WAVE * RS + i0 + 4);
+            }
 #pragma unroll
             for (int t = 0; t < TPW; t++) {
                 const f32x4 lo = *(const f32x4 *)(xb + t * HC + i0);
@@ -149,8 +161,7 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
             for (int u = 0; u < 8; u++)
 #pragma unroll
                 for (int j = 0; j < EJ; j++) {
-                    const uint32_t d = wq[s][j][u >> 1];
-                    const float w = __uint_as_float((u & 1) ? (d & 0xffff0000u) : (d << 16));
+                    const float w = wq[s][j][u >> 2][u & 3];
 #pragma unroll
                     for (int t = 0; t < NT; t++) prod[u][t][j] = xv[s][t][u] * w;
                 }
@@ -161,12 +172,15 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
 #pragma unroll
                     for (int j = 0; j < EJ; j++) lg[t][j] = lg[t][j] + prod[u][t][j];
         };
+        /* LDS reads run two groups of 8 ahead of the adds (an LDS round trip
+         * is longer than one group's 8 dependent adds) */
         auto run = [&](auto nt) {
             load(0, 0);
+            load(1, 8);
 #pragma unroll
             for (int g = 0; g < HC / 8; g++) {
-                if (g + 1 < HC / 8) load((g + 1) & 1, (g + 1) * 8);
-                comp(g & 1, nt);
+                if (g + 2 < HC / 8) load((g + 2) % 3, (g + 2) * 8);
+                comp(g % 3, nt);
             }
         };
         if (TPW == 1 || t0 + TPW <= T)
