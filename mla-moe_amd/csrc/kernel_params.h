@@ -157,15 +157,18 @@ typedef struct {
  * number of blocks per expert.  The shared expert's row tiles go to
  * MM_I8S_RT blocks 8 block ids apart (one XCD), so that their identical
  * weight reads meet in that XCD's L2. */
+/* Swept on MI355X at the config-4 shape (B = 64, DeepSeek-V2-Lite layer):
+ * 6 waves with rings of 3 (gate/up, 2 KB per step) and 6 (down, 1 KB) steps
+ * beat 4, 5, 7, 8, 12 and 16 waves and deeper rings by 3-6% per step. */
 #ifndef MM_I8S_W
-#define MM_I8S_W 8                 /* waves per block */
+#define MM_I8S_W 6                 /* waves per block */
 #endif
 #ifndef MM_I8S_SEG
 #define MM_I8S_SEG 1               /* column blocks per wave (<= 4) */
 #endif
 #ifndef MM_I8S_DEPTH_GU
-#define MM_I8S_DEPTH_GU 4          /* K steps of weight fragments in flight per wave */
-#define MM_I8S_DEPTH_DOWN 8
+#define MM_I8S_DEPTH_GU 3          /* K steps of weight fragments in flight per wave */
+#define MM_I8S_DEPTH_DOWN 6
 #endif
 #define MM_I8S_RT 4                /* row-tile blocks per shared-expert column group */
 #define MM_I8S_XCD 8               /* blocks are dealt to XCDs round robin */
