@@ -176,7 +176,10 @@ typedef struct {
 /* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
  * the routed experts' row lists (or all T rows for the shared expert). */
 #define MM_I8T_BM 128     /* rows per tile */
-#define MM_I8T_FR 16      /* B fragments (16 packed columns each) per column slab */
+#ifndef MM_I8T_FR
+#define MM_I8T_FR 8       /* B fragments (16 packed columns each) per column slab;
+                             8 (2 per wave) beat 16 by 13% at config 3 */
+#endif
 typedef struct {
     const int8_t *b;         /* packed fragments of expert 0 */
     size_t b_expert_stride;  /* bytes between experts' fragment sets */

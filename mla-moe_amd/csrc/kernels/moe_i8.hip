@@ -721,19 +721,19 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
 
 /* ---- tiled grouped GEMM (prefill) ------------------------------------------- */
 
-/* Block tile: MM_I8T_BM = 128 rows x MM_I8T_FR = 16 B fragments (gate/up: 8
- * column blocks of 16 with their gate and up fragments = 128 output columns;
- * plain: 16 column blocks = 256 output columns), K step 128 (two MFMA K
- * halves of 64).  The four waves split the fragments (4 each) and share the
- * rows.  The gathered A rows of a K step are staged through a 3-stage LDS
+/* Block tile: MM_I8T_BM = 128 rows x MM_I8T_FR B fragments (gate/up: the
+ * gate and up fragments of MM_I8T_FR / 2 column blocks of 16; plain:
+ * MM_I8T_FR column blocks), K step 128 (two MFMA K halves of 64).  The four
+ * waves split the fragments (MM_I8T_FR / 4 each) and share the rows.  The gathered A rows of a K step are staged through a 3-stage LDS
  * ring by direct global -> LDS loads of whole cache lines (8 rows x 128 B per
  * instruction: half-line accesses measured ~2.6x slower), XOR-swizzled so
  * that the operand reads are conflict-free, two steps ahead.  Every wave
  * streams its own B fragments (packed, 1 KB contiguous) with buffer loads
  * (scalar base and step offset, one lane-offset register) into a ring of
- * three 64-byte K halves, two halves ahead.  A wave tile is 128 x 4
- * fragments = 32 v_mfma_i32_16x16x64_i8 per K half; 2 blocks fit a CU. */
-#define T_WF 4                    /* B fragments per wave */
+ * three 64-byte K halves, two halves ahead.  A wave tile is 128 rows x
+ * MM_I8T_FR / 4 fragments (8 v_mfma_i32_16x16x64_i8 per fragment and K
+ * half); 2 blocks fit a CU. */
+#define T_WF (MM_I8T_FR / 4)      /* B fragments per wave */
 #define T_NSA 3                   /* A stages (issued 2 steps ahead) */
 #define T_ASTAGE (128 * 128)      /* one K step of A: 128 rows x 128 B */
 
@@ -785,7 +785,7 @@ __device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, 
     return s_e >= 0;
 }
 
-/* One 128-row x 16-fragment tile starting at row m0 of expert e (M rows). */
+/* One 128-row x MM_I8T_FR-fragment tile starting at row m0 of expert e (M rows). */
 __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_ASTAGE],
                                            int32_t *s_arow, float *s_sa, int32_t *s_rid,
                                            int e, int m0, int M, int slab) {
@@ -891,7 +891,8 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
         }
     };
     auto step = [&](int kb, int j) {   /* j = kb % 6: A stage j % 3, B slots (2j) % 3, (2j+1) % 3 */
-        VMCNT_WAIT(8);                 /* A(kb) and B(2kb) of this wave have landed */
+        VMCNT_WAIT(4 + T_WF);          /* A(kb) and B(2kb) of this wave have landed: only
+                                          A(kb+1) and B(2kb+1) came after B(2kb) */
         __builtin_amdgcn_s_barrier();  /* every wave's A part of step kb has landed,
                                           and step kb-1's stage is no longer read */
         __builtin_amdgcn_sched_barrier(0);
@@ -903,7 +904,7 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
         __builtin_amdgcn_sched_barrier(0);
         issue_b(2 * kb + 3, (2 * j) % 3);
         __builtin_amdgcn_sched_barrier(0);
-        VMCNT_WAIT(12);                /* B(2kb+1): three groups were issued after it */
+        VMCNT_WAIT(2 * T_WF + 4);      /* B(2kb+1): B(2kb+2), A(kb+2), B(2kb+3) came after it */
         /* a half last step (Kd % 128 == 64): the second half's B is zeroed
          * (no branch, which would cost registers) */
         half(st + rd1, (2 * j + 1) % 3, __builtin_amdgcn_readfirstlane(2 * kb + 1 < KH ? -1 : 0));
@@ -968,7 +969,10 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
  * groups of ONE slab: the slab's weights then come from HBM once per run
  * and from that XCD's L2 for the other row groups (the tiles of a hot
  * expert are consecutive row groups). */
-extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
+#ifndef T_OCC
+#define T_OCC 2                   /* blocks per CU the register budget is sized for */
+#endif
+extern "C" __global__ __launch_bounds__(256, T_OCC) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[T_NSA][T_ASTAGE];
     __shared__ int32_t s_arow[MM_I8T_BM], s_rid[MM_I8T_BM];
     __shared__ float s_sa[MM_I8T_BM];
