@@ -25,11 +25,23 @@ int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, i
     mm_cvt_bf16_args ca = {x, xh, xl, T, n_in, kp, split};
     const size_t chunks = (size_t)T * kp / 8;
     if ((st = mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca))) return st;
-    mm_gemm_bf16_args a = {xh, xl, w, y, T, d_out, n_in, kp, split, (flags & MM_MATMUL_ACCUMULATE) != 0};
-    /* LDS ring: 4 stages of A and B (32 KB) or 3 of A hi, A lo and B (48 KB);
-     * a 1-D grid of 8 XCD columns, each with every row block of its column
-     * blocks (the kernel maps blocks to tiles) */
-    const size_t lds = split ? (size_t)3 * 49152 : (size_t)4 * 32768;
-    const size_t nbx = ((size_t)d_out + 127) / 128, nby = ((size_t)T + 127) / 128;
+    /* block tile columns: the widest of 128, 64, 32 that still gives 192
+     * tiles (most of the 256 CUs), else 32 -- the projections of this path
+     * have too few 128 x 128 tiles to fill the machine (measured per width) */
+    const size_t nby = ((size_t)T + 127) / 128;
+    int bn = 32;
+    for (int cw = 128; cw >= 64; cw /= 2)
+        if (((size_t)d_out + cw - 1) / cw * nby >= 192) {
+            bn = cw;
+            break;
+        }
+    const size_t nbx = ((size_t)d_out + bn - 1) / bn;
+    mm_gemm_bf16_args a = {xh, xl, w, y, T, d_out, n_in, kp, split, (flags & MM_MATMUL_ACCUMULATE) != 0, bn};
+    /* LDS ring: 4 stages (3 for the hi/lo split) of A hi [, A lo] (16 KB
+     * each) and bn rows of B (128 B each); a 1-D grid of 8 XCD columns, each
+     * with every row block of its column blocks (the kernel maps blocks to
+     * tiles) */
+    const size_t stage = (size_t)(split ? 2 : 1) * 16384 + (size_t)bn * 128;
+    const size_t lds = (split ? 3 : 4) * stage;
     return mm_launch(c, K_GEMM_BF16, (unsigned)(8 * ((nbx + 7) / 8) * nby), 1, 1, 256, lds, &a);
 }

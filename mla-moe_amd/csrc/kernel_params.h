@@ -269,4 +269,5 @@ typedef struct {
     int T, d_out, n_in, kp;
     int split;               /* 1: two MFMAs per product (x = hi + lo) */
     int accumulate;
+    int bn;                  /* block tile columns: 128, 64 or 32 */
 } mm_gemm_bf16_args;

@@ -22,9 +22,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 #define GB_BM 128
-#define GB_BN 128
 #define GB_BK 64
-#define GB_COPY (128 * 128)             /* one operand of one stage: 128 rows x 128 B */
+#define GB_COPY (128 * 128)             /* A of one stage: 128 rows x 128 B */
 
 __device__ __forceinline__ uint16_t rne16(float x) {
     uint32_t u = __float_as_uint(x);
@@ -68,14 +67,15 @@ extern "C" __global__ __launch_bounds__(256) void mm_cvt_bf16(mm_cvt_bf16_args a
  * makes the operand reads below (16 rows, one chunk each) conflict-free. */
 __device__ __forceinline__ int gb_swz(int R) { return (R >> 1) & 7; }
 
-template <bool HL>
+template <bool HL, int GB_BN>
 __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *lds) {
-    constexpr int NCOPY = HL ? 3 : 2;
-    constexpr int SB = NCOPY * GB_COPY;          /* stage bytes */
-    constexpr int BOFF = (NCOPY - 1) * GB_COPY;
-    constexpr int NS = HL ? 3 : 4;               /* stages */
-    constexpr int D = NS - 1;                    /* steps issued ahead */
-    constexpr int G = 4 * NCOPY;                 /* transfers per wave per step */
+    constexpr int GB_NC = GB_BN / 32;             /* B fragments of 16 columns per wave */
+    constexpr int NA = HL ? 2 : 1;                /* A copies: hi (and lo) */
+    constexpr int BOFF = NA * GB_COPY;
+    constexpr int SB = BOFF + GB_BN * 128;        /* stage bytes */
+    constexpr int NS = HL ? 3 : 4;                /* stages */
+    constexpr int D = NS - 1;                     /* steps issued ahead */
+    constexpr int G = 4 * NA + GB_NC;             /* transfers per wave per step */
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -90,22 +90,26 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
     const int m0 = rb * GB_BM, n0 = cb * GB_BN;
     const int K = a.n_in, KB = a.kp / GB_BK;
 
-    /* wave w issues instructions 4 w .. 4 w + 3 (rows 32 w .. 32 w + 31) of A
-     * (hi, lo) and of B; rows past T / columns past d_out read the last one
-     * (results discarded); B chunks past n_in re-read chunk 0 of the row (A
-     * is zero there) */
-    const uint16_t *ah_src[4], *al_src[4], *b_src[4];
-    int bq[4];
+    /* wave w issues A instructions 4 w .. 4 w + 3 (rows 32 w .. 32 w + 31)
+     * (hi, lo) and B instructions GB_NC w .. GB_NC w + GB_NC - 1; rows past
+     * T / columns past d_out read the last one (results discarded); B chunks
+     * past n_in re-read chunk 0 of the row (A is zero there) */
+    const uint16_t *ah_src[4], *al_src[4], *b_src[GB_NC];
+    int bq[GB_NC];
 #pragma unroll
     for (int h = 0; h < 4; h++) {
         const int R = 8 * (4 * wave + h) + (lane >> 3);
         const int kq = 8 * ((lane & 7) ^ gb_swz(R));      /* element offset in the step */
         const int m = min(m0 + R, a.T - 1);
-        const int n = min(n0 + R, a.d_out - 1);
         ah_src[h] = a.xh + (size_t)m * a.kp + kq;
         al_src[h] = HL ? a.xl + (size_t)m * a.kp + kq : nullptr;
+    }
+#pragma unroll
+    for (int h = 0; h < GB_NC; h++) {
+        const int R = 8 * (GB_NC * wave + h) + (lane >> 3);
+        const int n = min(n0 + R, a.d_out - 1);
         b_src[h] = a.w + (size_t)n * K;
-        bq[h] = kq;
+        bq[h] = 8 * ((lane & 7) ^ gb_swz(R));
     }
     auto issue = [&](int kb, int st) {
         uint8_t *s0 = lds + st * SB;
@@ -114,8 +118,11 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
             const int i = 4 * wave + h;
             lds_dma16(ah_src[h] + kb * GB_BK, s0 + i * 1024);
             if (HL) lds_dma16(al_src[h] + kb * GB_BK, s0 + GB_COPY + i * 1024);
+        }
+#pragma unroll
+        for (int h = 0; h < GB_NC; h++) {
             const int k = kb * GB_BK + bq[h];
-            lds_dma16(b_src[h] + (k < K ? k : 0), s0 + BOFF + i * 1024);
+            lds_dma16(b_src[h] + (k < K ? k : 0), s0 + BOFF + (GB_NC * wave + h) * 1024);
         }
     };
     /* operand read of lane (c = l % 16, g = l / 16) for fragment row block r
@@ -125,11 +132,11 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
     const uint32_t rd0 = c16 * 128 + 16 * ((0 + g4) ^ gb_swz(c16));
     const uint32_t rd1 = c16 * 128 + 16 * ((4 + g4) ^ gb_swz(c16));
 
-    f32x4 acc[4][4];
+    f32x4 acc[4][GB_NC];
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[r][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < GB_NC; c++) acc[r][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
     /* every step issues one group (steps past the end re-load the last, so
      * that the wait counts are static) */
@@ -142,12 +149,12 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
         __builtin_amdgcn_sched_barrier(0);
         issue(min(kb + D, KB - 1), (j + D) % NS);
         __builtin_amdgcn_sched_barrier(0);
-        /* this wave's A rows 64 wm .. and B columns 64 wn .. */
+        /* this wave's A rows 64 wm .. and B columns GB_BN / 2 * wn .. */
         const uint32_t st0 = lds_addr(lds + j * SB);
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
             const uint32_t sa = st0 + (kh ? rd1 : rd0) + wm * 64 * 128;
-            const uint32_t sb = st0 + BOFF + (kh ? rd1 : rd0) + wn * 64 * 128;
+            const uint32_t sb = st0 + BOFF + (kh ? rd1 : rd0) + wn * (GB_BN / 2) * 128;
             i32x4 ah[4], al[4], bw[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -155,7 +162,7 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
                 if (HL) al[r] = ds_read16(sa, GB_COPY + r * 2048);
             }
 #pragma unroll
-            for (int c = 0; c < 4; c++) bw[c] = ds_read16(sb, c * 2048);
+            for (int c = 0; c < GB_NC; c++) bw[c] = ds_read16(sb, c * 2048);
             if (HL)
                 asm volatile("s_waitcnt lgkmcnt(0)"
                              : "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(al[0]), "+v"(al[1]),
@@ -167,7 +174,7 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
+                for (int c = 0; c < GB_NC; c++) {
                     const bf16x8 bb = __builtin_bit_cast(bf16x8, bw[c]);
                     acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[r]), bb,
                                                                         acc[r][c], 0, 0, 0);
@@ -192,8 +199,8 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int n = n0 + 64 * wn + 16 * c + (lane & 15);
+        for (int c = 0; c < GB_NC; c++) {
+            const int n = n0 + (GB_BN / 2) * wn + 16 * c + (lane & 15);
             if (n >= a.d_out) continue;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -210,6 +217,13 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
  * 3 x 48 KB (hi/lo x). */
 extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t glds[];
-    if (a.split) gemm_block<true>(a, glds);
-    else gemm_block<false>(a, glds);
+    if (a.split) {
+        if (a.bn == 128) gemm_block<true, 128>(a, glds);
+        else if (a.bn == 64) gemm_block<true, 64>(a, glds);
+        else gemm_block<true, 32>(a, glds);
+    } else {
+        if (a.bn == 128) gemm_block<false, 128>(a, glds);
+        else if (a.bn == 64) gemm_block<false, 64>(a, glds);
+        else gemm_block<false, 32>(a, glds);
+    }
 }
