@@ -104,8 +104,9 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                            part_o, probs, kv_len, NH, HG, nchunks, QKN};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
-    const size_t alds = (size_t)4 * 2 * (16 * 1056 + 16 * 128);
-    if ((st = mm_launch(c, K_MLA_ATTN, (unsigned)nchunks, (unsigned)B, (unsigned)HG, 256, alds, &aa)))
+    const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
+    if ((st = mm_launch(c, K_MLA_ATTN, (unsigned)nchunks, (unsigned)B, (unsigned)HG, 64 * MM_MLA_AW, alds,
+                        &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks};

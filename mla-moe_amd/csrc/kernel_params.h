@@ -205,7 +205,13 @@ typedef struct {
 #define MM_MLA_QKR 64             /* qk_rope_head_dim served by the kernels */
 #define MM_MLA_KVD (MM_MLA_KVL + MM_MLA_QKR)
 #define MM_MLA_KC (MM_MLA_KVD / 32) /* 32-wide latent chunks of one cache row */
-#define MM_MLA_CHUNK 512          /* keys per attention block (2 waves x 256) */
+#ifndef MM_MLA_CHUNK
+#define MM_MLA_CHUNK 512          /* keys per attention block */
+#endif
+#ifndef MM_MLA_AW
+#define MM_MLA_AW 4               /* waves per attention block */
+#endif
+#define MM_MLA_TILE_B (16 * 1056 + 16 * 128)   /* LDS bytes of one 16-key sub-tile */
 
 /* qabs = q_nope . W_UK per head. */
 typedef struct {

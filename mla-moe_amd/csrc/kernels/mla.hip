@@ -151,10 +151,11 @@ __device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr, int off) {
     return r;
 }
 
-#define AW 4                      /* waves per attention block */
+#define AW MM_MLA_AW               /* waves per attention block */
 #define KPW (MM_MLA_CHUNK / AW)   /* keys per wave */
 #define CROW_B 1056               /* bytes per LDS c_kv row: 1024 + 32 pad */
 #define TILE_B (16 * CROW_B + 16 * 128)   /* 16 keys: c_kv rows, then the k_pe parts */
+static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
 #define OROW (KVL + 4)            /* floats per head row of the merge buffer */
 /* Rescaling is lazy: a head's running maximum m moves only when a score
  * exceeds it by more than RESCALE_TAU, so exp(s - m) <= e^RESCALE_TAU and the
