@@ -34,7 +34,8 @@ def test_matmul_golden(ctx, oracle):
 
 
 @pytest.mark.parametrize("T,d_out,n_in", [(1, 64, 2048), (37, 100, 264), (512, 576, 2048),
-                                          (512, 4096, 512), (70, 3072, 2048)])
+                                          (512, 4096, 512), (70, 3072, 2048),
+                                          (1024, 3072, 136)])   # 128-column tiles
 def test_matmul_shapes(ctx, oracle, T, d_out, n_in):
     print(f"matmul T={T} d_out={d_out} n_in={n_in}", flush=True)
     rng = np.random.default_rng(T + d_out)
@@ -61,3 +62,15 @@ def test_matmul_integer_exact(ctx):
     exact = (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
     got = ctx.matmul(x, synth.bf16_from_f32(w), mlamoe.MM_MATMUL_X_BF16)
     assert np.array_equal(got, exact)
+
+
+def test_matmul_empty_is_a_no_op(ctx):
+    """T = 0: no launch, y untouched."""
+    y = ctx.empty((1, 64), np.float32)
+    ctx.fill(y, 64, mlamoe.MM_FILL_F32_NORMAL, 5, 1.0)
+    before = y.download()
+    x = ctx.empty((1, 128), np.float32)
+    w = ctx.empty((64, 128), np.uint16)
+    ctx.matmul_dev(y, x, w, 64, 128, 0)
+    ctx.sync()
+    assert np.array_equal(y.download(), before)

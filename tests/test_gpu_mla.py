@@ -72,6 +72,11 @@ def test_mla_lengths(ctx, oracle, kv_len):
     run_case(ctx, oracle, 16, 2, max(kv_len, 1), kv_len, 600 + kv_len)
 
 
+def test_mla_longest_context(ctx, oracle):
+    """kv_len = 64 chunks x 512 keys, the most the chunk merge serves."""
+    run_case(ctx, oracle, 16, 1, 32768, 32768, 640)
+
+
 def test_mla_ragged_batch(ctx, oracle):
     """Per-sequence lengths, including one sequence shorter than a sub-tile
     and chunks with no valid keys."""

@@ -205,3 +205,24 @@ def test_i8_dsv2_prefill_skewed(ctx, oracle):
         assert np.array_equal(dd["acc_gu"][rid, 0], _dot_exact(dd["qx"][t:t + 1], qw["qeg"][e])[0])
         assert np.array_equal(dd["acc_d"][rid], _dot_exact(dd["qh"][rid:rid + 1], qw["qed"][e])[0])
     assert max_abs_rel(out, ro) < TOL
+
+
+@pytest.mark.parametrize("E", [100, 160])
+def test_i8_many_experts(ctx, oracle, E):
+    """More than 64 experts (two or four per router lane), top-8, with the
+    row lists of the tiled path spread over all of them."""
+    run_case(ctx, oracle, 256, E, 8, 128, 1, 40, 97, check_all=False)
+
+
+def test_i8_empty_batch_is_a_no_op(ctx):
+    """T = 0: nothing is launched and the output is untouched."""
+    H, E, K, I, NS = 128, 8, 2, 64, 1
+    w = synth.moe_layer(98, H, E, I, NS)
+    ctx.moe_init(H, E, NS, K, I)
+    ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8)
+    out = ctx.empty((1, H), np.float32)
+    ctx.fill(out, H, mlamoe.MM_FILL_F32_NORMAL, 99, 1.0)
+    before = out.download()
+    ctx.moe_forward_dev(0, 0, None, out, flags=mlamoe.MM_FWD_INT8)
+    ctx.sync()
+    assert np.array_equal(out.download(), before)
