@@ -38,4 +38,11 @@ mm_co_mla:
 mm_co_gemm_bf16:
     .incbin "gemm_bf16.hsaco"
 
+    .balign 4096
+    .globl mm_co_gemm_i8
+    .hidden mm_co_gemm_i8
+    .type mm_co_gemm_i8, @object
+mm_co_gemm_i8:
+    .incbin "gemm_i8.hsaco"
+
     .section .note.GNU-stack, "", @progbits

@@ -19,11 +19,12 @@ extern const unsigned char mm_co_util[];
 extern const unsigned char mm_co_moe_i8[];
 extern const unsigned char mm_co_mla[];
 extern const unsigned char mm_co_gemm_bf16[];
+extern const unsigned char mm_co_gemm_i8[];
 
-enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_GEMM_BF16, MOD_COUNT };
+enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_GEMM_BF16, MOD_GEMM_I8, MOD_COUNT };
 static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util,
                                                           mm_co_moe_i8, mm_co_mla,
-                                                          mm_co_gemm_bf16};
+                                                          mm_co_gemm_bf16, mm_co_gemm_i8};
 
 static const struct {
     const char *name;
@@ -42,6 +43,7 @@ static const struct {
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
     [K_I8_TILED] = {"mm_i8_gemm_tiled", MOD_MOE_I8},
+    [K_I8_BT] = {"mm_i8_gemm_bt", MOD_GEMM_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
@@ -126,6 +128,9 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->i8_tiled_min_t = 256;
     const char *ev = getenv("MLAMOE_I8_TILED_MIN_T");
     if (ev && *ev) c->i8_tiled_min_t = atoi(ev);
+    c->i8_bt = 1;
+    ev = getenv("MLAMOE_I8_BT");
+    if (ev && *ev) c->i8_bt = atoi(ev);
     *out = c;
     return MM_OK;
 fail:

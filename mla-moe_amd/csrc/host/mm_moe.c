@@ -332,6 +332,16 @@ static unsigned tiled_blocks(unsigned nslab, unsigned groups) {
     return (unsigned)(ceil_div(runs, MM_I8S_XCD) * MM_I8S_XCD * MM_I8S_XCD);
 }
 
+/* One tiled grouped GEMM: the big-tile kernel (16-fragment slabs, one block
+ * per CU) or the 8-fragment tiled kernel.  `nfr` is the B fragment count of
+ * one expert, `groups` an upper bound on its row groups. */
+static int launch_tiled(mm_ctx *c, mm_i8_tiled_args *ta, unsigned nfr, unsigned groups) {
+    if (c->i8_bt)   /* persistent: two blocks per CU */
+        return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, ta);
+    return mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr, MM_I8T_FR), groups), 1, 1,
+                     256, 0, ta);
+}
+
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
                         const mm_moe_i8_debug *dbg) {
@@ -341,11 +351,15 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const size_t R = (size_t)T * K;   /* routed rows */
     mm_plan p = {0};
     const size_t o_rows = plan_take(&p, E * T * 4), o_qx = plan_take(&p, (size_t)T * H);
-    const size_t o_sx = plan_take(&p, (size_t)T * 4), o_h = plan_take(&p, R * I * 4);
-    const size_t o_hs = plan_take(&p, (size_t)T * S * 4), o_qh = plan_take(&p, R * I);
+    /* GEMM outputs carry one spare row (+256 floats) that absorbs the
+     * big-tile kernel's stores of padded rows and columns */
+#define SPARE(rows, n) ((((size_t)(rows) + 1) * (n) + 256) * 4)
+    const size_t o_sx = plan_take(&p, (size_t)T * 4), o_h = plan_take(&p, SPARE(R, I));
+    const size_t o_hs = plan_take(&p, SPARE(T, S)), o_qh = plan_take(&p, R * I);
     const size_t o_sh = plan_take(&p, R * 4), o_qhs = plan_take(&p, (size_t)T * S);
-    const size_t o_shs = plan_take(&p, (size_t)T * 4), o_y = plan_take(&p, R * H * 4);
-    const size_t o_ys = plan_take(&p, (size_t)T * H * 4), o_i = plan_take(&p, R * 4);
+    const size_t o_shs = plan_take(&p, (size_t)T * 4), o_y = plan_take(&p, SPARE(R, H));
+    const size_t o_ys = plan_take(&p, SPARE(T, H)), o_i = plan_take(&p, R * 4);
+#undef SPARE
     const size_t o_w = plan_take(&p, R * 4), o_lg = plan_take(&p, logits ? 0 : (size_t)T * E * 4);
     char *ws;
     int st = mm_workspace(c, p.off, (void **)&ws);
@@ -430,16 +444,13 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         /* routed experts, then the shared expert as one dense GEMM */
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
-                               (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(2 * I / 16, MM_I8T_FR), mt_routed), 1, 1, 256, 0,
-                            &ta)))
-            return st;
+                               (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed, (int)R};
+        if ((st = launch_tiled(c, &ta, (unsigned)(2 * I / 16), mt_routed))) return st;
         if (S) {
             mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
-                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(2 * S / 16, MM_I8T_FR), mt_shared), 1, 1,
-                                256, 0, &ts)))
-                return st;
+                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared,
+                                   T};
+            if ((st = launch_tiled(c, &ts, (unsigned)(2 * S / 16), mt_shared))) return st;
         }
     } else {
         /* shared-expert blocks (row-tile waves), then every routed unit */
@@ -459,15 +470,13 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     if (tiled) {
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
-                               0, I8T_MGROUP, (int)mt_routed};
-        if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(H / 16, MM_I8T_FR), mt_routed), 1, 1, 256, 0, &td)))
-            return st;
+                               0, I8T_MGROUP, (int)mt_routed, (int)R};
+        if ((st = launch_tiled(c, &td, (unsigned)(H / 16), mt_routed))) return st;
         if (S) {
             mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
-                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared};
-            if ((st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(H / 16, MM_I8T_FR), mt_shared), 1, 1, 256, 0,
-                                &tsd)))
-                return st;
+                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared,
+                                    T};
+            if ((st = launch_tiled(c, &tsd, (unsigned)(H / 16), mt_shared))) return st;
         }
     } else {
         ga.a = qh;

@@ -180,6 +180,11 @@ typedef struct {
 #define MM_I8T_FR 8       /* B fragments (16 packed columns each) per column slab;
                              8 (2 per wave) beat 16 by 13% at config 3 */
 #endif
+/* Big-tile variant (mm_i8_gemm_bt): 128 rows x 16 fragments per block, one
+ * block per CU, both operands staged through LDS. */
+#define MM_I8B_BM 128
+#define MM_I8B_FR 16
+#define MM_I8B_GRID 512          /* persistent grid: 2 blocks on each of 256 CUs */
 typedef struct {
     const int8_t *b;         /* packed fragments of expert 0 */
     size_t b_expert_stride;  /* bytes between experts' fragment sets */
@@ -198,6 +203,8 @@ typedef struct {
     int gu;                  /* 1: gate/up with SwiGLU epilogue, 0: plain dequantising GEMM */
     int mgroup;              /* consecutive 128-row tiles one block walks (weight reuse) */
     int max_groups;          /* grid.y bound */
+    int spare_row;           /* big-tile kernel: `out` has a spare row here (N + 256 floats)
+                                that absorbs the stores of padded rows and columns */
 } mm_i8_tiled_args;
 
 /* ---- MLA absorbed decode ----------------------------------------------------- */

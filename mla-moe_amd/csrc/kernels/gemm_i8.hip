@@ -1,0 +1,383 @@
+/* gemm_i8.hip -- big-tile grouped int8 GEMM for the prefill MoE FFN on
+ * v_mfma_i32_32x32x32_i8 (int32 accumulation).
+ *
+ * Same contract as mm_i8_gemm_tiled (moe_i8.hip): for each routed expert (or
+ * the shared expert as one dense GEMM) and each of its rows, out[rid] =
+ * dequant(qa[row] . qW^T), with the SwiGLU epilogue for gate/up; the
+ * weights are the packed 16-column x 64-K fragments of kernel_params.h.
+ *
+ * Block tile MM_I8B_BM = 128 rows x MM_I8B_FR = 16 fragments (gate/up: the
+ * gate and up fragments of 8 column blocks, 128 output columns; plain: 256
+ * output columns), K step (stage) 64 bytes.  Four waves in a 2 x 2 grid:
+ * wave (wr, wc) owns rows 64 wr .. + 63 and fragments 8 wc .. + 7, i.e. two
+ * 32-row blocks x four 32-column MFMA tiles (gate/up: gate and up of two
+ * 32-column pairs), 8 accumulators of 16 registers.
+ *
+ * The 32x32x32 MFMA is used because it keeps the pipe 85-90% busy at one or
+ * two waves per SIMD, where the 16x16x64 form is limited by issue to 58-75%
+ * (measured on MI355X).  Two blocks share a CU (72 KB of LDS each), so one
+ * block's set-up, load latency and epilogue overlap the other's MFMAs.
+ *
+ * Data path per stage: A rows (8 KB: 64 bytes of each row, 16-byte chunks
+ * XOR-swizzled by row) and B fragments (16 x 1 KB, one 64-byte K half) go
+ * global -> LDS by direct loads into a ring of three 24 KB stages, two
+ * stages ahead.  Operands of
+ * the next 32-byte K step are read from LDS while the 8 MFMAs of the current
+ * one run.  A 32x32x32 B operand (lane l: column l % 32, K bytes 16 (l / 32)
+ * .. + 15) is read straight out of two packed 16x64 fragments: the 16 bytes
+ * of (column c, K chunk q) sit at byte (16 q + c % 16) * 16 of fragment c / 16.
+ *
+ * MFMA 32x32x32 i8 layout: A lane l = row l % 32, K bytes 16 (l / 32) .. + 15;
+ * B likewise by column; result register 4 g + i of lane l is row
+ * 8 g + 4 (l / 32) + i, column l % 32.
+ */
+#include <type_traits>
+
+#include "i8_tile.h"
+
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+#define BT_A_BYTES (MM_I8B_BM * 64)
+#define BT_B_BYTES (MM_I8B_FR * 1024)
+#define BT_STAGE (BT_A_BYTES + BT_B_BYTES)
+#define BT_NS 3
+static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
+
+/* position of 16-byte chunk q of staged A row R (64 bytes per row): q ^ swz64(R);
+ * any 16 consecutive rows then cover all 64 banks once for a fixed q */
+__device__ __forceinline__ int swz64(int R) { return (R >> 2) & 3; }
+
+/* s_waitcnt lgkmcnt(0), tied to the operand registers it makes valid */
+__device__ __forceinline__ void lds_wait6(i32x4 (&A)[2], i32x4 (&B)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(A[0]), "+v"(A[1]), "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(B[3]));
+}
+
+/* Per-block schedule and row tables in LDS. */
+struct bt_shared {
+    int gstart[MM_EMAX + 1];                 /* exclusive prefix of 128-row groups per expert */
+    int arow[2][MM_I8B_BM];                  /* A row of each tile row (two tiles in flight) */
+    __attribute__((aligned(16))) int rid[2][MM_I8B_BM];     /* output row id, -1 = padding */
+    __attribute__((aligned(16))) float sa[2][MM_I8B_BM];    /* A row scale */
+};
+
+/* A tile of the grouped GEMM: expert e, column slab, rows m0 .. m0 + 127 of
+ * the expert's M rows. */
+struct bt_tile_id {
+    int e, slab, m0, M;
+};
+
+/* Tiles are ordered (expert, slab, row group): expert e owns tiles
+ * [nslab gstart[e], nslab gstart[e + 1]).  Uniform over the block. */
+__device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_tiled_args &a, const bt_shared &sh,
+                                                int nslab, int t) {
+    int lo = 0, hi = a.cnt ? a.E : 1;        /* largest e with nslab * gstart[e] <= t */
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (nslab * sh.gstart[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int ge = sh.gstart[lo + 1] - sh.gstart[lo];
+    const int loc = t - nslab * sh.gstart[lo];
+    bt_tile_id id;
+    id.e = lo;
+    id.slab = loc / ge;
+    id.m0 = (loc % ge) * MM_I8B_BM;
+    id.M = a.cnt ? min(a.cnt[lo], a.T) : a.T;
+    return id;
+}
+
+/* Row id and A row of tile row `r` (threads r < 128). */
+__device__ __forceinline__ void bt_row(const mm_i8_tiled_args &a, const bt_tile_id &id, int r,
+                                       int *rid, int *arow) {
+    const int m = id.m0 + r < id.M ? id.m0 + r : id.m0;
+    const int q = a.rows ? a.rows[(size_t)id.e * a.T + m] : m;
+    *arow = (a.a_by_route || !a.rows) ? q : q / a.K;
+    *rid = id.m0 + r < id.M ? q : -1;
+}
+
+template <bool GU>
+__device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, bt_shared &sh,
+                                       int t, int t_step, int t_end, int nslab) {
+    const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
+    const int wr = wave & 1, wc = wave >> 1;
+    const int KB = a.Kd / 64;               /* stages = 64-byte K halves of the packed fragments */
+    const int nfr_total = (GU ? 2 : 1) * (a.N / 16);
+    const int bstep = GU ? 2048 : 1024;
+    const uint32_t bytes_e = (uint32_t)(nfr_total * KB) * 1024u;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const uint32_t lds0 = lds_addr(lds);
+    constexpr int NT = GU ? 2 : 4;          /* output column tiles of 32 */
+
+    /* ---- per-tile load parameters ---- */
+    /* A loads: wave w issues instructions 2 w, 2 w + 1 of a stage (16 rows x
+     * 64 B each); lane l carries row R = 16 i + l / 4 and stores at position
+     * l % 4 of the row's 64 B the chunk (l % 4) ^ swz64(R).
+     * B loads: wave w loads fragments 4 w .. 4 w + 3 of the slab (clamped
+     * past the last; results discarded) at the stage's K half. */
+    uint32_t arow_off[2];
+    int aq[2];
+    __amdgpu_buffer_rsrc_t brs;
+    int bf0;
+    auto set_tile = [&](const bt_tile_id &id, int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int R = 16 * (2 * wave + h) + (lane >> 2);
+            arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)a.Kd;
+            aq[h] = 16 * ((lane & 3) ^ swz64(R));
+        }
+        brs = __builtin_amdgcn_make_buffer_rsrc((void *)(a.b + (size_t)id.e * a.b_expert_stride), 0,
+                                                (int)bytes_e, 0x00020000);
+        bf0 = __builtin_amdgcn_readfirstlane(id.slab * MM_I8B_FR + 4 * wave);
+    };
+    auto issue_stage = [&](int s) {   /* stage s into ring slot s % 3: 6 loads per wave */
+        const uint32_t st = (uint32_t)((s % BT_NS) * BT_STAGE);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            lds_dma16(a.a + (arow_off[h] + (uint32_t)(s * 64 + aq[h])),
+                      lds + st + (2 * wave + h) * 1024);
+        const int so = s * bstep;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int fr = min(bf0 + i, nfr_total - 1);
+            const int fo = GU ? ((fr >> 1) * 2 * KB + (fr & 1)) * 1024 : fr * KB * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                brs, (lds_void_t *)(lds + st + BT_A_BYTES + (4 * wave + i) * 1024), 16, lane * 16,
+                __builtin_amdgcn_readfirstlane(fo + so), 0, 0);
+        }
+    };
+    /* the stages issued ahead of a tile's K loop */
+    auto issue_head = [&]() {
+        for (int s = 0; s < min(BT_NS, KB); s++) issue_stage(s);
+    };
+
+    /* ---- operand reads ----
+     * K step ks (0, 1) of a stage:
+     *   A, row block ri: row 64 wr + 32 ri + l % 32, chunk 2 ks + l / 32
+     *     (swizzle depends on l % 32 only) -> + ri * 2048;
+     *   B, column tile cj: fragment j(cj) + (l % 32) / 16 * jstep of the
+     *     wave's 8, chunk 2 ks + l / 32, column l % 16.
+     * gate/up: tiles (gate, up) of pair p are j = 4 p + {0, 1}, jstep 2;
+     * plain: tile cj is j = 2 cj, jstep 1. */
+    uint32_t rdA[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+        rdA[ks] = (64 * wr + l32) * 64 + 16 * ((2 * ks + hi) ^ swz64(l32));
+    const uint32_t rdB = BT_A_BYTES + (8 * wc + (l32 >> 4) * (GU ? 2 : 1)) * 1024 +
+                         (hi * 16 + (lane & 15)) * 16;
+    auto read_ops = [&](int s, int ks, i32x4(&A)[2], i32x4(&B)[4]) {
+        const uint32_t sb = lds0 + (uint32_t)((s % BT_NS) * BT_STAGE);
+        const uint32_t ra = sb + rdA[ks], rb = sb + rdB;
+        A[0] = ds_read16(ra, 0);
+        A[1] = ds_read16(ra, 2048);
+#pragma unroll
+        for (int cj = 0; cj < 4; cj++) {
+            const int j = GU ? 4 * (cj >> 1) + (cj & 1) : 2 * cj;
+            B[cj] = ds_read16(rb, j * 1024 + ks * 512);
+        }
+    };
+
+    /* ---- first tile ---- */
+    bt_tile_id cur = bt_decode(a, sh, nslab, t);
+    int buf = 0;
+    if (tid < MM_I8B_BM) {
+        int rid, arow;
+        bt_row(a, cur, tid, &rid, &arow);
+        sh.rid[0][tid] = rid;
+        sh.arow[0][tid] = arow;
+    }
+    __syncthreads();
+    set_tile(cur, 0);
+    issue_head();
+    bool first = true;
+
+    for (;;) {
+        const int tn = t + t_step;
+        const bool has_next = tn < t_end;
+        const bt_tile_id nxt = has_next ? bt_decode(a, sh, nslab, tn) : cur;
+
+        /* this tile's stage 0: the previous tile's epilogue stores (at
+         * least 64 per wave) were issued after stages 0..2, so vmcnt(63)
+         * leaves the 6 oldest loads (stage 0) complete */
+        static_assert(32 * NT >= 63, "vmcnt(63) needs the stores to outnumber it");
+        if (!first) VMCNT_WAIT(63);
+        else if (KB >= 3) VMCNT_WAIT(12);
+        else if (KB == 2) VMCNT_WAIT(6);
+        else VMCNT_WAIT(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+
+        /* loads whose results are used after the K loop: this tile's row
+         * scales and column scales, the next tile's row ids */
+        float sa_r = 0.0f;
+        int nrid = -1, narow = 0;
+        if (tid < MM_I8B_BM) {
+            sa_r = a.sa[sh.arow[buf][tid]];
+            if (has_next) bt_row(a, nxt, tid, &nrid, &narow);
+        }
+        const float *sb0 = a.sb0 + (size_t)cur.e * a.sb_expert_stride;
+        const float *sb1 = GU ? a.sb1 + (size_t)cur.e * a.sb_expert_stride : nullptr;
+        const int fw = cur.slab * MM_I8B_FR + 8 * wc;   /* the wave's first fragment */
+        float c0[NT], c1[NT];
+        int colv[NT];
+#pragma unroll
+        for (int q = 0; q < NT; q++) {
+            const int col = (GU ? (fw >> 1) + 2 * q : fw + 2 * q) * 16 + l32;
+            colv[q] = col;
+            const int cc = min(col, a.N - 1);
+            c0[q] = sb0[cc];
+            c1[q] = GU ? sb1[cc] : 0.0f;
+        }
+
+        /* ---- K loop ---- */
+        i32x4 Ar[2][2], Br[2][4];
+        v16i acc[2][4];
+#pragma unroll
+        for (int ri = 0; ri < 2; ri++)
+#pragma unroll
+            for (int cj = 0; cj < 4; cj++) acc[ri][cj] = (v16i){};
+        auto mma = [&](i32x4(&A)[2], i32x4(&B)[4]) {
+#pragma unroll
+            for (int ri = 0; ri < 2; ri++)
+#pragma unroll
+                for (int cj = 0; cj < 4; cj++) acc[ri][cj] = mfma32_i8(A[ri], B[cj], acc[ri][cj]);
+        };
+        read_ops(0, 0, Ar[0], Br[0]);
+        for (int s = 0; s < KB; s++) {
+            lds_wait6(Ar[0], Br[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            read_ops(s, 1, Ar[1], Br[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(Ar[0], Br[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_wait6(Ar[1], Br[1]);
+            /* stage s + 1 of this wave has landed (only stage s + 2 was
+             * issued after it) */
+            if (s + 2 < KB) VMCNT_WAIT(6); else VMCNT_WAIT(0);
+            __builtin_amdgcn_s_barrier();  /* ... of every wave; stage s is no longer read */
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 3 < KB) issue_stage(s + 3);
+            if (s + 1 < KB) read_ops(s + 1, 0, Ar[0], Br[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(Ar[1], Br[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lds_wait6(Ar[0], Br[0]);
+        VMCNT_WAIT(0);
+
+        /* row tables: this tile's scales, the next tile's rows */
+        if (tid < MM_I8B_BM) {
+            sh.sa[buf][tid] = sa_r;
+            sh.rid[buf ^ 1][tid] = nrid;
+            sh.arow[buf ^ 1][tid] = narow;
+        }
+        __syncthreads();
+        /* the next tile's first stages go out before this tile's stores */
+        if (has_next) {
+            set_tile(nxt, buf ^ 1);
+            issue_head();
+        }
+
+        /* ---- epilogue ----
+         * accumulator register 4 g + i of lane l is row
+         * 64 wr + 32 ri + 8 g + 4 (l / 32) + i, column l % 32 of tile cj.
+         * Stores are unconditional (exactly 32 NT per wave): padded rows and
+         * columns past N go to the spare row of `out`. */
+        float *out = a.out;
+        const size_t spare = (size_t)a.spare_row * a.N;
+        auto epilogue = [&](auto dbg_on) {
+            int32_t *dbg = a.dbg_acc;
+#pragma unroll
+            for (int ri = 0; ri < 2; ri++) {
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int rb = 64 * wr + 32 * ri + 8 * g + 4 * hi;
+                    const i32x4 rid4 = *(const i32x4 *)(&sh.rid[buf][rb]);
+                    const f32x4 sa4 = *(const f32x4 *)(&sh.sa[buf][rb]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int rid = rid4[i];
+                        const float sa = sa4[i];
+#pragma unroll
+                        for (int q = 0; q < NT; q++) {
+                            const int col = colv[q];
+                            const bool ok = rid >= 0 && col < a.N;
+                            const size_t o = ok ? (size_t)rid * a.N + col : spare + col;
+                            if (GU) {
+                                const int32_t ag = acc[ri][2 * q][4 * g + i];
+                                const int32_t au = acc[ri][2 * q + 1][4 * g + i];
+                                out[o] = silu_mul(((float)ag * sa) * c0[q], ((float)au * sa) * c1[q]);
+                                if (decltype(dbg_on)::value && ok) {
+                                    dbg[((size_t)rid * 2) * a.N + col] = ag;
+                                    dbg[((size_t)rid * 2 + 1) * a.N + col] = au;
+                                }
+                            } else {
+                                const int32_t ac = acc[ri][q][4 * g + i];
+                                out[o] = ((float)ac * sa) * c0[q];
+                                if (decltype(dbg_on)::value && ok) dbg[(size_t)rid * a.N + col] = ac;
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        if (a.dbg_acc)
+            epilogue(std::true_type{});
+        else
+            epilogue(std::false_type{});
+        if (!has_next) break;
+        t = tn;
+        cur = nxt;
+        buf ^= 1;
+        first = false;
+    }
+    VMCNT_WAIT(0);
+}
+
+/* Persistent grid of 2 blocks per CU (the host launches a multiple of 8).
+ * Blocks are dealt to the 8 XCDs round robin (block b runs on XCD b % 8);
+ * XCD x owns the x-th eighth of the tile list and its blocks take those
+ * tiles in turn, so the blocks of one XCD work on neighbouring tiles at the
+ * same time: row groups of the same expert and slab, whose weights then come
+ * from HBM once and from that XCD's L2 for the others. */
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_tiled_args a) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_STAGE];
+    __shared__ bt_shared sh;
+    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
+    const int nslab = (nfr_total + MM_I8B_FR - 1) / MM_I8B_FR;
+    const int E = a.cnt ? a.E : 1;
+    /* exclusive prefix of row groups per expert (wave 0) */
+    if (threadIdx.x < MM_WAVE) {
+        const int lane = threadIdx.x;
+        int base = 0;
+        for (int e0 = 0; e0 < E; e0 += MM_WAVE) {
+            const int e = e0 + lane;
+            const int M = e < E ? (a.cnt ? min(a.cnt[e], a.T) : a.T) : 0;
+            const int nt = (M + MM_I8B_BM - 1) / MM_I8B_BM;
+            int incl = nt;
+#pragma unroll
+            for (int off = 1; off < MM_WAVE; off <<= 1) {
+                const int v = __shfl_up(incl, off, MM_WAVE);
+                if (lane >= off) incl += v;
+            }
+            if (e < E) sh.gstart[e] = base + incl - nt;
+            base += __shfl(incl, MM_WAVE - 1, MM_WAVE);
+        }
+        if (lane == 0) sh.gstart[E] = base;
+    }
+    __syncthreads();
+    const int n = sh.gstart[E] * nslab;
+    const int xcd = blockIdx.x % MM_I8S_XCD, j = blockIdx.x / MM_I8S_XCD;
+    const int nbx = gridDim.x / MM_I8S_XCD;
+    const int lo = (int)((long long)n * xcd / MM_I8S_XCD);
+    const int hi = (int)((long long)n * (xcd + 1) / MM_I8S_XCD);
+    if (lo + j >= hi) return;
+    if (a.gu)
+        bt_run<true>(a, lds, sh, lo + j, nbx, hi, nslab);
+    else
+        bt_run<false>(a, lds, sh, lo + j, nbx, hi, nslab);
+}

@@ -29,6 +29,7 @@
  * operand for one K step is one contiguous 1 KB block (kernel_params.h).
  */
 #include "router.h"
+#include "i8_tile.h"
 
 typedef i32x4 v4i;
 
@@ -283,7 +284,6 @@ extern "C" __global__ __launch_bounds__(MM_I8_RT_WAVES * MM_WAVE) void mm_i8_rou
 /* ---- streaming grouped GEMM (decode) ------------------------------------------- */
 
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 /* Decode-shaped grouped GEMMs.
  *
@@ -737,54 +737,6 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
 #define T_NSA 3                   /* A stages (issued 2 steps ahead) */
 #define T_ASTAGE (128 * 128)      /* one K step of A: 128 rows x 128 B */
 
-/* position of 16 B chunk q of tile row R within the row's 128 B in LDS */
-__device__ __forceinline__ int t_swz(int R) { return (R >> 1) & 7; }
-
-/* Expert, first row and row count of row-group `tile` (a group is up to
- * a.mgroup consecutive 128-row tiles of one expert); all threads of the
- * block get the same answer; false when the group is past the last expert. */
-__device__ __forceinline__ bool tile_owner(const mm_i8_tiled_args &a, int tile, int *e_out,
-                                           int *m0_out, int *M_out) {
-    __shared__ int s_e, s_m0, s_M;
-    if (threadIdx.x < MM_WAVE) {
-        const int lane = threadIdx.x;
-        int found = -1, m0 = 0, Mf = 0;
-        const int GR = MM_I8T_BM * a.mgroup;   /* rows per group */
-        if (!a.cnt) {
-            if (tile * GR < a.T) { found = 0; m0 = tile * GR; Mf = a.T; }
-        } else {
-            int base = 0;   /* tiles before this group of 64 experts */
-            for (int e0 = 0; e0 < a.E && found < 0; e0 += MM_WAVE) {
-                const int e = e0 + lane;
-                const int M = e < a.E ? min(a.cnt[e], a.T) : 0;
-                const int nt = (M + GR - 1) / GR;
-                int incl = nt;   /* inclusive wave prefix sum */
-#pragma unroll
-                for (int off = 1; off < MM_WAVE; off <<= 1) {
-                    int v = __shfl_up(incl, off, MM_WAVE);
-                    if (lane >= off) incl += v;
-                }
-                const int excl = base + incl - nt;
-                const bool mine = tile >= excl && tile < excl + nt;
-                const unsigned long long bal = __ballot(mine);
-                if (bal) {
-                    const int src = __ffsll((long long)bal) - 1;
-                    found = e0 + src;
-                    m0 = (tile - __shfl(excl, src, MM_WAVE)) * GR;
-                    Mf = __shfl(M, src, MM_WAVE);
-                }
-                base += __shfl(incl, MM_WAVE - 1, MM_WAVE);
-            }
-        }
-        if (lane == 0) { s_e = found; s_m0 = m0; s_M = Mf; }
-    }
-    __syncthreads();
-    *e_out = s_e;
-    *m0_out = s_m0;
-    *M_out = s_M;
-    return s_e >= 0;
-}
-
 /* One 128-row x MM_I8T_FR-fragment tile starting at row m0 of expert e (M rows). */
 __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_ASTAGE],
                                            int32_t *s_arow, float *s_sa, int32_t *s_rid,
@@ -925,6 +877,17 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
      * (lane % 16) of each of its fragments */
     const float *sb0 = a.sb0 + (size_t)e * a.sb_expert_stride;
     const float *sb1 = a.sb1 ? a.sb1 + (size_t)e * a.sb_expert_stride : nullptr;
+    /* column scales in registers before the stores (the compiler would
+     * otherwise reload them after every store, see bt_tile) */
+    float c0[T_WF], c1[T_WF];
+#pragma unroll
+    for (int f = 0; f < T_WF; f++) {
+        const int nb = a.gu ? (fr0 >> 1) + f : fr0 + f;
+        const int col = min(nb, a.N / 16 - 1) * 16 + (lane & 15);
+        c0[f] = sb0[col];
+        c1[f] = a.gu ? sb1[col] : 0.0f;
+        asm volatile("" : "+v"(c0[f]), "+v"(c1[f]));
+    }
 #pragma unroll
     for (int mi = 0; mi < 8; mi++) {
 #pragma unroll
@@ -940,8 +903,8 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
                     if (nb * 16 >= a.N) continue;
                     const int col = nb * 16 + (lane & 15);
                     const int32_t ag = acc[mi][2 * k][i], au = acc[mi][2 * k + 1][i];
-                    const float g = ((float)ag * sa) * sb0[col];
-                    const float u = ((float)au * sa) * sb1[col];
+                    const float g = ((float)ag * sa) * c0[k];
+                    const float u = ((float)au * sa) * c1[k];
                     a.out[(size_t)rid * a.N + col] = silu_mul(g, u);
                     if (a.dbg_acc) {
                         a.dbg_acc[((size_t)rid * 2) * a.N + col] = ag;
@@ -955,7 +918,7 @@ __device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*l
                     if (nb * 16 >= a.N) continue;
                     const int col = nb * 16 + (lane & 15);
                     const int32_t ac = acc[mi][f][i];
-                    a.out[(size_t)rid * a.N + col] = ((float)ac * sa) * sb0[col];
+                    a.out[(size_t)rid * a.N + col] = ((float)ac * sa) * c0[f];
                     if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.N + col] = ac;
                 }
             }
