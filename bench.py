@@ -196,14 +196,17 @@ def bench_prefill_i8(ctx, steps, warmup, T=2048):
     counts = np.bincount(ii.ravel(), minlength=E)
     names = ["mm_router", "mm_i8_route", "mm_i8_gemm_bt", "mm_i8_gemm_tiled", "mm_i8_quant_h",
              "mm_i8_combine"]
-    prof = profile_kernels(ctx, step, max(2, steps // 4), names)
+    psteps = max(2, steps // 4)
+    prof = profile_kernels(ctx, step, psteps, names)
     gk = "mm_i8_gemm_bt" if prof["mm_i8_gemm_bt"][1] else "mm_i8_gemm_tiled"
     prof.pop("mm_i8_gemm_tiled" if gk == "mm_i8_gemm_bt" else "mm_i8_gemm_bt")
     R = T * K
     gu_ops = 2.0 * R * 2 * I * H + 2.0 * T * 2 * S * H
     dn_ops = 2.0 * R * H * I + 2.0 * T * H * S
-    # the grouped GEMM runs four times per layer (routed/shared x gate-up/down)
-    gemm_ms = prof[gk][0] * 4
+    # grouped GEMM time per layer: mm_i8_gemm_bt runs twice (gate/up, down;
+    # routed and shared experts in one launch), mm_i8_gemm_tiled four times
+    launches = prof[gk][1] / psteps
+    gemm_ms = prof[gk][0] * launches
     res = dict(
         ms_per_step=ms, wall_ms_per_step=wall, tok_s=T / (ms * 1e-3),
         layer_tops=(gu_ops + dn_ops) / (ms * 1e-3) / 1e12,
@@ -211,7 +214,7 @@ def bench_prefill_i8(ctx, steps, warmup, T=2048):
         expert_rows_max=int(counts.max()), expert_rows_min=int(counts.min()),
         experts_touched=int((counts > 0).sum()),
         kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()},
-        roofline=dict(bound="mfma", kernel=f"{gk} (4 launches per layer)",
+        roofline=dict(bound="mfma", kernel=f"{gk} ({launches:.0f} launches per layer)",
                       achieved=(gu_ops + dn_ops) / (gemm_ms * 1e-3) / 1e12,
                       peak=INT8_PEAK_TOPS, unit="TOPS", ops_per_layer=gu_ops + dn_ops,
                       avg_launch_us=prof[gk][0] * 1e3))

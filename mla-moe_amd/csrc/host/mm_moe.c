@@ -332,14 +332,26 @@ static unsigned tiled_blocks(unsigned nslab, unsigned groups) {
     return (unsigned)(ceil_div(runs, MM_I8S_XCD) * MM_I8S_XCD * MM_I8S_XCD);
 }
 
-/* One tiled grouped GEMM: the big-tile kernel (16-fragment slabs, one block
- * per CU) or the 8-fragment tiled kernel.  `nfr` is the B fragment count of
- * one expert, `groups` an upper bound on its row groups. */
-static int launch_tiled(mm_ctx *c, mm_i8_tiled_args *ta, unsigned nfr, unsigned groups) {
-    if (c->i8_bt)   /* persistent: two blocks per CU */
-        return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, ta);
-    return mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr, MM_I8T_FR), groups), 1, 1,
-                     256, 0, ta);
+/* One grouped GEMM over the routed experts (ta) and, when ts is not NULL,
+ * the shared expert: one persistent launch of the big-tile kernel, or one
+ * launch per segment of the 8-fragment tiled kernel.  `nfr_r`/`nfr_s` are
+ * the B fragment counts of one expert, `mt_r`/`mt_s` upper bounds on the
+ * row groups. */
+static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled_args *ts,
+                        unsigned nfr_r, unsigned mt_r, unsigned nfr_s, unsigned mt_s) {
+    if (c->i8_bt) {
+        mm_i8_bt_args ba;
+        memset(&ba, 0, sizeof(ba));
+        ba.seg[0] = *ta;
+        if (ts) ba.seg[1] = *ts;
+        ba.nseg = ts ? 2 : 1;
+        return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
+    }
+    int st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr_r, MM_I8T_FR), mt_r), 1,
+                       1, 256, 0, (void *)ta);
+    if (st || !ts) return st;
+    return mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr_s, MM_I8T_FR), mt_s), 1, 1,
+                     256, 0, (void *)ts);
 }
 
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
@@ -445,13 +457,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
                                (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed, (int)R};
-        if ((st = launch_tiled(c, &ta, (unsigned)(2 * I / 16), mt_routed))) return st;
-        if (S) {
-            mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
-                                   hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared,
-                                   T};
-            if ((st = launch_tiled(c, &ts, (unsigned)(2 * S / 16), mt_shared))) return st;
-        }
+        mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
+                               hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared,
+                               T};
+        if ((st = launch_tiled(c, &ta, S ? &ts : NULL, (unsigned)(2 * I / 16), mt_routed,
+                               (unsigned)(2 * S / 16), mt_shared)))
+            return st;
     } else {
         /* shared-expert blocks (row-tile waves), then every routed unit */
         const size_t per_blk = (size_t)MM_I8S_W * MM_I8S_SEG;
@@ -471,13 +482,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
                                0, I8T_MGROUP, (int)mt_routed, (int)R};
-        if ((st = launch_tiled(c, &td, (unsigned)(H / 16), mt_routed))) return st;
-        if (S) {
-            mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
-                                    NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared,
-                                    T};
-            if ((st = launch_tiled(c, &tsd, (unsigned)(H / 16), mt_shared))) return st;
-        }
+        mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
+                                NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared,
+                                T};
+        if ((st = launch_tiled(c, &td, S ? &tsd : NULL, (unsigned)(H / 16), mt_routed,
+                               (unsigned)(H / 16), mt_shared)))
+            return st;
     } else {
         ga.a = qh;
         ga.sa = sh;

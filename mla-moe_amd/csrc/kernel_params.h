@@ -207,6 +207,14 @@ typedef struct {
                                 that absorbs the stores of padded rows and columns */
 } mm_i8_tiled_args;
 
+/* Big-tile kernel arguments: one launch serves the routed experts and the
+ * shared expert (segments 0 and 1, same gate/up flag); nseg = 1 when there
+ * is no shared expert. */
+typedef struct {
+    mm_i8_tiled_args seg[2];
+    int nseg;
+} mm_i8_bt_args;
+
 /* ---- MLA absorbed decode ----------------------------------------------------- */
 #define MM_MLA_KVL 512            /* kv_lora_rank served by the kernels */
 #define MM_MLA_QKR 64             /* qk_rope_head_dim served by the kernels */

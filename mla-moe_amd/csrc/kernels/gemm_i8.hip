@@ -59,62 +59,87 @@ __device__ __forceinline__ void lds_wait6(i32x4 (&A)[2], i32x4 (&B)[4]) {
 
 /* Per-block schedule and row tables in LDS. */
 struct bt_shared {
-    int gstart[MM_EMAX + 1];                 /* exclusive prefix of 128-row groups per expert */
+    int gstart[MM_EMAX + 1];                 /* segment 0: exclusive prefix of 128-row groups */
+    int g1;                                  /* segment 1 (one expert): its row groups */
+    int n0, n;                               /* tiles of segment 0, of both */
     int arow[2][MM_I8B_BM];                  /* A row of each tile row (two tiles in flight) */
     __attribute__((aligned(16))) int rid[2][MM_I8B_BM];     /* output row id, -1 = padding */
     __attribute__((aligned(16))) float sa[2][MM_I8B_BM];    /* A row scale */
 };
 
-/* A tile of the grouped GEMM: expert e, column slab, rows m0 .. m0 + 127 of
- * the expert's M rows. */
+/* A tile of the grouped GEMM: segment si, expert e, column slab, rows
+ * m0 .. m0 + 127 of the expert's M rows. */
 struct bt_tile_id {
-    int e, slab, m0, M;
+    int si, e, slab, m0, M;
 };
 
-/* Tiles are ordered (expert, slab, row group): expert e owns tiles
- * [nslab gstart[e], nslab gstart[e + 1]).  Uniform over the block. */
-__device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_tiled_args &a, const bt_shared &sh,
-                                                int nslab, int t) {
-    int lo = 0, hi = a.cnt ? a.E : 1;        /* largest e with nslab * gstart[e] <= t */
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (nslab * sh.gstart[mid] <= t) lo = mid; else hi = mid;
-    }
-    const int ge = sh.gstart[lo + 1] - sh.gstart[lo];
-    const int loc = t - nslab * sh.gstart[lo];
+__device__ __forceinline__ int bt_nslab(const mm_i8_tiled_args &g) {
+    return ((g.gu ? 2 : 1) * (g.N / 16) + MM_I8B_FR - 1) / MM_I8B_FR;
+}
+
+/* Tiles are ordered (segment, expert, slab, row group): expert e of
+ * segment 0 owns tiles [nslab gstart[e], nslab gstart[e + 1]); segment 1
+ * follows.  Uniform over the block. */
+__device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt_shared &sh,
+                                                int t) {
     bt_tile_id id;
-    id.e = lo;
-    id.slab = loc / ge;
-    id.m0 = (loc % ge) * MM_I8B_BM;
-    id.M = a.cnt ? min(a.cnt[lo], a.T) : a.T;
+    if (t < sh.n0) {
+        const mm_i8_tiled_args &g = a.seg[0];
+        const int nslab = bt_nslab(g);
+        int lo = 0, hi = g.cnt ? g.E : 1;    /* largest e with nslab * gstart[e] <= t */
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (nslab * sh.gstart[mid] <= t) lo = mid; else hi = mid;
+        }
+        const int ge = sh.gstart[lo + 1] - sh.gstart[lo];
+        const int loc = t - nslab * sh.gstart[lo];
+        id.si = 0;
+        id.e = lo;
+        id.slab = loc / ge;
+        id.m0 = (loc % ge) * MM_I8B_BM;
+        id.M = g.cnt ? min(g.cnt[lo], g.T) : g.T;
+    } else {
+        const mm_i8_tiled_args &g = a.seg[1];
+        const int loc = t - sh.n0;
+        id.si = 1;
+        id.e = 0;
+        id.slab = loc / sh.g1;
+        id.m0 = (loc % sh.g1) * MM_I8B_BM;
+        id.M = g.T;
+    }
     return id;
 }
 
 /* Row id and A row of tile row `r` (threads r < 128). */
-__device__ __forceinline__ void bt_row(const mm_i8_tiled_args &a, const bt_tile_id &id, int r,
+__device__ __forceinline__ void bt_row(const mm_i8_tiled_args &g, const bt_tile_id &id, int r,
                                        int *rid, int *arow) {
     const int m = id.m0 + r < id.M ? id.m0 + r : id.m0;
-    const int q = a.rows ? a.rows[(size_t)id.e * a.T + m] : m;
-    *arow = (a.a_by_route || !a.rows) ? q : q / a.K;
+    const int q = g.rows ? g.rows[(size_t)id.e * g.T + m] : m;
+    *arow = (g.a_by_route || !g.rows) ? q : q / g.K;
     *rid = id.m0 + r < id.M ? q : -1;
 }
 
+/* The tiles of one XCD: its eighth of segment 0 followed by its eighth of
+ * segment 1; local index t -> global tile index. */
+struct bt_xcd_list {
+    int lo0, len0, lo1, len;
+    __device__ int operator()(int t) const { return t < len0 ? lo0 + t : lo1 + (t - len0); }
+};
+
 template <bool GU>
-__device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, bt_shared &sh,
-                                       int t, int t_step, int t_end, int nslab) {
+__device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_shared &sh,
+                                       const bt_xcd_list &xl, int t, int t_step) {
+    const int t_end = xl.len;
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
     const int wr = wave & 1, wc = wave >> 1;
-    const int KB = a.Kd / 64;               /* stages = 64-byte K halves of the packed fragments */
-    const int nfr_total = (GU ? 2 : 1) * (a.N / 16);
     const int bstep = GU ? 2048 : 1024;
-    const uint32_t bytes_e = (uint32_t)(nfr_total * KB) * 1024u;
     const int l32 = lane & 31, hi = lane >> 5;
     const uint32_t lds0 = lds_addr(lds);
     constexpr int NT = GU ? 2 : 4;          /* output column tiles of 32 */
 
-    /* ---- per-tile load parameters ---- */
-    /* A loads: wave w issues instructions 2 w, 2 w + 1 of a stage (16 rows x
+    /* ---- load parameters of the tile whose stages are being issued ----
+     * A loads: wave w issues instructions 2 w, 2 w + 1 of a stage (16 rows x
      * 64 B each); lane l carries row R = 16 i + l / 4 and stores at position
      * l % 4 of the row's 64 B the chunk (l % 4) ^ swz64(R).
      * B loads: wave w loads fragments 4 w .. 4 w + 3 of the slab (clamped
@@ -122,29 +147,34 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
     uint32_t arow_off[2];
     int aq[2];
     __amdgpu_buffer_rsrc_t brs;
-    int bf0;
+    const int8_t *aptr;
+    int bf0, lkb, lnfr;
     auto set_tile = [&](const bt_tile_id &id, int buf) {
+        const mm_i8_tiled_args &g = a.seg[id.si];
+        lkb = g.Kd / 64;
+        lnfr = (GU ? 2 : 1) * (g.N / 16);
+        aptr = g.a;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int R = 16 * (2 * wave + h) + (lane >> 2);
-            arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)a.Kd;
+            arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd;
             aq[h] = 16 * ((lane & 3) ^ swz64(R));
         }
-        brs = __builtin_amdgcn_make_buffer_rsrc((void *)(a.b + (size_t)id.e * a.b_expert_stride), 0,
-                                                (int)bytes_e, 0x00020000);
+        brs = __builtin_amdgcn_make_buffer_rsrc((void *)(g.b + (size_t)id.e * g.b_expert_stride), 0,
+                                                (int)((uint32_t)(lnfr * lkb) * 1024u), 0x00020000);
         bf0 = __builtin_amdgcn_readfirstlane(id.slab * MM_I8B_FR + 4 * wave);
     };
     auto issue_stage = [&](int s) {   /* stage s into ring slot s % 3: 6 loads per wave */
         const uint32_t st = (uint32_t)((s % BT_NS) * BT_STAGE);
 #pragma unroll
         for (int h = 0; h < 2; h++)
-            lds_dma16(a.a + (arow_off[h] + (uint32_t)(s * 64 + aq[h])),
+            lds_dma16(aptr + (arow_off[h] + (uint32_t)(s * 64 + aq[h])),
                       lds + st + (2 * wave + h) * 1024);
         const int so = s * bstep;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int fr = min(bf0 + i, nfr_total - 1);
-            const int fo = GU ? ((fr >> 1) * 2 * KB + (fr & 1)) * 1024 : fr * KB * 1024;
+            const int fr = min(bf0 + i, lnfr - 1);
+            const int fo = GU ? ((fr >> 1) * 2 * lkb + (fr & 1)) * 1024 : fr * lkb * 1024;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 brs, (lds_void_t *)(lds + st + BT_A_BYTES + (4 * wave + i) * 1024), 16, lane * 16,
                 __builtin_amdgcn_readfirstlane(fo + so), 0, 0);
@@ -152,7 +182,7 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
     };
     /* the stages issued ahead of a tile's K loop */
     auto issue_head = [&]() {
-        for (int s = 0; s < min(BT_NS, KB); s++) issue_stage(s);
+        for (int s = 0; s < min(BT_NS, lkb); s++) issue_stage(s);
     };
 
     /* ---- operand reads ----
@@ -182,11 +212,11 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
     };
 
     /* ---- first tile ---- */
-    bt_tile_id cur = bt_decode(a, sh, nslab, t);
+    bt_tile_id cur = bt_decode(a, sh, xl(t));
     int buf = 0;
     if (tid < MM_I8B_BM) {
         int rid, arow;
-        bt_row(a, cur, tid, &rid, &arow);
+        bt_row(a.seg[cur.si], cur, tid, &rid, &arow);
         sh.rid[0][tid] = rid;
         sh.arow[0][tid] = arow;
     }
@@ -196,12 +226,14 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
     bool first = true;
 
     for (;;) {
+        const mm_i8_tiled_args &g = a.seg[cur.si];
+        const int KB = lkb;                 /* this tile's stages (set_tile(cur) was last) */
         const int tn = t + t_step;
         const bool has_next = tn < t_end;
-        const bt_tile_id nxt = has_next ? bt_decode(a, sh, nslab, tn) : cur;
+        const bt_tile_id nxt = has_next ? bt_decode(a, sh, xl(tn)) : cur;
 
         /* this tile's stage 0: the previous tile's epilogue stores (at
-         * least 64 per wave) were issued after stages 0..2, so vmcnt(63)
+         * least 64 per wave) were issued after its stages, so vmcnt(63)
          * leaves the 6 oldest loads (stage 0) complete */
         static_assert(32 * NT >= 63, "vmcnt(63) needs the stores to outnumber it");
         if (!first) VMCNT_WAIT(63);
@@ -216,19 +248,20 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
         float sa_r = 0.0f;
         int nrid = -1, narow = 0;
         if (tid < MM_I8B_BM) {
-            sa_r = a.sa[sh.arow[buf][tid]];
-            if (has_next) bt_row(a, nxt, tid, &nrid, &narow);
+            sa_r = g.sa[sh.arow[buf][tid]];
+            if (has_next) bt_row(a.seg[nxt.si], nxt, tid, &nrid, &narow);
         }
-        const float *sb0 = a.sb0 + (size_t)cur.e * a.sb_expert_stride;
-        const float *sb1 = GU ? a.sb1 + (size_t)cur.e * a.sb_expert_stride : nullptr;
+        const float *sb0 = g.sb0 + (size_t)cur.e * g.sb_expert_stride;
+        const float *sb1 = GU ? g.sb1 + (size_t)cur.e * g.sb_expert_stride : nullptr;
         const int fw = cur.slab * MM_I8B_FR + 8 * wc;   /* the wave's first fragment */
+        const int N = g.N;
         float c0[NT], c1[NT];
         int colv[NT];
 #pragma unroll
         for (int q = 0; q < NT; q++) {
             const int col = (GU ? (fw >> 1) + 2 * q : fw + 2 * q) * 16 + l32;
             colv[q] = col;
-            const int cc = min(col, a.N - 1);
+            const int cc = min(col, N - 1);
             c0[q] = sb0[cc];
             c1[q] = GU ? sb1[cc] : 0.0f;
         }
@@ -287,15 +320,15 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
          * 64 wr + 32 ri + 8 g + 4 (l / 32) + i, column l % 32 of tile cj.
          * Stores are unconditional (exactly 32 NT per wave): padded rows and
          * columns past N go to the spare row of `out`. */
-        float *out = a.out;
-        const size_t spare = (size_t)a.spare_row * a.N;
+        float *out = g.out;
+        const size_t spare = (size_t)g.spare_row * N;
         auto epilogue = [&](auto dbg_on) {
-            int32_t *dbg = a.dbg_acc;
+            int32_t *dbg = g.dbg_acc;
 #pragma unroll
             for (int ri = 0; ri < 2; ri++) {
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int rb = 64 * wr + 32 * ri + 8 * g + 4 * hi;
+                for (int gq = 0; gq < 4; gq++) {
+                    const int rb = 64 * wr + 32 * ri + 8 * gq + 4 * hi;
                     const i32x4 rid4 = *(const i32x4 *)(&sh.rid[buf][rb]);
                     const f32x4 sa4 = *(const f32x4 *)(&sh.sa[buf][rb]);
 #pragma unroll
@@ -305,27 +338,27 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
 #pragma unroll
                         for (int q = 0; q < NT; q++) {
                             const int col = colv[q];
-                            const bool ok = rid >= 0 && col < a.N;
-                            const size_t o = ok ? (size_t)rid * a.N + col : spare + col;
+                            const bool ok = rid >= 0 && col < N;
+                            const size_t o = ok ? (size_t)rid * N + col : spare + col;
                             if (GU) {
-                                const int32_t ag = acc[ri][2 * q][4 * g + i];
-                                const int32_t au = acc[ri][2 * q + 1][4 * g + i];
+                                const int32_t ag = acc[ri][2 * q][4 * gq + i];
+                                const int32_t au = acc[ri][2 * q + 1][4 * gq + i];
                                 out[o] = silu_mul(((float)ag * sa) * c0[q], ((float)au * sa) * c1[q]);
                                 if (decltype(dbg_on)::value && ok) {
-                                    dbg[((size_t)rid * 2) * a.N + col] = ag;
-                                    dbg[((size_t)rid * 2 + 1) * a.N + col] = au;
+                                    dbg[((size_t)rid * 2) * N + col] = ag;
+                                    dbg[((size_t)rid * 2 + 1) * N + col] = au;
                                 }
                             } else {
-                                const int32_t ac = acc[ri][q][4 * g + i];
+                                const int32_t ac = acc[ri][q][4 * gq + i];
                                 out[o] = ((float)ac * sa) * c0[q];
-                                if (decltype(dbg_on)::value && ok) dbg[(size_t)rid * a.N + col] = ac;
+                                if (decltype(dbg_on)::value && ok) dbg[(size_t)rid * N + col] = ac;
                             }
                         }
                     }
                 }
             }
         };
-        if (a.dbg_acc)
+        if (g.dbg_acc)
             epilogue(std::true_type{});
         else
             epilogue(std::false_type{});
@@ -340,23 +373,22 @@ __device__ __forceinline__ void bt_run(const mm_i8_tiled_args &a, int8_t *lds, b
 
 /* Persistent grid of 2 blocks per CU (the host launches a multiple of 8).
  * Blocks are dealt to the 8 XCDs round robin (block b runs on XCD b % 8);
- * XCD x owns the x-th eighth of the tile list and its blocks take those
- * tiles in turn, so the blocks of one XCD work on neighbouring tiles at the
- * same time: row groups of the same expert and slab, whose weights then come
- * from HBM once and from that XCD's L2 for the others. */
-extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_tiled_args a) {
+ * XCD x owns the x-th eighth of each segment's tile list and its blocks take
+ * those tiles in turn, so the blocks of one XCD work on neighbouring tiles at
+ * the same time: row groups of the same expert and slab, whose weights then
+ * come from HBM once and from that XCD's L2 for the others. */
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args a) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_STAGE];
     __shared__ bt_shared sh;
-    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int nslab = (nfr_total + MM_I8B_FR - 1) / MM_I8B_FR;
-    const int E = a.cnt ? a.E : 1;
-    /* exclusive prefix of row groups per expert (wave 0) */
+    const mm_i8_tiled_args &g0 = a.seg[0];
+    const int E = g0.cnt ? g0.E : 1;
+    /* segment 0: exclusive prefix of row groups per expert (wave 0) */
     if (threadIdx.x < MM_WAVE) {
         const int lane = threadIdx.x;
         int base = 0;
         for (int e0 = 0; e0 < E; e0 += MM_WAVE) {
             const int e = e0 + lane;
-            const int M = e < E ? (a.cnt ? min(a.cnt[e], a.T) : a.T) : 0;
+            const int M = e < E ? (g0.cnt ? min(g0.cnt[e], g0.T) : g0.T) : 0;
             const int nt = (M + MM_I8B_BM - 1) / MM_I8B_BM;
             int incl = nt;
 #pragma unroll
@@ -367,17 +399,26 @@ extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_tiled_a
             if (e < E) sh.gstart[e] = base + incl - nt;
             base += __shfl(incl, MM_WAVE - 1, MM_WAVE);
         }
-        if (lane == 0) sh.gstart[E] = base;
+        if (lane == 0) {
+            sh.gstart[E] = base;
+            sh.n0 = base * bt_nslab(g0);
+            sh.g1 = a.nseg > 1 ? (a.seg[1].T + MM_I8B_BM - 1) / MM_I8B_BM : 0;
+            sh.n = sh.n0 + (a.nseg > 1 ? sh.g1 * bt_nslab(a.seg[1]) : 0);
+        }
     }
     __syncthreads();
-    const int n = sh.gstart[E] * nslab;
+    /* XCD x takes the x-th eighth of each segment's tiles */
+    const int n0 = sh.n0, n1 = sh.n - sh.n0;
     const int xcd = blockIdx.x % MM_I8S_XCD, j = blockIdx.x / MM_I8S_XCD;
     const int nbx = gridDim.x / MM_I8S_XCD;
-    const int lo = (int)((long long)n * xcd / MM_I8S_XCD);
-    const int hi = (int)((long long)n * (xcd + 1) / MM_I8S_XCD);
-    if (lo + j >= hi) return;
-    if (a.gu)
-        bt_run<true>(a, lds, sh, lo + j, nbx, hi, nslab);
+    bt_xcd_list xl;
+    xl.lo0 = n0 * xcd / MM_I8S_XCD;
+    xl.len0 = n0 * (xcd + 1) / MM_I8S_XCD - xl.lo0;
+    xl.lo1 = n0 + n1 * xcd / MM_I8S_XCD;
+    xl.len = xl.len0 + n0 + n1 * (xcd + 1) / MM_I8S_XCD - xl.lo1;
+    if (j >= xl.len) return;
+    if (g0.gu)
+        bt_run<true>(a, lds, sh, xl, j, nbx);
     else
-        bt_run<false>(a, lds, sh, lo + j, nbx, hi, nslab);
+        bt_run<false>(a, lds, sh, xl, j, nbx);
 }
