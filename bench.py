@@ -194,17 +194,15 @@ def bench_prefill_i8(ctx, steps, warmup, T=2048):
     ms, wall = timed(ctx, step, steps, warmup)
     ii = idx.download()
     counts = np.bincount(ii.ravel(), minlength=E)
-    names = ["mm_router", "mm_i8_route", "mm_i8_gemm_bt", "mm_i8_gemm_tiled", "mm_i8_quant_h",
-             "mm_i8_combine"]
+    names = ["mm_router", "mm_i8_route", "mm_i8_gemm_bt", "mm_i8_quant_h", "mm_i8_combine"]
     psteps = max(2, steps // 4)
     prof = profile_kernels(ctx, step, psteps, names)
-    gk = "mm_i8_gemm_bt" if prof["mm_i8_gemm_bt"][1] else "mm_i8_gemm_tiled"
-    prof.pop("mm_i8_gemm_tiled" if gk == "mm_i8_gemm_bt" else "mm_i8_gemm_bt")
+    gk = "mm_i8_gemm_bt"
     R = T * K
     gu_ops = 2.0 * R * 2 * I * H + 2.0 * T * 2 * S * H
     dn_ops = 2.0 * R * H * I + 2.0 * T * H * S
     # grouped GEMM time per layer: mm_i8_gemm_bt runs twice (gate/up, down;
-    # routed and shared experts in one launch), mm_i8_gemm_tiled four times
+    # routed and shared experts in one launch each)
     launches = prof[gk][1] / psteps
     gemm_ms = prof[gk][0] * launches
     res = dict(

@@ -42,7 +42,6 @@ static const struct {
     [K_I8_DOWN] = {"mm_i8_down", MOD_MOE_I8},
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
-    [K_I8_TILED] = {"mm_i8_gemm_tiled", MOD_MOE_I8},
     [K_I8_BT] = {"mm_i8_gemm_bt", MOD_GEMM_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
@@ -128,9 +127,6 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->i8_tiled_min_t = 256;
     const char *ev = getenv("MLAMOE_I8_TILED_MIN_T");
     if (ev && *ev) c->i8_tiled_min_t = atoi(ev);
-    c->i8_bt = 1;
-    ev = getenv("MLAMOE_I8_BT");
-    if (ev && *ev) c->i8_bt = atoi(ev);
     *out = c;
     return MM_OK;
 fail:

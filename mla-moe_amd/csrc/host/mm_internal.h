@@ -23,7 +23,6 @@ typedef enum {
     K_I8_DOWN,
     K_I8_COMBINE,
     K_PACK_I8,
-    K_I8_TILED,
     K_I8_BT,
     K_MLA_QPREP,
     K_MLA_ATTN,
@@ -80,7 +79,6 @@ struct mm_ctx {
     uint16_t **mla_kvb;         /* [layers] device kv_b_proj weights */
 
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
-    int i8_bt;                  /* 1: the big-tile kernel serves the tiled path */
 
     /* growable device workspace */
     void *ws;

@@ -15,7 +15,6 @@
 #define GU_ROWS_PER_BLOCK 4   /* one gate/up row pair per wave */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
 #define ROUTER_TOKENS_PER_BLOCK 8
-#define I8T_MGROUP 1          /* 128-row tiles per block in the tiled int8 GEMM */
 
 void mm_moe_release(mm_ctx *c) {
     if (!c->layers) return;
@@ -323,35 +322,15 @@ static size_t sh_blocks(size_t groups) {
 
 static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
 
-/* 1-D grid of the tiled GEMM: every (column slab, run of 8 row groups) pair
- * gets 8 blocks on one XCD; the count is padded to a multiple of 64 so that
- * the kernel's block -> (slab, row group) map covers every pair once (blocks
- * past the last row group exit). */
-static unsigned tiled_blocks(unsigned nslab, unsigned groups) {
-    const size_t runs = (size_t)nslab * ceil_div(groups, MM_I8S_XCD);
-    return (unsigned)(ceil_div(runs, MM_I8S_XCD) * MM_I8S_XCD * MM_I8S_XCD);
-}
-
 /* One grouped GEMM over the routed experts (ta) and, when ts is not NULL,
- * the shared expert: one persistent launch of the big-tile kernel, or one
- * launch per segment of the 8-fragment tiled kernel.  `nfr_r`/`nfr_s` are
- * the B fragment counts of one expert, `mt_r`/`mt_s` upper bounds on the
- * row groups. */
-static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled_args *ts,
-                        unsigned nfr_r, unsigned mt_r, unsigned nfr_s, unsigned mt_s) {
-    if (c->i8_bt) {
-        mm_i8_bt_args ba;
-        memset(&ba, 0, sizeof(ba));
-        ba.seg[0] = *ta;
-        if (ts) ba.seg[1] = *ts;
-        ba.nseg = ts ? 2 : 1;
-        return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
-    }
-    int st = mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr_r, MM_I8T_FR), mt_r), 1,
-                       1, 256, 0, (void *)ta);
-    if (st || !ts) return st;
-    return mm_launch(c, K_I8_TILED, tiled_blocks((unsigned)ceil_div(nfr_s, MM_I8T_FR), mt_s), 1, 1,
-                     256, 0, (void *)ts);
+ * the shared expert: one persistent launch of the big-tile kernel. */
+static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled_args *ts) {
+    mm_i8_bt_args ba;
+    memset(&ba, 0, sizeof(ba));
+    ba.seg[0] = *ta;
+    if (ts) ba.seg[1] = *ts;
+    ba.nseg = ts ? 2 : 1;
+    return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
 }
 
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
@@ -448,21 +427,14 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ga.S = (int)S;
     ga.E = (int)E;
     ga.K = (int)K;
-    /* row groups of I8T_MGROUP tiles: upper bound over any routing */
-    const size_t GR = (size_t)MM_I8T_BM * I8T_MGROUP;
-    const unsigned mt_routed = (unsigned)((R + GR - 1) / GR + E);
-    const unsigned mt_shared = (unsigned)((T + GR - 1) / GR);
     if (tiled) {
         /* routed experts, then the shared expert as one dense GEMM */
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
                                rows, qx, sx, 0, h, dbg ? dbg->acc_gu : NULL, T, (int)K,
-                               (int)E, (int)I, (int)H, 1, I8T_MGROUP, (int)mt_routed, (int)R};
+                               (int)E, (int)I, (int)H, 1, (int)R};
         mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
-                               hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, I8T_MGROUP, (int)mt_shared,
-                               T};
-        if ((st = launch_tiled(c, &ta, S ? &ts : NULL, (unsigned)(2 * I / 16), mt_routed,
-                               (unsigned)(2 * S / 16), mt_shared)))
-            return st;
+                               hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, T};
+        if ((st = launch_tiled(c, &ta, S ? &ts : NULL))) return st;
     } else {
         /* shared-expert blocks (row-tile waves), then every routed unit */
         const size_t per_blk = (size_t)MM_I8S_W * MM_I8S_SEG;
@@ -481,13 +453,10 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     if (tiled) {
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
                                1, y, dbg ? dbg->acc_d : NULL, T, (int)K, (int)E, (int)H, (int)I,
-                               0, I8T_MGROUP, (int)mt_routed, (int)R};
+                               0, (int)R};
         mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
-                                NULL, T, (int)K, 1, (int)H, (int)S, 0, I8T_MGROUP, (int)mt_shared,
-                                T};
-        if ((st = launch_tiled(c, &td, S ? &tsd : NULL, (unsigned)(H / 16), mt_routed,
-                               (unsigned)(H / 16), mt_shared)))
-            return st;
+                                NULL, T, (int)K, 1, (int)H, (int)S, 0, T};
+        if ((st = launch_tiled(c, &td, S ? &tsd : NULL))) return st;
     } else {
         ga.a = qh;
         ga.sa = sh;

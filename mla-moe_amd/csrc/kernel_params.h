@@ -173,18 +173,14 @@ typedef struct {
 #define MM_I8S_RT 4                /* row-tile blocks per shared-expert column group */
 #define MM_I8S_XCD 8               /* blocks are dealt to XCDs round robin */
 
-/* Tiled grouped int8 GEMM (prefill): 128-row x 128-column block tiles over
- * the routed experts' row lists (or all T rows for the shared expert). */
-#define MM_I8T_BM 128     /* rows per tile */
-#ifndef MM_I8T_FR
-#define MM_I8T_FR 8       /* B fragments (16 packed columns each) per column slab;
-                             8 (2 per wave) beat 16 by 13% at config 3 */
-#endif
-/* Big-tile variant (mm_i8_gemm_bt): 128 rows x 16 fragments per block, one
- * block per CU, both operands staged through LDS. */
+/* Grouped int8 GEMM for prefill sizes (mm_i8_gemm_bt, gemm_i8.hip): block
+ * tiles of 128 rows x 16 B fragments over the routed experts' row lists (or
+ * all T rows for the shared expert), a persistent grid of two blocks per CU. */
 #define MM_I8B_BM 128
 #define MM_I8B_FR 16
 #define MM_I8B_GRID 512          /* persistent grid: 2 blocks on each of 256 CUs */
+/* One GEMM segment: the routed experts, or the shared expert as one dense
+ * GEMM. */
 typedef struct {
     const int8_t *b;         /* packed fragments of expert 0 */
     size_t b_expert_stride;  /* bytes between experts' fragment sets */
@@ -201,10 +197,8 @@ typedef struct {
     int N;                   /* output columns (I or S for gate/up, H for down) */
     int Kd;                  /* reduction length (H for gate/up, I or S for down) */
     int gu;                  /* 1: gate/up with SwiGLU epilogue, 0: plain dequantising GEMM */
-    int mgroup;              /* consecutive 128-row tiles one block walks (weight reuse) */
-    int max_groups;          /* grid.y bound */
-    int spare_row;           /* big-tile kernel: `out` has a spare row here (N + 256 floats)
-                                that absorbs the stores of padded rows and columns */
+    int spare_row;           /* `out` has a spare row here (N + 256 floats) that absorbs
+                                the stores of padded rows and columns */
 } mm_i8_tiled_args;
 
 /* Big-tile kernel arguments: one launch serves the routed experts and the

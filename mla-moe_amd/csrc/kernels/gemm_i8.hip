@@ -1,10 +1,11 @@
 /* gemm_i8.hip -- big-tile grouped int8 GEMM for the prefill MoE FFN on
  * v_mfma_i32_32x32x32_i8 (int32 accumulation).
  *
- * Same contract as mm_i8_gemm_tiled (moe_i8.hip): for each routed expert (or
- * the shared expert as one dense GEMM) and each of its rows, out[rid] =
- * dequant(qa[row] . qW^T), with the SwiGLU epilogue for gate/up; the
- * weights are the packed 16-column x 64-K fragments of kernel_params.h.
+ * The prefill-sized counterpart of mm_i8_gu / mm_i8_down (moe_i8.hip): for
+ * each routed expert (and the shared expert as one dense GEMM, in the same
+ * launch) and each of its rows, out[rid] = dequant(qa[row] . qW^T), with the
+ * SwiGLU epilogue for gate/up; the weights are the packed 16-column x 64-K
+ * fragments of kernel_params.h.
  *
  * Block tile MM_I8B_BM = 128 rows x MM_I8B_FR = 16 fragments (gate/up: the
  * gate and up fragments of 8 column blocks, 128 output columns; plain: 256
@@ -273,11 +274,21 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         for (int ri = 0; ri < 2; ri++)
 #pragma unroll
             for (int cj = 0; cj < 4; cj++) acc[ri][cj] = (v16i){};
+        /* 32-row blocks of this wave that hold valid rows (a wave-uniform
+         * count): padding-only blocks skip their MFMAs, which leaves the
+         * pipe to the CU's other block (tiles of cold experts are mostly
+         * padding) */
+        const int vrows = min(cur.M - cur.m0, MM_I8B_BM) - 64 * wr;
+        const int nri = __builtin_amdgcn_readfirstlane(vrows <= 0 ? 0 : vrows <= 32 ? 1 : 2);
         auto mma = [&](i32x4(&A)[2], i32x4(&B)[4]) {
+            if (nri > 0) {
 #pragma unroll
-            for (int ri = 0; ri < 2; ri++)
+                for (int cj = 0; cj < 4; cj++) acc[0][cj] = mfma32_i8(A[0], B[cj], acc[0][cj]);
+            }
+            if (nri > 1) {
 #pragma unroll
-                for (int cj = 0; cj < 4; cj++) acc[ri][cj] = mfma32_i8(A[ri], B[cj], acc[ri][cj]);
+                for (int cj = 0; cj < 4; cj++) acc[1][cj] = mfma32_i8(A[1], B[cj], acc[1][cj]);
+            }
         };
         read_ops(0, 0, Ar[0], Br[0]);
         for (int s = 0; s < KB; s++) {

@@ -15,7 +15,7 @@
  *                  routed and shared experts in one launch (decode sizes)
  *   mm_i8_quant_h  per-row quantisation of h -> qh, sh
  *   mm_i8_down     grouped down GEMM -> y per route (fp32)
- *   mm_i8_gemm_tiled  block-tiled variant of both GEMMs for prefill sizes
+ *   (prefill sizes use the big-tile GEMM of gemm_i8.hip instead of gu/down)
  *   mm_i8_combine  out[t] = sum_r w_r * y[t, r] + y_shared[t]
  *
  * The order of rows inside an expert's list depends on atomic timing, but
@@ -716,247 +716,5 @@ extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) 
         const size_t row = (size_t)nb * 16 + (lane & 15);
         const size_t col = (size_t)kb * 64 + 16 * (lane >> 4);
         *(v4i *)(a.dst + i * 16) = *(const v4i *)(src + row * a.K + col);
-    }
-}
-
-/* ---- tiled grouped GEMM (prefill) ------------------------------------------- */
-
-/* Block tile: MM_I8T_BM = 128 rows x MM_I8T_FR B fragments (gate/up: the
- * gate and up fragments of MM_I8T_FR / 2 column blocks of 16; plain:
- * MM_I8T_FR column blocks), K step 128 (two MFMA K halves of 64).  The four
- * waves split the fragments (MM_I8T_FR / 4 each) and share the rows.  The gathered A rows of a K step are staged through a 3-stage LDS
- * ring by direct global -> LDS loads of whole cache lines (8 rows x 128 B per
- * instruction: half-line accesses measured ~2.6x slower), XOR-swizzled so
- * that the operand reads are conflict-free, two steps ahead.  Every wave
- * streams its own B fragments (packed, 1 KB contiguous) with buffer loads
- * (scalar base and step offset, one lane-offset register) into a ring of
- * three 64-byte K halves, two halves ahead.  A wave tile is 128 rows x
- * MM_I8T_FR / 4 fragments (8 v_mfma_i32_16x16x64_i8 per fragment and K
- * half); 2 blocks fit a CU. */
-#define T_WF (MM_I8T_FR / 4)      /* B fragments per wave */
-#define T_NSA 3                   /* A stages (issued 2 steps ahead) */
-#define T_ASTAGE (128 * 128)      /* one K step of A: 128 rows x 128 B */
-
-/* One 128-row x MM_I8T_FR-fragment tile starting at row m0 of expert e (M rows). */
-__device__ __forceinline__ void tiled_tile(const mm_i8_tiled_args &a, int8_t (*lds)[T_ASTAGE],
-                                           int32_t *s_arow, float *s_sa, int32_t *s_rid,
-                                           int e, int m0, int M, int slab) {
-    const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
-    const int KB = (a.Kd + 127) / 128;                /* K steps; Kd % 128 == 64 leaves the
-                                                         last step half (its second half
-                                                         is skipped) */
-    const int KH = a.Kd / 64;                         /* 64-byte K halves */
-    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int fr0 = slab * MM_I8T_FR + wave * T_WF;   /* this wave's first fragment */
-    const int32_t *rows = a.rows ? a.rows + (size_t)e * a.T : nullptr;
-
-    /* the tile's rows: route id, A row and A scale (rows past M repeat row m0;
-     * their results are discarded) */
-    if (tid < MM_I8T_BM) {
-        const int m = m0 + tid < M ? m0 + tid : m0;
-        const int rid = rows ? rows[m] : m;
-        const int arow = (a.a_by_route || !rows) ? rid : rid / a.K;
-        s_rid[tid] = m0 + tid < M ? rid : -1;
-        s_arow[tid] = arow;
-        s_sa[tid] = a.sa[arow];
-    }
-    __syncthreads();
-
-    /* A: wave w issues instructions 4 w .. 4 w + 3 of a step (rows 32 w ..
-     * 32 w + 31); lane l carries row R = 8 i + l / 8 and stores at position
-     * l % 8 of the row's 128 B the chunk (l % 8) ^ swz(R).  32-bit offsets
-     * from a.a (rows x Kd < 2^31). */
-    uint32_t arow_off[4];
-    int aq[4];
-#pragma unroll
-    for (int h = 0; h < 4; h++) {
-        const int R = 8 * (4 * wave + h) + (lane >> 3);
-        arow_off[h] = (uint32_t)s_arow[R] * (uint32_t)a.Kd;
-        aq[h] = 16 * ((lane & 7) ^ t_swz(R));
-    }
-    /* B: fragment fr at K half k is 1 KB at gate/up [nb][k][gate|up]
-     * (fr = 2 nb + gate|up) or plain [nb][k]; fragments past the last are
-     * clamped (results discarded).  Buffer loads over the expert's fragments
-     * (cached: the other row tiles of the expert read them from L2). */
-    const int bstep = a.gu ? 2048 : 1024;
-    const uint32_t bytes_e = (uint32_t)(nfr_total * KH) * 1024u;
-    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(a.b + (size_t)e * a.b_expert_stride), 0, (int)bytes_e, 0x00020000);
-    int bfo[T_WF];   /* wave-uniform fragment offsets */
-#pragma unroll
-    for (int f = 0; f < T_WF; f++) {
-        const int fr = __builtin_amdgcn_readfirstlane(min(fr0 + f, nfr_total - 1));
-        bfo[f] = a.gu ? ((fr >> 1) * 2 * KH + (fr & 1)) * 1024 : fr * KH * 1024;
-    }
-    const int lane16 = lane * 16;
-    /* operand read of lane (c = l % 16, g = l / 16) for 16-row block mi and
-     * K half ks: row 16 mi + c, chunk 4 ks + g; the mi part is a compile-time
-     * offset */
-    const int c16 = lane & 15, g4 = lane >> 4;
-    const uint32_t rd0 = c16 * 128 + 16 * ((0 + g4) ^ t_swz(c16));
-    const uint32_t rd1 = c16 * 128 + 16 * ((4 + g4) ^ t_swz(c16));
-
-    v4i bq[3][T_WF];   /* B of three 64-byte K halves */
-    auto issue_a = [&](int kb, int st) {
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            const int k = kb * 128 + aq[h];   /* past Kd (a half last step): any valid chunk */
-            lds_dma16(a.a + (arow_off[h] + (uint32_t)(k < a.Kd ? k : k - 64)), lds[st] + (4 * wave + h) * 1024);
-        }
-    };
-    auto issue_b = [&](int hs, int slot) {   /* K half hs (clamped) */
-        const int so = __builtin_amdgcn_readfirstlane(min(hs, KH - 1) * bstep);
-#pragma unroll
-        for (int f = 0; f < T_WF; f++)
-            bq[slot][f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(brs, lane16, bfo[f] + so, 0));
-    };
-
-    v4i acc[8][T_WF];
-#pragma unroll
-    for (int mi = 0; mi < 8; mi++)
-#pragma unroll
-        for (int f = 0; f < T_WF; f++) acc[mi][f] = (v4i){0, 0, 0, 0};
-
-    /* Issue order: A(0), B(0), A(1), B(1); then step kb issues B(2kb+2),
-     * A(kb+2) at its start and B(2kb+3) after its first half.  At the top
-     * of step kb the groups after B(2kb) and A(kb) are A(kb+1) and B(2kb+1):
-     * 8 transfers.  Steps past the end re-load the last (unconditional loads
-     * keep the wait counts static). */
-    issue_a(0, 0);
-    issue_b(0, 0);
-    issue_a(min(1, KB - 1), 1);
-    issue_b(1, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    auto half = [&](uint32_t sa, int slot, int bmask) {   /* bmask 0: a half past Kd adds nothing */
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            v4i av[2];
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++) av[mi] = ds_read16(sa, (2 * h + mi) * 2048);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[0]), "+v"(av[1]));
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-                for (int f = 0; f < T_WF; f++)
-                    acc[2 * h + mi][f] = mfma_i8(av[mi], bq[slot][f] & bmask, acc[2 * h + mi][f]);
-        }
-    };
-    auto step = [&](int kb, int j) {   /* j = kb % 6: A stage j % 3, B slots (2j) % 3, (2j+1) % 3 */
-        VMCNT_WAIT(4 + T_WF);          /* A(kb) and B(2kb) of this wave have landed: only
-                                          A(kb+1) and B(2kb+1) came after B(2kb) */
-        __builtin_amdgcn_s_barrier();  /* every wave's A part of step kb has landed,
-                                          and step kb-1's stage is no longer read */
-        __builtin_amdgcn_sched_barrier(0);
-        issue_b(2 * kb + 2, (2 * j + 2) % 3);
-        issue_a(min(kb + 2, KB - 1), (j + 2) % 3);
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t st = lds_addr(lds[j % 3]);
-        half(st + rd0, (2 * j) % 3, -1);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_b(2 * kb + 3, (2 * j) % 3);
-        __builtin_amdgcn_sched_barrier(0);
-        VMCNT_WAIT(2 * T_WF + 4);      /* B(2kb+1): B(2kb+2), A(kb+2), B(2kb+3) came after it */
-        /* a half last step (Kd % 128 == 64): the second half's B is zeroed
-         * (no branch, which would cost registers) */
-        half(st + rd1, (2 * j + 1) % 3, __builtin_amdgcn_readfirstlane(2 * kb + 1 < KH ? -1 : 0));
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    /* rounds of 6 steps keep the slot and stage indices compile-time */
-    int k0 = 0;
-    for (; k0 + 6 <= KB; k0 += 6) {
-#pragma unroll
-        for (int j = 0; j < 6; j++) step(k0 + j, j);
-    }
-#pragma unroll
-    for (int j = 0; j < 5; j++)
-        if (k0 + j < KB) step(k0 + j, j);
-    VMCNT_WAIT(0);   /* the trailing groups land before the next tile reuses the stages */
-
-    /* epilogue: lane holds rows 16 mi + 4 (lane / 16) + i of column
-     * (lane % 16) of each of its fragments */
-    const float *sb0 = a.sb0 + (size_t)e * a.sb_expert_stride;
-    const float *sb1 = a.sb1 ? a.sb1 + (size_t)e * a.sb_expert_stride : nullptr;
-    /* column scales in registers before the stores (the compiler would
-     * otherwise reload them after every store, see bt_tile) */
-    float c0[T_WF], c1[T_WF];
-#pragma unroll
-    for (int f = 0; f < T_WF; f++) {
-        const int nb = a.gu ? (fr0 >> 1) + f : fr0 + f;
-        const int col = min(nb, a.N / 16 - 1) * 16 + (lane & 15);
-        c0[f] = sb0[col];
-        c1[f] = a.gu ? sb1[col] : 0.0f;
-        asm volatile("" : "+v"(c0[f]), "+v"(c1[f]));
-    }
-#pragma unroll
-    for (int mi = 0; mi < 8; mi++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = mi * 16 + 4 * (lane >> 4) + i;
-            const int rid = s_rid[r];
-            if (rid < 0) continue;
-            const float sa = s_sa[r];
-            if (a.gu) {
-#pragma unroll
-                for (int k = 0; k < T_WF / 2; k++) {
-                    const int nb = (fr0 >> 1) + k;
-                    if (nb * 16 >= a.N) continue;
-                    const int col = nb * 16 + (lane & 15);
-                    const int32_t ag = acc[mi][2 * k][i], au = acc[mi][2 * k + 1][i];
-                    const float g = ((float)ag * sa) * c0[k];
-                    const float u = ((float)au * sa) * c1[k];
-                    a.out[(size_t)rid * a.N + col] = silu_mul(g, u);
-                    if (a.dbg_acc) {
-                        a.dbg_acc[((size_t)rid * 2) * a.N + col] = ag;
-                        a.dbg_acc[((size_t)rid * 2 + 1) * a.N + col] = au;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int f = 0; f < T_WF; f++) {
-                    const int nb = fr0 + f;
-                    if (nb * 16 >= a.N) continue;
-                    const int col = nb * 16 + (lane & 15);
-                    const int32_t ac = acc[mi][f][i];
-                    a.out[(size_t)rid * a.N + col] = ((float)ac * sa) * c0[f];
-                    if (a.dbg_acc) a.dbg_acc[(size_t)rid * a.N + col] = ac;
-                }
-            }
-        }
-    }
-}
-
-/* 1-D grid (a multiple of 64 blocks, see the host).  Blocks are dealt to
- * the 8 XCDs round robin (block b runs on XCD b % 8); b is mapped to (column
- * slab, row group) so that each XCD receives runs of 8 consecutive row
- * groups of ONE slab: the slab's weights then come from HBM once per run
- * and from that XCD's L2 for the other row groups (the tiles of a hot
- * expert are consecutive row groups). */
-#ifndef T_OCC
-#define T_OCC 2                   /* blocks per CU the register budget is sized for */
-#endif
-extern "C" __global__ __launch_bounds__(256, T_OCC) void mm_i8_gemm_tiled(mm_i8_tiled_args a) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[T_NSA][T_ASTAGE];
-    __shared__ int32_t s_arow[MM_I8T_BM], s_rid[MM_I8T_BM];
-    __shared__ float s_sa[MM_I8T_BM];
-    const int nfr_total = (a.gu ? 2 : 1) * (a.N / 16);
-    const int nslab = (nfr_total + MM_I8T_FR - 1) / MM_I8T_FR;
-    const int b = blockIdx.x;
-    const int xcd = b % MM_I8S_XCD, j = b / MM_I8S_XCD;
-#ifdef T_MAP_SLAB_MINOR
-    const int slab = j % nslab;
-    const int grp = (j / nslab) * MM_I8S_XCD + xcd;
-#else
-    const int q = (j / MM_I8S_XCD) * MM_I8S_XCD + xcd;   /* (slab, row-group run) index */
-    const int slab = q % nslab;
-    const int grp = (q / nslab) * MM_I8S_XCD + j % MM_I8S_XCD;
-#endif
-    if (grp >= a.max_groups) return;                      /* uniform per block */
-    int e, g0, M;
-    if (!tile_owner(a, grp, &e, &g0, &M)) return;
-    const int g1 = min(M, g0 + a.mgroup * MM_I8T_BM);
-    for (int m0 = g0; m0 < g1; m0 += MM_I8T_BM) {
-        tiled_tile(a, lds, s_arow, s_sa, s_rid, e, m0, M, slab);
-        __syncthreads();   /* the LDS ring and row tables are refilled by the next tile */
     }
 }

@@ -19,13 +19,11 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.fixture(params=["decode", "tiled", "tiled8"])
+@pytest.fixture(params=["decode", "tiled"])
 def ctx(request, monkeypatch):
     """A context whose int8 GEMMs take the decode-shaped path or the tiled
-    (prefill) path for every T: the big-tile kernel ("tiled") or the
-    8-fragment tiled kernel ("tiled8")."""
-    monkeypatch.setenv("MLAMOE_I8_TILED_MIN_T", "1" if request.param != "decode" else "1000000000")
-    monkeypatch.setenv("MLAMOE_I8_BT", "0" if request.param == "tiled8" else "1")
+    (prefill, big-tile) path for every T."""
+    monkeypatch.setenv("MLAMOE_I8_TILED_MIN_T", "1" if request.param == "tiled" else "1000000000")
     print(f"int8 GEMM path: {request.param}", flush=True)
     c = mlamoe.Context(0)
     yield c
