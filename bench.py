@@ -6,9 +6,11 @@ per-output-channel weights (from bf16 N(0, 0.02)), uniform-random fp32 router
 logits per layer, residual carried through the stack (x += ffn(x)), weights
 resident in HBM.  A step is one pass of the 64 tokens through the 26 layers.
 
-The same line carries, under "extra", the other MoE configurations measured
-in the same run: config 3 (prefill T=2048, int8, Zipf-skewed routing, router
-GEMV included) and config 1 (T=1 decode layer, bf16 weights).
+The same line carries, under "extra", the other configurations measured in
+the same run: config 3 (prefill T=2048, int8, Zipf-skewed routing, router
+GEMV included), config 1 (T=1 decode layer, bf16 weights), config 5 (MLA
+absorbed decode), config 2 (dense bf16 projections) and the LM head of a
+decode step (vocabulary 102400, B = 1 and 64).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 """
@@ -303,6 +305,39 @@ def bench_dense_bf16(ctx, steps, warmup, T=512):
                 kernel_avg_us=round(prof["mm_gemm_bf16"][0] * 1e3, 2), gflop=flops / 1e9)
 
 
+def bench_lm_head(ctx, steps, warmup, V=102400, H=2048):
+    """LM head of a decode step on DeepSeek-V2-Lite's vocabulary: final
+    RMSNorm, logits over V (bf16 [V, H] weight), greedy argmax, for B = 1
+    (GEMV) and B = 64 (the config-4 batch; MFMA GEMM)."""
+    log("[lm_head] setup")
+    w = ctx.empty((V, H), np.uint16)
+    ctx.fill(w, V * H, mlamoe.MM_FILL_BF16_NORMAL, 61, 0.02)
+    norm = ctx.empty((H,), np.uint16)
+    ctx.fill(norm, H, mlamoe.MM_FILL_BF16_NORMAL, 62, 1.0)
+    lib, h = mlamoe.lib(), ctx.h
+    res = {}
+    for B in (1, 64):
+        x = ctx.empty((B, H), np.float32)
+        ctx.fill(x, B * H, mlamoe.MM_FILL_F32_NORMAL, 63 + B, 1.0)
+        lg = ctx.empty((B, V), np.float32)
+        tok = ctx.empty((B,), np.int32)
+
+        def step():
+            mlamoe._check(lib.mm_lm_head_dev(h, B, x.ptr, norm.ptr, 1e-6, w.ptr, V, H, lg.ptr,
+                                             tok.ptr))
+        ms, _ = timed(ctx, step, steps * 5, warmup)
+        names = ["mm_rmsnorm", "mm_lm_gemv", "mm_cvt_bf16", "mm_gemm_bf16", "mm_argmax_part",
+                 "mm_argmax_final"]
+        prof = profile_kernels(ctx, step, 20, names)
+        nbytes = V * H * 2 + B * V * 4 + B * H * 4 + H * 2  # weights, logits out, x, norm
+        flops = 2.0 * B * V * H
+        res[f"B{B}"] = dict(ms_per_step=ms, tok_s=B / (ms * 1e-3), gbs=nbytes / (ms * 1e-3) / 1e9,
+                            frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                            tflops=flops / (ms * 1e-3) / 1e12,
+                            kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items() if v[1]})
+    return res
+
+
 # ---------------------------------------------------------------------------
 
 def cpu_baseline_decode(B=64, seconds_hint=True):
@@ -348,7 +383,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["decode_i8", "prefill_i8", "decode_bf16", "mla", "dense",
-                                       "calib"],
+                                       "lm_head", "calib"],
                     help="run one workload and print its result dict (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (reference kernel for the "
@@ -372,7 +407,7 @@ def main():
     if args.only:
         fn = dict(decode_i8=bench_decode_i8, prefill_i8=bench_prefill_i8,
                   decode_bf16=bench_decode_bf16, mla=bench_mla_decode,
-                  dense=bench_dense_bf16)[args.only]
+                  dense=bench_dense_bf16, lm_head=bench_lm_head)[args.only]
         with mlamoe.Context(0) as ctx:
             print(json.dumps({args.only: fn(ctx, args.steps, args.warmup)}, default=float), flush=True)
         return
@@ -389,6 +424,8 @@ def main():
             extra["mla_decode_config5"] = bench_mla_decode(ctx, args.steps, args.warmup)
         with mlamoe.Context(0) as ctx:
             extra["dense_bf16_config2"] = bench_dense_bf16(ctx, args.steps, args.warmup)
+        with mlamoe.Context(0) as ctx:
+            extra["lm_head_dsv2"] = bench_lm_head(ctx, args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
     line = {

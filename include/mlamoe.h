@@ -194,6 +194,31 @@ MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, i
 MM_API int mm_matmul_bf16_dev(mm_ctx *ctx, float *y, const float *x, const uint16_t *w,
                               int d_out, int n_in, int T, unsigned flags);
 
+/* ---- LM head: final RMSNorm, logits, greedy sampling ------------------------- */
+
+/* rmsnorm (src/run.c:22-27) of T rows: y[t] = (x[t] * inv) * w with
+ * inv = 1 / sqrtf(sum(x[t]^2) / n + eps); w bf16 [n].  Device pointers,
+ * asynchronous; y may equal x. */
+MM_API int mm_rmsnorm_dev(mm_ctx *ctx, int T, const float *x, const uint16_t *w, int n, float eps,
+                          float *y);
+
+/* sample (src/run.c:503-508) of T rows of logits: tokens[t] = the first index
+ * of the maximum (strict '>' scan from index 0; NaNs never win; a NaN at
+ * index 0 selects 0).  Device pointers, asynchronous. */
+MM_API int mm_argmax_dev(mm_ctx *ctx, int T, const float *logits, int n, int32_t *tokens);
+
+/* The decode step's LM head for B tokens (src/run.c:493-494 followed by
+ * sample, run.c:503-508): xb = rmsnorm(x, norm, eps), logits = xb . lm_head^T
+ * (lm_head bf16 [vocab, hidden]), tokens = greedy argmax.  `logits` may be
+ * NULL (not returned).  Up to 4 tokens with hidden <= 2048 take a GEMV that
+ * reads each weight row once; more take the bf16 MFMA GEMM with x carried as
+ * a hi/lo pair.  hidden % 8 == 0.  Device pointers, asynchronous.  Replaces
+ * the reference's CPU tail of forward_absorbed / forward_unabsorbed and its
+ * GPU lm_head GEMV + argmax (src/getp_run.hip:550-554). */
+MM_API int mm_lm_head_dev(mm_ctx *ctx, int B, const float *x, const uint16_t *norm, float eps,
+                          const uint16_t *lm_head, int vocab, int hidden, float *logits,
+                          int32_t *tokens);
+
 /* ---- MLA absorbed decode --------------------------------------------------- */
 
 /* The attention fields of the reference Config (include/model.h:12-42). */

@@ -45,4 +45,11 @@ mm_co_gemm_bf16:
 mm_co_gemm_i8:
     .incbin "gemm_i8.hsaco"
 
+    .balign 4096
+    .globl mm_co_lm_head
+    .hidden mm_co_lm_head
+    .type mm_co_lm_head, @object
+mm_co_lm_head:
+    .incbin "lm_head.hsaco"
+
     .section .note.GNU-stack, "", @progbits

@@ -2,28 +2,22 @@
  * (src/run.c:29-37) batched over T rows. */
 #include "mm_internal.h"
 
-int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out,
-                       int n_in, int T, unsigned flags) {
-    if (!c || (T > 0 && (!y || !x || !w)))
-        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: NULL argument");
-    if (T < 0 || d_out <= 0 || n_in <= 0)
-        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: bad shape");
-    if (n_in % 8)
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_matmul_bf16_dev: n_in must be a multiple of 8");
-    if ((uintptr_t)x % 16 || (uintptr_t)w % 16)
-        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: x and w must be 16-byte aligned");
-    if (T == 0) return MM_OK;
-    int st = mm_set_device(c);
-    if (st) return st;
+size_t mm_gemm_bf16_ws_bytes(int T, int n_in, unsigned flags) {
+    const int split = (flags & MM_MATMUL_X_BF16) == 0;
+    const size_t xb = (size_t)T * ((n_in + 63) / 64 * 64) * 2;
+    return (split ? 2 : 1) * ((xb + 255) & ~(size_t)255);
+}
+
+int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
+                    int T, unsigned flags, char *ws) {
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
     /* x as bf16 rows of a stride padded to 64 (zeros past n_in) */
     const int kp = (n_in + 63) / 64 * 64;
     const size_t xb = (size_t)T * kp * 2;
-    char *ws;
-    if ((st = mm_workspace(c, (split ? 2 : 1) * ((xb + 255) & ~(size_t)255), (void **)&ws))) return st;
     uint16_t *xh = (uint16_t *)ws, *xl = split ? (uint16_t *)(ws + ((xb + 255) & ~(size_t)255)) : NULL;
     mm_cvt_bf16_args ca = {x, xh, xl, T, n_in, kp, split};
     const size_t chunks = (size_t)T * kp / 8;
+    int st;
     if ((st = mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca))) return st;
     /* block tile columns: the widest of 128, 64, 32 that still gives 192
      * tiles (most of the 256 CUs), else 32 -- the projections of this path
@@ -44,4 +38,22 @@ int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, i
     const size_t stage = (size_t)(split ? 2 : 1) * 16384 + (size_t)bn * 128;
     const size_t lds = (split ? 3 : 4) * stage;
     return mm_launch(c, K_GEMM_BF16, (unsigned)(8 * ((nbx + 7) / 8) * nby), 1, 1, 256, lds, &a);
+}
+
+int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out,
+                       int n_in, int T, unsigned flags) {
+    if (!c || (T > 0 && (!y || !x || !w)))
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: NULL argument");
+    if (T < 0 || d_out <= 0 || n_in <= 0)
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: bad shape");
+    if (n_in % 8)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_matmul_bf16_dev: n_in must be a multiple of 8");
+    if ((uintptr_t)x % 16 || (uintptr_t)w % 16)
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_dev: x and w must be 16-byte aligned");
+    if (T == 0) return MM_OK;
+    int st = mm_set_device(c);
+    if (st) return st;
+    char *ws;
+    if ((st = mm_workspace(c, mm_gemm_bf16_ws_bytes(T, n_in, flags), (void **)&ws))) return st;
+    return mm_gemm_bf16_ws(c, y, x, w, d_out, n_in, T, flags, ws);
 }

@@ -31,6 +31,10 @@ typedef enum {
     K_MLA_WPREP,
     K_GEMM_BF16,
     K_CVT_BF16,
+    K_RMSNORM,
+    K_LM_GEMV,
+    K_ARGMAX_PART,
+    K_ARGMAX_FINAL,
     K_COUNT
 } mm_kernel_id;
 
@@ -101,6 +105,12 @@ int mm_launch(mm_ctx *ctx, mm_kernel_id id, unsigned gx, unsigned gy, unsigned g
 /* Device workspace of at least `bytes`, reallocated (after a stream sync)
  * when too small. */
 int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
+
+/* Dense bf16 GEMM (mm_matmul_bf16_dev) on a caller-provided workspace of at
+ * least mm_gemm_bf16_ws_bytes(T, n_in, flags) bytes. */
+size_t mm_gemm_bf16_ws_bytes(int T, int n_in, unsigned flags);
+int mm_gemm_bf16_ws(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
+                    int T, unsigned flags, char *ws);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

@@ -69,9 +69,6 @@ typedef struct {
     int rows, K;
 } mm_quant_w_args;
 
-
-#endif
-
 /* ---- int8 MoE path ------------------------------------------------------ */
 
 /* Per-layer int8 weights in MFMA fragment order.  A "fragment" is the
@@ -286,3 +283,37 @@ typedef struct {
     int accumulate;
     int bn;                  /* block tile columns: 128, 64 or 32 */
 } mm_gemm_bf16_args;
+
+/* ---- LM head (final RMSNorm, logits, greedy argmax) ------------------------- */
+#define MM_LM_NB 4                /* tokens served by the logits GEMV (more: the MFMA GEMM) */
+#define MM_LM_HMAX 2048           /* hidden sizes served by the logits GEMV */
+typedef struct {
+    const float *x;          /* [T, n] */
+    const uint16_t *w;       /* [n] bf16 */
+    float *y;                /* [T, n] */
+    int n;
+    float eps;
+} mm_rmsnorm_args;
+
+typedef struct {
+    const float *x;          /* [B, H] activations before the final norm */
+    const uint16_t *norm;    /* [H] bf16 final RMSNorm weight */
+    float eps;
+    const uint16_t *w;       /* [V, H] bf16 */
+    float *y;                /* [B, V] logits */
+    float *part_v;           /* [B, waves] per-wave best logit */
+    int32_t *part_i;         /* [B, waves] its row */
+    int B, V, H;
+} mm_lm_gemv_args;
+
+#define MM_ARGMAX_SEG 1024       /* row elements per argmax segment (block) */
+#define MM_LM_GEMV_BLOCKS 2048   /* GEMV grid (4 waves each): argmax partials per token */
+typedef struct {
+    const float *logits;     /* [T, n] */
+    int32_t *tokens;         /* [T] */
+    float *part_v;           /* [T, nseg] segment maxima */
+    int32_t *part_i;         /* [T, nseg] their indices */
+    int n, T, nseg;
+} mm_argmax_args;
+
+#endif /* MLAMOE_KERNEL_PARAMS_H */

@@ -107,6 +107,10 @@ def lib():
         L.mm_moe_router_logits_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp]
         L.mm_moe_forward_i8_debug_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
                                                   _vp, _vp, C.c_uint, C.POINTER(MoeI8Debug)]
+        L.mm_rmsnorm_dev.argtypes = [_vp, C.c_int, _vp, _vp, C.c_int, C.c_float, _vp]
+        L.mm_argmax_dev.argtypes = [_vp, C.c_int, _vp, C.c_int, _vp]
+        L.mm_lm_head_dev.argtypes = [_vp, C.c_int, _vp, _vp, C.c_float, _vp, C.c_int, C.c_int,
+                                     _vp, _vp]
         _lib = L
     return _lib
 
@@ -345,6 +349,54 @@ class Context:
             b.free()
             self._bufs.remove(b)
         return y
+
+    # LM head ------------------------------------------------------------------
+    def _tmp(self, bufs):
+        for b in bufs:
+            if b is not None:
+                b.free()
+                self._bufs.remove(b)
+
+    def rmsnorm(self, x, w, eps):
+        """Mirror of rmsnorm (src/run.c:22-27) over the rows of x."""
+        w = np.ascontiguousarray(w, np.uint16)
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, w.size)
+        dx, dw, dy = self.to_device(x), self.to_device(w), self.empty(x.shape, np.float32)
+        _check(lib().mm_rmsnorm_dev(self.h, x.shape[0], dx.ptr, dw.ptr, w.size, float(eps), dy.ptr))
+        y = dy.download()
+        self._tmp((dx, dw, dy))
+        return y
+
+    def argmax(self, logits):
+        """Mirror of sample (src/run.c:503-508) over the rows of logits."""
+        lg = np.ascontiguousarray(logits, np.float32)
+        rows = lg.reshape(-1, lg.shape[-1])
+        dl, dt = self.to_device(rows), self.empty((rows.shape[0],), np.int32)
+        _check(lib().mm_argmax_dev(self.h, rows.shape[0], dl.ptr, rows.shape[1], dt.ptr))
+        t = dt.download()
+        self._tmp((dl, dt))
+        return t.reshape(lg.shape[:-1])
+
+    def lm_head_dev(self, B, x, norm, eps, lm_head, vocab, hidden, logits, tokens):
+        _check(lib().mm_lm_head_dev(self.h, B, x.ptr, norm.ptr, float(eps), lm_head.ptr, vocab,
+                                    hidden, logits.ptr if logits is not None else None, tokens.ptr))
+
+    def lm_head(self, x, norm, eps, lm_head, want_logits=True):
+        """Final rmsnorm + lm_head matmul + greedy argmax for the rows of x
+        (src/run.c:493-494, 503-508); returns (logits or None, tokens)."""
+        lm_head = np.ascontiguousarray(lm_head, np.uint16)
+        V, H = lm_head.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
+        B = x.shape[0]
+        dx, dn, dw = self.to_device(x), self.to_device(np.ascontiguousarray(norm, np.uint16)), \
+            self.to_device(lm_head)
+        dl = self.empty((B, V), np.float32) if want_logits else None
+        dt = self.empty((B,), np.int32)
+        self.lm_head_dev(B, dx, dn, eps, dw, V, H, dl, dt)
+        logits = dl.download() if dl is not None else None
+        tokens = dt.download()
+        self._tmp((dx, dn, dw, dl, dt))
+        return logits, tokens
 
     # MLA absorbed decode -------------------------------------------------------
     def mla_init(self, NH, QKN=128, QKR=64, KVL=512, VHD=128, scale=None, n_layers=1):

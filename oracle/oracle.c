@@ -54,6 +54,39 @@ void or_matmul_rows(float *y, const float *x, const uint16_t *w, int T, int d_ou
         or_matmul(y + (size_t)t * d_out, x + (size_t)t * n_in, w, d_out, n_in);
 }
 
+/* src/run.c:22-27 (rmsnorm). */
+void or_rmsnorm(float *y, const float *x, const uint16_t *w, int n, float eps) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = 0; i < n; i++) y[i] = x[i] * inv * or_bf16_to_f32(w[i]);
+}
+
+/* src/run.c:503-508 (sample: greedy argmax). */
+int or_argmax(const float *logits, int n) {
+    int best = 0;
+    float bv = logits[0];
+    for (int i = 1; i < n; i++)
+        if (logits[i] > bv) {
+            bv = logits[i];
+            best = i;
+        }
+    return best;
+}
+
+/* src/run.c:493-494 (final rmsnorm + lm_head matmul) followed by sample(). */
+void or_lm_head_rows(const float *x, const uint16_t *norm, float eps, const uint16_t *lm_head,
+                     int T, int vocab, int hidden, float *logits, int32_t *tokens) {
+    float *xb = malloc((size_t)hidden * sizeof(float));
+    for (int t = 0; t < T; t++) {
+        float *lg = logits + (size_t)t * vocab;
+        or_rmsnorm(xb, x + (size_t)t * hidden, norm, hidden, eps);
+        or_matmul(lg, xb, lm_head, vocab, hidden);
+        tokens[t] = or_argmax(lg, vocab);
+    }
+    free(xb);
+}
+
 /* src/run.c:39 */
 float or_silu(float x) { return x / (1.0f + expf(-x)); }
 

@@ -13,7 +13,8 @@
  *
  * Parity pinning (how each function is checked, see tests/test_oracle_*.py):
  *   - bf16 conversions, or_matmul, or_silu, or_swiglu, or_softmax, or_route,
- *     or_ffn_compute, or_absorbed_*: bit-exact against golden vectors written
+ *     or_ffn_compute, or_absorbed_*, or_rmsnorm, or_argmax: bit-exact against
+ *     golden vectors written
  *     by the reference's own compiled run.c (tests/golden/), against
  *     oracle/_ref/libref.so where it is built, and against closed forms
  *     (integer-valued operands, one-hot weights, equal logits, kv_len == 1).
@@ -48,6 +49,17 @@ float or_silu(float x);
 void  or_swiglu(float *dst, const float *x, const uint16_t *gate, const uint16_t *up,
                 const uint16_t *down, int inter, int hidden, float *hb, float *hb2);
 void  or_softmax(float *x, int n);
+
+/* ---- LM head (src/run.c:22-27, 493-494, 503-508) ---------------------- */
+/* y = (x / rms(x)) * w over n elements: sequential sum of squares, one
+ * 1/sqrtf(ss/n + eps), then (x[i] * inv) * w[i]. */
+void  or_rmsnorm(float *y, const float *x, const uint16_t *w, int n, float eps);
+/* greedy argmax: the first index of the maximum under a strict '>' scan
+ * from index 0 (a NaN never wins; logits[0] = NaN selects 0). */
+int   or_argmax(const float *logits, int n);
+/* T tokens: xb = rmsnorm(x[t]), logits[t] = matmul(xb), tokens[t] = argmax. */
+void  or_lm_head_rows(const float *x, const uint16_t *norm, float eps, const uint16_t *lm_head,
+                      int T, int vocab, int hidden, float *logits, int32_t *tokens);
 
 /* ---- MoE FFN (src/run.c:107-162) ------------------------------------- */
 /* Mirrors the MoE fields of Config (include/model.h:12-42). */

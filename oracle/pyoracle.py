@@ -83,6 +83,11 @@ def lib():
         L.or_swiglu.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, C.c_int, C.c_int,
                                 _f32p, _f32p]
         L.or_softmax.argtypes = [_f32p, C.c_int]
+        L.or_rmsnorm.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_float]
+        L.or_argmax.restype = C.c_int
+        L.or_argmax.argtypes = [_f32p, C.c_int]
+        L.or_lm_head_rows.argtypes = [_f32p, _u16p, C.c_float, _u16p, C.c_int, C.c_int, C.c_int,
+                                      _f32p, _i32p]
         L.or_route.argtypes = [C.POINTER(MoeCfg), _f32p, _f32p, _ip, _f32p]
         L.or_ffn_compute.argtypes = [C.POINTER(MoeCfg), C.POINTER(MoeWeights), _f32p,
                                      _f32p, _ip, _f32p, _f32p]
@@ -119,6 +124,9 @@ def ref():
         R.ref_silu.restype = C.c_float
         R.ref_silu.argtypes = [C.c_float]
         R.ref_softmax.argtypes = [_f32p, C.c_int]
+        R.ref_rmsnorm.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_float]
+        R.ref_sample.restype = C.c_int
+        R.ref_sample.argtypes = [_f32p, C.c_int]
         R.ref_swiglu.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, C.c_int, C.c_int,
                                  _f32p, _f32p]
         R.ref_ffn_compute.argtypes = [C.c_int] * 7 + [C.c_float] + [_u16p, _f32p] + \
@@ -153,6 +161,42 @@ def softmax(x):
     x = c32(x).copy()
     lib().or_softmax(_p(x, _f32p), x.size)
     return x
+
+
+def rmsnorm(x, w, eps):
+    """run.c:22-27 on each row of x ([T, n] or [n]); w bf16 [n]."""
+    x = c32(x)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    n = w.size
+    x2 = x.reshape(-1, n)
+    y = np.empty_like(x2)
+    for t in range(x2.shape[0]):
+        lib().or_rmsnorm(_p(y[t], _f32p), _p(np.ascontiguousarray(x2[t]), _f32p), _p(w, _u16p),
+                         n, float(eps))
+    return y.reshape(x.shape)
+
+
+def argmax(logits):
+    """run.c:503-508 sample() on each row of logits."""
+    lg = c32(logits)
+    rows = lg.reshape(-1, lg.shape[-1])
+    return np.array([lib().or_argmax(_p(np.ascontiguousarray(r), _f32p), r.size) for r in rows],
+                    np.int32).reshape(lg.shape[:-1])
+
+
+def lm_head_rows(x, norm, eps, lm_head):
+    """Final rmsnorm + lm_head matmul + greedy argmax (run.c:493-494, 503-508)
+    for T tokens; returns (logits [T, V], tokens [T])."""
+    x = c32(x)
+    norm = np.ascontiguousarray(norm, dtype=np.uint16)
+    lm_head = np.ascontiguousarray(lm_head, dtype=np.uint16)
+    V, H = lm_head.shape
+    T = x.shape[0]
+    logits = np.empty((T, V), np.float32)
+    tokens = np.empty(T, np.int32)
+    lib().or_lm_head_rows(_p(x, _f32p), _p(norm, _u16p), float(eps), _p(lm_head, _u16p), T, V, H,
+                          _p(logits, _f32p), _p(tokens, _i32p))
+    return logits, tokens
 
 
 def moe_cfg(H, E, n_shared, K, I, router_sigmoid=0, norm_topk=0, routed_scaling=1.0):
@@ -291,6 +335,19 @@ def absorbed_decode(q, kv_b, cache, kv_len, NH, QKN, QKR, KVL, VHD, scale=None,
 # ---------------------------------------------------------------------------
 # reference-library helpers (build container only)
 # ---------------------------------------------------------------------------
+
+def ref_rmsnorm(x, w, eps):
+    x = c32(x)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    y = np.empty_like(x)
+    ref().ref_rmsnorm(_p(y, _f32p), _p(x, _f32p), _p(w, _u16p), x.size, float(eps))
+    return y
+
+
+def ref_sample(logits):
+    lg = c32(logits).copy()
+    return int(ref().ref_sample(_p(lg, _f32p), lg.size))
+
 
 def ref_matmul(x, w):
     x = c32(x)

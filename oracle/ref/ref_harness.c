@@ -6,7 +6,7 @@
  * /root/reference/src and /root/reference/include. That makes the
  * `#include "run.c"` below pull in the reference's src/run.c from where it
  * lies, unmodified, and that is the only way to reach its `static`
- * functions (matmul, swiglu, softmax, ffn_compute). `main` is renamed to an
+ * functions (matmul, swiglu, softmax, rmsnorm, ffn_compute). `main` is renamed to an
  * unused static function on the command line, so the library needs nothing
  * beyond libc/libm and the reference's src/dump.c.  The output goes only to
  * oracle/_ref/ (git-ignored).
@@ -22,6 +22,12 @@ void ref_matmul(float *y, const float *x, const uint16_t *w, int d_out, int n_in
 float ref_silu(float x) { return silu(x); }
 
 void ref_softmax(float *x, int n) { softmax(x, n); }
+
+void ref_rmsnorm(float *y, const float *x, const uint16_t *w, int n, float eps) {
+    rmsnorm(y, x, w, n, eps);
+}
+
+int ref_sample(float *logits, int n) { return sample(logits, n); }
 
 void ref_swiglu(float *dst, const float *x, const uint16_t *gate, const uint16_t *up,
                 const uint16_t *down, int inter, int hidden, float *hb, float *hb2) {

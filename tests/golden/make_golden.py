@@ -7,7 +7,7 @@ reference's src/run.c compiled from its own sources into oracle/_ref/libref.so
 regenerated from the recorded seed with mlamoe.synth, and a checksum of each
 regenerated tensor is stored so a test can prove it rebuilt the same bytes.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [fixture ...]
 """
 from __future__ import annotations
 
@@ -182,14 +182,53 @@ def gen_absorbed():
     np.savez_compressed(os.path.join(OUT, "absorbed.npz"), **d)
 
 
+def gen_lm_head():
+    """rmsnorm (run.c:22-27), sample (run.c:503-508) and the final norm +
+    lm_head matmul + sample of one small decode step (run.c:493-494)."""
+    rng = np.random.default_rng(601)
+    d = {}
+    for name, (n, eps, xs) in dict(small=(8, 1e-6, 1.0), hidden=(2048, 1e-6, 1.0),
+                                   glm=(64, 1e-5, 30.0), tiny=(64, 1e-6, 1e-3)).items():
+        x = synth.normal_f32(rng, (n,), xs)
+        w = synth.bf16_from_f32(1.0 + synth.normal_f32(rng, (n,), 0.1))
+        d[f"rms_{name}_x"], d[f"rms_{name}_w"] = x, w
+        d[f"rms_{name}_eps"] = np.float32(eps)
+        d[f"rms_{name}_y"] = O.ref_rmsnorm(x, w, eps)
+    lg = synth.normal_f32(rng, (1000,))
+    tie = synth.normal_f32(rng, (50,))
+    tie[7] = tie[31] = np.float32(tie.max() + 1.0)
+    nan0 = synth.normal_f32(rng, (40,))
+    nan0[0] = np.nan
+    nanmid = synth.normal_f32(rng, (40,))
+    nanmid[[3, 17]] = np.nan
+    ninf = np.full(20, -np.inf, np.float32)
+    pinf = synth.normal_f32(rng, (30,))
+    pinf[[12, 20]] = np.inf
+    for name, v in dict(random=lg, tie=tie, nan0=nan0, nanmid=nanmid, ninf=ninf,
+                        pinf=pinf).items():
+        v = v.astype(np.float32)
+        d[f"sample_{name}_in"] = v
+        d[f"sample_{name}_out"] = np.int32(O.ref_sample(v))
+    T, V, H = 3, 512, 256
+    x = synth.normal_f32(rng, (T, H))
+    norm = synth.bf16_from_f32(1.0 + synth.normal_f32(rng, (H,), 0.1))
+    lm = synth.normal_bf16(rng, (V, H), 0.02)
+    logits = np.stack([O.ref_matmul(O.ref_rmsnorm(x[t], norm, 1e-6), lm) for t in range(T)])
+    d.update(lm_x=x, lm_norm=norm, lm_w=lm, lm_eps=np.float32(1e-6), lm_logits=logits,
+             lm_tokens=np.array([O.ref_sample(r) for r in logits], np.int32))
+    np.savez_compressed(os.path.join(OUT, "lm_head.npz"), **d)
+
+
+GENERATORS = dict(matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),
+                  ffn_tiny=lambda: gen_ffn_tiny(), absorbed=lambda: gen_absorbed(),
+                  ffn_dsv2=lambda: gen_ffn_dsv2(), lm_head=lambda: gen_lm_head())
+
 if __name__ == "__main__":
     if not O.ref_available():
         O.build(ref=True)
-    gen_matmul()
-    gen_softmax_silu()
-    gen_ffn_tiny()
-    gen_absorbed()
-    gen_ffn_dsv2()
+    # python make_golden.py [name ...]: only the named fixtures
+    for name in (sys.argv[1:] or list(GENERATORS)):
+        GENERATORS[name]()
     for f in sorted(os.listdir(OUT)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(OUT, f)))

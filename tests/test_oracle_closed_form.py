@@ -241,3 +241,39 @@ def test_absorbed_closed_forms(oracle):
     c2, *_ = oracle.absorbed_decode(q, kv_b, cf.astype(np.float32), 8, NH, QKN, QKR, KVL, VHD)
     c3, *_ = oracle.absorbed_decode(q, kv_b, cache, 8, NH, QKN, QKR, KVL, VHD)
     assert np.array_equal(c2, c3)
+
+
+def test_rmsnorm_closed_form(oracle):
+    # constant x = c with unit weights: ss = n c^2 exactly (small integers), so
+    # y = c * (1 / sqrt(c^2 + eps)) with every fp32 step correctly rounded
+    for c, n, eps in ((2.0, 64, 1e-6), (-3.0, 2048, 1e-5), (0.5, 8, 0.0)):
+        x = np.full(n, c, np.float32)
+        w = synth.bf16_from_f32(np.ones(n, np.float32))
+        ss = np.float32(c * c * n)
+        inv = np.float32(1.0) / np.sqrt(ss / np.float32(n) + np.float32(eps))
+        assert np.array_equal(oracle.rmsnorm(x, w, eps), np.full(n, np.float32(c) * inv))
+    # the weight multiplies last: w = 2^k scales the output exactly
+    rng = np.random.default_rng(3)
+    x = synth.normal_f32(rng, (256,))
+    one = synth.bf16_from_f32(np.ones(256, np.float32))
+    four = synth.bf16_from_f32(np.full(256, 4.0, np.float32))
+    assert np.array_equal(oracle.rmsnorm(x, four, 1e-6), 4.0 * oracle.rmsnorm(x, one, 1e-6))
+    # scale invariance up to eps: rmsnorm(k x) ~ rmsnorm(x)
+    assert max_abs_rel(oracle.rmsnorm(8.0 * x, one, 0.0), oracle.rmsnorm(x, one, 0.0)) < 1e-6
+
+
+def test_argmax_tie_and_nan_rules(oracle):
+    rng = np.random.default_rng(4)
+    v = synth.normal_f32(rng, (513,))
+    assert oracle.argmax(v) == int(np.argmax(v))              # first maximum
+    assert oracle.argmax(np.arange(10, dtype=np.float32)) == 9
+    t = np.zeros(9, np.float32)
+    t[[2, 6]] = 5.0
+    assert oracle.argmax(t) == 2                               # lowest index on a tie
+    n = v.copy()
+    n[0] = np.nan
+    assert oracle.argmax(n) == 0                               # NaN at 0 is never beaten
+    m = v.copy()
+    m[int(np.argmax(v))] = np.nan
+    assert oracle.argmax(m) == int(np.nanargmax(m))            # other NaNs never win
+    assert oracle.argmax(np.full(5, -np.inf, np.float32)) == 0

@@ -135,3 +135,36 @@ def test_ffn_vs_reference_random(oracle, seed):
         assert np.array_equal(out[t].view(np.uint32), ro.view(np.uint32))
         assert np.array_equal(wt[t].view(np.uint32), rw.view(np.uint32))
         assert np.array_equal(probs[t].view(np.uint32), rp.view(np.uint32))
+
+
+def test_rmsnorm_golden(oracle):
+    g = load_golden("lm_head.npz")
+    for name in ("small", "hidden", "glm", "tiny"):
+        y = oracle.rmsnorm(g[f"rms_{name}_x"], g[f"rms_{name}_w"], float(g[f"rms_{name}_eps"]))
+        assert np.array_equal(y.view(np.uint32), g[f"rms_{name}_y"].view(np.uint32)), name
+
+
+def test_argmax_golden(oracle):
+    g = load_golden("lm_head.npz")
+    for name in ("random", "tie", "nan0", "nanmid", "ninf", "pinf"):
+        assert oracle.argmax(g[f"sample_{name}_in"]) == int(g[f"sample_{name}_out"]), name
+
+
+def test_lm_head_golden(oracle):
+    g = load_golden("lm_head.npz")
+    logits, tokens = oracle.lm_head_rows(g["lm_x"], g["lm_norm"], float(g["lm_eps"]), g["lm_w"])
+    assert np.array_equal(logits.view(np.uint32), g["lm_logits"].view(np.uint32))
+    assert np.array_equal(tokens, g["lm_tokens"])
+
+
+@needs_ref
+def test_rmsnorm_argmax_vs_reference_random(oracle):
+    rng = np.random.default_rng(17)
+    for n, eps, scale in ((1, 1e-6, 1.0), (100, 1e-5, 7.0), (2048, 1e-6, 0.01)):
+        x = synth.normal_f32(rng, (n,), scale)
+        w = synth.normal_bf16(rng, (n,), 1.0)
+        a, b = oracle.rmsnorm(x, w, eps), oracle.ref_rmsnorm(x, w, eps)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for n in (1, 2, 1000, 102400):
+        lg = synth.normal_f32(rng, (n,))
+        assert oracle.argmax(lg) == oracle.ref_sample(lg)
