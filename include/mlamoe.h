@@ -189,7 +189,9 @@ MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, i
 /* matmul (src/run.c:29-37) over T rows: y[t, d] = sum_i x[t, i] * W[d, i],
  * W bf16 row-major [d_out, n_in] (nn.Linear layout), x/y fp32.  Without
  * MM_MATMUL_X_BF16 the fp32 x is carried as a bf16 hi/lo pair (two MFMAs),
- * tracking the fp32 reference to ~1e-5.  n_in % 8 == 0.  Device pointers,
+ * tracking the fp32 reference to ~1e-5.  Up to 4 rows with n_in <= 2048 take
+ * a GEMV that reads each weight row once with x in fp32 registers (the decode
+ * step's o_proj, src/run.c:463-464).  n_in % 8 == 0.  Device pointers,
  * asynchronous. */
 MM_API int mm_matmul_bf16_dev(mm_ctx *ctx, float *y, const float *x, const uint16_t *w,
                               int d_out, int n_in, int T, unsigned flags);
@@ -253,6 +255,67 @@ MM_API int mm_mla_absorbed_decode_dev(mm_ctx *ctx, int layer, int B, const float
                                       const uint16_t *cache, int seq_stride,
                                       const int32_t *kv_lens, int kv_len, float *ctx_out,
                                       float *qabs, float *probs, float *clat);
+
+/* ---- MLA decode front: projections, RoPE, latent-cache append -------------- */
+
+/* The RoPE inverse-frequency table of build_rope_inv_freq
+ * (src/model_load.c:299-325): inv_freq[j], j < rope_dim / 2, blends the
+ * extrapolated 1 / theta^(2j / rope_dim) with the interpolated (that /
+ * factor) over the YaRN correction range of beta_fast / beta_slow at
+ * orig_max positions; factor 1 is plain RoPE.  The reference reads the
+ * parameters from config.json's rope_theta / rope_scaling
+ * (src/model_load.c:271-279).  Host computation, fp32, the reference's steps. */
+MM_API int mm_rope_inv_freq(int rope_dim, float theta, float factor, float beta_fast,
+                            float beta_slow, float orig_max, float *inv_freq);
+
+/* The Config fields of the decode front beyond mm_mla_config
+ * (include/model.h:12-42). */
+typedef struct {
+    int hidden_size;            /* H */
+    int q_lora_rank;            /* 0: q_proj (DeepSeek-V2-Lite); > 0: q_a_proj ->
+                                   q_a_layernorm -> q_b_proj (GLM) */
+    float rms_eps;              /* input_layernorm */
+    float mla_norm_eps;         /* q_a / kv_a layernorms (1e-6, src/model_load.c:269) */
+    int rope_interleaved;       /* 0: rotate adjacent pairs in place (dsv2); 1: rotated
+                                   evens then rotated odds (glm) -- src/run.c:40-67 */
+    const float *rope_inv_freq; /* host [qk_rope_head_dim / 2]: the engine's
+                                   t->rope_inv_freq, or mm_rope_inv_freq */
+} mm_mla_front_config;
+
+/* Configure the decode front (after mm_mla_init); copies the RoPE table to
+ * the device.  hidden_size and q_lora_rank must be multiples of 8. */
+MM_API int mm_mla_front_init(mm_ctx *ctx, const mm_mla_front_config *cfg);
+
+/* One layer's front weights, device pointers, bf16 row-major [out, in]
+ * (ModelWeights, include/model.h:44-96). */
+typedef struct {
+    const uint16_t *input_norm; /* [H] input_layernorm */
+    const uint16_t *q_proj;     /* [NH*(QKN+QKR), H]        q_lora_rank == 0 */
+    const uint16_t *q_a_proj;   /* [q_lora_rank, H]         q_lora_rank > 0 */
+    const uint16_t *q_a_norm;   /* [q_lora_rank]            q_a_layernorm */
+    const uint16_t *q_b_proj;   /* [NH*(QKN+QKR), q_lora_rank] */
+    const uint16_t *kv_a_proj;  /* [KVL+QKR, H] */
+    const uint16_t *kv_a_norm;  /* [KVL] kv_a_layernorm */
+} mm_mla_front_weights;
+
+/* The decode step's attention front for B tokens, token b of sequence b at
+ * position pos[b] (forward_absorbed, src/run.c:418-428, and its GPU form,
+ * src/getp_run.hip:494-520):
+ *   xb = rmsnorm(x[b], input_norm, rms_eps)
+ *   q[b] = project_q(xb) (run.c:73-83), RoPE on each head's q_pe slice
+ *   comp = kv_a_proj . xb
+ *   cache[b, pos[b]] = rmsnorm(comp[:KVL], kv_a_norm, mla_norm_eps) | RoPE(comp[KVL:])
+ * x [B, H] fp32; q [B, NH*(QKN+QKR)] fp32 out (the input of
+ * mm_mla_absorbed_decode_dev); cache the [B, seq_stride, KVL+QKR] bf16 latent
+ * cache of mm_mla_absorbed_decode_dev (round to nearest even; the reference
+ * keeps fp32, include/model.h:117); kv_rows [B, KVL+QKR] fp32 copy of the
+ * appended rows, or NULL.  A pos[b] outside [0, seq_stride) writes no cache
+ * row.  Up to 4 tokens with H <= 2048 take fused GEMVs (norm in registers,
+ * q and kv_a projections in one pass); more take the MFMA GEMM.  Device
+ * pointers, asynchronous. */
+MM_API int mm_mla_front_dev(mm_ctx *ctx, int B, const float *x, const mm_mla_front_weights *w,
+                            const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
+                            float *kv_rows);
 
 #ifdef __cplusplus
 }

@@ -52,4 +52,11 @@ mm_co_gemm_i8:
 mm_co_lm_head:
     .incbin "lm_head.hsaco"
 
+    .balign 4096
+    .globl mm_co_gemv
+    .hidden mm_co_gemv
+    .type mm_co_gemv, @object
+mm_co_gemv:
+    .incbin "gemv.hsaco"
+
     .section .note.GNU-stack, "", @progbits

@@ -21,13 +21,14 @@ extern const unsigned char mm_co_mla[];
 extern const unsigned char mm_co_gemm_bf16[];
 extern const unsigned char mm_co_gemm_i8[];
 extern const unsigned char mm_co_lm_head[];
+extern const unsigned char mm_co_gemv[];
 
 enum { MOD_MOE_BF16, MOD_UTIL, MOD_MOE_I8, MOD_MLA, MOD_GEMM_BF16, MOD_GEMM_I8, MOD_LM_HEAD,
-       MOD_COUNT };
+       MOD_GEMV, MOD_COUNT };
 static const unsigned char *const mod_blob[MOD_COUNT] = {mm_co_moe_bf16, mm_co_util,
                                                           mm_co_moe_i8, mm_co_mla,
                                                           mm_co_gemm_bf16, mm_co_gemm_i8,
-                                                          mm_co_lm_head};
+                                                          mm_co_lm_head, mm_co_gemv};
 
 static const struct {
     const char *name;
@@ -54,9 +55,15 @@ static const struct {
     [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
     [K_CVT_BF16] = {"mm_cvt_bf16", MOD_GEMM_BF16},
     [K_RMSNORM] = {"mm_rmsnorm", MOD_LM_HEAD},
-    [K_LM_GEMV] = {"mm_lm_gemv", MOD_LM_HEAD},
+    [K_LM_GEMV1] = {"mm_lm_gemv_1", MOD_LM_HEAD},
+    [K_LM_GEMV2] = {"mm_lm_gemv_2", MOD_LM_HEAD},
+    [K_LM_GEMV4] = {"mm_lm_gemv_4", MOD_LM_HEAD},
     [K_ARGMAX_PART] = {"mm_argmax_part", MOD_LM_HEAD},
     [K_ARGMAX_FINAL] = {"mm_argmax_final", MOD_LM_HEAD},
+    [K_GEMV1] = {"mm_gemv_1", MOD_GEMV},
+    [K_GEMV2] = {"mm_gemv_2", MOD_GEMV},
+    [K_GEMV4] = {"mm_gemv_4", MOD_GEMV},
+    [K_MLA_ROPE] = {"mm_mla_rope", MOD_MLA},
 };
 
 /* ---- errors ------------------------------------------------------------- */

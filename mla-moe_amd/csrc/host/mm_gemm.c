@@ -40,6 +40,19 @@ int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int 
     return mm_launch(c, K_GEMM_BF16, (unsigned)(8 * ((nbx + 7) / 8) * nby), 1, 1, 256, lds, &a);
 }
 
+unsigned mm_gemv_blocks(int rows) {
+    /* 4 waves per block, GV_RPW (4) rows per wave per turn: one turn covers
+     * every row when the grid allows */
+    const unsigned b = (unsigned)((rows + 15) / 16);
+    return b < 2048 ? b : 2048;
+}
+
+int mm_gemv_launch(mm_ctx *c, const mm_gemv_args *a) {
+    mm_gemv_args k = *a;
+    const mm_kernel_id id = a->B <= 1 ? K_GEMV1 : a->B <= 2 ? K_GEMV2 : K_GEMV4;
+    return mm_launch(c, id, mm_gemv_blocks(a->rows0 + a->rows1), 1, 1, 256, 0, &k);
+}
+
 int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out,
                        int n_in, int T, unsigned flags) {
     if (!c || (T > 0 && (!y || !x || !w)))
@@ -53,6 +66,11 @@ int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, i
     if (T == 0) return MM_OK;
     int st = mm_set_device(c);
     if (st) return st;
+    if (T <= MM_GEMV_NB && n_in <= MM_LM_HMAX) {
+        mm_gemv_args a = {x, NULL, 0.0f, w, NULL, y, NULL, d_out, 0, d_out, 0, T, n_in,
+                          (flags & MM_MATMUL_ACCUMULATE) != 0, (flags & MM_MATMUL_X_BF16) != 0};
+        return mm_gemv_launch(c, &a);
+    }
     char *ws;
     if ((st = mm_workspace(c, mm_gemm_bf16_ws_bytes(T, n_in, flags), (void **)&ws))) return st;
     return mm_gemm_bf16_ws(c, y, x, w, d_out, n_in, T, flags, ws);

@@ -32,9 +32,15 @@ typedef enum {
     K_GEMM_BF16,
     K_CVT_BF16,
     K_RMSNORM,
-    K_LM_GEMV,
+    K_LM_GEMV1,
+    K_LM_GEMV2,
+    K_LM_GEMV4,
     K_ARGMAX_PART,
     K_ARGMAX_FINAL,
+    K_GEMV1,
+    K_GEMV2,
+    K_GEMV4,
+    K_MLA_ROPE,
     K_COUNT
 } mm_kernel_id;
 
@@ -81,6 +87,9 @@ struct mm_ctx {
     mm_mla_config mla;
     int mla_layers;
     uint16_t **mla_kvb;         /* [layers] device kv_b_proj weights */
+    int front_ready;
+    mm_mla_front_config front;  /* rope_inv_freq points at front_inv (device) */
+    float *front_inv;           /* [qk_rope_head_dim / 2] device RoPE table */
 
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
 
@@ -111,6 +120,11 @@ int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
 size_t mm_gemm_bf16_ws_bytes(int T, int n_in, unsigned flags);
 int mm_gemm_bf16_ws(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
                     int T, unsigned flags, char *ws);
+
+/* GEMV over up to MM_GEMV_NB tokens (hidden <= GV_HMAX): the launch shape
+ * for `rows` output rows in total. */
+unsigned mm_gemv_blocks(int rows);
+int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

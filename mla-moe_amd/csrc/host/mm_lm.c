@@ -71,7 +71,8 @@ int mm_lm_head_dev(mm_ctx *c, int B, const float *x, const uint16_t *norm, float
         float *pv = (float *)(ws + o_am);
         int32_t *pi = (int32_t *)(ws + o_am + al256((size_t)B * nb * 4));
         mm_lm_gemv_args ga = {x, norm, eps, lm_head, lg, pv, pi, B, vocab, hidden};
-        if ((st = mm_launch(c, K_LM_GEMV, (unsigned)nb, 1, 1, 256, 0, &ga))) return st;
+        const mm_kernel_id id = B <= 1 ? K_LM_GEMV1 : B <= 2 ? K_LM_GEMV2 : K_LM_GEMV4;
+        if ((st = mm_launch(c, id, (unsigned)nb, 1, 1, 256, 0, &ga))) return st;
         mm_argmax_args fa = {lg, tokens, pv, pi, vocab, B, (int)nb};
         return mm_launch(c, K_ARGMAX_FINAL, (unsigned)B, 1, 1, 256, 0, &fa);
     }

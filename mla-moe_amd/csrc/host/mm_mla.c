@@ -4,12 +4,16 @@
  * for B sequences at once.  kv_b is the reference's kv_b_proj weight,
  * head-interleaved [W_UK_h | W_UV_h] per head (src/model_load.c:80-86).
  */
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
 #include "mm_internal.h"
 
 void mm_mla_release(mm_ctx *c) {
+    if (c->front_inv) hipFree(c->front_inv);
+    c->front_inv = NULL;
+    c->front_ready = 0;
     if (!c->mla_kvb) return;
     for (int l = 0; l < c->mla_layers; l++)
         if (c->mla_kvb[l]) hipFree(c->mla_kvb[l]);
@@ -113,4 +117,127 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
     if ((st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, 1, 256, 0, &ca))) return st;
     return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,
                      (unsigned)((B + 31) / 32), 256, 0, &ca);
+}
+
+/* ---- decode front ---------------------------------------------------------- */
+
+/* build_rope_inv_freq (src/model_load.c:299-325), step for step in fp32. */
+int mm_rope_inv_freq(int rope_dim, float theta, float factor, float beta_fast, float beta_slow,
+                     float orig_max, float *inv) {
+    if (!inv) return mm_fail(MM_ERR_INVALID, "mm_rope_inv_freq: NULL argument");
+    if (rope_dim <= 0 || rope_dim % 2 || !(theta > 1.0f) || !(factor > 0.0f) ||
+        !(beta_fast > 0.0f) || !(beta_slow > 0.0f) || !(orig_max > 0.0f))
+        return mm_fail(MM_ERR_INVALID, "mm_rope_inv_freq: bad parameter");
+    const float pi = 3.14159265358979323846f;
+    const float lo_d = ((float)rope_dim * logf(orig_max / (beta_fast * 2.0f * pi))) /
+                       (2.0f * logf(theta));
+    const float hi_d = ((float)rope_dim * logf(orig_max / (beta_slow * 2.0f * pi))) /
+                       (2.0f * logf(theta));
+    float low = floorf(lo_d), high = ceilf(hi_d);
+    if (low < 0) low = 0;
+    if (high > rope_dim - 1) high = (float)(rope_dim - 1);
+    const float span = high == low ? 0.001f : high - low;
+    for (int j = 0; j < rope_dim / 2; j++) {
+        const float f_ex = 1.0f / powf(theta, (float)(2 * j) / (float)rope_dim);
+        const float f_in = f_ex / factor;
+        float t = ((float)j - low) / span;
+        if (t < 0) t = 0;
+        if (t > 1) t = 1;
+        const float m = 1.0f - t;
+        inv[j] = f_in * (1.0f - m) + f_ex * m;
+    }
+    return MM_OK;
+}
+
+int mm_mla_front_init(mm_ctx *c, const mm_mla_front_config *cfg) {
+    if (!c || !cfg || !cfg->rope_inv_freq) return mm_fail(MM_ERR_INVALID, "mm_mla_front_init: NULL argument");
+    if (!c->mla_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_init: call mm_mla_init first");
+    if (c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_init: already initialised");
+    if (cfg->hidden_size <= 0 || cfg->hidden_size % 8 || cfg->q_lora_rank < 0 || cfg->q_lora_rank % 8)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_front_init: hidden_size and q_lora_rank must be "
+                       "multiples of 8");
+    if (cfg->rope_interleaved != 0 && cfg->rope_interleaved != 1)
+        return mm_fail(MM_ERR_INVALID, "mm_mla_front_init: rope_interleaved must be 0 or 1");
+    const mm_mla_config *g = &c->mla;
+    if (g->n_heads * g->qk_rope_head_dim / 2 > MM_ROPE_PAIRS_MAX)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_front_init: n_heads * qk_rope_head_dim / 2 > %d",
+                       MM_ROPE_PAIRS_MAX);
+    int st = mm_set_device(c);
+    if (st) return st;
+    const size_t nb = (size_t)g->qk_rope_head_dim / 2 * sizeof(float);
+    MM_HIP(hipMalloc((void **)&c->front_inv, nb));
+    MM_HIP(hipMemcpy(c->front_inv, cfg->rope_inv_freq, nb, hipMemcpyHostToDevice));
+    c->front = *cfg;
+    c->front.rope_inv_freq = c->front_inv;
+    c->front_ready = 1;
+    return MM_OK;
+}
+
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
+                     const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
+                     float *kv_rows) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL context");
+    if (!c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_dev: call mm_mla_front_init first");
+    if (B < 0) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: B < 0");
+    if (B == 0) return MM_OK;
+    const mm_mla_front_config *f = &c->front;
+    const int ql = f->q_lora_rank;
+    if (!x || !w || !pos || !q || !cache || !w->input_norm || !w->kv_a_proj || !w->kv_a_norm ||
+        (ql ? (!w->q_a_proj || !w->q_a_norm || !w->q_b_proj) : !w->q_proj))
+        return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL argument");
+    if (seq_stride < 1) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: seq_stride < 1");
+    const void *al[] = {x, w->input_norm, w->q_proj, w->q_a_proj, w->q_a_norm, w->q_b_proj,
+                        w->kv_a_proj, w->kv_a_norm, cache};
+    for (size_t i = 0; i < sizeof(al) / sizeof(al[0]); i++)
+        if ((uintptr_t)al[i] % 16)
+            return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: x, weights and cache must be "
+                           "16-byte aligned");
+    int st = mm_set_device(c);
+    if (st) return st;
+    const mm_mla_config *g = &c->mla;
+    const int H = f->hidden_size, NH = g->n_heads;
+    const int QD = NH * (g->qk_nope_head_dim + g->qk_rope_head_dim);
+    const int KVD = g->kv_lora_rank + g->qk_rope_head_dim;
+    const int gemv = B <= MM_GEMV_NB && H <= MM_LM_HMAX && ql <= MM_LM_HMAX;
+    /* workspace: comp [B, KVD], q_a [B, q_lora]; the GEMM path adds xb [B, H]
+     * and the GEMM staging */
+    const size_t o_cp = 0, o_qa = al256((size_t)B * KVD * 4);
+    const size_t o_xb = o_qa + al256((size_t)B * ql * 4);
+    size_t gw = mm_gemm_bf16_ws_bytes(B, H, 0);
+    if (ql && mm_gemm_bf16_ws_bytes(B, ql, 0) > gw) gw = mm_gemm_bf16_ws_bytes(B, ql, 0);
+    const size_t o_gm = o_xb + (gemv ? 0 : al256((size_t)B * H * 4));
+    char *ws;
+    if ((st = mm_workspace(c, o_gm + (gemv ? 0 : gw), (void **)&ws))) return st;
+    float *comp = (float *)(ws + o_cp), *qa = (float *)(ws + o_qa);
+    if (gemv) {
+        /* input norm fused; the query projection (or q_a) and kv_a in one row space */
+        mm_gemv_args a = {x, w->input_norm, f->rms_eps, ql ? w->q_a_proj : w->q_proj, w->kv_a_proj,
+                          ql ? qa : q, comp, ql ? ql : QD, KVD, ql ? ql : QD, KVD, B, H, 0, 0};
+        if ((st = mm_gemv_launch(c, &a))) return st;
+        if (ql) {
+            mm_gemv_args b = {qa, w->q_a_norm, f->mla_norm_eps, w->q_b_proj, NULL, q, NULL,
+                              QD, 0, QD, 0, B, ql, 0, 0};
+            if ((st = mm_gemv_launch(c, &b))) return st;
+        }
+    } else {
+        float *xb = (float *)(ws + o_xb);
+        char *gws = ws + o_gm;
+        mm_rmsnorm_args ra = {x, w->input_norm, xb, H, f->rms_eps};
+        if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+        if (ql) {
+            if ((st = mm_gemm_bf16_ws(c, qa, xb, w->q_a_proj, ql, H, B, 0, gws))) return st;
+            mm_rmsnorm_args qn = {qa, w->q_a_norm, qa, ql, f->mla_norm_eps};
+            if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &qn))) return st;
+            if ((st = mm_gemm_bf16_ws(c, q, qa, w->q_b_proj, QD, ql, B, 0, gws))) return st;
+        } else if ((st = mm_gemm_bf16_ws(c, q, xb, w->q_proj, QD, H, B, 0, gws))) {
+            return st;
+        }
+        if ((st = mm_gemm_bf16_ws(c, comp, xb, w->kv_a_proj, KVD, H, B, 0, gws))) return st;
+    }
+    mm_mla_rope_args r = {q, comp, w->kv_a_norm, c->front_inv, pos, cache, kv_rows, B, NH,
+                          g->qk_nope_head_dim, g->qk_rope_head_dim, g->kv_lora_rank, seq_stride,
+                          f->rope_interleaved, f->mla_norm_eps};
+    return mm_launch(c, K_MLA_ROPE, (unsigned)B, 1, 1, 256, 0, &r);
 }

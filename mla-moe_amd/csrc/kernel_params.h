@@ -316,4 +316,35 @@ typedef struct {
     int n, T, nseg;
 } mm_argmax_args;
 
+/* ---- dense GEMV for a few tokens (decode projections) ----------------------- */
+/* Up to two weight matrices ("segments") over one activation row set: rows
+ * [0, rows0) of the row space are W0's, [rows0, rows0 + rows1) W1's;
+ * y_s[t * ys_s + r] receives token t's output row r of segment s. */
+typedef struct {
+    const float *x;          /* [B, H] */
+    const uint16_t *norm;    /* [H] rmsnorm weight applied to x first, or NULL */
+    float eps;
+    const uint16_t *w0, *w1; /* [rows_s, H] bf16 */
+    float *y0, *y1;
+    int rows0, rows1, ys0, ys1;
+    int B, H;
+    int accumulate;          /* y += x' . W^T */
+    int x_bf16;              /* x' = bf16(x) by truncation (no norm) */
+} mm_gemv_args;
+#define MM_GEMV_NB 4              /* tokens served by the GEMV (more: the MFMA GEMM) */
+
+/* ---- MLA decode front: RoPE, kv norm, latent-cache append -------------------- */
+#define MM_ROPE_PAIRS_MAX 2048    /* q_pe pairs per token (NH * QKR / 2) */
+typedef struct {
+    float *q;                /* [B, NH * (QKN + QKR)]: RoPE applied to each q_pe in place */
+    const float *comp;       /* [B, KVL + QKR] kv_a output: c_kv | k_pe before norm/RoPE */
+    const uint16_t *kv_norm; /* [KVL] kv_a_layernorm */
+    const float *inv_freq;   /* [QKR / 2] */
+    const int32_t *pos;      /* [B] positions */
+    uint16_t *cache;         /* [B, seq_stride, KVL + QKR] bf16 latent cache */
+    float *kv_out;           /* [B, KVL + QKR] fp32 copy of the appended rows, or NULL */
+    int B, nh, qkn, qkr, kvl, seq_stride, interleaved;
+    float eps;               /* kv_a_layernorm eps */
+} mm_mla_rope_args;
+
 #endif /* MLAMOE_KERNEL_PARAMS_H */

@@ -491,3 +491,99 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_uv(mm_mla_combine_args 
                 a.ctx[((size_t)(b0 + bb) * a.NH + h) * a.VHD + vw + (lane & 15)] = acc[t][i];
         }
 }
+
+/* ---- decode front: RoPE, kv_a_layernorm, latent-cache append ----------------- */
+
+/* One block per token b at position p = pos[b] (src/run.c:420-428):
+ *   q_pe of every head   rope_apply(q_h + QKN, p)                (run.c:420-421)
+ *   c_kv                 rmsnorm(comp[0:KVL], kv_a_layernorm, eps) (run.c:426)
+ *   k_pe                 rope_apply(comp[KVL:KVL+QKR], p)         (run.c:427-428)
+ * The row c_kv | k_pe goes to the bf16 cache at (b, p), rounded to nearest
+ * even (the reference keeps an fp32 cache, include/model.h:117), and, when
+ * kv_out is given, to kv_out in fp32.  A position outside [0, seq_stride)
+ * writes no cache row.  cos / sin of the angle p * inv_freq[j] are evaluated
+ * in fp64 and rounded once, so they are the correctly rounded fp32 values
+ * except for angles within ~2^-29 relative of a rounding boundary; the
+ * rotations are unfused multiply / add, in the reference's order. */
+__device__ __forceinline__ uint16_t bf16_rne_keepnan(float x) {
+    return x != x ? (uint16_t)0x7fc0u : bf16_rne(x);
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_mla_rope(mm_mla_rope_args a) {
+#pragma clang fp contract(off)
+    __shared__ float cs[2][128];
+    __shared__ float red[256 / MM_WAVE];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int half = a.qkr / 2, kvd = a.kvl + a.qkr;
+    const int p = a.pos[b];
+    if (tid < half) {
+        const double ang = (double)((float)p * a.inv_freq[tid]);
+        cs[0][tid] = (float)cos(ang);
+        cs[1][tid] = (float)sin(ang);
+    }
+    const float *comp = a.comp + (size_t)b * kvd;
+    float ss = 0.0f;
+    for (int i = tid; i < a.kvl; i += 256) ss += comp[i] * comp[i];
+    ss = wave_sum(ss);
+    if ((tid & (MM_WAVE - 1)) == 0) red[tid / MM_WAVE] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 256 / MM_WAVE; w++) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)a.kvl + a.eps);
+
+    /* q_pe of every head, in place: all pairs are read before any is written
+     * (the split-half layout moves values across pairs) */
+    const int qhd = a.qkn + a.qkr;
+    float *q = a.q + (size_t)b * a.nh * qhd + a.qkn;
+    const int npairs = a.nh * half;
+    constexpr int QK = MM_ROPE_PAIRS_MAX / 256;
+    float qe[QK], qo[QK];
+#pragma unroll
+    for (int k = 0; k < QK; k++) {
+        const int i = tid + 256 * k;
+        if (i < npairs) {
+            const int h = i / half, j = i - h * half;
+            qe[k] = q[(size_t)h * qhd + 2 * j];
+            qo[k] = q[(size_t)h * qhd + 2 * j + 1];
+        }
+    }
+    if (a.interleaved) __syncthreads();
+#pragma unroll
+    for (int k = 0; k < QK; k++) {
+        const int i = tid + 256 * k;
+        if (i < npairs) {
+            const int h = i / half, j = i - h * half;
+            const float c = cs[0][j], s = cs[1][j];
+            float *v = q + (size_t)h * qhd;
+            if (!a.interleaved) {
+                v[2 * j] = qe[k] * c - qo[k] * s;
+                v[2 * j + 1] = qe[k] * s + qo[k] * c;
+            } else {
+                v[j] = qe[k] * c - qo[k] * s;
+                v[half + j] = qo[k] * c + qe[k] * s;
+            }
+        }
+    }
+
+    /* the cache row */
+    const bool wr = p >= 0 && p < a.seq_stride;
+    uint16_t *dst = a.cache + ((size_t)b * a.seq_stride + (wr ? p : 0)) * kvd;
+    float *ko = a.kv_out ? a.kv_out + (size_t)b * kvd : nullptr;
+    for (int i = 2 * tid; i < a.kvl; i += 512) {
+        const float y0 = comp[i] * inv * bf16_f32(a.kv_norm[i]);
+        const float y1 = comp[i + 1] * inv * bf16_f32(a.kv_norm[i + 1]);
+        if (wr) *(uint32_t *)(dst + i) = (uint32_t)bf16_rne_keepnan(y0) | (uint32_t)bf16_rne_keepnan(y1) << 16;
+        if (ko) { ko[i] = y0; ko[i + 1] = y1; }
+    }
+    for (int j = tid; j < half; j += 256) {
+        const float c = cs[0][j], s = cs[1][j];
+        const float x0 = comp[a.kvl + 2 * j], x1 = comp[a.kvl + 2 * j + 1];
+        const int o0 = a.kvl + (a.interleaved ? j : 2 * j);
+        const int o1 = a.kvl + (a.interleaved ? half + j : 2 * j + 1);
+        const float r0 = x0 * c - x1 * s;
+        const float r1 = a.interleaved ? x1 * c + x0 * s : x0 * s + x1 * c;
+        if (wr) { dst[o0] = bf16_rne_keepnan(r0); dst[o1] = bf16_rne_keepnan(r1); }
+        if (ko) { ko[o0] = r0; ko[o1] = r1; }
+    }
+}

@@ -54,6 +54,22 @@ class MlaConfig(C.Structure):
                 ("v_head_dim", C.c_int), ("softmax_scale", C.c_float)]
 
 
+class MlaFrontConfig(C.Structure):
+    """Mirror of mm_mla_front_config."""
+    _fields_ = [("hidden_size", C.c_int), ("q_lora_rank", C.c_int), ("rms_eps", C.c_float),
+                ("mla_norm_eps", C.c_float), ("rope_interleaved", C.c_int),
+                ("rope_inv_freq", C.POINTER(C.c_float))]
+
+
+FRONT_WEIGHTS = ("input_norm", "q_proj", "q_a_proj", "q_a_norm", "q_b_proj", "kv_a_proj",
+                 "kv_a_norm")
+
+
+class MlaFrontWeights(C.Structure):
+    """Mirror of mm_mla_front_weights (device pointers)."""
+    _fields_ = [(n, _vp) for n in FRONT_WEIGHTS]
+
+
 class MoeI8Debug(C.Structure):
     _fields_ = [(n, _vp) for n in ("qx", "sx", "acc_gu", "h", "qh", "sh", "acc_d", "y", "hs",
                                    "qhs", "shs", "ys")]
@@ -111,8 +127,21 @@ def lib():
         L.mm_argmax_dev.argtypes = [_vp, C.c_int, _vp, C.c_int, _vp]
         L.mm_lm_head_dev.argtypes = [_vp, C.c_int, _vp, _vp, C.c_float, _vp, C.c_int, C.c_int,
                                      _vp, _vp]
+        L.mm_rope_inv_freq.argtypes = [C.c_int] + [C.c_float] * 5 + [C.POINTER(C.c_float)]
+        L.mm_mla_front_init.argtypes = [_vp, C.POINTER(MlaFrontConfig)]
+        L.mm_mla_front_dev.argtypes = [_vp, C.c_int, _vp, C.POINTER(MlaFrontWeights), _vp, _vp,
+                                       _vp, C.c_int, _vp]
         _lib = L
     return _lib
+
+
+def rope_inv_freq(dim, theta, factor=1.0, beta_fast=32.0, beta_slow=1.0, orig_max=4096.0):
+    """The RoPE inverse-frequency table (build_rope_inv_freq,
+    src/model_load.c:299-325) from the library's host code."""
+    inv = np.empty(dim // 2, np.float32)
+    _check(lib().mm_rope_inv_freq(dim, theta, factor, beta_fast, beta_slow, orig_max,
+                                  inv.ctypes.data_as(C.POINTER(C.c_float))))
+    return inv
 
 
 def _check(st):
@@ -441,6 +470,48 @@ class Context:
         for b in bufs.values():
             b.free()
             self._bufs.remove(b)
+        return out
+
+    # MLA decode front -----------------------------------------------------------
+    def mla_front_init(self, H, inv_freq, q_lora=0, rms_eps=1e-6, mla_eps=1e-6, interleaved=0):
+        inv = np.ascontiguousarray(inv_freq, np.float32)
+        cfg = MlaFrontConfig(H, q_lora, rms_eps, mla_eps, interleaved,
+                             inv.ctypes.data_as(C.POINTER(C.c_float)))
+        _check(lib().mm_mla_front_init(self.h, C.byref(cfg)))
+        self._front_cfg = (H, q_lora)
+
+    def front_weights(self, w):
+        """Upload a dict of host weights (FRONT_WEIGHTS names, or in_norm /
+        kv_a for input_norm / kv_a_proj; None or absent for unused ones) and
+        return (struct, buffers)."""
+        alias = dict(input_norm="in_norm", kv_a_proj="kv_a")   # synth.attn_layer's names
+        get = lambda k: w.get(k) if w.get(k) is not None else w.get(alias.get(k))  # noqa: E731
+        bufs = {k: self.to_device(np.ascontiguousarray(get(k), np.uint16))
+                for k in FRONT_WEIGHTS if get(k) is not None}
+        return MlaFrontWeights(*[bufs[k].ptr if k in bufs else None for k in FRONT_WEIGHTS]), bufs
+
+    def mla_front_dev(self, B, x, wstruct, pos, q, cache, seq_stride, kv_rows=None):
+        _check(lib().mm_mla_front_dev(self.h, B, x.ptr, C.byref(wstruct), pos.ptr, q.ptr,
+                                      cache.ptr, seq_stride,
+                                      kv_rows.ptr if kv_rows is not None else None))
+
+    def mla_front(self, x, w, pos, cache):
+        """Host arrays: x [B, H] fp32, w a dict of bf16 weights, pos [B],
+        cache [B, L, KVL+QKR] bf16 (uint16).  Returns (q [B, NH*(QKN+QKR)],
+        kv_rows [B, KVL+QKR] fp32, the cache after the append)."""
+        m = self._mla_cfg
+        x = np.ascontiguousarray(x, np.float32)
+        cache = np.ascontiguousarray(cache, np.uint16)
+        B, L = cache.shape[0], cache.shape[1]
+        QD = m.n_heads * (m.qk_nope_head_dim + m.qk_rope_head_dim)
+        KVD = m.kv_lora_rank + m.qk_rope_head_dim
+        ws, wb = self.front_weights(w)
+        dx, dp, dc = self.to_device(x), self.to_device(np.ascontiguousarray(pos, np.int32)), \
+            self.to_device(cache)
+        dq, dk = self.empty((B, QD), np.float32), self.empty((B, KVD), np.float32)
+        self.mla_front_dev(B, dx, ws, dp, dq, dc, L, dk)
+        out = dq.download(), dk.download(), dc.download()
+        self._tmp((dx, dp, dc, dq, dk, *wb.values()))
         return out
 
     def ffn_compute(self, layer, xn, flags=MM_FWD_BF16):

@@ -56,6 +56,32 @@ def moe_layer(seed: int, H: int, E: int, I: int, n_shared: int, std: float = 0.0
     return w
 
 
+def attn_layer(seed: int, H: int, NH: int, QKN: int, QKR: int, KVL: int, VHD: int,
+               q_lora: int = 0, std: float = 0.02) -> dict:
+    """One MLA layer's bf16 weights (nn.Linear layout [out, in]): the
+    input_layernorm, q_proj [NH*(QKN+QKR), H] (or, with q_lora > 0, q_a_proj
+    [q_lora, H], q_a_layernorm and q_b_proj [NH*(QKN+QKR), q_lora]),
+    kv_a_proj [KVL+QKR, H], kv_a_layernorm, the head-interleaved kv_b
+    [NH*(QKN+VHD), KVL] and o_proj [H, NH*VHD].  Norm weights are
+    1 + N(0, 0.1) so that a dropped norm multiply shows."""
+    rng = np.random.default_rng(seed)
+    QD = NH * (QKN + QKR)
+
+    def norm(n):
+        return bf16_from_f32(1.0 + normal_f32(rng, (n,), 0.1))
+
+    w = dict(in_norm=norm(H), q_proj=None, q_a_proj=None, q_a_norm=None, q_b_proj=None)
+    if q_lora > 0:
+        w.update(q_a_proj=normal_bf16(rng, (q_lora, H), std), q_a_norm=norm(q_lora),
+                 q_b_proj=normal_bf16(rng, (QD, q_lora), std))
+    else:
+        w["q_proj"] = normal_bf16(rng, (QD, H), std)
+    w.update(kv_a=normal_bf16(rng, (KVL + QKR, H), std), kv_a_norm=norm(KVL),
+             kv_b=normal_bf16(rng, (NH * (QKN + VHD), KVL), std),
+             o_proj=normal_bf16(rng, (H, NH * VHD), std))
+    return w
+
+
 def activations(seed: int, T: int, H: int) -> np.ndarray:
     return normal_f32(np.random.default_rng(seed), (T, H))
 

@@ -401,3 +401,74 @@ void or_absorbed_decode(const float *q, const uint16_t *kv_b, const void *cache,
     }
     free(cf); free(qa); free(sc); free(cl);
 }
+
+/* ---- MLA decode front -------------------------------------------------- */
+
+/* src/model_load.c:299-325, step for step (float arithmetic throughout,
+ * left-to-right products as written there). */
+void or_rope_inv_freq(int dim, float theta, float factor, float beta_fast, float beta_slow,
+                      float orig_max, float *inv) {
+    const int half = dim / 2;
+    const float pi = 3.14159265358979323846f;
+    const float lo_d = ((float)dim * logf(orig_max / (beta_fast * 2.0f * pi))) / (2.0f * logf(theta));
+    const float hi_d = ((float)dim * logf(orig_max / (beta_slow * 2.0f * pi))) / (2.0f * logf(theta));
+    float low = floorf(lo_d), high = ceilf(hi_d);
+    if (low < 0) low = 0;
+    if (high > dim - 1) high = (float)(dim - 1);
+    const float denom = high == low ? 0.001f : high - low;
+    for (int j = 0; j < half; j++) {
+        const float extra = 1.0f / powf(theta, (float)(2 * j) / (float)dim);
+        const float inter = extra / factor;
+        float ramp = ((float)j - low) / denom;
+        ramp = ramp < 0 ? 0 : ramp > 1 ? 1 : ramp;
+        const float keep = 1.0f - ramp;
+        inv[j] = inter * (1.0f - keep) + extra * keep;
+    }
+}
+
+/* src/run.c:47-67 */
+void or_rope_apply(float *v, int pos, const float *inv, int dim, int interleaved) {
+    const int half = dim / 2;
+    float tmp[512];
+    for (int j = 0; j < half; j++) {
+        const float ang = (float)pos * inv[j];
+        const float c = cosf(ang), s = sinf(ang);
+        const float a = v[2 * j], b = v[2 * j + 1];
+        if (interleaved) {
+            tmp[j] = a * c - b * s;
+            tmp[half + j] = b * c + a * s;
+        } else {
+            v[2 * j] = a * c - b * s;
+            v[2 * j + 1] = a * s + b * c;
+        }
+    }
+    if (interleaved) memcpy(v, tmp, (size_t)dim * sizeof(float));
+}
+
+/* src/run.c:418-428 with project_q (run.c:73-83) */
+void or_mla_front(const or_front_cfg *c, const or_front_weights *w, const float *inv,
+                  const float *x, int pos, float *q, float *kv, float *comp) {
+    const int H = c->hidden, QHD = c->qk_nope + c->qk_rope, QD = c->n_heads * QHD;
+    const int KVD = c->kv_lora + c->qk_rope;
+    float *xb = malloc((size_t)H * sizeof(float));
+    float *cp = malloc((size_t)KVD * sizeof(float));
+    or_rmsnorm(xb, x, w->in_norm, H, c->rms_eps);
+    if (c->q_lora > 0) {
+        float *qa = malloc((size_t)c->q_lora * sizeof(float));
+        or_matmul(qa, xb, w->q_a_proj, c->q_lora, H);
+        or_rmsnorm(qa, qa, w->q_a_norm, c->q_lora, c->mla_eps);
+        or_matmul(q, qa, w->q_b_proj, QD, c->q_lora);
+        free(qa);
+    } else {
+        or_matmul(q, xb, w->q_proj, QD, H);
+    }
+    for (int h = 0; h < c->n_heads; h++)
+        or_rope_apply(q + (size_t)h * QHD + c->qk_nope, pos, inv, c->qk_rope, c->interleaved);
+    or_matmul(cp, xb, w->kv_a, KVD, H);
+    if (comp) memcpy(comp, cp, (size_t)KVD * sizeof(float));
+    or_rmsnorm(kv, cp, w->kv_a_norm, c->kv_lora, c->mla_eps);
+    memcpy(kv + c->kv_lora, cp + c->kv_lora, (size_t)c->qk_rope * sizeof(float));
+    or_rope_apply(kv + c->kv_lora, pos, inv, c->qk_rope, c->interleaved);
+    free(xb);
+    free(cp);
+}

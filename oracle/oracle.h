@@ -163,6 +163,49 @@ void or_absorbed_decode(const float *q, const uint16_t *kv_b, const void *cache,
                         int VHD, int kv_len, int seq_stride, float scale, float *ctx,
                         float *qabs, float *probs, float *clat);
 
+/* ---- MLA decode front: norms, projections, RoPE, latent-cache row ----- */
+/* DeepSeek-V2 YaRN inverse frequencies (src/model_load.c:299-325): inv[j]
+ * for j < dim/2 blends 1/theta^(2j/dim) (extrapolated) and that / factor
+ * (interpolated) by a ramp over the correction range set by beta_fast /
+ * beta_slow and orig_max.  factor == 1 gives plain RoPE. */
+void or_rope_inv_freq(int dim, float theta, float factor, float beta_fast, float beta_slow,
+                      float orig_max, float *inv);
+/* In-place RoPE of a dim-long slice at `pos` (src/run.c:47-67): angle
+ * pos * inv[j]; interleaved == 0 rotates (v[2j], v[2j+1]) in place,
+ * interleaved == 1 writes the rotated evens then the rotated odds. */
+void or_rope_apply(float *v, int pos, const float *inv, int dim, int interleaved);
+
+/* The attention fields of Config the decode front needs. */
+typedef struct {
+    int   hidden;        /* H */
+    int   n_heads;       /* NH */
+    int   qk_nope;       /* QKN */
+    int   qk_rope;       /* QKR */
+    int   kv_lora;       /* KVL */
+    int   q_lora;        /* 0: q_proj; > 0: q_a_proj -> q_a_layernorm -> q_b_proj */
+    float rms_eps;       /* input_layernorm */
+    float mla_eps;       /* q_a / kv_a layernorms (model_load.c:269) */
+    int   interleaved;   /* RoPE layout */
+} or_front_cfg;
+
+typedef struct {
+    const uint16_t *in_norm;     /* [H] */
+    const uint16_t *q_proj;      /* [NH*(QKN+QKR), H]   (q_lora == 0) */
+    const uint16_t *q_a_proj;    /* [q_lora, H]          (q_lora > 0) */
+    const uint16_t *q_a_norm;    /* [q_lora] */
+    const uint16_t *q_b_proj;    /* [NH*(QKN+QKR), q_lora] */
+    const uint16_t *kv_a;        /* [KVL+QKR, H] */
+    const uint16_t *kv_a_norm;   /* [KVL] */
+} or_front_weights;
+
+/* One token of forward_absorbed up to the latent-cache append
+ * (src/run.c:418-428, project_q run.c:73-83): xb = rmsnorm(x); q =
+ * project_q(xb) with RoPE on each head's q_pe; comp = kv_a . xb; kv =
+ * rmsnorm(comp[:KVL], kv_a_norm, mla_eps) | rope(comp[KVL:]).  q is
+ * [NH*(QKN+QKR)], kv [KVL+QKR] (the cache row); comp [KVL+QKR] may be NULL. */
+void or_mla_front(const or_front_cfg *c, const or_front_weights *w, const float *inv,
+                  const float *x, int pos, float *q, float *kv, float *comp);
+
 #ifdef __cplusplus
 }
 #endif

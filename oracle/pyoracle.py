@@ -62,6 +62,17 @@ class I8Debug(C.Structure):
                 ("sh", _f32p), ("acc_d", _i32p), ("qhs", _i8p), ("shs", _f32p)]
 
 
+class FrontCfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_heads", C.c_int), ("qk_nope", C.c_int),
+                ("qk_rope", C.c_int), ("kv_lora", C.c_int), ("q_lora", C.c_int),
+                ("rms_eps", C.c_float), ("mla_eps", C.c_float), ("interleaved", C.c_int)]
+
+
+class FrontWeights(C.Structure):
+    _fields_ = [(n, _u16p) for n in ("in_norm", "q_proj", "q_a_proj", "q_a_norm", "q_b_proj",
+                                     "kv_a", "kv_a_norm")]
+
+
 _lib = None
 _ref = None
 
@@ -107,6 +118,10 @@ def lib():
         L.or_absorbed_decode.argtypes = [_f32p, _u16p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_float, _f32p, _f32p, _f32p, _f32p]
+        L.or_rope_inv_freq.argtypes = [C.c_int] + [C.c_float] * 5 + [_f32p]
+        L.or_rope_apply.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int]
+        L.or_mla_front.argtypes = [C.POINTER(FrontCfg), C.POINTER(FrontWeights), _f32p, _f32p,
+                                   C.c_int, _f32p, _f32p, _f32p]
         _lib = L
     return _lib
 
@@ -134,6 +149,12 @@ def ref():
         R.ref_absorbed_decode.restype = C.c_int
         R.ref_absorbed_decode.argtypes = [C.c_int] * 9 + [C.c_float, _f32p] + [_u16p] * 13 + \
             [_f32p, C.c_char_p, _f32p]
+        R.ref_absorbed_decode_ex.restype = C.c_int
+        R.ref_absorbed_decode_ex.argtypes = [C.c_int] * 9 + [C.c_float, _f32p, C.c_int, C.c_int] + \
+            [_u16p] * 16 + [_f32p, C.c_char_p, _f32p]
+        R.ref_rope_apply.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int]
+        R.ref_config_rope.restype = C.c_int
+        R.ref_config_rope.argtypes = [C.c_char_p, _f32p, _ip, _f32p]
         _ref = R
     return _ref
 
@@ -332,6 +353,51 @@ def absorbed_decode(q, kv_b, cache, kv_len, NH, QKN, QKR, KVL, VHD, scale=None,
     return ctx, qabs, probs, clat
 
 
+def rope_inv_freq(dim, theta, factor=1.0, beta_fast=32.0, beta_slow=1.0, orig_max=4096.0):
+    inv = np.empty(dim // 2, np.float32)
+    lib().or_rope_inv_freq(dim, theta, factor, beta_fast, beta_slow, orig_max, _p(inv, _f32p))
+    return inv
+
+
+def rope_apply(v, pos, inv, interleaved=0):
+    """RoPE of every row of v [..., dim] at `pos` (one position for all rows)."""
+    v = c32(v).copy()
+    inv = c32(inv)
+    dim = v.shape[-1]
+    for row in v.reshape(-1, dim):
+        lib().or_rope_apply(_p(row, _f32p), int(pos), _p(inv, _f32p), dim, int(interleaved))
+    return v
+
+
+def front_cfg(H, NH, QKN, QKR, KVL, q_lora=0, rms_eps=1e-6, mla_eps=1e-6, interleaved=0):
+    return FrontCfg(H, NH, QKN, QKR, KVL, q_lora, rms_eps, mla_eps, interleaved)
+
+
+def _front_struct(w):
+    return FrontWeights(*[_p(w.get(n), _u16p) if w.get(n) is not None else None
+                          for n, _ in FrontWeights._fields_])
+
+
+def mla_front(cfg, w, inv, x, pos):
+    """B tokens of the decode front, token b at position pos[b].  Returns q
+    [B, NH*(QKN+QKR)], kv [B, KVL+QKR] (the fp32 cache rows), comp [B, KVL+QKR]."""
+    x = c32(np.atleast_2d(x))
+    B = x.shape[0]
+    inv = c32(inv)
+    QD = cfg.n_heads * (cfg.qk_nope + cfg.qk_rope)
+    KVD = cfg.kv_lora + cfg.qk_rope
+    q = np.empty((B, QD), np.float32)
+    kv = np.empty((B, KVD), np.float32)
+    comp = np.empty((B, KVD), np.float32)
+    ws = _front_struct({k: np.ascontiguousarray(v, dtype=np.uint16) for k, v in w.items()
+                        if v is not None})
+    pos = np.broadcast_to(np.asarray(pos), (B,))
+    for b in range(B):
+        lib().or_mla_front(C.byref(cfg), C.byref(ws), _p(inv, _f32p), _p(x[b], _f32p),
+                           int(pos[b]), _p(q[b], _f32p), _p(kv[b], _f32p), _p(comp[b], _f32p))
+    return q, kv, comp
+
+
 # ---------------------------------------------------------------------------
 # reference-library helpers (build container only)
 # ---------------------------------------------------------------------------
@@ -382,3 +448,23 @@ def ref_ffn_compute(cfg, w, xn):
                           _p(xn, _f32p), _p(out, _f32p), _p(idx, _ip), _p(wt, _f32p),
                           _p(probs, _f32p))
     return out, idx, wt, probs
+
+
+def ref_rope_apply(v, pos, inv, interleaved=0):
+    v = c32(v).copy()
+    inv = c32(inv)
+    dim = v.shape[-1]
+    for row in v.reshape(-1, dim):
+        ref().ref_rope_apply(_p(row, _f32p), int(pos), _p(inv, _f32p), dim, int(interleaved))
+    return v
+
+
+def ref_config_rope(model_dir):
+    """The reference's config_from_json + build_rope_inv_freq on
+    <model_dir>/config.json.  Returns (inv_freq, ints, floats) as documented
+    in oracle/ref/ref_model.c."""
+    ints = np.zeros(8, np.int32)
+    flts = np.zeros(8, np.float32)
+    inv = np.zeros(512, np.float32)
+    ref().ref_config_rope(model_dir.encode(), _p(inv, _f32p), _p(ints, _ip), _p(flts, _f32p))
+    return inv[:ints[0] // 2].copy(), ints, flts

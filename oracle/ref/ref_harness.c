@@ -102,14 +102,16 @@ void ref_ffn_compute(int H, int E, int n_shared, int K, int I, int router_sigmoi
  * receives the post-RoPE query of every head, computed with the reference's
  * own rmsnorm/project_q/rope_apply exactly as forward_absorbed does
  * (run.c:418-421), because the dumps do not include q. */
-int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int dense_inter,
-                        int vocab, int pos, float rms_eps, const float *inv_freq,
-                        const uint16_t *embed, const uint16_t *in_norm, const uint16_t *q_proj,
-                        const uint16_t *kv_a, const uint16_t *kv_a_norm, const uint16_t *kv_b,
-                        const uint16_t *o_proj, const uint16_t *post_norm,
-                        const uint16_t *dgate, const uint16_t *dup, const uint16_t *ddown,
-                        const uint16_t *final_norm, const uint16_t *lm_head,
-                        const float *cache_in, const char *dump_dir, float *q_out) {
+int ref_absorbed_decode_ex(int NH, int QKN, int QKR, int KVL, int VHD, int H, int dense_inter,
+                           int vocab, int pos, float rms_eps, const float *inv_freq,
+                           int q_lora, int interleaved, const uint16_t *q_a_proj,
+                           const uint16_t *q_a_norm, const uint16_t *q_b_proj,
+                           const uint16_t *embed, const uint16_t *in_norm, const uint16_t *q_proj,
+                           const uint16_t *kv_a, const uint16_t *kv_a_norm, const uint16_t *kv_b,
+                           const uint16_t *o_proj, const uint16_t *post_norm,
+                           const uint16_t *dgate, const uint16_t *dup, const uint16_t *ddown,
+                           const uint16_t *final_norm, const uint16_t *lm_head,
+                           const float *cache_in, const char *dump_dir, float *q_out) {
     const int KVD = KVL + QKR, QHD = QKN + QKR;
     Transformer t;
     memset(&t, 0, sizeof(t));
@@ -118,7 +120,7 @@ int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int d
     c->hidden_size = H;
     c->n_heads = NH;
     c->n_kv_heads = NH;
-    c->q_lora_rank = 0;
+    c->q_lora_rank = q_lora;
     c->first_k_dense = 1;
     c->kv_lora_rank = KVL;
     c->qk_rope_head_dim = QKR;
@@ -130,10 +132,12 @@ int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int d
     c->rms_eps = rms_eps;
     c->mla_norm_eps = 1e-6f;                             /* model_load.c:269 */
     c->softmax_scale = 1.0f / sqrtf((float)(QKN + QKR)); /* model_load.c:270 */
-    c->rope_interleaved = 0;
+    c->rope_interleaved = interleaved;
 
     ModelWeights *w = &t.weights;
-    bf16_t *qp[1] = {(bf16_t *)q_proj}, *nul[1] = {NULL};
+    bf16_t *qp[1] = {(bf16_t *)q_proj};
+    bf16_t *qa[1] = {(bf16_t *)q_a_proj}, *qan[1] = {(bf16_t *)q_a_norm};
+    bf16_t *qb[1] = {(bf16_t *)q_b_proj};
     bf16_t *kva[1] = {(bf16_t *)kv_a}, *kvan[1] = {(bf16_t *)kv_a_norm};
     bf16_t *wuk[1] = {(bf16_t *)kv_b};
     bf16_t *wuv[1] = {(bf16_t *)kv_b + (size_t)QKN * KVL};   /* model_load.c:80-86 */
@@ -142,9 +146,9 @@ int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int d
     bf16_t *dg[1] = {(bf16_t *)dgate}, *du[1] = {(bf16_t *)dup}, *dd[1] = {(bf16_t *)ddown};
     w->embed_tokens = (bf16_t *)embed;
     w->q_proj = qp;
-    w->q_a_proj = nul;
-    w->q_b_proj = nul;
-    w->q_a_layernorm = nul;
+    w->q_a_proj = qa;
+    w->q_b_proj = qb;
+    w->q_a_layernorm = qan;
     w->kv_a_proj = kva;
     w->kv_a_layernorm = kvan;
     w->W_UK = wuk;
@@ -164,6 +168,7 @@ int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int d
     s->hb = malloc((size_t)dense_inter * sizeof(float));
     s->hb2 = malloc((size_t)dense_inter * sizeof(float));
     s->logits = malloc((size_t)vocab * sizeof(float));
+    s->q_a = q_lora > 0 ? malloc((size_t)q_lora * sizeof(float)) : NULL;
     t.rope_inv_freq = (float *)inv_freq;
 
     /* q for token 0 at `pos`, as forward_absorbed computes it (run.c:414-421). */
@@ -181,6 +186,25 @@ int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int d
     forward_absorbed(&t, 0, pos);
     run_set_dump(NULL);
 
-    free(s->kv_cache); free(s->hb); free(s->hb2); free(s->logits);
+    free(s->kv_cache); free(s->hb); free(s->hb2); free(s->logits); free(s->q_a);
     return 0;
+}
+
+/* The dsv2 form: single q_proj, adjacent-pair RoPE. */
+int ref_absorbed_decode(int NH, int QKN, int QKR, int KVL, int VHD, int H, int dense_inter,
+                        int vocab, int pos, float rms_eps, const float *inv_freq,
+                        const uint16_t *embed, const uint16_t *in_norm, const uint16_t *q_proj,
+                        const uint16_t *kv_a, const uint16_t *kv_a_norm, const uint16_t *kv_b,
+                        const uint16_t *o_proj, const uint16_t *post_norm,
+                        const uint16_t *dgate, const uint16_t *dup, const uint16_t *ddown,
+                        const uint16_t *final_norm, const uint16_t *lm_head,
+                        const float *cache_in, const char *dump_dir, float *q_out) {
+    return ref_absorbed_decode_ex(NH, QKN, QKR, KVL, VHD, H, dense_inter, vocab, pos, rms_eps,
+                                  inv_freq, 0, 0, NULL, NULL, NULL, embed, in_norm, q_proj, kv_a,
+                                  kv_a_norm, kv_b, o_proj, post_norm, dgate, dup, ddown,
+                                  final_norm, lm_head, cache_in, dump_dir, q_out);
+}
+
+void ref_rope_apply(float *v, int pos, const float *inv_freq, int rope_dim, int interleaved) {
+    rope_apply(v, pos, inv_freq, rope_dim, interleaved);
 }

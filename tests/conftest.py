@@ -39,3 +39,26 @@ def oracle():
     import pyoracle
     pyoracle.lib()
     return pyoracle
+
+
+def front_case(g, name):
+    """Rebuild one decode-front golden case of mla_front.npz: its dimensions,
+    the weights (synth.attn_layer, checked against the stored checksums) and
+    the earlier latent-cache rows, exactly as tests/golden/make_golden.py
+    drew them."""
+    from mlamoe import synth
+    H, NH, QKN, QKR, KVL, VHD, q_lora, il, pos, seed = (int(v) for v in g[f"{name}_cfg"])
+    w = synth.attn_layer(seed, H, NH, QKN, QKR, KVL, VHD, q_lora)
+    for k, v in w.items():
+        if v is not None:
+            assert synth.checksum_u16(v) == int(g[f"{name}_sum_{k}"]), k
+    r = np.random.default_rng(seed + 1)
+    for shape, std in (((2, H), 1.0), ((4, H), 0.02), ((4, H), 0.02), ((H, 4), 0.02),
+                       ((2, H), 0.02)):
+        synth.normal_bf16(r, shape, std)   # embed, dense FFN and lm_head draws
+    cache_in = synth.normal_bf16(r, (pos, KVL + QKR), 1.0)
+    assert synth.checksum_u16(cache_in) == int(g[f"{name}_sum_cache"])
+    eps = g[f"{name}_eps"]
+    return dict(H=H, NH=NH, QKN=QKN, QKR=QKR, KVL=KVL, VHD=VHD, q_lora=q_lora, il=il, pos=pos,
+                rms_eps=float(eps[0]), mla_eps=float(eps[1]), inv=g[f"{name}_inv"],
+                x=g[f"{name}_x"], w=w, cache_in=cache_in)

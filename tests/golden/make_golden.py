@@ -219,7 +219,113 @@ def gen_lm_head():
     np.savez_compressed(os.path.join(OUT, "lm_head.npz"), **d)
 
 
-GENERATORS = dict(matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),
+# config.json fields the reference's config_from_json reads (model_load.c:242-292)
+_CFG_BASE = dict(num_hidden_layers=1, first_k_dense_replace=1, n_routed_experts=64,
+                 n_shared_experts=2, num_experts_per_tok=6, intermediate_size=10944,
+                 moe_intermediate_size=1408, vocab_size=102400, topk_method="greedy",
+                 norm_topk_prob=False, routed_scaling_factor=1.0)
+ROPE_CONFIGS = {
+    # DeepSeek-V2-Lite's published attention/RoPE fields (YaRN, factor 40)
+    "dsv2": dict(model_type="deepseek_v2", hidden_size=2048, num_attention_heads=16,
+                 q_lora_rank=None, kv_lora_rank=512, qk_nope_head_dim=128, qk_rope_head_dim=64,
+                 v_head_dim=128, max_position_embeddings=163840, rms_norm_eps=1e-6,
+                 rope_theta=10000, rope_scaling=dict(
+                     type="yarn", factor=40, beta_fast=32, beta_slow=1, mscale=0.707,
+                     mscale_all_dim=0.707, original_max_position_embeddings=4096)),
+    # GLM-style: q-LoRA, split-half RoPE, no rope_scaling (plain RoPE)
+    "glm": dict(model_type="glm4_moe_lite", hidden_size=512, num_attention_heads=4,
+                q_lora_rank=96, kv_lora_rank=512, qk_nope_head_dim=64, qk_rope_head_dim=64,
+                v_head_dim=64, max_position_embeddings=202752, rms_norm_eps=1e-5,
+                rope_theta=1000000, rope_scaling=None, topk_method="noaux_tc"),
+    # a second YaRN correction range (low/high inside (0, dim-1), small factor)
+    "yarn2": dict(model_type="deepseek_v2", hidden_size=256, num_attention_heads=2,
+                  kv_lora_rank=512, qk_nope_head_dim=32, qk_rope_head_dim=64, v_head_dim=32,
+                  rms_norm_eps=1e-6, rope_theta=50000, rope_scaling=dict(
+                      type="yarn", factor=4, beta_fast=16, beta_slow=2,
+                      original_max_position_embeddings=2048)),
+}
+
+
+def _ref_config(name):
+    import json
+    with tempfile.TemporaryDirectory() as td:
+        with open(os.path.join(td, "config.json"), "w") as f:
+            json.dump(dict(_CFG_BASE, **ROPE_CONFIGS[name]), f)
+        return O.ref_config_rope(td)
+
+
+def _front_case(name, cfg_name, seed, pos):
+    """One decode token through the reference's forward_absorbed on a
+    one-layer model (ref_absorbed_decode_ex): the post-RoPE q, the latent-cache
+    row the reference appends at `pos`, and attn_out (o_proj . ctx)."""
+    inv, ints, flts = _ref_config(cfg_name)
+    QKR, inter, q_lora, NH, QKN, KVL, VHD, H = (int(v) for v in ints)
+    rms_eps = float(flts[0])
+    KVD, QHD = KVL + QKR, QKN + QKR
+    w = synth.attn_layer(seed, H, NH, QKN, QKR, KVL, VHD, q_lora)
+    r = np.random.default_rng(seed + 1)
+    DI, V = 4, 2
+    embed = synth.normal_bf16(r, (V, H), 1.0)
+    dg = synth.normal_bf16(r, (DI, H), 0.02)
+    du = synth.normal_bf16(r, (DI, H), 0.02)
+    dd = synth.normal_bf16(r, (H, DI), 0.02)
+    one = np.full(H, np.uint16(0x3F80), np.uint16)
+    lm_head = synth.normal_bf16(r, (V, H), 0.02)
+    cache_in = synth.bf16_to_f32(synth.normal_bf16(r, (pos, KVD), 1.0))
+    q = np.empty(NH * QHD, np.float32)
+    u16p, f32p = C.POINTER(C.c_uint16), C.POINTER(C.c_float)
+    z = np.zeros(1, np.uint16)
+
+    def u(a):
+        return _p(z if a is None else a, u16p)
+    with tempfile.TemporaryDirectory() as td:
+        rc = O.ref().ref_absorbed_decode_ex(
+            NH, QKN, QKR, KVL, VHD, H, DI, V, pos, C.c_float(rms_eps), _p(inv, f32p),
+            q_lora, inter, u(w["q_a_proj"]), u(w["q_a_norm"]), u(w["q_b_proj"]),
+            u(embed), u(w["in_norm"]), u(w["q_proj"]), u(w["kv_a"]), u(w["kv_a_norm"]),
+            u(w["kv_b"]), u(w["o_proj"]), u(one), u(dg), u(du), u(dd), u(one), u(lm_head),
+            _p(np.ascontiguousarray(cache_in), f32p), td.encode(), _p(q, f32p))
+        assert rc == 0
+
+        def rd(n):
+            return np.fromfile(os.path.join(td, f"decode_layer0_{n}.bin"), np.float32)
+        ckv = rd("c_kv_cache").reshape(pos + 1, KVL)
+        kpe = rd("k_pe_cache").reshape(pos + 1, QKR)
+        ao = rd("attn_out")
+    assert np.array_equal(ckv[:pos], cache_in[:, :KVL])
+    d = {f"{name}_{k}": v for k, v in dict(
+        cfg=np.array([H, NH, QKN, QKR, KVL, VHD, q_lora, inter, pos, seed], np.int64),
+        eps=np.array([rms_eps, flts[1]], np.float32), inv=inv,
+        x=synth.bf16_to_f32(embed[0]), q=q, kv=np.concatenate([ckv[pos], kpe[pos]]),
+        attn_out=ao).items()}
+    for k, v in w.items():
+        if v is not None:
+            d[f"{name}_sum_{k}"] = np.uint64(synth.checksum_u16(v))
+    d[f"{name}_sum_cache"] = np.uint64(synth.checksum_u16(synth.bf16_from_f32(cache_in)))
+    return d
+
+
+def gen_mla_front():
+    """RoPE (run.c:47-67), the YaRN table as config_from_json +
+    build_rope_inv_freq make it (model_load.c:242-325), and whole decode
+    fronts (run.c:418-428) with the attention behind them (attn_out)."""
+    d = {}
+    rng = np.random.default_rng(700)
+    for name in ROPE_CONFIGS:
+        inv, ints, flts = _ref_config(name)
+        d[f"cfg_{name}_inv"], d[f"cfg_{name}_ints"], d[f"cfg_{name}_flts"] = inv, ints, flts
+    inv = d["cfg_dsv2_inv"]
+    v = synth.normal_f32(rng, (6, 64))
+    for il in (0, 1):
+        for pos in (0, 1, 7, 4095, 163839):
+            d[f"rope_il{il}_p{pos}_out"] = O.ref_rope_apply(v, pos, inv, il)
+    d["rope_in"], d["rope_inv"] = v, inv
+    d.update(_front_case("dsv2", "dsv2", 701, 1000))
+    d.update(_front_case("glm", "glm", 702, 37))
+    np.savez_compressed(os.path.join(OUT, "mla_front.npz"), **d)
+
+
+GENERATORS = dict(mla_front=lambda: gen_mla_front(), matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),
                   ffn_tiny=lambda: gen_ffn_tiny(), absorbed=lambda: gen_absorbed(),
                   ffn_dsv2=lambda: gen_ffn_dsv2(), lm_head=lambda: gen_lm_head())
 

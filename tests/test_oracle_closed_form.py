@@ -277,3 +277,47 @@ def test_argmax_tie_and_nan_rules(oracle):
     m[int(np.argmax(v))] = np.nan
     assert oracle.argmax(m) == int(np.nanargmax(m))            # other NaNs never win
     assert oracle.argmax(np.full(5, -np.inf, np.float32)) == 0
+
+
+def test_rope_closed_forms(oracle):
+    """RoPE (run.c:47-67): position 0 is the identity; each rotated pair keeps
+    its length; rotating by -p undoes p; the split-half layout holds exactly
+    the adjacent layout's values, evens first (a dropped sign, a swapped
+    sin/cos or a wrong output index fails one of these)."""
+    rng = np.random.default_rng(3)
+    inv = oracle.rope_inv_freq(64, 10000.0)
+    v = synth.normal_f32(rng, (5, 64))
+    for il in (0, 1):
+        assert np.array_equal(oracle.rope_apply(v, 0, inv, il), v if il == 0 else
+                              np.concatenate([v[:, 0::2], v[:, 1::2]], axis=1))
+    for pos in (1, 17, 3000):
+        a = oracle.rope_apply(v, pos, inv, 0)
+        n0 = np.hypot(v[:, 0::2], v[:, 1::2])
+        assert np.allclose(np.hypot(a[:, 0::2], a[:, 1::2]), n0, rtol=1e-6, atol=0)
+        assert np.allclose(oracle.rope_apply(a, -pos, inv, 0), v, rtol=0, atol=2e-6)
+        b = oracle.rope_apply(v, pos, inv, 1)
+        assert np.array_equal(b, np.concatenate([a[:, 0::2], a[:, 1::2]], axis=1))
+        # pair j rotates by pos * inv[j]: compare with a float64 rotation
+        ang = (np.float32(pos) * inv).astype(np.float64)
+        c, s = np.cos(ang), np.sin(ang)
+        e = v[:, 0::2].astype(np.float64) * c - v[:, 1::2] * s
+        o = v[:, 0::2].astype(np.float64) * s + v[:, 1::2] * c
+        assert np.allclose(a[:, 0::2], e, rtol=0, atol=1e-6)
+        assert np.allclose(a[:, 1::2], o, rtol=0, atol=1e-6)
+
+
+def test_rope_inv_freq_closed_forms(oracle):
+    """YaRN blend (model_load.c:299-325): factor 1 is plain RoPE (1 / theta^(2j/d));
+    below the correction range the table is the extrapolated frequency, above
+    it the interpolated one (that / factor), strictly between them inside."""
+    plain = oracle.rope_inv_freq(64, 10000.0, 1.0)
+    j = np.arange(32)
+    assert np.allclose(plain, 1.0 / 10000.0 ** (2.0 * j / 64), rtol=2e-7, atol=0)
+    y = oracle.rope_inv_freq(64, 10000.0, 40.0, 32.0, 1.0, 4096.0)
+    lo = np.floor(64 * np.log(4096 / (32 * 2 * np.pi)) / (2 * np.log(10000.0)))
+    hi = np.ceil(64 * np.log(4096 / (1 * 2 * np.pi)) / (2 * np.log(10000.0)))
+    assert 0 < lo < hi < 31
+    assert np.array_equal(y[j <= lo], plain[j <= lo])
+    assert np.array_equal(y[j >= hi], (plain / np.float32(40.0))[j >= hi])
+    mid = (j > lo) & (j < hi)
+    assert np.all(y[mid] < plain[mid]) and np.all(y[mid] > plain[mid] / 40.0)

@@ -1,6 +1,10 @@
 """The CPU oracle against golden vectors written by the reference's own
 compiled src/run.c (tests/golden/make_golden.py), bit for bit, and against
 the compiled reference itself on fresh random inputs where it is built."""
+import json
+import os
+import tempfile
+
 import numpy as np
 import pytest
 
@@ -168,3 +172,79 @@ def test_rmsnorm_argmax_vs_reference_random(oracle):
     for n in (1, 2, 1000, 102400):
         lg = synth.normal_f32(rng, (n,))
         assert oracle.argmax(lg) == oracle.ref_sample(lg)
+
+
+# ---- MLA decode front (mla_front.npz) -----------------------------------------
+
+def test_rope_inv_freq_golden(oracle):
+    """The YaRN table as the reference's config_from_json + build_rope_inv_freq
+    produce it from a config.json (model_load.c:242-325), bit for bit, from
+    the oracle and from the library's own host code."""
+    import mlamoe
+    g = load_golden("mla_front.npz")
+    for name in ("dsv2", "glm", "yarn2"):
+        f = g[f"cfg_{name}_flts"]
+        dim = int(g[f"cfg_{name}_ints"][0])
+        args = (dim, *(float(v) for v in f[3:8]))
+        assert np.array_equal(oracle.rope_inv_freq(*args), g[f"cfg_{name}_inv"]), name
+        assert np.array_equal(mlamoe.rope_inv_freq(*args), g[f"cfg_{name}_inv"]), name
+    # the parsed fields the front uses
+    assert list(g["cfg_dsv2_ints"][:3]) == [64, 0, 0] and list(g["cfg_glm_ints"][:3]) == [64, 1, 96]
+    assert g["cfg_glm_flts"][0] == np.float32(1e-5) and g["cfg_dsv2_flts"][1] == np.float32(1e-6)
+
+
+def test_rope_apply_golden(oracle):
+    g = load_golden("mla_front.npz")
+    for il in (0, 1):
+        for pos in (0, 1, 7, 4095, 163839):
+            out = oracle.rope_apply(g["rope_in"], pos, g["rope_inv"], il)
+            assert np.array_equal(out.view(np.uint32), g[f"rope_il{il}_p{pos}_out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["dsv2", "glm"])
+def test_mla_front_golden(oracle, name):
+    """q after RoPE and the latent-cache row that forward_absorbed appends
+    (run.c:418-428), then the attention output behind them (run.c:430-468:
+    absorbed chain on the fp32 cache, o_proj), all bit for bit."""
+    from conftest import front_case
+    g = load_golden("mla_front.npz")
+    c = front_case(g, name)
+    cfg = oracle.front_cfg(c["H"], c["NH"], c["QKN"], c["QKR"], c["KVL"], c["q_lora"],
+                           c["rms_eps"], c["mla_eps"], c["il"])
+    q, kv, _ = oracle.mla_front(cfg, c["w"], c["inv"], c["x"], c["pos"])
+    assert np.array_equal(q[0].view(np.uint32), g[f"{name}_q"].view(np.uint32))
+    assert np.array_equal(kv[0].view(np.uint32), g[f"{name}_kv"].view(np.uint32))
+    cache = np.concatenate([synth.bf16_to_f32(c["cache_in"]), kv], axis=0)[None]
+    ctx, _, _, _ = oracle.absorbed_decode(q.reshape(1, c["NH"], -1), c["w"]["kv_b"], cache,
+                                          c["pos"] + 1, c["NH"], c["QKN"], c["QKR"], c["KVL"],
+                                          c["VHD"])
+    ao = oracle.matmul(ctx[0], c["w"]["o_proj"])
+    assert np.array_equal(ao.view(np.uint32), g[f"{name}_attn_out"].view(np.uint32))
+
+
+@pytest.mark.skipif(not __import__("pyoracle").ref_available(),
+                    reason="compiled reference (oracle/_ref) not built here")
+def test_rope_against_reference_random(oracle):
+    rng = np.random.default_rng(31)
+    for _ in range(20):
+        dim = int(rng.choice([8, 32, 64, 128]))
+        theta = float(rng.choice([10000.0, 50000.0, 1e6]))
+        factor = float(rng.choice([1.0, 4.0, 40.0]))
+        bf, bs = float(rng.choice([16.0, 32.0])), float(rng.choice([1.0, 2.0]))
+        om = float(rng.choice([2048.0, 4096.0]))
+        inv = oracle.rope_inv_freq(dim, theta, factor, bf, bs, om)
+        # the reference's own table for the same config.json fields
+        with tempfile.TemporaryDirectory() as td:
+            with open(os.path.join(td, "config.json"), "w") as f:
+                json.dump(dict(num_hidden_layers=1, hidden_size=64, kv_lora_rank=512,
+                               qk_rope_head_dim=dim, rope_theta=theta,
+                               rope_scaling=dict(type="yarn", factor=factor, beta_fast=bf,
+                                                 beta_slow=bs,
+                                                 original_max_position_embeddings=om)), f)
+            ref_inv, _, _ = oracle.ref_config_rope(td)
+        assert np.array_equal(inv, ref_inv), (dim, theta, factor, bf, bs, om)
+        v = synth.normal_f32(rng, (3, dim))
+        for il in (0, 1):
+            pos = int(rng.integers(0, 200000))
+            assert np.array_equal(oracle.rope_apply(v, pos, inv, il),
+                                  oracle.ref_rope_apply(v, pos, inv, il))
