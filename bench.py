@@ -17,6 +17,7 @@ decode step (vocabulary 102400, B = 1 and 64).
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -305,6 +306,65 @@ def bench_dense_bf16(ctx, steps, warmup, T=512):
                 kernel_avg_us=round(prof["mm_gemm_bf16"][0] * 1e3, 2), gflop=flops / 1e9)
 
 
+def bench_attn_layer(ctx_unused, steps, warmup, L=4096, NH=16):
+    """The attention half of a DeepSeek-V2-Lite decode layer (src/run.c:418-469)
+    for B sequences, each appending at position L-1 and attending all L
+    positions: input norm + q_proj/kv_a projections + RoPE + kv_a_layernorm
+    into the bf16 latent cache (mm_mla_front_dev), the absorbed chain
+    (mm_mla_absorbed_decode_dev), o_proj with the residual add
+    (mm_matmul_bf16_dev, MM_MATMUL_ACCUMULATE).  B = 1 (latency) and B = 32
+    (the config-5 batch)."""
+    Hd, QKN, QKR, KVL, VHD = 2048, 128, 64, 512, 128
+    QD, KVD = NH * (QKN + QKR), KVL + QKR
+    lib = mlamoe.lib()
+    res = {}
+    for B in (1, 32):
+        log(f"[attn_layer] B={B} setup")
+        with mlamoe.Context(0) as ctx:
+            h = ctx.h
+            ctx.mla_init(NH, QKN, QKR, KVL, VHD)
+            ctx.mla_front_init(Hd, mlamoe.rope_inv_freq(QKR, 10000.0, 40.0, 32.0, 1.0, 4096.0))
+            kvb = ctx.empty((NH * (QKN + VHD), KVL), np.uint16)
+            ctx.fill(kvb, NH * (QKN + VHD) * KVL, mlamoe.MM_FILL_BF16_NORMAL, 71, 0.02)
+            ctx.mla_load_layer(0, kvb, mlamoe.MM_LOAD_DEVICE_PTRS)
+            shapes = dict(input_norm=(Hd,), q_proj=(QD, Hd), kv_a_proj=(KVD, Hd),
+                          kv_a_norm=(KVL,), o_proj=(Hd, NH * VHD))
+            wd = {}
+            for i, (k, shp) in enumerate(shapes.items()):
+                wd[k] = ctx.empty(shp, np.uint16)
+                ctx.fill(wd[k], int(np.prod(shp)), mlamoe.MM_FILL_BF16_NORMAL, 72 + i,
+                         0.1 if len(shp) == 1 else 0.02)
+            ws = mlamoe.MlaFrontWeights(*[wd[k].ptr if k in wd else None
+                                          for k in mlamoe.FRONT_WEIGHTS])
+            cache = ctx.empty((B, L, KVD), np.uint16)
+            ctx.fill(cache, B * L * KVD, mlamoe.MM_FILL_BF16_NORMAL, 80, 1.0)
+            x = ctx.empty((B, Hd), np.float32)
+            ctx.fill(x, B * Hd, mlamoe.MM_FILL_F32_NORMAL, 81, 1.0)
+            pos = ctx.to_device(np.full(B, L - 1, np.int32))
+            q = ctx.empty((B, QD), np.float32)
+            co = ctx.empty((B, NH * VHD), np.float32)
+
+            def step():
+                mlamoe._check(lib.mm_mla_front_dev(h, B, x.ptr, C.byref(ws), pos.ptr, q.ptr,
+                                                   cache.ptr, L, None))
+                mlamoe._check(lib.mm_mla_absorbed_decode_dev(h, 0, B, q.ptr, cache.ptr, L, None,
+                                                             L, co.ptr, None, None, None))
+                mlamoe._check(lib.mm_matmul_bf16_dev(h, x.ptr, co.ptr, wd["o_proj"].ptr, Hd,
+                                                     NH * VHD, B, mlamoe.MM_MATMUL_ACCUMULATE))
+            ms, _ = timed(ctx, step, steps * 5, warmup)
+            names = ["mm_gemv_1", "mm_gemv_4", "mm_rmsnorm", "mm_cvt_bf16", "mm_gemm_bf16",
+                     "mm_mla_rope", "mm_mla_qprep", "mm_mla_attn", "mm_mla_combine", "mm_mla_uv"]
+            prof = profile_kernels(ctx, step, 20, names)
+            wbytes = 2 * (QD * Hd + KVD * Hd + Hd * NH * VHD + 2 * NH * QKN * KVL + Hd + KVL)
+            nbytes = wbytes + B * L * KVD * 2
+            res[f"B{B}"] = dict(ms_per_step=ms, tok_s=B / (ms * 1e-3), mb=nbytes / 1e6,
+                                gbs=nbytes / (ms * 1e-3) / 1e9,
+                                frac_hbm=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                kernels_us={n: [round(v[0] * 1e3, 2), v[1]]
+                                            for n, v in prof.items() if v[1]})
+    return res
+
+
 def bench_lm_head(ctx, steps, warmup, V=102400, H=2048):
     """LM head of a decode step on DeepSeek-V2-Lite's vocabulary: final
     RMSNorm, logits over V (bf16 [V, H] weight), greedy argmax, for B = 1
@@ -383,7 +443,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["decode_i8", "prefill_i8", "decode_bf16", "mla", "dense",
-                                       "lm_head", "calib"],
+                                       "lm_head", "attn_layer", "calib"],
                     help="run one workload and print its result dict (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (reference kernel for the "
@@ -407,7 +467,12 @@ def main():
     if args.only:
         fn = dict(decode_i8=bench_decode_i8, prefill_i8=bench_prefill_i8,
                   decode_bf16=bench_decode_bf16, mla=bench_mla_decode,
-                  dense=bench_dense_bf16, lm_head=bench_lm_head)[args.only]
+                  dense=bench_dense_bf16, lm_head=bench_lm_head,
+                  attn_layer=bench_attn_layer)[args.only]
+        if args.only == "attn_layer":
+            print(json.dumps({args.only: fn(None, args.steps, args.warmup)}, default=float),
+                  flush=True)
+            return
         with mlamoe.Context(0) as ctx:
             print(json.dumps({args.only: fn(ctx, args.steps, args.warmup)}, default=float), flush=True)
         return
@@ -426,6 +491,7 @@ def main():
             extra["dense_bf16_config2"] = bench_dense_bf16(ctx, args.steps, args.warmup)
         with mlamoe.Context(0) as ctx:
             extra["lm_head_dsv2"] = bench_lm_head(ctx, args.steps, args.warmup)
+        extra["attn_layer_dsv2"] = bench_attn_layer(None, args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
     line = {

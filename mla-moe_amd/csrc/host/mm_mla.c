@@ -76,7 +76,17 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
     if (B == 0) return MM_OK;
     if (kv_len < 1 || seq_stride < kv_len)
         return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: need 1 <= kv_len <= seq_stride");
-    const int nchunks = (kv_len + MM_MLA_CHUNK - 1) / MM_MLA_CHUNK;
+    const int g_nh = c->mla.n_heads, HG0 = (g_nh + 15) / 16;
+    /* chunk length: MM_MLA_CHUNK keys per block, halved (down to 16 keys per
+     * wave) while the grid has fewer than MM_MLA_MIN_BLOCKS blocks and the
+     * chunk count stays <= 64 (the merge's limit) -- small batches then spread
+     * the cache read over more CUs */
+    int chunk = MM_MLA_CHUNK;
+    while (chunk > 16 * MM_MLA_AW &&
+           (size_t)B * HG0 * ((kv_len + chunk - 1) / chunk) < MM_MLA_MIN_BLOCKS &&
+           (kv_len + chunk / 2 - 1) / (chunk / 2) <= 64)
+        chunk /= 2;
+    const int nchunks = (kv_len + chunk - 1) / chunk;
     if (nchunks > 64)
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_absorbed_decode_dev: kv_len > %d",
                        64 * MM_MLA_CHUNK);
@@ -105,7 +115,7 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                         0, &qa)))
         return st;
     mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
-                           part_o, probs, kv_len, NH, HG, nchunks, QKN};
+                           part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */

@@ -212,7 +212,10 @@ typedef struct {
 #define MM_MLA_KVD (MM_MLA_KVL + MM_MLA_QKR)
 #define MM_MLA_KC (MM_MLA_KVD / 32) /* 32-wide latent chunks of one cache row */
 #ifndef MM_MLA_CHUNK
-#define MM_MLA_CHUNK 512          /* keys per attention block */
+#define MM_MLA_CHUNK 512          /* keys per attention block (the longest chunk) */
+#endif
+#ifndef MM_MLA_MIN_BLOCKS
+#define MM_MLA_MIN_BLOCKS 256     /* chunks shrink (to 16 keys per wave) until the grid has this many blocks */
 #endif
 #ifndef MM_MLA_AW
 #define MM_MLA_AW 4               /* waves per attention block */
@@ -248,6 +251,7 @@ typedef struct {
     float *scores;            /* [B, NH, probs_stride] scaled scores (debug) or 0 */
     int probs_stride;
     int NH, HG, nchunks, QKN;
+    int chunk;                /* keys per block: a multiple of 16 * MM_MLA_AW, <= MM_MLA_CHUNK */
 } mm_mla_attn_args;
 
 /* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */

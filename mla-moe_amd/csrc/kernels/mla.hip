@@ -152,7 +152,6 @@ __device__ __forceinline__ s16x4 ds_read_tr16(uint32_t addr, int off) {
 }
 
 #define AW MM_MLA_AW               /* waves per attention block */
-#define KPW (MM_MLA_CHUNK / AW)   /* keys per wave */
 #define CROW_B 1056               /* bytes per LDS c_kv row: 1024 + 32 pad */
 #define TILE_B (16 * CROW_B + 16 * 128)   /* 16 keys: c_kv rows, then the k_pe parts */
 static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
@@ -165,8 +164,9 @@ static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
 static_assert((AW * 16 * OROW + AW * 32) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
 static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
-/* grid (nchunks, B, HG), AW waves; wave w handles keys [chunk * 512 + w * KPW,
- * + KPW) in 16-key sub-tiles, each staged into LDS by direct global -> LDS
+/* grid (nchunks, B, HG), AW waves; with KPW = a.chunk / AW keys per wave,
+ * wave w handles keys [chunk * a.chunk + w * KPW, + KPW) in 16-key
+ * sub-tiles, each staged into LDS by direct global -> LDS
  * loads one sub-tile ahead of its use (two LDS stages per wave):
  *   S^T[key][head] = C[key] . Q[head]^T on v_mfma_f32_16x16x32_bf16 with the
  *     cache rows as the A operand and Q (hi and lo halves, in registers) as
@@ -188,8 +188,9 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
     uint8_t *wt0 = alds + (size_t)w * 2 * TILE_B;     /* this wave's two stages */
 
-    const int kbeg = chunk * MM_MLA_CHUNK + w * KPW;
-    const int kend = min(kbeg + KPW, L);
+    const int kpw = a.chunk / AW;                     /* keys per wave */
+    const int kbeg = chunk * a.chunk + w * kpw;
+    const int kend = min(kbeg + kpw, L);
     const uint8_t *cseq = (const uint8_t *)(a.cache + (size_t)b * a.seq_stride * KVD);
     /* sub-tile at key k0 -> stage st: row p's c_kv (1 KB, one load per lane
      * of 16 B) at p * CROW_B; the k_pe parts (128 B per row) of rows 0..7 and
@@ -442,13 +443,26 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_
     }
     __syncthreads();
     const float mx = stat[0], inv = 1.0f / stat[1];
+    /* thread t owns latent columns 2t, 2t + 1; the chunk partials are read
+     * 16 at a time (all loads in flight before the first is used) and summed
+     * in chunk order */
+    static_assert(KVL == 2 * 256, "combine: two latent columns per thread");
     float *cl = a.clat + ((size_t)b * a.NH + h) * KVL;
-    for (int r = tid; r < KVL; r += blockDim.x) {
-        float o = 0.0f;
-        for (int c = 0; c < a.nchunks; c++)
-            o += wch[c] * a.part_o[((pbase + c) * 16 + hl) * KVL + r];
-        cl[r] = o * inv;
+    const float *po = a.part_o + (pbase * 16 + hl) * KVL + 2 * tid;
+    float o0 = 0.0f, o1 = 0.0f;
+    for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
+        float2 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            v[k] = *(const float2 *)(po + (size_t)min(c0 + k, a.nchunks - 1) * 16 * KVL);
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (c0 + k < a.nchunks) {
+                o0 += wch[c0 + k] * v[k].x;
+                o1 += wch[c0 + k] * v[k].y;
+            }
     }
+    *(float2 *)(cl + 2 * tid) = make_float2(o0 * inv, o1 * inv);
     if (a.probs) {
         float *pr = a.probs + ((size_t)b * a.NH + h) * a.probs_stride;
         for (int k = tid; k < L; k += blockDim.x) pr[k] = __expf(pr[k] - mx) * inv;
