@@ -119,6 +119,29 @@ MM_API int mm_moe_init(mm_ctx *ctx, const mm_moe_config *cfg, int n_layers);
 /* Upload one layer's weights (synchronous). */
 MM_API int mm_moe_load_layer(mm_ctx *ctx, int layer, const mm_moe_layer_weights *w, unsigned flags);
 
+/* ---- the packed int8 expert format (offline quantisation) ------------------ */
+/* One layer's int8 experts as the MFMA kernels read them: a pool of 16-row x
+ * 64-byte fragments -- routed gate/up [E][I/16][H/64][gate, up], routed down
+ * [E][H/16][I/64], shared gate/up [S/16][H/64][gate, up], shared down
+ * [H/16][S/64]; fragment byte 16 l + b = row 16 nb + (l % 16), column
+ * 64 kb + 16 (l / 16) + b -- and a scale table s_g [E*I] | s_u [E*I] |
+ * s_d [E*H] | ss_g [S] | ss_u [S] | ss_d [H] (fp32, per output row: q =
+ * clamp(rint(w / s), -127, 127), s = max|w| / 127).  The reference packs its
+ * bf16 experts at start-up (src/getp_run.hip:58-113, 797-808); this format
+ * holds the int8 pack so a loader uploads it without quantising.  Written by
+ * mlamoe.weights (safetensors container, format "mlamoe-i8"). */
+MM_API int mm_moe_i8_layer_size(const mm_moe_config *cfg, size_t *pool_bytes, size_t *n_scales);
+/* Copy a layer loaded with MM_LOAD_INT8 (quantised on the device) to host
+ * buffers of mm_moe_i8_layer_size.  Synchronous. */
+MM_API int mm_moe_export_layer_i8(mm_ctx *ctx, int layer, void *pool, float *scales);
+/* Load a layer from its packed pool and scales plus the router weight
+ * (moe_gate [E, H] bf16, moe_gate_bias [E] or NULL), host pointers or, with
+ * MM_LOAD_DEVICE_PTRS, device pointers: no quantisation, int8 format only
+ * (MM_FWD_INT8).  Synchronous. */
+MM_API int mm_moe_load_layer_i8_packed(mm_ctx *ctx, int layer, const uint16_t *moe_gate,
+                                       const float *moe_gate_bias, const void *pool,
+                                       const float *scales, unsigned flags);
+
 #define MM_FWD_BF16 0u           /* bf16 weights, fp32 activations */
 #define MM_FWD_INT8 1u           /* int8 weights, per-token int8 activations */
 #define MM_FWD_ACCUMULATE 2u     /* out += ffn(x) (residual fused) instead of out = */

@@ -93,21 +93,31 @@ static int pack_dev(mm_ctx *c, const int8_t *s0, const int8_t *s1, int8_t *dst, 
 
 /* Quantise every expert matrix per output channel (s = max|w|/127) and pack
  * it into MFMA fragment order (kernel_params.h, mm_i8_weights). */
-static int load_int8(mm_ctx *c, mm_moe_layer *L, const mm_moe_layer_weights *w, int dev) {
+/* The packed int8 layer: one pool of fragments, gate/up [E][I/16][H/64][2]
+ * then down [E][H/16][I/64], then the shared expert's gate/up and down
+ * likewise (16 x 64-byte fragments, mm_pack_i8), and one scale table
+ * s_g [E*I] | s_u [E*I] | s_d [E*H] | ss_g [S] | ss_u [S] | ss_d [H]. */
+static void i8_sizes(const mm_moe_config *g, size_t *pool, size_t *nsc) {
+    const size_t H = g->hidden_size, E = g->n_routed_experts, I = g->moe_inter_size;
+    const size_t S = (size_t)g->n_shared_experts * I;
+    *pool = 3 * E * I * H + 3 * S * H;
+    *nsc = 2 * E * I + E * H + 2 * S + H;
+}
+
+/* Allocate the pool and scales of L and point L->i8 into them. */
+static int i8_alloc(mm_ctx *c, mm_moe_layer *L) {
     const mm_moe_config *g = &c->moe;
     const size_t H = g->hidden_size, E = g->n_routed_experts, I = g->moe_inter_size;
     const size_t S = (size_t)g->n_shared_experts * I;
-    const size_t ne = I * H;
-    const size_t gu_b = 2 * E * ne, d_b = E * ne, sgu_b = 2 * S * H, sd_b = S * H;
-    const size_t nsc = 2 * E * I + E * H + 2 * S + H;
-    int st = MM_OK;
-    MM_HIP(hipMalloc((void **)&L->i8_pool, gu_b + d_b + sgu_b + sd_b));
+    size_t pool, nsc;
+    i8_sizes(g, &pool, &nsc);
+    MM_HIP(hipMalloc((void **)&L->i8_pool, pool));
     MM_HIP(hipMalloc((void **)&L->i8_scales, nsc * sizeof(float)));
     mm_i8_weights *q = &L->i8;
     q->gu = L->i8_pool;
-    q->d = q->gu + gu_b;
-    q->sgu = q->d + d_b;
-    q->sdn = q->sgu + sgu_b;
+    q->d = q->gu + 2 * E * I * H;
+    q->sgu = q->d + E * I * H;
+    q->sdn = q->sgu + 2 * S * H;
     float *sc = L->i8_scales;
     q->s_g = sc;
     q->s_u = sc + E * I;
@@ -115,6 +125,17 @@ static int load_int8(mm_ctx *c, mm_moe_layer *L, const mm_moe_layer_weights *w, 
     q->ss_g = sc + 2 * E * I + E * H;
     q->ss_u = q->ss_g + S;
     q->ss_d = q->ss_u + S;
+    return MM_OK;
+}
+
+static int load_int8(mm_ctx *c, mm_moe_layer *L, const mm_moe_layer_weights *w, int dev) {
+    const mm_moe_config *g = &c->moe;
+    const size_t H = g->hidden_size, E = g->n_routed_experts, I = g->moe_inter_size;
+    const size_t S = (size_t)g->n_shared_experts * I;
+    const size_t ne = I * H;
+    int st = i8_alloc(c, L);
+    if (st) return st;
+    mm_i8_weights *q = &L->i8;
 
     const size_t fam = E * ne > S * H ? E * ne : S * H;
     uint16_t *tb = NULL;
@@ -155,6 +176,10 @@ static int load_int8(mm_ctx *c, mm_moe_layer *L, const mm_moe_layer_weights *w, 
         else if (!(st = upload(c, tb, w->shared_down, S * H * 2, dev))) src = tb;
         if (st || (st = quant_rows_dev(c, src, H, S, t0, (float *)q->ss_d))) goto out;
         if ((st = pack_dev(c, t0, NULL, (int8_t *)q->sdn, H, S))) goto out;
+    } else if (hipMemsetAsync((void *)q->ss_d, 0, H * sizeof(float), c->stream) != hipSuccess) {
+        /* no shared expert: its scale slot holds zeros, as in the packed format */
+        st = mm_fail(MM_ERR_HIP, "mm_moe_load_layer: clearing the shared scales");
+        goto out;
     }
 out:;
     hipError_t e = hipStreamSynchronize(c->stream);
@@ -230,6 +255,77 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
 out:;
     hipError_t e = hipStreamSynchronize(c->stream);
     if (!st && e != hipSuccess) st = mm_hip_fail(e, "mm_moe_load_layer");
+    return st;
+}
+
+/* ---- packed int8 layers (the offline expert format) ------------------------ */
+
+static int i8_cfg_ok(const mm_moe_config *g) {
+    return g->hidden_size > 0 && g->n_routed_experts > 0 && g->moe_inter_size > 0 &&
+           g->n_shared_experts >= 0 && g->hidden_size % 64 == 0 && g->moe_inter_size % 64 == 0;
+}
+
+int mm_moe_i8_layer_size(const mm_moe_config *cfg, size_t *pool_bytes, size_t *n_scales) {
+    if (!cfg || !pool_bytes || !n_scales) return mm_fail(MM_ERR_INVALID, "mm_moe_i8_layer_size: NULL argument");
+    if (!i8_cfg_ok(cfg))
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_i8_layer_size: int8 format needs positive sizes "
+                       "with hidden and moe_inter multiples of 64");
+    i8_sizes(cfg, pool_bytes, n_scales);
+    return MM_OK;
+}
+
+int mm_moe_export_layer_i8(mm_ctx *c, int layer, void *pool, float *scales) {
+    if (!c || !pool || !scales) return mm_fail(MM_ERR_INVALID, "mm_moe_export_layer_i8: NULL argument");
+    if (!c->moe_ready || layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded ||
+        !(c->layers[layer].formats & MM_LOAD_INT8))
+        return mm_fail(MM_ERR_STATE, "mm_moe_export_layer_i8: layer %d has no int8 weights", layer);
+    int st = mm_set_device(c);
+    if (st) return st;
+    size_t pb, nsc;
+    i8_sizes(&c->moe, &pb, &nsc);
+    MM_HIP(hipStreamSynchronize(c->stream));
+    MM_HIP(hipMemcpy(pool, c->layers[layer].i8_pool, pb, hipMemcpyDeviceToHost));
+    MM_HIP(hipMemcpy(scales, c->layers[layer].i8_scales, nsc * sizeof(float), hipMemcpyDeviceToHost));
+    return MM_OK;
+}
+
+int mm_moe_load_layer_i8_packed(mm_ctx *c, int layer, const uint16_t *moe_gate,
+                                const float *moe_gate_bias, const void *pool, const float *scales,
+                                unsigned flags) {
+    if (!c || !moe_gate || !pool || !scales)
+        return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer_i8_packed: NULL argument");
+    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer_i8_packed: call mm_moe_init first");
+    if (layer < 0 || layer >= c->n_layers)
+        return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer_i8_packed: layer %d out of range", layer);
+    if (!i8_cfg_ok(&c->moe))
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_load_layer_i8_packed: int8 format needs hidden "
+                       "and moe_inter multiples of 64");
+    mm_moe_layer *L = &c->layers[layer];
+    if (L->loaded) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer_i8_packed: layer %d already loaded", layer);
+    int st = mm_set_device(c);
+    if (st) return st;
+    const mm_moe_config *g = &c->moe;
+    const size_t H = g->hidden_size, E = g->n_routed_experts;
+    const int dev = (flags & MM_LOAD_DEVICE_PTRS) != 0;
+    size_t pb, nsc;
+    i8_sizes(g, &pb, &nsc);
+    MM_HIP(hipMalloc((void **)&L->wg, H * E * sizeof(uint16_t)));
+    if ((st = upload(c, L->wg, moe_gate, H * E * 2, dev))) goto out;
+    if (moe_gate_bias) {
+        if (hipMalloc((void **)&L->bias, E * sizeof(float)) != hipSuccess) {
+            st = mm_fail(MM_ERR_NOMEM, "mm_moe_load_layer_i8_packed: bias");
+            goto out;
+        }
+        if ((st = upload(c, L->bias, moe_gate_bias, E * sizeof(float), dev))) goto out;
+    }
+    if ((st = i8_alloc(c, L))) goto out;
+    if ((st = upload(c, L->i8_pool, pool, pb, dev))) goto out;
+    if ((st = upload(c, L->i8_scales, scales, nsc * sizeof(float), dev))) goto out;
+    L->formats = MM_LOAD_INT8;
+    L->loaded = 1;
+out:;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (!st && e != hipSuccess) st = mm_hip_fail(e, "mm_moe_load_layer_i8_packed");
     return st;
 }
 

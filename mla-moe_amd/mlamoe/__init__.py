@@ -127,6 +127,10 @@ def lib():
         L.mm_argmax_dev.argtypes = [_vp, C.c_int, _vp, C.c_int, _vp]
         L.mm_lm_head_dev.argtypes = [_vp, C.c_int, _vp, _vp, C.c_float, _vp, C.c_int, C.c_int,
                                      _vp, _vp]
+        L.mm_moe_i8_layer_size.argtypes = [C.POINTER(MoeConfig), C.POINTER(C.c_size_t),
+                                           C.POINTER(C.c_size_t)]
+        L.mm_moe_export_layer_i8.argtypes = [_vp, C.c_int, _vp, _vp]
+        L.mm_moe_load_layer_i8_packed.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
         L.mm_rope_inv_freq.argtypes = [C.c_int] + [C.c_float] * 5 + [C.POINTER(C.c_float)]
         L.mm_mla_front_init.argtypes = [_vp, C.POINTER(MlaFrontConfig)]
         L.mm_mla_front_dev.argtypes = [_vp, C.c_int, _vp, C.POINTER(MlaFrontWeights), _vp, _vp,
