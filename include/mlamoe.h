@@ -340,6 +340,69 @@ MM_API int mm_mla_front_dev(mm_ctx *ctx, int B, const float *x, const mm_mla_fro
                             const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
                             float *kv_rows);
 
+/* ---- batched decode engine ------------------------------------------------- */
+
+/* The model-level fields of Config (include/model.h:12-42) the decode step
+ * needs beyond mm_moe_config / mm_mla_config / mm_mla_front_config, and the
+ * engine's capacity. */
+typedef struct {
+    int n_layers;
+    int first_k_dense;       /* layers [0, first_k_dense) have a dense SwiGLU MLP */
+    int hidden_size;
+    int dense_inter_size;
+    int vocab_size;
+    float rms_eps;           /* post_attention_layernorm and the final norm */
+    int max_batch;           /* sequence slots decoded together */
+    int max_seq;             /* positions per slot (the latent cache's seq_stride) */
+    unsigned moe_flags;      /* MM_FWD_BF16 or MM_FWD_INT8 for the MoE layers */
+} mm_engine_config;
+
+/* One layer's non-expert weights, device pointers (ModelWeights,
+ * include/model.h:44-96); the experts and kv_b live in the context
+ * (mm_moe_load_layer*, mm_mla_load_layer). */
+typedef struct {
+    mm_mla_front_weights front;
+    const uint16_t *o_proj;       /* [H, NH*VHD] */
+    const uint16_t *post_norm;    /* [H] post_attention_layernorm */
+    const uint16_t *dense_gate;   /* [dense_inter, H], dense layers only */
+    const uint16_t *dense_up;     /* [dense_inter, H] */
+    const uint16_t *dense_down;   /* [H, dense_inter] */
+} mm_engine_layer;
+
+typedef struct mm_engine mm_engine;
+
+/* An engine over ctx, whose MoE layers (mm_moe_init with n_layers layers,
+ * every MoE layer loaded), MLA layers (mm_mla_init, every layer loaded) and
+ * front (mm_mla_front_init) are set up.  Allocates the latent caches
+ * (n_layers x max_batch x max_seq x (KVL+QKR) bf16) and step buffers. */
+MM_API int mm_engine_create(mm_ctx *ctx, const mm_engine_config *cfg, mm_engine **out);
+MM_API void mm_engine_destroy(mm_engine *e);
+MM_API int mm_engine_set_layer(mm_engine *e, int layer, const mm_engine_layer *w);
+/* embed [vocab, H], final norm [H], lm_head [vocab, H]: device bf16. */
+MM_API int mm_engine_set_head(mm_engine *e, const uint16_t *embed, const uint16_t *final_norm,
+                              const uint16_t *lm_head);
+
+/* One decode step (forward_absorbed, src/run.c:379-501) for batch rows
+ * b < B: slot b takes token tokens[b] at position pos[b] (host arrays) and
+ * next[b] (host) receives the greedy next token; logits (device [B, vocab])
+ * may be NULL.  Slot b's cache rows [0, pos[b]) must hold its earlier
+ * positions.  Synchronous. */
+MM_API int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *pos,
+                          int32_t *next, float *logits);
+
+/* Continuous-batching greedy generation, the work of the reference's
+ * inference() (src/getp_run.hip:920-995) for n_req prompts (token ids):
+ * every step decodes one token of each active slot (a prompt token while
+ * the prompt lasts -- the absorbed decode is exact for prefill, run.c:375-378
+ * -- then the previous step's sample), a finished slot takes the next
+ * waiting request.  Request r stops after max_steps generated tokens, at
+ * eos (not stored; eos < 0: none) or when max_seq positions are used.
+ * out_tokens[r] (capacity max_steps) and out_lens[r] receive its tokens.
+ * Returns the total generated (>= 0) or a negative status. */
+MM_API long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prompts,
+                                    const int32_t *prompt_lens, int max_steps, int eos,
+                                    int32_t *const *out_tokens, int32_t *out_lens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,8 @@ static const struct {
     [K_GEMV2] = {"mm_gemv_2", MOD_GEMV},
     [K_GEMV4] = {"mm_gemv_4", MOD_GEMV},
     [K_MLA_ROPE] = {"mm_mla_rope", MOD_MLA},
+    [K_EMBED] = {"mm_embed", MOD_UTIL},
+    [K_SWIGLU] = {"mm_swiglu", MOD_UTIL},
 };
 
 /* ---- errors ------------------------------------------------------------- */

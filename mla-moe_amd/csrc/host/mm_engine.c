@@ -1,0 +1,287 @@
+/* mm_engine.c -- batched greedy decoding over the library's kernels.
+ *
+ * One decode step (forward_absorbed, src/run.c:379-501) for B sequence
+ * slots at once: embedding, then per layer the attention front
+ * (mm_mla_front_dev: input norm, q / kv_a projections, RoPE, kv_a norm, the
+ * bf16 latent-cache append), the absorbed chain (mm_mla_absorbed_decode_dev
+ * with per-slot lengths), o_proj with the residual add, the post-attention
+ * norm and the FFN (dense SwiGLU for the first layers, the MoE layer with
+ * its residual add), then the LM head's norm, logits and greedy argmax.
+ *
+ * mm_engine_generate is the scheduler: the reference's inference()
+ * (src/getp_run.hip:920-995) prefills and decodes one request at a time;
+ * here every active slot advances one position per step (prompt tokens
+ * first, then its own samples) and a slot that finishes takes the next
+ * waiting request, so the weights stream once per step for the whole batch.
+ * Slot b is batch row b; a step covers rows [0, 1 + the highest active
+ * slot), an idle row inside that range decodes token 0 at position 0 of its
+ * own (free) cache.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "mm_internal.h"
+
+struct mm_engine {
+    mm_ctx *c;
+    mm_engine_config cfg;
+    mm_engine_layer *layers;
+    unsigned char *layer_set;
+    const uint16_t *embed, *final_norm, *lm_head;
+    uint16_t **cache;          /* [n_layers] device [max_batch, max_seq, KVL+QKR] bf16 */
+    float *x, *xn, *q, *ctxo, *g, *u;
+    int32_t *d_io;             /* device [4][max_batch]: tokens, pos, kv_lens, next */
+    int32_t *h_io;             /* pinned host, same layout */
+};
+
+void mm_engine_destroy(mm_engine *e) {
+    if (!e) return;
+    if (e->c) mm_set_device(e->c);
+    if (e->cache) {
+        for (int l = 0; l < e->cfg.n_layers; l++)
+            if (e->cache[l]) hipFree(e->cache[l]);
+        free(e->cache);
+    }
+    void *dev[] = {e->x, e->xn, e->q, e->ctxo, e->g, e->u, e->d_io};
+    for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
+        if (dev[i]) hipFree(dev[i]);
+    if (e->h_io) hipHostFree(e->h_io);
+    free(e->layers);
+    free(e->layer_set);
+    free(e);
+}
+
+int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
+    if (!c || !cfg || !out) return mm_fail(MM_ERR_INVALID, "mm_engine_create: NULL argument");
+    *out = NULL;
+    if (!c->mla_ready || !c->front_ready)
+        return mm_fail(MM_ERR_STATE, "mm_engine_create: call mm_mla_init and mm_mla_front_init first");
+    if (cfg->first_k_dense < cfg->n_layers && !c->moe_ready)
+        return mm_fail(MM_ERR_STATE, "mm_engine_create: call mm_moe_init first");
+    if (cfg->n_layers <= 0 || cfg->n_layers > c->mla_layers ||
+        (cfg->first_k_dense < cfg->n_layers && cfg->n_layers > c->n_layers) || cfg->first_k_dense < 0 ||
+        cfg->max_batch <= 0 || cfg->max_seq <= 0 || cfg->vocab_size <= 0 ||
+        cfg->hidden_size != c->front.hidden_size ||
+        (cfg->first_k_dense < cfg->n_layers && cfg->hidden_size != c->moe.hidden_size) ||
+        (cfg->first_k_dense > 0 && (cfg->dense_inter_size <= 0 || cfg->dense_inter_size % 8)))
+        return mm_fail(MM_ERR_INVALID, "mm_engine_create: configuration does not match the context");
+    if (cfg->moe_flags & ~(unsigned)MM_FWD_INT8)
+        return mm_fail(MM_ERR_INVALID, "mm_engine_create: moe_flags must be MM_FWD_BF16 or MM_FWD_INT8");
+    for (int l = cfg->first_k_dense; l < cfg->n_layers; l++)
+        if (!c->layers[l].loaded)
+            return mm_fail(MM_ERR_STATE, "mm_engine_create: MoE layer %d not loaded", l);
+    for (int l = 0; l < cfg->n_layers; l++)
+        if (!c->mla_kvb[l]) return mm_fail(MM_ERR_STATE, "mm_engine_create: MLA layer %d not loaded", l);
+    int st = mm_set_device(c);
+    if (st) return st;
+    mm_engine *e = calloc(1, sizeof(*e));
+    if (!e) return mm_fail(MM_ERR_NOMEM, "mm_engine_create: calloc");
+    e->c = c;
+    e->cfg = *cfg;
+    e->layers = calloc((size_t)cfg->n_layers, sizeof(mm_engine_layer));
+    e->layer_set = calloc((size_t)cfg->n_layers, 1);
+    e->cache = calloc((size_t)cfg->n_layers, sizeof(uint16_t *));
+    if (!e->layers || !e->layer_set || !e->cache) {
+        mm_engine_destroy(e);
+        return mm_fail(MM_ERR_NOMEM, "mm_engine_create: calloc");
+    }
+    const mm_mla_config *g = &c->mla;
+    const size_t B = (size_t)cfg->max_batch, H = (size_t)cfg->hidden_size;
+    const size_t KVD = (size_t)g->kv_lora_rank + g->qk_rope_head_dim;
+    const size_t QD = (size_t)g->n_heads * (g->qk_nope_head_dim + g->qk_rope_head_dim);
+    const size_t DI = cfg->first_k_dense > 0 ? (size_t)cfg->dense_inter_size : 8;
+    struct { void **p; size_t n; } bufs[] = {
+        {(void **)&e->x, B * H * 4}, {(void **)&e->xn, B * H * 4}, {(void **)&e->q, B * QD * 4},
+        {(void **)&e->ctxo, B * (size_t)g->n_heads * g->v_head_dim * 4},
+        {(void **)&e->g, B * DI * 4}, {(void **)&e->u, B * DI * 4}, {(void **)&e->d_io, 4 * B * 4}};
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+        if (hipMalloc(bufs[i].p, bufs[i].n) != hipSuccess) {
+            mm_engine_destroy(e);
+            return mm_fail(MM_ERR_NOMEM, "mm_engine_create: step buffers");
+        }
+    if (hipHostMalloc((void **)&e->h_io, 4 * B * 4, 0) != hipSuccess) {
+        mm_engine_destroy(e);
+        return mm_fail(MM_ERR_NOMEM, "mm_engine_create: pinned host buffer");
+    }
+    for (int l = 0; l < cfg->n_layers; l++)
+        if (hipMalloc((void **)&e->cache[l], B * cfg->max_seq * KVD * 2) != hipSuccess) {
+            mm_engine_destroy(e);
+            return mm_fail(MM_ERR_NOMEM, "mm_engine_create: latent cache of layer %d (%zu bytes)", l,
+                           B * cfg->max_seq * KVD * 2);
+        }
+    *out = e;
+    return MM_OK;
+}
+
+int mm_engine_set_layer(mm_engine *e, int layer, const mm_engine_layer *w) {
+    if (!e || !w) return mm_fail(MM_ERR_INVALID, "mm_engine_set_layer: NULL argument");
+    if (layer < 0 || layer >= e->cfg.n_layers)
+        return mm_fail(MM_ERR_INVALID, "mm_engine_set_layer: layer %d out of range", layer);
+    if (!w->o_proj || !w->post_norm ||
+        (layer < e->cfg.first_k_dense && (!w->dense_gate || !w->dense_up || !w->dense_down)))
+        return mm_fail(MM_ERR_INVALID, "mm_engine_set_layer: NULL weight");
+    e->layers[layer] = *w;
+    e->layer_set[layer] = 1;
+    return MM_OK;
+}
+
+int mm_engine_set_head(mm_engine *e, const uint16_t *embed, const uint16_t *final_norm,
+                       const uint16_t *lm_head) {
+    if (!e || !embed || !final_norm || !lm_head) return mm_fail(MM_ERR_INVALID, "mm_engine_set_head: NULL argument");
+    e->embed = embed;
+    e->final_norm = final_norm;
+    e->lm_head = lm_head;
+    return MM_OK;
+}
+
+/* The dense SwiGLU MLP with its residual add: x += down . (silu(gate . xn) * (up . xn)),
+ * xn = rmsnorm(x, post_norm) (src/run.c:470-472, 86-93). */
+static int dense_ffn(mm_engine *e, const mm_engine_layer *L, int B) {
+    mm_ctx *c = e->c;
+    const int H = e->cfg.hidden_size, DI = e->cfg.dense_inter_size;
+    int st;
+    if (B <= MM_GEMV_NB && H <= MM_LM_HMAX) {
+        mm_gemv_args a = {e->x, L->post_norm, e->cfg.rms_eps, L->dense_gate, L->dense_up, e->g, e->u,
+                          DI, DI, DI, DI, B, H, 0, 0};
+        if ((st = mm_gemv_launch(c, &a))) return st;
+    } else {
+        mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, e->cfg.rms_eps};
+        if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+        if ((st = mm_matmul_bf16_dev(c, e->g, e->xn, L->dense_gate, DI, H, B, 0))) return st;
+        if ((st = mm_matmul_bf16_dev(c, e->u, e->xn, L->dense_up, DI, H, B, 0))) return st;
+    }
+    const size_t n = (size_t)B * DI;
+    mm_swiglu_args sa = {e->g, e->u, e->g, n};
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    if ((st = mm_launch(c, K_SWIGLU, (unsigned)blocks, 1, 1, 256, 0, &sa))) return st;
+    return mm_matmul_bf16_dev(c, e->x, e->g, L->dense_down, H, DI, B, MM_MATMUL_ACCUMULATE);
+}
+
+int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *pos, int32_t *next,
+                   float *logits) {
+    if (!e || !tokens || !pos || !next) return mm_fail(MM_ERR_INVALID, "mm_engine_step: NULL argument");
+    if (B < 1 || B > e->cfg.max_batch)
+        return mm_fail(MM_ERR_INVALID, "mm_engine_step: B = %d outside [1, %d]", B, e->cfg.max_batch);
+    if (!e->embed) return mm_fail(MM_ERR_STATE, "mm_engine_step: call mm_engine_set_head first");
+    for (int l = 0; l < e->cfg.n_layers; l++)
+        if (!e->layer_set[l]) return mm_fail(MM_ERR_STATE, "mm_engine_step: layer %d not set", l);
+    mm_ctx *c = e->c;
+    const mm_engine_config *f = &e->cfg;
+    const int MB = f->max_batch;
+    int kvmax = 1;
+    for (int b = 0; b < B; b++) {
+        if (pos[b] < 0 || pos[b] >= f->max_seq)
+            return mm_fail(MM_ERR_INVALID, "mm_engine_step: pos[%d] = %d outside [0, %d)", b, pos[b],
+                           f->max_seq);
+        e->h_io[b] = tokens[b];
+        e->h_io[MB + b] = pos[b];
+        e->h_io[2 * MB + b] = pos[b] + 1;
+        if (pos[b] + 1 > kvmax) kvmax = pos[b] + 1;
+    }
+    int st = mm_set_device(c);
+    if (st) return st;
+    int32_t *d_tok = e->d_io, *d_pos = e->d_io + MB, *d_len = e->d_io + 2 * MB, *d_next = e->d_io + 3 * MB;
+    MM_HIP(hipMemcpyAsync(e->d_io, e->h_io, (size_t)3 * MB * 4, hipMemcpyHostToDevice, c->stream));
+    const mm_mla_config *g = &c->mla;
+    const int H = f->hidden_size;
+    mm_embed_args ea = {e->embed, d_tok, e->x, H, f->vocab_size};
+    if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)B, 1, 256, 0, &ea))) return st;
+    for (int l = 0; l < f->n_layers; l++) {
+        const mm_engine_layer *L = &e->layers[l];
+        if ((st = mm_mla_front_dev(c, B, e->x, &L->front, d_pos, e->q, e->cache[l], f->max_seq, NULL)))
+            return st;
+        if ((st = mm_mla_absorbed_decode_dev(c, l, B, e->q, e->cache[l], f->max_seq, d_len, kvmax,
+                                             e->ctxo, NULL, NULL, NULL)))
+            return st;
+        if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, g->n_heads * g->v_head_dim, B,
+                                     MM_MATMUL_ACCUMULATE)))
+            return st;
+        if (l < f->first_k_dense) {
+            if ((st = dense_ffn(e, L, B))) return st;
+        } else {
+            mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, f->rms_eps};
+            if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+            if ((st = mm_moe_forward_dev(c, l, B, e->xn, e->x, NULL, NULL, NULL, NULL,
+                                         f->moe_flags | MM_FWD_ACCUMULATE)))
+                return st;
+        }
+    }
+    if ((st = mm_lm_head_dev(c, B, e->x, e->final_norm, f->rms_eps, e->lm_head, f->vocab_size, H,
+                             logits, d_next)))
+        return st;
+    MM_HIP(hipMemcpyAsync(e->h_io + 3 * MB, d_next, (size_t)B * 4, hipMemcpyDeviceToHost, c->stream));
+    MM_HIP(hipStreamSynchronize(c->stream));
+    memcpy(next, e->h_io + 3 * MB, (size_t)B * 4);
+    return MM_OK;
+}
+
+long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prompts,
+                             const int32_t *prompt_lens, int max_steps, int eos,
+                             int32_t *const *out_tokens, int32_t *out_lens) {
+    if (!e || n_req < 0 || (n_req > 0 && (!prompts || !prompt_lens || !out_tokens || !out_lens)))
+        return mm_fail(MM_ERR_INVALID, "mm_engine_generate: NULL argument");
+    const int MB = e->cfg.max_batch;
+    int *req = malloc((size_t)MB * sizeof(int)), *limit = malloc((size_t)MB * sizeof(int));
+    int32_t *tok = malloc((size_t)MB * 4), *pos = malloc((size_t)MB * 4), *nxt = malloc((size_t)MB * 4);
+    int32_t *last = malloc((size_t)MB * 4);
+    if (!req || !limit || !tok || !pos || !nxt || !last) {
+        free(req); free(limit); free(tok); free(pos); free(nxt); free(last);
+        return mm_fail(MM_ERR_NOMEM, "mm_engine_generate: malloc");
+    }
+    for (int s = 0; s < MB; s++) req[s] = -1;
+    for (int r = 0; r < n_req; r++) out_lens[r] = 0;
+    long long total = 0;
+    int next_req = 0, st = MM_OK;
+    for (;;) {
+        /* admit waiting requests into free slots (lowest first) */
+        for (int s = 0; s < MB && next_req < n_req; s++) {
+            if (req[s] >= 0) continue;
+            while (next_req < n_req) {
+                const int r = next_req++;
+                const int n = prompt_lens[r];
+                /* generated tokens: max_steps, and no more than the positions
+                 * left after the prompt (getp_run.hip:946-952) */
+                const int lim = max_steps < e->cfg.max_seq - n ? max_steps : e->cfg.max_seq - n;
+                if (n < 1 || lim < 1 || !prompts[r]) continue;
+                req[s] = r;
+                limit[s] = lim;
+                pos[s] = 0;
+                break;
+            }
+        }
+        int hi = -1;
+        for (int s = 0; s < MB; s++)
+            if (req[s] >= 0) hi = s;
+        if (hi < 0) break;
+        const int B = hi + 1;
+        for (int s = 0; s < B; s++) {
+            if (req[s] < 0) {
+                tok[s] = 0;
+                pos[s] = 0;
+                continue;
+            }
+            const int r = req[s];
+            tok[s] = pos[s] < prompt_lens[r] ? prompts[r][pos[s]] : last[s];
+        }
+        if ((st = mm_engine_step(e, B, tok, pos, nxt, NULL))) break;
+        for (int s = 0; s < B; s++) {
+            if (req[s] < 0) continue;
+            const int r = req[s];
+            int done = 0;
+            if (pos[s] >= prompt_lens[r] - 1) {           /* this step sampled a token */
+                if (eos >= 0 && nxt[s] == eos) {
+                    done = 1;
+                } else {
+                    out_tokens[r][out_lens[r]++] = nxt[s];
+                    total++;
+                    last[s] = nxt[s];
+                    done = out_lens[r] >= limit[s];
+                }
+            }
+            pos[s]++;
+            if (done) req[s] = -1;
+        }
+    }
+    free(req); free(limit); free(tok); free(pos); free(nxt); free(last);
+    return st ? (long long)st : total;
+}

@@ -41,6 +41,8 @@ typedef enum {
     K_GEMV2,
     K_GEMV4,
     K_MLA_ROPE,
+    K_EMBED,
+    K_SWIGLU,
     K_COUNT
 } mm_kernel_id;
 

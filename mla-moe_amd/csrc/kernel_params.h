@@ -69,6 +69,21 @@ typedef struct {
     int rows, K;
 } mm_quant_w_args;
 
+/* Embedding rows of B tokens: x[b, :] = embed[tokens[b], :] in fp32. */
+typedef struct {
+    const uint16_t *embed;   /* [vocab, H] bf16 */
+    const int32_t *tokens;   /* [B] */
+    float *x;                /* [B, H] */
+    int H, vocab;
+} mm_embed_args;
+
+/* h = silu(g) * u elementwise over n values (the dense SwiGLU MLP). */
+typedef struct {
+    const float *g, *u;
+    float *h;
+    size_t n;
+} mm_swiglu_args;
+
 /* ---- int8 MoE path ------------------------------------------------------ */
 
 /* Per-layer int8 weights in MFMA fragment order.  A "fragment" is the

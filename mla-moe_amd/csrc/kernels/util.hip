@@ -1,5 +1,6 @@
-/* util.hip -- device-side data preparation: synthetic inputs and the int8
- * per-output-channel weight quantiser. */
+/* util.hip -- device-side data preparation (synthetic inputs, the int8
+ * per-output-channel weight quantiser) and the decode step's elementwise
+ * pieces (token embedding, dense SwiGLU). */
 #include "common.h"
 
 /* Counter-based generator: splitmix64 of (seed, index), so any element can be
@@ -55,3 +56,24 @@ extern "C" __global__ __launch_bounds__(256) void mm_quant_weight(mm_quant_w_arg
     }
 }
 
+
+/* x[b] = embed[tokens[b]] widened to fp32 (src/run.c:413, the embedding of
+ * forward_absorbed); a token outside [0, vocab) reads row 0.  grid (ceil(H /
+ * 2048), B), 256 threads, 8 values per thread. */
+extern "C" __global__ __launch_bounds__(256) void mm_embed(mm_embed_args a) {
+    const int b = blockIdx.y;
+    const int tok = a.tokens[b];
+    const uint16_t *src = a.embed + (size_t)(tok >= 0 && tok < a.vocab ? tok : 0) * a.H;
+    float *dst = a.x + (size_t)b * a.H;
+    for (int i = blockIdx.x * 2048 + threadIdx.x; i < a.H && i < (int)(blockIdx.x + 1) * 2048; i += 256)
+        dst[i] = bf16_f32(src[i]);
+}
+
+/* h = silu(g) * u with silu(x) = x / (1 + e^-x) (src/run.c:39, 86-93). */
+extern "C" __global__ __launch_bounds__(256) void mm_swiglu(mm_swiglu_args a) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const float g = a.g[i];
+        a.h[i] = g / (1.0f + expf(-g)) * a.u[i];
+    }
+}

@@ -70,6 +70,19 @@ class MlaFrontWeights(C.Structure):
     _fields_ = [(n, _vp) for n in FRONT_WEIGHTS]
 
 
+class EngineConfig(C.Structure):
+    """Mirror of mm_engine_config."""
+    _fields_ = [("n_layers", C.c_int), ("first_k_dense", C.c_int), ("hidden_size", C.c_int),
+                ("dense_inter_size", C.c_int), ("vocab_size", C.c_int), ("rms_eps", C.c_float),
+                ("max_batch", C.c_int), ("max_seq", C.c_int), ("moe_flags", C.c_uint)]
+
+
+class EngineLayer(C.Structure):
+    """Mirror of mm_engine_layer (device pointers)."""
+    _fields_ = [("front", MlaFrontWeights), ("o_proj", _vp), ("post_norm", _vp),
+                ("dense_gate", _vp), ("dense_up", _vp), ("dense_down", _vp)]
+
+
 class MoeI8Debug(C.Structure):
     _fields_ = [(n, _vp) for n in ("qx", "sx", "acc_gu", "h", "qh", "sh", "acc_d", "y", "hs",
                                    "qhs", "shs", "ys")]
@@ -131,6 +144,15 @@ def lib():
                                            C.POINTER(C.c_size_t)]
         L.mm_moe_export_layer_i8.argtypes = [_vp, C.c_int, _vp, _vp]
         L.mm_moe_load_layer_i8_packed.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_engine_create.argtypes = [_vp, C.POINTER(EngineConfig), C.POINTER(_vp)]
+        L.mm_engine_destroy.argtypes = [_vp]
+        L.mm_engine_destroy.restype = None
+        L.mm_engine_set_layer.argtypes = [_vp, C.c_int, C.POINTER(EngineLayer)]
+        L.mm_engine_set_head.argtypes = [_vp, _vp, _vp, _vp]
+        L.mm_engine_step.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp]
+        L.mm_engine_generate.argtypes = [_vp, C.c_int, C.POINTER(_vp), _vp, C.c_int, C.c_int,
+                                         C.POINTER(_vp), _vp]
+        L.mm_engine_generate.restype = C.c_longlong
         L.mm_rope_inv_freq.argtypes = [C.c_int] + [C.c_float] * 5 + [C.POINTER(C.c_float)]
         L.mm_mla_front_init.argtypes = [_vp, C.POINTER(MlaFrontConfig)]
         L.mm_mla_front_dev.argtypes = [_vp, C.c_int, _vp, C.POINTER(MlaFrontWeights), _vp, _vp,

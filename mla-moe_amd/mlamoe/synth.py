@@ -82,6 +82,32 @@ def attn_layer(seed: int, H: int, NH: int, QKN: int, QKR: int, KVL: int, VHD: in
     return w
 
 
+def model(seed: int, n_layers: int, first_dense: int, H: int, NH: int, QKN: int, QKR: int,
+          KVL: int, VHD: int, dense_inter: int, E: int, I: int, n_shared: int, vocab: int,
+          gate_bias: bool = False) -> dict:
+    """A whole decoder's bf16 weights with DeepSeek-V2's layout: embed
+    [vocab, H], per layer an attn_layer() dict plus post_norm and either a
+    dense MLP (dgate/dup [dense_inter, H], ddown [H, dense_inter]) for the
+    first `first_dense` layers or a moe_layer() dict, then the final norm and
+    lm_head [vocab, H].  Layer l's tensors come from seed + 100 (l + 1)."""
+    rng = np.random.default_rng(seed)
+    m = dict(embed=normal_bf16(rng, (vocab, H), 1.0),
+             final_norm=bf16_from_f32(1.0 + normal_f32(rng, (H,), 0.1)),
+             lm_head=normal_bf16(rng, (vocab, H), 0.02), layers=[])
+    for l in range(n_layers):
+        s = seed + 100 * (l + 1)
+        lw = attn_layer(s, H, NH, QKN, QKR, KVL, VHD)
+        r = np.random.default_rng(s + 1)
+        lw["post_norm"] = bf16_from_f32(1.0 + normal_f32(r, (H,), 0.1))
+        if l < first_dense:
+            lw.update(dgate=normal_bf16(r, (dense_inter, H)), dup=normal_bf16(r, (dense_inter, H)),
+                      ddown=normal_bf16(r, (H, dense_inter)))
+        else:
+            lw.update(moe_layer(s + 2, H, E, I, n_shared, gate_bias=gate_bias))
+        m["layers"].append(lw)
+    return m
+
+
 def activations(seed: int, T: int, H: int) -> np.ndarray:
     return normal_f32(np.random.default_rng(seed), (T, H))
 

@@ -153,6 +153,8 @@ def ref():
         R.ref_absorbed_decode_ex.argtypes = [C.c_int] * 9 + [C.c_float, _f32p, C.c_int, C.c_int] + \
             [_u16p] * 16 + [_f32p, C.c_char_p, _f32p]
         R.ref_rope_apply.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int]
+        R.ref_forward_tokens.restype = C.c_int
+        R.ref_forward_tokens.argtypes = [C.c_void_p, _ip, C.c_int, _f32p]
         R.ref_config_rope.restype = C.c_int
         R.ref_config_rope.argtypes = [C.c_char_p, _f32p, _ip, _f32p]
         _ref = R
@@ -468,3 +470,92 @@ def ref_config_rope(model_dir):
     inv = np.zeros(512, np.float32)
     ref().ref_config_rope(model_dir.encode(), _p(inv, _f32p), _p(ints, _ip), _p(flts, _f32p))
     return inv[:ints[0] // 2].copy(), ints, flts
+
+
+# ---------------------------------------------------------------------------
+# whole decode steps (src/run.c:379-501)
+# ---------------------------------------------------------------------------
+
+def model_logits(c, m, tokens, inv):
+    """forward_absorbed at positions 0..n-1 on tokens (teacher forcing),
+    composed from the restated pieces in the reference's order; c: dict of
+    the Config fields (n_layers, first_dense, H, NH, QKN, QKR, KVL, VHD,
+    dense_inter, E, n_shared, K, I, vocab, router_sigmoid, norm_topk,
+    routed_scaling, rms_eps), m: synth.model().  Returns [n, vocab]."""
+    H, NH, QKN, QKR, KVL, VHD = (c[k] for k in ("H", "NH", "QKN", "QKR", "KVL", "VHD"))
+    KVD, eps, n = KVL + QKR, c["rms_eps"], len(tokens)
+    fc = front_cfg(H, NH, QKN, QKR, KVL, 0, eps, 1e-6, 0)
+    mc = moe_cfg(H, c["E"], c["n_shared"], c["K"], c["I"], c["router_sigmoid"], c["norm_topk"],
+                 c["routed_scaling"])
+    caches = [np.zeros((n, KVD), np.float32) for _ in m["layers"]]
+    out = np.empty((n, c["vocab"]), np.float32)
+    for p, tok in enumerate(tokens):
+        x = (m["embed"][tok].astype(np.uint32) << 16).view(np.float32).copy()
+        for l, lw in enumerate(m["layers"]):
+            q, kv, _ = mla_front(fc, lw, inv, x, p)
+            caches[l][p] = kv[0]
+            ctx, _, _, _ = absorbed_decode(q.reshape(1, NH, -1), lw["kv_b"], caches[l][None, :p + 1],
+                                           p + 1, NH, QKN, QKR, KVL, VHD)
+            x = (x + matmul(ctx[0], lw["o_proj"])).astype(np.float32)
+            xb = rmsnorm(x, lw["post_norm"], eps)
+            if l < c["first_dense"]:
+                hb = np.empty(c["dense_inter"], np.float32)
+                hb2 = np.empty(c["dense_inter"], np.float32)
+                mo = np.empty(H, np.float32)
+                lib().or_swiglu(_p(mo, _f32p), _p(c32(xb), _f32p), _p(lw["dgate"], _u16p),
+                                _p(lw["dup"], _u16p), _p(lw["ddown"], _u16p), c["dense_inter"], H,
+                                _p(hb, _f32p), _p(hb2, _f32p))
+            else:
+                mo = ffn_compute_rows(mc, lw, xb[None])[0][0]
+            x = (x + mo).astype(np.float32)
+        out[p] = matmul(rmsnorm(x, m["final_norm"], eps), m["lm_head"])
+    return out
+
+
+class RefModelSpec(C.Structure):
+    _fields_ = [(k, C.c_int) for k in ("n_layers", "first_k_dense", "H", "NH", "QKN", "QKR",
+                                        "KVL", "VHD", "dense_inter", "E", "n_shared", "K", "I",
+                                        "vocab", "router_sigmoid", "norm_topk", "max_seq")] + \
+        [("routed_scaling", C.c_float), ("rms_eps", C.c_float), ("inv_freq", _f32p),
+         ("embed", _u16p), ("final_norm", _u16p), ("lm_head", _u16p)] + \
+        [(k, C.POINTER(_u16p)) for k in ("in_norm", "q_proj", "kv_a", "kv_a_norm", "kv_b",
+                                         "o_proj", "post_norm", "dgate", "dup", "ddown",
+                                         "moe_gate", "eg", "eu", "ed", "sg", "su", "sd")] + \
+        [("moe_bias", C.POINTER(_f32p))]
+
+
+def ref_forward_tokens(c, m, tokens, inv):
+    """The reference's own forward_absorbed over tokens (teacher forcing)."""
+    L = len(m["layers"])
+    keep = []
+
+    def arr(key, src="layers"):
+        ptrs = (_u16p * L)()
+        for l, lw in enumerate(m["layers"]):
+            a = lw.get(key)
+            if a is not None:
+                a = np.ascontiguousarray(a, np.uint16)
+                keep.append(a)
+                ptrs[l] = _p(a, _u16p)
+        return ptrs
+    bias = (_f32p * L)()
+    for l, lw in enumerate(m["layers"]):
+        if lw.get("moe_gate_bias") is not None:
+            b = c32(lw["moe_gate_bias"])
+            keep.append(b)
+            bias[l] = _p(b, _f32p)
+    n = len(tokens)
+    inv = c32(inv)
+    spec = RefModelSpec(L, c["first_dense"], c["H"], c["NH"], c["QKN"], c["QKR"], c["KVL"], c["VHD"],
+                        c["dense_inter"], c["E"], c["n_shared"], c["K"], c["I"], c["vocab"],
+                        c["router_sigmoid"], c["norm_topk"], max(n, 1), c["routed_scaling"],
+                        c["rms_eps"], _p(inv, _f32p), _p(m["embed"], _u16p),
+                        _p(m["final_norm"], _u16p), _p(m["lm_head"], _u16p),
+                        *[arr(k) for k in ("in_norm", "q_proj", "kv_a", "kv_a_norm", "kv_b",
+                                           "o_proj", "post_norm", "dgate", "dup", "ddown",
+                                           "moe_gate", "eg", "eu", "ed", "sg", "su", "sd")],
+                        bias)
+    out = np.empty((n, c["vocab"]), np.float32)
+    tk = np.ascontiguousarray(tokens, np.int32)
+    assert ref().ref_forward_tokens(C.byref(spec), _p(tk, _ip), n, _p(out, _f32p)) == 0
+    return out

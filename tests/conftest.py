@@ -62,3 +62,20 @@ def front_case(g, name):
     return dict(H=H, NH=NH, QKN=QKN, QKR=QKR, KVL=KVL, VHD=VHD, q_lora=q_lora, il=il, pos=pos,
                 rms_eps=float(eps[0]), mla_eps=float(eps[1]), inv=g[f"{name}_inv"],
                 x=g[f"{name}_x"], w=w, cache_in=cache_in)
+
+
+def engine_case():
+    """The engine golden's model (tests/golden/engine.npz), rebuilt from its
+    seed and checked against the stored checksums: (config dict, model, npz)."""
+    sys.path.insert(0, GOLDEN)
+    from make_golden import ENGINE_CFG, engine_model
+    from mlamoe import synth
+    g = load_golden("engine.npz")
+    m = engine_model(int(g["seed"]))
+    for k in ("embed", "final_norm", "lm_head"):
+        assert synth.checksum_u16(m[k]) == int(g[f"sum_{k}"]), k
+    for l, lw in enumerate(m["layers"]):
+        for k, v in lw.items():
+            if v is not None and v.dtype == np.uint16:
+                assert synth.checksum_u16(v) == int(g[f"sum_l{l}_{k}"]), (l, k)
+    return dict(ENGINE_CFG), m, g

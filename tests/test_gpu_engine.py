@@ -1,0 +1,87 @@
+"""GPU checks of the batched decode engine (mm_engine_*): whole decode steps
+against the reference's forward_absorbed (tests/golden/engine.npz, pinned
+bit for bit by the oracle's composition), and the continuous-batching
+generation against the oracle token by token.
+
+Bars: logits normwise <= 2e-3 of the reference's (the north-star bf16 bar;
+this build's latent cache is bf16 where the reference's is fp32); a
+generated token is the oracle's argmax for the same prefix, or within 2e-3
+(normwise) of its maximum where the two differ by a near-tie.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import mlamoe
+from conftest import engine_case, max_abs_rel
+from mlamoe.engine import Engine
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_engine_teacher_forced_logits(int8):
+    """B = 1 (GEMV projections) and B = 6 slots (MFMA GEMMs) on the same
+    token sequence at once, bf16 and int8 experts (measured 2.5e-4 and
+    6.7e-4 of the reference)."""
+    c, m, g = engine_case()
+    toks, ref = g["tokens"], g["logits"]
+    print(f"engine teacher forced int8={int8}", flush=True)
+    with mlamoe.Context(0) as ctx:
+        eng = Engine.from_host(ctx, c, m, g["inv"], max_batch=6, max_seq=32, int8=int8)
+        try:
+            for B in (1, 6):
+                errs = []
+                for p, t in enumerate(toks):
+                    nxt, lg = eng.step(np.full(B, t), np.full(B, p), want_logits=True)
+                    for b in range(B):
+                        errs.append(max_abs_rel(lg[b], ref[p]))
+                        if not int8:
+                            assert lg[b][nxt[b]] >= ref[p].max() - TOL * np.abs(ref[p]).max()
+                print(f"B={B} worst normwise logits error {max(errs):.2e}", flush=True)
+                assert max(errs) < TOL
+        finally:
+            eng.close()
+
+
+def test_engine_generate_continuous_batching(oracle):
+    """7 requests of different prompt lengths through 3 slots: every
+    generated token checked against the oracle's logits for its prefix; the
+    position budget (max_seq) and max_steps limits; eos stops a request."""
+    c, m, g = engine_case()
+    inv = g["inv"]
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, c["vocab"], n).astype(np.int32) for n in (3, 1, 7, 2, 5, 9, 4)]
+    max_seq, max_steps = 14, 6
+    with mlamoe.Context(0) as ctx:
+        eng = Engine.from_host(ctx, c, m, inv, max_batch=3, max_seq=max_seq)
+        try:
+            outs, total = eng.generate(prompts, max_steps)
+            assert total == sum(len(o) for o in outs)
+            for p, o in zip(prompts, outs):
+                assert len(o) == min(max_steps, max_seq - len(p))
+                seq = np.concatenate([p, o])
+                lg = oracle.model_logits(c, m, seq[:-1], inv)
+                for k, t in enumerate(o):
+                    row = lg[len(p) - 1 + k]
+                    assert t == row.argmax() or row[t] >= row.max() - TOL * np.abs(row).max()
+            # eos: stop at the first sampled eos (not stored)
+            eos = int(outs[0][2])
+            outs2, _ = eng.generate(prompts[:1], max_steps, eos=eos)
+            assert list(outs2[0]) == list(outs[0][:2])
+            # an empty prompt generates nothing
+            o, t = eng.generate([np.zeros(0, np.int32), prompts[1]], 0)
+            assert t == 0 and len(o[0]) == 0 and len(o[1]) == 0
+        finally:
+            eng.close()
+
+
+def test_engine_errors():
+    L = mlamoe.lib()
+    with mlamoe.Context(0) as ctx:
+        cfg = mlamoe.EngineConfig(1, 1, 256, 64, 100, 1e-6, 2, 8, 0)
+        h = ctypes.c_void_p()
+        assert L.mm_engine_create(ctx.h, cfg, ctypes.byref(h)) != 0
+        assert b"mm_mla_init" in L.mm_last_error()

@@ -248,3 +248,16 @@ def test_rope_against_reference_random(oracle):
             pos = int(rng.integers(0, 200000))
             assert np.array_equal(oracle.rope_apply(v, pos, inv, il),
                                   oracle.ref_rope_apply(v, pos, inv, il))
+
+
+# ---- whole decode steps (engine.npz) -----------------------------------------
+
+def test_model_logits_golden(oracle):
+    """The oracle's composition of a decode step (front, absorbed chain,
+    o_proj, dense / MoE FFN, final norm, lm_head) equals the reference's
+    forward_absorbed bit for bit at every position of a teacher-forced
+    sequence on a dense + MoE model."""
+    from conftest import engine_case
+    c, m, g = engine_case()
+    lg = oracle.model_logits(c, m, g["tokens"], g["inv"])
+    assert np.array_equal(lg.view(np.uint32), g["logits"].view(np.uint32))
