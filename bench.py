@@ -365,6 +365,87 @@ def bench_attn_layer(ctx_unused, steps, warmup, L=4096, NH=16):
     return res
 
 
+def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
+    """End-to-end greedy decoding of a DeepSeek-V2-Lite-shaped model (27
+    layers: a dense SwiGLU layer 0 (intermediate 10944), 26 MoE layers with
+    int8 experts, vocabulary 102400; random weights generated on the device)
+    through the batched engine: (1) one decode step of B slots at context
+    `prompt` (the steady-state step), (2) mm_engine_generate over B requests
+    of `prompt` tokens generating `gen` tokens each (prompts consumed by the
+    same decode steps, continuous batching over B slots)."""
+    from mlamoe.engine import Engine
+    NL, DI, V, NH, QKN, QKR, KVL, VHD = 27, 10944, 102400, 16, 128, 64, 512, 128
+    QD, KVD = NH * (QKN + QKR), KVL + QKR
+    log("[engine] building a 27-layer DeepSeek-V2-Lite-shaped model on the device")
+    lib = mlamoe.lib()
+    with mlamoe.Context(0) as ctx:
+        ctx.mla_init(NH, QKN, QKR, KVL, VHD, n_layers=NL)
+        ctx.mla_front_init(H, mlamoe.rope_inv_freq(QKR, 10000.0, 40.0, 32.0, 1.0, 4096.0))
+        ctx.moe_init(H, E, NS, K, I, n_layers=NL)
+        stage = bf16_buffers(ctx)
+        wst = dict(stage)
+        wst["moe_gate_bias"] = None
+        kvb = ctx.empty((NH * (QKN + VHD), KVL), np.uint16)
+        seed = [1000]
+
+        def filled(shape, std=0.02):
+            b = ctx.empty(shape, np.uint16)
+            seed[0] += 1
+            ctx.fill(b, int(np.prod(shape)), mlamoe.MM_FILL_BF16_NORMAL, seed[0], std)
+            return b
+        layers = []
+        for l in range(NL):
+            ctx.fill(kvb, int(np.prod(kvb.shape)), mlamoe.MM_FILL_BF16_NORMAL, 5000 + l, 0.02)
+            ctx.mla_load_layer(l, kvb, mlamoe.MM_LOAD_DEVICE_PTRS)
+            fr = mlamoe.MlaFrontWeights(filled((H,), 0.1).ptr, filled((QD, H)).ptr, None, None, None,
+                                        filled((KVD, H)).ptr, filled((KVL,), 0.1).ptr)
+            ly = mlamoe.EngineLayer(fr, filled((H, NH * VHD)).ptr, filled((H,), 0.1).ptr)
+            if l == 0:
+                ly.dense_gate, ly.dense_up = filled((DI, H)).ptr, filled((DI, H)).ptr
+                ly.dense_down = filled((H, DI)).ptr
+            else:
+                fill_layer_bf16(ctx, stage, 7000 + l)
+                ctx.moe_load_layer(l, wst, mlamoe.MM_LOAD_INT8 | mlamoe.MM_LOAD_DEVICE_PTRS)
+            layers.append(ly)
+        for b in list(stage.values()) + [kvb]:
+            b.free()
+            ctx._bufs.remove(b)
+        max_seq = prompt + gen + 8
+        cfg = mlamoe.EngineConfig(NL, 1, H, DI, V, 1e-6, B, max_seq, mlamoe.MM_FWD_INT8)
+        h = C.c_void_p()
+        mlamoe._check(lib.mm_engine_create(ctx.h, C.byref(cfg), C.byref(h)))
+        eng = Engine(ctx, h.value, cfg, [])
+        try:
+            for l, ly in enumerate(layers):
+                mlamoe._check(lib.mm_engine_set_layer(eng.h, l, C.byref(ly)))
+            mlamoe._check(lib.mm_engine_set_head(eng.h, filled((V, H), 1.0).ptr, filled((H,), 0.1).ptr,
+                                                 filled((V, H)).ptr))
+            rng = np.random.default_rng(11)
+            toks = rng.integers(0, V, B).astype(np.int32)
+            pos = np.full(B, prompt, np.int32)
+            log(f"[engine] decode step B={B} at context {prompt}")
+            for _ in range(warmup):
+                eng.step(toks, pos)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                eng.step(toks, pos)
+            step_ms = (time.perf_counter() - t0) * 1e3 / steps
+            prompts = [rng.integers(0, V, prompt).astype(np.int32) for _ in range(B)]
+            log(f"[engine] generate: {B} requests x ({prompt} prompt + {gen} generated) tokens")
+            eng.generate(prompts[:2], 2)                      # warm the generate path
+            t0 = time.perf_counter()
+            outs, total = eng.generate(prompts, gen)
+            gen_s = time.perf_counter() - t0
+        finally:
+            eng.close()
+    return dict(model="DeepSeek-V2-Lite shape, 27 layers, int8 experts, random weights",
+                step_B=B, step_context=prompt + 1, step_ms=step_ms, step_tok_s=B / (step_ms * 1e-3),
+                generate_requests=B, generate_prompt=prompt, generate_new=gen,
+                generate_tokens=total, generate_s=gen_s, generate_tok_s=total / gen_s,
+                generate_steps=prompt + gen - 1,
+                generate_positions_per_s=B * (prompt + gen - 1) / gen_s)
+
+
 def bench_lm_head(ctx, steps, warmup, V=102400, H=2048):
     """LM head of a decode step on DeepSeek-V2-Lite's vocabulary: final
     RMSNorm, logits over V (bf16 [V, H] weight), greedy argmax, for B = 1
@@ -443,7 +524,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["decode_i8", "prefill_i8", "decode_bf16", "mla", "dense",
-                                       "lm_head", "attn_layer", "calib"],
+                                       "lm_head", "attn_layer", "engine", "calib"],
                     help="run one workload and print its result dict (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (reference kernel for the "
@@ -468,9 +549,13 @@ def main():
         fn = dict(decode_i8=bench_decode_i8, prefill_i8=bench_prefill_i8,
                   decode_bf16=bench_decode_bf16, mla=bench_mla_decode,
                   dense=bench_dense_bf16, lm_head=bench_lm_head,
-                  attn_layer=bench_attn_layer)[args.only]
+                  attn_layer=bench_attn_layer, engine=None)[args.only]
         if args.only == "attn_layer":
             print(json.dumps({args.only: fn(None, args.steps, args.warmup)}, default=float),
+                  flush=True)
+            return
+        if args.only == "engine":
+            print(json.dumps({args.only: bench_engine(args.steps, args.warmup)}, default=float),
                   flush=True)
             return
         with mlamoe.Context(0) as ctx:
@@ -492,6 +577,7 @@ def main():
         with mlamoe.Context(0) as ctx:
             extra["lm_head_dsv2"] = bench_lm_head(ctx, args.steps, args.warmup)
         extra["attn_layer_dsv2"] = bench_attn_layer(None, args.steps, args.warmup)
+        extra["engine_dsv2"] = bench_engine(args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
     line = {

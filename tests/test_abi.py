@@ -41,3 +41,17 @@ def test_no_gpu_context_fails_loudly():
         pytest.skip("a GPU is present")
     with pytest.raises(mlamoe.MMError):
         mlamoe.Context(0)
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/include"),
+                    reason="the reference tree is not present here")
+def test_getp_shim_compiles_against_reference_headers():
+    """mla-moe_amd/shim/getp_mlamoe.c implements include/getp.h's warm_up /
+    inference / finish on the C-ABI; it must compile against the reference's
+    own headers (model.h, getp.h, tokenizer.h) with the reference's C flags."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run(["gcc", "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
+                        "-I/root/reference/include", "-I" + os.path.join(root, "include"),
+                        os.path.join(root, "mla-moe_amd", "shim", "getp_mlamoe.c")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
