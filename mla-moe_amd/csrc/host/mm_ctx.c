@@ -66,6 +66,8 @@ static const struct {
     [K_MLA_ROPE] = {"mm_mla_rope", MOD_MLA},
     [K_EMBED] = {"mm_embed", MOD_UTIL},
     [K_SWIGLU] = {"mm_swiglu", MOD_UTIL},
+    [K_GEMM_SKINNY] = {"mm_gemm_skinny", MOD_GEMM_BF16},
+    [K_SKINNY_REDUCE] = {"mm_skinny_reduce", MOD_GEMM_BF16},
 };
 
 /* ---- errors ------------------------------------------------------------- */

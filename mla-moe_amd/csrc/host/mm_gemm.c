@@ -2,10 +2,33 @@
  * (src/run.c:29-37) batched over T rows. */
 #include "mm_internal.h"
 
-size_t mm_gemm_bf16_ws_bytes(int T, int n_in, unsigned flags) {
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+/* Skinny-M plan: T <= MM_SKINNY_T rows and n_in a multiple of 64.  Blocks of
+ * MM_SKINNY_BN output columns; the K range splits until the grid has about one block
+ * per CU (partials summed by mm_skinny_reduce). */
+static int skinny_ok(int T, int n_in) { return T <= MM_SKINNY_T && n_in % 64 == 0; }
+
+static void skinny_plan(int d_out, int n_in, int *nsplit, int *kr) {
+    const int nb = (d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN, nk = n_in / 64;
+    int ns = (256 + nb - 1) / nb;
+    if (ns > nk) ns = nk;
+    if (ns < 1) ns = 1;
+    const int kc = (nk + ns - 1) / ns;          /* 64-input chunks per split */
+    *kr = 64 * kc;
+    *nsplit = (nk + kc - 1) / kc;
+}
+
+size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags) {
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
     const size_t xb = (size_t)T * ((n_in + 63) / 64 * 64) * 2;
-    return (split ? 2 : 1) * ((xb + 255) & ~(size_t)255);
+    size_t b = (split ? 2 : 1) * al256(xb);
+    if (skinny_ok(T, n_in)) {
+        int ns, kr;
+        skinny_plan(d_out, n_in, &ns, &kr);
+        if (ns > 1) b += al256((size_t)ns * T * d_out * 4);
+    }
+    return b;
 }
 
 int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
@@ -14,11 +37,25 @@ int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int 
     /* x as bf16 rows of a stride padded to 64 (zeros past n_in) */
     const int kp = (n_in + 63) / 64 * 64;
     const size_t xb = (size_t)T * kp * 2;
-    uint16_t *xh = (uint16_t *)ws, *xl = split ? (uint16_t *)(ws + ((xb + 255) & ~(size_t)255)) : NULL;
+    uint16_t *xh = (uint16_t *)ws, *xl = split ? (uint16_t *)(ws + al256(xb)) : NULL;
     mm_cvt_bf16_args ca = {x, xh, xl, T, n_in, kp, split};
     const size_t chunks = (size_t)T * kp / 8;
     int st;
     if ((st = mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca))) return st;
+    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
+    if (skinny_ok(T, n_in)) {
+        int ns, kr;
+        skinny_plan(d_out, n_in, &ns, &kr);
+        float *part = ns > 1 ? (float *)(ws + (split ? 2 : 1) * al256(xb)) : NULL;
+        mm_gemm_skinny_args k = {xh, xl, w, y, part, T, d_out, n_in, kp, ns, kr, acc};
+        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)((d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN),
+                            (unsigned)ns, 1, 256, 0, &k)))
+            return st;
+        if (ns == 1) return MM_OK;
+        mm_skinny_reduce_args r = {part, y, T, d_out, ns, acc};
+        const size_t n = (size_t)T * d_out, blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+        return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
+    }
     /* block tile columns: the widest of 128, 64, 32 that still gives 192
      * tiles (most of the 256 CUs), else 32 -- the projections of this path
      * have too few 128 x 128 tiles to fill the machine (measured per width) */
@@ -30,7 +67,7 @@ int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int 
             break;
         }
     const size_t nbx = ((size_t)d_out + bn - 1) / bn;
-    mm_gemm_bf16_args a = {xh, xl, w, y, T, d_out, n_in, kp, split, (flags & MM_MATMUL_ACCUMULATE) != 0, bn};
+    mm_gemm_bf16_args a = {xh, xl, w, y, T, d_out, n_in, kp, split, acc, bn};
     /* LDS ring: 4 stages (3 for the hi/lo split) of A hi [, A lo] (16 KB
      * each) and bn rows of B (128 B each); a 1-D grid of 8 XCD columns, each
      * with every row block of its column blocks (the kernel maps blocks to
@@ -72,6 +109,6 @@ int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, i
         return mm_gemv_launch(c, &a);
     }
     char *ws;
-    if ((st = mm_workspace(c, mm_gemm_bf16_ws_bytes(T, n_in, flags), (void **)&ws))) return st;
+    if ((st = mm_workspace(c, mm_gemm_bf16_ws_bytes(T, n_in, d_out, flags), (void **)&ws))) return st;
     return mm_gemm_bf16_ws(c, y, x, w, d_out, n_in, T, flags, ws);
 }

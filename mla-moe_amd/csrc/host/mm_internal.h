@@ -43,6 +43,8 @@ typedef enum {
     K_MLA_ROPE,
     K_EMBED,
     K_SWIGLU,
+    K_GEMM_SKINNY,
+    K_SKINNY_REDUCE,
     K_COUNT
 } mm_kernel_id;
 
@@ -118,8 +120,8 @@ int mm_launch(mm_ctx *ctx, mm_kernel_id id, unsigned gx, unsigned gy, unsigned g
 int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
 
 /* Dense bf16 GEMM (mm_matmul_bf16_dev) on a caller-provided workspace of at
- * least mm_gemm_bf16_ws_bytes(T, n_in, flags) bytes. */
-size_t mm_gemm_bf16_ws_bytes(int T, int n_in, unsigned flags);
+ * least mm_gemm_bf16_ws_bytes(T, n_in, d_out, flags) bytes. */
+size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags);
 int mm_gemm_bf16_ws(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
                     int T, unsigned flags, char *ws);
 

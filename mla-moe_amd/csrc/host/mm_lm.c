@@ -59,7 +59,7 @@ int mm_lm_head_dev(mm_ctx *c, int B, const float *x, const uint16_t *norm, float
                            : 0;                  /* GEMV blocks: 4 waves x 4 rows per turn */
     const size_t o_xb = 0, n_xb = gemv ? 0 : al256((size_t)B * hidden * 4);
     const size_t o_lg = o_xb + n_xb, n_lg = logits ? 0 : al256((size_t)B * vocab * 4);
-    const size_t o_gm = o_lg + n_lg, n_gm = gemv ? 0 : al256(mm_gemm_bf16_ws_bytes(B, hidden, 0));
+    const size_t o_gm = o_lg + n_lg, n_gm = gemv ? 0 : al256(mm_gemm_bf16_ws_bytes(B, hidden, vocab, 0));
     const size_t o_am = o_gm + n_gm;
     const size_t n_am = gemv ? 2 * al256((size_t)B * nb * 4) : argmax_ws(B, vocab);
     char *ws;

@@ -215,8 +215,10 @@ int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weight
      * and the GEMM staging */
     const size_t o_cp = 0, o_qa = al256((size_t)B * KVD * 4);
     const size_t o_xb = o_qa + al256((size_t)B * ql * 4);
-    size_t gw = mm_gemm_bf16_ws_bytes(B, H, 0);
-    if (ql && mm_gemm_bf16_ws_bytes(B, ql, 0) > gw) gw = mm_gemm_bf16_ws_bytes(B, ql, 0);
+    /* GEMM staging: the largest of the projections' needs */
+    size_t gw = mm_gemm_bf16_ws_bytes(B, H, KVD, 0), g2;
+    if ((g2 = mm_gemm_bf16_ws_bytes(B, H, ql ? ql : QD, 0)) > gw) gw = g2;
+    if (ql && (g2 = mm_gemm_bf16_ws_bytes(B, ql, QD, 0)) > gw) gw = g2;
     const size_t o_gm = o_xb + (gemv ? 0 : al256((size_t)B * H * 4));
     char *ws;
     if ((st = mm_workspace(c, o_gm + (gemv ? 0 : gw), (void **)&ws))) return st;

@@ -303,6 +303,27 @@ typedef struct {
     int bn;                  /* block tile columns: 128, 64 or 32 */
 } mm_gemm_bf16_args;
 
+/* Skinny-M GEMM (T <= MM_SKINNY_T rows of x): block (MM_SKINNY_BN output columns,
+ * one K split); partials [nsplit, T, d_out] when nsplit > 1. */
+#define MM_SKINNY_T 64
+#ifndef MM_SKINNY_BN
+#define MM_SKINNY_BN 64           /* output columns per block (4 waves x 16) */
+#endif
+typedef struct {
+    const uint16_t *xh, *xl; /* [T, kp] converted x (xl: split mode, else NULL) */
+    const uint16_t *w;       /* [d_out, n_in] */
+    float *y;                /* [T, d_out], written when nsplit == 1 */
+    float *part;             /* [nsplit, T, d_out] when nsplit > 1 */
+    int T, d_out, n_in, kp, nsplit, kr;   /* kr: inputs per split, a multiple of 64 */
+    int accumulate;
+} mm_gemm_skinny_args;
+
+typedef struct {
+    const float *part;       /* [nsplit, T, d_out] */
+    float *y;                /* [T, d_out] */
+    int T, d_out, nsplit, accumulate;
+} mm_skinny_reduce_args;
+
 /* ---- LM head (final RMSNorm, logits, greedy argmax) ------------------------- */
 #define MM_LM_NB 4                /* tokens served by the logits GEMV (more: the MFMA GEMM) */
 #define MM_LM_HMAX 2048           /* hidden sizes served by the logits GEMV */

@@ -227,3 +227,151 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args
         else gemm_block<false, 32>(a, glds);
     }
 }
+
+/* ---- skinny-M GEMM: T <= 64 rows of x (batched decode) ------------------------
+ *
+ * Every weight row is read from HBM once per K split.  Block = 4 waves x
+ * 16 SK_WC output columns; a wave holds C[64 tokens][16 SK_WC columns] (4
+ * token groups x SK_WC column groups of v_mfma_f32_16x16x32_bf16, x as the
+ * A operand -- each x fragment read from LDS feeds SK_WC MFMAs -- and W as
+ * the B operand).  The
+ * W fragments of the block's K range stream straight into registers, SK_D
+ * 64-input chunks ahead of their MFMAs; x (hi and lo) is loaded two chunks
+ * ahead into registers and staged into LDS one 64-input chunk at a time
+ * (double-buffered; rows padded to 72 bf16 against bank conflicts; token
+ * rows past T read row T - 1 and are not stored).  With
+ * nsplit > 1 the K range is split over grid.y and mm_skinny_reduce sums the
+ * partials in split order. */
+#ifndef SK_D
+#define SK_D 4                       /* chunks of W in flight per wave */
+#endif
+#define SK_WC (MM_SKINNY_BN / 64)   /* 16-column groups per wave */
+#define SK_ROW 72                    /* LDS row stride (bf16) of a staged x chunk */
+#define SK_STAGE (2 * 64 * SK_ROW)   /* bf16 per stage: hi rows then lo rows */
+
+template <bool SPLIT>
+__device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*xs)[SK_STAGE]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * (64 * SK_WC) + wave * (16 * SK_WC);
+    const int kb = blockIdx.y * a.kr;
+    const int nch = (min(a.n_in, kb + a.kr) - kb) / 64;    /* 64-input chunks of this split */
+    const uint16_t *wrow[SK_WC];
+#pragma unroll
+    for (int j = 0; j < SK_WC; j++) {
+        const int col = min(n0 + 16 * j + (lane & 15), a.d_out - 1);   /* past d_out: not stored */
+        wrow[j] = a.w + (size_t)col * a.n_in + kb + 8 * (lane >> 4);
+    }
+
+    /* x chunk c -> registers (two slots: chunks are loaded two ahead of their
+     * use): thread t copies 16 B pieces p = t + 256 j of [hi rows | lo rows]
+     * (64 rows x 8 pieces each) */
+    constexpr int XJ = SPLIT ? 4 : 2;
+    u16x8 xr[2][XJ];
+    auto load_x = [&](int slot, int c) {
+#pragma unroll
+        for (int j = 0; j < XJ; j++) {
+            const int p = tid + 256 * j, half = p >> 9, r = (p >> 3) & 63, q = p & 7;
+            const uint16_t *src = (half ? a.xl : a.xh) + (size_t)min(r, a.T - 1) * a.kp + kb + 64 * c + 8 * q;
+            xr[slot][j] = *(const u16x8 *)src;
+        }
+    };
+    auto store_x = [&](int slot, int st) {
+#pragma unroll
+        for (int j = 0; j < XJ; j++) {
+            const int p = tid + 256 * j, half = p >> 9, r = (p >> 3) & 63, q = p & 7;
+            *(u16x8 *)&xs[st][(half * 64 + r) * SK_ROW + 8 * q] = xr[slot][j];
+        }
+    };
+    bf16x8 wr[SK_D][SK_WC][2];
+    auto load_w = [&](int slot, int c) {
+        const int cc = min(c, nch - 1);                     /* past the end: reload the last */
+#pragma unroll
+        for (int j = 0; j < SK_WC; j++)
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+                wr[slot][j][s] = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(
+                                                                (const u16x8 *)(wrow[j] + 64 * cc + 32 * s)));
+    };
+#pragma unroll
+    for (int d = 0; d < SK_D; d++) load_w(d, d);
+    load_x(0, 0);
+    if (nch > 1) load_x(1, 1);
+    store_x(0, 0);
+    __syncthreads();
+
+    f32x4 acc[SK_WC][4];
+#pragma unroll
+    for (int j = 0; j < SK_WC; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) acc[j][g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    static_assert(SK_D % 2 == 0, "the x slots alternate with the chunk parity");
+    for (int c0 = 0; c0 < nch; c0 += SK_D) {
+#pragma unroll
+        for (int d = 0; d < SK_D; d++) {
+            const int c = c0 + d;
+            /* slot d & 1 held chunk c (in LDS since the last barrier): refill it with c + 2 */
+            if (c + 2 < nch) load_x(d & 1, c + 2);
+            if (c < nch) {
+                const uint16_t *xb = xs[d & 1];
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    const int ko = 32 * s + 8 * (lane >> 4);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int r = 16 * g + (lane & 15);
+                        const bf16x8 ah = *(const bf16x8 *)&xb[r * SK_ROW + ko];
+                        bf16x8 al;
+                        if (SPLIT) al = *(const bf16x8 *)&xb[(64 + r) * SK_ROW + ko];
+#pragma unroll
+                        for (int j = 0; j < SK_WC; j++) {
+                            acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wr[d][j][s], acc[j][g], 0, 0, 0);
+                            if (SPLIT)
+                                acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wr[d][j][s], acc[j][g], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            load_w(d, c + SK_D);
+            if (c + 1 < nch) store_x((d + 1) & 1, (d + 1) & 1);
+            __syncthreads();
+        }
+    }
+    /* C[token 16 g + 4 (l / 16) + i][column n0 + 16 j + l % 16] */
+#pragma unroll
+    for (int j = 0; j < SK_WC; j++) {
+        const int n = n0 + 16 * j + (lane & 15);
+        if (n >= a.d_out) continue;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * g + 4 * (lane >> 4) + i;
+                if (t >= a.T) continue;
+                if (a.nsplit > 1) {
+                    a.part[((size_t)blockIdx.y * a.T + t) * a.d_out + n] = acc[j][g][i];
+                } else {
+                    float *y = a.y + (size_t)t * a.d_out + n;
+                    *y = a.accumulate ? *y + acc[j][g][i] : acc[j][g][i];
+                }
+            }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny(mm_gemm_skinny_args a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][SK_STAGE];
+    if (a.xl)
+        skinny<true>(a, xs);
+    else
+        skinny<false>(a, xs);
+}
+
+/* y (+)= sum over splits s = 0 .. nsplit-1 of part[s], in that order. */
+extern "C" __global__ __launch_bounds__(256) void mm_skinny_reduce(mm_skinny_reduce_args a) {
+    const size_t n = (size_t)a.T * a.d_out;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = a.part[i];
+        for (int s = 1; s < a.nsplit; s++) v += a.part[(size_t)s * n + i];
+        a.y[i] = a.accumulate ? a.y[i] + v : v;
+    }
+}

@@ -35,7 +35,12 @@ def test_matmul_golden(ctx, oracle):
 
 @pytest.mark.parametrize("T,d_out,n_in", [(1, 64, 2048), (37, 100, 264), (512, 576, 2048),
                                           (512, 4096, 512), (70, 3072, 2048),
-                                          (1024, 3072, 136)])   # 128-column tiles
+                                          (1024, 3072, 136),    # 128-column tiles
+                                          # skinny-M GEMM (5 <= T <= 64, n_in % 64 == 0):
+                                          # one split, many splits, ragged columns
+                                          (64, 102400 // 16, 2048), (5, 3072, 2048),
+                                          (33, 576, 2048), (17, 100, 64), (64, 2048, 10944),
+                                          (8, 130, 1408)])
 def test_matmul_shapes(ctx, oracle, T, d_out, n_in):
     print(f"matmul T={T} d_out={d_out} n_in={n_in}", flush=True)
     rng = np.random.default_rng(T + d_out)
@@ -51,6 +56,17 @@ def test_matmul_shapes(ctx, oracle, T, d_out, n_in):
     y0 = synth.normal_f32(rng, (T, d_out))
     got_acc = ctx.matmul(x, w, mlamoe.MM_MATMUL_ACCUMULATE, y0=y0)
     assert max_abs_rel(got_acc - y0, ref) < 1e-5
+
+
+def test_skinny_integer_exact(ctx):
+    """The skinny-M path with integer-valued operands (every summation order
+    exact): bit for bit, with and without splits of K."""
+    rng = np.random.default_rng(4)
+    for T, d_out, n_in in ((64, 640, 256), (7, 96, 4096)):
+        w = rng.integers(-8, 9, size=(d_out, n_in)).astype(np.float32)
+        x = rng.integers(-8, 9, size=(T, n_in)).astype(np.float32)
+        got = ctx.matmul(x, synth.bf16_from_f32(w))
+        assert np.array_equal(got, x @ w.T), (T, d_out, n_in)
 
 
 def test_matmul_integer_exact(ctx):
