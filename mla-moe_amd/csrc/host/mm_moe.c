@@ -14,7 +14,7 @@
 #define BF16_NT_MAX 8         /* tokens per pass of the bf16 GEMV path */
 #define GU_ROWS_PER_BLOCK 4   /* one gate/up row pair per wave */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
-#define ROUTER_TOKENS_PER_BLOCK 8
+#define ROUTER_TOKENS_PER_BLOCK (4 * MM_ROUTER_TPW)
 
 void mm_moe_release(mm_ctx *c) {
     if (!c->layers) return;

@@ -10,6 +10,10 @@
 /* Router: logits (sequential fp32 dot products in the reference's order, or
  * caller-supplied), softmax/sigmoid, greedy top-k with the lowest-index tie
  * rule, optional normalisation and scaling. */
+#ifndef MM_ROUTER_TPW
+#define MM_ROUTER_TPW 1           /* router: tokens per wave (4 waves per block) */
+#endif
+
 typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */
     const uint16_t *wg;      /* [E, H] router weight, bf16 (checkpoint layout) */

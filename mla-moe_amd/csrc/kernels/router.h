@@ -22,7 +22,6 @@
 #include "common.h"
 
 #define MM_KMAX 16
-#define MM_ROUTER_TPW 2
 #define MM_ROUTER_WAVES 4
 #define MM_ROUTER_THREADS (MM_ROUTER_WAVES * MM_WAVE)
 #define MM_ROUTER_CHUNK_FLOATS 8192   /* router-weight chunk: HC rows x E experts */
