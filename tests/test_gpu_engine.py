@@ -78,6 +78,22 @@ def test_engine_generate_continuous_batching(oracle):
             eng.close()
 
 
+def test_engine_step_errors():
+    """Out-of-range batch sizes and positions are rejected before any launch."""
+    c, m, g = engine_case()
+    with mlamoe.Context(0) as ctx:
+        eng = Engine.from_host(ctx, c, m, g["inv"], max_batch=2, max_seq=8)
+        try:
+            with pytest.raises(mlamoe.MMError, match="outside"):
+                eng.step(np.zeros(3, np.int32), np.zeros(3, np.int32))
+            with pytest.raises(mlamoe.MMError, match="pos"):
+                eng.step(np.zeros(1, np.int32), np.full(1, 8, np.int32))
+            nxt, _ = eng.step(np.zeros(2, np.int32), np.zeros(2, np.int32))   # still usable
+            assert nxt.shape == (2,)
+        finally:
+            eng.close()
+
+
 def test_engine_errors():
     L = mlamoe.lib()
     with mlamoe.Context(0) as ctx:
