@@ -27,10 +27,12 @@ class Engine:
     def from_host(cls, ctx, c, m, inv_freq, max_batch, max_seq, int8=False):
         """c: dict of Config fields (n_layers, first_dense, H, NH, QKN, QKR,
         KVL, VHD, dense_inter, E, n_shared, K, I, vocab, router_sigmoid,
-        norm_topk, routed_scaling, rms_eps); m: synth.model()."""
+        norm_topk, routed_scaling, rms_eps, and optionally q_lora,
+        interleaved); m: synth.model()."""
         L = c["n_layers"]
         ctx.mla_init(c["NH"], c["QKN"], c["QKR"], c["KVL"], c["VHD"], n_layers=L)
-        ctx.mla_front_init(c["H"], inv_freq, 0, c["rms_eps"], 1e-6, 0)
+        ctx.mla_front_init(c["H"], inv_freq, c.get("q_lora", 0), c["rms_eps"], 1e-6,
+                           c.get("interleaved", 0))
         if c["first_dense"] < L:
             ctx.moe_init(c["H"], c["E"], c["n_shared"], c["K"], c["I"], c["router_sigmoid"],
                          c["norm_topk"], c["routed_scaling"], n_layers=L)

@@ -84,7 +84,7 @@ def attn_layer(seed: int, H: int, NH: int, QKN: int, QKR: int, KVL: int, VHD: in
 
 def model(seed: int, n_layers: int, first_dense: int, H: int, NH: int, QKN: int, QKR: int,
           KVL: int, VHD: int, dense_inter: int, E: int, I: int, n_shared: int, vocab: int,
-          gate_bias: bool = False) -> dict:
+          gate_bias: bool = False, q_lora: int = 0) -> dict:
     """A whole decoder's bf16 weights with DeepSeek-V2's layout: embed
     [vocab, H], per layer an attn_layer() dict plus post_norm and either a
     dense MLP (dgate/dup [dense_inter, H], ddown [H, dense_inter]) for the
@@ -96,7 +96,7 @@ def model(seed: int, n_layers: int, first_dense: int, H: int, NH: int, QKN: int,
              lm_head=normal_bf16(rng, (vocab, H), 0.02), layers=[])
     for l in range(n_layers):
         s = seed + 100 * (l + 1)
-        lw = attn_layer(s, H, NH, QKN, QKR, KVL, VHD)
+        lw = attn_layer(s, H, NH, QKN, QKR, KVL, VHD, q_lora)
         r = np.random.default_rng(s + 1)
         lw["post_norm"] = bf16_from_f32(1.0 + normal_f32(r, (H,), 0.1))
         if l < first_dense:

@@ -484,7 +484,7 @@ def model_logits(c, m, tokens, inv):
     routed_scaling, rms_eps), m: synth.model().  Returns [n, vocab]."""
     H, NH, QKN, QKR, KVL, VHD = (c[k] for k in ("H", "NH", "QKN", "QKR", "KVL", "VHD"))
     KVD, eps, n = KVL + QKR, c["rms_eps"], len(tokens)
-    fc = front_cfg(H, NH, QKN, QKR, KVL, 0, eps, 1e-6, 0)
+    fc = front_cfg(H, NH, QKN, QKR, KVL, c.get("q_lora", 0), eps, 1e-6, c.get("interleaved", 0))
     mc = moe_cfg(H, c["E"], c["n_shared"], c["K"], c["I"], c["router_sigmoid"], c["norm_topk"],
                  c["routed_scaling"])
     caches = [np.zeros((n, KVD), np.float32) for _ in m["layers"]]
@@ -515,12 +515,14 @@ def model_logits(c, m, tokens, inv):
 class RefModelSpec(C.Structure):
     _fields_ = [(k, C.c_int) for k in ("n_layers", "first_k_dense", "H", "NH", "QKN", "QKR",
                                         "KVL", "VHD", "dense_inter", "E", "n_shared", "K", "I",
-                                        "vocab", "router_sigmoid", "norm_topk", "max_seq")] + \
+                                        "vocab", "router_sigmoid", "norm_topk", "max_seq",
+                                        "q_lora", "interleaved")] + \
         [("routed_scaling", C.c_float), ("rms_eps", C.c_float), ("inv_freq", _f32p),
          ("embed", _u16p), ("final_norm", _u16p), ("lm_head", _u16p)] + \
         [(k, C.POINTER(_u16p)) for k in ("in_norm", "q_proj", "kv_a", "kv_a_norm", "kv_b",
                                          "o_proj", "post_norm", "dgate", "dup", "ddown",
-                                         "moe_gate", "eg", "eu", "ed", "sg", "su", "sd")] + \
+                                         "moe_gate", "eg", "eu", "ed", "sg", "su", "sd",
+                                         "q_a_proj", "q_a_norm", "q_b_proj")] + \
         [("moe_bias", C.POINTER(_f32p))]
 
 
@@ -548,12 +550,14 @@ def ref_forward_tokens(c, m, tokens, inv):
     inv = c32(inv)
     spec = RefModelSpec(L, c["first_dense"], c["H"], c["NH"], c["QKN"], c["QKR"], c["KVL"], c["VHD"],
                         c["dense_inter"], c["E"], c["n_shared"], c["K"], c["I"], c["vocab"],
-                        c["router_sigmoid"], c["norm_topk"], max(n, 1), c["routed_scaling"],
+                        c["router_sigmoid"], c["norm_topk"], max(n, 1), c.get("q_lora", 0),
+                        c.get("interleaved", 0), c["routed_scaling"],
                         c["rms_eps"], _p(inv, _f32p), _p(m["embed"], _u16p),
                         _p(m["final_norm"], _u16p), _p(m["lm_head"], _u16p),
                         *[arr(k) for k in ("in_norm", "q_proj", "kv_a", "kv_a_norm", "kv_b",
                                            "o_proj", "post_norm", "dgate", "dup", "ddown",
-                                           "moe_gate", "eg", "eu", "ed", "sg", "su", "sd")],
+                                           "moe_gate", "eg", "eu", "ed", "sg", "su", "sd",
+                                           "q_a_proj", "q_a_norm", "q_b_proj")],
                         bias)
     out = np.empty((n, c["vocab"]), np.float32)
     tk = np.ascontiguousarray(tokens, np.int32)

@@ -36,18 +36,19 @@ int ref_config_rope(const char *model_dir, float *inv, int *ints, float *flts) {
 
 /* A small model for whole-step golden vectors: n_layers layers, the first
  * first_k_dense of them dense, the rest MoE (experts contiguous per layer:
- * eg/eu [E, I, H], ed [E, H, I]); q_proj only (no q-LoRA).  Pointer arrays
- * are indexed by layer (NULL where a layer has no such tensor). */
+ * eg/eu [E, I, H], ed [E, H, I]); q_proj, or with q_lora > 0 the q-LoRA
+ * chain; RoPE layout `interleaved`.  Pointer arrays are indexed by layer
+ * (NULL where a layer has no such tensor). */
 typedef struct {
     int n_layers, first_k_dense, H, NH, QKN, QKR, KVL, VHD, dense_inter, E, n_shared, K, I,
-        vocab, router_sigmoid, norm_topk, max_seq;
+        vocab, router_sigmoid, norm_topk, max_seq, q_lora, interleaved;
     float routed_scaling, rms_eps;
     const float *inv_freq;
     const uint16_t *embed, *final_norm, *lm_head;
     const uint16_t *const *in_norm, *const *q_proj, *const *kv_a, *const *kv_a_norm,
         *const *kv_b, *const *o_proj, *const *post_norm, *const *dgate, *const *dup,
         *const *ddown, *const *moe_gate, *const *eg, *const *eu, *const *ed, *const *sg,
-        *const *su, *const *sd;
+        *const *su, *const *sd, *const *q_a_proj, *const *q_a_norm, *const *q_b_proj;
     const float *const *moe_bias;
 } ref_model_spec;
 
@@ -79,6 +80,8 @@ int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float 
     c->router_sigmoid = m->router_sigmoid;
     c->norm_topk = m->norm_topk;
     c->routed_scaling = m->routed_scaling;
+    c->q_lora_rank = m->q_lora;
+    c->rope_interleaved = m->interleaved;
     ModelWeights *w = &t.weights;
 #define PA(field) w->field = calloc((size_t)L, sizeof(*w->field))
     PA(q_proj); PA(q_a_proj); PA(q_b_proj); PA(kv_a_proj); PA(W_UK); PA(W_UV); PA(o_proj);
@@ -91,7 +94,12 @@ int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float 
     w->lm_head = (bf16_t *)m->lm_head;
     const size_t ne = (size_t)m->I * m->H;
     for (int l = 0; l < L; l++) {
-        w->q_proj[l] = (bf16_t *)m->q_proj[l];
+        w->q_proj[l] = m->q_proj ? (bf16_t *)m->q_proj[l] : NULL;
+        if (m->q_lora > 0) {
+            w->q_a_proj[l] = (bf16_t *)m->q_a_proj[l];
+            w->q_a_layernorm[l] = (bf16_t *)m->q_a_norm[l];
+            w->q_b_proj[l] = (bf16_t *)m->q_b_proj[l];
+        }
         w->kv_a_proj[l] = (bf16_t *)m->kv_a[l];
         w->kv_a_layernorm[l] = (bf16_t *)m->kv_a_norm[l];
         w->W_UK[l] = (bf16_t *)m->kv_b[l];                              /* model_load.c:80-86 */

@@ -64,18 +64,20 @@ def front_case(g, name):
                 x=g[f"{name}_x"], w=w, cache_in=cache_in)
 
 
-def engine_case():
-    """The engine golden's model (tests/golden/engine.npz), rebuilt from its
-    seed and checked against the stored checksums: (config dict, model, npz)."""
+def engine_case(name="dsv2"):
+    """One engine golden model (tests/golden/engine.npz: "dsv2" or "glm"),
+    rebuilt from its seed and checked against the stored checksums:
+    (config dict, model, {tokens, inv, logits})."""
     sys.path.insert(0, GOLDEN)
-    from make_golden import ENGINE_CFG, engine_model
+    from make_golden import ENGINE_CASES, engine_model
     from mlamoe import synth
     g = load_golden("engine.npz")
-    m = engine_model(int(g["seed"]))
+    m = engine_model(name)
     for k in ("embed", "final_norm", "lm_head"):
-        assert synth.checksum_u16(m[k]) == int(g[f"sum_{k}"]), k
+        assert synth.checksum_u16(m[k]) == int(g[f"{name}_sum_{k}"]), k
     for l, lw in enumerate(m["layers"]):
         for k, v in lw.items():
             if v is not None and v.dtype == np.uint16:
-                assert synth.checksum_u16(v) == int(g[f"sum_l{l}_{k}"]), (l, k)
-    return dict(ENGINE_CFG), m, g
+                assert synth.checksum_u16(v) == int(g[f"{name}_sum_l{l}_{k}"]), (l, k)
+    return (dict(ENGINE_CASES[name][0]), m,
+            {k: g[f"{name}_{k}"] for k in ("tokens", "inv", "logits")})

@@ -328,31 +328,38 @@ def gen_mla_front():
 ENGINE_CFG = dict(n_layers=3, first_dense=1, H=256, NH=2, QKN=32, QKR=64, KVL=512, VHD=32,
                   dense_inter=192, E=8, n_shared=1, K=2, I=128, vocab=384, router_sigmoid=0,
                   norm_topk=0, routed_scaling=1.0, rms_eps=1e-6)
+# GLM-style: q-LoRA, split-half RoPE, sigmoid router with a score bias,
+# normalised top-k, routed scaling, eps 1e-5
+ENGINE_GLM_CFG = dict(ENGINE_CFG, NH=4, q_lora=96, interleaved=1, router_sigmoid=1, norm_topk=1,
+                      routed_scaling=1.8, rms_eps=1e-5, K=3)
+ENGINE_CASES = {"dsv2": (ENGINE_CFG, 900, False), "glm": (ENGINE_GLM_CFG, 950, True)}
 
 
-def engine_model(seed):
-    c = ENGINE_CFG
+def engine_model(name):
+    c, seed, bias = ENGINE_CASES[name]
     return synth.model(seed, c["n_layers"], c["first_dense"], c["H"], c["NH"], c["QKN"], c["QKR"],
                        c["KVL"], c["VHD"], c["dense_inter"], c["E"], c["I"], c["n_shared"],
-                       c["vocab"])
+                       c["vocab"], gate_bias=bias, q_lora=c.get("q_lora", 0))
 
 
 def gen_engine():
     """Whole decode steps of the reference's forward_absorbed (run.c:379-501)
-    on a three-layer model (dense layer 0, MoE layers 1-2), teacher forced on
-    a token sequence: the logits at every position."""
-    seed = 900
-    m = engine_model(seed)
-    inv = O.rope_inv_freq(ENGINE_CFG["QKR"], 10000.0)
-    tokens = np.random.default_rng(901).integers(0, ENGINE_CFG["vocab"], 16).astype(np.int32)
-    logits = O.ref_forward_tokens(ENGINE_CFG, m, tokens, inv)
-    sums = {f"sum_{k}": np.uint64(synth.checksum_u16(m[k])) for k in ("embed", "final_norm", "lm_head")}
-    for l, lw in enumerate(m["layers"]):
-        for k, v in lw.items():
-            if v is not None and v.dtype == np.uint16:
-                sums[f"sum_l{l}_{k}"] = np.uint64(synth.checksum_u16(v))
-    np.savez_compressed(os.path.join(OUT, "engine.npz"), seed=np.int64(seed), tokens=tokens,
-                        inv=inv, logits=logits, **sums)
+    on three-layer models (dense layer 0, MoE layers 1-2) of both flavours,
+    teacher forced on a token sequence: the logits at every position."""
+    d = {}
+    for name, (c, seed, _) in ENGINE_CASES.items():
+        m = engine_model(name)
+        inv = O.rope_inv_freq(c["QKR"], 10000.0)
+        tokens = np.random.default_rng(seed + 1).integers(0, c["vocab"], 16).astype(np.int32)
+        d[f"{name}_tokens"], d[f"{name}_inv"] = tokens, inv
+        d[f"{name}_logits"] = O.ref_forward_tokens(c, m, tokens, inv)
+        for k in ("embed", "final_norm", "lm_head"):
+            d[f"{name}_sum_{k}"] = np.uint64(synth.checksum_u16(m[k]))
+        for l, lw in enumerate(m["layers"]):
+            for k, v in lw.items():
+                if v is not None and v.dtype == np.uint16:
+                    d[f"{name}_sum_l{l}_{k}"] = np.uint64(synth.checksum_u16(v))
+    np.savez_compressed(os.path.join(OUT, "engine.npz"), **d)
 
 
 GENERATORS = dict(engine=lambda: gen_engine(), mla_front=lambda: gen_mla_front(), matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),

@@ -21,14 +21,16 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
+@pytest.mark.parametrize("name", ["dsv2", "glm"])
 @pytest.mark.parametrize("int8", [False, True])
-def test_engine_teacher_forced_logits(int8):
+def test_engine_teacher_forced_logits(name, int8):
     """B = 1 (GEMV projections) and B = 6 slots (MFMA GEMMs) on the same
     token sequence at once, bf16 and int8 experts (measured 2.5e-4 and
-    6.7e-4 of the reference)."""
-    c, m, g = engine_case()
+    6.7e-4 of the reference for the DeepSeek-V2 flavour); the GLM flavour
+    adds q-LoRA, split-half RoPE and the sigmoid router with bias."""
+    c, m, g = engine_case(name)
     toks, ref = g["tokens"], g["logits"]
-    print(f"engine teacher forced int8={int8}", flush=True)
+    print(f"engine teacher forced {name} int8={int8}", flush=True)
     with mlamoe.Context(0) as ctx:
         eng = Engine.from_host(ctx, c, m, g["inv"], max_batch=6, max_seq=32, int8=int8)
         try:

@@ -252,12 +252,15 @@ def test_rope_against_reference_random(oracle):
 
 # ---- whole decode steps (engine.npz) -----------------------------------------
 
-def test_model_logits_golden(oracle):
+@pytest.mark.parametrize("name", ["dsv2", "glm"])
+def test_model_logits_golden(oracle, name):
     """The oracle's composition of a decode step (front, absorbed chain,
     o_proj, dense / MoE FFN, final norm, lm_head) equals the reference's
     forward_absorbed bit for bit at every position of a teacher-forced
-    sequence on a dense + MoE model."""
+    sequence on a dense + MoE model, in the DeepSeek-V2 flavour and the GLM
+    one (q-LoRA, split-half RoPE, sigmoid router with bias, normalised and
+    scaled top-k)."""
     from conftest import engine_case
-    c, m, g = engine_case()
+    c, m, g = engine_case(name)
     lg = oracle.model_logits(c, m, g["tokens"], g["inv"])
     assert np.array_equal(lg.view(np.uint32), g["logits"].view(np.uint32))
