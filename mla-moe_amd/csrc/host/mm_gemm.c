@@ -20,42 +20,41 @@ static void skinny_plan(int d_out, int n_in, int *nsplit, int *kr) {
 }
 
 size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags) {
-    const int split = (flags & MM_MATMUL_X_BF16) == 0;
-    const size_t xb = (size_t)T * ((n_in + 63) / 64 * 64) * 2;
-    size_t b = (split ? 2 : 1) * al256(xb);
-    if (skinny_ok(T, n_in)) {
+    if (skinny_ok(T, n_in)) {                    /* only the split partials */
         int ns, kr;
         skinny_plan(d_out, n_in, &ns, &kr);
-        if (ns > 1) b += al256((size_t)ns * T * d_out * 4);
+        return ns > 1 ? al256((size_t)ns * T * d_out * 4) : 256;
     }
-    return b;
+    const int split = (flags & MM_MATMUL_X_BF16) == 0;
+    const size_t xb = (size_t)T * ((n_in + 63) / 64 * 64) * 2;
+    return (split ? 2 : 1) * al256(xb);
 }
 
 int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
                     int T, unsigned flags, char *ws) {
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
+    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
+    int st;
+    if (skinny_ok(T, n_in)) {
+        /* fp32 x converted while staged; ws holds the split partials */
+        int ns, kr;
+        skinny_plan(d_out, n_in, &ns, &kr);
+        mm_gemm_skinny_args k = {x, w, y, (float *)ws, T, d_out, n_in, ns, kr, split, acc};
+        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)((d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN),
+                            (unsigned)ns, 1, 256, 0, &k)))
+            return st;
+        if (ns == 1) return MM_OK;
+        mm_skinny_reduce_args r = {(float *)ws, y, T, d_out, ns, acc};
+        const size_t n = (size_t)T * d_out, blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+        return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
+    }
     /* x as bf16 rows of a stride padded to 64 (zeros past n_in) */
     const int kp = (n_in + 63) / 64 * 64;
     const size_t xb = (size_t)T * kp * 2;
     uint16_t *xh = (uint16_t *)ws, *xl = split ? (uint16_t *)(ws + al256(xb)) : NULL;
     mm_cvt_bf16_args ca = {x, xh, xl, T, n_in, kp, split};
     const size_t chunks = (size_t)T * kp / 8;
-    int st;
     if ((st = mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca))) return st;
-    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
-    if (skinny_ok(T, n_in)) {
-        int ns, kr;
-        skinny_plan(d_out, n_in, &ns, &kr);
-        float *part = ns > 1 ? (float *)(ws + (split ? 2 : 1) * al256(xb)) : NULL;
-        mm_gemm_skinny_args k = {xh, xl, w, y, part, T, d_out, n_in, kp, ns, kr, acc};
-        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)((d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN),
-                            (unsigned)ns, 1, 256, 0, &k)))
-            return st;
-        if (ns == 1) return MM_OK;
-        mm_skinny_reduce_args r = {part, y, T, d_out, ns, acc};
-        const size_t n = (size_t)T * d_out, blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
-        return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
-    }
     /* block tile columns: the widest of 128, 64, 32 that still gives 192
      * tiles (most of the 256 CUs), else 32 -- the projections of this path
      * have too few 128 x 128 tiles to fill the machine (measured per width) */

@@ -314,11 +314,12 @@ typedef struct {
 #define MM_SKINNY_BN 64           /* output columns per block (4 waves x 16) */
 #endif
 typedef struct {
-    const uint16_t *xh, *xl; /* [T, kp] converted x (xl: split mode, else NULL) */
+    const float *x;          /* [T, n_in] fp32, converted while staged */
     const uint16_t *w;       /* [d_out, n_in] */
     float *y;                /* [T, d_out], written when nsplit == 1 */
     float *part;             /* [nsplit, T, d_out] when nsplit > 1 */
-    int T, d_out, n_in, kp, nsplit, kr;   /* kr: inputs per split, a multiple of 64 */
+    int T, d_out, n_in, nsplit, kr;   /* kr: inputs per split, a multiple of 64 */
+    int split;               /* 1: x as a bf16 hi/lo pair; 0: x truncated to bf16 */
     int accumulate;
 } mm_gemm_skinny_args;
 

@@ -236,10 +236,11 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args
  * A operand -- each x fragment read from LDS feeds SK_WC MFMAs -- and W as
  * the B operand).  The
  * W fragments of the block's K range stream straight into registers, SK_D
- * 64-input chunks ahead of their MFMAs; x (hi and lo) is loaded two chunks
- * ahead into registers and staged into LDS one 64-input chunk at a time
- * (double-buffered; rows padded to 72 bf16 against bank conflicts; token
- * rows past T read row T - 1 and are not stored).  With
+ * 64-input chunks ahead of their MFMAs; fp32 x is loaded two chunks ahead
+ * into registers and staged into LDS as bf16 (hi and lo) one 64-input chunk
+ * at a time, so no separate conversion pass runs (double-buffered; rows
+ * padded to 72 bf16 against bank conflicts; token rows past T read row
+ * T - 1 and are not stored).  With
  * nsplit > 1 the K range is split over grid.y and mm_skinny_reduce sums the
  * partials in split order. */
 #ifndef SK_D
@@ -262,24 +263,37 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
         wrow[j] = a.w + (size_t)col * a.n_in + kb + 8 * (lane >> 4);
     }
 
-    /* x chunk c -> registers (two slots: chunks are loaded two ahead of their
-     * use): thread t copies 16 B pieces p = t + 256 j of [hi rows | lo rows]
-     * (64 rows x 8 pieces each) */
-    constexpr int XJ = SPLIT ? 4 : 2;
-    u16x8 xr[2][XJ];
+    /* x chunk c (fp32) -> registers, two slots: chunks are loaded two ahead
+     * of their use.  Thread t holds the 16 B pieces p = t + 256 j (64 rows x
+     * 16 pieces); staging converts them to bf16 -- the hi/lo pair of
+     * mm_cvt_bf16 (RNE hi, RNE of the remainder) or the truncation -- and
+     * writes hi rows then lo rows. */
+    f32x4 xr[2][4];
     auto load_x = [&](int slot, int c) {
 #pragma unroll
-        for (int j = 0; j < XJ; j++) {
-            const int p = tid + 256 * j, half = p >> 9, r = (p >> 3) & 63, q = p & 7;
-            const uint16_t *src = (half ? a.xl : a.xh) + (size_t)min(r, a.T - 1) * a.kp + kb + 64 * c + 8 * q;
-            xr[slot][j] = *(const u16x8 *)src;
+        for (int j = 0; j < 4; j++) {
+            const int p = tid + 256 * j, r = p >> 4, q = p & 15;
+            xr[slot][j] = *(const f32x4 *)(a.x + (size_t)min(r, a.T - 1) * a.n_in + kb + 64 * c + 4 * q);
         }
     };
     auto store_x = [&](int slot, int st) {
 #pragma unroll
-        for (int j = 0; j < XJ; j++) {
-            const int p = tid + 256 * j, half = p >> 9, r = (p >> 3) & 63, q = p & 7;
-            *(u16x8 *)&xs[st][(half * 64 + r) * SK_ROW + 8 * q] = xr[slot][j];
+        for (int j = 0; j < 4; j++) {
+            const int p = tid + 256 * j, r = p >> 4, q = p & 15;
+            typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+            u16x4 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v = xr[slot][j][e];
+                if (SPLIT) {
+                    hi[e] = rne16(v);
+                    lo[e] = rne16(v - bf16_f32(hi[e]));
+                } else {
+                    hi[e] = (uint16_t)(__float_as_uint(v) >> 16);
+                }
+            }
+            *(u16x4 *)&xs[st][r * SK_ROW + 4 * q] = hi;
+            if (SPLIT) *(u16x4 *)&xs[st][(64 + r) * SK_ROW + 4 * q] = lo;
         }
     };
     bf16x8 wr[SK_D][SK_WC][2];
@@ -359,7 +373,7 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
 
 extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny(mm_gemm_skinny_args a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][SK_STAGE];
-    if (a.xl)
+    if (a.split)
         skinny<true>(a, xs);
     else
         skinny<false>(a, xs);
