@@ -9,9 +9,12 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
  * per CU (partials summed by mm_skinny_reduce). */
 static int skinny_ok(int T, int n_in) { return T <= MM_SKINNY_T && n_in % 64 == 0; }
 
+#ifndef MM_SKINNY_BLOCKS
+#define MM_SKINNY_BLOCKS 256      /* target grid: about one block per CU */
+#endif
 static void skinny_plan(int d_out, int n_in, int *nsplit, int *kr) {
     const int nb = (d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN, nk = n_in / 64;
-    int ns = (256 + nb - 1) / nb;
+    int ns = (MM_SKINNY_BLOCKS + nb - 1) / nb;
     if (ns > nk) ns = nk;
     if (ns < 1) ns = 1;
     const int kc = (nk + ns - 1) / ns;          /* 64-input chunks per split */
