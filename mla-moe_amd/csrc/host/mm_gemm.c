@@ -80,9 +80,9 @@ int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int 
 }
 
 unsigned mm_gemv_blocks(int rows) {
-    /* 4 waves per block, GV_RPW (4) rows per wave per turn: one turn covers
+    /* 4 waves per block, MM_GEMV_RPW rows per wave per turn: one turn covers
      * every row when the grid allows */
-    const unsigned b = (unsigned)((rows + 15) / 16);
+    const unsigned b = (unsigned)((rows + 4 * MM_GEMV_RPW - 1) / (4 * MM_GEMV_RPW));
     return b < 2048 ? b : 2048;
 }
 

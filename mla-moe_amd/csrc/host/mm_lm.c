@@ -54,9 +54,10 @@ int mm_lm_head_dev(mm_ctx *c, int B, const float *x, const uint16_t *norm, float
     const int gemv = B <= MM_LM_NB && hidden <= MM_LM_HMAX;
     /* workspace: xb [B, hidden] (GEMM path), logits [B, vocab] when not
      * returned, GEMM staging, argmax partials */
-    const size_t nb = gemv ? (((size_t)vocab + 15) / 16 < MM_LM_GEMV_BLOCKS
-                                  ? ((size_t)vocab + 15) / 16 : MM_LM_GEMV_BLOCKS)
-                           : 0;                  /* GEMV blocks: 4 waves x 4 rows per turn */
+    const size_t rpb = 4 * MM_GEMV_RPW;           /* GEMV rows per block per turn */
+    const size_t nb = gemv ? (((size_t)vocab + rpb - 1) / rpb < MM_LM_GEMV_BLOCKS
+                                  ? ((size_t)vocab + rpb - 1) / rpb : MM_LM_GEMV_BLOCKS)
+                           : 0;
     const size_t o_xb = 0, n_xb = gemv ? 0 : al256((size_t)B * hidden * 4);
     const size_t o_lg = o_xb + n_xb, n_lg = logits ? 0 : al256((size_t)B * vocab * 4);
     const size_t o_gm = o_lg + n_lg, n_gm = gemv ? 0 : al256(mm_gemm_bf16_ws_bytes(B, hidden, vocab, 0));

@@ -377,6 +377,9 @@ typedef struct {
     int x_bf16;              /* x' = bf16(x) by truncation (no norm) */
 } mm_gemv_args;
 #define MM_GEMV_NB 4              /* tokens served by the GEMV (more: the MFMA GEMM) */
+#ifndef MM_GEMV_RPW
+#define MM_GEMV_RPW 2             /* GEMV rows per wave per turn (4 waves per block) */
+#endif
 
 /* ---- MLA decode front: RoPE, kv norm, latent-cache append -------------------- */
 #define MM_ROPE_PAIRS_MAX 2048    /* q_pe pairs per token (NH * QKR / 2) */

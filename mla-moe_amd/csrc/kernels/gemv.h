@@ -15,7 +15,7 @@
 
 #define GV_HMAX MM_LM_HMAX
 #define GV_PPL (GV_HMAX / 8 / MM_WAVE)   /* pieces per lane at the maximum H */
-#define GV_RPW 4                         /* rows per wave per turn */
+#define GV_RPW MM_GEMV_RPW               /* rows per wave per turn */
 
 /* Load NB tokens' activation rows x [B, H] (16-byte aligned, H % 8 == 0) as
  * pieces; tokens >= B and pieces past H read as zero.  norm != NULL applies
