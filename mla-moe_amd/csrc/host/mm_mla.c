@@ -124,7 +124,10 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks};
-    if ((st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, 1, 256, 0, &ca))) return st;
+    /* merge: split the latent columns over 4 blocks per (head, sequence)
+     * when the grid would otherwise have fewer than 128 blocks */
+    const unsigned zc = (size_t)NH * B < 128 ? MM_MLA_KVL / 128 : 1;
+    if ((st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, zc, 256, 0, &ca))) return st;
     return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,
                      (unsigned)((B + 31) / 32), 256, 0, &ca);
 }

@@ -418,11 +418,16 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
 
 /* Merge the chunk partials of (head h, sequence b): clat = sum_c w_c O_c / l
  * with w_c = e^(m_c - m); also turns the debug scores into probabilities.
- * grid (NH, B), 256 threads. */
+ * grid (NH, B, Z) with Z = 1 or KVL / 128, 256 threads: block z owns the
+ * latent columns [z KVL / Z, (z + 1) KVL / Z); thread t sums the column pair
+ * t % (pairs per block) over the chunks of its group t / (pairs per block)
+ * (16 loads in flight); with Z > 1 the chunk groups meet in LDS in group
+ * order (small batches: more blocks, fewer chunks each). */
 extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_args a) {
     __shared__ float wch[64];
     __shared__ float stat[2];
-    const int h = blockIdx.x, b = blockIdx.y;
+    __shared__ float2 red[256];
+    const int h = blockIdx.x, b = blockIdx.y, z = blockIdx.z;
     const int hg = h >> 4, hl = h & 15;
     const int tid = threadIdx.x;
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
@@ -443,27 +448,36 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_
     }
     __syncthreads();
     const float mx = stat[0], inv = 1.0f / stat[1];
-    /* thread t owns latent columns 2t, 2t + 1; the chunk partials are read
-     * 16 at a time (all loads in flight before the first is used) and summed
-     * in chunk order */
-    static_assert(KVL == 2 * 256, "combine: two latent columns per thread");
-    float *cl = a.clat + ((size_t)b * a.NH + h) * KVL;
-    const float *po = a.part_o + (pbase * 16 + hl) * KVL + 2 * tid;
+    static_assert(KVL == 512, "combine: 256 column pairs per sequence and head");
+    const int npair = (KVL / 2) / gridDim.z, ng = 256 / npair;   /* pairs per block, chunk groups */
+    const int cp = tid % npair, cg = tid / npair;
+    const int col = z * (KVL / gridDim.z) + 2 * cp;
+    const float *po = a.part_o + (pbase * 16 + hl) * KVL + col;
     float o0 = 0.0f, o1 = 0.0f;
-    for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
+    for (int c0 = cg; c0 < a.nchunks; c0 += ng * 16) {
         float2 v[16];
 #pragma unroll
         for (int k = 0; k < 16; k++)
-            v[k] = *(const float2 *)(po + (size_t)min(c0 + k, a.nchunks - 1) * 16 * KVL);
+            v[k] = *(const float2 *)(po + (size_t)min(c0 + ng * k, a.nchunks - 1) * 16 * KVL);
 #pragma unroll
         for (int k = 0; k < 16; k++)
-            if (c0 + k < a.nchunks) {
-                o0 += wch[c0 + k] * v[k].x;
-                o1 += wch[c0 + k] * v[k].y;
+            if (c0 + ng * k < a.nchunks) {
+                o0 += wch[c0 + ng * k] * v[k].x;
+                o1 += wch[c0 + ng * k] * v[k].y;
             }
     }
-    *(float2 *)(cl + 2 * tid) = make_float2(o0 * inv, o1 * inv);
-    if (a.probs) {
+    red[tid] = make_float2(o0, o1);
+    __syncthreads();
+    if (cg == 0) {
+        float2 s2 = red[cp];
+        for (int g = 1; g < ng; g++) {
+            s2.x += red[g * npair + cp].x;
+            s2.y += red[g * npair + cp].y;
+        }
+        float *cl = a.clat + ((size_t)b * a.NH + h) * KVL;
+        *(float2 *)(cl + col) = make_float2(s2.x * inv, s2.y * inv);
+    }
+    if (a.probs && z == 0) {
         float *pr = a.probs + ((size_t)b * a.NH + h) * a.probs_stride;
         for (int k = tid; k < L; k += blockDim.x) pr[k] = __expf(pr[k] - mx) * inv;
     }
