@@ -370,7 +370,8 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
     layers: a dense SwiGLU layer 0 (intermediate 10944), 26 MoE layers with
     int8 experts, vocabulary 102400; random weights generated on the device)
     through the batched engine: (1) one decode step of B slots at context
-    `prompt` (the steady-state step), (2) mm_engine_generate over B requests
+    `prompt` (the steady-state step) and of one slot (latency), (2)
+    mm_engine_generate over B requests
     of `prompt` tokens generating `gen` tokens each (prompts consumed by the
     same decode steps, continuous batching over B slots)."""
     from mlamoe.engine import Engine
@@ -430,6 +431,13 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
             for _ in range(steps):
                 eng.step(toks, pos)
             step_ms = (time.perf_counter() - t0) * 1e3 / steps
+            log(f"[engine] decode step B=1 at context {prompt}")
+            for _ in range(warmup):
+                eng.step(toks[:1], pos[:1])
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                eng.step(toks[:1], pos[:1])
+            step1_ms = (time.perf_counter() - t0) * 1e3 / steps
             prompts = [rng.integers(0, V, prompt).astype(np.int32) for _ in range(B)]
             log(f"[engine] generate: {B} requests x ({prompt} prompt + {gen} generated) tokens")
             eng.generate(prompts[:2], 2)                      # warm the generate path
@@ -440,6 +448,7 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
             eng.close()
     return dict(model="DeepSeek-V2-Lite shape, 27 layers, int8 experts, random weights",
                 step_B=B, step_context=prompt + 1, step_ms=step_ms, step_tok_s=B / (step_ms * 1e-3),
+                step_B1_ms=step1_ms, step_B1_tok_s=1.0 / (step1_ms * 1e-3),
                 generate_requests=B, generate_prompt=prompt, generate_new=gen,
                 generate_tokens=total, generate_s=gen_s, generate_tok_s=total / gen_s,
                 generate_steps=prompt + gen - 1,
