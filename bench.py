@@ -541,7 +541,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding plan is design-only (DESIGN.md).", file=sys.stderr)
+              "the multi-GPU sharding plan is a design, not built here.", file=sys.stderr)
         sys.exit(2)
 
     if args.calibrate_copy:
