@@ -147,8 +147,11 @@ static int dense_ffn(mm_engine *e, const mm_engine_layer *L, int B) {
     } else {
         mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, e->cfg.rms_eps};
         if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
-        if ((st = mm_matmul_bf16_dev(c, e->g, e->xn, L->dense_gate, DI, H, B, 0))) return st;
-        if ((st = mm_matmul_bf16_dev(c, e->u, e->xn, L->dense_up, DI, H, B, 0))) return st;
+        /* gate and up over the same xn in one pass */
+        char *ws;
+        if ((st = mm_workspace(c, mm_gemm_bf16_ws2_bytes(B, H, DI, DI, 0), (void **)&ws))) return st;
+        if ((st = mm_gemm_bf16_ws2(c, e->g, L->dense_gate, DI, e->u, L->dense_up, DI, e->xn, H, B, 0, ws)))
+            return st;
     }
     const size_t n = (size_t)B * DI;
     mm_swiglu_args sa = {e->g, e->u, e->g, n};

@@ -12,8 +12,10 @@ static int skinny_ok(int T, int n_in) { return T <= MM_SKINNY_T && n_in % 64 == 
 #ifndef MM_SKINNY_BLOCKS
 #define MM_SKINNY_BLOCKS 256      /* target grid: about one block per CU */
 #endif
-static void skinny_plan(int d_out, int n_in, int *nsplit, int *kr) {
-    const int nb = (d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN, nk = n_in / 64;
+/* nb column blocks in all: split K until the grid has about
+ * MM_SKINNY_BLOCKS blocks */
+static void skinny_plan(int nb, int n_in, int *nsplit, int *kr) {
+    const int nk = n_in / 64;
     int ns = (MM_SKINNY_BLOCKS + nb - 1) / nb;
     if (ns > nk) ns = nk;
     if (ns < 1) ns = 1;
@@ -22,35 +24,55 @@ static void skinny_plan(int d_out, int n_in, int *nsplit, int *kr) {
     *nsplit = (nk + kc - 1) / kc;
 }
 
-size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags) {
+static int skinny_nb(int d) { return (d + MM_SKINNY_BN - 1) / MM_SKINNY_BN; }
+
+size_t mm_gemm_bf16_ws2_bytes(int T, int n_in, int d0, int d1, unsigned flags) {
     if (skinny_ok(T, n_in)) {                    /* only the split partials */
         int ns, kr;
-        skinny_plan(d_out, n_in, &ns, &kr);
-        return ns > 1 ? al256((size_t)ns * T * d_out * 4) : 256;
+        skinny_plan(skinny_nb(d0) + (d1 > 0 ? skinny_nb(d1) : 0), n_in, &ns, &kr);
+        return ns > 1 ? al256((size_t)ns * T * ((size_t)d0 + (d1 > 0 ? d1 : 0)) * 4) : 256;
     }
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
     const size_t xb = (size_t)T * ((n_in + 63) / 64 * 64) * 2;
     return (split ? 2 : 1) * al256(xb);
 }
 
-int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
-                    int T, unsigned flags, char *ws) {
+size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags) {
+    return mm_gemm_bf16_ws2_bytes(T, n_in, d_out, 0, flags);
+}
+
+int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1,
+                     const uint16_t *w1, int d1, const float *x, int n_in, int T, unsigned flags,
+                     char *ws) {
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
     const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
     int st;
+    if (!w1) d1 = 0;
     if (skinny_ok(T, n_in)) {
-        /* fp32 x converted while staged; ws holds the split partials */
+        /* fp32 x converted while staged; ws holds the split partials; both
+         * matrices in one launch */
+        const int nb0 = skinny_nb(d0), nb = nb0 + (d1 ? skinny_nb(d1) : 0);
         int ns, kr;
-        skinny_plan(d_out, n_in, &ns, &kr);
-        mm_gemm_skinny_args k = {x, w, y, (float *)ws, T, d_out, n_in, ns, kr, split, acc};
-        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)((d_out + MM_SKINNY_BN - 1) / MM_SKINNY_BN),
-                            (unsigned)ns, 1, 256, 0, &k)))
-            return st;
+        skinny_plan(nb, n_in, &ns, &kr);
+        mm_gemm_skinny_args k = {x, w0, y0, (float *)ws, T, d0, n_in, ns, kr, split, acc,
+                                 w1, y1, d1, nb0};
+        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
         if (ns == 1) return MM_OK;
-        mm_skinny_reduce_args r = {(float *)ws, y, T, d_out, ns, acc};
-        const size_t n = (size_t)T * d_out, blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+        mm_skinny_reduce_args r = {(float *)ws, y0, T, d0, ns, acc, d1 ? y1 : NULL, d1};
+        const size_t n = (size_t)T * ((size_t)d0 + d1);
+        const size_t blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
         return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
     }
+    if ((st = mm_gemm_bf16_ws(c, y0, x, w0, d0, n_in, T, flags, ws))) return st;
+    return d1 ? mm_gemm_bf16_ws(c, y1, x, w1, d1, n_in, T, flags, ws) : MM_OK;
+}
+
+int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
+                    int T, unsigned flags, char *ws) {
+    if (skinny_ok(T, n_in)) return mm_gemm_bf16_ws2(c, y, w, d_out, NULL, NULL, 0, x, n_in, T, flags, ws);
+    const int split = (flags & MM_MATMUL_X_BF16) == 0;
+    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
+    int st;
     /* x as bf16 rows of a stride padded to 64 (zeros past n_in) */
     const int kp = (n_in + 63) / 64 * 64;
     const size_t xb = (size_t)T * kp * 2;

@@ -122,6 +122,12 @@ int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
 /* Dense bf16 GEMM (mm_matmul_bf16_dev) on a caller-provided workspace of at
  * least mm_gemm_bf16_ws_bytes(T, n_in, d_out, flags) bytes. */
 size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags);
+/* Two matrices over the same x (y0 = x . W0^T, y1 = x . W1^T; w1 may be
+ * NULL): one skinny-M launch when that path applies. */
+size_t mm_gemm_bf16_ws2_bytes(int T, int n_in, int d0, int d1, unsigned flags);
+int mm_gemm_bf16_ws2(mm_ctx *ctx, float *y0, const uint16_t *w0, int d0, float *y1,
+                     const uint16_t *w1, int d1, const float *x, int n_in, int T, unsigned flags,
+                     char *ws);
 int mm_gemm_bf16_ws(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
                     int T, unsigned flags, char *ws);
 

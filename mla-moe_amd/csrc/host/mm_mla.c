@@ -218,9 +218,8 @@ int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weight
      * and the GEMM staging */
     const size_t o_cp = 0, o_qa = al256((size_t)B * KVD * 4);
     const size_t o_xb = o_qa + al256((size_t)B * ql * 4);
-    /* GEMM staging: the largest of the projections' needs */
-    size_t gw = mm_gemm_bf16_ws_bytes(B, H, KVD, 0), g2;
-    if ((g2 = mm_gemm_bf16_ws_bytes(B, H, ql ? ql : QD, 0)) > gw) gw = g2;
+    /* GEMM staging: the larger of the two passes' needs */
+    size_t gw = mm_gemm_bf16_ws2_bytes(B, H, ql ? ql : QD, KVD, 0), g2;
     if (ql && (g2 = mm_gemm_bf16_ws_bytes(B, ql, QD, 0)) > gw) gw = g2;
     const size_t o_gm = o_xb + (gemv ? 0 : al256((size_t)B * H * 4));
     char *ws;
@@ -241,15 +240,15 @@ int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weight
         char *gws = ws + o_gm;
         mm_rmsnorm_args ra = {x, w->input_norm, xb, H, f->rms_eps};
         if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+        /* the query projection (or q_a) and kv_a over the same xb: one pass */
+        if ((st = mm_gemm_bf16_ws2(c, ql ? qa : q, ql ? w->q_a_proj : w->q_proj, ql ? ql : QD, comp,
+                                   w->kv_a_proj, KVD, xb, H, B, 0, gws)))
+            return st;
         if (ql) {
-            if ((st = mm_gemm_bf16_ws(c, qa, xb, w->q_a_proj, ql, H, B, 0, gws))) return st;
             mm_rmsnorm_args qn = {qa, w->q_a_norm, qa, ql, f->mla_norm_eps};
             if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &qn))) return st;
             if ((st = mm_gemm_bf16_ws(c, q, qa, w->q_b_proj, QD, ql, B, 0, gws))) return st;
-        } else if ((st = mm_gemm_bf16_ws(c, q, xb, w->q_proj, QD, H, B, 0, gws))) {
-            return st;
         }
-        if ((st = mm_gemm_bf16_ws(c, comp, xb, w->kv_a_proj, KVD, H, B, 0, gws))) return st;
     }
     mm_mla_rope_args r = {q, comp, w->kv_a_norm, c->front_inv, pos, cache, kv_rows, B, NH,
                           g->qk_nope_head_dim, g->qk_rope_head_dim, g->kv_lora_rank, seq_stride,

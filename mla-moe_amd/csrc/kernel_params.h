@@ -321,12 +321,19 @@ typedef struct {
     int T, d_out, n_in, nsplit, kr;   /* kr: inputs per split, a multiple of 64 */
     int split;               /* 1: x as a bf16 hi/lo pair; 0: x truncated to bf16 */
     int accumulate;
+    /* an optional second matrix over the same x: column blocks >= nb0 are
+     * its (w1 [d_out1, n_in] -> y1 [T, d_out1], partials after the first's) */
+    const uint16_t *w1;
+    float *y1;
+    int d_out1, nb0;
 } mm_gemm_skinny_args;
 
 typedef struct {
-    const float *part;       /* [nsplit, T, d_out] */
+    const float *part;       /* [nsplit, T, d_out], then [nsplit, T, d_out1] */
     float *y;                /* [T, d_out] */
     int T, d_out, nsplit, accumulate;
+    float *y1;               /* [T, d_out1] (second matrix) or NULL */
+    int d_out1;
 } mm_skinny_reduce_args;
 
 /* ---- LM head (final RMSNorm, logits, greedy argmax) ------------------------- */

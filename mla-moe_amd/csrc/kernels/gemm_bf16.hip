@@ -253,14 +253,19 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args
 template <bool SPLIT>
 __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*xs)[SK_STAGE]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * (64 * SK_WC) + wave * (16 * SK_WC);
+    /* column block bx of matrix `seg` (the second one past nb0 blocks) */
+    const bool seg = (int)blockIdx.x >= a.nb0;
+    const int bx = seg ? blockIdx.x - a.nb0 : blockIdx.x;
+    const int d_out = seg ? a.d_out1 : a.d_out;
+    const uint16_t *wm = seg ? a.w1 : a.w;
+    const int n0 = bx * (64 * SK_WC) + wave * (16 * SK_WC);
     const int kb = blockIdx.y * a.kr;
     const int nch = (min(a.n_in, kb + a.kr) - kb) / 64;    /* 64-input chunks of this split */
     const uint16_t *wrow[SK_WC];
 #pragma unroll
     for (int j = 0; j < SK_WC; j++) {
-        const int col = min(n0 + 16 * j + (lane & 15), a.d_out - 1);   /* past d_out: not stored */
-        wrow[j] = a.w + (size_t)col * a.n_in + kb + 8 * (lane >> 4);
+        const int col = min(n0 + 16 * j + (lane & 15), d_out - 1);   /* past d_out: not stored */
+        wrow[j] = wm + (size_t)col * a.n_in + kb + 8 * (lane >> 4);
     }
 
     /* x chunk c (fp32) -> registers, two slots: chunks are loaded two ahead
@@ -354,7 +359,8 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
 #pragma unroll
     for (int j = 0; j < SK_WC; j++) {
         const int n = n0 + 16 * j + (lane & 15);
-        if (n >= a.d_out) continue;
+        if (n >= d_out) continue;
+        float *part = a.part + (seg ? (size_t)a.nsplit * a.T * a.d_out : 0);
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
@@ -362,9 +368,9 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
                 const int t = 16 * g + 4 * (lane >> 4) + i;
                 if (t >= a.T) continue;
                 if (a.nsplit > 1) {
-                    a.part[((size_t)blockIdx.y * a.T + t) * a.d_out + n] = acc[j][g][i];
+                    part[((size_t)blockIdx.y * a.T + t) * d_out + n] = acc[j][g][i];
                 } else {
-                    float *y = a.y + (size_t)t * a.d_out + n;
+                    float *y = (seg ? a.y1 : a.y) + (size_t)t * d_out + n;
                     *y = a.accumulate ? *y + acc[j][g][i] : acc[j][g][i];
                 }
             }
@@ -381,11 +387,15 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny(mm_gemm_skinny_
 
 /* y (+)= sum over splits s = 0 .. nsplit-1 of part[s], in that order. */
 extern "C" __global__ __launch_bounds__(256) void mm_skinny_reduce(mm_skinny_reduce_args a) {
-    const size_t n = (size_t)a.T * a.d_out;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
-        float v = a.part[i];
-        for (int s = 1; s < a.nsplit; s++) v += a.part[(size_t)s * n + i];
-        a.y[i] = a.accumulate ? a.y[i] + v : v;
+    const size_t n0 = (size_t)a.T * a.d_out, n1 = a.y1 ? (size_t)a.T * a.d_out1 : 0;
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < n0 + n1;
+         k += (size_t)gridDim.x * blockDim.x) {
+        const bool seg = k >= n0;
+        const size_t n = seg ? n1 : n0, i = seg ? k - n0 : k;
+        const float *part = a.part + (seg ? (size_t)a.nsplit * n0 : 0);
+        float *y = seg ? a.y1 : a.y;
+        float v = part[i];
+        for (int s = 1; s < a.nsplit; s++) v += part[(size_t)s * n + i];
+        y[i] = a.accumulate ? y[i] + v : v;
     }
 }
