@@ -52,8 +52,18 @@ typedef struct mm_ctx mm_ctx;
  * creates the context's stream (default priority). */
 MM_API int mm_ctx_create(int device, mm_ctx **out);
 MM_API void mm_ctx_destroy(mm_ctx *ctx);
-/* The context's hipStream_t, as an opaque pointer. */
+/* The hipStream_t the context currently queues on, as an opaque pointer. */
 MM_API void *mm_ctx_stream(mm_ctx *ctx);
+/* Queue the context's work on a caller-owned hipStream_t (passed as an
+ * opaque pointer) from now on; NULL returns to the context's own stream.
+ * Work already queued on the previous stream stays ordered before anything
+ * queued afterwards (the new stream waits on an event of the old one), so
+ * the switch is safe at any point.  The caller keeps the stream alive while
+ * it is set, and synchronous entry points then wait on it.  The reference
+ * runs everything on one hipStreamNonBlocking stream of its own
+ * (src/getp_run.hip:735); this lets a host engine put the hot path on the
+ * stream it already orders its other work on. */
+MM_API int mm_ctx_set_stream(mm_ctx *ctx, void *stream);
 /* Wait for all work queued on the context stream. */
 MM_API int mm_ctx_sync(mm_ctx *ctx);
 
@@ -265,8 +275,12 @@ MM_API int mm_mla_init(mm_ctx *ctx, const mm_mla_config *cfg, int n_layers);
  * (src/model_load.c:80-86; include/model.h:56-65).  Synchronous. */
 MM_API int mm_mla_load_layer(mm_ctx *ctx, int layer, const uint16_t *kv_b, unsigned flags);
 
+/* Longest context the absorbed chain serves (512 chunks of 512 keys); the
+ * reference caps its cache at KV_CACHE_CAP = 163,840 (src/model_load.c:237). */
+#define MM_MAX_KV_LEN 262144
+
 /* The absorbed per-head decode chain of forward_absorbed (src/run.c:430-460)
- * for B sequences.  Device pointers, asynchronous:
+ * for B sequences, kv_len <= MM_MAX_KV_LEN.  Device pointers, asynchronous:
  *   q      [B, NH, QKN + QKR] fp32, q_nope | q_pe (RoPE applied)
  *   cache  [B, seq_stride, KVL + QKR] bf16 latent cache (c_kv | k_pe), the
  *          first kv_len (or kv_lens[b]) rows of each sequence attended
@@ -353,8 +367,11 @@ typedef struct {
     int vocab_size;
     float rms_eps;           /* post_attention_layernorm and the final norm */
     int max_batch;           /* sequence slots decoded together */
-    int max_seq;             /* positions per slot (the latent cache's seq_stride) */
+    int max_seq;             /* positions per slot at most (Config.max_seq_len) */
     unsigned moe_flags;      /* MM_FWD_BF16 or MM_FWD_INT8 for the MoE layers */
+    int init_seq;            /* positions per slot allocated at creation (0: the
+                                smaller of max_seq and 1024); the latent caches
+                                grow on demand up to max_seq */
 } mm_engine_config;
 
 /* One layer's non-expert weights, device pointers (ModelWeights,
@@ -374,19 +391,32 @@ typedef struct mm_engine mm_engine;
 /* An engine over ctx, whose MoE layers (mm_moe_init with n_layers layers,
  * every MoE layer loaded), MLA layers (mm_mla_init, every layer loaded) and
  * front (mm_mla_front_init) are set up.  Allocates the latent caches
- * (n_layers x max_batch x max_seq x (KVL+QKR) bf16) and step buffers. */
+ * (n_layers x max_batch x init_seq x (KVL+QKR) bf16) and step buffers.
+ * max_seq may exceed what fits in device memory: the caches grow only as
+ * far as requests need (mm_engine_reserve). */
 MM_API int mm_engine_create(mm_ctx *ctx, const mm_engine_config *cfg, mm_engine **out);
 MM_API void mm_engine_destroy(mm_engine *e);
+/* Positions per slot the latent caches hold now. */
+MM_API int mm_engine_capacity(const mm_engine *e);
+/* Grow the latent caches to hold at least `positions` per slot (<= max_seq),
+ * doubling the capacity up to max_seq as the reference's
+ * ensure_sequence_capacity does (src/getp_run.hip:269-290); every slot's
+ * rows are kept.  Layers grow one at a time, so the extra memory during a
+ * growth is one layer's new cache; if an allocation fails the engine keeps
+ * working at its previous capacity.  Synchronous.  mm_engine_step and
+ * mm_engine_generate call it themselves. */
+MM_API int mm_engine_reserve(mm_engine *e, int positions);
 MM_API int mm_engine_set_layer(mm_engine *e, int layer, const mm_engine_layer *w);
 /* embed [vocab, H], final norm [H], lm_head [vocab, H]: device bf16. */
 MM_API int mm_engine_set_head(mm_engine *e, const uint16_t *embed, const uint16_t *final_norm,
                               const uint16_t *lm_head);
 
 /* One decode step (forward_absorbed, src/run.c:379-501) for batch rows
- * b < B: slot b takes token tokens[b] at position pos[b] (host arrays) and
- * next[b] (host) receives the greedy next token; logits (device [B, vocab])
- * may be NULL.  Slot b's cache rows [0, pos[b]) must hold its earlier
- * positions.  Synchronous. */
+ * b < B: slot b takes token tokens[b] at position pos[b] (host arrays,
+ * 0 <= pos[b] < max_seq; the caches grow when a position is past their
+ * capacity) and next[b] (host) receives the greedy next token; logits
+ * (device [B, vocab]) may be NULL.  Slot b's cache rows [0, pos[b]) must
+ * hold its earlier positions.  Synchronous. */
 MM_API int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *pos,
                           int32_t *next, float *logits);
 

@@ -68,6 +68,7 @@ static const struct {
     [K_SWIGLU] = {"mm_swiglu", MOD_UTIL},
     [K_GEMM_SKINNY] = {"mm_gemm_skinny", MOD_GEMM_BF16},
     [K_SKINNY_REDUCE] = {"mm_skinny_reduce", MOD_GEMM_BF16},
+    [K_ZERO32] = {"mm_zero32", MOD_UTIL},
 };
 
 /* ---- errors ------------------------------------------------------------- */
@@ -115,11 +116,13 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->device = device;
     int st = MM_OK;
     if ((e = hipSetDevice(device)) != hipSuccess ||
-        (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreate(&c->t0)) != hipSuccess || (e = hipEventCreate(&c->t1)) != hipSuccess) {
+        (e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreate(&c->t0)) != hipSuccess || (e = hipEventCreate(&c->t1)) != hipSuccess ||
+        (e = hipEventCreateWithFlags(&c->ev_switch, hipEventDisableTiming)) != hipSuccess) {
         st = mm_hip_fail(e, "mm_ctx_create");
         goto fail;
     }
+    c->stream = c->own_stream;
     c->modules = calloc(MOD_COUNT, sizeof(hipModule_t));
     if (!c->modules) {
         st = mm_fail(MM_ERR_NOMEM, "mm_ctx_create: calloc");
@@ -156,6 +159,7 @@ void mm_ctx_destroy(mm_ctx *c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->own_stream && c->own_stream != c->stream) hipStreamSynchronize(c->own_stream);
     mm_moe_release(c);
     mm_mla_release(c);
     if (c->ws) hipFree(c->ws);
@@ -166,11 +170,23 @@ void mm_ctx_destroy(mm_ctx *c) {
     free(c->modules);
     if (c->t0) hipEventDestroy(c->t0);
     if (c->t1) hipEventDestroy(c->t1);
-    if (c->stream) hipStreamDestroy(c->stream);
+    if (c->ev_switch) hipEventDestroy(c->ev_switch);
+    if (c->own_stream) hipStreamDestroy(c->own_stream);
     free(c);
 }
 
 void *mm_ctx_stream(mm_ctx *c) { return c ? (void *)c->stream : NULL; }
+
+int mm_ctx_set_stream(mm_ctx *c, void *stream) {
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_ctx_set_stream: NULL context");
+    hipStream_t s = stream ? (hipStream_t)stream : c->own_stream;
+    if (s == c->stream) return MM_OK;
+    MM_HIP(hipSetDevice(c->device));
+    MM_HIP(hipEventRecord(c->ev_switch, c->stream));
+    MM_HIP(hipStreamWaitEvent(s, c->ev_switch, 0));
+    c->stream = s;
+    return MM_OK;
+}
 
 int mm_ctx_sync(mm_ctx *c) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_ctx_sync: NULL context");

@@ -28,7 +28,9 @@ struct mm_engine {
     mm_engine_layer *layers;
     unsigned char *layer_set;
     const uint16_t *embed, *final_norm, *lm_head;
-    uint16_t **cache;          /* [n_layers] device [max_batch, max_seq, KVL+QKR] bf16 */
+    uint16_t **cache;          /* [n_layers] device [max_batch, lcap[l], KVL+QKR] bf16 */
+    int *lcap;                 /* [n_layers] positions per slot of each layer's cache */
+    int cap;                   /* positions every layer holds: min of lcap */
     float *x, *xn, *q, *ctxo, *g, *u;
     int32_t *d_io;             /* device [4][max_batch]: tokens, pos, kv_lens, next */
     int32_t *h_io;             /* pinned host, same layout */
@@ -46,9 +48,60 @@ void mm_engine_destroy(mm_engine *e) {
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (e->h_io) hipHostFree(e->h_io);
+    free(e->lcap);
     free(e->layers);
     free(e->layer_set);
     free(e);
+}
+
+/* Bytes of one layer's latent cache at `cap` positions per slot. */
+static size_t cache_bytes(const mm_engine *e, int cap) {
+    const mm_mla_config *g = &e->c->mla;
+    return (size_t)e->cfg.max_batch * (size_t)cap * ((size_t)g->kv_lora_rank + g->qk_rope_head_dim) * 2;
+}
+
+int mm_engine_capacity(const mm_engine *e) { return e ? e->cap : 0; }
+
+int mm_engine_reserve(mm_engine *e, int positions) {
+    if (!e) return mm_fail(MM_ERR_INVALID, "mm_engine_reserve: NULL engine");
+    if (positions <= e->cap) return MM_OK;
+    if (positions > e->cfg.max_seq)
+        return mm_fail(MM_ERR_INVALID, "mm_engine_reserve: %d positions > max_seq %d", positions,
+                       e->cfg.max_seq);
+    mm_ctx *c = e->c;
+    int st = mm_set_device(c);
+    if (st) return st;
+    /* doubling up to max_seq, as ensure_sequence_capacity (getp_run.hip:269-290) */
+    int cap = e->cap > 0 ? e->cap : 1;
+    while (cap < positions && cap < e->cfg.max_seq)
+        cap = (long long)cap * 2 < e->cfg.max_seq ? cap * 2 : e->cfg.max_seq;
+    if (cap < positions) cap = positions;
+    const size_t row = (size_t)(c->mla.kv_lora_rank + c->mla.qk_rope_head_dim) * 2;
+    MM_HIP(hipStreamSynchronize(c->stream));
+    for (int l = 0; l < e->cfg.n_layers; l++) {
+        if (e->lcap[l] >= cap) continue;
+        uint16_t *nc = NULL;
+        if (hipMalloc((void **)&nc, cache_bytes(e, cap)) != hipSuccess) {
+            (void)hipGetLastError();
+            return mm_fail(MM_ERR_NOMEM, "mm_engine_reserve: latent cache of layer %d at %d "
+                           "positions (%zu bytes); the engine keeps %d positions", l, cap,
+                           cache_bytes(e, cap), e->cap);
+        }
+        /* every slot's rows [0, lcap) to the new stride */
+        hipError_t he = hipMemcpy2DAsync(nc, (size_t)cap * row, e->cache[l], (size_t)e->lcap[l] * row,
+                                         (size_t)e->lcap[l] * row, (size_t)e->cfg.max_batch,
+                                         hipMemcpyDeviceToDevice, c->stream);
+        if (he == hipSuccess) he = hipStreamSynchronize(c->stream);
+        if (he != hipSuccess) {
+            hipFree(nc);
+            return mm_hip_fail(he, "mm_engine_reserve: copying the cache");
+        }
+        hipFree(e->cache[l]);
+        e->cache[l] = nc;
+        e->lcap[l] = cap;
+    }
+    e->cap = cap;
+    return MM_OK;
 }
 
 int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
@@ -81,7 +134,8 @@ int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
     e->layers = calloc((size_t)cfg->n_layers, sizeof(mm_engine_layer));
     e->layer_set = calloc((size_t)cfg->n_layers, 1);
     e->cache = calloc((size_t)cfg->n_layers, sizeof(uint16_t *));
-    if (!e->layers || !e->layer_set || !e->cache) {
+    e->lcap = calloc((size_t)cfg->n_layers, sizeof(int));
+    if (!e->layers || !e->layer_set || !e->cache || !e->lcap) {
         mm_engine_destroy(e);
         return mm_fail(MM_ERR_NOMEM, "mm_engine_create: calloc");
     }
@@ -103,12 +157,20 @@ int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
         mm_engine_destroy(e);
         return mm_fail(MM_ERR_NOMEM, "mm_engine_create: pinned host buffer");
     }
-    for (int l = 0; l < cfg->n_layers; l++)
-        if (hipMalloc((void **)&e->cache[l], B * cfg->max_seq * KVD * 2) != hipSuccess) {
+    if (cfg->init_seq < 0 || cfg->init_seq > cfg->max_seq) {
+        mm_engine_destroy(e);
+        return mm_fail(MM_ERR_INVALID, "mm_engine_create: init_seq outside [0, max_seq]");
+    }
+    e->cap = cfg->init_seq ? cfg->init_seq : (cfg->max_seq < 1024 ? cfg->max_seq : 1024);
+    for (int l = 0; l < cfg->n_layers; l++) {
+        if (hipMalloc((void **)&e->cache[l], B * (size_t)e->cap * KVD * 2) != hipSuccess) {
+            (void)hipGetLastError();
             mm_engine_destroy(e);
             return mm_fail(MM_ERR_NOMEM, "mm_engine_create: latent cache of layer %d (%zu bytes)", l,
-                           B * cfg->max_seq * KVD * 2);
+                           B * (size_t)e->cap * KVD * 2);
         }
+        e->lcap[l] = e->cap;
+    }
     *out = e;
     return MM_OK;
 }
@@ -176,13 +238,16 @@ int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *po
         if (pos[b] < 0 || pos[b] >= f->max_seq)
             return mm_fail(MM_ERR_INVALID, "mm_engine_step: pos[%d] = %d outside [0, %d)", b, pos[b],
                            f->max_seq);
+        if (pos[b] + 1 > kvmax) kvmax = pos[b] + 1;
+    }
+    int st = mm_engine_reserve(e, kvmax);
+    if (st) return st;
+    for (int b = 0; b < B; b++) {
         e->h_io[b] = tokens[b];
         e->h_io[MB + b] = pos[b];
         e->h_io[2 * MB + b] = pos[b] + 1;
-        if (pos[b] + 1 > kvmax) kvmax = pos[b] + 1;
     }
-    int st = mm_set_device(c);
-    if (st) return st;
+    if ((st = mm_set_device(c))) return st;
     int32_t *d_tok = e->d_io, *d_pos = e->d_io + MB, *d_len = e->d_io + 2 * MB, *d_next = e->d_io + 3 * MB;
     MM_HIP(hipMemcpyAsync(e->d_io, e->h_io, (size_t)3 * MB * 4, hipMemcpyHostToDevice, c->stream));
     const mm_mla_config *g = &c->mla;
@@ -191,9 +256,9 @@ int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *po
     if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)B, 1, 256, 0, &ea))) return st;
     for (int l = 0; l < f->n_layers; l++) {
         const mm_engine_layer *L = &e->layers[l];
-        if ((st = mm_mla_front_dev(c, B, e->x, &L->front, d_pos, e->q, e->cache[l], f->max_seq, NULL)))
+        if ((st = mm_mla_front_dev(c, B, e->x, &L->front, d_pos, e->q, e->cache[l], e->lcap[l], NULL)))
             return st;
-        if ((st = mm_mla_absorbed_decode_dev(c, l, B, e->q, e->cache[l], f->max_seq, d_len, kvmax,
+        if ((st = mm_mla_absorbed_decode_dev(c, l, B, e->q, e->cache[l], e->lcap[l], d_len, kvmax,
                                              e->ctxo, NULL, NULL, NULL)))
             return st;
         if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, g->n_heads * g->v_head_dim, B,
@@ -237,7 +302,7 @@ long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prom
     int next_req = 0, st = MM_OK;
     for (;;) {
         /* admit waiting requests into free slots (lowest first) */
-        for (int s = 0; s < MB && next_req < n_req; s++) {
+        for (int s = 0; s < MB && next_req < n_req && !st; s++) {
             if (req[s] >= 0) continue;
             while (next_req < n_req) {
                 const int r = next_req++;
@@ -246,12 +311,16 @@ long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prom
                  * left after the prompt (getp_run.hip:946-952) */
                 const int lim = max_steps < e->cfg.max_seq - n ? max_steps : e->cfg.max_seq - n;
                 if (n < 1 || lim < 1 || !prompts[r]) continue;
+                /* the positions this request will use: its prompt and all
+                 * but the last generated token */
+                if ((st = mm_engine_reserve(e, n + lim - 1))) break;
                 req[s] = r;
                 limit[s] = lim;
                 pos[s] = 0;
                 break;
             }
         }
+        if (st) break;
         int hi = -1;
         for (int s = 0; s < MB; s++)
             if (req[s] >= 0) hi = s;

@@ -45,6 +45,7 @@ typedef enum {
     K_SWIGLU,
     K_GEMM_SKINNY,
     K_SKINNY_REDUCE,
+    K_ZERO32,
     K_COUNT
 } mm_kernel_id;
 
@@ -67,7 +68,9 @@ typedef struct {
 
 struct mm_ctx {
     int device;
-    hipStream_t stream;
+    hipStream_t stream;         /* where work is queued: own_stream or the caller's */
+    hipStream_t own_stream;     /* created with the context */
+    hipEvent_t ev_switch;       /* orders work across a stream switch */
     hipModule_t *modules;
     int n_modules;
     hipFunction_t fn[K_COUNT];
@@ -84,7 +87,8 @@ struct mm_ctx {
     mm_moe_config moe;
     int n_layers;
     mm_moe_layer *layers;
-    int32_t *moe_cnt;           /* [E] per-expert row counters, zero between calls */
+    int32_t *moe_cnt;           /* [E] per-expert row counters of the tiled path */
+    float *ffn_io;              /* mm_ffn_compute staging: x [H] | out [H] | idx [K] | w [K] */
 
     /* MLA */
     int mla_ready;

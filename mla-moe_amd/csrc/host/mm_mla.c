@@ -79,17 +79,18 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
     const int g_nh = c->mla.n_heads, HG0 = (g_nh + 15) / 16;
     /* chunk length: MM_MLA_CHUNK keys per block, halved (down to 16 keys per
      * wave) while the grid has fewer than MM_MLA_MIN_BLOCKS blocks and the
-     * chunk count stays <= 64 (the merge's limit) -- small batches then spread
-     * the cache read over more CUs */
+     * chunk count stays <= 64 -- small batches then spread the cache read
+     * over more CUs; long contexts keep the longest chunk, up to
+     * MM_MLA_MAXCH of them (the merge's limit) */
     int chunk = MM_MLA_CHUNK;
     while (chunk > 16 * MM_MLA_AW &&
            (size_t)B * HG0 * ((kv_len + chunk - 1) / chunk) < MM_MLA_MIN_BLOCKS &&
            (kv_len + chunk / 2 - 1) / (chunk / 2) <= 64)
         chunk /= 2;
     const int nchunks = (kv_len + chunk - 1) / chunk;
-    if (nchunks > 64)
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_absorbed_decode_dev: kv_len > %d",
-                       64 * MM_MLA_CHUNK);
+    if (kv_len > MM_MAX_KV_LEN || nchunks > MM_MLA_MAXCH)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_absorbed_decode_dev: kv_len %d > %d", kv_len,
+                       MM_MAX_KV_LEN);
     if ((uintptr_t)cache % 16)
         return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: cache must be 16-byte aligned");
     int st = mm_set_device(c);

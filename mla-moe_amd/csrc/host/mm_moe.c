@@ -30,6 +30,8 @@ void mm_moe_release(mm_ctx *c) {
     c->layers = NULL;
     if (c->moe_cnt) hipFree(c->moe_cnt);
     c->moe_cnt = NULL;
+    if (c->ffn_io) hipFree(c->ffn_io);
+    c->ffn_io = NULL;
     c->moe_ready = 0;
 }
 
@@ -48,8 +50,7 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     int st = mm_set_device(c);
     if (st) return st;
     MM_HIP(hipMalloc((void **)&c->moe_cnt, (size_t)E * sizeof(int32_t)));
-    MM_HIP(hipMemsetAsync(c->moe_cnt, 0, (size_t)E * sizeof(int32_t), c->stream));
-    MM_HIP(hipStreamSynchronize(c->stream));
+    MM_HIP(hipMalloc((void **)&c->ffn_io, (2 * (size_t)H + 2 * (size_t)K) * sizeof(float)));
     c->layers = calloc((size_t)n_layers, sizeof(mm_moe_layer));
     if (!c->layers) return mm_fail(MM_ERR_NOMEM, "mm_moe_init: calloc");
     c->moe = *cfg;
@@ -502,6 +503,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ra.x = xn;
     ra.qx = qx;
     ra.sx = sx;
+    if (tiled) {
+        /* the route kernel appends to the per-expert counters: clear them
+         * first, in stream order, so no earlier call's state is carried */
+        mm_zero32_args za = {(uint32_t *)c->moe_cnt, E};
+        if ((st = mm_launch(c, K_ZERO32, 1, 1, 1, 256, 0, &za))) return st;
+    }
     if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
                         64 * MM_I8_RT_WAVES, 0, &ra)))
         return st;
@@ -568,7 +575,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             return st;
     }
 
-    mm_i8_combine_args ca = {y, ys, wts, out, c->moe_cnt, T, (int)H, (int)K, (int)E, acc, S > 0};
+    mm_i8_combine_args ca = {y, ys, wts, out, T, (int)H, (int)K, acc, S > 0};
     if ((st = mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca))) return st;
 
     if (dbg) {
@@ -664,11 +671,8 @@ int mm_ffn_compute(mm_ctx *c, int layer, const float *xn, float *out, int *topk_
     const int H = c->moe.hidden_size, K = c->moe.n_experts_per_tok;
     int st = mm_set_device(c);
     if (st) return st;
-    /* private device staging: [x | out | idx | w] */
-    char *buf = NULL;
-    const size_t bytes = 2 * (size_t)H * sizeof(float) + (size_t)K * 8;
-    MM_HIP(hipMalloc((void **)&buf, bytes));
-    float *dx = (float *)buf, *dout = dx + H;
+    /* the context's staging (allocated by mm_moe_init): [x | out | idx | w] */
+    float *dx = c->ffn_io, *dout = dx + H;
     int32_t *didx = (int32_t *)(dout + H);
     float *dw = (float *)(didx + K);
     if (!(st = mm_h2d(c, dx, xn, (size_t)H * sizeof(float))))
@@ -677,7 +681,5 @@ int mm_ffn_compute(mm_ctx *c, int layer, const float *xn, float *out, int *topk_
     if (!st) st = mm_d2h(c, out, dout, (size_t)H * sizeof(float));
     if (!st && topk_idx) st = mm_d2h(c, topk_idx, didx, (size_t)K * sizeof(int32_t));
     if (!st && topk_w) st = mm_d2h(c, topk_w, dw, (size_t)K * sizeof(float));
-    hipStreamSynchronize(c->stream);
-    hipFree(buf);
     return st;
 }

@@ -73,6 +73,12 @@ typedef struct {
     int rows, K;
 } mm_quant_w_args;
 
+/* dst[i] = 0 for i < n 32-bit words. */
+typedef struct {
+    uint32_t *dst;
+    uint64_t n;
+} mm_zero32_args;
+
 /* Embedding rows of B tokens: x[b, :] = embed[tokens[b], :] in fp32. */
 typedef struct {
     const uint16_t *embed;   /* [vocab, H] bf16 */
@@ -147,13 +153,12 @@ typedef struct {
     int rows2, n2;
 } mm_i8_quant_rows_args;
 
-/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]; also re-zeroes cnt. */
+/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]. */
 typedef struct {
     const float *y, *ys;
     const float *topk_w;
     float *out;
-    int32_t *cnt;
-    int T, H, K, E;
+    int T, H, K;
     int accumulate;
     int has_shared;
 } mm_i8_combine_args;
@@ -239,6 +244,10 @@ typedef struct {
 #ifndef MM_MLA_AW
 #define MM_MLA_AW 4               /* waves per attention block */
 #endif
+/* Key chunks one (head group, sequence) may have: 512 x 512 = 262,144 keys at
+ * the longest chunk, above the reference's KV_CACHE_CAP of 163,840
+ * (src/model_load.c:237). */
+#define MM_MLA_MAXCH 512
 #define MM_MLA_TILE_B (16 * 1056 + 16 * 128)   /* LDS bytes of one 16-key sub-tile */
 
 /* qabs = q_nope . W_UK per head. */

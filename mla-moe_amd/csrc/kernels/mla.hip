@@ -424,7 +424,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
  * (16 loads in flight); with Z > 1 the chunk groups meet in LDS in group
  * order (small batches: more blocks, fewer chunks each). */
 extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_args a) {
-    __shared__ float wch[64];
+    __shared__ float wch[MM_MLA_MAXCH];
     __shared__ float stat[2];
     __shared__ float2 red[256];
     const int h = blockIdx.x, b = blockIdx.y, z = blockIdx.z;
@@ -433,14 +433,20 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_combine(mm_mla_combine_
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
     const size_t pbase = (size_t)(b * a.HG + hg) * a.nchunks;
     if (tid < MM_WAVE) {
-        /* chunk maxima and sums, one lane per chunk (nchunks <= 64) */
-        const bool ok = tid < a.nchunks;
-        const float mc = ok ? a.part_ml[(pbase + tid) * 32 + hl] : -INFINITY;
-        const float lc = ok ? a.part_ml[(pbase + tid) * 32 + 16 + hl] : 0.0f;
-        const float mx = wave_max(mc);
-        const float wc = mc == -INFINITY ? 0.0f : __expf(mc - mx);
-        const float ls = wave_sum(lc * wc);
-        if (ok) wch[tid] = wc;
+        /* chunk maxima and sums: lane l takes chunks l, l + 64, ...
+         * (nchunks <= MM_MLA_MAXCH) */
+        float mx = -INFINITY;
+        for (int c = tid; c < a.nchunks; c += MM_WAVE)
+            mx = fmaxf(mx, a.part_ml[(pbase + c) * 32 + hl]);
+        mx = wave_max(mx);
+        float ls = 0.0f;
+        for (int c = tid; c < a.nchunks; c += MM_WAVE) {
+            const float mc = a.part_ml[(pbase + c) * 32 + hl];
+            const float wc = mc == -INFINITY ? 0.0f : __expf(mc - mx);
+            ls += a.part_ml[(pbase + c) * 32 + 16 + hl] * wc;
+            wch[c] = wc;
+        }
+        ls = wave_sum(ls);
         if (tid == 0) {
             stat[0] = mx;
             stat[1] = ls;

@@ -35,6 +35,14 @@ extern "C" __global__ __launch_bounds__(256) void mm_fill(mm_fill_args a) {
     }
 }
 
+/* Zero n 32-bit words in stream order (per-expert counters of the tiled
+ * int8 path are cleared this way before every routing pass). */
+extern "C" __global__ __launch_bounds__(256) void mm_zero32(mm_zero32_args a) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        a.dst[i] = 0u;
+}
+
 /* One wave per row: s = max|w| / 127, q = clamp(rint(w / s), -127, 127),
  * with IEEE fp32 division and round-half-even, bit-identical to the CPU
  * quantiser; s == 0 gives an all-zero row. */

@@ -74,7 +74,8 @@ class EngineConfig(C.Structure):
     """Mirror of mm_engine_config."""
     _fields_ = [("n_layers", C.c_int), ("first_k_dense", C.c_int), ("hidden_size", C.c_int),
                 ("dense_inter_size", C.c_int), ("vocab_size", C.c_int), ("rms_eps", C.c_float),
-                ("max_batch", C.c_int), ("max_seq", C.c_int), ("moe_flags", C.c_uint)]
+                ("max_batch", C.c_int), ("max_seq", C.c_int), ("moe_flags", C.c_uint),
+                ("init_seq", C.c_int)]
 
 
 class EngineLayer(C.Structure):
@@ -112,6 +113,7 @@ def lib():
         L.mm_ctx_stream.argtypes = [_vp]
         L.mm_ctx_stream.restype = _vp
         L.mm_ctx_sync.argtypes = [_vp]
+        L.mm_ctx_set_stream.argtypes = [_vp, _vp]
         L.mm_dev_alloc.argtypes = [_vp, C.c_size_t, C.POINTER(_vp)]
         L.mm_dev_free.argtypes = [_vp, _vp]
         for f in (L.mm_h2d, L.mm_d2h, L.mm_d2d):
@@ -150,6 +152,8 @@ def lib():
         L.mm_engine_set_layer.argtypes = [_vp, C.c_int, C.POINTER(EngineLayer)]
         L.mm_engine_set_head.argtypes = [_vp, _vp, _vp, _vp]
         L.mm_engine_step.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp]
+        L.mm_engine_capacity.argtypes = [_vp]
+        L.mm_engine_reserve.argtypes = [_vp, C.c_int]
         L.mm_engine_generate.argtypes = [_vp, C.c_int, C.POINTER(_vp), _vp, C.c_int, C.c_int,
                                          C.POINTER(_vp), _vp]
         L.mm_engine_generate.restype = C.c_longlong
@@ -249,6 +253,14 @@ class Context:
 
     def sync(self):
         _check(lib().mm_ctx_sync(self.h))
+
+    def set_stream(self, stream):
+        """Queue on a caller-owned hipStream_t (an int handle), or on the
+        context's own stream again with None."""
+        _check(lib().mm_ctx_set_stream(self.h, stream))
+
+    def stream(self):
+        return lib().mm_ctx_stream(self.h)
 
     # timing --------------------------------------------------------------
     def timer_start(self):

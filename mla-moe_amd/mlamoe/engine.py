@@ -24,11 +24,12 @@ class Engine:
         self.ctx, self.h, self.cfg, self._bufs = ctx, handle, cfg, bufs
 
     @classmethod
-    def from_host(cls, ctx, c, m, inv_freq, max_batch, max_seq, int8=False):
+    def from_host(cls, ctx, c, m, inv_freq, max_batch, max_seq, int8=False, init_seq=0):
         """c: dict of Config fields (n_layers, first_dense, H, NH, QKN, QKR,
         KVL, VHD, dense_inter, E, n_shared, K, I, vocab, router_sigmoid,
         norm_topk, routed_scaling, rms_eps, and optionally q_lora,
-        interleaved); m: synth.model()."""
+        interleaved); m: synth.model(); init_seq: positions per slot the
+        latent caches start with (0: the library's default)."""
         L = c["n_layers"]
         ctx.mla_init(c["NH"], c["QKN"], c["QKR"], c["KVL"], c["VHD"], n_layers=L)
         ctx.mla_front_init(c["H"], inv_freq, c.get("q_lora", 0), c["rms_eps"], 1e-6,
@@ -55,7 +56,8 @@ class Engine:
             layers.append(EngineLayer(front, dev(lw["o_proj"]), dev(lw["post_norm"]),
                                       dev(lw.get("dgate")), dev(lw.get("dup")), dev(lw.get("ddown"))))
         cfg = EngineConfig(L, c["first_dense"], c["H"], c.get("dense_inter", 8), c["vocab"],
-                           c["rms_eps"], max_batch, max_seq, MM_FWD_INT8 if int8 else MM_FWD_BF16)
+                           c["rms_eps"], max_batch, max_seq, MM_FWD_INT8 if int8 else MM_FWD_BF16,
+                           init_seq)
         h = _vp()
         _check(lib().mm_engine_create(ctx.h, C.byref(cfg), C.byref(h)))
         eng = cls(ctx, h.value, cfg, bufs)
@@ -69,6 +71,13 @@ class Engine:
         if self.h:
             lib().mm_engine_destroy(self.h)
             self.h = None
+
+    def capacity(self):
+        """Positions per slot the latent caches hold now."""
+        return int(lib().mm_engine_capacity(self.h))
+
+    def reserve(self, positions):
+        _check(lib().mm_engine_reserve(self.h, positions))
 
     def step(self, tokens, pos, want_logits=False):
         """One decode step; returns (next tokens [B], logits [B, vocab] or None)."""

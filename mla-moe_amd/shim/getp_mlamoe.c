@@ -9,11 +9,14 @@
  *
  * warm_up uploads the Transformer's weights (host pointers into the
  * checkpoint mmaps, include/model.h:44-96) once: the experts as int8
- * (quantised on the device), every other tensor as bf16.  inference encodes
- * the prompts with the reference's tokenizer (prompt cap as
+ * (quantised on the device), every other tensor as bf16; it applies the
+ * reference's GLM position cap (src/getp_run.hip:709-710) and starts the
+ * latent caches at MLAMOE_GETP_INIT_SEQ positions per slot.  inference
+ * encodes the prompts with the reference's tokenizer (prompt cap as
  * src/getp_run.hip:932-953) and runs mm_engine_generate: all requests
  * decode together in slots of a batch instead of one after another
- * (src/getp_run.hip:958-993), prompts consumed by the same absorbed decode
+ * (src/getp_run.hip:958-993), the caches growing as requests need
+ * (src/getp_run.hip:269-290), prompts consumed by the same absorbed decode
  * steps.  Generated ids stop at EOS as there.  Errors print the library's
  * message and exit, as the reference's harness does (src/getp_run.hip:480-484).
  */
@@ -28,6 +31,9 @@
 
 #ifndef MLAMOE_GETP_BATCH
 #define MLAMOE_GETP_BATCH 64    /* decode slots */
+#endif
+#ifndef MLAMOE_GETP_INIT_SEQ
+#define MLAMOE_GETP_INIT_SEQ 256  /* positions per slot the caches start with */
 #endif
 
 static mm_ctx *g_ctx;
@@ -56,6 +62,12 @@ static const uint16_t *up(const void *h, size_t bytes) {
 }
 
 void warm_up(Transformer *t) {
+    if (g_owner) {
+        fprintf(stderr, "getp_mlamoe: warm_up: already initialised\n");
+        exit(EXIT_FAILURE);
+    }
+    /* the reference's GLM runtime caps its positions (src/getp_run.hip:709-710) */
+    if (t->config.rope_interleaved && t->config.q_lora_rank > 0) t->config.max_seq_len = 512 + 64;
     const Config *c = &t->config;
     const ModelWeights *w = &t->weights;
     const size_t H = (size_t)c->hidden_size, QD = (size_t)c->n_heads * (c->qk_nope_head_dim + c->qk_rope_head_dim);
@@ -71,8 +83,14 @@ void warm_up(Transformer *t) {
                         c->n_experts_per_tok, c->moe_inter_size, c->router_sigmoid,
                         c->norm_topk, c->routed_scaling};
     if (c->first_k_dense < c->n_layers && mm_moe_init(g_ctx, &mc, c->n_layers)) die("mm_moe_init");
+    /* positions per slot: the model's max_seq_len (163,840 for DeepSeek-V2-Lite,
+     * src/model_load.c:237), at most what the absorbed chain serves; the
+     * latent caches start small and grow with the requests, as the
+     * reference's ensure_sequence_capacity does (src/getp_run.hip:269-290) */
+    const int max_seq = c->max_seq_len < MM_MAX_KV_LEN ? c->max_seq_len : MM_MAX_KV_LEN;
     mm_engine_config ec = {c->n_layers, c->first_k_dense, c->hidden_size, c->dense_inter_size,
-                           c->vocab_size, c->rms_eps, MLAMOE_GETP_BATCH, c->max_seq_len, MM_FWD_INT8};
+                           c->vocab_size, c->rms_eps, MLAMOE_GETP_BATCH, max_seq, MM_FWD_INT8,
+                           MLAMOE_GETP_INIT_SEQ < max_seq ? MLAMOE_GETP_INIT_SEQ : max_seq};
     mm_engine_layer *ls = calloc((size_t)c->n_layers, sizeof(*ls));
     if (!ls) die("calloc");
     for (int l = 0; l < c->n_layers; l++) {
@@ -121,7 +139,8 @@ long long inference(Transformer *t, Requests *reqs) {
         fprintf(stderr, "getp_mlamoe: model_dir has no tokenizer.json\n");
         exit(EXIT_FAILURE);
     }
-    const int n = reqs->num_reqs, max_seq = t->config.max_seq_len;
+    const int n = reqs->num_reqs;
+    const int max_seq = t->config.max_seq_len < MM_MAX_KV_LEN ? t->config.max_seq_len : MM_MAX_KV_LEN;
     /* prompt cap of the reference's GLM runtime (src/getp_run.hip:932-936) */
     const int glm = t->config.rope_interleaved && t->config.q_lora_rank > 0;
     const int steps_cap = reqs->max_steps < 64 ? reqs->max_steps : 64;

@@ -73,8 +73,17 @@ def test_mla_lengths(ctx, oracle, kv_len):
 
 
 def test_mla_longest_context(ctx, oracle):
-    """kv_len = 64 chunks x 512 keys, the most the chunk merge serves."""
+    """kv_len = 64 chunks x 512 keys (the last length whose chunks may still
+    shrink for a small batch)."""
     run_case(ctx, oracle, 16, 1, 32768, 32768, 640)
+
+
+@pytest.mark.parametrize("kv_len", [32769, 163840])
+def test_mla_beyond_64_chunks(ctx, oracle, kv_len):
+    """Past 64 chunks the merge strides over up to 512 chunk partials:
+    one key past 32768, and the reference's KV_CACHE_CAP of 163,840
+    positions (src/model_load.c:237; 320 chunks of 512 keys)."""
+    run_case(ctx, oracle, 16, 1, kv_len, kv_len, 641)
 
 
 def test_mla_ragged_batch(ctx, oracle):
@@ -113,3 +122,20 @@ def test_mla_closed_forms(ctx, oracle):
 def test_mla_config5_subset(ctx, oracle):
     """BASELINE config-5 geometry (16 heads, 4096 context) on 3 sequences."""
     run_case(ctx, oracle, 16, 3, 4096, 4096, 640)
+
+
+def test_mla_config5_full(ctx, oracle):
+    """BASELINE config 5 at its own size: B = 32 sequences x 16 heads over
+    4096 positions, every sequence checked.  This is the shape the bench
+    times: 512-key chunks (32 x 8 = 256 blocks, no halving), the one-block
+    merge per (head, sequence) (NH * B = 512 >= 128) and full 32-row tiles in
+    the W_UK and W_UV products."""
+    run_case(ctx, oracle, 16, 32, 4096, 4096, 650)
+
+
+def test_mla_two_row_tiles_ragged(ctx, oracle):
+    """B = 40 (> 32: a second, partial row tile in the W_UK / W_UV products)
+    with ragged lengths up to 1500 and NH * B = 640 (one-block merge)."""
+    lens = [1500 - 37 * b for b in range(40)]
+    lens[3], lens[17], lens[39] = 1, 16, 513
+    run_case(ctx, oracle, 16, 40, 1500, 1500, 651, kv_lens=lens)
