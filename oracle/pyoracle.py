@@ -476,12 +476,14 @@ def ref_config_rope(model_dir):
 # whole decode steps (src/run.c:379-501)
 # ---------------------------------------------------------------------------
 
-def model_logits(c, m, tokens, inv):
+def model_logits(c, m, tokens, inv, int8=False):
     """forward_absorbed at positions 0..n-1 on tokens (teacher forcing),
     composed from the restated pieces in the reference's order; c: dict of
     the Config fields (n_layers, first_dense, H, NH, QKN, QKR, KVL, VHD,
     dense_inter, E, n_shared, K, I, vocab, router_sigmoid, norm_topk,
-    routed_scaling, rms_eps), m: synth.model().  Returns [n, vocab]."""
+    routed_scaling, rms_eps), m: synth.model().  With int8 the MoE layers
+    run the int8 expert scheme (ffn_i8 on per-channel quantised weights,
+    the library's MM_FWD_INT8) instead of ffn_compute.  Returns [n, vocab]."""
     H, NH, QKN, QKR, KVL, VHD = (c[k] for k in ("H", "NH", "QKN", "QKR", "KVL", "VHD"))
     KVD, eps, n = KVL + QKR, c["rms_eps"], len(tokens)
     fc = front_cfg(H, NH, QKN, QKR, KVL, c.get("q_lora", 0), eps, 1e-6, c.get("interleaved", 0))
@@ -489,6 +491,8 @@ def model_logits(c, m, tokens, inv):
                  c["routed_scaling"])
     caches = [np.zeros((n, KVD), np.float32) for _ in m["layers"]]
     out = np.empty((n, c["vocab"]), np.float32)
+    qws = [quantize_moe_weights(lw) if int8 and l >= c["first_dense"] else None
+           for l, lw in enumerate(m["layers"])]
     for p, tok in enumerate(tokens):
         x = (m["embed"][tok].astype(np.uint32) << 16).view(np.float32).copy()
         for l, lw in enumerate(m["layers"]):
@@ -505,6 +509,8 @@ def model_logits(c, m, tokens, inv):
                 lib().or_swiglu(_p(mo, _f32p), _p(c32(xb), _f32p), _p(lw["dgate"], _u16p),
                                 _p(lw["dup"], _u16p), _p(lw["ddown"], _u16p), c["dense_inter"], H,
                                 _p(hb, _f32p), _p(hb2, _f32p))
+            elif int8:
+                mo = ffn_i8(mc, lw, qws[l], xb[None])[0][0]
             else:
                 mo = ffn_compute_rows(mc, lw, xb[None])[0][0]
             x = (x + mo).astype(np.float32)

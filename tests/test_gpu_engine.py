@@ -56,13 +56,15 @@ def test_engine_distinct_slots(oracle, name, int8):
     before it, so rows hold different tokens, positions and cache lengths in
     every step: a row or cache mix-up changes some slot's logits.  Each
     slot's logits are checked against the oracle's forward_absorbed
-    composition for its own sequence."""
+    composition for its own sequence (with int8 experts, the oracle's int8
+    expert scheme: the int8-vs-bf16 drift is quantisation, not parity, and
+    reaches ~1e-2 on some of these rows)."""
     c, m, g = engine_case(name)
     inv = g["inv"]
     B, n = 6, 9
     rng = np.random.default_rng(77)
     seqs = [rng.integers(0, c["vocab"], n).astype(np.int32) for _ in range(B)]
-    refs = [oracle.model_logits(c, m, s, inv) for s in seqs]
+    refs = [oracle.model_logits(c, m, s, inv, int8=int8) for s in seqs]
     print(f"engine distinct slots {name} int8={int8}", flush=True)
     errs = []
     with mlamoe.Context(0) as ctx:

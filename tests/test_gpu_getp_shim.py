@@ -9,7 +9,8 @@ starts without allocating for it (the caches grow with the requests, as
 src/getp_run.hip:269-290); the GLM flavour gets the reference's 576-position
 cap (src/getp_run.hip:709-710) and prompt cap (src/getp_run.hip:932-936);
 every generated token is the oracle's argmax for its prefix (near-ties within
-2e-3 normwise accepted: the shim serves int8 experts); lengths follow
+2e-3 normwise accepted; the oracle runs the int8 expert scheme the shim
+serves); lengths follow
 min(max_steps, max_seq - prompt) and generation stops at EOS.
 """
 import ctypes as C
@@ -87,8 +88,10 @@ def run_shim(c, m, inv, prompts, max_steps, eos, max_seq):
 
 
 def _check_tokens(oracle, c, m, inv, prompt, out):
+    """Each generated id is the argmax of the oracle's logits for its prefix
+    (the oracle running the int8 expert scheme the shim serves)."""
     seq = np.concatenate([prompt, out])
-    lg = oracle.model_logits(c, m, seq[:-1], inv)
+    lg = oracle.model_logits(c, m, seq[:-1], inv, int8=True)
     for k, t in enumerate(out):
         row = lg[len(prompt) - 1 + k]
         assert t == row.argmax() or row[t] >= row.max() - TOL * np.abs(row).max(), k
