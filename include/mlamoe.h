@@ -170,6 +170,22 @@ MM_API int mm_moe_forward_dev(mm_ctx *ctx, int layer, int T, const float *xn, fl
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags);
 
+/* mm_moe_forward_dev without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results; the call's workspace is a static
+ * device array of MM_NOALLOC_SCRATCH_BYTES per device (32 MiB: e.g. up to
+ * ~280 tokens of a DeepSeek-V2-Lite int8 layer, 64 for the bench's decode
+ * batch) instead of the context's growable buffer.  A call that would need
+ * more fails with MM_ERR_UNSUPPORTED before launching anything; so does a
+ * call while per-kernel profiling is on.  Every call on a device shares that
+ * device's array: calls that overlap on one device (two streams, two host
+ * threads) race. */
+#define MM_NOALLOC_SCRATCH_BYTES (32u << 20)
+MM_API int mm_moe_forward_noalloc_dev(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
+                                      const float *logits, int32_t *topk_idx, float *topk_w,
+                                      float *probs, unsigned flags);
+
 /* Router logits alone: logits[t, e] = sum_i xn[t, i] * moe_gate[e, i] in the
  * reference's sequential fp32 order (the matmul at src/run.c:124), plus
  * logit_bias[e] when logit_bias != NULL (a per-expert prior; not in the

@@ -148,6 +148,7 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->i8_tiled_min_t = 256;
     const char *ev = getenv("MLAMOE_I8_TILED_MIN_T");
     if (ev && *ev) c->i8_tiled_min_t = atoi(ev);
+    if ((st = mm_noalloc_setup(c))) goto fail;
     *out = c;
     return MM_OK;
 fail:

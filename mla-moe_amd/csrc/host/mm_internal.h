@@ -104,7 +104,29 @@ struct mm_ctx {
     /* growable device workspace */
     void *ws;
     size_t ws_bytes;
+
+    /* this device's copy of the no-allocation entry point's static scratch
+     * array (its device address, from hipGetSymbolAddress at set-up) */
+    void *scratch;
+    size_t scratch_bytes;
 };
+
+/* A fixed device workspace region (no growth). */
+typedef struct {
+    char *base;
+    size_t cap;
+} mm_fixed_ws;
+
+/* mm_moe_forward_dev on the fixed workspace fx: fails with
+ * MM_ERR_UNSUPPORTED before any launch when the call needs more than
+ * fx->cap bytes; allocates nothing. */
+int mm_moe_forward_fixed(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
+                         const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
+                         unsigned flags, const mm_fixed_ws *fx);
+
+/* Set-up of the no-allocation scratch for the context's device (with that
+ * device current): its device address and size. */
+int mm_noalloc_setup(mm_ctx *ctx);
 
 /* error reporting (thread-local message) */
 int mm_fail(int status, const char *fmt, ...);

@@ -343,11 +343,27 @@ static size_t plan_take(mm_plan *p, size_t bytes) {
     return o;
 }
 
+/* The device workspace of one forward call: the context's growable one, or
+ * a fixed region (the no-allocation entry point's scratch) that must hold
+ * the whole plan. */
+static int take_ws(mm_ctx *c, const mm_fixed_ws *fx, size_t need, char **ws) {
+    if (fx) {
+        if (need > fx->cap)
+            return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_forward_noalloc_dev: this call needs %zu bytes "
+                           "of scratch, the entry point holds %zu (use mm_moe_forward_dev)", need,
+                           fx->cap);
+        *ws = fx->base;
+        return MM_OK;
+    }
+    return mm_workspace(c, need, (void **)ws);
+}
+
 /* ---- bf16 forward ------------------------------------------------------------ */
 
 /* bf16 weights, GEMV stages (kernels/moe_bf16.hip), BF16_NT_MAX tokens per pass. */
 static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
-                        const float *logits, int32_t *idx, float *wts, float *probs, int acc) {
+                        const float *logits, int32_t *idx, float *wts, float *probs, int acc,
+                        const mm_fixed_ws *fx) {
     const mm_moe_config *g = &c->moe;
     const int H = g->hidden_size, E = g->n_routed_experts, K = g->n_experts_per_tok;
     const int I = g->moe_inter_size, S = g->n_shared_experts * I;
@@ -357,7 +373,7 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const size_t o_i = plan_take(&p, (size_t)T * K * sizeof(int32_t));
     const size_t o_w = plan_take(&p, (size_t)T * K * sizeof(float));
     char *ws;
-    int st = mm_workspace(c, p.off, (void **)&ws);
+    int st = take_ws(c, fx, p.off, &ws);
     if (st) return st;
     float *hcat = (float *)(ws + o_h);
     if (!idx) idx = (int32_t *)(ws + o_i);
@@ -432,7 +448,7 @@ static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled
 
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
-                        const mm_moe_i8_debug *dbg) {
+                        const mm_moe_i8_debug *dbg, const mm_fixed_ws *fx) {
     const mm_moe_config *g = &c->moe;
     const size_t H = g->hidden_size, E = g->n_routed_experts, K = g->n_experts_per_tok;
     const size_t I = g->moe_inter_size, S = (size_t)g->n_shared_experts * I;
@@ -450,7 +466,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
 #undef SPARE
     const size_t o_w = plan_take(&p, R * 4), o_lg = plan_take(&p, logits ? 0 : (size_t)T * E * 4);
     char *ws;
-    int st = mm_workspace(c, p.off, (void **)&ws);
+    int st = take_ws(c, fx, p.off, &ws);
     if (st) return st;
     if (!idx) idx = (int32_t *)(ws + o_i);
     if (!wts) wts = (float *)(ws + o_w);
@@ -598,7 +614,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
 
 static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, const float *logits,
                    int32_t *topk_idx, float *topk_w, float *probs, unsigned flags,
-                   const mm_moe_i8_debug *dbg) {
+                   const mm_moe_i8_debug *dbg, const mm_fixed_ws *fx) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: NULL context");
     if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_forward: call mm_moe_init first");
     if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded)
@@ -615,13 +631,13 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
     if (flags & MM_FWD_INT8) {
         if (!(L->formats & MM_LOAD_INT8))
             return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no int8 weights", layer);
-        return forward_int8(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc, dbg);
+        return forward_int8(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc, dbg, fx);
     }
     if (dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: debug outputs need MM_FWD_INT8");
     if (!(L->formats & MM_LOAD_BF16))
         return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no bf16 weights", layer);
     if (xn == out) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: bf16 path needs out != xn");
-    return forward_bf16(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc);
+    return forward_bf16(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc, fx);
 }
 
 int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
@@ -653,7 +669,13 @@ int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
 int mm_moe_forward_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,
                        const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                        unsigned flags) {
-    return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags, NULL);
+    return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags, NULL, NULL);
+}
+
+int mm_moe_forward_fixed(mm_ctx *c, int layer, int T, const float *xn, float *out,
+                         const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
+                         unsigned flags, const mm_fixed_ws *fx) {
+    return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags, NULL, fx);
 }
 
 int mm_moe_forward_i8_debug_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,
@@ -661,7 +683,7 @@ int mm_moe_forward_i8_debug_dev(mm_ctx *c, int layer, int T, const float *xn, fl
                                 float *probs, unsigned flags, const mm_moe_i8_debug *dbg) {
     if (!dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward_i8_debug_dev: NULL debug block");
     return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags | MM_FWD_INT8,
-                   dbg);
+                   dbg, NULL);
 }
 
 int mm_ffn_compute(mm_ctx *c, int layer, const float *xn, float *out, int *topk_idx,

@@ -130,6 +130,8 @@ def lib():
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
         L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_moe_forward_noalloc_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
+                                                 _vp, C.c_uint]
         L.mm_matmul_bf16_dev.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
         L.mm_mla_init.argtypes = [_vp, C.POINTER(MlaConfig), C.c_int]
         L.mm_mla_load_layer.argtypes = [_vp, C.c_int, _vp, C.c_uint]
