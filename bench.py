@@ -365,15 +365,17 @@ def bench_attn_layer(ctx_unused, steps, warmup, L=4096, NH=16):
     return res
 
 
-def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
+def bench_engine(steps, warmup, B=64, prompt=64, gen=64, prefill_len=2048):
     """End-to-end greedy decoding of a DeepSeek-V2-Lite-shaped model (27
     layers: a dense SwiGLU layer 0 (intermediate 10944), 26 MoE layers with
     int8 experts, vocabulary 102400; random weights generated on the device)
     through the batched engine: (1) one decode step of B slots at context
-    `prompt` (the steady-state step) and of one slot (latency), (2)
-    mm_engine_generate over B requests
-    of `prompt` tokens generating `gen` tokens each (prompts consumed by the
-    same decode steps, continuous batching over B slots)."""
+    `prompt` (the steady-state step) and of one slot (latency), (2) the
+    batched prefill of one `prefill_len`-token prompt in one step
+    (mm_engine_step_rows: every layer over all prompt rows, the int8 grouped
+    GEMM at T = prefill_len), (3) mm_engine_generate over B requests of
+    `prompt` tokens generating `gen` tokens each (prompts prefilled in
+    chunks beside the decode rows, continuous batching over B slots)."""
     from mlamoe.engine import Engine
     NL, DI, V, NH, QKN, QKR, KVL, VHD = 27, 10944, 102400, 16, 128, 64, 512, 128
     QD, KVD = NH * (QKN + QKR), KVL + QKR
@@ -411,8 +413,9 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
         for b in list(stage.values()) + [kvb]:
             b.free()
             ctx._bufs.remove(b)
-        max_seq = prompt + gen + 8
-        cfg = mlamoe.EngineConfig(NL, 1, H, DI, V, 1e-6, B, max_seq, mlamoe.MM_FWD_INT8)
+        max_seq = max(prompt + gen + 8, prefill_len + 8)
+        cfg = mlamoe.EngineConfig(NL, 1, H, DI, V, 1e-6, B, max_seq, mlamoe.MM_FWD_INT8, 0,
+                                  prefill_len)
         h = C.c_void_p()
         mlamoe._check(lib.mm_engine_create(ctx.h, C.byref(cfg), C.byref(h)))
         eng = Engine(ctx, h.value, cfg, [])
@@ -438,6 +441,17 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
             for _ in range(steps):
                 eng.step(toks[:1], pos[:1])
             step1_ms = (time.perf_counter() - t0) * 1e3 / steps
+            log(f"[engine] prefill of one {prefill_len}-token prompt in one step")
+            ptoks = rng.integers(0, V, prefill_len).astype(np.int32)
+            pslots = np.zeros(prefill_len, np.int32)
+            ppos = np.arange(prefill_len, dtype=np.int32)
+            last = np.array([prefill_len - 1], np.int32)
+            for _ in range(max(1, warmup)):
+                eng.step_rows(pslots, ptoks, ppos, last)
+            t0 = time.perf_counter()
+            for _ in range(max(2, steps // 4)):
+                eng.step_rows(pslots, ptoks, ppos, last)
+            prefill_ms = (time.perf_counter() - t0) * 1e3 / max(2, steps // 4)
             prompts = [rng.integers(0, V, prompt).astype(np.int32) for _ in range(B)]
             log(f"[engine] generate: {B} requests x ({prompt} prompt + {gen} generated) tokens")
             eng.generate(prompts[:2], 2)                      # warm the generate path
@@ -449,6 +463,8 @@ def bench_engine(steps, warmup, B=64, prompt=64, gen=64):
     return dict(model="DeepSeek-V2-Lite shape, 27 layers, int8 experts, random weights",
                 step_B=B, step_context=prompt + 1, step_ms=step_ms, step_tok_s=B / (step_ms * 1e-3),
                 step_B1_ms=step1_ms, step_B1_tok_s=1.0 / (step1_ms * 1e-3),
+                prefill_tokens=prefill_len, prefill_ms=prefill_ms,
+                prefill_tok_s=prefill_len / (prefill_ms * 1e-3),
                 generate_requests=B, generate_prompt=prompt, generate_new=gen,
                 generate_tokens=total, generate_s=gen_s, generate_tok_s=total / gen_s,
                 generate_steps=prompt + gen - 1,

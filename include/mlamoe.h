@@ -388,6 +388,8 @@ typedef struct {
     int init_seq;            /* positions per slot allocated at creation (0: the
                                 smaller of max_seq and 1024); the latent caches
                                 grow on demand up to max_seq */
+    int max_rows;            /* token rows one step may carry, prompt chunks
+                                included (0: the larger of max_batch and 1024) */
 } mm_engine_config;
 
 /* One layer's non-expert weights, device pointers (ModelWeights,
@@ -436,13 +438,33 @@ MM_API int mm_engine_set_head(mm_engine *e, const uint16_t *embed, const uint16_
 MM_API int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *pos,
                           int32_t *next, float *logits);
 
+/* One step over R token rows (R <= max_rows), the batched prefill of
+ * forward_unabsorbed (src/run.c:189-370; its GPU form, gpu_forward_unabsorbed
+ * + batched_gpu_ffn, src/getp_run.hip:394-460, 558-701) and decode rows in
+ * one pass: row r is token tokens[r] at position pos[r] of slot slots[r]
+ * (host arrays).  Every row's latent-cache entry is written before any row
+ * attends, so a slot may contribute several consecutive positions (a prompt
+ * chunk, attended causally: row r sees positions [0, pos[r]] of its slot),
+ * and other slots may decode in the same step.  A (slot, position) pair may
+ * appear once per step; a slot's positions below its rows must hold its
+ * earlier tokens.  The attention is the absorbed form, equal to the
+ * reference's unabsorbed prefill in exact arithmetic (src/run.c:375-378).
+ * The n_want rows listed in want_rows (ascending) are normed, projected to
+ * the vocabulary and sampled: next[j] receives row want_rows[j]'s greedy
+ * token, logits (device [n_want, vocab]) its logits, or NULL.  Synchronous. */
+MM_API int mm_engine_step_rows(mm_engine *e, int R, const int32_t *slots, const int32_t *tokens,
+                               const int32_t *pos, int n_want, const int32_t *want_rows,
+                               int32_t *next, float *logits);
+
 /* Continuous-batching greedy generation, the work of the reference's
  * inference() (src/getp_run.hip:920-995) for n_req prompts (token ids):
- * every step decodes one token of each active slot (a prompt token while
- * the prompt lasts -- the absorbed decode is exact for prefill, run.c:375-378
- * -- then the previous step's sample), a finished slot takes the next
- * waiting request.  Request r stops after max_steps generated tokens, at
- * eos (not stored; eos < 0: none) or when max_seq positions are used.
+ * every step carries one decode row per slot past its prompt (the previous
+ * step's sample) and, in the rows left up to max_rows, the next chunk of
+ * the prompts still being prefilled (mm_engine_step_rows); a slot whose
+ * prompt ends in a step samples its first token there, and a finished slot
+ * takes the next waiting request.  Request r stops after max_steps
+ * generated tokens, at eos (not stored; eos < 0: none) or when max_seq
+ * positions are used.
  * out_tokens[r] (capacity max_steps) and out_lens[r] receive its tokens.
  * Returns the total generated (>= 0) or a negative status. */
 MM_API long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prompts,

@@ -31,10 +31,15 @@ struct mm_engine {
     uint16_t **cache;          /* [n_layers] device [max_batch, lcap[l], KVL+QKR] bf16 */
     int *lcap;                 /* [n_layers] positions per slot of each layer's cache */
     int cap;                   /* positions every layer holds: min of lcap */
-    float *x, *xn, *q, *ctxo, *g, *u;
-    int32_t *d_io;             /* device [4][max_batch]: tokens, pos, kv_lens, next */
+    int max_rows;              /* token rows per step */
+    float *x, *xn, *q, *ctxo, *g, *u;   /* [max_rows, ...] step activations */
+    int32_t *d_io;             /* device [IO_ARRAYS][max_rows]: see IO_* */
     int32_t *h_io;             /* pinned host, same layout */
+    int32_t *last_pos;         /* [max_batch] host: a step's check of its rows' positions */
 };
+
+/* the per-row arrays of a step, device and pinned host */
+enum { IO_TOK, IO_POS, IO_LEN, IO_SLOT, IO_WANT, IO_NEXT, IO_ARRAYS };
 
 void mm_engine_destroy(mm_engine *e) {
     if (!e) return;
@@ -48,6 +53,7 @@ void mm_engine_destroy(mm_engine *e) {
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (e->h_io) hipHostFree(e->h_io);
+    free(e->last_pos);
     free(e->lcap);
     free(e->layers);
     free(e->layer_set);
@@ -141,21 +147,34 @@ int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
     }
     const mm_mla_config *g = &c->mla;
     const size_t B = (size_t)cfg->max_batch, H = (size_t)cfg->hidden_size;
+    if (cfg->max_rows < 0) {
+        mm_engine_destroy(e);
+        return mm_fail(MM_ERR_INVALID, "mm_engine_create: max_rows < 0");
+    }
+    e->max_rows = cfg->max_rows ? cfg->max_rows : (cfg->max_batch > 1024 ? cfg->max_batch : 1024);
+    if (e->max_rows < cfg->max_batch) e->max_rows = cfg->max_batch;
+    const size_t MR = (size_t)e->max_rows;
     const size_t KVD = (size_t)g->kv_lora_rank + g->qk_rope_head_dim;
     const size_t QD = (size_t)g->n_heads * (g->qk_nope_head_dim + g->qk_rope_head_dim);
     const size_t DI = cfg->first_k_dense > 0 ? (size_t)cfg->dense_inter_size : 8;
     struct { void **p; size_t n; } bufs[] = {
-        {(void **)&e->x, B * H * 4}, {(void **)&e->xn, B * H * 4}, {(void **)&e->q, B * QD * 4},
-        {(void **)&e->ctxo, B * (size_t)g->n_heads * g->v_head_dim * 4},
-        {(void **)&e->g, B * DI * 4}, {(void **)&e->u, B * DI * 4}, {(void **)&e->d_io, 4 * B * 4}};
+        {(void **)&e->x, MR * H * 4}, {(void **)&e->xn, MR * H * 4}, {(void **)&e->q, MR * QD * 4},
+        {(void **)&e->ctxo, MR * (size_t)g->n_heads * g->v_head_dim * 4},
+        {(void **)&e->g, MR * DI * 4}, {(void **)&e->u, MR * DI * 4},
+        {(void **)&e->d_io, IO_ARRAYS * MR * 4}};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         if (hipMalloc(bufs[i].p, bufs[i].n) != hipSuccess) {
             mm_engine_destroy(e);
-            return mm_fail(MM_ERR_NOMEM, "mm_engine_create: step buffers");
+            return mm_fail(MM_ERR_NOMEM, "mm_engine_create: step buffers for %zu rows", MR);
         }
-    if (hipHostMalloc((void **)&e->h_io, 4 * B * 4, 0) != hipSuccess) {
+    if (hipHostMalloc((void **)&e->h_io, IO_ARRAYS * MR * 4, 0) != hipSuccess) {
         mm_engine_destroy(e);
         return mm_fail(MM_ERR_NOMEM, "mm_engine_create: pinned host buffer");
+    }
+    e->last_pos = malloc(B * sizeof(int32_t));
+    if (!e->last_pos) {
+        mm_engine_destroy(e);
+        return mm_fail(MM_ERR_NOMEM, "mm_engine_create: malloc");
     }
     if (cfg->init_seq < 0 || cfg->init_seq > cfg->max_seq) {
         mm_engine_destroy(e);
@@ -222,65 +241,127 @@ static int dense_ffn(mm_engine *e, const mm_engine_layer *L, int B) {
     return mm_matmul_bf16_dev(c, e->x, e->g, L->dense_down, H, DI, B, MM_MATMUL_ACCUMULATE);
 }
 
+/* One step over R rows (h_io filled: tokens, positions, slots; want rows):
+ * embedding, every layer over all rows, the LM head over the wanted rows. */
+static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *logits) {
+    mm_ctx *c = e->c;
+    const mm_engine_config *f = &e->cfg;
+    const int MR = e->max_rows;
+    int32_t *hio = e->h_io;
+    int kvmax = 1;
+    for (int b = 0; b < f->max_batch; b++) e->last_pos[b] = -1;
+    for (int r = 0; r < R; r++) {
+        const int s = hio[IO_SLOT * MR + r], p = hio[IO_POS * MR + r];
+        if (s < 0 || s >= f->max_batch)
+            return mm_fail(MM_ERR_INVALID, "mm_engine_step: row %d: slot %d outside [0, %d)", r, s,
+                           f->max_batch);
+        if (p < 0 || p >= f->max_seq)
+            return mm_fail(MM_ERR_INVALID, "mm_engine_step: row %d: pos %d outside [0, %d)", r, p,
+                           f->max_seq);
+        /* a slot's rows in ascending positions: no cache row written twice */
+        if (p <= e->last_pos[s])
+            return mm_fail(MM_ERR_INVALID, "mm_engine_step: row %d: slot %d position %d not above "
+                           "its previous row's", r, s, p);
+        e->last_pos[s] = p;
+        hio[IO_LEN * MR + r] = p + 1;
+        if (p + 1 > kvmax) kvmax = p + 1;
+    }
+    for (int j = 0; j < n_want; j++) {
+        const int w = hio[IO_WANT * MR + j];
+        if (w < 0 || w >= R || (j > 0 && w <= hio[IO_WANT * MR + j - 1]))
+            return mm_fail(MM_ERR_INVALID, "mm_engine_step: want_rows must ascend within [0, %d)", R);
+    }
+    int st = mm_engine_reserve(e, kvmax);
+    if (st) return st;
+    if ((st = mm_set_device(c))) return st;
+    int32_t *d_tok = e->d_io + IO_TOK * MR, *d_pos = e->d_io + IO_POS * MR;
+    int32_t *d_len = e->d_io + IO_LEN * MR, *d_slot = e->d_io + IO_SLOT * MR;
+    int32_t *d_want = e->d_io + IO_WANT * MR, *d_next = e->d_io + IO_NEXT * MR;
+    MM_HIP(hipMemcpyAsync(e->d_io, hio, (size_t)IO_NEXT * MR * 4, hipMemcpyHostToDevice, c->stream));
+    const mm_mla_config *g = &c->mla;
+    const int H = f->hidden_size;
+    mm_embed_args ea = {e->embed, d_tok, e->x, H, f->vocab_size};
+    if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)R, 1, 256, 0, &ea))) return st;
+    for (int l = 0; l < f->n_layers; l++) {
+        const mm_engine_layer *L = &e->layers[l];
+        if ((st = mm_mla_front_rows(c, R, e->x, &L->front, d_pos, d_slot, e->q, e->cache[l], e->lcap[l],
+                                    NULL)))
+            return st;
+        if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
+                                     e->ctxo, NULL, NULL, NULL)))
+            return st;
+        if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, g->n_heads * g->v_head_dim, R,
+                                     MM_MATMUL_ACCUMULATE)))
+            return st;
+        if (l < f->first_k_dense) {
+            if ((st = dense_ffn(e, L, R))) return st;
+        } else {
+            mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, f->rms_eps};
+            if ((st = mm_launch(c, K_RMSNORM, (unsigned)R, 1, 1, 256, 0, &ra))) return st;
+            if ((st = mm_moe_forward_dev(c, l, R, e->xn, e->x, NULL, NULL, NULL, NULL,
+                                         f->moe_flags | MM_FWD_ACCUMULATE)))
+                return st;
+        }
+    }
+    if (n_want > 0) {
+        /* the sampled rows, gathered (xn is free by now) unless they are all rows */
+        const float *xs = e->x;
+        if (n_want < R) {
+            mm_gather_rows_args ga = {e->x, d_want, e->xn, n_want, H};
+            if ((st = mm_launch(c, K_GATHER_ROWS, (unsigned)n_want, 1, 1, 256, 0, &ga))) return st;
+            xs = e->xn;
+        }
+        if ((st = mm_lm_head_dev(c, n_want, xs, e->final_norm, f->rms_eps, e->lm_head, f->vocab_size,
+                                 H, logits, d_next)))
+            return st;
+        MM_HIP(hipMemcpyAsync(hio + IO_NEXT * MR, d_next, (size_t)n_want * 4, hipMemcpyDeviceToHost,
+                              c->stream));
+    }
+    MM_HIP(hipStreamSynchronize(c->stream));
+    if (n_want > 0) memcpy(next, hio + IO_NEXT * MR, (size_t)n_want * 4);
+    return MM_OK;
+}
+
+static int engine_ready(const mm_engine *e, const char *fn) {
+    if (!e->embed) return mm_fail(MM_ERR_STATE, "%s: call mm_engine_set_head first", fn);
+    for (int l = 0; l < e->cfg.n_layers; l++)
+        if (!e->layer_set[l]) return mm_fail(MM_ERR_STATE, "%s: layer %d not set", fn, l);
+    return MM_OK;
+}
+
 int mm_engine_step(mm_engine *e, int B, const int32_t *tokens, const int32_t *pos, int32_t *next,
                    float *logits) {
     if (!e || !tokens || !pos || !next) return mm_fail(MM_ERR_INVALID, "mm_engine_step: NULL argument");
     if (B < 1 || B > e->cfg.max_batch)
         return mm_fail(MM_ERR_INVALID, "mm_engine_step: B = %d outside [1, %d]", B, e->cfg.max_batch);
-    if (!e->embed) return mm_fail(MM_ERR_STATE, "mm_engine_step: call mm_engine_set_head first");
-    for (int l = 0; l < e->cfg.n_layers; l++)
-        if (!e->layer_set[l]) return mm_fail(MM_ERR_STATE, "mm_engine_step: layer %d not set", l);
-    mm_ctx *c = e->c;
-    const mm_engine_config *f = &e->cfg;
-    const int MB = f->max_batch;
-    int kvmax = 1;
-    for (int b = 0; b < B; b++) {
-        if (pos[b] < 0 || pos[b] >= f->max_seq)
-            return mm_fail(MM_ERR_INVALID, "mm_engine_step: pos[%d] = %d outside [0, %d)", b, pos[b],
-                           f->max_seq);
-        if (pos[b] + 1 > kvmax) kvmax = pos[b] + 1;
-    }
-    int st = mm_engine_reserve(e, kvmax);
+    int st = engine_ready(e, "mm_engine_step");
     if (st) return st;
+    const int MR = e->max_rows;
     for (int b = 0; b < B; b++) {
-        e->h_io[b] = tokens[b];
-        e->h_io[MB + b] = pos[b];
-        e->h_io[2 * MB + b] = pos[b] + 1;
+        e->h_io[IO_TOK * MR + b] = tokens[b];
+        e->h_io[IO_POS * MR + b] = pos[b];
+        e->h_io[IO_SLOT * MR + b] = b;
+        e->h_io[IO_WANT * MR + b] = b;
     }
-    if ((st = mm_set_device(c))) return st;
-    int32_t *d_tok = e->d_io, *d_pos = e->d_io + MB, *d_len = e->d_io + 2 * MB, *d_next = e->d_io + 3 * MB;
-    MM_HIP(hipMemcpyAsync(e->d_io, e->h_io, (size_t)3 * MB * 4, hipMemcpyHostToDevice, c->stream));
-    const mm_mla_config *g = &c->mla;
-    const int H = f->hidden_size;
-    mm_embed_args ea = {e->embed, d_tok, e->x, H, f->vocab_size};
-    if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)B, 1, 256, 0, &ea))) return st;
-    for (int l = 0; l < f->n_layers; l++) {
-        const mm_engine_layer *L = &e->layers[l];
-        if ((st = mm_mla_front_dev(c, B, e->x, &L->front, d_pos, e->q, e->cache[l], e->lcap[l], NULL)))
-            return st;
-        if ((st = mm_mla_absorbed_decode_dev(c, l, B, e->q, e->cache[l], e->lcap[l], d_len, kvmax,
-                                             e->ctxo, NULL, NULL, NULL)))
-            return st;
-        if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, g->n_heads * g->v_head_dim, B,
-                                     MM_MATMUL_ACCUMULATE)))
-            return st;
-        if (l < f->first_k_dense) {
-            if ((st = dense_ffn(e, L, B))) return st;
-        } else {
-            mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, f->rms_eps};
-            if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
-            if ((st = mm_moe_forward_dev(c, l, B, e->xn, e->x, NULL, NULL, NULL, NULL,
-                                         f->moe_flags | MM_FWD_ACCUMULATE)))
-                return st;
-        }
-    }
-    if ((st = mm_lm_head_dev(c, B, e->x, e->final_norm, f->rms_eps, e->lm_head, f->vocab_size, H,
-                             logits, d_next)))
-        return st;
-    MM_HIP(hipMemcpyAsync(e->h_io + 3 * MB, d_next, (size_t)B * 4, hipMemcpyDeviceToHost, c->stream));
-    MM_HIP(hipStreamSynchronize(c->stream));
-    memcpy(next, e->h_io + 3 * MB, (size_t)B * 4);
-    return MM_OK;
+    return engine_run(e, B, B, next, logits);
+}
+
+int mm_engine_step_rows(mm_engine *e, int R, const int32_t *slots, const int32_t *tokens,
+                        const int32_t *pos, int n_want, const int32_t *want_rows, int32_t *next,
+                        float *logits) {
+    if (!e || !slots || !tokens || !pos || (n_want > 0 && (!want_rows || !next)))
+        return mm_fail(MM_ERR_INVALID, "mm_engine_step_rows: NULL argument");
+    if (R < 1 || R > e->max_rows || n_want < 0 || n_want > R)
+        return mm_fail(MM_ERR_INVALID, "mm_engine_step_rows: R = %d outside [1, %d] or n_want = %d "
+                       "outside [0, R]", R, e->max_rows, n_want);
+    int st = engine_ready(e, "mm_engine_step_rows");
+    if (st) return st;
+    const int MR = e->max_rows;
+    memcpy(e->h_io + IO_TOK * MR, tokens, (size_t)R * 4);
+    memcpy(e->h_io + IO_POS * MR, pos, (size_t)R * 4);
+    memcpy(e->h_io + IO_SLOT * MR, slots, (size_t)R * 4);
+    if (n_want) memcpy(e->h_io + IO_WANT * MR, want_rows, (size_t)n_want * 4);
+    return engine_run(e, R, n_want, next, logits);
 }
 
 long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prompts,
@@ -288,18 +369,23 @@ long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prom
                              int32_t *const *out_tokens, int32_t *out_lens) {
     if (!e || n_req < 0 || (n_req > 0 && (!prompts || !prompt_lens || !out_tokens || !out_lens)))
         return mm_fail(MM_ERR_INVALID, "mm_engine_generate: NULL argument");
-    const int MB = e->cfg.max_batch;
+    int st = engine_ready(e, "mm_engine_generate");
+    if (st) return st;
+    const int MB = e->cfg.max_batch, MR = e->max_rows;
+    /* per slot: request, token budget, next position to feed, last sample */
     int *req = malloc((size_t)MB * sizeof(int)), *limit = malloc((size_t)MB * sizeof(int));
-    int32_t *tok = malloc((size_t)MB * 4), *pos = malloc((size_t)MB * 4), *nxt = malloc((size_t)MB * 4);
-    int32_t *last = malloc((size_t)MB * 4);
-    if (!req || !limit || !tok || !pos || !nxt || !last) {
-        free(req); free(limit); free(tok); free(pos); free(nxt); free(last);
+    int *npos = malloc((size_t)MB * sizeof(int)), *wslot = malloc((size_t)MR * sizeof(int));
+    int32_t *last = malloc((size_t)MB * 4), *nxt = malloc((size_t)MR * 4);
+    if (!req || !limit || !npos || !wslot || !last || !nxt) {
+        free(req); free(limit); free(npos); free(wslot); free(last); free(nxt);
         return mm_fail(MM_ERR_NOMEM, "mm_engine_generate: malloc");
     }
+    int32_t *rtok = e->h_io + IO_TOK * MR, *rpos = e->h_io + IO_POS * MR;
+    int32_t *rslot = e->h_io + IO_SLOT * MR, *rwant = e->h_io + IO_WANT * MR;
     for (int s = 0; s < MB; s++) req[s] = -1;
     for (int r = 0; r < n_req; r++) out_lens[r] = 0;
     long long total = 0;
-    int next_req = 0, st = MM_OK;
+    int next_req = 0;
     for (;;) {
         /* admit waiting requests into free slots (lowest first) */
         for (int s = 0; s < MB && next_req < n_req && !st; s++) {
@@ -316,44 +402,56 @@ long long mm_engine_generate(mm_engine *e, int n_req, const int32_t *const *prom
                 if ((st = mm_engine_reserve(e, n + lim - 1))) break;
                 req[s] = r;
                 limit[s] = lim;
-                pos[s] = 0;
+                npos[s] = 0;
                 break;
             }
         }
         if (st) break;
-        int hi = -1;
-        for (int s = 0; s < MB; s++)
-            if (req[s] >= 0) hi = s;
-        if (hi < 0) break;
-        const int B = hi + 1;
-        for (int s = 0; s < B; s++) {
-            if (req[s] < 0) {
-                tok[s] = 0;
-                pos[s] = 0;
-                continue;
-            }
-            const int r = req[s];
-            tok[s] = pos[s] < prompt_lens[r] ? prompts[r][pos[s]] : last[s];
+        /* the step's rows: one decode row per slot past its prompt, then the
+         * prompts' next chunks in the rows left */
+        int R = 0, nw = 0;
+        for (int s = 0; s < MB; s++) {
+            if (req[s] < 0 || npos[s] < prompt_lens[req[s]]) continue;
+            rslot[R] = s;
+            rpos[R] = npos[s];
+            rtok[R] = last[s];
+            wslot[nw] = s;
+            rwant[nw++] = R++;
         }
-        if ((st = mm_engine_step(e, B, tok, pos, nxt, NULL))) break;
-        for (int s = 0; s < B; s++) {
+        for (int s = 0; s < MB && R < MR; s++) {
             if (req[s] < 0) continue;
-            const int r = req[s];
-            int done = 0;
-            if (pos[s] >= prompt_lens[r] - 1) {           /* this step sampled a token */
-                if (eos >= 0 && nxt[s] == eos) {
-                    done = 1;
-                } else {
-                    out_tokens[r][out_lens[r]++] = nxt[s];
-                    total++;
-                    last[s] = nxt[s];
-                    done = out_lens[r] >= limit[s];
-                }
+            const int n = prompt_lens[req[s]];
+            if (npos[s] >= n) continue;
+            const int k = n - npos[s] < MR - R ? n - npos[s] : MR - R;
+            for (int i = 0; i < k; i++) {
+                rslot[R + i] = s;
+                rpos[R + i] = npos[s] + i;
+                rtok[R + i] = prompts[req[s]][npos[s] + i];
             }
-            pos[s]++;
+            R += k;
+            if (npos[s] + k == n) {          /* the prompt's last row samples */
+                wslot[nw] = s;
+                rwant[nw++] = R - 1;
+            }
+        }
+        if (R == 0) break;
+        if ((st = engine_run(e, R, nw, nxt, NULL))) break;
+        /* positions fed this step */
+        for (int i = 0; i < R; i++) npos[rslot[i]] = rpos[i] + 1;
+        for (int j = 0; j < nw; j++) {
+            const int s = wslot[j], r = req[s];
+            int done;
+            if (eos >= 0 && nxt[j] == eos) {
+                done = 1;
+            } else {
+                out_tokens[r][out_lens[r]++] = nxt[j];
+                total++;
+                last[s] = nxt[j];
+                done = out_lens[r] >= limit[s];
+            }
             if (done) req[s] = -1;
         }
     }
-    free(req); free(limit); free(tok); free(pos); free(nxt); free(last);
+    free(req); free(limit); free(npos); free(wslot); free(last); free(nxt);
     return st ? (long long)st : total;
 }

@@ -46,6 +46,7 @@ typedef enum {
     K_GEMM_SKINNY,
     K_SKINNY_REDUCE,
     K_ZERO32,
+    K_GATHER_ROWS,
     K_COUNT
 } mm_kernel_id;
 
@@ -161,6 +162,17 @@ int mm_gemm_bf16_ws(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, in
  * for `rows` output rows in total. */
 unsigned mm_gemv_blocks(int rows);
 int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
+
+/* mm_mla_front_dev / mm_mla_absorbed_decode_dev with row b on cache
+ * sequence slots[b] (slots NULL: sequence b): rows of one sequence may share
+ * a call (prefill chunks), causality coming from each row's position /
+ * kv_lens[b]. */
+int mm_mla_front_rows(mm_ctx *ctx, int B, const float *x, const mm_mla_front_weights *w,
+                      const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
+                      int seq_stride, float *kv_rows);
+int mm_mla_decode_rows(mm_ctx *ctx, int layer, int B, const float *q, const uint16_t *cache,
+                       int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
+                       float *ctx_out, float *qabs, float *probs, float *clat);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

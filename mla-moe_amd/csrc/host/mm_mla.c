@@ -68,6 +68,13 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                                const uint16_t *cache, int seq_stride, const int32_t *kv_lens,
                                int kv_len, float *ctx_out, float *qabs, float *probs,
                                float *clat) {
+    return mm_mla_decode_rows(c, layer, B, q, cache, seq_stride, NULL, kv_lens, kv_len, ctx_out,
+                              qabs, probs, clat);
+}
+
+int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
+                       int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
+                       float *ctx_out, float *qabs, float *probs, float *clat) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
     if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
         return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
@@ -116,7 +123,7 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                         0, &qa)))
         return st;
     mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
-                           part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk};
+                           part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
@@ -192,6 +199,12 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                      const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
                      float *kv_rows) {
+    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows);
+}
+
+int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
+                      const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
+                      int seq_stride, float *kv_rows) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL context");
     if (!c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_dev: call mm_mla_front_init first");
     if (B < 0) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: B < 0");
@@ -253,6 +266,6 @@ int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weight
     }
     mm_mla_rope_args r = {q, comp, w->kv_a_norm, c->front_inv, pos, cache, kv_rows, B, NH,
                           g->qk_nope_head_dim, g->qk_rope_head_dim, g->kv_lora_rank, seq_stride,
-                          f->rope_interleaved, f->mla_norm_eps};
+                          f->rope_interleaved, f->mla_norm_eps, slots};
     return mm_launch(c, K_MLA_ROPE, (unsigned)B, 1, 1, 256, 0, &r);
 }

@@ -50,6 +50,8 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     int st = mm_set_device(c);
     if (st) return st;
     MM_HIP(hipMalloc((void **)&c->moe_cnt, (size_t)E * sizeof(int32_t)));
+    MM_HIP(hipMemsetAsync(c->moe_cnt, 0, (size_t)E * sizeof(int32_t), c->stream));
+    MM_HIP(hipStreamSynchronize(c->stream));
     MM_HIP(hipMalloc((void **)&c->ffn_io, (2 * (size_t)H + 2 * (size_t)K) * sizeof(float)));
     c->layers = calloc((size_t)n_layers, sizeof(mm_moe_layer));
     if (!c->layers) return mm_fail(MM_ERR_NOMEM, "mm_moe_init: calloc");
@@ -446,6 +448,15 @@ static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled
     return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
 }
 
+/* A tiled call that fails after its routing launch leaves rows counted in
+ * the per-expert counters that its combine would have cleared: clear them
+ * here (best effort: the launch itself may be what fails) and return st. */
+static int clear_counters(mm_ctx *c, int st) {
+    mm_zero32_args za = {(uint32_t *)c->moe_cnt, (uint64_t)c->moe.n_routed_experts};
+    (void)mm_launch(c, K_ZERO32, 1, 1, 1, 256, 0, &za);
+    return st;
+}
+
 static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
                         const mm_moe_i8_debug *dbg, const mm_fixed_ws *fx) {
@@ -519,15 +530,16 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ra.x = xn;
     ra.qx = qx;
     ra.sx = sx;
-    if (tiled) {
-        /* the route kernel appends to the per-expert counters: clear them
-         * first, in stream order, so no earlier call's state is carried */
-        mm_zero32_args za = {(uint32_t *)c->moe_cnt, E};
-        if ((st = mm_launch(c, K_ZERO32, 1, 1, 1, 256, 0, &za))) return st;
-    }
+    /* the route kernel appends to the per-expert counters (zero on entry:
+     * cleared at init and by every tiled call's combine); a failure after it
+     * clears them itself (FAIL_ROUTED) */
     if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
                         64 * MM_I8_RT_WAVES, 0, &ra)))
-        return st;
+        return tiled ? clear_counters(c, st) : st;
+#define FAIL_ROUTED(call)                                   \
+    do {                                                    \
+        if ((st = (call))) return tiled ? clear_counters(c, st) : st; \
+    } while (0)
 
     mm_i8_gemm_args ga;
     memset(&ga, 0, sizeof(ga));
@@ -553,21 +565,19 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                                (int)E, (int)I, (int)H, 1, (int)R};
         mm_i8_tiled_args ts = {L->i8.sgu, 0, L->i8.ss_g, L->i8.ss_u, 0, NULL, NULL, qx, sx, 0,
                                hs, NULL, T, (int)K, 1, (int)S, (int)H, 1, T};
-        if ((st = launch_tiled(c, &ta, S ? &ts : NULL))) return st;
+        FAIL_ROUTED(launch_tiled(c, &ta, S ? &ts : NULL));
     } else {
         /* shared-expert blocks (row-tile waves), then every routed unit */
         const size_t per_blk = (size_t)MM_I8S_W * MM_I8S_SEG;
         const unsigned nb = (unsigned)((S ? sh_blocks(ceil_div(S / 16, per_blk)) : 0) +
                                        E * ceil_div(I / 16, per_blk));
         /* dynamic LDS: the 16-row A tile, 16 * K bytes */
-        if ((st = mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H + 4 * (size_t)T, &ga)))
-            return st;
+        FAIL_ROUTED(mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H + 4 * (size_t)T, &ga));
     }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
                                 S ? T : 0, (int)S};
-    if ((st = mm_launch(c, K_I8_QUANT_H, (unsigned)((R + (S ? T : 0) + 3) / 4), 1, 1, 256, 0, &qa)))
-        return st;
+    FAIL_ROUTED(mm_launch(c, K_I8_QUANT_H, (unsigned)((R + (S ? T : 0) + 3) / 4), 1, 1, 256, 0, &qa));
 
     if (tiled) {
         mm_i8_tiled_args td = {L->i8.d, H * I, L->i8.s_d, NULL, (int)H, c->moe_cnt, rows, qh, sh,
@@ -575,7 +585,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                                0, (int)R};
         mm_i8_tiled_args tsd = {L->i8.sdn, 0, L->i8.ss_d, NULL, 0, NULL, NULL, qhs, shs, 1, ys,
                                 NULL, T, (int)K, 1, (int)H, (int)S, 0, T};
-        if ((st = launch_tiled(c, &td, S ? &tsd : NULL))) return st;
+        FAIL_ROUTED(launch_tiled(c, &td, S ? &tsd : NULL));
     } else {
         ga.a = qh;
         ga.sa = sh;
@@ -586,13 +596,14 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
         const size_t gpe = ceil_div(H / 16, (size_t)MM_I8S_W * MM_I8S_SEG);
         const unsigned nb = (unsigned)((S ? sh_blocks(gpe) : 0) + E * gpe);
-        if ((st = mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W,
-                            16 * (S > I ? S : I) + 4 * (size_t)T, &ga)))
-            return st;
+        FAIL_ROUTED(mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W,
+                              16 * (S > I ? S : I) + 4 * (size_t)T, &ga));
     }
 
-    mm_i8_combine_args ca = {y, ys, wts, out, T, (int)H, (int)K, acc, S > 0};
-    if ((st = mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca))) return st;
+    mm_i8_combine_args ca = {y, ys, wts, out, tiled ? c->moe_cnt : NULL, T, (int)H, (int)K,
+                             (int)E, acc, S > 0};
+    FAIL_ROUTED(mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca));
+#undef FAIL_ROUTED
 
     if (dbg) {
         struct {

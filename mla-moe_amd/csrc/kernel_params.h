@@ -87,6 +87,14 @@ typedef struct {
     int H, vocab;
 } mm_embed_args;
 
+/* dst[j, :] = src[idx[j], :] for n rows of H floats. */
+typedef struct {
+    const float *src;
+    const int32_t *idx;
+    float *dst;
+    int n, H;
+} mm_gather_rows_args;
+
 /* h = silu(g) * u elementwise over n values (the dense SwiGLU MLP). */
 typedef struct {
     const float *g, *u;
@@ -153,12 +161,14 @@ typedef struct {
     int rows2, n2;
 } mm_i8_quant_rows_args;
 
-/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]. */
+/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]; clears cnt[0..E) when
+ * cnt is given (the tiled path's per-expert counters, read by then). */
 typedef struct {
     const float *y, *ys;
     const float *topk_w;
     float *out;
-    int T, H, K;
+    int32_t *cnt;
+    int T, H, K, E;
     int accumulate;
     int has_shared;
 } mm_i8_combine_args;
@@ -269,7 +279,7 @@ typedef struct {
 typedef struct {
     const float *qabs;        /* [B, NH, KVL] */
     const float *q;           /* [B, NH, QKN + QKR] (the q_pe part) */
-    const uint16_t *cache;    /* [B, seq_stride, KVD] bf16 */
+    const uint16_t *cache;    /* [sequences, seq_stride, KVD] bf16 */
     const int32_t *kv_lens;   /* [B] or 0 */
     int kv_len;               /* used when kv_lens == 0 */
     int seq_stride;
@@ -280,6 +290,7 @@ typedef struct {
     int probs_stride;
     int NH, HG, nchunks, QKN;
     int chunk;                /* keys per block: a multiple of 16 * MM_MLA_AW, <= MM_MLA_CHUNK */
+    const int32_t *slots;     /* [B] cache sequence of row b, or 0: sequence b */
 } mm_mla_attn_args;
 
 /* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */
@@ -405,10 +416,11 @@ typedef struct {
     const uint16_t *kv_norm; /* [KVL] kv_a_layernorm */
     const float *inv_freq;   /* [QKR / 2] */
     const int32_t *pos;      /* [B] positions */
-    uint16_t *cache;         /* [B, seq_stride, KVL + QKR] bf16 latent cache */
+    uint16_t *cache;         /* [sequences, seq_stride, KVL + QKR] bf16 latent cache */
     float *kv_out;           /* [B, KVL + QKR] fp32 copy of the appended rows, or NULL */
     int B, nh, qkn, qkr, kvl, seq_stride, interleaved;
     float eps;               /* kv_a_layernorm eps */
+    const int32_t *slots;    /* [B] cache sequence of token b, or 0: sequence b */
 } mm_mla_rope_args;
 
 #endif /* MLAMOE_KERNEL_PARAMS_H */

@@ -164,7 +164,9 @@ static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
 static_assert((AW * 16 * OROW + AW * 32) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
 static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
-/* grid (nchunks, B, HG), AW waves; with KPW = a.chunk / AW keys per wave,
+/* grid (nchunks, B, HG), AW waves; row b attends to the first kv_lens[b]
+ * rows of cache sequence slots[b] (b without slots); with KPW = a.chunk / AW
+ * keys per wave,
  * wave w handles keys [chunk * a.chunk + w * KPW, + KPW) in 16-key
  * sub-tiles, each staged into LDS by direct global -> LDS
  * loads one sub-tile ahead of its use (two LDS stages per wave):
@@ -191,7 +193,8 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
     const int kpw = a.chunk / AW;                     /* keys per wave */
     const int kbeg = chunk * a.chunk + w * kpw;
     const int kend = min(kbeg + kpw, L);
-    const uint8_t *cseq = (const uint8_t *)(a.cache + (size_t)b * a.seq_stride * KVD);
+    const int seq = a.slots ? a.slots[b] : b;
+    const uint8_t *cseq = (const uint8_t *)(a.cache + (size_t)seq * a.seq_stride * KVD);
     /* sub-tile at key k0 -> stage st: row p's c_kv (1 KB, one load per lane
      * of 16 B) at p * CROW_B; the k_pe parts (128 B per row) of rows 0..7 and
      * 8..15 as two 1 KB pieces after the c_kv rows.  Rows past L load row
@@ -528,7 +531,8 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_uv(mm_mla_combine_args 
 
 /* ---- decode front: RoPE, kv_a_layernorm, latent-cache append ----------------- */
 
-/* One block per token b at position p = pos[b] (src/run.c:420-428):
+/* One block per token b at position p = pos[b] of cache sequence slots[b]
+ * (b without slots) (src/run.c:420-428):
  *   q_pe of every head   rope_apply(q_h + QKN, p)                (run.c:420-421)
  *   c_kv                 rmsnorm(comp[0:KVL], kv_a_layernorm, eps) (run.c:426)
  *   k_pe                 rope_apply(comp[KVL:KVL+QKR], p)         (run.c:427-428)
@@ -602,7 +606,8 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_rope(mm_mla_rope_args a
 
     /* the cache row */
     const bool wr = p >= 0 && p < a.seq_stride;
-    uint16_t *dst = a.cache + ((size_t)b * a.seq_stride + (wr ? p : 0)) * kvd;
+    const int seq = a.slots ? a.slots[b] : b;
+    uint16_t *dst = a.cache + ((size_t)seq * a.seq_stride + (wr ? p : 0)) * kvd;
     float *ko = a.kv_out ? a.kv_out + (size_t)b * kvd : nullptr;
     for (int i = 2 * tid; i < a.kvl; i += 512) {
         const float y0 = comp[i] * inv * bf16_f32(a.kv_norm[i]);

@@ -695,6 +695,8 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_ar
         if (a.has_shared) acc += ys;
         *op = a.accumulate ? o + acc : acc;
     }
+    if (a.cnt && t == 0)
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
 }
 
 /* ---- weight packing ----------------------------------------------------------- */

@@ -77,6 +77,15 @@ extern "C" __global__ __launch_bounds__(256) void mm_embed(mm_embed_args a) {
         dst[i] = bf16_f32(src[i]);
 }
 
+/* dst[j] = src[idx[j]] (rows of H floats): the rows of a step that are
+ * sampled, gathered for the LM head.  grid (n), 256 threads. */
+extern "C" __global__ __launch_bounds__(256) void mm_gather_rows(mm_gather_rows_args a) {
+    const int j = blockIdx.x;
+    const float *s = a.src + (size_t)a.idx[j] * a.H;
+    float *d = a.dst + (size_t)j * a.H;
+    for (int i = threadIdx.x; i < a.H; i += 256) d[i] = s[i];
+}
+
 /* h = silu(g) * u with silu(x) = x / (1 + e^-x) (src/run.c:39, 86-93). */
 extern "C" __global__ __launch_bounds__(256) void mm_swiglu(mm_swiglu_args a) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;

@@ -75,7 +75,7 @@ class EngineConfig(C.Structure):
     _fields_ = [("n_layers", C.c_int), ("first_k_dense", C.c_int), ("hidden_size", C.c_int),
                 ("dense_inter_size", C.c_int), ("vocab_size", C.c_int), ("rms_eps", C.c_float),
                 ("max_batch", C.c_int), ("max_seq", C.c_int), ("moe_flags", C.c_uint),
-                ("init_seq", C.c_int)]
+                ("init_seq", C.c_int), ("max_rows", C.c_int)]
 
 
 class EngineLayer(C.Structure):
@@ -154,6 +154,7 @@ def lib():
         L.mm_engine_set_layer.argtypes = [_vp, C.c_int, C.POINTER(EngineLayer)]
         L.mm_engine_set_head.argtypes = [_vp, _vp, _vp, _vp]
         L.mm_engine_step.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp]
+        L.mm_engine_step_rows.argtypes = [_vp, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp]
         L.mm_engine_capacity.argtypes = [_vp]
         L.mm_engine_reserve.argtypes = [_vp, C.c_int]
         L.mm_engine_generate.argtypes = [_vp, C.c_int, C.POINTER(_vp), _vp, C.c_int, C.c_int,

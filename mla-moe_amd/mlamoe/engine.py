@@ -24,12 +24,14 @@ class Engine:
         self.ctx, self.h, self.cfg, self._bufs = ctx, handle, cfg, bufs
 
     @classmethod
-    def from_host(cls, ctx, c, m, inv_freq, max_batch, max_seq, int8=False, init_seq=0):
+    def from_host(cls, ctx, c, m, inv_freq, max_batch, max_seq, int8=False, init_seq=0,
+                  max_rows=0):
         """c: dict of Config fields (n_layers, first_dense, H, NH, QKN, QKR,
         KVL, VHD, dense_inter, E, n_shared, K, I, vocab, router_sigmoid,
         norm_topk, routed_scaling, rms_eps, and optionally q_lora,
         interleaved); m: synth.model(); init_seq: positions per slot the
-        latent caches start with (0: the library's default)."""
+        latent caches start with, max_rows: token rows per step (0: the
+        library's defaults)."""
         L = c["n_layers"]
         ctx.mla_init(c["NH"], c["QKN"], c["QKR"], c["KVL"], c["VHD"], n_layers=L)
         ctx.mla_front_init(c["H"], inv_freq, c.get("q_lora", 0), c["rms_eps"], 1e-6,
@@ -57,7 +59,7 @@ class Engine:
                                       dev(lw.get("dgate")), dev(lw.get("dup")), dev(lw.get("ddown"))))
         cfg = EngineConfig(L, c["first_dense"], c["H"], c.get("dense_inter", 8), c["vocab"],
                            c["rms_eps"], max_batch, max_seq, MM_FWD_INT8 if int8 else MM_FWD_BF16,
-                           init_seq)
+                           init_seq, max_rows)
         h = _vp()
         _check(lib().mm_engine_create(ctx.h, C.byref(cfg), C.byref(h)))
         eng = cls(ctx, h.value, cfg, bufs)
@@ -90,6 +92,28 @@ class Engine:
             _check(lib().mm_engine_step(self.h, B, tokens.ctypes.data, pos.ctypes.data,
                                         nxt.ctypes.data, lg.ptr if lg is not None else None))
             return nxt, (lg.download() if lg is not None else None)
+        finally:
+            if lg is not None:
+                self.ctx._tmp((lg,))
+
+    def step_rows(self, slots, tokens, pos, want_rows, want_logits=False):
+        """One step over token rows (slot, token, position): prompt chunks and
+        decode rows together.  Returns (next tokens of want_rows, logits
+        [len(want_rows), vocab] or None)."""
+        slots = np.ascontiguousarray(slots, np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        want = np.ascontiguousarray(want_rows, np.int32)
+        nw = want.size
+        nxt = np.empty(max(nw, 1), np.int32)
+        lg = self.ctx.empty((max(nw, 1), self.cfg.vocab_size), np.float32) if want_logits else None
+        try:
+            _check(lib().mm_engine_step_rows(self.h, slots.size, slots.ctypes.data,
+                                             tokens.ctypes.data, pos.ctypes.data, nw,
+                                             want.ctypes.data if nw else None,
+                                             nxt.ctypes.data if nw else None,
+                                             lg.ptr if lg is not None else None))
+            return nxt[:nw], (lg.download()[:nw] if lg is not None else None)
         finally:
             if lg is not None:
                 self.ctx._tmp((lg,))

@@ -16,8 +16,10 @@
  * src/getp_run.hip:932-953) and runs mm_engine_generate: all requests
  * decode together in slots of a batch instead of one after another
  * (src/getp_run.hip:958-993), the caches growing as requests need
- * (src/getp_run.hip:269-290), prompts consumed by the same absorbed decode
- * steps.  Generated ids stop at EOS as there.  Errors print the library's
+ * (src/getp_run.hip:269-290), each prompt prefilled in batched chunks of up
+ * to MLAMOE_GETP_ROWS rows beside the decoding slots (the reference's
+ * gpu_forward_unabsorbed, src/getp_run.hip:558-701).  Generated ids stop at
+ * EOS as there.  Errors print the library's
  * message and exit, as the reference's harness does (src/getp_run.hip:480-484).
  */
 #include <stdio.h>
@@ -34,6 +36,9 @@
 #endif
 #ifndef MLAMOE_GETP_INIT_SEQ
 #define MLAMOE_GETP_INIT_SEQ 256  /* positions per slot the caches start with */
+#endif
+#ifndef MLAMOE_GETP_ROWS
+#define MLAMOE_GETP_ROWS 2048   /* token rows per step: prompt chunks and decode rows */
 #endif
 
 static mm_ctx *g_ctx;
@@ -90,7 +95,8 @@ void warm_up(Transformer *t) {
     const int max_seq = c->max_seq_len < MM_MAX_KV_LEN ? c->max_seq_len : MM_MAX_KV_LEN;
     mm_engine_config ec = {c->n_layers, c->first_k_dense, c->hidden_size, c->dense_inter_size,
                            c->vocab_size, c->rms_eps, MLAMOE_GETP_BATCH, max_seq, MM_FWD_INT8,
-                           MLAMOE_GETP_INIT_SEQ < max_seq ? MLAMOE_GETP_INIT_SEQ : max_seq};
+                           MLAMOE_GETP_INIT_SEQ < max_seq ? MLAMOE_GETP_INIT_SEQ : max_seq,
+                           MLAMOE_GETP_ROWS};
     mm_engine_layer *ls = calloc((size_t)c->n_layers, sizeof(*ls));
     if (!ls) die("calloc");
     for (int l = 0; l < c->n_layers; l++) {

@@ -155,6 +155,8 @@ def ref():
         R.ref_rope_apply.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int]
         R.ref_forward_tokens.restype = C.c_int
         R.ref_forward_tokens.argtypes = [C.c_void_p, _ip, C.c_int, _f32p]
+        R.ref_prefill_tokens.restype = C.c_int
+        R.ref_prefill_tokens.argtypes = [C.c_void_p, _ip, C.c_int, C.c_char_p, _f32p]
         R.ref_config_rope.restype = C.c_int
         R.ref_config_rope.argtypes = [C.c_char_p, _f32p, _ip, _f32p]
         _ref = R
@@ -532,8 +534,10 @@ class RefModelSpec(C.Structure):
         [("moe_bias", C.POINTER(_f32p))]
 
 
-def ref_forward_tokens(c, m, tokens, inv):
-    """The reference's own forward_absorbed over tokens (teacher forcing)."""
+def ref_forward_tokens(c, m, tokens, inv, prefill=False):
+    """The reference's own forward_absorbed over tokens (teacher forcing), or
+    with prefill its forward_unabsorbed over the whole prompt (every
+    position's logits, from its dump).  Returns [n, vocab]."""
     L = len(m["layers"])
     keep = []
 
@@ -567,5 +571,11 @@ def ref_forward_tokens(c, m, tokens, inv):
                         bias)
     out = np.empty((n, c["vocab"]), np.float32)
     tk = np.ascontiguousarray(tokens, np.int32)
-    assert ref().ref_forward_tokens(C.byref(spec), _p(tk, _ip), n, _p(out, _f32p)) == 0
+    if not prefill:
+        assert ref().ref_forward_tokens(C.byref(spec), _p(tk, _ip), n, _p(out, _f32p)) == 0
+        return out
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        assert ref().ref_prefill_tokens(C.byref(spec), _p(tk, _ip), n, d.encode(),
+                                        _p(out, _f32p)) == 0
     return out

@@ -32,6 +32,7 @@ int ref_config_rope(const char *model_dir, float *inv, int *ints, float *flts) {
     return 0;
 }
 
+#include "dump.h"
 #include "engine.h"
 
 /* A small model for whole-step golden vectors: n_layers layers, the first
@@ -52,12 +53,10 @@ typedef struct {
     const float *const *moe_bias;
 } ref_model_spec;
 
-/* forward_absorbed (src/run.c:379-501) at positions 0..n-1 on tokens[p]
- * (teacher forcing): logits[p] = the step's logits. */
-int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float *logits) {
-    Transformer t;
-    memset(&t, 0, sizeof(t));
-    Config *c = &t.config;
+/* A Transformer over the spec's arrays (borrowed), run state allocated. */
+static void ref_build(const ref_model_spec *m, Transformer *t) {
+    memset(t, 0, sizeof(*t));
+    Config *c = &t->config;
     const int L = m->n_layers;
     c->n_layers = L;
     c->hidden_size = m->H;
@@ -82,7 +81,7 @@ int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float 
     c->routed_scaling = m->routed_scaling;
     c->q_lora_rank = m->q_lora;
     c->rope_interleaved = m->interleaved;
-    ModelWeights *w = &t.weights;
+    ModelWeights *w = &t->weights;
 #define PA(field) w->field = calloc((size_t)L, sizeof(*w->field))
     PA(q_proj); PA(q_a_proj); PA(q_b_proj); PA(kv_a_proj); PA(W_UK); PA(W_UV); PA(o_proj);
     PA(input_layernorm); PA(post_attn_norm); PA(q_a_layernorm); PA(kv_a_layernorm);
@@ -128,14 +127,14 @@ int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float 
         w->shared_down[l] = (bf16_t *)m->sd[l];
     }
     /* the RoPE table stays the caller's */
-    t.rope_inv_freq = (float *)m->inv_freq;
-    malloc_run_state(&t.state, c);
-    for (int p = 0; p < n; p++) {
-        const float *lg = forward_absorbed(&t, tokens[p], p);
-        memcpy(logits + (size_t)p * m->vocab, lg, (size_t)m->vocab * sizeof(float));
-    }
-    free_run_state(&t.state);
-    for (int l = 0; l < L; l++) {
+    t->rope_inv_freq = (float *)m->inv_freq;
+    malloc_run_state(&t->state, c);
+}
+
+static void ref_release(Transformer *t) {
+    ModelWeights *w = &t->weights;
+    free_run_state(&t->state);
+    for (int l = 0; l < t->config.n_layers; l++) {
         free(w->expert_gate[l]); free(w->expert_up[l]); free(w->expert_down[l]);
     }
     void *arrs[] = {w->q_proj, w->q_a_proj, w->q_b_proj, w->kv_a_proj, w->W_UK, w->W_UV, w->o_proj,
@@ -144,5 +143,41 @@ int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float 
                     w->expert_gate, w->expert_up, w->expert_down, w->shared_gate, w->shared_up,
                     w->shared_down};
     for (size_t i = 0; i < sizeof(arrs) / sizeof(arrs[0]); i++) free(arrs[i]);
+}
+
+/* forward_absorbed (src/run.c:379-501) at positions 0..n-1 on tokens[p]
+ * (teacher forcing): logits[p] = the step's logits. */
+int ref_forward_tokens(const ref_model_spec *m, const int *tokens, int n, float *logits) {
+    Transformer t;
+    ref_build(m, &t);
+    for (int p = 0; p < n; p++) {
+        const float *lg = forward_absorbed(&t, tokens[p], p);
+        memcpy(logits + (size_t)p * m->vocab, lg, (size_t)m->vocab * sizeof(float));
+    }
+    ref_release(&t);
     return 0;
+}
+
+/* forward_unabsorbed (src/run.c:189-370), the whole-prompt prefill, on
+ * tokens[0..n): logits[p] = the logits at every prompt position, as the
+ * reference dumps them ("prefill_logits", run.c:356-364) into dump_dir (a
+ * writable directory; the file is read back and left there).  The
+ * reference's router dump keeps n * n_experts_per_tok <= 128
+ * (run.c:324-330): callers keep n within that. */
+int ref_prefill_tokens(const ref_model_spec *m, const int *tokens, int n, const char *dump_dir,
+                       float *logits) {
+    Transformer t;
+    ref_build(m, &t);
+    run_set_dump(dump_dir);
+    forward_unabsorbed(&t, tokens, n, NULL, NULL);
+    run_set_dump(NULL);
+    ref_release(&t);
+    char path[512];
+    snprintf(path, sizeof(path), "%s/prefill_logits.bin", dump_dir);
+    FILE *f = fopen(path, "rb");
+    if (!f) return -1;
+    const size_t want = (size_t)n * m->vocab;
+    const size_t got = fread(logits, sizeof(float), want, f);
+    fclose(f);
+    return got == want ? 0 : -2;
 }

@@ -362,7 +362,22 @@ def gen_engine():
     np.savez_compressed(os.path.join(OUT, "engine.npz"), **d)
 
 
-GENERATORS = dict(engine=lambda: gen_engine(), mla_front=lambda: gen_mla_front(), matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),
+def gen_prefill():
+    """The reference's whole-prompt prefill, forward_unabsorbed (run.c:189-370),
+    on the two engine models: every position's logits of a 24-token prompt
+    (the reference's own dump, run.c:356-364; its router dump limits a
+    prompt to 128 / n_experts_per_tok positions, run.c:324-330)."""
+    d = {}
+    for name, (c, seed, _) in ENGINE_CASES.items():
+        m = engine_model(name)
+        inv = O.rope_inv_freq(c["QKR"], 10000.0)
+        tokens = np.random.default_rng(seed + 7).integers(0, c["vocab"], 24).astype(np.int32)
+        d[f"{name}_tokens"], d[f"{name}_inv"] = tokens, inv
+        d[f"{name}_logits"] = O.ref_forward_tokens(c, m, tokens, inv, prefill=True)
+    np.savez_compressed(os.path.join(OUT, "prefill.npz"), **d)
+
+
+GENERATORS = dict(prefill=lambda: gen_prefill(), engine=lambda: gen_engine(), mla_front=lambda: gen_mla_front(), matmul=lambda: gen_matmul(), softmax_silu=lambda: gen_softmax_silu(),
                   ffn_tiny=lambda: gen_ffn_tiny(), absorbed=lambda: gen_absorbed(),
                   ffn_dsv2=lambda: gen_ffn_dsv2(), lm_head=lambda: gen_lm_head())
 
