@@ -533,8 +533,9 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     /* the route kernel appends to the per-expert counters (zero on entry:
      * cleared at init and by every tiled call's combine); a failure after it
      * clears them itself (FAIL_ROUTED) */
+    /* routing waves and as many x-quantising waves per block */
     if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
-                        64 * MM_I8_RT_WAVES, 0, &ra)))
+                        2 * 64 * MM_I8_RT_WAVES, 0, &ra)))
         return tiled ? clear_counters(c, st) : st;
 #define FAIL_ROUTED(call)                                   \
     do {                                                    \
@@ -602,7 +603,8 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
 
     mm_i8_combine_args ca = {y, ys, wts, out, tiled ? c->moe_cnt : NULL, T, (int)H, (int)K,
                              (int)E, acc, S > 0};
-    FAIL_ROUTED(mm_launch(c, K_I8_COMBINE, (unsigned)T, 1, 1, 256, 0, &ca));
+    /* two blocks per token: one round of loads per thread at H = 2048 */
+    FAIL_ROUTED(mm_launch(c, K_I8_COMBINE, (unsigned)T, 2, 1, 256, 0, &ca));
 #undef FAIL_ROUTED
 
     if (dbg) {

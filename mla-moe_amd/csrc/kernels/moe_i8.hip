@@ -203,76 +203,69 @@ __device__ __forceinline__ void route_token(const mm_router_args &a, int tok, co
 }
 
 /* Routing, per-expert row lists and per-token quantisation of x.  Block =
- * MM_I8_RT_WAVES waves x RT_TPW tokens.  Row-list slots are claimed per
- * block: LDS counters give each route its place among the block's routes to
- * the same expert, then one global atomic per (block, expert) reserves the
- * block's range of the expert's list.  Logits come from logits_in. */
+ * 2 * MM_I8_RT_WAVES waves over RT_TOKENS tokens: wave w < MM_I8_RT_WAVES
+ * routes token t0 + w while wave MM_I8_RT_WAVES + w quantises the same
+ * token's x row, so the two chains run side by side.  Row-list slots are
+ * claimed per block: LDS counters give each route its place among the
+ * block's routes to the same expert, then one global atomic per (block,
+ * expert) reserves the block's range of the expert's list.  Logits come
+ * from logits_in. */
 template <int EJ>
 __device__ __forceinline__ void i8_route(const mm_i8_route_args &a) {
+    static_assert(RT_TPW == 1, "one token per routing wave");
     __shared__ int lcnt[MM_EMAX];
     __shared__ float wsc[MM_I8_RT_WAVES][2 * MM_EMAX + 2 * MM_KMAX];
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const bool router = wave < MM_I8_RT_WAVES;
     const mm_router_args &r = a.r;
     const int T = r.T, E = r.E, K = r.K;
     for (int e = threadIdx.x; e < E; e += blockDim.x) lcnt[e] = 0;
-    const int t0 = blockIdx.x * RT_TOKENS + wave * RT_TPW;
-    /* the x rows' first chunks are fetched now, consumed after the routing */
-    f32x4 xv[RT_TPW][QC];
-#pragma unroll
-    for (int t = 0; t < RT_TPW; t++)
-        quant_row_load(a.x + (size_t)min(t0 + t, T - 1) * r.H, r.H, 0, xv[t]);
-    float lg[RT_TPW][EJ];
-#pragma unroll
-    for (int t = 0; t < RT_TPW; t++)
-#pragma unroll
-        for (int j = 0; j < EJ; j++) {
-            const int e = lane + MM_WAVE * j, tt = min(t0 + t, T - 1);
-            lg[t][j] = e < E ? r.logits_in[(size_t)tt * E + e] : -INFINITY;
+    const int tok = blockIdx.x * RT_TOKENS + (router ? wave : wave - MM_I8_RT_WAVES);
+    if (!router) {
+        /* quantising wave: its x row in one round trip, nothing shared */
+        if (tok < T) quant_row_wave(a.x + (size_t)tok * r.H, r.H, a.qx + (size_t)tok * r.H, a.sx + tok);
+        if (a.rows) {   /* the block's barriers of the row-list pass */
+            __syncthreads();
+            __syncthreads();
+            __syncthreads();
         }
-    __syncthreads();
-    int my_e[RT_TPW], my_pos[RT_TPW];
+        return;
+    }
+    float lg[EJ];
 #pragma unroll
-    for (int t = 0; t < RT_TPW; t++) {
-        my_e[t] = -1;
-        const int tok = t0 + t;
-        if (tok >= T) continue;
+    for (int j = 0; j < EJ; j++) {
+        const int e = lane + MM_WAVE * j, tt = min(tok, T - 1);
+        lg[j] = e < E ? r.logits_in[(size_t)tt * E + e] : -INFINITY;
+    }
+    int my_e = -1, my_pos = 0;
+    if (tok < T) {
         int e;
         float w;
-        route_token<EJ>(r, tok, lg[t], wsc[wave], &e, &w);
+        route_token<EJ>(r, tok, lg, wsc[wave], &e, &w);
         if (lane < K) {
             r.topk_idx[(size_t)tok * K + lane] = e;
             r.topk_w[(size_t)tok * K + lane] = w;
-            my_e[t] = e;
-            if (a.rows) my_pos[t] = atomicAdd(&lcnt[e], 1);
+            my_e = e;
         }
     }
     if (a.rows) {   /* per-expert row lists (block-uniform) */
+        __syncthreads();   /* lcnt cleared */
+        if (my_e >= 0) my_pos = atomicAdd(&lcnt[my_e], 1);
         __syncthreads();
-        for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        for (int e = threadIdx.x; e < E; e += MM_I8_RT_WAVES * MM_WAVE) {
             const int n = lcnt[e];
             lcnt[e] = n ? atomicAdd(&a.cnt[e], n) : 0;   /* now the block's base */
         }
         __syncthreads();
-#pragma unroll
-        for (int t = 0; t < RT_TPW; t++) {
-            const int e = my_e[t];
-            if (e >= 0) {
-                const int pos = lcnt[e] + my_pos[t];
-                if (pos < T) a.rows[(size_t)e * T + pos] = (t0 + t) * K + lane;
-            }
+        if (my_e >= 0) {
+            const int pos = lcnt[my_e] + my_pos;
+            if (pos < T) a.rows[(size_t)my_e * T + pos] = tok * K + lane;
         }
-    }
-#pragma unroll
-    for (int t = 0; t < RT_TPW; t++) {
-        const int tok = t0 + t;
-        if (tok < T)
-            quant_row_wave_pre(a.x + (size_t)tok * r.H, r.H, a.qx + (size_t)tok * r.H, a.sx + tok,
-                               xv[t]);
     }
 }
 
-extern "C" __global__ __launch_bounds__(MM_I8_RT_WAVES * MM_WAVE) void mm_i8_route(mm_i8_route_args a) {
+extern "C" __global__ __launch_bounds__(2 * MM_I8_RT_WAVES * MM_WAVE) void mm_i8_route(mm_i8_route_args a) {
     if (a.r.E <= 64)
         i8_route<1>(a);
     else if (a.r.E <= 128)
@@ -671,12 +664,15 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_quant_h(mm_i8_quant_rows
     }
 }
 
-/* out[t] (=|+=) sum_r w_r * y[t*K + r] (slot order) + ys[t].  All of a
- * thread's loads are issued before the sums (one round trip). */
+/* out[t] (=|+=) sum_r w_r * y[t*K + r] (slot order) + ys[t].  grid (T,
+ * column parts): block (t, p) takes every gridDim.y-th group of 4 columns
+ * from 4 * p; all of a thread's loads are issued before the sums (one round
+ * trip per group). */
 extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_args a) {
     const int t = blockIdx.x;
     const float *w = a.topk_w + (size_t)t * a.K;
-    for (int n = threadIdx.x * 4; n < a.H; n += blockDim.x * 4) {
+    for (int n = (blockIdx.y * blockDim.x + threadIdx.x) * 4; n < a.H;
+         n += gridDim.y * blockDim.x * 4) {
         f32x4 y[MM_KMAX], ys = {0.0f, 0.0f, 0.0f, 0.0f}, o = {0.0f, 0.0f, 0.0f, 0.0f};
         float wr[MM_KMAX];
 #pragma unroll
@@ -695,7 +691,7 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_ar
         if (a.has_shared) acc += ys;
         *op = a.accumulate ? o + acc : acc;
     }
-    if (a.cnt && t == 0)
+    if (a.cnt && t == 0 && blockIdx.y == 0)
         for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
 }
 
