@@ -9,24 +9,29 @@
  *
  * Block tile MM_I8B_BM = 128 rows x MM_I8B_FR = 16 fragments (gate/up: the
  * gate and up fragments of 8 column blocks, 128 output columns; plain: 256
- * output columns), K step (stage) 64 bytes.  Four waves in a 2 x 2 grid:
- * wave (wr, wc) owns rows 64 wr .. + 63 and fragments 8 wc .. + 7, i.e. two
- * 32-row blocks x four 32-column MFMA tiles (gate/up: gate and up of two
- * 32-column pairs), 8 accumulators of 16 registers.
+ * output columns), K step (stage) 64 bytes.  The four waves split the
+ * columns: wave w owns all 128 rows and fragments 4 w .. 4 w + 3, i.e. four
+ * 32-row blocks x two 32-column MFMA tiles (gate/up: the gate and the up
+ * tile of one 32-column pair), 8 accumulators of 16 registers.
  *
  * The 32x32x32 MFMA is used because it keeps the pipe 85-90% busy at one or
  * two waves per SIMD, where the 16x16x64 form is limited by issue to 58-75%
- * (measured on MI355X).  Two blocks share a CU (72 KB of LDS each), so one
- * block's set-up, load latency and epilogue overlap the other's MFMAs.
+ * (measured on MI355X).  Two blocks share a CU, so one block's set-up, load
+ * latency and epilogue overlap the other's MFMAs.
  *
- * Data path per stage: A rows (8 KB: 64 bytes of each row, 16-byte chunks
- * XOR-swizzled by row) and B fragments (16 x 1 KB, one 64-byte K half) go
- * global -> LDS by direct loads into a ring of three 24 KB stages, two
- * stages ahead.  Operands of
- * the next 32-byte K step are read from LDS while the 8 MFMAs of the current
- * one run.  A 32x32x32 B operand (lane l: column l % 32, K bytes 16 (l / 32)
- * .. + 15) is read straight out of two packed 16x64 fragments: the 16 bytes
- * of (column c, K chunk q) sit at byte (16 q + c % 16) * 16 of fragment c / 16.
+ * Data path per stage: the A rows (8 KB: 64 bytes of each row, 16-byte
+ * chunks XOR-swizzled by row) go global -> LDS by direct loads, read by all
+ * four waves; each wave loads its own B operands (4 KB) straight into
+ * registers, as the decode GEMMs do.  A ring of BT_NS slots (LDS for A,
+ * registers for B) runs BT_P stages ahead.  A 32x32x32 B operand (lane l:
+ * column l % 32, K bytes 16 (l / 32) .. + 15) is one 16-byte load per lane
+ * out of two packed 16x64 fragments: the 16 bytes of (column c, K chunk q)
+ * sit at byte (16 q + c % 16) * 16 of fragment c / 16.  Measured on MI355X
+ * against staging both operands in LDS (which costs each wave 12 LDS reads
+ * per stage instead of 8): gate/up 10-15% faster at config 3's skewed
+ * routing; with its MFMAs, A loads or B loads switched off in a test build,
+ * the kernel is bound by the loads a CU can take in from L2, not by MFMA
+ * issue or load latency (a deeper ring changes nothing).
  *
  * MFMA 32x32x32 i8 layout: A lane l = row l % 32, K bytes 16 (l / 32) .. + 15;
  * B likewise by column; result register 4 g + i of lane l is row
@@ -43,19 +48,24 @@ __device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
 }
 
 #define BT_A_BYTES (MM_I8B_BM * 64)
-#define BT_B_BYTES (MM_I8B_FR * 1024)
-#define BT_STAGE (BT_A_BYTES + BT_B_BYTES)
-#define BT_NS 3
+#define BT_P 2                   /* stages issued ahead of the one consumed */
+#define BT_NS (BT_P + 1)         /* ring slots: A rows in LDS, B operands in registers */
+#define BT_LPS 6                 /* loads per wave per stage: 2 of A, 4 of B */
 static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
+static_assert(BT_P >= 1 && BT_P <= 3, "the vmcnt waits of the K loop count up to two later stages");
 
 /* position of 16-byte chunk q of staged A row R (64 bytes per row): q ^ swz64(R);
  * any 16 consecutive rows then cover all 64 banks once for a fixed q */
 __device__ __forceinline__ int swz64(int R) { return (R >> 2) & 3; }
 
 /* s_waitcnt lgkmcnt(0), tied to the operand registers it makes valid */
-__device__ __forceinline__ void lds_wait6(i32x4 (&A)[2], i32x4 (&B)[4]) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(A[0]), "+v"(A[1]), "+v"(B[0]), "+v"(B[1]), "+v"(B[2]), "+v"(B[3]));
+template <int N>
+__device__ __forceinline__ void lds_wait_regs(i32x4 (&A)[N]) {
+    if constexpr (N == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]));
+    if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]));
+    if constexpr (N == 3) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]));
+    if constexpr (N == 4)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]));
 }
 
 /* Per-block schedule and row tables in LDS. */
@@ -133,27 +143,30 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
     const int t_end = xl.len;
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / MM_WAVE);
-    const int wr = wave & 1, wc = wave >> 1;
-    const int bstep = GU ? 2048 : 1024;
     const int l32 = lane & 31, hi = lane >> 5;
     const uint32_t lds0 = lds_addr(lds);
-    constexpr int NT = GU ? 2 : 4;          /* output column tiles of 32 */
+    constexpr int NT = GU ? 1 : 2;          /* output column tiles of 32 per wave */
 
     /* ---- load parameters of the tile whose stages are being issued ----
-     * A loads: wave w issues instructions 2 w, 2 w + 1 of a stage (16 rows x
-     * 64 B each); lane l carries row R = 16 i + l / 4 and stores at position
-     * l % 4 of the row's 64 B the chunk (l % 4) ^ swz64(R).
-     * B loads: wave w loads fragments 4 w .. 4 w + 3 of the slab (clamped
-     * past the last; results discarded) at the stage's K half. */
+     * A (DMA into LDS): wave w issues instructions 2 w, 2 w + 1 of a stage
+     * (16 rows x 64 B each); lane l carries row R = 16 i + l / 4 and stores
+     * at position l % 4 of the row's 64 B the chunk (l % 4) ^ swz64(R).
+     * B (into registers): column tile cj, K step ks of the stage: lane l
+     * reads column l % 32 of the tile, K chunk 2 ks + l / 32: the 16 bytes at
+     * (16 (2 ks + l / 32) + l % 16) * 16 of the tile's fragment (l % 32) / 16.
+     * gate/up: the wave's column blocks are 2 w, 2 w + 1 of the slab; tile 0
+     * is their gate fragments, tile 1 their up fragments.  plain: column
+     * blocks 4 w .. 4 w + 3, tile cj = blocks 4 w + 2 cj, + 1.  Column
+     * blocks past the last are clamped (results not stored). */
     uint32_t arow_off[2];
     int aq[2];
     __amdgpu_buffer_rsrc_t brs;
     const int8_t *aptr;
-    int bf0, lkb, lnfr;
+    uint32_t boff[2];
+    int lkb, bstep;
     auto set_tile = [&](const bt_tile_id &id, int buf) {
         const mm_i8_tiled_args &g = a.seg[id.si];
         lkb = g.Kd / 64;
-        lnfr = (GU ? 2 : 1) * (g.N / 16);
         aptr = g.a;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -161,56 +174,57 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
             arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd;
             aq[h] = 16 * ((lane & 3) ^ swz64(R));
         }
+        const int ncb = g.N / 16;
+        const uint32_t in_frag = (uint32_t)((16 * hi + (lane & 15)) * 16);
+#pragma unroll
+        for (int cj = 0; cj < 2; cj++) {
+            if (GU) {
+                const int cb = min(id.slab * 8 + 2 * wave + (l32 >> 4), ncb - 1);
+                boff[cj] = (uint32_t)((cb * 2 * lkb + cj) * 1024) + in_frag;
+            } else {
+                const int cb = min(id.slab * 16 + 4 * wave + 2 * cj + (l32 >> 4), ncb - 1);
+                boff[cj] = (uint32_t)(cb * lkb * 1024) + in_frag;
+            }
+        }
+        bstep = GU ? 2048 : 1024;
         brs = __builtin_amdgcn_make_buffer_rsrc((void *)(g.b + (size_t)id.e * g.b_expert_stride), 0,
-                                                (int)((uint32_t)(lnfr * lkb) * 1024u), 0x00020000);
-        bf0 = __builtin_amdgcn_readfirstlane(id.slab * MM_I8B_FR + 4 * wave);
+                                                (int)((uint32_t)((GU ? 2 : 1) * ncb * lkb) * 1024u),
+                                                0x00020000);
     };
-    auto issue_stage = [&](int s) {   /* stage s into ring slot s % 3: 6 loads per wave */
-        const uint32_t st = (uint32_t)((s % BT_NS) * BT_STAGE);
+    /* B operands of the ring slots: [slot][column tile][K step] */
+    i32x4 bq[BT_NS][2][2];
+    auto issue_a = [&](int s, int slot) {
+        const uint32_t st = (uint32_t)(slot * BT_A_BYTES);
 #pragma unroll
         for (int h = 0; h < 2; h++)
             lds_dma16(aptr + (arow_off[h] + (uint32_t)(s * 64 + aq[h])),
                       lds + st + (2 * wave + h) * 1024);
-        const int so = s * bstep;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int fr = min(bf0 + i, lnfr - 1);
-            const int fo = GU ? ((fr >> 1) * 2 * lkb + (fr & 1)) * 1024 : fr * lkb * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                brs, (lds_void_t *)(lds + st + BT_A_BYTES + (4 * wave + i) * 1024), 16, lane * 16,
-                __builtin_amdgcn_readfirstlane(fo + so), 0, 0);
-        }
     };
-    /* the stages issued ahead of a tile's K loop */
-    auto issue_head = [&]() {
-        for (int s = 0; s < min(BT_NS, lkb); s++) issue_stage(s);
+    auto issue_b = [&](int slot, int s) {
+        const int so = __builtin_amdgcn_readfirstlane(s * bstep);
+#pragma unroll
+        for (int cj = 0; cj < 2; cj++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+                bq[slot][cj][ks] = __builtin_bit_cast(
+                    i32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, boff[cj] + 512 * ks, so, 0));
     };
 
-    /* ---- operand reads ----
-     * K step ks (0, 1) of a stage:
-     *   A, row block ri: row 64 wr + 32 ri + l % 32, chunk 2 ks + l / 32
-     *     (swizzle depends on l % 32 only) -> + ri * 2048;
-     *   B, column tile cj: fragment j(cj) + (l % 32) / 16 * jstep of the
-     *     wave's 8, chunk 2 ks + l / 32, column l % 16.
-     * gate/up: tiles (gate, up) of pair p are j = 4 p + {0, 1}, jstep 2;
-     * plain: tile cj is j = 2 cj, jstep 1. */
-    uint32_t rdA[2];
+    /* a tile's first BT_P stages (its last one again where it has fewer),
+     * into slots 0 .. BT_P - 1 */
+    auto issue_head = [&]() {
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-        rdA[ks] = (64 * wr + l32) * 64 + 16 * ((2 * ks + hi) ^ swz64(l32));
-    const uint32_t rdB = BT_A_BYTES + (8 * wc + (l32 >> 4) * (GU ? 2 : 1)) * 1024 +
-                         (hi * 16 + (lane & 15)) * 16;
-    auto read_ops = [&](int s, int ks, i32x4(&A)[2], i32x4(&B)[4]) {
-        const uint32_t sb = lds0 + (uint32_t)((s % BT_NS) * BT_STAGE);
-        const uint32_t ra = sb + rdA[ks], rb = sb + rdB;
-        A[0] = ds_read16(ra, 0);
-        A[1] = ds_read16(ra, 2048);
-#pragma unroll
-        for (int cj = 0; cj < 4; cj++) {
-            const int j = GU ? 4 * (cj >> 1) + (cj & 1) : 2 * cj;
-            B[cj] = ds_read16(rb, j * 1024 + ks * 512);
+        for (int d = 0; d < BT_P; d++) {
+            issue_a(min(d, lkb - 1), d);
+            issue_b(d, min(d, lkb - 1));
         }
     };
+
+    /* A operand of row block ri, K step ks: row 32 ri + l % 32, chunk
+     * 2 ks + l / 32 (the swizzle depends on l % 32 only) */
+    uint32_t rdA[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) rdA[ks] = l32 * 64 + 16 * ((2 * ks + hi) ^ swz64(l32));
 
     /* ---- first tile ---- */
     bt_tile_id cur = bt_decode(a, sh, xl(t));
@@ -233,17 +247,6 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         const bool has_next = tn < t_end;
         const bt_tile_id nxt = has_next ? bt_decode(a, sh, xl(tn)) : cur;
 
-        /* this tile's stage 0: the previous tile's epilogue stores (at
-         * least 64 per wave) were issued after its stages, so vmcnt(63)
-         * leaves the 6 oldest loads (stage 0) complete */
-        static_assert(32 * NT >= 63, "vmcnt(63) needs the stores to outnumber it");
-        if (!first) VMCNT_WAIT(63);
-        else if (KB >= 3) VMCNT_WAIT(12);
-        else if (KB == 2) VMCNT_WAIT(6);
-        else VMCNT_WAIT(0);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-
         /* loads whose results are used after the K loop: this tile's row
          * scales and column scales, the next tile's row ids */
         float sa_r = 0.0f;
@@ -254,13 +257,12 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         }
         const float *sb0 = g.sb0 + (size_t)cur.e * g.sb_expert_stride;
         const float *sb1 = GU ? g.sb1 + (size_t)cur.e * g.sb_expert_stride : nullptr;
-        const int fw = cur.slab * MM_I8B_FR + 8 * wc;   /* the wave's first fragment */
         const int N = g.N;
         float c0[NT], c1[NT];
         int colv[NT];
 #pragma unroll
         for (int q = 0; q < NT; q++) {
-            const int col = (GU ? (fw >> 1) + 2 * q : fw + 2 * q) * 16 + l32;
+            const int col = (GU ? cur.slab * 8 + 2 * wave : cur.slab * 16 + 4 * wave + 2 * q) * 16 + l32;
             colv[q] = col;
             const int cc = min(col, N - 1);
             c0[q] = sb0[cc];
@@ -268,49 +270,61 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         }
 
         /* ---- K loop ---- */
-        i32x4 Ar[2][2], Br[2][4];
-        v16i acc[2][4];
+        v16i acc[4][2];
 #pragma unroll
-        for (int ri = 0; ri < 2; ri++)
+        for (int ri = 0; ri < 4; ri++)
 #pragma unroll
-            for (int cj = 0; cj < 4; cj++) acc[ri][cj] = (v16i){};
-        /* 32-row blocks of this wave that hold valid rows (a wave-uniform
-         * count): padding-only blocks skip their MFMAs, which leaves the
-         * pipe to the CU's other block (tiles of cold experts are mostly
-         * padding) */
-        const int vrows = min(cur.M - cur.m0, MM_I8B_BM) - 64 * wr;
-        const int nri = __builtin_amdgcn_readfirstlane(vrows <= 0 ? 0 : vrows <= 32 ? 1 : 2);
-        auto mma = [&](i32x4(&A)[2], i32x4(&B)[4]) {
-            if (nri > 0) {
+            for (int cj = 0; cj < 2; cj++) acc[ri][cj] = (v16i){};
+        /* 32-row blocks that hold valid rows (uniform over the block):
+         * padding-only blocks skip their reads and MFMAs */
+        const int vrows = min(cur.M - cur.m0, MM_I8B_BM);
+        const int nri = __builtin_amdgcn_readfirstlane((vrows + 31) >> 5);
+        /* step s, ring slot d = s % BT_NS.  Every step issues one stage
+         * (s + BT_P, or the tile's last one again past the end: results
+         * unused), so the loads of exactly BT_P - 1 later stages are
+         * outstanding when stage s must have landed -- except on the first
+         * step of a later tile, where the previous tile's stores were issued
+         * after this tile's head stages and vmcnt(63) leaves stage 0
+         * complete.  The barrier then makes every wave's A rows of stage s
+         * visible and frees slot (s - 1) % BT_NS for the stage issued. */
+        auto kloop = [&](auto nri_c) {
+            constexpr int NRI = decltype(nri_c)::value;
+            auto kstep = [&](int d, int s) {
+                if (!first && s == 0) VMCNT_WAIT(63);
+                else VMCNT_WAIT((BT_P - 1) * BT_LPS);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                const int sn = min(s + BT_P, KB - 1);
+                issue_a(sn, (s + BT_P) % BT_NS);
+                issue_b((d + BT_P) % BT_NS, sn);
+                __builtin_amdgcn_sched_barrier(0);
+                const uint32_t sb = lds0 + (uint32_t)((s % BT_NS) * BT_A_BYTES);
 #pragma unroll
-                for (int cj = 0; cj < 4; cj++) acc[0][cj] = mfma32_i8(A[0], B[cj], acc[0][cj]);
+                for (int ks = 0; ks < 2; ks++) {
+                    i32x4 A[NRI];
+#pragma unroll
+                    for (int ri = 0; ri < NRI; ri++) A[ri] = ds_read16(sb + rdA[ks], ri * 2048);
+                    lds_wait_regs(A);
+#pragma unroll
+                    for (int ri = 0; ri < NRI; ri++)
+#pragma unroll
+                        for (int cj = 0; cj < 2; cj++)
+                            acc[ri][cj] = mfma32_i8(A[ri], bq[d][cj][ks], acc[ri][cj]);
+                }
+            };
+            int s0 = 0;
+            for (; s0 + BT_NS <= KB; s0 += BT_NS) {
+#pragma unroll
+                for (int d = 0; d < BT_NS; d++) kstep(d, s0 + d);
             }
-            if (nri > 1) {
 #pragma unroll
-                for (int cj = 0; cj < 4; cj++) acc[1][cj] = mfma32_i8(A[1], B[cj], acc[1][cj]);
-            }
+            for (int d = 0; d < BT_NS; d++)
+                if (s0 + d < KB) kstep(d, s0 + d);
         };
-        read_ops(0, 0, Ar[0], Br[0]);
-        for (int s = 0; s < KB; s++) {
-            lds_wait6(Ar[0], Br[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            read_ops(s, 1, Ar[1], Br[1]);
-            __builtin_amdgcn_sched_barrier(0);
-            mma(Ar[0], Br[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            lds_wait6(Ar[1], Br[1]);
-            /* stage s + 1 of this wave has landed (only stage s + 2 was
-             * issued after it) */
-            if (s + 2 < KB) VMCNT_WAIT(6); else VMCNT_WAIT(0);
-            __builtin_amdgcn_s_barrier();  /* ... of every wave; stage s is no longer read */
-            __builtin_amdgcn_sched_barrier(0);
-            if (s + 3 < KB) issue_stage(s + 3);
-            if (s + 1 < KB) read_ops(s + 1, 0, Ar[0], Br[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            mma(Ar[1], Br[1]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        lds_wait6(Ar[0], Br[0]);
+        if (nri >= 4) kloop(std::integral_constant<int, 4>());
+        else if (nri == 3) kloop(std::integral_constant<int, 3>());
+        else if (nri == 2) kloop(std::integral_constant<int, 2>());
+        else kloop(std::integral_constant<int, 1>());
         VMCNT_WAIT(0);
 
         /* row tables: this tile's scales, the next tile's rows */
@@ -320,7 +334,7 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
             sh.arow[buf ^ 1][tid] = narow;
         }
         __syncthreads();
-        /* the next tile's first stages go out before this tile's stores */
+        /* the next tile's head stages go out before this tile's stores */
         if (has_next) {
             set_tile(nxt, buf ^ 1);
             issue_head();
@@ -328,18 +342,18 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
 
         /* ---- epilogue ----
          * accumulator register 4 g + i of lane l is row
-         * 64 wr + 32 ri + 8 g + 4 (l / 32) + i, column l % 32 of tile cj.
-         * Stores are unconditional (exactly 32 NT per wave): padded rows and
+         * 32 ri + 8 g + 4 (l / 32) + i, column l % 32 of tile cj.
+         * Stores are unconditional (exactly 64 NT per wave): padded rows and
          * columns past N go to the spare row of `out`. */
         float *out = g.out;
         const size_t spare = (size_t)g.spare_row * N;
         auto epilogue = [&](auto dbg_on) {
             int32_t *dbg = g.dbg_acc;
 #pragma unroll
-            for (int ri = 0; ri < 2; ri++) {
+            for (int ri = 0; ri < 4; ri++) {
 #pragma unroll
                 for (int gq = 0; gq < 4; gq++) {
-                    const int rb = 64 * wr + 32 * ri + 8 * gq + 4 * hi;
+                    const int rb = 32 * ri + 8 * gq + 4 * hi;
                     const i32x4 rid4 = *(const i32x4 *)(&sh.rid[buf][rb]);
                     const f32x4 sa4 = *(const f32x4 *)(&sh.sa[buf][rb]);
 #pragma unroll
@@ -352,8 +366,8 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
                             const bool ok = rid >= 0 && col < N;
                             const size_t o = ok ? (size_t)rid * N + col : spare + col;
                             if (GU) {
-                                const int32_t ag = acc[ri][2 * q][4 * gq + i];
-                                const int32_t au = acc[ri][2 * q + 1][4 * gq + i];
+                                const int32_t ag = acc[ri][0][4 * gq + i];
+                                const int32_t au = acc[ri][1][4 * gq + i];
                                 out[o] = silu_mul(((float)ag * sa) * c0[q], ((float)au * sa) * c1[q]);
                                 if (decltype(dbg_on)::value && ok) {
                                     dbg[((size_t)rid * 2) * N + col] = ag;
@@ -389,7 +403,7 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
  * the same time: row groups of the same expert and slab, whose weights then
  * come from HBM once and from that XCD's L2 for the others. */
 extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args a) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_STAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_A_BYTES];
     __shared__ bt_shared sh;
     const mm_i8_tiled_args &g0 = a.seg[0];
     const int E = g0.cnt ? g0.E : 1;
