@@ -12,6 +12,7 @@
 /* Kernels, one entry per extern "C" __global__ in csrc/kernels. */
 typedef enum {
     K_ROUTER,
+    K_ROUTER_PC,
     K_MOE_BF16_S1,
     K_MOE_BF16_S2,
     K_MOE_BF16_S3,

@@ -427,6 +427,15 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     return MM_OK;
 }
 
+/* Router logits only (a->logits_out set): one token per block for small
+ * batches, where the chain-per-lane form leaves most CUs idle. */
+static int launch_router_logits(mm_ctx *c, mm_router_args *a) {
+    if (a->E <= 64 && a->H % 8 == 0 && a->T <= MM_ROUTER_PC_TMAX)
+        return mm_launch(c, K_ROUTER_PC, (unsigned)a->T, 1, 1, 256, 0, a);
+    return mm_launch(c, K_ROUTER, (a->T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK, 1,
+                     1, 256, 0, a);
+}
+
 /* ---- int8 forward ----------------------------------------------------------- */
 
 /* Blocks of a decode GEMM that serve the shared expert's `groups` column
@@ -498,9 +507,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         la.H = (int)H;
         la.E = (int)E;
         la.K = (int)K;
-        if ((st = mm_launch(c, K_ROUTER, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK,
-                            1, 1, 256, 0, &la)))
-            return st;
+        if ((st = launch_router_logits(c, &la))) return st;
         logits = la.logits_out;
     }
     mm_i8_route_args ra;
@@ -675,8 +682,7 @@ int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
     a.H = c->moe.hidden_size;
     a.E = c->moe.n_routed_experts;
     a.K = c->moe.n_experts_per_tok;
-    return mm_launch(c, K_ROUTER, (T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK, 1, 1,
-                     256, 0, &a);
+    return launch_router_logits(c, &a);
 }
 
 int mm_moe_forward_dev(mm_ctx *c, int layer, int T, const float *xn, float *out,

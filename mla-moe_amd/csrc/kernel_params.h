@@ -14,6 +14,10 @@
 #define MM_ROUTER_TPW 1           /* router: tokens per wave (4 waves per block) */
 #endif
 
+/* Logits-only router with one token per block (mm_router_pc): used for
+ * E <= 64, H % 8 == 0 and T up to this many tokens. */
+#define MM_ROUTER_PC_TMAX 256
+
 typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */
     const uint16_t *wg;      /* [E, H] router weight, bf16 (checkpoint layout) */

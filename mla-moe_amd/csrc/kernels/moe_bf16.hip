@@ -71,6 +71,12 @@ extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_rou
     router_block(a, blockIdx.x, lds);
 }
 
+/* Router logits, one token per block (E <= 64; router_logits_pc). */
+extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc(mm_router_args a) {
+    __shared__ __attribute__((aligned(16))) float lds[RPC_LDS_FLOATS];
+    router_logits_pc(a, lds);
+}
+
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_gu_bf16_args a) {
     __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     if ((int)blockIdx.x < a.r.n_router_blocks) {

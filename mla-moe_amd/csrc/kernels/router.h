@@ -377,3 +377,119 @@ __device__ __forceinline__ void router_block(const mm_router_args &a, int block,
     else
         router_block_t<4>(a, block, lds, post);
 }
+
+/* ---- logits of one token per block, products and sums on separate waves ----
+ *
+ * For small T the sequential add chains above leave most of the machine idle
+ * and each chain's wave spends more than half of its instructions on loads
+ * and multiplies.  Here a block of 4 waves serves one token with E <= 64:
+ * wave 0 (the chain wave, lane e = expert e) only adds, in ascending hidden
+ * order, the products x[i] * W[e, i] that waves 1..3 compute (each rounded
+ * to fp32 on its own, as the reference's separate multiply and add round
+ * them) and leave in LDS.  Chunks of RPC_HC hidden indices: in phase k the
+ * product waves fill chunks 3 k .. 3 k + 2 while the chain wave consumes
+ * those of phase k - 1 (two sets of three buffers, one barrier per phase).
+ * Indices past H contribute +0 (exact, as in router_logits_block).
+ * Writes logits_out[tok][e] (+ logit_bias[e]). */
+#define RPC_HC 64
+#define RPC_RS (RPC_HC + 4)                  /* padded product row (floats) */
+#define RPC_NPROD 3
+#define RPC_BUF_FLOATS (MM_WAVE * RPC_RS)
+#define RPC_LDS_FLOATS (2 * RPC_NPROD * (RPC_BUF_FLOATS + RPC_HC))
+
+__device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float *lds) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int tok = blockIdx.x, H = a.H, E = a.E;
+    const int nch = (H + RPC_HC - 1) / RPC_HC;
+    const int nph = (nch + RPC_NPROD - 1) / RPC_NPROD;
+    float *prod = lds;                                   /* [6][64][RS] */
+    float *xs = lds + 2 * RPC_NPROD * RPC_BUF_FLOATS;    /* [6][HC] */
+    const float *xrow = a.x + (size_t)tok * H;
+    if (wave > 0) {
+        /* product wave p fills chunk 3 k + p of every phase k; the loads of
+         * the next phase's chunk are in flight while this one is computed */
+        const int p = wave - 1;
+        const int e = min(lane, E - 1);
+        const uint16_t *wrow = a.wg + (size_t)e * H;
+        u32x4 wr[RPC_HC / 8];
+        float xv;
+        auto fetch = [&](int c) {
+            const int i0 = c * RPC_HC;
+#pragma unroll
+            for (int q = 0; q < RPC_HC / 8; q++) {
+                const int i = i0 + 8 * q;
+                /* in range: H is a multiple of 8; past H: zeros */
+                wr[q] = (c < nch && i < H) ? *(const u32x4 *)(wrow + i) : (u32x4){0u, 0u, 0u, 0u};
+            }
+            const int i = i0 + lane;
+            xv = (c < nch && i < H) ? xrow[i] : 0.0f;
+        };
+        fetch(p);
+        for (int k = 0; k <= nph; k++) {
+            const int c = RPC_NPROD * k + p;
+            if (k < nph) {
+#pragma clang fp contract(off)
+                const int b = (k & 1) * RPC_NPROD + p;
+                float *xb = xs + b * RPC_HC;
+                /* this chunk's x to LDS (read back by this wave only: its
+                 * LDS accesses complete in order) */
+                xb[lane] = xv;
+                u32x4 w[RPC_HC / 8];
+#pragma unroll
+                for (int q = 0; q < RPC_HC / 8; q++) w[q] = wr[q];
+                fetch(c + RPC_NPROD);                    /* the next chunk's loads */
+                float *pb = prod + b * RPC_BUF_FLOATS + (size_t)lane * RPC_RS;
+#pragma unroll
+                for (int q = 0; q < RPC_HC / 8; q++) {
+                    const f32x4 x0 = *(const f32x4 *)(xb + 8 * q);
+                    const f32x4 x1 = *(const f32x4 *)(xb + 8 * q + 4);
+                    const u32x4 d = w[q];
+                    f32x4 lo, hi;
+                    lo.x = x0.x * __uint_as_float(d.x << 16);
+                    lo.y = x0.y * __uint_as_float(d.x & 0xffff0000u);
+                    lo.z = x0.z * __uint_as_float(d.y << 16);
+                    lo.w = x0.w * __uint_as_float(d.y & 0xffff0000u);
+                    hi.x = x1.x * __uint_as_float(d.z << 16);
+                    hi.y = x1.y * __uint_as_float(d.z & 0xffff0000u);
+                    hi.z = x1.z * __uint_as_float(d.w << 16);
+                    hi.w = x1.w * __uint_as_float(d.w & 0xffff0000u);
+                    *(f32x4 *)(pb + 8 * q) = lo;
+                    *(f32x4 *)(pb + 8 * q + 4) = hi;
+                }
+            }
+            __syncthreads();
+        }
+    } else {
+        float acc = 0.0f;
+        for (int k = 0; k <= nph; k++) {
+            if (k > 0) {
+#pragma clang fp contract(off)
+                const int kp = k - 1;
+#pragma unroll
+                for (int j = 0; j < RPC_NPROD; j++) {
+                    if (RPC_NPROD * kp + j >= nch) break;
+                    const float *pb =
+                        prod + ((kp & 1) * RPC_NPROD + j) * RPC_BUF_FLOATS + (size_t)lane * RPC_RS;
+                    f32x4 v[RPC_HC / 4];
+#pragma unroll
+                    for (int q = 0; q < RPC_HC / 4; q++) v[q] = *(const f32x4 *)(pb + 4 * q);
+#pragma unroll
+                    for (int q = 0; q < RPC_HC / 4; q++) {
+                        acc = acc + v[q].x;
+                        acc = acc + v[q].y;
+                        acc = acc + v[q].z;
+                        acc = acc + v[q].w;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (lane < E) {
+            float lg = acc;
+            if (a.logit_bias) lg += a.logit_bias[lane];
+            a.logits_out[(size_t)tok * E + lane] = lg;
+        }
+    }
+}
+

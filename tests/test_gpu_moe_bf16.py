@@ -141,13 +141,16 @@ def test_rejects_bad_shapes(ctx):
         ctx.moe_forward(0, np.zeros((1, 64), np.float32))
 
 
-@pytest.mark.parametrize("H,E", [(2048, 64), (1000, 40), (256, 160)])
-def test_router_logits_bit_exact(ctx, oracle, H, E):
+@pytest.mark.parametrize("H,E,T", [(2048, 64, 29), (1000, 40, 29), (256, 160, 29), (2048, 64, 1),
+                                   (2048, 64, 300)])
+def test_router_logits_bit_exact(ctx, oracle, H, E, T):
     """Logits-only router: bit-identical to the reference matmul (run.c:29-37,
-    sequential fp32, no FMA), for a partial last LDS chunk (H=1000) and more
-    than 64 experts per wave (E=160); the optional prior is a plain fp32 add."""
-    print(f"router logits H={H} E={E}", flush=True)
-    K, I, T = 4, 8, 29
+    sequential fp32, no FMA), for a partial last chunk (H=1000), more than 64
+    experts per wave (E=160), one token, and more tokens than the
+    one-token-per-block form takes (T=300, the chain-per-lane form); the
+    optional prior is a plain fp32 add."""
+    print(f"router logits H={H} E={E} T={T}", flush=True)
+    K, I = 4, 8
     w = synth.moe_layer(55 + E, H, E, I, 0)
     _layer_ctx(ctx, w, H, E, 0, K, I)
     x = synth.activations(56, T, H)
