@@ -215,19 +215,47 @@ int mm_engine_set_head(mm_engine *e, const uint16_t *embed, const uint16_t *fina
     return MM_OK;
 }
 
+/* GEMV sizes: the post-attention norm is fused into the consumer's GEMV
+ * (dense gate/up) or runs on its own; larger batches fuse it into o_proj's
+ * reduce instead. */
+static int gemv_rows(const mm_engine *e, int B) {
+    return B <= MM_GEMV_NB && e->cfg.hidden_size <= MM_LM_HMAX;
+}
+
+/* o_proj with its residual add, x += ctxo . o_proj^T (src/run.c:462-468),
+ * then xn = rmsnorm(x, post_norm) (src/run.c:470-472) unless the dense
+ * GEMV path applies it itself: one GEMM + one reduce-and-norm pass for
+ * more than MM_GEMV_NB rows. */
+static int oproj_post_norm(mm_engine *e, const mm_engine_layer *L, int R, int dense) {
+    mm_ctx *c = e->c;
+    const mm_mla_config *g = &c->mla;
+    const int H = e->cfg.hidden_size, NIN = g->n_heads * g->v_head_dim;
+    int st;
+    if (gemv_rows(e, R)) {
+        if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, NIN, R, MM_MATMUL_ACCUMULATE)))
+            return st;
+        if (dense && gemv_rows(e, R)) return MM_OK;
+        mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, e->cfg.rms_eps};
+        return mm_launch(c, K_RMSNORM, (unsigned)R, 1, 1, 256, 0, &ra);
+    }
+    char *ws;
+    if ((st = mm_workspace(c, mm_gemm_bf16_add_rmsnorm_ws_bytes(R, NIN, H), (void **)&ws))) return st;
+    return mm_gemm_bf16_add_rmsnorm(c, e->x, e->ctxo, L->o_proj, H, NIN, R, L->post_norm,
+                                    e->cfg.rms_eps, e->xn, ws);
+}
+
 /* The dense SwiGLU MLP with its residual add: x += down . (silu(gate . xn) * (up . xn)),
- * xn = rmsnorm(x, post_norm) (src/run.c:470-472, 86-93). */
+ * xn = rmsnorm(x, post_norm) (src/run.c:470-472, 86-93): computed by
+ * oproj_post_norm, or here by the gate/up GEMV at GEMV sizes. */
 static int dense_ffn(mm_engine *e, const mm_engine_layer *L, int B) {
     mm_ctx *c = e->c;
     const int H = e->cfg.hidden_size, DI = e->cfg.dense_inter_size;
     int st;
-    if (B <= MM_GEMV_NB && H <= MM_LM_HMAX) {
+    if (gemv_rows(e, B)) {
         mm_gemv_args a = {e->x, L->post_norm, e->cfg.rms_eps, L->dense_gate, L->dense_up, e->g, e->u,
                           DI, DI, DI, DI, B, H, 0, 0};
         if ((st = mm_gemv_launch(c, &a))) return st;
     } else {
-        mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, e->cfg.rms_eps};
-        if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
         /* gate and up over the same xn in one pass */
         char *ws;
         if ((st = mm_workspace(c, mm_gemm_bf16_ws2_bytes(B, H, DI, DI, 0), (void **)&ws))) return st;
@@ -278,7 +306,6 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
     int32_t *d_len = e->d_io + IO_LEN * MR, *d_slot = e->d_io + IO_SLOT * MR;
     int32_t *d_want = e->d_io + IO_WANT * MR, *d_next = e->d_io + IO_NEXT * MR;
     MM_HIP(hipMemcpyAsync(e->d_io, hio, (size_t)IO_NEXT * MR * 4, hipMemcpyHostToDevice, c->stream));
-    const mm_mla_config *g = &c->mla;
     const int H = f->hidden_size;
     mm_embed_args ea = {e->embed, d_tok, e->x, H, f->vocab_size};
     if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)R, 1, 256, 0, &ea))) return st;
@@ -290,14 +317,11 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
         if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
                                      e->ctxo, NULL, NULL, NULL)))
             return st;
-        if ((st = mm_matmul_bf16_dev(c, e->x, e->ctxo, L->o_proj, H, g->n_heads * g->v_head_dim, R,
-                                     MM_MATMUL_ACCUMULATE)))
-            return st;
-        if (l < f->first_k_dense) {
+        const int dense = l < f->first_k_dense;
+        if ((st = oproj_post_norm(e, L, R, dense))) return st;
+        if (dense) {
             if ((st = dense_ffn(e, L, R))) return st;
         } else {
-            mm_rmsnorm_args ra = {e->x, L->post_norm, e->xn, H, f->rms_eps};
-            if ((st = mm_launch(c, K_RMSNORM, (unsigned)R, 1, 1, 256, 0, &ra))) return st;
             if ((st = mm_moe_forward_dev(c, l, R, e->xn, e->x, NULL, NULL, NULL, NULL,
                                          f->moe_flags | MM_FWD_ACCUMULATE)))
                 return st;

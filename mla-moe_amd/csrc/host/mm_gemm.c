@@ -55,7 +55,7 @@ int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1
         int ns, kr;
         skinny_plan(nb, n_in, &ns, &kr);
         mm_gemm_skinny_args k = {x, w0, y0, (float *)ws, T, d0, n_in, ns, kr, split, acc,
-                                 w1, y1, d1, nb0};
+                                 w1, y1, d1, nb0, 0};
         if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
         if (ns == 1) return MM_OK;
         mm_skinny_reduce_args r = {(float *)ws, y0, T, d0, ns, acc, d1 ? y1 : NULL, d1};
@@ -65,6 +65,40 @@ int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1
     }
     if ((st = mm_gemm_bf16_ws(c, y0, x, w0, d0, n_in, T, flags, ws))) return st;
     return d1 ? mm_gemm_bf16_ws(c, y1, x, w1, d1, n_in, T, flags, ws) : MM_OK;
+}
+
+/* x += a . w^T, then xn = rmsnorm(x, norm_w) -- for T <= MM_SKINNY_T rows
+ * the split-K partials are summed by the norm pass itself (one launch fewer;
+ * the partial sums and residual adds are the skinny reduce's, the norm's sum
+ * of squares is reduced over 1024 threads instead of 256);
+ * otherwise the GEMM accumulates and mm_rmsnorm follows.  d_out is the row
+ * length of x. */
+size_t mm_gemm_bf16_add_rmsnorm_ws_bytes(int T, int n_in, int d_out) {
+    if (skinny_ok(T, n_in) && d_out <= MM_RRN_THREADS * MM_RRN_PT) {
+        int ns, kr;
+        skinny_plan(skinny_nb(d_out), n_in, &ns, &kr);
+        return al256((size_t)ns * T * d_out * 4);
+    }
+    return mm_gemm_bf16_ws_bytes(T, n_in, d_out, 0);
+}
+
+int mm_gemm_bf16_add_rmsnorm(mm_ctx *c, float *x, const float *a, const uint16_t *w, int d_out,
+                             int n_in, int T, const uint16_t *norm_w, float eps, float *xn,
+                             char *ws) {
+    int st;
+    if (skinny_ok(T, n_in) && d_out <= MM_RRN_THREADS * MM_RRN_PT) {
+        const int nb = skinny_nb(d_out);
+        int ns, kr;
+        skinny_plan(nb, n_in, &ns, &kr);
+        mm_gemm_skinny_args k = {a, w, x, (float *)ws, T, d_out, n_in, ns, kr, 1, 0,
+                                 NULL, NULL, 0, nb, 1};
+        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
+        mm_reduce_rmsnorm_args r = {(const float *)ws, x, norm_w, xn, T, d_out, ns, eps};
+        return mm_launch(c, K_REDUCE_RMSNORM, (unsigned)T, 1, 1, MM_RRN_THREADS, 0, &r);
+    }
+    if ((st = mm_gemm_bf16_ws(c, x, a, w, d_out, n_in, T, MM_MATMUL_ACCUMULATE, ws))) return st;
+    mm_rmsnorm_args r = {x, norm_w, xn, d_out, eps};
+    return mm_launch(c, K_RMSNORM, (unsigned)T, 1, 1, 256, 0, &r);
 }
 
 int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,

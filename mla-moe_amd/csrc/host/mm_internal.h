@@ -46,6 +46,7 @@ typedef enum {
     K_SWIGLU,
     K_GEMM_SKINNY,
     K_SKINNY_REDUCE,
+    K_REDUCE_RMSNORM,
     K_ZERO32,
     K_GATHER_ROWS,
     K_COUNT
@@ -153,6 +154,12 @@ size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags);
 /* Two matrices over the same x (y0 = x . W0^T, y1 = x . W1^T; w1 may be
  * NULL): one skinny-M launch when that path applies. */
 size_t mm_gemm_bf16_ws2_bytes(int T, int n_in, int d0, int d1, unsigned flags);
+/* x += a . w^T (bf16 w [d_out, n_in]) then xn = rmsnorm(x, norm_w) over rows
+ * of d_out; ws of mm_gemm_bf16_add_rmsnorm_ws_bytes bytes. */
+size_t mm_gemm_bf16_add_rmsnorm_ws_bytes(int T, int n_in, int d_out);
+int mm_gemm_bf16_add_rmsnorm(mm_ctx *c, float *x, const float *a, const uint16_t *w, int d_out,
+                             int n_in, int T, const uint16_t *norm_w, float eps, float *xn,
+                             char *ws);
 int mm_gemm_bf16_ws2(mm_ctx *ctx, float *y0, const uint16_t *w0, int d0, float *y1,
                      const uint16_t *w1, int d1, const float *x, int n_in, int T, unsigned flags,
                      char *ws);

@@ -350,6 +350,7 @@ typedef struct {
     const uint16_t *w1;
     float *y1;
     int d_out1, nb0;
+    int part_out;            /* 1: partials even when nsplit == 1 (a fused reduce reads them) */
 } mm_gemm_skinny_args;
 
 typedef struct {
@@ -370,6 +371,22 @@ typedef struct {
     int n;
     float eps;
 } mm_rmsnorm_args;
+
+#define MM_RRN_THREADS 1024      /* mm_reduce_rmsnorm: threads per row block */
+#define MM_RRN_PT 4              /* row elements per thread (rows up to 4096) */
+/* Split-K partials summed into the residual rows, then their RMSNorm: per
+ * row t, v = part[0][t] + part[1][t] + ... (split order), x[t] += v, then
+ * xn[t] = rmsnorm(x[t], w) -- mm_skinny_reduce followed by mm_rmsnorm in
+ * one pass (the norm's sum of squares reduced over the block's 1024
+ * threads). */
+typedef struct {
+    const float *part;       /* [nsplit, T, n] */
+    float *x;                /* [T, n] residual rows, updated */
+    const uint16_t *w;       /* [n] bf16 norm weight */
+    float *xn;               /* [T, n] */
+    int T, n, nsplit;
+    float eps;
+} mm_reduce_rmsnorm_args;
 
 typedef struct {
     const float *x;          /* [B, H] activations before the final norm */

@@ -367,7 +367,7 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * g + 4 * (lane >> 4) + i;
                 if (t >= a.T) continue;
-                if (a.nsplit > 1) {
+                if (a.nsplit > 1 || a.part_out) {
                     part[((size_t)blockIdx.y * a.T + t) * d_out + n] = acc[j][g][i];
                 } else {
                     float *y = (seg ? a.y1 : a.y) + (size_t)t * d_out + n;

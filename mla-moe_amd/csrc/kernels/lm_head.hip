@@ -24,22 +24,80 @@
 
 /* ---- RMSNorm ---------------------------------------------------------------- */
 
-extern "C" __global__ __launch_bounds__(256) void mm_rmsnorm(mm_rmsnorm_args a) {
-    __shared__ float red[256 / MM_WAVE];
-    const int t = blockIdx.x;
-    const float *x = a.x + (size_t)t * a.n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < a.n; i += 256) ss += x[i] * x[i];
+/* 1 / sqrt(sum / n + eps) over the block's NT threads, ss = this thread's
+ * sum of squares (every thread calls it). */
+template <int NT>
+__device__ __forceinline__ float rms_inv_block(float ss, int n, float eps) {
+    __shared__ float red[NT / MM_WAVE];
     ss = wave_sum(ss);
     const int lane = threadIdx.x & (MM_WAVE - 1), wave = threadIdx.x / MM_WAVE;
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 256 / MM_WAVE; w++) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / (float)a.n + a.eps);
+    for (int w = 0; w < NT / MM_WAVE; w++) tot += red[w];
+    return 1.0f / sqrtf(tot / (float)n + eps);
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_rmsnorm(mm_rmsnorm_args a) {
+    const int t = blockIdx.x;
+    const float *x = a.x + (size_t)t * a.n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < a.n; i += 256) ss += x[i] * x[i];
+    const float inv = rms_inv_block<256>(ss, a.n, a.eps);
     float *y = a.y + (size_t)t * a.n;
     for (int i = threadIdx.x; i < a.n; i += 256) y[i] = x[i] * inv * bf16_f32(a.w[i]);
+}
+
+/* mm_reduce_rmsnorm_args: one block of RRN_T threads per row, each thread
+ * RRN_PT elements (n <= RRN_T * RRN_PT) kept in registers between the sum
+ * and the norm.  The partial loads of up to RRN_SU splits are issued
+ * together: a row block is one latency-bound pass, so the loads must not
+ * wait for each other. */
+#define RRN_T MM_RRN_THREADS
+#define RRN_PT MM_RRN_PT
+#define RRN_SU 8
+extern "C" __global__ __launch_bounds__(RRN_T) void mm_reduce_rmsnorm(mm_reduce_rmsnorm_args a) {
+    const int t = blockIdx.x, n = a.n;
+    const size_t plane = (size_t)a.T * n;
+    float *x = a.x + (size_t)t * n;
+    const float *p0 = a.part + (size_t)t * n;
+    float v[RRN_PT];
+#pragma unroll
+    for (int k = 0; k < RRN_PT; k++) v[k] = 0.0f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += RRN_SU) {
+        float pv[RRN_SU][RRN_PT];
+#pragma unroll
+        for (int u = 0; u < RRN_SU; u++)
+#pragma unroll
+            for (int k = 0; k < RRN_PT; k++) {
+                const int i = threadIdx.x + RRN_T * k;
+                pv[u][k] = (s0 + u < a.nsplit && i < n) ? p0[(size_t)(s0 + u) * plane + i] : 0.0f;
+            }
+#pragma unroll
+        for (int u = 0; u < RRN_SU; u++)
+#pragma unroll
+            for (int k = 0; k < RRN_PT; k++)
+                if (s0 + u < a.nsplit) v[k] = (s0 + u == 0) ? pv[u][k] : v[k] + pv[u][k];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RRN_PT; k++) {
+        const int i = threadIdx.x + RRN_T * k;
+        if (i < n) {
+            const float xv = x[i] + v[k];
+            x[i] = xv;
+            v[k] = xv;
+            ss += xv * xv;
+        }
+    }
+    const float inv = rms_inv_block<RRN_T>(ss, n, a.eps);
+    float *xn = a.xn + (size_t)t * n;
+#pragma unroll
+    for (int k = 0; k < RRN_PT; k++) {
+        const int i = threadIdx.x + RRN_T * k;
+        if (i < n) xn[i] = v[k] * inv * bf16_f32(a.w[i]);
+    }
 }
 
 /* ---- greedy argmax ---------------------------------------------------------- */

@@ -408,22 +408,27 @@ __device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float 
     const float *xrow = a.x + (size_t)tok * H;
     if (wave > 0) {
         /* product wave p fills chunk 3 k + p of every phase k; the loads of
-         * the next phase's chunk are in flight while this one is computed */
+         * the next phase's chunk are in flight while this one is computed.
+         * The chunk's [64 experts][RPC_HC] block of W is read row-contiguous:
+         * load j of lane l is expert 8 j + l / 8, hidden offsets
+         * 8 (l % 8) .. + 7 (each load instruction covers 8 whole 128-byte
+         * rows); the lane writes the 64 products it holds. */
+        static_assert(RPC_HC == 64, "a chunk row is 8 lanes x 8 bf16");
         const int p = wave - 1;
-        const int e = min(lane, E - 1);
-        const uint16_t *wrow = a.wg + (size_t)e * H;
-        u32x4 wr[RPC_HC / 8];
+        const int o = 8 * (lane & 7);
+        u32x4 wr[8];
         float xv;
         auto fetch = [&](int c) {
-            const int i0 = c * RPC_HC;
+            const int i = c * RPC_HC + o;
 #pragma unroll
-            for (int q = 0; q < RPC_HC / 8; q++) {
-                const int i = i0 + 8 * q;
+            for (int j = 0; j < 8; j++) {
+                const int e = min(8 * j + (lane >> 3), E - 1);
                 /* in range: H is a multiple of 8; past H: zeros */
-                wr[q] = (c < nch && i < H) ? *(const u32x4 *)(wrow + i) : (u32x4){0u, 0u, 0u, 0u};
+                wr[j] = (c < nch && i < H) ? *(const u32x4 *)(a.wg + (size_t)e * H + i)
+                                           : (u32x4){0u, 0u, 0u, 0u};
             }
-            const int i = i0 + lane;
-            xv = (c < nch && i < H) ? xrow[i] : 0.0f;
+            const int ix = c * RPC_HC + lane;
+            xv = (c < nch && ix < H) ? xrow[ix] : 0.0f;
         };
         fetch(p);
         for (int k = 0; k <= nph; k++) {
@@ -435,16 +440,16 @@ __device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float 
                 /* this chunk's x to LDS (read back by this wave only: its
                  * LDS accesses complete in order) */
                 xb[lane] = xv;
-                u32x4 w[RPC_HC / 8];
+                u32x4 w[8];
 #pragma unroll
-                for (int q = 0; q < RPC_HC / 8; q++) w[q] = wr[q];
+                for (int j = 0; j < 8; j++) w[j] = wr[j];
                 fetch(c + RPC_NPROD);                    /* the next chunk's loads */
-                float *pb = prod + b * RPC_BUF_FLOATS + (size_t)lane * RPC_RS;
+                const f32x4 x0 = *(const f32x4 *)(xb + o);
+                const f32x4 x1 = *(const f32x4 *)(xb + o + 4);
+                float *pb = prod + b * RPC_BUF_FLOATS + o;
 #pragma unroll
-                for (int q = 0; q < RPC_HC / 8; q++) {
-                    const f32x4 x0 = *(const f32x4 *)(xb + 8 * q);
-                    const f32x4 x1 = *(const f32x4 *)(xb + 8 * q + 4);
-                    const u32x4 d = w[q];
+                for (int j = 0; j < 8; j++) {
+                    const u32x4 d = w[j];
                     f32x4 lo, hi;
                     lo.x = x0.x * __uint_as_float(d.x << 16);
                     lo.y = x0.y * __uint_as_float(d.x & 0xffff0000u);
@@ -454,8 +459,9 @@ __device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float 
                     hi.y = x1.y * __uint_as_float(d.z & 0xffff0000u);
                     hi.z = x1.z * __uint_as_float(d.w << 16);
                     hi.w = x1.w * __uint_as_float(d.w & 0xffff0000u);
-                    *(f32x4 *)(pb + 8 * q) = lo;
-                    *(f32x4 *)(pb + 8 * q + 4) = hi;
+                    float *row = pb + (size_t)(8 * j + (lane >> 3)) * RPC_RS;
+                    *(f32x4 *)row = lo;
+                    *(f32x4 *)(row + 4) = hi;
                 }
             }
             __syncthreads();
