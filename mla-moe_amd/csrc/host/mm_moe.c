@@ -398,10 +398,7 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         a.r.sigmoid = g->router_sigmoid;
         a.r.norm_topk = g->norm_topk;
         a.r.scale = g->routed_scaling;
-        a.r.n_router_blocks = (Tc + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK;
         a.x = xn + (size_t)t0 * H;
-        a.gate = L->sg;
-        a.up = L->su;
         a.hcat = hcat;
         a.T = Tc;
         a.H = H;
@@ -409,14 +406,35 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         a.S = S;
         a.K = K;
         a.rows_per_block = GU_ROWS_PER_BLOCK;
-        unsigned nb1 = a.r.n_router_blocks + (S + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK;
-        if ((st = mm_launch(c, K_MOE_BF16_S1, nb1, 1, 1, 256, 0, &a))) return st;
-
-        a.gate = L->eg;
-        a.up = L->eu;
         a.n_blocks_per_token = (I + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK;
-        if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
-            return st;
+        if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
+            /* small T: the router one token per block (product / chain
+             * form), then every gate/up -- routed and shared -- in one
+             * launch: the shared expert's GEMV does not wait on the router's
+             * add chains, but stage 1's LDS and registers (those of the
+             * chain-per-lane router) no longer hold its blocks to two per
+             * CU either */
+            a.r.n_router_blocks = Tc;
+            if ((st = mm_launch(c, K_ROUTER_PC, (unsigned)Tc, 1, 1, 256, 0, &a.r))) return st;
+            a.gate = L->eg;
+            a.up = L->eu;
+            a.sgate = L->sg;
+            a.sup = L->su;
+            a.nsh_parts = S / I;
+            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token,
+                                (unsigned)(Tc * K + Tc * a.nsh_parts), 1, 256, 0, &a)))
+                return st;
+        } else {
+            a.r.n_router_blocks = (Tc + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK;
+            a.gate = L->sg;
+            a.up = L->su;
+            unsigned nb1 = a.r.n_router_blocks + (S + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK;
+            if ((st = mm_launch(c, K_MOE_BF16_S1, nb1, 1, 1, 256, 0, &a))) return st;
+            a.gate = L->eg;
+            a.up = L->eu;
+            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
+                return st;
+        }
 
         mm_down_bf16_args d = {hcat, L->ed, L->sd, idx + (size_t)t0 * K, out + (size_t)t0 * H,
                                Tc, H, I, S, K, E, acc, DOWN_ROWS_PER_BLOCK};

@@ -46,6 +46,10 @@ typedef struct {
     int T, H, I, S, K;
     int rows_per_block;      /* gate/up row pairs per block */
     int n_blocks_per_token;  /* stage 2: row blocks per route */
+    /* stage 2 may also take the shared expert (then no stage 1 gate/up):
+     * grid rows T*K .. T*K + T*nsh_parts - 1, S = nsh_parts * I */
+    const uint16_t *sgate, *sup;
+    int nsh_parts;
 } mm_gu_bf16_args;
 
 /* bf16 GEMV MoE, stage 3: out[t] (=|+=) sum over routed slots and the shared

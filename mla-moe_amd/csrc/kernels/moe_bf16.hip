@@ -74,7 +74,7 @@ extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_rou
 /* Router logits, one token per block (E <= 64; router_logits_pc). */
 extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc(mm_router_args a) {
     __shared__ __attribute__((aligned(16))) float lds[RPC_LDS_FLOATS];
-    router_logits_pc(a, lds);
+    router_block_pc<RPC_HC>(a, lds);
 }
 
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_gu_bf16_args a) {
@@ -96,10 +96,21 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_g
 
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_gu_bf16_args a) {
     const int route = blockIdx.y;               /* t*K + r */
-    const int t = route / a.K, r = route % a.K;
     const int row0 = blockIdx.x * a.rows_per_block;
     const int nrows = min(a.rows_per_block, a.I - row0);
     if (nrows <= 0) return;
+    if (route >= a.T * a.K) {
+        /* shared expert of token t as nsh_parts blocks of I rows: part j is
+         * rows j I .. j I + I - 1 of the shared gate/up, hidden columns
+         * K I + j I .. of hcat (weight 1) */
+        const int v = route - a.T * a.K, t = v / a.nsh_parts, j = v % a.nsh_parts;
+        const size_t off = (size_t)j * a.I * a.H;
+        const float one = 1.0f;
+        gu_rows(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, 1, a.H, row0, nrows,
+                a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), 0, (a.K + j) * a.I, &one);
+        return;
+    }
+    const int t = route / a.K, r = route % a.K;
     const int e = min(max(a.r.topk_idx[route], 0), a.r.E - 1);
     const float wr = a.r.topk_w[route];
     const size_t off = (size_t)e * a.I * a.H;

@@ -382,92 +382,106 @@ __device__ __forceinline__ void router_block(const mm_router_args &a, int block,
  *
  * For small T the sequential add chains above leave most of the machine idle
  * and each chain's wave spends more than half of its instructions on loads
- * and multiplies.  Here a block of 4 waves serves one token with E <= 64:
- * wave 0 (the chain wave, lane e = expert e) only adds, in ascending hidden
- * order, the products x[i] * W[e, i] that waves 1..3 compute (each rounded
- * to fp32 on its own, as the reference's separate multiply and add round
- * them) and leave in LDS.  Chunks of RPC_HC hidden indices: in phase k the
- * product waves fill chunks 3 k .. 3 k + 2 while the chain wave consumes
- * those of phase k - 1 (two sets of three buffers, one barrier per phase).
- * Indices past H contribute +0 (exact, as in router_logits_block).
- * Writes logits_out[tok][e] (+ logit_bias[e]). */
-#define RPC_HC 64
-#define RPC_RS (RPC_HC + 4)                  /* padded product row (floats) */
+ * and multiplies.  Here a block of 4 waves serves one token (blockIdx.x)
+ * with E <= 64: wave 0 (the chain wave, lane e = expert e) only adds, in
+ * ascending hidden order, the products x[i] * W[e, i] that waves 1..3
+ * compute (each rounded to fp32 on its own, as the reference's separate
+ * multiply and add round them) and leave in LDS.  Chunks of HC hidden
+ * indices: in phase k the product waves fill chunks 3 k .. 3 k + 2 while the
+ * chain wave consumes those of phase k - 1 (two sets of three buffers, one
+ * barrier per phase), the W loads of a product wave RPC_PF phases ahead of
+ * its products.  A chunk's [64 experts][HC] block of W is read as
+ * whole rows: load j of lane l is expert (64 / LPR) j + l / LPR, hidden
+ * offsets 8 (l % LPR) .. + 7, LPR = HC / 8 lanes per row.  Indices past H
+ * contribute +0 (exact, as in router_logits_block).  Returns the logit of
+ * expert `lane` in wave 0 (0 elsewhere). */
 #define RPC_NPROD 3
-#define RPC_BUF_FLOATS (MM_WAVE * RPC_RS)
-#define RPC_LDS_FLOATS (2 * RPC_NPROD * (RPC_BUF_FLOATS + RPC_HC))
+#define RPC_PF 2            /* phases of W loads in flight ahead of the one computed */
+template <int HC>
+struct rpc_shape {
+    static constexpr int RS = HC + 4;                   /* padded product row (floats) */
+    static constexpr int BUF = MM_WAVE * RS;            /* floats per chunk buffer */
+    static constexpr int LDS_FLOATS = 2 * RPC_NPROD * (BUF + HC);
+    static constexpr int LPR = HC / 8;                  /* lanes per W row */
+    static constexpr int NLD = LPR;                     /* W loads per lane per chunk */
+};
+#define RPC_HC 64                                       /* chunk of the standalone kernel */
+#define RPC_LDS_FLOATS (rpc_shape<RPC_HC>::LDS_FLOATS)
 
-__device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float *lds) {
+template <int HC>
+__device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float *lds) {
+    using S = rpc_shape<HC>;
+    static_assert(HC % 8 == 0 && MM_WAVE % S::LPR == 0, "chunk rows of whole 16-byte pieces");
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int tok = blockIdx.x, H = a.H, E = a.E;
-    const int nch = (H + RPC_HC - 1) / RPC_HC;
+    const int nch = (H + HC - 1) / HC;
     const int nph = (nch + RPC_NPROD - 1) / RPC_NPROD;
     float *prod = lds;                                   /* [6][64][RS] */
-    float *xs = lds + 2 * RPC_NPROD * RPC_BUF_FLOATS;    /* [6][HC] */
+    float *xs = lds + 2 * RPC_NPROD * S::BUF;            /* [6][HC] */
     const float *xrow = a.x + (size_t)tok * H;
+    float acc = 0.0f;
     if (wave > 0) {
         /* product wave p fills chunk 3 k + p of every phase k; the loads of
-         * the next phase's chunk are in flight while this one is computed.
-         * The chunk's [64 experts][RPC_HC] block of W is read row-contiguous:
-         * load j of lane l is expert 8 j + l / 8, hidden offsets
-         * 8 (l % 8) .. + 7 (each load instruction covers 8 whole 128-byte
-         * rows); the lane writes the 64 products it holds. */
-        static_assert(RPC_HC == 64, "a chunk row is 8 lanes x 8 bf16");
+         * the chunks of the next RPC_PF phases are in flight meanwhile */
+        constexpr int RPL = MM_WAVE / S::LPR;            /* rows per load */
+        constexpr int NSL = RPC_PF + 1;                  /* register slots */
         const int p = wave - 1;
-        const int o = 8 * (lane & 7);
-        u32x4 wr[8];
-        float xv;
-        auto fetch = [&](int c) {
-            const int i = c * RPC_HC + o;
+        const int o = 8 * (lane % S::LPR);
+        u32x4 wr[NSL][S::NLD];
+        float xv[NSL];
+        auto fetch = [&](int slot, int c) {
+            const int i = c * HC + o;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int e = min(8 * j + (lane >> 3), E - 1);
+            for (int j = 0; j < S::NLD; j++) {
+                const int e = min(RPL * j + lane / S::LPR, E - 1);
                 /* in range: H is a multiple of 8; past H: zeros */
-                wr[j] = (c < nch && i < H) ? *(const u32x4 *)(a.wg + (size_t)e * H + i)
-                                           : (u32x4){0u, 0u, 0u, 0u};
+                wr[slot][j] = (c < nch && i < H) ? *(const u32x4 *)(a.wg + (size_t)e * H + i)
+                                                 : (u32x4){0u, 0u, 0u, 0u};
             }
-            const int ix = c * RPC_HC + lane;
-            xv = (c < nch && ix < H) ? xrow[ix] : 0.0f;
+            const int ix = c * HC + lane;
+            xv[slot] = (c < nch && lane < HC && ix < H) ? xrow[ix] : 0.0f;
         };
-        fetch(p);
-        for (int k = 0; k <= nph; k++) {
-            const int c = RPC_NPROD * k + p;
-            if (k < nph) {
+#pragma unroll
+        for (int d = 0; d < RPC_PF; d++) fetch(d, RPC_NPROD * d + p);
+        /* phase k uses slot k % NSL and refills slot (k + RPC_PF) % NSL */
+        for (int k0 = 0; k0 <= nph; k0 += NSL) {
+#pragma unroll
+            for (int d = 0; d < NSL; d++) {
+                const int k = k0 + d;
+                if (k > nph) break;
+                if (k < nph) {
 #pragma clang fp contract(off)
-                const int b = (k & 1) * RPC_NPROD + p;
-                float *xb = xs + b * RPC_HC;
-                /* this chunk's x to LDS (read back by this wave only: its
-                 * LDS accesses complete in order) */
-                xb[lane] = xv;
-                u32x4 w[8];
+                    const int b = (k & 1) * RPC_NPROD + p;
+                    float *xb = xs + b * HC;
+                    /* this chunk's x to LDS (read back by this wave only:
+                     * its LDS accesses complete in order) */
+                    if (lane < HC) xb[lane] = xv[d];
+                    fetch((d + RPC_PF) % NSL, RPC_NPROD * (k + RPC_PF) + p);
+                    const f32x4 x0 = *(const f32x4 *)(xb + o);
+                    const f32x4 x1 = *(const f32x4 *)(xb + o + 4);
+                    float *pb = prod + b * S::BUF + o;
 #pragma unroll
-                for (int j = 0; j < 8; j++) w[j] = wr[j];
-                fetch(c + RPC_NPROD);                    /* the next chunk's loads */
-                const f32x4 x0 = *(const f32x4 *)(xb + o);
-                const f32x4 x1 = *(const f32x4 *)(xb + o + 4);
-                float *pb = prod + b * RPC_BUF_FLOATS + o;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const u32x4 d = w[j];
-                    f32x4 lo, hi;
-                    lo.x = x0.x * __uint_as_float(d.x << 16);
-                    lo.y = x0.y * __uint_as_float(d.x & 0xffff0000u);
-                    lo.z = x0.z * __uint_as_float(d.y << 16);
-                    lo.w = x0.w * __uint_as_float(d.y & 0xffff0000u);
-                    hi.x = x1.x * __uint_as_float(d.z << 16);
-                    hi.y = x1.y * __uint_as_float(d.z & 0xffff0000u);
-                    hi.z = x1.z * __uint_as_float(d.w << 16);
-                    hi.w = x1.w * __uint_as_float(d.w & 0xffff0000u);
-                    float *row = pb + (size_t)(8 * j + (lane >> 3)) * RPC_RS;
-                    *(f32x4 *)row = lo;
-                    *(f32x4 *)(row + 4) = hi;
+                    for (int j = 0; j < S::NLD; j++) {
+                        const u32x4 w = wr[d][j];
+                        f32x4 lo, hi;
+                        lo.x = x0.x * __uint_as_float(w.x << 16);
+                        lo.y = x0.y * __uint_as_float(w.x & 0xffff0000u);
+                        lo.z = x0.z * __uint_as_float(w.y << 16);
+                        lo.w = x0.w * __uint_as_float(w.y & 0xffff0000u);
+                        hi.x = x1.x * __uint_as_float(w.z << 16);
+                        hi.y = x1.y * __uint_as_float(w.z & 0xffff0000u);
+                        hi.z = x1.z * __uint_as_float(w.w << 16);
+                        hi.w = x1.w * __uint_as_float(w.w & 0xffff0000u);
+                        float *row = pb + (size_t)(RPL * j + lane / S::LPR) * S::RS;
+                        *(f32x4 *)row = lo;
+                        *(f32x4 *)(row + 4) = hi;
+                    }
                 }
+                __syncthreads();
             }
-            __syncthreads();
         }
     } else {
-        float acc = 0.0f;
         for (int k = 0; k <= nph; k++) {
             if (k > 0) {
 #pragma clang fp contract(off)
@@ -476,12 +490,12 @@ __device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float 
                 for (int j = 0; j < RPC_NPROD; j++) {
                     if (RPC_NPROD * kp + j >= nch) break;
                     const float *pb =
-                        prod + ((kp & 1) * RPC_NPROD + j) * RPC_BUF_FLOATS + (size_t)lane * RPC_RS;
-                    f32x4 v[RPC_HC / 4];
+                        prod + ((kp & 1) * RPC_NPROD + j) * S::BUF + (size_t)lane * S::RS;
+                    f32x4 v[HC / 4];
 #pragma unroll
-                    for (int q = 0; q < RPC_HC / 4; q++) v[q] = *(const f32x4 *)(pb + 4 * q);
+                    for (int q = 0; q < HC / 4; q++) v[q] = *(const f32x4 *)(pb + 4 * q);
 #pragma unroll
-                    for (int q = 0; q < RPC_HC / 4; q++) {
+                    for (int q = 0; q < HC / 4; q++) {
                         acc = acc + v[q].x;
                         acc = acc + v[q].y;
                         acc = acc + v[q].z;
@@ -491,11 +505,119 @@ __device__ __forceinline__ void router_logits_pc(const mm_router_args &a, float 
             }
             __syncthreads();
         }
-        if (lane < E) {
-            float lg = acc;
-            if (a.logit_bias) lg += a.logit_bias[lane];
-            a.logits_out[(size_t)tok * E + lane] = lg;
+    }
+    return acc;
+}
+
+/* Scores and top-k of one token (E <= 64, lane e = expert e), the result
+ * of router_select_wave<1, 1> computed with LDS broadcasts instead of 64
+ * readlane rounds: the softmax sum in ascending expert order and each
+ * expert's rank read the 64 values from `ws` (this wave's LDS scratch of
+ * 64 floats; nothing else may use it meanwhile).  Calls post(tok, idx, w). */
+template <class Post>
+__device__ __forceinline__ void router_select_one(const mm_router_args &a, int tok, float v,
+                                                  float *ws, Post post) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int E = a.E, K = a.K;
+    const bool ok = lane < E;
+    /* the sequential sum of ws[0 .. E - 1] (every lane) */
+    auto seq_sum = [&]() {
+        float sum = 0.0f;
+        for (int l0 = 0; l0 < E; l0 += 4) {
+            const f32x4 q = *(const f32x4 *)(ws + l0);
+            sum += q.x;
+            if (l0 + 1 < E) sum += q.y;
+            if (l0 + 2 < E) sum += q.z;
+            if (l0 + 3 < E) sum += q.w;
+        }
+        return sum;
+    };
+    float p;
+    if (a.sigmoid) {
+        p = 1.0f / (1.0f + exp_cr(-v));
+    } else {
+        const float mx = wave_max(ok ? v : -INFINITY);
+        p = (ok && v != -INFINITY) ? exp_cr(v - mx) : 0.0f;
+        ws[lane] = p;
+        p = p / seq_sum();
+    }
+    if (a.probs && ok) a.probs[(size_t)tok * E + lane] = p;
+    /* rank of this expert in the order (score + bias descending, index
+     * ascending): the pass of the CPU's strict '>' scan that picks it */
+    const float sel = p + (a.bias && ok ? a.bias[lane] : 0.0f);
+    ws[lane] = sel;
+    int rank = 0;
+    for (int l0 = 0; l0 < E; l0 += 4) {
+        const f32x4 q = *(const f32x4 *)(ws + l0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int l = l0 + u;
+            const float so = q[u];
+            rank += (l < E && (so > sel || (so == sel && l < lane))) ? 1 : 0;
         }
     }
+    int idx[MM_KMAX];
+    float w[MM_KMAX];
+#pragma unroll
+    for (int r = 0; r < MM_KMAX; r++) {
+        idx[r] = 0;
+        w[r] = 0.0f;
+        if (r >= K) continue;
+        const unsigned long long m = __ballot(ok && rank == r);
+        if (m) {
+            const int l = __ffsll((long long)m) - 1;
+            idx[r] = l;
+            w[r] = readlane_f(p, l);
+        }
+    }
+    if (a.norm_topk) {
+        float s = 1e-20f;
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < K) s += w[r];
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < K) w[r] /= s;
+    }
+#pragma unroll
+    for (int r = 0; r < MM_KMAX; r++)
+        if (r < K) w[r] *= a.scale;
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < K) {
+                a.topk_idx[(size_t)tok * K + r] = idx[r];
+                a.topk_w[(size_t)tok * K + r] = w[r];
+            }
+    }
+    post(tok, idx, w);
+}
+
+/* Router of one token per block with the logits of router_logits_pc (the
+ * selection by the chain wave, as router_block_t does it for its tokens).
+ * Every thread of the block must call it; lds holds
+ * rpc_shape<HC>::LDS_FLOATS floats. */
+template <int HC, class Post = router_no_post>
+__device__ __forceinline__ void router_block_pc(const mm_router_args &a, float *lds,
+                                                Post post = Post()) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    float lg[1][1];
+    if (a.logits_in) {       /* given logits: the selection only */
+        if (threadIdx.x >= MM_WAVE) return;
+        lg[0][0] = lane < a.E ? a.logits_in[(size_t)blockIdx.x * a.E + lane] : 0.0f;
+        router_select_one(a, (int)blockIdx.x, lg[0][0], lds, post);
+        return;
+    }
+    const float acc = router_logits_pc<HC>(a, lds);
+    if (threadIdx.x >= MM_WAVE) return;
+    lg[0][0] = lane < a.E ? acc : 0.0f;
+    if (a.logit_bias && lane < a.E) lg[0][0] += a.logit_bias[lane];
+    if (a.logits_out) {
+        if (lane < a.E) a.logits_out[(size_t)blockIdx.x * a.E + lane] = lg[0][0];
+        return;
+    }
+    /* the other waves have left after the last barrier of the logits:
+     * their LDS is this wave's scratch */
+    router_select_one(a, (int)blockIdx.x, lg[0][0], lds, post);
 }
 
