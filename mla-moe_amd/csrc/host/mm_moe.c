@@ -12,7 +12,8 @@
 #include "mm_internal.h"
 
 #define BF16_NT_MAX 8         /* tokens per pass of the bf16 GEMV path */
-#define GU_ROWS_PER_BLOCK 4   /* one gate/up row pair per wave */
+#define GU_ROWS_PER_BLOCK 4   /* stage 1: one gate/up row pair per wave */
+#define GU2_ROWS_PER_BLOCK 16 /* stage 2: four row pairs per wave, two at a time */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
 #define ROUTER_TOKENS_PER_BLOCK (4 * MM_ROUTER_TPW)
 
@@ -405,8 +406,8 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         a.I = I;
         a.S = S;
         a.K = K;
-        a.rows_per_block = GU_ROWS_PER_BLOCK;
-        a.n_blocks_per_token = (I + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK;
+        a.rows_per_block = GU2_ROWS_PER_BLOCK;
+        a.n_blocks_per_token = (I + GU2_ROWS_PER_BLOCK - 1) / GU2_ROWS_PER_BLOCK;
         if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
             /* small T: the router one token per block (product / chain
              * form), then every gate/up -- routed and shared -- in one
@@ -428,8 +429,10 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             a.r.n_router_blocks = (Tc + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK;
             a.gate = L->sg;
             a.up = L->su;
+            a.rows_per_block = GU_ROWS_PER_BLOCK;
             unsigned nb1 = a.r.n_router_blocks + (S + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK;
             if ((st = mm_launch(c, K_MOE_BF16_S1, nb1, 1, 1, 256, 0, &a))) return st;
+            a.rows_per_block = GU2_ROWS_PER_BLOCK;
             a.gate = L->eg;
             a.up = L->eu;
             if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))

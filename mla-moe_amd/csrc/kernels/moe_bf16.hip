@@ -66,6 +66,71 @@ __device__ __forceinline__ void gu_rows(const uint16_t *__restrict__ gate, const
     }
 }
 
+/* gu_rows for stage 2, one token: each wave keeps the token's x chunks in
+ * registers (loaded with its first weights) and takes its rows GU_RPW at a
+ * time with all of their gate and up loads in flight together (gu_rows
+ * reads x from global memory again for every row). */
+#define GU_RPW 2
+#define GU_MAXC 4
+__device__ __forceinline__ void gu_rows_x1(const uint16_t *__restrict__ gate,
+                                           const uint16_t *__restrict__ up, const float *x, int H,
+                                           int row0, int nrows, float *__restrict__ h, int hoff,
+                                           float wt) {
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = threadIdx.x / MM_WAVE;
+    const int nch = H >> 3;
+    for (int rb = wave * GU_RPW; rb < nrows; rb += GU_WAVES * GU_RPW) {
+        float ag[GU_RPW], au[GU_RPW];
+#pragma unroll
+        for (int q = 0; q < GU_RPW; q++) ag[q] = au[q] = 0.0f;
+        /* groups of 64 * GU_MAXC chunks of the row (one for H <= 2048) */
+        for (int c0 = 0; c0 < nch; c0 += MM_WAVE * GU_MAXC) {
+            u32x4 gv[GU_RPW][GU_MAXC], uv[GU_RPW][GU_MAXC];
+            f32x4 xa[GU_MAXC], xb[GU_MAXC];
+#pragma unroll
+            for (int q = 0; q < GU_RPW; q++) {
+                const int row = row0 + min(rb + q, nrows - 1);
+                const u32x4 *gp = (const u32x4 *)(gate + (size_t)row * H);
+                const u32x4 *upp = (const u32x4 *)(up + (size_t)row * H);
+#pragma unroll
+                for (int k = 0; k < GU_MAXC; k++) {
+                    const int c = c0 + lane + MM_WAVE * k;
+                    if (c < nch) {
+                        gv[q][k] = __builtin_nontemporal_load(gp + c);
+                        uv[q][k] = __builtin_nontemporal_load(upp + c);
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < GU_MAXC; k++) {
+                const int c = c0 + lane + MM_WAVE * k;
+                if (c < nch) {
+                    xa[k] = *(const f32x4 *)(x + 8 * c);
+                    xb[k] = *(const f32x4 *)(x + 8 * c + 4);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < GU_MAXC; k++) {
+                const int c = c0 + lane + MM_WAVE * k;
+                if (c >= nch) continue;
+                float xv[8] = {xa[k].x, xa[k].y, xa[k].z, xa[k].w, xb[k].x, xb[k].y, xb[k].z, xb[k].w};
+#pragma unroll
+                for (int q = 0; q < GU_RPW; q++) {
+                    ag[q] = dot8_bf16(gv[q][k], xv, ag[q]);
+                    au[q] = dot8_bf16(uv[q][k], xv, au[q]);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < GU_RPW; q++) {
+            if (rb + q >= nrows) break;
+            const float g = wave_sum(ag[q]);
+            const float u = wave_sum(au[q]);
+            if (lane == 0) h[hoff + row0 + rb + q] = wt * swiglu_f(g, u);
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_router_args a) {
     __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     router_block(a, blockIdx.x, lds);
@@ -105,17 +170,16 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_g
          * K I + j I .. of hcat (weight 1) */
         const int v = route - a.T * a.K, t = v / a.nsh_parts, j = v % a.nsh_parts;
         const size_t off = (size_t)j * a.I * a.H;
-        const float one = 1.0f;
-        gu_rows(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, 1, a.H, row0, nrows,
-                a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), 0, (a.K + j) * a.I, &one);
+        gu_rows_x1(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
+                   a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), (a.K + j) * a.I, 1.0f);
         return;
     }
     const int t = route / a.K, r = route % a.K;
     const int e = min(max(a.r.topk_idx[route], 0), a.r.E - 1);
     const float wr = a.r.topk_w[route];
     const size_t off = (size_t)e * a.I * a.H;
-    gu_rows(a.gate + off, a.up + off, a.x + (size_t)t * a.H, 1, a.H, row0, nrows,
-            a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), 0, r * a.I, &wr);
+    gu_rows_x1(a.gate + off, a.up + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
+               a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), r * a.I, wr);
 }
 
 /* Down rows: a wave's row d takes, per lane, chunks c = lane, lane + 64, ...
