@@ -466,6 +466,9 @@ static size_t sh_blocks(size_t groups) {
 }
 
 static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+static size_t al16(size_t b) { return (b + 15) & ~(size_t)15; }
+/* LDS of the K split's partials: MM_I8S_W waves x n accumulators x 64 lanes x 16 B */
+#define KSPLIT_RED(n) ((size_t)MM_I8S_W * (n) * 64 * 16)
 
 /* One grouped GEMM over the routed experts (ta) and, when ts is not NULL,
  * the shared expert: one persistent launch of the big-tile kernel. */
@@ -587,6 +590,9 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     ga.S = (int)S;
     ga.E = (int)E;
     ga.K = (int)K;
+    /* few tokens: few experts hold rows, so the gate/up GEMM splits K
+     * (the hidden size) over a block's waves to have enough blocks */
+    ga.ksplit = !tiled && T <= MM_I8_KSPLIT_TMAX && H / 64 >= MM_I8S_W;
     if (tiled) {
         /* routed experts, then the shared expert as one dense GEMM */
         mm_i8_tiled_args ta = {L->i8.gu, 2 * I * H, L->i8.s_g, L->i8.s_u, (int)I, c->moe_cnt,
@@ -597,11 +603,16 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         FAIL_ROUTED(launch_tiled(c, &ta, S ? &ts : NULL));
     } else {
         /* shared-expert blocks (row-tile waves), then every routed unit */
-        const size_t per_blk = (size_t)MM_I8S_W * MM_I8S_SEG;
+        const size_t per_blk = ga.ksplit ? 1 : (size_t)MM_I8S_W * MM_I8S_SEG;
+        /* routed block rows: one per expert, or per route slot with the K
+         * split (few slots; a slot repeating an earlier slot's expert exits) */
+        const size_t rrows = ga.ksplit ? R : E;
         const unsigned nb = (unsigned)((S ? sh_blocks(ceil_div(S / 16, per_blk)) : 0) +
-                                       E * ceil_div(I / 16, per_blk));
-        /* dynamic LDS: the 16-row A tile, 16 * K bytes */
-        FAIL_ROUTED(mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W, 16 * H + 4 * (size_t)T, &ga));
+                                       rrows * ceil_div(I / 16, per_blk));
+        /* dynamic LDS: the 16-row A tile (16 * K bytes), the row list, the
+         * K split's partials */
+        FAIL_ROUTED(mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W,
+                              16 * H + al16(4 * (size_t)T) + (ga.ksplit ? KSPLIT_RED(2) : 0), &ga));
     }
 
     mm_i8_quant_rows_args qa = {h, qh, sh, (int)R, (int)I, S ? hs : NULL, qhs, shs,
@@ -623,6 +634,10 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         ga.y = y;
         ga.ys = ys;
         ga.dbg_acc = dbg ? dbg->acc_d : NULL;
+        /* the down GEMM keeps its column groups: its K (the intermediate
+         * size, 22 steps at I = 1408) split six ways left each wave too
+         * short a stream (14.3 against 13.2 us per layer at one token) */
+        ga.ksplit = 0;
         const size_t gpe = ceil_div(H / 16, (size_t)MM_I8S_W * MM_I8S_SEG);
         const unsigned nb = (unsigned)((S ? sh_blocks(gpe) : 0) + E * gpe);
         FAIL_ROUTED(mm_launch(c, K_I8_DOWN, nb, 1, 1, 64 * MM_I8S_W,

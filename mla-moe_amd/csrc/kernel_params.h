@@ -155,7 +155,10 @@ typedef struct {
     float *ys;               /* down out: shared [T, H] */
     int32_t *dbg_acc;        /* debug: raw accumulators, gate/up [T*K, 2, I], down [T*K, H], or 0 */
     int T, H, I, S, E, K;
+    int ksplit;              /* gate/up: 1 = a block's waves split K for one column block (few rows) */
 } mm_i8_gemm_args;
+/* The decode gate/up GEMM splits K over a block's waves up to this many tokens. */
+#define MM_I8_KSPLIT_TMAX 4
 
 /* Per-row quantisation of the SwiGLU output. */
 typedef struct {

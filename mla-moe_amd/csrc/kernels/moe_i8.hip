@@ -417,10 +417,34 @@ __device__ __forceinline__ void shared_block(int b, int *group, int *rt) {
     *rt = (b / MM_I8S_XCD) % MM_I8S_RT;
 }
 
-/* Column blocks per wave and blocks per expert of a decode GEMM over nbl
- * 16-column blocks. */
-__device__ __forceinline__ int units_per_wave_group(int nbl) {
-    return (nbl + MM_I8S_W * MM_I8S_SEG - 1) / (MM_I8S_W * MM_I8S_SEG);
+/* Column groups (blocks per expert) of a decode GEMM over nbl 16-column
+ * blocks: MM_I8S_W * MM_I8S_SEG column blocks per group, or one when the
+ * waves split K (ksplit). */
+__device__ __forceinline__ int units_per_wave_group(int nbl, int ksplit) {
+    const int upg = ksplit ? 1 : MM_I8S_W * MM_I8S_SEG;
+    return (nbl + upg - 1) / upg;
+}
+
+/* K split (few rows, hence few active experts: too few blocks to stream the
+ * weights at full rate otherwise): the block's waves share one column block,
+ * wave w taking K steps [w KB / W, (w + 1) KB / W); their int32 partials
+ * meet in LDS (exact, so the sum equals the one-wave accumulation) and wave
+ * 0 runs the epilogue.  ks_range gives a wave's first step and count. */
+__device__ __forceinline__ void ks_range(int KB, int wave, int *k0, int *n) {
+    *k0 = wave * KB / MM_I8S_W;
+    *n = (wave + 1) * KB / MM_I8S_W - *k0;
+}
+static_assert(MM_I8S_SEG == 1, "the K split serves one column block per block");
+
+/* Expert of routed block row u: expert u, or with the K split (grid over
+ * route slots, T * K of them) the expert of slot u unless an earlier slot
+ * names it too (-1: that block has nothing to do). */
+__device__ __forceinline__ int routed_expert(const mm_i8_gemm_args &a, int u) {
+    if (!a.ksplit) return u;
+    const int e = a.topk[u];
+    for (int j = 0; j < u; j++)
+        if (a.topk[j] == e) return -1;
+    return e;
 }
 
 /* Decode-shaped gate/up + SwiGLU.  Blocks [0, n_sh): the shared expert
@@ -434,7 +458,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int KB = a.H / 64;
-    const int gs = units_per_wave_group(a.S / 16);
+    const int gs = units_per_wave_group(a.S / 16, a.ksplit);
     const int n_sh = a.S ? (gs + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT : 0;
     const int b = blockIdx.x;
     const int8_t *bbase;
@@ -461,8 +485,9 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         kdiv = 1;
     } else {
         nbl = a.I / 16;
-        G = units_per_wave_group(nbl);
-        const int v = b - n_sh, e = v / G;
+        G = units_per_wave_group(nbl, a.ksplit);
+        const int v = b - n_sh, e = routed_expert(a, v / G);
+        if (e < 0) return;
         g = v % G;
         int *list = (int *)(lds_a + 16 * a.H);
         M = expert_rows(a.topk, a.T * a.K, e, list);
@@ -479,12 +504,16 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
     }
     if (m0 >= M) return;   /* whole block: a shared row tile past T */
     const int ncols = nbl * 16;
-    const int nb0 = (g + G * wave) * MM_I8S_SEG;   /* this wave's first column block */
+    /* this wave's first column block (K split: the block's one) */
+    const int nb0 = a.ksplit ? g : (g + G * wave) * MM_I8S_SEG;
     const int nseg = max(0, min(MM_I8S_SEG, nbl - nb0));
     /* per-column scales: lane l holds column l % 16 of block nb0 + l / 16 */
     const int scol = (min(nb0 + min(lane >> 4, MM_I8S_SEG - 1), nbl - 1)) * 16 + (lane & 15);
     const float cg_all = sg[scol], cu_all = su[scol];
-    const int8_t *bp = bbase + (size_t)min(nb0, nbl - 1) * 2 * KB * 1024 + lane * 16;
+    int kw0 = 0, nkw = KB;                          /* this wave's K steps */
+    if (a.ksplit) ks_range(KB, wave, &kw0, &nkw);
+    const int8_t *bp = bbase + (size_t)min(nb0, nbl - 1) * 2 * KB * 1024 + (size_t)kw0 * 2048 + lane * 16;
+    v4i *red = (v4i *)(lds_a + 16 * a.H + ((4 * a.T + 15) & ~15));   /* K split: [W][2][64] */
     v4i bq[MM_I8S_DEPTH_GU][2];
     for (; m0 < M; m0 += mstep) {
         /* row of this thread's A piece (tile row lane % 16) */
@@ -498,7 +527,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         for (int d = 0; d < MM_I8S_DEPTH_GU; d++)
 #pragma unroll
             for (int f = 0; f < 2; f++)
-                bq[d][f] = ldg16(bp + (size_t)min(d, KB * max(nseg, 1) - 1) * 2048 + f * 1024);
+                bq[d][f] = ldg16(bp + (size_t)min(d, nkw * max(nseg, 1) - 1) * 2048 + f * 1024);
         __builtin_amdgcn_sched_barrier(0);
         const int rid_a = m < M ? rl : -1;
         const int t = rid_a >= 0 ? rid_a / kdiv : 0;
@@ -507,9 +536,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         stage_a(lds_a, rid_a >= 0 ? a.a + (size_t)t * a.H : nullptr, KB, a.a);
         __syncthreads();
         if (nseg == 0) continue;
-        stream_lds<true, MM_I8S_DEPTH_GU>(
-            bp, KB, nseg, lds_addr(lds_a) + lane * 16, true, bq,
-            [&](int seg, v4i ag, v4i au) {
+        auto finish = [&](int seg, v4i ag, v4i au) {
                 const int col = (nb0 + seg) * 16 + (lane & 15);
                 const float cg = __shfl(cg_all, seg * 16 + (lane & 15), MM_WAVE);
                 const float cu = __shfl(cu_all, seg * 16 + (lane & 15), MM_WAVE);
@@ -526,7 +553,26 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
                         dbg[((size_t)rid * 2 + 1) * ncols + col] = au[i];
                     }
                 }
-            });
+        };
+        if (!a.ksplit) {
+            stream_lds<true, MM_I8S_DEPTH_GU>(bp, KB, nseg, lds_addr(lds_a) + lane * 16, true, bq,
+                                              finish);
+            continue;
+        }
+        stream_lds<true, MM_I8S_DEPTH_GU>(bp, nkw, 1, lds_addr(lds_a) + kw0 * 1024 + lane * 16,
+                                          true, bq, [&](int, v4i ag, v4i au) {
+                                              red[(2 * wave) * MM_WAVE + lane] = ag;
+                                              red[(2 * wave + 1) * MM_WAVE + lane] = au;
+                                          });
+        __syncthreads();
+        if (wave == 0) {
+            v4i ag = red[lane], au = red[MM_WAVE + lane];
+            for (int w = 1; w < MM_I8S_W; w++) {
+                ag += red[(2 * w) * MM_WAVE + lane];
+                au += red[(2 * w + 1) * MM_WAVE + lane];
+            }
+            finish(0, ag, au);
+        }
     }
 }
 
@@ -538,7 +584,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int nbl = a.H / 16;
-    const int G = units_per_wave_group(nbl);
+    const int G = units_per_wave_group(nbl, 0);
     const int n_sh = a.S ? (G + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT : 0;
     const int b = blockIdx.x;
     const int8_t *abase, *bbase;

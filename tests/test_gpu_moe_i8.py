@@ -128,6 +128,16 @@ def test_i8_dsv2_decode_batch(ctx, oracle):
              check_all=False)
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_i8_dsv2_few_tokens(ctx, oracle, T):
+    """DeepSeek-V2-Lite shape at 1 and 3 tokens: the decode-shaped gate/up
+    GEMM splits K over a block's waves there (few experts hold rows); the
+    int32 accumulators of every route and of the shared expert stay
+    bit-exact."""
+    d = synth.DSV2
+    run_case(ctx, oracle, d["H"], d["E"], d["K"], d["I"], d["n_shared"], T, 72 + T)
+
+
 def test_i8_accumulate_in_place(ctx, oracle):
     """MM_FWD_ACCUMULATE with out aliasing xn: x += ffn(x) (residual stream)."""
     H, E, K, I, NS, T = 256, 16, 4, 128, 2, 23
