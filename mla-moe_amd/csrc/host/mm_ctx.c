@@ -46,6 +46,7 @@ static const struct {
     [K_I8_QUANT_H] = {"mm_i8_quant_h", MOD_MOE_I8},
     [K_I8_DOWN] = {"mm_i8_down", MOD_MOE_I8},
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
+    [K_I8_COMBINE_NORM] = {"mm_i8_combine_norm", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
     [K_I8_BT] = {"mm_i8_gemm_bt", MOD_GEMM_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},

@@ -309,10 +309,13 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
     const int H = f->hidden_size;
     mm_embed_args ea = {e->embed, d_tok, e->x, H, f->vocab_size};
     if ((st = mm_launch(c, K_EMBED, (unsigned)((H + 2047) / 2048), (unsigned)R, 1, 256, 0, &ea))) return st;
+    int xn_ready = 0;   /* xn holds rmsnorm(x, this layer's input_norm) */
     for (int l = 0; l < f->n_layers; l++) {
         const mm_engine_layer *L = &e->layers[l];
+        const int pre = xn_ready;
+        xn_ready = 0;
         if ((st = mm_mla_front_rows(c, R, e->x, &L->front, d_pos, d_slot, e->q, e->cache[l], e->lcap[l],
-                                    NULL)))
+                                    NULL, pre ? e->xn : NULL)))
             return st;
         if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
                                      e->ctxo, NULL, NULL, NULL)))
@@ -322,9 +325,16 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
         if (dense) {
             if ((st = dense_ffn(e, L, R))) return st;
         } else {
-            if ((st = mm_moe_forward_dev(c, l, R, e->xn, e->x, NULL, NULL, NULL, NULL,
-                                         f->moe_flags | MM_FWD_ACCUMULATE)))
+            /* above GEMV sizes the next layer's input norm is computed by
+             * the MoE's combine pass (int8 experts) into xn, which the MoE
+             * no longer reads by then */
+            const int next_norm = l + 1 < f->n_layers && !gemv_rows(e, R);
+            int fused = 0;
+            if ((st = mm_moe_forward_norm(c, l, R, e->xn, e->x, f->moe_flags | MM_FWD_ACCUMULATE,
+                                          next_norm ? e->layers[l + 1].front.input_norm : NULL,
+                                          c->front.rms_eps, e->xn, &fused)))
                 return st;
+            xn_ready = fused;
         }
     }
     if (n_want > 0) {

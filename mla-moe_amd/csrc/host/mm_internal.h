@@ -23,6 +23,7 @@ typedef enum {
     K_I8_QUANT_H,
     K_I8_DOWN,
     K_I8_COMBINE,
+    K_I8_COMBINE_NORM,
     K_PACK_I8,
     K_I8_BT,
     K_MLA_QPREP,
@@ -91,6 +92,11 @@ struct mm_ctx {
     int n_layers;
     mm_moe_layer *layers;
     int32_t *moe_cnt;           /* [E] per-expert row counters of the tiled path */
+    /* set by mm_moe_forward_norm for the duration of one forward: the int8
+     * combine also writes rmsnorm(out, norm_w) into norm_xn */
+    const uint16_t *norm_w;
+    float *norm_xn;
+    float norm_eps;
     float *ffn_io;              /* mm_ffn_compute staging: x [H] | out [H] | idx [K] | w [K] */
 
     /* MLA */
@@ -123,6 +129,11 @@ typedef struct {
 /* mm_moe_forward_dev on the fixed workspace fx: fails with
  * MM_ERR_UNSUPPORTED before any launch when the call needs more than
  * fx->cap bytes; allocates nothing. */
+/* mm_moe_forward_dev whose output rows are also normalised into xn_next
+ * (rmsnorm with norm_w, eps) in the combine pass when the int8 path runs
+ * (returns 1 in *fused then; else the caller normalises). */
+int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out, unsigned flags,
+                        const uint16_t *norm_w, float eps, float *xn_next, int *fused);
 int mm_moe_forward_fixed(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
                          const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                          unsigned flags, const mm_fixed_ws *fx);
@@ -174,10 +185,11 @@ int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
 /* mm_mla_front_dev / mm_mla_absorbed_decode_dev with row b on cache
  * sequence slots[b] (slots NULL: sequence b): rows of one sequence may share
  * a call (prefill chunks), causality coming from each row's position /
- * kv_lens[b]. */
+ * kv_lens[b].  xn_pre: rmsnorm(x, input_norm) already computed by the
+ * caller (used above MM_GEMV_NB rows), or NULL. */
 int mm_mla_front_rows(mm_ctx *ctx, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows);
+                      int seq_stride, float *kv_rows, const float *xn_pre);
 int mm_mla_decode_rows(mm_ctx *ctx, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat);

@@ -199,12 +199,12 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                      const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
                      float *kv_rows) {
-    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows);
+    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows, NULL);
 }
 
 int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows) {
+                      int seq_stride, float *kv_rows, const float *xn_pre) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL context");
     if (!c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_dev: call mm_mla_front_init first");
     if (B < 0) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: B < 0");
@@ -250,10 +250,14 @@ int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weigh
             if ((st = mm_gemv_launch(c, &b))) return st;
         }
     } else {
-        float *xb = (float *)(ws + o_xb);
+        const float *xb = (float *)(ws + o_xb);
         char *gws = ws + o_gm;
-        mm_rmsnorm_args ra = {x, w->input_norm, xb, H, f->rms_eps};
-        if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+        if (xn_pre) {
+            xb = (float *)xn_pre;      /* rmsnorm(x, input_norm), computed by the caller */
+        } else {
+            mm_rmsnorm_args ra = {x, w->input_norm, (float *)xb, H, f->rms_eps};
+            if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;
+        }
         /* the query projection (or q_a) and kv_a over the same xb: one pass */
         if ((st = mm_gemm_bf16_ws2(c, ql ? qa : q, ql ? w->q_a_proj : w->q_proj, ql ? ql : QD, comp,
                                    w->kv_a_proj, KVD, xb, H, B, 0, gws)))

@@ -645,9 +645,11 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     }
 
     mm_i8_combine_args ca = {y, ys, wts, out, tiled ? c->moe_cnt : NULL, T, (int)H, (int)K,
-                             (int)E, acc, S > 0};
-    /* two blocks per token: one round of loads per thread at H = 2048 */
-    FAIL_ROUTED(mm_launch(c, K_I8_COMBINE, (unsigned)T, 2, 1, 256, 0, &ca));
+                             (int)E, acc, S > 0, c->norm_w, c->norm_xn, c->norm_eps};
+    if (c->norm_w)   /* one block per token, the row's norm in the same pass */
+        FAIL_ROUTED(mm_launch(c, K_I8_COMBINE_NORM, (unsigned)T, 1, 1, MM_I8_CN_THREADS, 0, &ca));
+    else             /* two blocks per token: one round of loads per thread at H = 2048 */
+        FAIL_ROUTED(mm_launch(c, K_I8_COMBINE, (unsigned)T, 2, 1, 256, 0, &ca));
 #undef FAIL_ROUTED
 
     if (dbg) {
@@ -694,6 +696,24 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
         return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no bf16 weights", layer);
     if (xn == out) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: bf16 path needs out != xn");
     return forward_bf16(c, L, T, xn, out, logits, topk_idx, topk_w, probs, acc, fx);
+}
+
+int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out, unsigned flags,
+                        const uint16_t *norm_w, float eps, float *xn_next, int *fused) {
+    *fused = 0;
+    if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: NULL context");
+    const int can = (flags & MM_FWD_INT8) && c->moe.hidden_size <= MM_I8_CN_MAXH &&
+                    c->moe.hidden_size % 4 == 0 && norm_w && xn_next;
+    if (can) {
+        c->norm_w = norm_w;
+        c->norm_xn = xn_next;
+        c->norm_eps = eps;
+    }
+    const int st = forward(c, layer, T, xn, out, NULL, NULL, NULL, NULL, flags, NULL, NULL);
+    c->norm_w = NULL;
+    c->norm_xn = NULL;
+    if (!st) *fused = can;
+    return st;
 }
 
 int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,

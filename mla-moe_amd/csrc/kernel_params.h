@@ -182,7 +182,13 @@ typedef struct {
     int T, H, K, E;
     int accumulate;
     int has_shared;
+    /* mm_i8_combine_norm: then xn[t] = rmsnorm(out[t], norm_w) (eps) */
+    const uint16_t *norm_w;
+    float *xn;
+    float eps;
 } mm_i8_combine_args;
+#define MM_I8_CN_THREADS 512      /* mm_i8_combine_norm: one block per token */
+#define MM_I8_CN_MAXH 4096
 
 /* Pack a row-major int8 [N, K] matrix into 16x64 fragments, optionally
  * interleaving two matrices per 16-row block (gate/up). */

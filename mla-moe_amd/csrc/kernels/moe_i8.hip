@@ -744,6 +744,66 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_ar
 /* ---- weight packing ----------------------------------------------------------- */
 
 /* One thread per 16-byte lane slice of a fragment. */
+/* mm_i8_combine for one token per block, then the RMSNorm of the combined
+ * row (src/run.c:22-27: (x * inv) * w, inv = 1 / sqrt(sum x^2 / n + eps))
+ * into xn: the next layer's input norm in the same pass.  The row's values
+ * stay in registers; the sum of squares is reduced over the block. */
+extern "C" __global__ __launch_bounds__(MM_I8_CN_THREADS) void mm_i8_combine_norm(mm_i8_combine_args a) {
+    constexpr int NI = MM_I8_CN_MAXH / (4 * MM_I8_CN_THREADS);
+    __shared__ float red[MM_I8_CN_THREADS / MM_WAVE];
+    const int t = blockIdx.x;
+    const float *w = a.topk_w + (size_t)t * a.K;
+    f32x4 res[NI];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int n = (threadIdx.x + MM_I8_CN_THREADS * k) * 4;
+        if (n >= a.H) continue;
+        f32x4 y[MM_KMAX], ys = {0.0f, 0.0f, 0.0f, 0.0f}, o = {0.0f, 0.0f, 0.0f, 0.0f};
+        float wr[MM_KMAX];
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < a.K) {
+                y[r] = *(const f32x4 *)(a.y + ((size_t)t * a.K + r) * a.H + n);
+                wr[r] = w[r];
+            }
+        if (a.has_shared) ys = *(const f32x4 *)(a.ys + (size_t)t * a.H + n);
+        f32x4 *op = (f32x4 *)(a.out + (size_t)t * a.H + n);
+        if (a.accumulate) o = *op;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < MM_KMAX; r++)
+            if (r < a.K) acc += wr[r] * y[r];
+        if (a.has_shared) acc += ys;
+        res[k] = a.accumulate ? o + acc : acc;
+        *op = res[k];
+#pragma unroll
+        for (int u = 0; u < 4; u++) ss += res[k][u] * res[k][u];
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & (MM_WAVE - 1)) == 0) red[threadIdx.x / MM_WAVE] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int v = 0; v < MM_I8_CN_THREADS / MM_WAVE; v++) tot += red[v];
+    const float inv = 1.0f / sqrtf(tot / (float)a.H + a.eps);
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int n = (threadIdx.x + MM_I8_CN_THREADS * k) * 4;
+        if (n >= a.H) continue;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 nw = *(const u32x2 *)(a.norm_w + n);   /* 4 bf16 weights */
+        f32x4 o;
+        o.x = res[k].x * inv * bf16_lo(nw.x);
+        o.y = res[k].y * inv * bf16_hi(nw.x);
+        o.z = res[k].z * inv * bf16_lo(nw.y);
+        o.w = res[k].w * inv * bf16_hi(nw.y);
+        *(f32x4 *)(a.xn + (size_t)t * a.H + n) = o;
+    }
+    if (a.cnt && t == 0)
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
+}
+
 extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) {
     const int KB = a.K / 64, NB = a.N / 16, NS = a.src1 ? 2 : 1;
     const size_t total = (size_t)NB * NS * KB * 64;
