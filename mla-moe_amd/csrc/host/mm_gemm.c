@@ -26,10 +26,19 @@ static void skinny_plan(int nb, int n_in, int *nsplit, int *kr) {
 
 static int skinny_nb(int d) { return (d + MM_SKINNY_BN - 1) / MM_SKINNY_BN; }
 
+/* one long matrix (the LM head): the wide form, 64 * MM_SKINNY_WIDE_WC
+ * columns per block */
+static int skinny_wide(int d0, int d1) { return d1 <= 0 && skinny_nb(d0) >= MM_SKINNY_WIDE_MIN_NB; }
+static int skinny_nb_wide(int d) {
+    return (d + 64 * MM_SKINNY_WIDE_WC - 1) / (64 * MM_SKINNY_WIDE_WC);
+}
+
 size_t mm_gemm_bf16_ws2_bytes(int T, int n_in, int d0, int d1, unsigned flags) {
     if (skinny_ok(T, n_in)) {                    /* only the split partials */
         int ns, kr;
-        skinny_plan(skinny_nb(d0) + (d1 > 0 ? skinny_nb(d1) : 0), n_in, &ns, &kr);
+        skinny_plan(skinny_wide(d0, d1) ? skinny_nb_wide(d0)
+                                        : skinny_nb(d0) + (d1 > 0 ? skinny_nb(d1) : 0),
+                    n_in, &ns, &kr);
         return ns > 1 ? al256((size_t)ns * T * ((size_t)d0 + (d1 > 0 ? d1 : 0)) * 4) : 256;
     }
     const int split = (flags & MM_MATMUL_X_BF16) == 0;
@@ -51,12 +60,15 @@ int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1
     if (skinny_ok(T, n_in)) {
         /* fp32 x converted while staged; ws holds the split partials; both
          * matrices in one launch */
-        const int nb0 = skinny_nb(d0), nb = nb0 + (d1 ? skinny_nb(d1) : 0);
+        const int wide = skinny_wide(d0, d1);
+        const int nb0 = wide ? skinny_nb_wide(d0) : skinny_nb(d0), nb = nb0 + (d1 ? skinny_nb(d1) : 0);
         int ns, kr;
         skinny_plan(nb, n_in, &ns, &kr);
         mm_gemm_skinny_args k = {x, w0, y0, (float *)ws, T, d0, n_in, ns, kr, split, acc,
                                  w1, y1, d1, nb0, 0};
-        if ((st = mm_launch(c, K_GEMM_SKINNY, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
+        if ((st = mm_launch(c, wide ? K_GEMM_SKINNY_WIDE : K_GEMM_SKINNY, (unsigned)nb, (unsigned)ns,
+                            1, 256, 0, &k)))
+            return st;
         if (ns == 1) return MM_OK;
         mm_skinny_reduce_args r = {(float *)ws, y0, T, d0, ns, acc, d1 ? y1 : NULL, d1};
         const size_t n = (size_t)T * ((size_t)d0 + d1);

@@ -46,6 +46,7 @@ typedef enum {
     K_EMBED,
     K_SWIGLU,
     K_GEMM_SKINNY,
+    K_GEMM_SKINNY_WIDE,
     K_SKINNY_REDUCE,
     K_REDUCE_RMSNORM,
     K_ZERO32,

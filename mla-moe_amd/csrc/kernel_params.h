@@ -350,6 +350,11 @@ typedef struct {
 #ifndef MM_SKINNY_BN
 #define MM_SKINNY_BN 64           /* output columns per block (4 waves x 16) */
 #endif
+#ifndef MM_SKINNY_WIDE_WC
+#define MM_SKINNY_WIDE_WC 2       /* mm_gemm_skinny_wide: 16-column groups per wave */
+#endif
+/* one matrix of at least this many 64-column blocks takes the wide form */
+#define MM_SKINNY_WIDE_MIN_NB 1024
 typedef struct {
     const float *x;          /* [T, n_in] fp32, converted while staged */
     const uint16_t *w;       /* [d_out, n_in] */

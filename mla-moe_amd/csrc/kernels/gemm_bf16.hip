@@ -243,14 +243,19 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_bf16(mm_gemm_bf16_args
  * T - 1 and are not stored).  With
  * nsplit > 1 the K range is split over grid.y and mm_skinny_reduce sums the
  * partials in split order. */
-#ifndef SK_D
-#define SK_D 4                       /* chunks of W in flight per wave */
-#endif
-#define SK_WC (MM_SKINNY_BN / 64)   /* 16-column groups per wave */
+/* Two forms: 64 output columns per block (one 16-column group per wave,
+ * 4 chunks of W in flight), and for long outputs (the LM head) 64 *
+ * MM_SKINNY_WIDE_WC columns per block (MM_SKINNY_WIDE_WC groups per wave, 2
+ * chunks in flight), which stages each x chunk (64 rows x 64 inputs, fp32:
+ * twice the bytes of one wave-group's weights) once for more weights.  LM
+ * head at 64 rows (102400 x 2048): 154.6 -> ~136 us with 2 or 4 groups. */
+#define SK_WC1 (MM_SKINNY_BN / 64)   /* 16-column groups per wave */
+#define SK_D1 4                      /* chunks of W in flight per wave */
+#define SK_DW 2
 #define SK_ROW 72                    /* LDS row stride (bf16) of a staged x chunk */
 #define SK_STAGE (2 * 64 * SK_ROW)   /* bf16 per stage: hi rows then lo rows */
 
-template <bool SPLIT>
+template <bool SPLIT, int SK_WC, int SK_D>
 __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*xs)[SK_STAGE]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     /* column block bx of matrix `seg` (the second one past nb0 blocks) */
@@ -380,9 +385,17 @@ __device__ __forceinline__ void skinny(const mm_gemm_skinny_args &a, uint16_t (*
 extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny(mm_gemm_skinny_args a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][SK_STAGE];
     if (a.split)
-        skinny<true>(a, xs);
+        skinny<true, SK_WC1, SK_D1>(a, xs);
     else
-        skinny<false>(a, xs);
+        skinny<false, SK_WC1, SK_D1>(a, xs);
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny_wide(mm_gemm_skinny_args a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][SK_STAGE];
+    if (a.split)
+        skinny<true, MM_SKINNY_WIDE_WC, SK_DW>(a, xs);
+    else
+        skinny<false, MM_SKINNY_WIDE_WC, SK_DW>(a, xs);
 }
 
 /* y (+)= sum over splits s = 0 .. nsplit-1 of part[s], in that order. */

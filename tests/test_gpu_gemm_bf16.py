@@ -60,9 +60,10 @@ def test_matmul_shapes(ctx, oracle, T, d_out, n_in):
 
 def test_skinny_integer_exact(ctx):
     """The skinny-M path with integer-valued operands (every summation order
-    exact): bit for bit, with and without splits of K."""
+    exact): bit for bit, with and without splits of K, and the wide form
+    of long outputs (65600 columns)."""
     rng = np.random.default_rng(4)
-    for T, d_out, n_in in ((64, 640, 256), (7, 96, 4096)):
+    for T, d_out, n_in in ((64, 640, 256), (7, 96, 4096), (33, 65600, 128)):
         w = rng.integers(-8, 9, size=(d_out, n_in)).astype(np.float32)
         x = rng.integers(-8, 9, size=(T, n_in)).astype(np.float32)
         got = ctx.matmul(x, synth.bf16_from_f32(w))

@@ -93,12 +93,12 @@ def test_lm_head_shapes(ctx, oracle, B, V, H):
 
 def test_lm_head_dsv2_vocab(ctx, oracle):
     """DeepSeek-V2-Lite's LM head: vocab 102400 x hidden 2048, one decode
-    token (GEMV) and five (GEMM)."""
+    token (GEMV), five and 64 (the skinny GEMM's wide form)."""
     rng = np.random.default_rng(77)
     V, H = 102400, 2048
     lm = synth.normal_bf16(rng, (V, H), 0.02)
     norm = synth.bf16_from_f32(1.0 + synth.normal_f32(rng, (H,), 0.1))
-    for B in (1, 5):
+    for B in (1, 5, 64):
         print(f"lm_head dsv2 B={B}", flush=True)
         x = synth.normal_f32(rng, (B, H))
         logits, tokens = ctx.lm_head(x, norm, 1e-6, lm)
