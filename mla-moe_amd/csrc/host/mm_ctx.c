@@ -50,6 +50,7 @@ static const struct {
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
     [K_I8_BT] = {"mm_i8_gemm_bt", MOD_GEMM_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
+    [K_MLA_ROPE_QPREP] = {"mm_mla_rope_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
     [K_MLA_UV] = {"mm_mla_uv", MOD_MLA},

@@ -33,6 +33,8 @@ struct mm_engine {
     int cap;                   /* positions every layer holds: min of lcap */
     int max_rows;              /* token rows per step */
     float *x, *xn, *q, *ctxo, *g, *u;   /* [max_rows, ...] step activations */
+    float *fcomp;              /* [MM_SKINNY_T, KVL + QKR]: kv_a's output of steps of up to
+                                  MM_SKINNY_T rows, read by the RoPE / qprep launch */
     int32_t *d_io;             /* device [IO_ARRAYS][max_rows]: see IO_* */
     int32_t *h_io;             /* pinned host, same layout */
     int32_t *last_pos;         /* [max_batch] host: a step's check of its rows' positions */
@@ -49,7 +51,7 @@ void mm_engine_destroy(mm_engine *e) {
             if (e->cache[l]) hipFree(e->cache[l]);
         free(e->cache);
     }
-    void *dev[] = {e->x, e->xn, e->q, e->ctxo, e->g, e->u, e->d_io};
+    void *dev[] = {e->x, e->xn, e->q, e->ctxo, e->g, e->u, e->d_io, e->fcomp};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (e->h_io) hipHostFree(e->h_io);
@@ -161,7 +163,8 @@ int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
         {(void **)&e->x, MR * H * 4}, {(void **)&e->xn, MR * H * 4}, {(void **)&e->q, MR * QD * 4},
         {(void **)&e->ctxo, MR * (size_t)g->n_heads * g->v_head_dim * 4},
         {(void **)&e->g, MR * DI * 4}, {(void **)&e->u, MR * DI * 4},
-        {(void **)&e->d_io, IO_ARRAYS * MR * 4}};
+        {(void **)&e->d_io, IO_ARRAYS * MR * 4},
+        {(void **)&e->fcomp, (size_t)MM_SKINNY_T * KVD * 4}};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         if (hipMalloc(bufs[i].p, bufs[i].n) != hipSuccess) {
             mm_engine_destroy(e);
@@ -314,11 +317,16 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
         const mm_engine_layer *L = &e->layers[l];
         const int pre = xn_ready;
         xn_ready = 0;
+        /* up to MM_SKINNY_T rows the RoPE / cache append runs in the absorbed
+         * queries' launch (one launch fewer per layer) */
+        mm_mla_rope_args ra;
+        const int fuse = R <= MM_SKINNY_T;
         if ((st = mm_mla_front_rows(c, R, e->x, &L->front, d_pos, d_slot, e->q, e->cache[l], e->lcap[l],
-                                    NULL, pre ? e->xn : NULL)))
+                                    NULL, pre ? e->xn : NULL, fuse ? e->fcomp : NULL,
+                                    fuse ? &ra : NULL)))
             return st;
         if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
-                                     e->ctxo, NULL, NULL, NULL)))
+                                     e->ctxo, NULL, NULL, NULL, fuse ? &ra : NULL)))
             return st;
         const int dense = l < f->first_k_dense;
         if ((st = oproj_post_norm(e, L, R, dense))) return st;

@@ -27,6 +27,7 @@ typedef enum {
     K_PACK_I8,
     K_I8_BT,
     K_MLA_QPREP,
+    K_MLA_ROPE_QPREP,
     K_MLA_ATTN,
     K_MLA_COMBINE,
     K_MLA_UV,
@@ -188,12 +189,20 @@ int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
  * a call (prefill chunks), causality coming from each row's position /
  * kv_lens[b].  xn_pre: rmsnorm(x, input_norm) already computed by the
  * caller (used above MM_GEMV_NB rows), or NULL. */
+/* defer (or NULL; B <= MM_SKINNY_T): the RoPE / cache-append launch is not
+ * made; its arguments go to *defer for mm_mla_decode_rows to run with the
+ * absorbed queries in one launch, and kv_a's output goes to comp_buf
+ * ([B, KVL + QKR] fp32, the caller's) instead of the workspace, which later
+ * calls reuse before that launch runs. */
 int mm_mla_front_rows(mm_ctx *ctx, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows, const float *xn_pre);
+                      int seq_stride, float *kv_rows, const float *xn_pre, float *comp_buf,
+                      mm_mla_rope_args *defer);
+/* rope (or NULL): the deferred RoPE of mm_mla_front_rows, run with qprep. */
 int mm_mla_decode_rows(mm_ctx *ctx, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
-                       float *ctx_out, float *qabs, float *probs, float *clat);
+                       float *ctx_out, float *qabs, float *probs, float *clat,
+                       const mm_mla_rope_args *rope);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

@@ -69,12 +69,13 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                                int kv_len, float *ctx_out, float *qabs, float *probs,
                                float *clat) {
     return mm_mla_decode_rows(c, layer, B, q, cache, seq_stride, NULL, kv_lens, kv_len, ctx_out,
-                              qabs, probs, clat);
+                              qabs, probs, clat, NULL);
 }
 
 int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
-                       float *ctx_out, float *qabs, float *probs, float *clat) {
+                       float *ctx_out, float *qabs, float *probs, float *clat,
+                       const mm_mla_rope_args *rope) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
     if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
         return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
@@ -119,9 +120,16 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const int QKN = g->qk_nope_head_dim;
     const size_t nkvb = (size_t)NH * (QKN + g->v_head_dim) * MM_MLA_KVL;
     mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, B, NH, QKN};
-    if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVL / 64, (unsigned)NH, (unsigned)((B + 31) / 32), 256,
-                        0, &qa)))
+    if (rope) {   /* the front's RoPE / cache append in the same launch */
+        mm_mla_rope_qprep_args rq;
+        rq.r = *rope;
+        rq.qp = qa;
+        const unsigned nq = (unsigned)(MM_MLA_KVL / 64 * NH * ((B + 31) / 32));
+        if ((st = mm_launch(c, K_MLA_ROPE_QPREP, (unsigned)B + nq, 1, 1, 256, 0, &rq))) return st;
+    } else if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVL / 64, (unsigned)NH, (unsigned)((B + 31) / 32),
+                               256, 0, &qa))) {
         return st;
+    }
     mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
                            part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
@@ -199,12 +207,13 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                      const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
                      float *kv_rows) {
-    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows, NULL);
+    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows, NULL, NULL, NULL);
 }
 
 int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows, const float *xn_pre) {
+                      int seq_stride, float *kv_rows, const float *xn_pre, float *comp_buf,
+                      mm_mla_rope_args *defer) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL context");
     if (!c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_dev: call mm_mla_front_init first");
     if (B < 0) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: B < 0");
@@ -239,6 +248,14 @@ int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weigh
     char *ws;
     if ((st = mm_workspace(c, o_gm + (gemv ? 0 : gw), (void **)&ws))) return st;
     float *comp = (float *)(ws + o_cp), *qa = (float *)(ws + o_qa);
+    if (defer) {
+        /* the deferred launch runs after later calls have reused the
+         * workspace: comp lives in the caller's buffer instead */
+        if (!comp_buf || B > MM_SKINNY_T)
+            return mm_fail(MM_ERR_INVALID, "mm_mla_front_rows: a deferred RoPE needs comp_buf and "
+                           "B <= %d", MM_SKINNY_T);
+        comp = comp_buf;
+    }
     if (gemv) {
         /* input norm fused; the query projection (or q_a) and kv_a in one row space */
         mm_gemv_args a = {x, w->input_norm, f->rms_eps, ql ? w->q_a_proj : w->q_proj, w->kv_a_proj,
@@ -271,5 +288,9 @@ int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weigh
     mm_mla_rope_args r = {q, comp, w->kv_a_norm, c->front_inv, pos, cache, kv_rows, B, NH,
                           g->qk_nope_head_dim, g->qk_rope_head_dim, g->kv_lora_rank, seq_stride,
                           f->rope_interleaved, f->mla_norm_eps, slots};
+    if (defer) {
+        *defer = r;
+        return MM_OK;
+    }
     return mm_launch(c, K_MLA_ROPE, (unsigned)B, 1, 1, 256, 0, &r);
 }

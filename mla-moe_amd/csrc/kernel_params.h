@@ -462,4 +462,12 @@ typedef struct {
     const int32_t *slots;    /* [B] cache sequence of token b, or 0: sequence b */
 } mm_mla_rope_args;
 
+/* RoPE / kv norm / cache append (one block per token) and the absorbed
+ * queries in one launch: blocks [0, B) are mm_mla_rope's, the rest
+ * mm_mla_qprep's grid (KVL / 64, NH, ceil(B / 32)) in x-fastest order. */
+typedef struct {
+    mm_mla_rope_args r;
+    mm_mla_qprep_args qp;
+} mm_mla_rope_qprep_args;
+
 #endif /* MLAMOE_KERNEL_PARAMS_H */

@@ -98,8 +98,7 @@ __device__ __forceinline__ void hl_gemm_32x16(const float *X, size_t xs, int mro
  * per-head GEMM with W_UK_h kept transposed ([r][d], prepared at load
  * time).  grid (KVL / 64 column slabs, NH, ceil(B / 32)), 4 waves of 16
  * columns. */
-extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
-    const int slab = blockIdx.x, h = blockIdx.y, b0 = blockIdx.z * 32;
+__device__ __forceinline__ void qprep_block(const mm_mla_qprep_args &a, int slab, int h, int b0) {
     const int QKR = MM_MLA_QKR, QKN = a.QKN;
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
@@ -115,6 +114,10 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args
             const int bb = 16 * t + 4 * (lane >> 4) + i;
             if (bb < mrows) a.qabs[((size_t)(b0 + bb) * a.NH + h) * KVL + e] = acc[t][i];
         }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
+    qprep_block(a, blockIdx.x, blockIdx.y, blockIdx.z * 32);
 }
 
 /* Load-time: W_UK_h transposed, wukT[h][r][d] = kv_b[h (QKN + VHD) + d][r]. */
@@ -547,11 +550,11 @@ __device__ __forceinline__ uint16_t bf16_rne_keepnan(float x) {
     return x != x ? (uint16_t)0x7fc0u : bf16_rne(x);
 }
 
-extern "C" __global__ __launch_bounds__(256) void mm_mla_rope(mm_mla_rope_args a) {
+__device__ __forceinline__ void rope_token(const mm_mla_rope_args &a, int b) {
 #pragma clang fp contract(off)
     __shared__ float cs[2][128];
     __shared__ float red[256 / MM_WAVE];
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int half = a.qkr / 2, kvd = a.kvl + a.qkr;
     const int p = a.pos[b];
     if (tid < half) {
@@ -625,4 +628,21 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_rope(mm_mla_rope_args a
         if (wr) { dst[o0] = bf16_rne_keepnan(r0); dst[o1] = bf16_rne_keepnan(r1); }
         if (ko) { ko[o0] = r0; ko[o1] = r1; }
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void mm_mla_rope(mm_mla_rope_args a) {
+    rope_token(a, blockIdx.x);
+}
+
+/* mm_mla_rope and mm_mla_qprep in one launch (independent: RoPE writes the
+ * q_pe parts and the cache row, qprep reads the q_nope parts): one launch
+ * fewer per decode layer. */
+extern "C" __global__ __launch_bounds__(256) void mm_mla_rope_qprep(mm_mla_rope_qprep_args a) {
+    const int b = blockIdx.x;
+    if (b < a.r.B) {
+        rope_token(a.r, b);
+        return;
+    }
+    const int v = b - a.r.B, nx = KVL / 64;
+    qprep_block(a.qp, v % nx, (v / nx) % a.qp.NH, v / (nx * a.qp.NH) * 32);
 }
