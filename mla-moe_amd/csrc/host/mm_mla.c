@@ -95,7 +95,12 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
            (size_t)B * HG0 * ((kv_len + chunk - 1) / chunk) < MM_MLA_MIN_BLOCKS &&
            (kv_len + chunk / 2 - 1) / (chunk / 2) <= 64)
         chunk /= 2;
+    /* a second chunk of under half a chunk (short contexts): one chunk of
+     * twice the length instead, whose block writes clat itself (no merge
+     * launch) */
+    if (chunk < MM_MLA_CHUNK && kv_len > chunk && kv_len <= chunk + chunk / 2) chunk *= 2;
     const int nchunks = (kv_len + chunk - 1) / chunk;
+    const int direct = nchunks == 1 && !probs;
     if (kv_len > MM_MAX_KV_LEN || nchunks > MM_MLA_MAXCH)
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_mla_absorbed_decode_dev: kv_len %d > %d", kv_len,
                        MM_MAX_KV_LEN);
@@ -131,7 +136,8 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
         return st;
     }
     mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
-                           part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots};
+                           part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots,
+                           direct ? clat : NULL};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
@@ -143,7 +149,8 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     /* merge: split the latent columns over 4 blocks per (head, sequence)
      * when the grid would otherwise have fewer than 128 blocks */
     const unsigned zc = (size_t)NH * B < 128 ? MM_MLA_KVL / 128 : 1;
-    if ((st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, zc, 256, 0, &ca))) return st;
+    if (!direct && (st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, zc, 256, 0, &ca)))
+        return st;
     return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,
                      (unsigned)((B + 31) / 32), 256, 0, &ca);
 }

@@ -308,6 +308,8 @@ typedef struct {
     int NH, HG, nchunks, QKN;
     int chunk;                /* keys per block: a multiple of 16 * MM_MLA_AW, <= MM_MLA_CHUNK */
     const int32_t *slots;     /* [B] cache sequence of row b, or 0: sequence b */
+    float *clat;              /* one chunk (nchunks == 1, no probabilities): clat [B, NH, KVL]
+                                 written here, O / l as the merge computes it; else 0 */
 } mm_mla_attn_args;
 
 /* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */

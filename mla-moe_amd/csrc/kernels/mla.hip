@@ -164,7 +164,7 @@ static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
  * accumulator is rescaled on few sub-tiles.  The final O / l is the same
  * quantity for any m. */
 #define RESCALE_TAU 8.0f
-static_assert((AW * 16 * OROW + AW * 32) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
+static_assert((AW * 16 * OROW + AW * 32 + 16) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
 static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
 /* grid (nchunks, B, HG), AW waves; row b attends to the first kv_lens[b]
@@ -399,6 +399,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
         }
     }
     const size_t pidx = ((size_t)(b * a.HG + hg) * a.nchunks + chunk);
+    float *linv = mlb + AW * 32;                     /* [16]: one chunk, 1 / l per head */
     if (w == 0 && g == 0) {
         float lsum = 0.0f;
 #pragma unroll
@@ -406,10 +407,27 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             const float mj = mlb[j * 32 + kl];
             lsum += mj == -INFINITY ? 0.0f : mlb[j * 32 + 16 + kl] * __expf(mj - mm);
         }
-        a.part_ml[pidx * 32 + kl] = mm;
-        a.part_ml[pidx * 32 + 16 + kl] = lsum;
+        if (a.clat) {
+            linv[kl] = 1.0f / lsum;
+        } else {
+            a.part_ml[pidx * 32 + kl] = mm;
+            a.part_ml[pidx * 32 + 16 + kl] = lsum;
+        }
     }
     __syncthreads();
+    if (a.clat) {   /* the whole context in this block: clat = O (1 / l), the merge's values */
+#pragma unroll
+        for (int j = 0; j < 16 * KVL / (4 * AW * MM_WAVE); j++) {
+            const int e = 4 * (tid + j * AW * MM_WAVE);
+            const int hh = e / KVL, col = e % KVL;
+            f32x4 v = *(const f32x4 *)(ob + hh * OROW + col);
+#pragma unroll
+            for (int k = 1; k < AW; k++) v += *(const f32x4 *)(ob + (size_t)k * 16 * OROW + hh * OROW + col);
+            const int head = hg * 16 + hh;
+            if (head < a.NH) *(f32x4 *)(a.clat + ((size_t)b * a.NH + head) * KVL + col) = v * linv[hh];
+        }
+        return;
+    }
     float *po = a.part_o + pidx * 16 * KVL;
 #pragma unroll
     for (int j = 0; j < 16 * KVL / (4 * AW * MM_WAVE); j++) {
