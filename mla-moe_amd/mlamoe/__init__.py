@@ -490,9 +490,10 @@ class Context:
                                                 p(kv_lens), kv_len, ctx_out.ptr, p(qabs),
                                                 p(probs), p(clat)))
 
-    def mla_absorbed_decode(self, layer, q, cache, kv_len, kv_lens=None):
+    def mla_absorbed_decode(self, layer, q, cache, kv_len, kv_lens=None, want_probs=True):
         """Host arrays: q [B, NH, QKN+QKR] fp32, cache [B, L, KVL+QKR] bf16
-        (uint16).  Returns ctx [B, NH*VHD], qabs, probs, clat."""
+        (uint16).  Returns ctx [B, NH*VHD], qabs, probs (None without
+        want_probs), clat."""
         cfg = self._mla_cfg
         q = np.ascontiguousarray(q, np.float32)
         cache = np.ascontiguousarray(cache, np.uint16)
@@ -501,13 +502,14 @@ class Context:
         bufs = dict(q=self.to_device(q), cache=self.to_device(cache),
                     ctx=self.empty((B, NH * VHD), np.float32),
                     qabs=self.empty((B, NH, KVL), np.float32),
-                    probs=self.empty((B, NH, kv_len), np.float32),
                     clat=self.empty((B, NH, KVL), np.float32))
+        if want_probs:
+            bufs["probs"] = self.empty((B, NH, kv_len), np.float32)
         if kv_lens is not None:
             bufs["lens"] = self.to_device(np.ascontiguousarray(kv_lens, np.int32))
         self.mla_absorbed_decode_dev(layer, B, bufs["q"], bufs["cache"], L, kv_len, bufs["ctx"],
-                                     bufs.get("lens"), bufs["qabs"], bufs["probs"], bufs["clat"])
-        out = tuple(bufs[k].download() for k in ("ctx", "qabs", "probs", "clat"))
+                                     bufs.get("lens"), bufs["qabs"], bufs.get("probs"), bufs["clat"])
+        out = tuple(bufs[k].download() if k in bufs else None for k in ("ctx", "qabs", "probs", "clat"))
         for b in bufs.values():
             b.free()
             self._bufs.remove(b)

@@ -78,6 +78,22 @@ def test_mla_longest_context(ctx, oracle):
     run_case(ctx, oracle, 16, 1, 32768, 32768, 640)
 
 
+@pytest.mark.parametrize("B,kv_len", [(2, 1), (2, 37), (2, 80), (64, 65), (64, 90)])
+def test_mla_one_chunk_without_probs(ctx, oracle, B, kv_len):
+    """Without the probabilities a context of one chunk (at most 1.5 of the
+    small-grid chunk of 64 keys) has its attention block write clat: the
+    same values as the merge's (bit for bit) and the oracle's."""
+    got = run_case(ctx, oracle, 16, B, kv_len, kv_len, 700 + B + kv_len)
+    rng = np.random.default_rng(700 + B + kv_len)
+    KVL, QKR, QKN, VHD, NH = 512, 64, 128, 128, 16
+    synth.normal_bf16(rng, (NH * (QKN + VHD), KVL), 0.02)
+    q = synth.normal_f32(rng, (B, NH, QKN + QKR))
+    cache = synth.normal_bf16(rng, (B, kv_len, KVL + QKR), 1.0)
+    c2, _, p2, cl2 = ctx.mla_absorbed_decode(0, q, cache, kv_len, want_probs=False)
+    assert p2 is None
+    assert np.array_equal(cl2, got[3]) and np.array_equal(c2, got[0])
+
+
 @pytest.mark.parametrize("kv_len", [32769, 163840])
 def test_mla_beyond_64_chunks(ctx, oracle, kv_len):
     """Past 64 chunks the merge strides over up to 512 chunk partials:
