@@ -355,8 +355,10 @@ typedef struct {
 #ifndef MM_SKINNY_WIDE_WC
 #define MM_SKINNY_WIDE_WC 2       /* mm_gemm_skinny_wide: 16-column groups per wave */
 #endif
-/* one matrix of at least this many 64-column blocks takes the wide form */
+/* outputs of at least this many 64-column blocks take the wide form */
+#ifndef MM_SKINNY_WIDE_MIN_NB
 #define MM_SKINNY_WIDE_MIN_NB 1024
+#endif
 typedef struct {
     const float *x;          /* [T, n_in] fp32, converted while staged */
     const uint16_t *w;       /* [d_out, n_in] */
