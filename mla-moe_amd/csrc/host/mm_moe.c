@@ -14,6 +14,7 @@
 #define BF16_NT_MAX 8         /* tokens per pass of the bf16 GEMV path */
 #define GU_ROWS_PER_BLOCK 4   /* stage 1: one gate/up row pair per wave */
 #define GU2_ROWS_PER_BLOCK 16 /* stage 2: four row pairs per wave, two at a time */
+#define RSH_TMAX 4            /* tokens up to which the shared gate/up joins the router launch */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
 #define ROUTER_TOKENS_PER_BLOCK (4 * MM_ROUTER_TPW)
 
@@ -410,21 +411,29 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         a.n_blocks_per_token = (I + GU2_ROWS_PER_BLOCK - 1) / GU2_ROWS_PER_BLOCK;
         if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
             /* small T: the router one token per block (product / chain
-             * form), then every gate/up -- routed and shared -- in one
-             * launch: the shared expert's GEMV does not wait on the router's
-             * add chains, but stage 1's LDS and registers (those of the
-             * chain-per-lane router) no longer hold its blocks to two per
-             * CU either */
+             * form); up to RSH_TMAX tokens the shared expert's gate/up runs
+             * in the same launch (it does not wait on the routing; one block
+             * per CU there, the router's LDS), else with the routed gate/up */
             a.r.n_router_blocks = Tc;
-            if ((st = mm_launch(c, K_ROUTER_PC, (unsigned)Tc, 1, 1, 256, 0, &a.r))) return st;
             a.gate = L->eg;
             a.up = L->eu;
             a.sgate = L->sg;
             a.sup = L->su;
             a.nsh_parts = S / I;
-            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token,
-                                (unsigned)(Tc * K + Tc * a.nsh_parts), 1, 256, 0, &a)))
-                return st;
+            const unsigned nsh = (unsigned)(Tc * a.nsh_parts);
+            if (Tc <= RSH_TMAX) {
+                if ((st = mm_launch(c, K_MOE_BF16_RSH, (unsigned)Tc + a.n_blocks_per_token * nsh, 1, 1,
+                                    256, 0, &a)))
+                    return st;
+                if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, (unsigned)(Tc * K), 1, 256,
+                                    0, &a)))
+                    return st;
+            } else {
+                if ((st = mm_launch(c, K_ROUTER_PC, (unsigned)Tc, 1, 1, 256, 0, &a.r))) return st;
+                if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, (unsigned)(Tc * K) + nsh, 1,
+                                    256, 0, &a)))
+                    return st;
+            }
         } else {
             a.r.n_router_blocks = (Tc + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK;
             a.gate = L->sg;

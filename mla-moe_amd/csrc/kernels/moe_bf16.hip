@@ -142,6 +142,27 @@ extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc(mm_router
     router_block_pc<RPC_HC>(a, lds);
 }
 
+/* Small T: the router (one token per block, blocks [0, T)) and the shared
+ * expert's gate/up (the other blocks, stage 2's shared parts: row block
+ * x, then (token, part) v = t nsh_parts + j) in one launch -- the shared
+ * weight stream runs on the CUs the router's add chains leave idle.  The
+ * router's LDS holds every block of the launch to one per CU, which is
+ * enough for a 23 MB stream in the chains' ~11 us. */
+extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_moe_bf16_router_sh(mm_gu_bf16_args a) {
+    __shared__ __attribute__((aligned(16))) float lds[RPC_LDS_FLOATS];
+    if ((int)blockIdx.x < a.T) {
+        router_block_pc<RPC_HC>(a.r, lds);
+        return;
+    }
+    const int b = blockIdx.x - a.T;
+    const int row0 = (b % a.n_blocks_per_token) * a.rows_per_block;
+    const int nrows = min(a.rows_per_block, a.I - row0);
+    const int v = b / a.n_blocks_per_token, t = v / a.nsh_parts, j = v % a.nsh_parts;
+    const size_t off = (size_t)j * a.I * a.H;
+    gu_rows_x1(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
+               a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), (a.K + j) * a.I, 1.0f);
+}
+
 extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_gu_bf16_args a) {
     __shared__ float lds[MM_ROUTER_LDS_FLOATS];
     if ((int)blockIdx.x < a.r.n_router_blocks) {
