@@ -487,7 +487,7 @@ static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled
     ba.seg[0] = *ta;
     if (ts) ba.seg[1] = *ts;
     ba.nseg = ts ? 2 : 1;
-    return mm_launch(c, K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
+    return mm_launch(c, ta->dbg_acc ? K_I8_BT_DBG : K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
 }
 
 /* A tiled call that fails after its routing launch leaves rows counted in

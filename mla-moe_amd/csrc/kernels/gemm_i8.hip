@@ -33,9 +33,14 @@
  * the kernel is bound by the loads a CU can take in from L2, not by MFMA
  * issue or load latency (a deeper ring changes nothing).
  *
- * MFMA 32x32x32 i8 layout: A lane l = row l % 32, K bytes 16 (l / 32) .. + 15;
- * B likewise by column; result register 4 g + i of lane l is row
- * 8 g + 4 (l / 32) + i, column l % 32.
+ * MFMA 32x32x32 i8 layout: src0 lane l = row l % 32, K bytes 16 (l / 32) .. + 15;
+ * src1 likewise by column; result register 4 g + i of lane l is row
+ * 8 g + 4 (l / 32) + i, column l % 32.  The weights go in as src0 and the
+ * activation rows as src1, so the result is the output tile transposed:
+ * lane l holds activation row l % 32 and, in registers 4 g .. 4 g + 3, four
+ * consecutive output columns 8 g + 4 (l / 32) .. + 3, which the epilogue
+ * stores as one 16-byte write (a quarter of the stores of the other operand
+ * order, whose lanes hold one column of four rows).
  */
 #include <type_traits>
 
@@ -53,6 +58,11 @@ __device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
 #define BT_LPS 6                 /* loads per wave per stage: 2 of A, 4 of B */
 static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
 static_assert(BT_P >= 1 && BT_P <= 3, "the vmcnt waits of the K loop count up to two later stages");
+
+/* registers 4 g .. 4 g + 3 of an accumulator */
+__device__ __forceinline__ i32x4 acc4(const v16i &c, int g) {
+    return (i32x4){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+}
 
 /* position of 16-byte chunk q of staged A row R (64 bytes per row): q ^ swz64(R);
  * any 16 consecutive rows then cover all 64 banks once for a fixed q */
@@ -76,6 +86,8 @@ struct bt_shared {
     int arow[2][MM_I8B_BM];                  /* A row of each tile row (two tiles in flight) */
     __attribute__((aligned(16))) int rid[2][MM_I8B_BM];     /* output row id, -1 = padding */
     __attribute__((aligned(16))) float sa[2][MM_I8B_BM];    /* A row scale */
+    /* column scales of the slab: gate/up [gate 128 | up 128], plain 256 */
+    __attribute__((aligned(16))) float cs[2][2 * MM_I8B_BM];
 };
 
 /* A tile of the grouped GEMM: segment si, expert e, column slab, rows
@@ -137,7 +149,7 @@ struct bt_xcd_list {
     __device__ int operator()(int t) const { return t < len0 ? lo0 + t : lo1 + (t - len0); }
 };
 
-template <bool GU>
+template <bool GU, bool DBG>
 __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_shared &sh,
                                        const bt_xcd_list &xl, int t, int t_step) {
     const int t_end = xl.len;
@@ -248,25 +260,20 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         const bt_tile_id nxt = has_next ? bt_decode(a, sh, xl(tn)) : cur;
 
         /* loads whose results are used after the K loop: this tile's row
-         * scales and column scales, the next tile's row ids */
+         * scales and column scales (thread tid: slab column tid, gate/up:
+         * gate column tid or up column tid - 128), the next tile's row ids */
         float sa_r = 0.0f;
         int nrid = -1, narow = 0;
         if (tid < MM_I8B_BM) {
             sa_r = g.sa[sh.arow[buf][tid]];
             if (has_next) bt_row(a.seg[nxt.si], nxt, tid, &nrid, &narow);
         }
-        const float *sb0 = g.sb0 + (size_t)cur.e * g.sb_expert_stride;
-        const float *sb1 = GU ? g.sb1 + (size_t)cur.e * g.sb_expert_stride : nullptr;
         const int N = g.N;
-        float c0[NT], c1[NT];
-        int colv[NT];
-#pragma unroll
-        for (int q = 0; q < NT; q++) {
-            const int col = (GU ? cur.slab * 8 + 2 * wave : cur.slab * 16 + 4 * wave + 2 * q) * 16 + l32;
-            colv[q] = col;
-            const int cc = min(col, N - 1);
-            c0[q] = sb0[cc];
-            c1[q] = GU ? sb1[cc] : 0.0f;
+        const int slab_c0 = cur.slab * (GU ? 128 : 256);   /* first output column of the slab */
+        float cs_r;
+        {
+            const float *sb = (GU && tid >= 128 ? g.sb1 : g.sb0) + (size_t)cur.e * g.sb_expert_stride;
+            cs_r = sb[min(slab_c0 + (GU ? (tid & 127) : tid), N - 1)];
         }
 
         /* ---- K loop ---- */
@@ -309,7 +316,7 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
                     for (int ri = 0; ri < NRI; ri++)
 #pragma unroll
                         for (int cj = 0; cj < 2; cj++)
-                            acc[ri][cj] = mfma32_i8(A[ri], bq[d][cj][ks], acc[ri][cj]);
+                            acc[ri][cj] = mfma32_i8(bq[d][cj][ks], A[ri], acc[ri][cj]);
                 }
             };
             int s0 = 0;
@@ -333,6 +340,7 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
             sh.rid[buf ^ 1][tid] = nrid;
             sh.arow[buf ^ 1][tid] = narow;
         }
+        sh.cs[buf][tid] = cs_r;
         __syncthreads();
         /* the next tile's head stages go out before this tile's stores */
         if (has_next) {
@@ -341,52 +349,52 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         }
 
         /* ---- epilogue ----
-         * accumulator register 4 g + i of lane l is row
-         * 32 ri + 8 g + 4 (l / 32) + i, column l % 32 of tile cj.
-         * Stores are unconditional (exactly 64 NT per wave): padded rows and
-         * columns past N go to the spare row of `out`. */
+         * accumulator register 4 g + i of lane l is row 32 ri + l % 32,
+         * column 8 g + 4 (l / 32) + i of the wave's 32-column tile cj
+         * (gate/up: slab columns 32 w .., tile 0 gate, tile 1 up; plain:
+         * slab columns 64 w + 32 cj ..).  One 16-byte store per (ri, tile,
+         * g); stores are unconditional (exactly 16 NT per wave): padded rows
+         * and columns past N go to the spare row of `out`. */
         float *out = g.out;
         const size_t spare = (size_t)g.spare_row * N;
-        auto epilogue = [&](auto dbg_on) {
+        {
             int32_t *dbg = g.dbg_acc;
 #pragma unroll
             for (int ri = 0; ri < 4; ri++) {
+                const int rid = sh.rid[buf][32 * ri + l32];
+                const float sa = sh.sa[buf][32 * ri + l32];
 #pragma unroll
-                for (int gq = 0; gq < 4; gq++) {
-                    const int rb = 32 * ri + 8 * gq + 4 * hi;
-                    const i32x4 rid4 = *(const i32x4 *)(&sh.rid[buf][rb]);
-                    const f32x4 sa4 = *(const f32x4 *)(&sh.sa[buf][rb]);
+                for (int q = 0; q < NT; q++) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int rid = rid4[i];
-                        const float sa = sa4[i];
+                    for (int gq = 0; gq < 4; gq++) {
+                        const int cl = (GU ? 32 * wave : 64 * wave + 32 * q) + 8 * gq + 4 * hi;
+                        const int col = slab_c0 + cl;
+                        const bool ok = rid >= 0 && col < N;
+                        const size_t o = ok ? (size_t)rid * N + col : spare + col;
+                        const f32x4 c0 = *(const f32x4 *)(&sh.cs[buf][cl]);
+                        f32x4 v;
+                        if (GU) {
+                            const f32x4 c1 = *(const f32x4 *)(&sh.cs[buf][128 + cl]);
 #pragma unroll
-                        for (int q = 0; q < NT; q++) {
-                            const int col = colv[q];
-                            const bool ok = rid >= 0 && col < N;
-                            const size_t o = ok ? (size_t)rid * N + col : spare + col;
-                            if (GU) {
-                                const int32_t ag = acc[ri][0][4 * gq + i];
-                                const int32_t au = acc[ri][1][4 * gq + i];
-                                out[o] = silu_mul(((float)ag * sa) * c0[q], ((float)au * sa) * c1[q]);
-                                if (decltype(dbg_on)::value && ok) {
-                                    dbg[((size_t)rid * 2) * N + col] = ag;
-                                    dbg[((size_t)rid * 2 + 1) * N + col] = au;
-                                }
-                            } else {
-                                const int32_t ac = acc[ri][q][4 * gq + i];
-                                out[o] = ((float)ac * sa) * c0[q];
-                                if (decltype(dbg_on)::value && ok) dbg[(size_t)rid * N + col] = ac;
+                            for (int i = 0; i < 4; i++)
+                                v[i] = silu_mul(((float)acc[ri][0][4 * gq + i] * sa) * c0[i],
+                                                ((float)acc[ri][1][4 * gq + i] * sa) * c1[i]);
+                            if (DBG && dbg && ok) {
+                                int32_t *d = dbg + ((size_t)rid * 2) * N + col;
+                                *(i32x4 *)d = acc4(acc[ri][0], gq);
+                                *(i32x4 *)(d + N) = acc4(acc[ri][1], gq);
                             }
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; i++) v[i] = ((float)acc[ri][q][4 * gq + i] * sa) * c0[i];
+                            if (DBG && dbg && ok)
+                                *(i32x4 *)(dbg + (size_t)rid * N + col) = acc4(acc[ri][q], gq);
                         }
+                        *(f32x4 *)(out + o) = v;
                     }
                 }
             }
-        };
-        if (g.dbg_acc)
-            epilogue(std::true_type{});
-        else
-            epilogue(std::false_type{});
+        }
         if (!has_next) break;
         t = tn;
         cur = nxt;
@@ -402,7 +410,8 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
  * those tiles in turn, so the blocks of one XCD work on neighbouring tiles at
  * the same time: row groups of the same expert and slab, whose weights then
  * come from HBM once and from that XCD's L2 for the others. */
-extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args a) {
+template <bool DBG>
+__device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_A_BYTES];
     __shared__ bt_shared sh;
     const mm_i8_tiled_args &g0 = a.seg[0];
@@ -443,7 +452,19 @@ extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args
     xl.len = xl.len0 + n0 + n1 * (xcd + 1) / MM_I8S_XCD - xl.lo1;
     if (j >= xl.len) return;
     if (g0.gu)
-        bt_run<true>(a, lds, sh, xl, j, nbx);
+        bt_run<true, DBG>(a, lds, sh, xl, j, nbx);
     else
-        bt_run<false>(a, lds, sh, xl, j, nbx);
+        bt_run<false, DBG>(a, lds, sh, xl, j, nbx);
+}
+
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args a) {
+    bt_kernel<false>(a);
+}
+
+/* As mm_i8_gemm_bt, also writing the raw accumulators of each segment whose
+ * dbg_acc is set (the shared segment's is not); debug entry point only: a
+ * kernel of its own keeps these stores and their registers out of the
+ * product kernel. */
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt_dbg(mm_i8_bt_args a) {
+    bt_kernel<true>(a);
 }
