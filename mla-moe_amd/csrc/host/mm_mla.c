@@ -114,17 +114,20 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const size_t ml_b = (size_t)B * HG * nchunks * 32 * 4;
     const size_t po_b = (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
     const size_t cl_b = clat ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
+    const size_t qhl_b = (size_t)B * NH * 2 * MM_MLA_KVL * 2;   /* qabs as bf16 hi + lo */
     char *ws;
     const size_t a1 = 0, a2 = (qa_b + 255) & ~(size_t)255;
     const size_t a3 = (ml_b + 255) & ~(size_t)255, a4 = (po_b + 255) & ~(size_t)255;
-    if ((st = mm_workspace(c, a1 + a2 + a3 + a4 + cl_b, (void **)&ws))) return st;
+    const size_t a5 = (cl_b + 255) & ~(size_t)255;
+    if ((st = mm_workspace(c, a1 + a2 + a3 + a4 + a5 + qhl_b, (void **)&ws))) return st;
     if (!qabs) qabs = (float *)(ws + a1);
     float *part_ml = (float *)(ws + a1 + a2), *part_o = (float *)(ws + a1 + a2 + a3);
     if (!clat) clat = (float *)(ws + a1 + a2 + a3 + a4);
+    uint16_t *qhl = (uint16_t *)(ws + a1 + a2 + a3 + a4 + a5);
 
     const int QKN = g->qk_nope_head_dim;
     const size_t nkvb = (size_t)NH * (QKN + g->v_head_dim) * MM_MLA_KVL;
-    mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, B, NH, QKN};
+    mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, qhl, B, NH, QKN};
     if (rope) {   /* the front's RoPE / cache append in the same launch */
         mm_mla_rope_qprep_args rq;
         rq.r = *rope;
@@ -135,7 +138,7 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
                                256, 0, &qa))) {
         return st;
     }
-    mm_mla_attn_args aa = {qabs, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
+    mm_mla_attn_args aa = {qhl, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
                            part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots,
                            direct ? clat : NULL};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,

@@ -282,6 +282,7 @@ typedef struct {
     const float *q;           /* [B, NH, QKN + QKR] */
     const uint16_t *wukT;     /* [NH, KVL, QKN] bf16: W_UK per head, transposed */
     float *qabs;              /* [B, NH, KVL] */
+    uint16_t *qhl;            /* [B, NH, 2, KVL] bf16: qabs split into hi (row 0) + lo (row 1) */
     int B, NH, QKN;
 } mm_mla_qprep_args;
 
@@ -294,7 +295,7 @@ typedef struct {
 
 /* Flash-decoding partials: block (chunk, b, head group). */
 typedef struct {
-    const float *qabs;        /* [B, NH, KVL] */
+    const uint16_t *qhl;      /* [B, NH, 2, KVL] bf16: qabs as hi + lo halves (qprep) */
     const float *q;           /* [B, NH, QKN + QKR] (the q_pe part) */
     const uint16_t *cache;    /* [sequences, seq_stride, KVD] bf16 */
     const int32_t *kv_lens;   /* [B] or 0 */

@@ -96,8 +96,9 @@ __device__ __forceinline__ void hl_gemm_32x16(const float *X, size_t xs, int mro
 
 /* Absorbed queries, qabs[b, h, r] = sum_d q_nope[b, h, d] W_UK_h[d, r], as a
  * per-head GEMM with W_UK_h kept transposed ([r][d], prepared at load
- * time).  grid (KVL / 64 column slabs, NH, ceil(B / 32)), 4 waves of 16
- * columns. */
+ * time), also written split into bf16 hi + lo (the attention's Q operands,
+ * split once here rather than by each of its waves).  grid (KVL / 64
+ * column slabs, NH, ceil(B / 32)), 4 waves of 16 columns. */
 __device__ __forceinline__ void qprep_block(const mm_mla_qprep_args &a, int slab, int h, int b0) {
     const int QKR = MM_MLA_QKR, QKN = a.QKN;
     const int lane = threadIdx.x & (MM_WAVE - 1);
@@ -112,7 +113,14 @@ __device__ __forceinline__ void qprep_block(const mm_mla_qprep_args &a, int slab
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int bb = 16 * t + 4 * (lane >> 4) + i;
-            if (bb < mrows) a.qabs[((size_t)(b0 + bb) * a.NH + h) * KVL + e] = acc[t][i];
+            if (bb < mrows) {
+                const size_t row = (size_t)(b0 + bb) * a.NH + h;
+                uint16_t hi, lo;
+                split_bf16(acc[t][i], &hi, &lo);
+                a.qabs[row * KVL + e] = acc[t][i];
+                a.qhl[row * 2 * KVL + e] = hi;
+                a.qhl[(row * 2 + 1) * KVL + e] = lo;
+            }
         }
 }
 
@@ -202,6 +210,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
      * of 16 B) at p * CROW_B; the k_pe parts (128 B per row) of rows 0..7 and
      * 8..15 as two 1 KB pieces after the c_kv rows.  Rows past L load row
      * L - 1 (masked in the softmax). */
+#define ISSUE_LOADS 18            /* direct loads per issue(): 16 c_kv rows + 2 k_pe pieces */
     auto issue = [&](int st, int k0) {
         uint8_t *t = wt0 + st * TILE_B;
 #pragma unroll
@@ -216,20 +225,33 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
                       t + 16 * CROW_B + p * 1024);
         }
     };
+    /* both stages from the start: the first two sub-tiles' loads are in
+     * flight while Q is prepared, and each later sub-tile is issued one
+     * sub-tile of compute before its use */
     if (kbeg < kend) issue(0, kbeg);
+    if (kbeg + 16 < kend) issue(1, kbeg + 16);
 
     /* Q operands in registers: lane (head kl, g) holds [qabs | q_pe] of its
-     * head, latent 32 c + 8 g .. +7, split into bf16 hi + lo; head slots
-     * past NH are zero */
+     * head, latent 32 c + 8 g .. +7, as bf16 hi + lo; head slots past NH are
+     * zero.  qabs comes split by qprep (splitting all 16 heads' 576 values
+     * in every wave cost ~3-4 us of VALU per block); the 64 q_pe values
+     * are split here. */
     bf16x8 qh[KC], ql[KC];
     {
         const int qhd = hg * 16 + kl;
         const bool real = qhd < a.NH;
-        const float *qa = a.qabs + ((size_t)b * a.NH + (real ? qhd : 0)) * KVL;
+        const uint16_t *qa = a.qhl + ((size_t)b * a.NH + (real ? qhd : 0)) * 2 * KVL + 8 * g;
         const float *qp = a.q + ((size_t)b * a.NH + (real ? qhd : 0)) * (a.QKN + MM_MLA_QKR) + a.QKN;
+        const bf16x8 z8 = __builtin_bit_cast(bf16x8, (u16x8){});
 #pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const float *src = c < KVL / 32 ? qa + 32 * c + 8 * g : qp + 32 * (c - KVL / 32) + 8 * g;
+        for (int c = 0; c < KVL / 32; c++) {
+            const bf16x8 h8 = *(const bf16x8 *)(qa + 32 * c), l8 = *(const bf16x8 *)(qa + KVL + 32 * c);
+            qh[c] = real ? h8 : z8;
+            ql[c] = real ? l8 : z8;
+        }
+#pragma unroll
+        for (int c = KVL / 32; c < KC; c++) {
+            const float *src = qp + 32 * (c - KVL / 32) + 8 * g;
             const f32x4 x0 = *(const f32x4 *)src, x1 = *(const f32x4 *)(src + 4);
             u16x8 hi, lo;
 #pragma unroll
@@ -258,7 +280,10 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
      * row kl, latent 32 c + 8 g .. +7; LDS reads run one batch of 6 ahead of
      * the MFMAs.  Returns the scaled scores, -inf past kend. */
     auto score = [&](uint32_t t, int k0, float *sv) {
-        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+        /* the hi and lo products in two independent MFMA chains (one chain
+         * of 36 dependent MFMAs waits out each one's latency), added at the
+         * end */
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
         i32x4 af[2][6];
 #pragma unroll
         for (int c = 0; c < 6; c++) af[0][c] = read_a(t, c);
@@ -274,9 +299,10 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             for (int c = 0; c < 6; c++) {
                 const bf16x8 ab = __builtin_bit_cast(bf16x8, af[bt & 1][c]);
                 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[6 * bt + c], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[6 * bt + c], s, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[6 * bt + c], s2, 0, 0, 0);
             }
         }
+        s += s2;
         const int head = hg * 16 + kl;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -330,9 +356,12 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
         float sv[4];
         bool moved = false;
         for (;;) {
-            VMCNT_WAIT(0);                      /* this sub-tile's rows are in LDS */
-            __builtin_amdgcn_sched_barrier(0);
-            if (k0 + 16 < kend) issue(st ^ 1, k0 + 16);   /* the other stage's reads are done */
+            /* this sub-tile's rows are in LDS: the loads of the next one
+             * (ISSUE_LOADS, issued later) may stay outstanding, as may
+             * nothing else (the score stores of the previous sub-tile were
+             * issued before them) */
+            if (k0 + 16 < kend) VMCNT_WAIT(ISSUE_LOADS);
+            else VMCNT_WAIT(0);
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t t = lds_addr(wt0 + st * TILE_B);
             score(t, k0, sv);
@@ -342,6 +371,10 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
                 break;
             }
             accumulate(t, sv);
+            __builtin_amdgcn_sched_barrier(0);
+            /* this stage's LDS reads are complete (accumulate waits for them
+             * before its last MFMAs): refill it with the sub-tile after next */
+            if (k0 + 32 < kend) issue(st, k0 + 32);
             __builtin_amdgcn_sched_barrier(0);
             k0 += 16;
             st ^= 1;
@@ -354,18 +387,25 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
         mx = fmaxf(mx, __shfl_xor(mx, 16, MM_WAVE));
         mx = fmaxf(mx, __shfl_xor(mx, 32, MM_WAVE));
         const float mnew = fmaxf(m, mx);
-        const float cr = m == -INFINITY ? 0.0f : __expf(m - mnew);
-        l *= cr;
-        m = mnew;
-        /* rescale O rows: lane (r, g) holds heads 4g + i, whose factor sits
-         * in lane 4g + i */
+        /* m is uniform over the wave's lanes of a head, and -inf for every
+         * head until the wave's first sub-tile: O and l are still zero then
+         * and need no rescale */
+        if (__builtin_amdgcn_ballot_w64(m != -INFINITY)) {
+            const float cr = m == -INFINITY ? 0.0f : __expf(m - mnew);
+            l *= cr;
+            /* rescale O rows: lane (r, g) holds heads 4g + i, whose factor
+             * sits in lane 4g + i */
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float ci = __shfl(cr, 4 * g + i, MM_WAVE);
+            for (int i = 0; i < 4; i++) {
+                const float ci = __shfl(cr, 4 * g + i, MM_WAVE);
 #pragma unroll
-            for (int nb = 0; nb < KVL / 16; nb++) O[nb][i] *= ci;
+                for (int nb = 0; nb < KVL / 16; nb++) O[nb][i] *= ci;
+            }
         }
+        m = mnew;
         accumulate(lds_addr(wt0 + st * TILE_B), sv);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k0 + 32 < kend) issue(st, k0 + 32);
         __builtin_amdgcn_sched_barrier(0);
         k0 += 16;
         st ^= 1;
