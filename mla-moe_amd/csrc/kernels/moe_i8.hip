@@ -164,6 +164,9 @@ __device__ __forceinline__ void route_token(const mm_router_args &a, int tok, co
     for (int j = 0; j < EJ; j++) {
         const int e = lane + MM_WAVE * j;
         sel[j] = p[j] + (a.bias && e < E ? a.bias[e] : 0.0f);
+        /* NaN: after every number (ties by index), so the ranks stay a
+         * permutation and every slot below K gets exactly one expert */
+        if (sel[j] != sel[j]) sel[j] = -INFINITY;
         rank[j] = 0;
         if (e < E) ss[e] = sel[j];
     }
@@ -379,10 +382,12 @@ __device__ __forceinline__ float tile_row_f(float a_side, int i) {
 
 /* Row list of routed expert e, built by the whole block from the routing
  * (topk [R] expert ids): the route ids with topk[rid] == e in ascending
- * order, into LDS `list` (at most T entries; a token picks an expert at most
- * once).  Returns the count (block-uniform).  No atomics: each wave ballots
- * its hits and places them after the hits of the waves before it. */
-__device__ __forceinline__ int expert_rows(const int32_t *topk, int R, int e, int *list) {
+ * order, into LDS `list` (at most cap = T entries: a token picks an expert
+ * at most once; hits past cap are dropped, so a malformed routing cannot
+ * write past the list).  Returns the count (block-uniform).  No atomics:
+ * each wave ballots its hits and places them after the hits of the waves
+ * before it. */
+__device__ __forceinline__ int expert_rows(const int32_t *topk, int R, int e, int *list, int cap) {
     __shared__ int wsum[MM_I8S_W];
     constexpr int NTHR = MM_I8S_W * MM_WAVE;
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
@@ -401,11 +406,12 @@ __device__ __forceinline__ int expert_rows(const int32_t *topk, int R, int e, in
             off += w < wave ? c : 0;
             all += c;
         }
-        if (hit) list[off + __popcll(bal & ((1ull << lane) - 1ull))] = i;
+        const int pos = off + __popcll(bal & ((1ull << lane) - 1ull));
+        if (hit && pos < cap) list[pos] = i;
         __syncthreads();
         total += all;
     }
-    return total;
+    return min(total, cap);
 }
 
 /* Shared-expert block b of a decode GEMM: column group and row tile, with
@@ -490,7 +496,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         if (e < 0) return;
         g = v % G;
         int *list = (int *)(lds_a + 16 * a.H);
-        M = expert_rows(a.topk, a.T * a.K, e, list);
+        M = expert_rows(a.topk, a.T * a.K, e, list, a.T);
         if (M == 0) return;
         bbase = a.w.gu + (size_t)e * nbl * 2 * KB * 1024;
         sg = a.w.s_g + (size_t)e * a.I;
@@ -612,7 +618,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_down(mm_i
         const int v = b - n_sh, e = v / G;
         g = v % G;
         int *list = (int *)(lds_a + 16 * (a.S > a.I ? a.S : a.I));
-        M = expert_rows(a.topk, a.T * a.K, e, list);
+        M = expert_rows(a.topk, a.T * a.K, e, list, a.T);
         if (M == 0) return;
         abase = a.a;
         sa = a.sa;

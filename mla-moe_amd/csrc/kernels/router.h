@@ -268,6 +268,10 @@ __device__ __forceinline__ void router_select_wave(const mm_router_args &a, int 
         for (int j = 0; j < EJ; j++) {
             const int e = lane + MM_WAVE * j;
             sel[j] = p[j] + (a.bias && e < E ? a.bias[e] : 0.0f);
+            /* a NaN score is never picked by the CPU's strict '>' scan; as
+             * -inf it ranks after every number (ties by index), so the
+             * ranks stay a permutation and no expert is picked twice */
+            if (sel[j] != sel[j]) sel[j] = -INFINITY;
             rank[j] = 0;
         }
 #pragma unroll
@@ -544,7 +548,8 @@ __device__ __forceinline__ void router_select_one(const mm_router_args &a, int t
     if (a.probs && ok) a.probs[(size_t)tok * E + lane] = p;
     /* rank of this expert in the order (score + bias descending, index
      * ascending): the pass of the CPU's strict '>' scan that picks it */
-    const float sel = p + (a.bias && ok ? a.bias[lane] : 0.0f);
+    float sel = p + (a.bias && ok ? a.bias[lane] : 0.0f);
+    if (sel != sel) sel = -INFINITY;   /* NaN: after every number, ranks stay a permutation */
     ws[lane] = sel;
     int rank = 0;
     for (int l0 = 0; l0 < E; l0 += 4) {
