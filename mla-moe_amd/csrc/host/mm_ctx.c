@@ -36,6 +36,7 @@ static const struct {
 } kinfo[K_COUNT] = {
     [K_ROUTER] = {"mm_router", MOD_MOE_BF16},
     [K_ROUTER_PC] = {"mm_router_pc", MOD_MOE_BF16},
+    [K_ROUTER_PC_SPLIT] = {"mm_router_pc_split", MOD_MOE_BF16},
     [K_MOE_BF16_RSH] = {"mm_moe_bf16_router_sh", MOD_MOE_BF16},
     [K_MOE_BF16_S1] = {"mm_moe_bf16_stage1", MOD_MOE_BF16},
     [K_MOE_BF16_S2] = {"mm_moe_bf16_stage2", MOD_MOE_BF16},

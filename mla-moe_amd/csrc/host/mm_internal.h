@@ -13,6 +13,7 @@
 typedef enum {
     K_ROUTER,
     K_ROUTER_PC,
+    K_ROUTER_PC_SPLIT,
     K_MOE_BF16_RSH,
     K_MOE_BF16_S1,
     K_MOE_BF16_S2,

@@ -457,11 +457,14 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     return MM_OK;
 }
 
-/* Router logits only (a->logits_out set): one token per block for small
- * batches, where the chain-per-lane form leaves most CUs idle. */
+/* Router logits only (a->logits_out set): for small batches, where the
+ * chain-per-lane form leaves most CUs idle, one token per block row and
+ * MM_ROUTER_PC_EB experts per block (the token's products spread over
+ * several CUs' LDS). */
 static int launch_router_logits(mm_ctx *c, mm_router_args *a) {
     if (a->E <= 64 && a->H % 8 == 0 && a->T <= MM_ROUTER_PC_TMAX)
-        return mm_launch(c, K_ROUTER_PC, (unsigned)a->T, 1, 1, 256, 0, a);
+        return mm_launch(c, K_ROUTER_PC_SPLIT, (unsigned)a->T,
+                         (unsigned)((a->E + MM_ROUTER_PC_EB - 1) / MM_ROUTER_PC_EB), 1, 256, 0, a);
     return mm_launch(c, K_ROUTER, (a->T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK, 1,
                      1, 256, 0, a);
 }

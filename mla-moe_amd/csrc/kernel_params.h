@@ -17,6 +17,7 @@
 /* Logits-only router with one token per block (mm_router_pc): used for
  * E <= 64, H % 8 == 0 and T up to this many tokens. */
 #define MM_ROUTER_PC_TMAX 256
+#define MM_ROUTER_PC_EB 16        /* experts per block of the logits-only product/chain router */
 
 typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */

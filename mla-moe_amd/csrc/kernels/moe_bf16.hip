@@ -142,6 +142,16 @@ extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc(mm_router
     router_block_pc<RPC_HC>(a, lds);
 }
 
+/* Router logits only, RPC_EB_SPLIT experts per block: grid (T, ceil(E /
+ * RPC_EB_SPLIT)); each logit is the same sequential sum as in mm_router_pc. */
+extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc_split(mm_router_args a) {
+    __shared__ __attribute__((aligned(16))) float lds[rpc_shape<RPC_HC, RPC_EB_SPLIT>::LDS_FLOATS];
+    const float acc = router_logits_pc<RPC_HC, RPC_EB_SPLIT>(a, lds);
+    const int e = (int)blockIdx.y * RPC_EB_SPLIT + (int)threadIdx.x;
+    if (threadIdx.x < RPC_EB_SPLIT && e < a.E)
+        a.logits_out[(size_t)blockIdx.x * a.E + e] = a.logit_bias ? acc + a.logit_bias[e] : acc;
+}
+
 /* Small T: the router (one token per block, blocks [0, T)) and the shared
  * expert's gate/up (the other blocks, stage 2's shared parts: row block
  * x, then (token, part) v = t nsh_parts + j) in one launch -- the shared

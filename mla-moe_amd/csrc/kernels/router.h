@@ -398,30 +398,41 @@ __device__ __forceinline__ void router_block(const mm_router_args &a, int block,
  * whole rows: load j of lane l is expert (64 / LPR) j + l / LPR, hidden
  * offsets 8 (l % LPR) .. + 7, LPR = HC / 8 lanes per row.  Indices past H
  * contribute +0 (exact, as in router_logits_block).  Returns the logit of
- * expert `lane` in wave 0 (0 elsewhere). */
+ * expert `lane` in wave 0 (0 elsewhere).
+ *
+ * EB < 64: the block serves experts EB blockIdx.y .. + EB - 1 of its token
+ * only (lane e of the chain wave: expert EB blockIdx.y + e, lanes >= EB
+ * idle), so a token's products -- written to LDS and read back, 2 x 4 B
+ * per product -- spread over 64 / EB CUs: with all 64 experts in one block
+ * that LDS traffic (1 MB per token), not the add chains, set the pace. */
 #define RPC_NPROD 3
+#ifndef RPC_PF
 #define RPC_PF 2            /* phases of W loads in flight ahead of the one computed */
-template <int HC>
+#endif
+template <int HC, int EB = MM_WAVE>
 struct rpc_shape {
     static constexpr int RS = HC + 4;                   /* padded product row (floats) */
-    static constexpr int BUF = MM_WAVE * RS;            /* floats per chunk buffer */
+    static constexpr int BUF = EB * RS;                 /* floats per chunk buffer */
     static constexpr int LDS_FLOATS = 2 * RPC_NPROD * (BUF + HC);
     static constexpr int LPR = HC / 8;                  /* lanes per W row */
-    static constexpr int NLD = LPR;                     /* W loads per lane per chunk */
+    static constexpr int NLD = EB / (MM_WAVE / LPR);    /* W loads per lane per chunk */
 };
 #define RPC_HC 64                                       /* chunk of the standalone kernel */
 #define RPC_LDS_FLOATS (rpc_shape<RPC_HC>::LDS_FLOATS)
+#define RPC_EB_SPLIT MM_ROUTER_PC_EB                    /* experts per block, logits only */
 
-template <int HC>
+template <int HC, int EB = MM_WAVE>
 __device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float *lds) {
-    using S = rpc_shape<HC>;
+    using S = rpc_shape<HC, EB>;
     static_assert(HC % 8 == 0 && MM_WAVE % S::LPR == 0, "chunk rows of whole 16-byte pieces");
+    static_assert(EB <= MM_WAVE && EB % (MM_WAVE / S::LPR) == 0, "whole loads of expert rows");
+    const int e0 = EB < MM_WAVE ? (int)blockIdx.y * EB : 0;
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int tok = blockIdx.x, H = a.H, E = a.E;
     const int nch = (H + HC - 1) / HC;
     const int nph = (nch + RPC_NPROD - 1) / RPC_NPROD;
-    float *prod = lds;                                   /* [6][64][RS] */
+    float *prod = lds;                                   /* [6][EB][RS] */
     float *xs = lds + 2 * RPC_NPROD * S::BUF;            /* [6][HC] */
     const float *xrow = a.x + (size_t)tok * H;
     float acc = 0.0f;
@@ -438,7 +449,7 @@ __device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float
             const int i = c * HC + o;
 #pragma unroll
             for (int j = 0; j < S::NLD; j++) {
-                const int e = min(RPL * j + lane / S::LPR, E - 1);
+                const int e = min(e0 + RPL * j + lane / S::LPR, E - 1);
                 /* in range: H is a multiple of 8; past H: zeros */
                 wr[slot][j] = (c < nch && i < H) ? *(const u32x4 *)(a.wg + (size_t)e * H + i)
                                                  : (u32x4){0u, 0u, 0u, 0u};
@@ -494,7 +505,7 @@ __device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float
                 for (int j = 0; j < RPC_NPROD; j++) {
                     if (RPC_NPROD * kp + j >= nch) break;
                     const float *pb =
-                        prod + ((kp & 1) * RPC_NPROD + j) * S::BUF + (size_t)lane * S::RS;
+                        prod + ((kp & 1) * RPC_NPROD + j) * S::BUF + (size_t)min(lane, EB - 1) * S::RS;
                     f32x4 v[HC / 4];
 #pragma unroll
                     for (int q = 0; q < HC / 4; q++) v[q] = *(const f32x4 *)(pb + 4 * q);
