@@ -492,9 +492,9 @@ def bench_lm_head(ctx, steps, warmup, V=102400, H=2048):
             mlamoe._check(lib.mm_lm_head_dev(h, B, x.ptr, norm.ptr, 1e-6, w.ptr, V, H, lg.ptr,
                                              tok.ptr))
         ms, _ = timed(ctx, step, steps * 5, warmup)
-        names = ["mm_rmsnorm", "mm_lm_gemv_1", "mm_lm_gemv_4", "mm_cvt_bf16", "mm_gemm_bf16", "mm_gemm_skinny",
-                 "mm_gemm_skinny_wide", "mm_argmax_part",
-                 "mm_argmax_final"]
+        names = ["mm_rmsnorm", "mm_rmsnorm_hl", "mm_lm_gemv_1", "mm_lm_gemv_4", "mm_cvt_bf16",
+                 "mm_gemm_bf16", "mm_gemm_skinny", "mm_gemm_skinny_wide", "mm_lm_gemm",
+                 "mm_argmax_part", "mm_argmax_final"]
         prof = profile_kernels(ctx, step, 20, names)
         nbytes = V * H * 2 + B * V * 4 + B * H * 4 + H * 2  # weights, logits out, x, norm
         flops = 2.0 * B * V * H

@@ -61,6 +61,8 @@ static const struct {
     [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
     [K_CVT_BF16] = {"mm_cvt_bf16", MOD_GEMM_BF16},
     [K_RMSNORM] = {"mm_rmsnorm", MOD_LM_HEAD},
+    [K_RMSNORM_HL] = {"mm_rmsnorm_hl", MOD_LM_HEAD},
+    [K_LM_GEMM] = {"mm_lm_gemm", MOD_LM_HEAD},
     [K_LM_GEMV1] = {"mm_lm_gemv_1", MOD_LM_HEAD},
     [K_LM_GEMV2] = {"mm_lm_gemv_2", MOD_LM_HEAD},
     [K_LM_GEMV4] = {"mm_lm_gemv_4", MOD_LM_HEAD},

@@ -38,6 +38,8 @@ typedef enum {
     K_GEMM_BF16,
     K_CVT_BF16,
     K_RMSNORM,
+    K_RMSNORM_HL,
+    K_LM_GEMM,
     K_LM_GEMV1,
     K_LM_GEMV2,
     K_LM_GEMV4,

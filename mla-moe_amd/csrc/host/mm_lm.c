@@ -77,6 +77,18 @@ int mm_lm_head_dev(mm_ctx *c, int B, const float *x, const uint16_t *norm, float
         mm_argmax_args fa = {lg, tokens, pv, pi, vocab, B, (int)nb};
         return mm_launch(c, K_ARGMAX_FINAL, (unsigned)B, 1, 1, 256, 0, &fa);
     }
+    if (B <= 64 && hidden % 64 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)norm % 16 == 0) {
+        /* the norm writes bf16 hi/lo planes (the same bytes as xb's fp32)
+         * for the logits GEMM's direct-to-LDS ring */
+        uint16_t *xhl = (uint16_t *)(ws + o_xb);
+        mm_rmsnorm_hl_args rh = {x, norm, xhl, hidden, eps};
+        if ((st = mm_launch(c, K_RMSNORM_HL, (unsigned)B, 1, 1, 256, 0, &rh))) return st;
+        mm_lm_gemm_args lg_a = {xhl, lm_head, lg, B, vocab, hidden};
+        if ((st = mm_launch(c, K_LM_GEMM, (unsigned)((vocab + MM_LMG_BN - 1) / MM_LMG_BN), 1, 1, 256,
+                            (size_t)MM_LMG_NS * MM_LMG_STAGE, &lg_a)))
+            return st;
+        return argmax_launch(c, B, lg, vocab, tokens, ws + o_am);
+    }
     float *xb = (float *)(ws + o_xb);
     mm_rmsnorm_args ra = {x, norm, xb, hidden, eps};
     if ((st = mm_launch(c, K_RMSNORM, (unsigned)B, 1, 1, 256, 0, &ra))) return st;

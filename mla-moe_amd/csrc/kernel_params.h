@@ -17,7 +17,9 @@
 /* Logits-only router with one token per block (mm_router_pc): used for
  * E <= 64, H % 8 == 0 and T up to this many tokens. */
 #define MM_ROUTER_PC_TMAX 256
+#ifndef MM_ROUTER_PC_EB
 #define MM_ROUTER_PC_EB 16        /* experts per block of the logits-only product/chain router */
+#endif
 
 typedef struct {
     const float *x;          /* [T, H] activations (unused when logits_in != 0) */
@@ -422,6 +424,27 @@ typedef struct {
     int32_t *part_i;         /* [B, waves] its row */
     int B, V, H;
 } mm_lm_gemv_args;
+
+/* RMSNorm rows written as bf16 hi/lo planes (the LM head GEMM's operand). */
+typedef struct {
+    const float *x;          /* [T, n] */
+    const uint16_t *w;       /* [n] bf16 */
+    uint16_t *yhl;           /* [2, T, n]: rne16(y), then rne16(y - hi) */
+    int n;
+    float eps;
+} mm_rmsnorm_hl_args;
+
+/* Logits GEMM for MM_LM_NB < T <= 64 rows: y[T, N] = x . W^T with x given
+ * as bf16 hi/lo planes; MM_LMG_BN columns per block. */
+#define MM_LMG_BN 256
+#define MM_LMG_NS 3                                  /* ring stages (two chunks ahead) */
+#define MM_LMG_STAGE (MM_LMG_BN * 128 + 2 * 64 * 128) /* LDS bytes per stage: W, x hi, x lo */
+typedef struct {
+    const uint16_t *xhl;     /* [2, T, K] */
+    const uint16_t *w;       /* [N, K] bf16 */
+    float *y;                /* [T, N] */
+    int T, N, K;             /* K a multiple of 64 */
+} mm_lm_gemm_args;
 
 #define MM_ARGMAX_SEG 1024       /* row elements per argmax segment (block) */
 #define MM_LM_GEMV_BLOCKS 2048   /* GEMV grid (4 waves each): argmax partials per token */

@@ -16,6 +16,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 __device__ __forceinline__ float bf16_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+/* fp32 -> bf16, round to nearest even (the hi part of the hi/lo splits of
+ * fp32 activations; lo = rne16(x - bf16_f32(hi))) */
+__device__ __forceinline__ uint16_t rne16(float x) {
+    uint32_t u = __float_as_uint(x);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
 
 /* 8 bf16 weights (one 128-bit load) dotted with 8 fp32 activations read as
  * two 128-bit loads (x must be 16-byte aligned). */

@@ -25,12 +25,6 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 #define GB_BK 64
 #define GB_COPY (128 * 128)             /* A of one stage: 128 rows x 128 B */
 
-__device__ __forceinline__ uint16_t rne16(float x) {
-    uint32_t u = __float_as_uint(x);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
 /* x -> bf16 rows of stride kp (zeros past n_in), 8 values per thread:
  * truncation (the reference's cast, include/tensor.h:16-20) or the RNE
  * hi/lo split. */

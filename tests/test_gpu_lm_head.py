@@ -93,7 +93,7 @@ def test_lm_head_shapes(ctx, oracle, B, V, H):
 
 def test_lm_head_dsv2_vocab(ctx, oracle):
     """DeepSeek-V2-Lite's LM head: vocab 102400 x hidden 2048, one decode
-    token (GEMV), five and 64 (the skinny GEMM's wide form)."""
+    token (GEMV), five and 64 (the logits GEMM)."""
     rng = np.random.default_rng(77)
     V, H = 102400, 2048
     lm = synth.normal_bf16(rng, (V, H), 0.02)
@@ -105,6 +105,25 @@ def test_lm_head_dsv2_vocab(ctx, oracle):
         rl, rt = oracle.lm_head_rows(x, norm, 1e-6, lm)
         assert max_abs_rel(logits, rl) < 1e-5
         _check_tokens(tokens, rl, rt)
+
+
+def test_lm_head_gemm_matches_skinny(ctx):
+    """5..64 rows: the logits GEMM (bf16 hi/lo planes written by the norm,
+    both operands through a direct-to-LDS ring) gives the same bits as the
+    skinny GEMM's wide form over the fp32 norm output (the same split, the
+    same MFMA sequence per output, one pass over K: the wide form takes
+    vocabularies past 65536); V = 65600 is not a multiple of the 256-row
+    tile."""
+    rng = np.random.default_rng(90)
+    V, H = 65600, 2048
+    lm = synth.normal_bf16(rng, (V, H), 0.02)
+    norm = synth.bf16_from_f32(1.0 + synth.normal_f32(rng, (H,), 0.1))
+    for B in (5, 64):
+        print(f"lm_head gemm vs skinny B={B} V={V}", flush=True)
+        x = synth.normal_f32(rng, (B, H))
+        logits, _ = ctx.lm_head(x, norm, 1e-6, lm)
+        ref = ctx.matmul(ctx.rmsnorm(x, norm, 1e-6), lm)
+        assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32)), B
 
 
 def test_lm_head_errors(ctx):
