@@ -352,7 +352,8 @@ def bench_attn_layer(ctx_unused, steps, warmup, L=4096, NH=16):
                 mlamoe._check(lib.mm_matmul_bf16_dev(h, x.ptr, co.ptr, wd["o_proj"].ptr, Hd,
                                                      NH * VHD, B, mlamoe.MM_MATMUL_ACCUMULATE))
             ms, _ = timed(ctx, step, steps * 5, warmup)
-            names = ["mm_gemv_1", "mm_gemv_4", "mm_rmsnorm", "mm_cvt_bf16", "mm_gemm_bf16", "mm_gemm_skinny", "mm_skinny_reduce",
+            names = ["mm_gemv_1", "mm_gemv_4", "mm_rmsnorm", "mm_rmsnorm_hl", "mm_cvt_bf16", "mm_gemm_bf16",
+                     "mm_gemm_skinny", "mm_gemm_hl", "mm_skinny_reduce",
                      "mm_mla_rope", "mm_mla_qprep", "mm_mla_attn", "mm_mla_combine", "mm_mla_uv"]
             prof = profile_kernels(ctx, step, 20, names)
             wbytes = 2 * (QD * Hd + KVD * Hd + Hd * NH * VHD + 2 * NH * QKN * KVL + Hd + KVL)

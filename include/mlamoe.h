@@ -245,6 +245,17 @@ MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, i
 MM_API int mm_matmul_bf16_dev(mm_ctx *ctx, float *y, const float *x, const uint16_t *w,
                               int d_out, int n_in, int T, unsigned flags);
 
+/* The same product over T <= 64 rows (the batched decode step's
+ * projections) with x given already split: xhl [2, T, n_in] bf16, plane 0
+ * the round-to-nearest-even bf16 of each x, plane 1 that of x minus it (the
+ * pair mm_matmul_bf16_dev carries fp32 x as).  Same results, bit for bit, as
+ * mm_matmul_bf16_dev on the fp32 rows from 5 rows on; n_in % 64 == 0.  No
+ * counterpart in the reference: it serves callers whose kernels write their
+ * rows in this form (the engine's norms and W_UV product) and the parity
+ * tests of that path.  Device pointers, asynchronous. */
+MM_API int mm_matmul_bf16_hl_dev(mm_ctx *ctx, float *y, const uint16_t *xhl, const uint16_t *w,
+                                 int d_out, int n_in, int T, unsigned flags);
+
 /* ---- LM head: final RMSNorm, logits, greedy sampling ------------------------- */
 
 /* rmsnorm (src/run.c:22-27) of T rows: y[t] = (x[t] * inv) * w with

@@ -76,6 +76,7 @@ static const struct {
     [K_SWIGLU] = {"mm_swiglu", MOD_UTIL},
     [K_GEMM_SKINNY] = {"mm_gemm_skinny", MOD_GEMM_BF16},
     [K_GEMM_SKINNY_WIDE] = {"mm_gemm_skinny_wide", MOD_GEMM_BF16},
+    [K_GEMM_HL] = {"mm_gemm_hl", MOD_GEMM_BF16},
     [K_SKINNY_REDUCE] = {"mm_skinny_reduce", MOD_GEMM_BF16},
     [K_REDUCE_RMSNORM] = {"mm_reduce_rmsnorm", MOD_LM_HEAD},
     [K_ZERO32] = {"mm_zero32", MOD_UTIL},

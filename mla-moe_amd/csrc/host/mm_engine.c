@@ -35,6 +35,8 @@ struct mm_engine {
     float *x, *xn, *q, *ctxo, *g, *u;   /* [max_rows, ...] step activations */
     float *fcomp;              /* [MM_SKINNY_T, KVL + QKR]: kv_a's output of steps of up to
                                   MM_SKINNY_T rows, read by the RoPE / qprep launch */
+    uint16_t *xn_hl, *ctx_hl;  /* xn and ctxo of steps of 5..MM_SKINNY_T rows as bf16 hi/lo
+                                  planes [2, rows, n]: the projections' operands */
     int32_t *d_io;             /* device [IO_ARRAYS][max_rows]: see IO_* */
     int32_t *h_io;             /* pinned host, same layout */
     int32_t *last_pos;         /* [max_batch] host: a step's check of its rows' positions */
@@ -51,7 +53,7 @@ void mm_engine_destroy(mm_engine *e) {
             if (e->cache[l]) hipFree(e->cache[l]);
         free(e->cache);
     }
-    void *dev[] = {e->x, e->xn, e->q, e->ctxo, e->g, e->u, e->d_io, e->fcomp};
+    void *dev[] = {e->x, e->xn, e->q, e->ctxo, e->g, e->u, e->d_io, e->fcomp, e->xn_hl, e->ctx_hl};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (e->h_io) hipHostFree(e->h_io);
@@ -164,7 +166,9 @@ int mm_engine_create(mm_ctx *c, const mm_engine_config *cfg, mm_engine **out) {
         {(void **)&e->ctxo, MR * (size_t)g->n_heads * g->v_head_dim * 4},
         {(void **)&e->g, MR * DI * 4}, {(void **)&e->u, MR * DI * 4},
         {(void **)&e->d_io, IO_ARRAYS * MR * 4},
-        {(void **)&e->fcomp, (size_t)MM_SKINNY_T * KVD * 4}};
+        {(void **)&e->fcomp, (size_t)MM_SKINNY_T * KVD * 4},
+        {(void **)&e->xn_hl, (size_t)MM_SKINNY_T * H * 4},
+        {(void **)&e->ctx_hl, (size_t)MM_SKINNY_T * g->n_heads * g->v_head_dim * 4}};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         if (hipMalloc(bufs[i].p, bufs[i].n) != hipSuccess) {
             mm_engine_destroy(e);
@@ -225,6 +229,14 @@ static int gemv_rows(const mm_engine *e, int B) {
     return B <= MM_GEMV_NB && e->cfg.hidden_size <= MM_LM_HMAX;
 }
 
+/* Steps whose projections read their x as bf16 hi/lo planes (5 to
+ * MM_SKINNY_T rows, both widths multiples of 64). */
+static int hl_rows(const mm_engine *e, int R) {
+    const mm_mla_config *g = &e->c->mla;
+    return !gemv_rows(e, R) && R <= MM_SKINNY_T && e->cfg.hidden_size % 64 == 0 &&
+           (g->n_heads * g->v_head_dim) % 64 == 0;
+}
+
 /* o_proj with its residual add, x += ctxo . o_proj^T (src/run.c:462-468),
  * then xn = rmsnorm(x, post_norm) (src/run.c:470-472) unless the dense
  * GEMV path applies it itself: one GEMM + one reduce-and-norm pass for
@@ -243,6 +255,9 @@ static int oproj_post_norm(mm_engine *e, const mm_engine_layer *L, int R, int de
     }
     char *ws;
     if ((st = mm_workspace(c, mm_gemm_bf16_add_rmsnorm_ws_bytes(R, NIN, H), (void **)&ws))) return st;
+    if (hl_rows(e, R))   /* ctx as the hi/lo planes the W_UV product wrote */
+        return mm_gemm_bf16_add_rmsnorm_hl(c, e->x, e->ctx_hl, L->o_proj, H, NIN, R, L->post_norm,
+                                           e->cfg.rms_eps, e->xn, ws);
     return mm_gemm_bf16_add_rmsnorm(c, e->x, e->ctxo, L->o_proj, H, NIN, R, L->post_norm,
                                     e->cfg.rms_eps, e->xn, ws);
 }
@@ -322,11 +337,13 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
         mm_mla_rope_args ra;
         const int fuse = R <= MM_SKINNY_T;
         if ((st = mm_mla_front_rows(c, R, e->x, &L->front, d_pos, d_slot, e->q, e->cache[l], e->lcap[l],
-                                    NULL, pre ? e->xn : NULL, fuse ? e->fcomp : NULL,
+                                    NULL, pre ? e->xn : NULL, pre && hl_rows(e, R) ? e->xn_hl : NULL,
+                                    fuse ? e->fcomp : NULL,
                                     fuse ? &ra : NULL)))
             return st;
         if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
-                                     e->ctxo, NULL, NULL, NULL, fuse ? &ra : NULL)))
+                                     e->ctxo, NULL, NULL, NULL, fuse ? &ra : NULL,
+                                     hl_rows(e, R) ? e->ctx_hl : NULL)))
             return st;
         const int dense = l < f->first_k_dense;
         if ((st = oproj_post_norm(e, L, R, dense))) return st;
@@ -340,7 +357,8 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
             int fused = 0;
             if ((st = mm_moe_forward_norm(c, l, R, e->xn, e->x, f->moe_flags | MM_FWD_ACCUMULATE,
                                           next_norm ? e->layers[l + 1].front.input_norm : NULL,
-                                          c->front.rms_eps, e->xn, &fused)))
+                                          c->front.rms_eps, e->xn, hl_rows(e, R) ? e->xn_hl : NULL,
+                                          &fused)))
                 return st;
             xn_ready = fused;
         }

@@ -79,6 +79,29 @@ int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1
     return d1 ? mm_gemm_bf16_ws(c, y1, x, w1, d1, n_in, T, flags, ws) : MM_OK;
 }
 
+size_t mm_gemm_bf16_hl_ws_bytes(int T, int n_in, int d0, int d1) {
+    int ns, kr;
+    skinny_plan(skinny_nb(d0) + (d1 > 0 ? skinny_nb(d1) : 0), n_in, &ns, &kr);
+    return ns > 1 ? al256((size_t)ns * T * ((size_t)d0 + (d1 > 0 ? d1 : 0)) * 4) : 256;
+}
+
+int mm_gemm_bf16_hl(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1,
+                    const uint16_t *w1, int d1, const uint16_t *xhl, int n_in, int T, int acc,
+                    char *ws) {
+    if (!w1) d1 = 0;
+    /* the skinny plan: 64-column blocks, K split until ~one block per CU */
+    const int nb0 = skinny_nb(d0), nb = nb0 + (d1 ? skinny_nb(d1) : 0);
+    int ns, kr, st;
+    skinny_plan(nb, n_in, &ns, &kr);
+    mm_gemm_hl_args k = {xhl, w0, y0, (float *)ws, T, d0, n_in, ns, kr, acc, w1, y1, d1, nb0, 0};
+    if ((st = mm_launch(c, K_GEMM_HL, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
+    if (ns == 1) return MM_OK;
+    mm_skinny_reduce_args r = {(float *)ws, y0, T, d0, ns, acc, d1 ? y1 : NULL, d1};
+    const size_t n = (size_t)T * ((size_t)d0 + d1);
+    const size_t blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+    return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
+}
+
 /* x += a . w^T, then xn = rmsnorm(x, norm_w) -- for T <= MM_SKINNY_T rows
  * the split-K partials are summed by the norm pass itself (one launch fewer;
  * the partial sums and residual adds are the skinny reduce's, the norm's sum
@@ -111,6 +134,18 @@ int mm_gemm_bf16_add_rmsnorm(mm_ctx *c, float *x, const float *a, const uint16_t
     if ((st = mm_gemm_bf16_ws(c, x, a, w, d_out, n_in, T, MM_MATMUL_ACCUMULATE, ws))) return st;
     mm_rmsnorm_args r = {x, norm_w, xn, d_out, eps};
     return mm_launch(c, K_RMSNORM, (unsigned)T, 1, 1, 256, 0, &r);
+}
+
+int mm_gemm_bf16_add_rmsnorm_hl(mm_ctx *c, float *x, const uint16_t *ahl, const uint16_t *w,
+                                int d_out, int n_in, int T, const uint16_t *norm_w, float eps,
+                                float *xn, char *ws) {
+    const int nb = skinny_nb(d_out);
+    int ns, kr, st;
+    skinny_plan(nb, n_in, &ns, &kr);
+    mm_gemm_hl_args k = {ahl, w, x, (float *)ws, T, d_out, n_in, ns, kr, 0, NULL, NULL, 0, nb, 1};
+    if ((st = mm_launch(c, K_GEMM_HL, (unsigned)nb, (unsigned)ns, 1, 256, 0, &k))) return st;
+    mm_reduce_rmsnorm_args r = {(const float *)ws, x, norm_w, xn, T, d_out, ns, eps};
+    return mm_launch(c, K_REDUCE_RMSNORM, (unsigned)T, 1, 1, MM_RRN_THREADS, 0, &r);
 }
 
 int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
@@ -158,6 +193,27 @@ int mm_gemv_launch(mm_ctx *c, const mm_gemv_args *a) {
     mm_gemv_args k = *a;
     const mm_kernel_id id = a->B <= 1 ? K_GEMV1 : a->B <= 2 ? K_GEMV2 : K_GEMV4;
     return mm_launch(c, id, mm_gemv_blocks(a->rows0 + a->rows1), 1, 1, 256, 0, &k);
+}
+
+int mm_matmul_bf16_hl_dev(mm_ctx *c, float *y, const uint16_t *xhl, const uint16_t *w, int d_out,
+                          int n_in, int T, unsigned flags) {
+    if (!c || (T > 0 && (!y || !xhl || !w)))
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_hl_dev: NULL argument");
+    if (T < 0 || T > MM_SKINNY_T || d_out <= 0 || n_in <= 0)
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_hl_dev: need 0 <= T <= %d", MM_SKINNY_T);
+    if (n_in % 64)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_matmul_bf16_hl_dev: n_in must be a multiple of 64");
+    if ((uintptr_t)xhl % 16 || (uintptr_t)w % 16)
+        return mm_fail(MM_ERR_INVALID, "mm_matmul_bf16_hl_dev: xhl and w must be 16-byte aligned");
+    if (flags & MM_MATMUL_X_BF16)
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_matmul_bf16_hl_dev: x is a hi/lo pair");
+    if (T == 0) return MM_OK;
+    int st = mm_set_device(c);
+    if (st) return st;
+    char *ws;
+    if ((st = mm_workspace(c, mm_gemm_bf16_hl_ws_bytes(T, n_in, d_out, 0), (void **)&ws))) return st;
+    return mm_gemm_bf16_hl(c, y, w, d_out, NULL, NULL, 0, xhl, n_in, T,
+                           (flags & MM_MATMUL_ACCUMULATE) != 0, ws);
 }
 
 int mm_matmul_bf16_dev(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out,

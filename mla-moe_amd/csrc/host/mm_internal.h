@@ -53,6 +53,7 @@ typedef enum {
     K_SWIGLU,
     K_GEMM_SKINNY,
     K_GEMM_SKINNY_WIDE,
+    K_GEMM_HL,
     K_SKINNY_REDUCE,
     K_REDUCE_RMSNORM,
     K_ZERO32,
@@ -103,6 +104,7 @@ struct mm_ctx {
      * combine also writes rmsnorm(out, norm_w) into norm_xn */
     const uint16_t *norm_w;
     float *norm_xn;
+    uint16_t *norm_xn_hl;
     float norm_eps;
     float *ffn_io;              /* mm_ffn_compute staging: x [H] | out [H] | idx [K] | w [K] */
 
@@ -138,9 +140,11 @@ typedef struct {
  * fx->cap bytes; allocates nothing. */
 /* mm_moe_forward_dev whose output rows are also normalised into xn_next
  * (rmsnorm with norm_w, eps) in the combine pass when the int8 path runs
- * (returns 1 in *fused then; else the caller normalises). */
+ * (returns 1 in *fused then; else the caller normalises); xn_next_hl (or
+ * NULL) also receives them as bf16 hi/lo planes [2, T, H]. */
 int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out, unsigned flags,
-                        const uint16_t *norm_w, float eps, float *xn_next, int *fused);
+                        const uint16_t *norm_w, float eps, float *xn_next, uint16_t *xn_next_hl,
+                        int *fused);
 int mm_moe_forward_fixed(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
                          const float *logits, int32_t *topk_idx, float *topk_w, float *probs,
                          unsigned flags, const mm_fixed_ws *fx);
@@ -172,12 +176,24 @@ size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags);
 /* Two matrices over the same x (y0 = x . W0^T, y1 = x . W1^T; w1 may be
  * NULL): one skinny-M launch when that path applies. */
 size_t mm_gemm_bf16_ws2_bytes(int T, int n_in, int d0, int d1, unsigned flags);
+/* The skinny-M GEMM (T <= MM_SKINNY_T, n_in % 64 == 0) over x given as bf16
+ * hi/lo planes [2, T, n_in]; y0 (and y1 over w1 when d1 > 0) as
+ * mm_gemm_bf16_ws2 computes them from the fp32 rows the planes split. */
+size_t mm_gemm_bf16_hl_ws_bytes(int T, int n_in, int d0, int d1);
+int mm_gemm_bf16_hl(mm_ctx *ctx, float *y0, const uint16_t *w0, int d0, float *y1,
+                    const uint16_t *w1, int d1, const uint16_t *xhl, int n_in, int T, int acc,
+                    char *ws);
 /* x += a . w^T (bf16 w [d_out, n_in]) then xn = rmsnorm(x, norm_w) over rows
  * of d_out; ws of mm_gemm_bf16_add_rmsnorm_ws_bytes bytes. */
 size_t mm_gemm_bf16_add_rmsnorm_ws_bytes(int T, int n_in, int d_out);
 int mm_gemm_bf16_add_rmsnorm(mm_ctx *c, float *x, const float *a, const uint16_t *w, int d_out,
                              int n_in, int T, const uint16_t *norm_w, float eps, float *xn,
                              char *ws);
+/* The same with a given as bf16 hi/lo planes [2, T, n_in]: T <= MM_SKINNY_T,
+ * n_in % 64 == 0, d_out <= MM_RRN_THREADS * MM_RRN_PT (ws as above). */
+int mm_gemm_bf16_add_rmsnorm_hl(mm_ctx *c, float *x, const uint16_t *ahl, const uint16_t *w,
+                                int d_out, int n_in, int T, const uint16_t *norm_w, float eps,
+                                float *xn, char *ws);
 int mm_gemm_bf16_ws2(mm_ctx *ctx, float *y0, const uint16_t *w0, int d0, float *y1,
                      const uint16_t *w1, int d1, const float *x, int n_in, int T, unsigned flags,
                      char *ws);
@@ -193,7 +209,8 @@ int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
  * sequence slots[b] (slots NULL: sequence b): rows of one sequence may share
  * a call (prefill chunks), causality coming from each row's position /
  * kv_lens[b].  xn_pre: rmsnorm(x, input_norm) already computed by the
- * caller (used above MM_GEMV_NB rows), or NULL. */
+ * caller (used above MM_GEMV_NB rows), or NULL; xn_pre_hl (or NULL) the
+ * same rows as bf16 hi/lo planes, which the projections then read. */
 /* defer (or NULL; B <= MM_SKINNY_T): the RoPE / cache-append launch is not
  * made; its arguments go to *defer for mm_mla_decode_rows to run with the
  * absorbed queries in one launch, and kv_a's output goes to comp_buf
@@ -201,13 +218,14 @@ int mm_gemv_launch(mm_ctx *ctx, const mm_gemv_args *a);
  * calls reuse before that launch runs. */
 int mm_mla_front_rows(mm_ctx *ctx, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows, const float *xn_pre, float *comp_buf,
-                      mm_mla_rope_args *defer);
-/* rope (or NULL): the deferred RoPE of mm_mla_front_rows, run with qprep. */
+                      int seq_stride, float *kv_rows, const float *xn_pre,
+                      const uint16_t *xn_pre_hl, float *comp_buf, mm_mla_rope_args *defer);
+/* rope (or NULL): the deferred RoPE of mm_mla_front_rows, run with qprep;
+ * ctx_hl (or NULL): ctx_out also as bf16 hi/lo planes [2, B, NH * VHD]. */
 int mm_mla_decode_rows(mm_ctx *ctx, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope);
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

@@ -69,13 +69,13 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                                int kv_len, float *ctx_out, float *qabs, float *probs,
                                float *clat) {
     return mm_mla_decode_rows(c, layer, B, q, cache, seq_stride, NULL, kv_lens, kv_len, ctx_out,
-                              qabs, probs, clat, NULL);
+                              qabs, probs, clat, NULL, NULL);
 }
 
 int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope) {
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
     if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
         return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
@@ -148,7 +148,8 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
                         &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
-                              probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks};
+                              probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks,
+                              ctx_hl};
     /* merge: split the latent columns over 4 blocks per (head, sequence)
      * when the grid would otherwise have fewer than 128 blocks */
     const unsigned zc = (size_t)NH * B < 128 ? MM_MLA_KVL / 128 : 1;
@@ -217,13 +218,14 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 int mm_mla_front_dev(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                      const int32_t *pos, float *q, uint16_t *cache, int seq_stride,
                      float *kv_rows) {
-    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows, NULL, NULL, NULL);
+    return mm_mla_front_rows(c, B, x, w, pos, NULL, q, cache, seq_stride, kv_rows, NULL, NULL, NULL,
+                             NULL);
 }
 
 int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weights *w,
                       const int32_t *pos, const int32_t *slots, float *q, uint16_t *cache,
-                      int seq_stride, float *kv_rows, const float *xn_pre, float *comp_buf,
-                      mm_mla_rope_args *defer) {
+                      int seq_stride, float *kv_rows, const float *xn_pre,
+                      const uint16_t *xn_pre_hl, float *comp_buf, mm_mla_rope_args *defer) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: NULL context");
     if (!c->front_ready) return mm_fail(MM_ERR_STATE, "mm_mla_front_dev: call mm_mla_front_init first");
     if (B < 0) return mm_fail(MM_ERR_INVALID, "mm_mla_front_dev: B < 0");
@@ -254,6 +256,11 @@ int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weigh
     /* GEMM staging: the larger of the two passes' needs */
     size_t gw = mm_gemm_bf16_ws2_bytes(B, H, ql ? ql : QD, KVD, 0), g2;
     if (ql && (g2 = mm_gemm_bf16_ws_bytes(B, ql, QD, 0)) > gw) gw = g2;
+    /* up to MM_SKINNY_T rows without q-LoRA the projections read x as bf16
+     * hi/lo planes (the caller's, or this norm's), both operands through
+     * one direct-to-LDS ring: the same results as the fp32-row GEMM */
+    const int hl = !gemv && !ql && B <= MM_SKINNY_T && H % 64 == 0;
+    if (hl && (g2 = mm_gemm_bf16_hl_ws_bytes(B, H, QD, KVD)) > gw) gw = g2;
     const size_t o_gm = o_xb + (gemv ? 0 : al256((size_t)B * H * 4));
     char *ws;
     if ((st = mm_workspace(c, o_gm + (gemv ? 0 : gw), (void **)&ws))) return st;
@@ -276,6 +283,17 @@ int mm_mla_front_rows(mm_ctx *c, int B, const float *x, const mm_mla_front_weigh
                               QD, 0, QD, 0, B, ql, 0, 0};
             if ((st = mm_gemv_launch(c, &b))) return st;
         }
+    } else if (hl && (xn_pre_hl || !xn_pre)) {
+        char *gws = ws + o_gm;
+        const uint16_t *xhl = xn_pre_hl;
+        if (!xhl) {   /* the norm writes the planes (the o_xb region holds them) */
+            uint16_t *p = (uint16_t *)(ws + o_xb);
+            mm_rmsnorm_hl_args rh = {x, w->input_norm, p, H, f->rms_eps};
+            if ((st = mm_launch(c, K_RMSNORM_HL, (unsigned)B, 1, 1, 256, 0, &rh))) return st;
+            xhl = p;
+        }
+        if ((st = mm_gemm_bf16_hl(c, q, w->q_proj, QD, comp, w->kv_a_proj, KVD, xhl, H, B, 0, gws)))
+            return st;
     } else {
         const float *xb = (float *)(ws + o_xb);
         char *gws = ws + o_gm;

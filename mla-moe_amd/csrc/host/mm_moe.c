@@ -657,7 +657,8 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     }
 
     mm_i8_combine_args ca = {y, ys, wts, out, tiled ? c->moe_cnt : NULL, T, (int)H, (int)K,
-                             (int)E, acc, S > 0, c->norm_w, c->norm_xn, c->norm_eps};
+                             (int)E, acc, S > 0, c->norm_w, c->norm_xn, c->norm_eps,
+                             c->norm_w ? c->norm_xn_hl : NULL};
     if (c->norm_w)   /* one block per token, the row's norm in the same pass */
         FAIL_ROUTED(mm_launch(c, K_I8_COMBINE_NORM, (unsigned)T, 1, 1, MM_I8_CN_THREADS, 0, &ca));
     else             /* two blocks per token: one round of loads per thread at H = 2048 */
@@ -711,7 +712,8 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
 }
 
 int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out, unsigned flags,
-                        const uint16_t *norm_w, float eps, float *xn_next, int *fused) {
+                        const uint16_t *norm_w, float eps, float *xn_next, uint16_t *xn_next_hl,
+                        int *fused) {
     *fused = 0;
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: NULL context");
     const int can = (flags & MM_FWD_INT8) && c->moe.hidden_size <= MM_I8_CN_MAXH &&
@@ -719,11 +721,13 @@ int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out
     if (can) {
         c->norm_w = norm_w;
         c->norm_xn = xn_next;
+        c->norm_xn_hl = xn_next_hl;
         c->norm_eps = eps;
     }
     const int st = forward(c, layer, T, xn, out, NULL, NULL, NULL, NULL, flags, NULL, NULL);
     c->norm_w = NULL;
     c->norm_xn = NULL;
+    c->norm_xn_hl = NULL;
     if (!st) *fused = can;
     return st;
 }

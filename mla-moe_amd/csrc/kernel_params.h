@@ -189,6 +189,7 @@ typedef struct {
     const uint16_t *norm_w;
     float *xn;
     float eps;
+    uint16_t *xn_hl;         /* or 0: xn also as bf16 hi/lo planes [2, T, H] */
 } mm_i8_combine_args;
 #define MM_I8_CN_THREADS 512      /* mm_i8_combine_norm: one block per token */
 #define MM_I8_CN_MAXH 4096
@@ -327,6 +328,7 @@ typedef struct {
     float *probs;             /* [B, NH, probs_stride]: scores in, probabilities out, or 0 */
     int probs_stride;
     int B, NH, QKN, VHD, HG, nchunks;
+    uint16_t *ctx_hl;         /* or 0: ctx also as bf16 hi/lo planes [2, B, NH * VHD] */
 } mm_mla_combine_args;
 
 /* ---- dense bf16 matmul --------------------------------------------------------- */
@@ -378,6 +380,21 @@ typedef struct {
     int d_out1, nb0;
     int part_out;            /* 1: partials even when nsplit == 1 (a fused reduce reads them) */
 } mm_gemm_skinny_args;
+
+/* As mm_gemm_skinny_args, with x given as bf16 hi/lo planes ([2, T, n_in]:
+ * rne16(x), then rne16(x - hi)) instead of fp32 rows; always split. */
+typedef struct {
+    const uint16_t *xhl;
+    const uint16_t *w;
+    float *y;
+    float *part;
+    int T, d_out, n_in, nsplit, kr;
+    int accumulate;
+    const uint16_t *w1;
+    float *y1;
+    int d_out1, nb0;
+    int part_out;
+} mm_gemm_hl_args;
 
 typedef struct {
     const float *part;       /* [nsplit, T, d_out], then [nsplit, T, d_out1] */

@@ -393,6 +393,132 @@ extern "C" __global__ __launch_bounds__(256) void mm_gemm_skinny_wide(mm_gemm_sk
 }
 
 /* y (+)= sum over splits s = 0 .. nsplit-1 of part[s], in that order. */
+/* ---- skinny-M GEMM over pre-split x ------------------------------------------
+ *
+ * The mm_gemm_skinny computation (same column blocks, K splits, partials and
+ * MFMA sequence per output: per 32-wide K step the hi product, then the lo
+ * product) with x arriving as bf16 hi/lo planes written by its producer.
+ * Both operands then go global -> LDS by direct loads into one ring of
+ * HL_NS stages of a 64-wide K chunk (W: 64 rows x 128 B; x: 64 rows x 128 B
+ * per plane), two chunks ahead: every load of the loop belongs to the ring,
+ * so no wait for an x chunk (an L2 hit) also waits for weight loads issued
+ * before it, as the register staging of fp32 x did (vector memory counts
+ * complete in order; measured 0.75 us per chunk at q_proj + kv_a_proj,
+ * B = 64).  Wave w owns token rows 16 w .. + 15 and the block's 64 columns
+ * (4 x 16-column MFMA tiles).  LDS rows are 128 B of 8 pieces; piece p of
+ * row r sits in slot p ^ swz(r) (16 consecutive rows, one piece: 16
+ * distinct bank groups).  Two blocks per CU. */
+#define HL_NS 3
+#define HL_WB (64 * 128)                 /* W bytes per stage */
+#define HL_STAGE (HL_WB + 2 * 64 * 128)  /* + the x planes: 24 KB */
+#define HL_LPW 6                         /* direct loads per wave per stage: 2 of W, 4 of x */
+
+__device__ __forceinline__ int hl_swz(int r) { return (r >> 1) & 7; }
+
+extern "C" __global__ __launch_bounds__(256) void mm_gemm_hl(mm_gemm_hl_args a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[HL_NS * HL_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* column block bx of matrix `seg` (the second one past nb0 blocks) */
+    const bool seg = (int)blockIdx.x >= a.nb0;
+    const int bx = seg ? blockIdx.x - a.nb0 : blockIdx.x;
+    const int d_out = seg ? a.d_out1 : a.d_out;
+    const uint16_t *wm = seg ? a.w1 : a.w;
+    const int n0 = bx * 64, K = a.n_in, T = a.T, q = lane & 7;
+    const int kb = blockIdx.y * a.kr;
+    const int nch = (min(K, kb + a.kr) - kb) / 64;      /* 64-input chunks of this split */
+
+    /* direct loads of a chunk: W instruction 2 wave + u covers weight rows
+     * (output columns) 8 (2 wave + u) .. + 7 of the block, x instruction
+     * 4 wave + u plane (4 wave + u) / 8, token rows 8 ((4 wave + u) % 8) ..
+     * + 7; lane l loads row + l / 8, slot q = l % 8, i.e. piece q ^ swz(row).
+     * Rows past d_out or T load the last one (not stored). */
+    const uint16_t *wp[2], *xp[4];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int c = 8 * (2 * wave + u) + (lane >> 3);
+        wp[u] = wm + (size_t)min(n0 + c, d_out - 1) * K + kb + 8 * (q ^ hl_swz(c));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = 4 * wave + u, r = 8 * (i & 7) + (lane >> 3);
+        xp[u] = a.xhl + (size_t)(i >> 3) * T * K + (size_t)min(r, T - 1) * K + kb + 8 * (q ^ hl_swz(r));
+    }
+    auto issue = [&](int c, int st) {
+        uint8_t *sb = lds + st * HL_STAGE;
+#pragma unroll
+        for (int u = 0; u < 2; u++) lds_dma16(wp[u] + 64 * c, sb + (2 * wave + u) * 1024);
+#pragma unroll
+        for (int u = 0; u < 4; u++) lds_dma16(xp[u] + 64 * c, sb + HL_WB + (4 * wave + u) * 1024);
+    };
+    /* operand reads (bytes within a stage), K half s: A row 16 wave + l % 16,
+     * B row (column) 16 j + l % 16, piece 4 s + l / 16 */
+    uint32_t ao[2], bo[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int p = 4 * s + (lane >> 4), r = 16 * wave + (lane & 15);
+        ao[s] = HL_WB + r * 128 + 16 * (p ^ hl_swz(r));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = 16 * j + (lane & 15);
+            bo[s][j] = c * 128 + 16 * (p ^ hl_swz(c));
+        }
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    const uint32_t l0 = lds_addr(lds);
+    issue(0, 0);
+    if (nch > 1) issue(1, 1);
+    for (int c = 0; c < nch; c++) {
+        /* chunk c landed (chunk c + 1's loads, issued after, may stay out);
+         * the barrier shows every wave's loads of chunk c and frees the stage
+         * of chunk c - 1 for chunk c + 2 */
+        if (c + 1 < nch) VMCNT_WAIT(HL_LPW);
+        else VMCNT_WAIT(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 2 < nch) issue(c + 2, (c + 2) % HL_NS);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t sb = l0 + (uint32_t)((c % HL_NS) * HL_STAGE);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            i32x4 xa[2], wb[4];
+            xa[0] = ds_read16(sb + ao[s]);
+            xa[1] = ds_read16(sb + ao[s] + 64 * 128);
+#pragma unroll
+            for (int j = 0; j < 4; j++) wb[j] = ds_read16(sb + bo[s][j]);
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(xa[0]), "+v"(xa[1]), "+v"(wb[0]), "+v"(wb[1]), "+v"(wb[2]), "+v"(wb[3]));
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, xa[h]), __builtin_bit_cast(bf16x8, wb[j]), acc[j], 0, 0, 0);
+        }
+    }
+    /* C[token 16 wave + 4 (l / 16) + i][column n0 + 16 j + l % 16] */
+    float *part = a.part + (seg ? (size_t)a.nsplit * T * a.d_out : 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + (lane & 15);
+        if (n >= d_out) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * wave + 4 * (lane >> 4) + i;
+            if (t >= T) continue;
+            if (a.nsplit > 1 || a.part_out) {
+                part[((size_t)blockIdx.y * T + t) * d_out + n] = acc[j][i];
+            } else {
+                float *y = (seg ? a.y1 : a.y) + (size_t)t * d_out + n;
+                *y = a.accumulate ? *y + acc[j][i] : acc[j][i];
+            }
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void mm_skinny_reduce(mm_skinny_reduce_args a) {
     const size_t n0 = (size_t)a.T * a.d_out, n1 = a.y1 ? (size_t)a.T * a.d_out1 : 0;
     for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < n0 + n1;

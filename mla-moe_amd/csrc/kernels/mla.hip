@@ -585,8 +585,15 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_uv(mm_mla_combine_args 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int bb = 16 * t + 4 * (lane >> 4) + i;
-            if (bb < mrows && (lane & 15) < nv)
-                a.ctx[((size_t)(b0 + bb) * a.NH + h) * a.VHD + vw + (lane & 15)] = acc[t][i];
+            if (bb < mrows && (lane & 15) < nv) {
+                const size_t o = ((size_t)(b0 + bb) * a.NH + h) * a.VHD + vw + (lane & 15);
+                a.ctx[o] = acc[t][i];
+                if (a.ctx_hl) {   /* o_proj's operand split once here */
+                    const uint16_t hi = rne16(acc[t][i]);
+                    a.ctx_hl[o] = hi;
+                    a.ctx_hl[(size_t)a.B * a.NH * a.VHD + o] = rne16(acc[t][i] - bf16_f32(hi));
+                }
+            }
         }
 }
 

@@ -805,6 +805,18 @@ extern "C" __global__ __launch_bounds__(MM_I8_CN_THREADS) void mm_i8_combine_nor
         o.z = res[k].z * inv * bf16_lo(nw.y);
         o.w = res[k].w * inv * bf16_hi(nw.y);
         *(f32x4 *)(a.xn + (size_t)t * a.H + n) = o;
+        if (a.xn_hl) {   /* the split of the stored fp32 values (no contraction) */
+            typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+            u16x4 hi, lo;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+#pragma clang fp contract(off)
+                hi[u] = rne16(o[u]);
+                lo[u] = rne16(o[u] - bf16_f32(hi[u]));
+            }
+            *(u16x4 *)(a.xn_hl + (size_t)t * a.H + n) = hi;
+            *(u16x4 *)(a.xn_hl + ((size_t)a.T + t) * a.H + n) = lo;
+        }
     }
     if (a.cnt && t == 0)
         for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;

@@ -133,6 +133,7 @@ def lib():
         L.mm_moe_forward_noalloc_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                                  _vp, C.c_uint]
         L.mm_matmul_bf16_dev.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
+        L.mm_matmul_bf16_hl_dev.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
         L.mm_mla_init.argtypes = [_vp, C.POINTER(MlaConfig), C.c_int]
         L.mm_mla_load_layer.argtypes = [_vp, C.c_int, _vp, C.c_uint]
         L.mm_mla_absorbed_decode_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
@@ -404,6 +405,21 @@ class Context:
     # dense bf16 matmul ----------------------------------------------------------
     def matmul_dev(self, y, x, w, d_out, n_in, T, flags=0):
         _check(lib().mm_matmul_bf16_dev(self.h, y.ptr, x.ptr, w.ptr, d_out, n_in, T, flags))
+
+    def matmul_hl(self, xhl, w, flags=0, y0=None):
+        """mm_matmul_bf16_hl_dev: x given as bf16 hi/lo planes [2, T, n_in]."""
+        xhl = np.ascontiguousarray(xhl, np.uint16)
+        w = np.ascontiguousarray(w, np.uint16)
+        T, (d_out, n_in) = xhl.shape[1], w.shape
+        dx, dw = self.to_device(xhl), self.to_device(w)
+        dy = self.to_device(np.ascontiguousarray(y0, np.float32)) if y0 is not None else \
+            self.empty((T, d_out), np.float32)
+        _check(lib().mm_matmul_bf16_hl_dev(self.h, dy.ptr, dx.ptr, dw.ptr, d_out, n_in, T, flags))
+        y = dy.download()
+        for b in (dx, dw, dy):
+            b.free()
+            self._bufs.remove(b)
+        return y
 
     def matmul(self, x, w, flags=0, y0=None):
         """Mirror of the reference matmul (src/run.c:30) over the rows of x."""

@@ -91,3 +91,36 @@ def test_matmul_empty_is_a_no_op(ctx):
     ctx.matmul_dev(y, x, w, 64, 128, 0)
     ctx.sync()
     assert np.array_equal(y.download(), before)
+
+
+def _rne16(x):
+    """fp32 -> bf16 bits, round to nearest even (the GPU's rne16)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def _split_hl(x):
+    """The bf16 hi/lo planes of fp32 rows: hi = rne(x), lo = rne(x - hi)."""
+    hi = _rne16(x)
+    lo = _rne16((x - synth.bf16_to_f32(hi)).astype(np.float32))
+    return np.stack([hi, lo])
+
+
+@pytest.mark.parametrize("T,d,n", [(5, 3648, 2048), (33, 2048, 2048), (64, 3648, 2048),
+                                   (64, 576, 512), (64, 2000, 2048)])
+def test_gemm_hl_matches_skinny(ctx, T, d, n):
+    """x given as bf16 hi/lo planes (mm_matmul_bf16_hl_dev: both operands
+    through a direct-to-LDS ring) gives the skinny GEMM's bits on the fp32
+    rows: the same split, K splits, partial order and MFMA sequence; plain
+    and accumulating, d not a multiple of the 64-column block."""
+    print(f"gemm hl T={T} d={d} n={n}", flush=True)
+    rng = np.random.default_rng(500 + T + d)
+    x = synth.normal_f32(rng, (T, n))
+    w = synth.normal_bf16(rng, (d, n), 0.02)
+    ref = ctx.matmul(x, w)
+    got = ctx.matmul_hl(_split_hl(x), w)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    y0 = synth.normal_f32(rng, (T, d))
+    ref = ctx.matmul(x, w, mlamoe.MM_MATMUL_ACCUMULATE, y0)
+    got = ctx.matmul_hl(_split_hl(x), w, mlamoe.MM_MATMUL_ACCUMULATE, y0)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
