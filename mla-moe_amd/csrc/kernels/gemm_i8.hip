@@ -250,7 +250,6 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
     __syncthreads();
     set_tile(cur, 0);
     issue_head();
-    bool first = true;
 
     for (;;) {
         const mm_i8_tiled_args &g = a.seg[cur.si];
@@ -289,16 +288,17 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         /* step s, ring slot d = s % BT_NS.  Every step issues one stage
          * (s + BT_P, or the tile's last one again past the end: results
          * unused), so the loads of exactly BT_P - 1 later stages are
-         * outstanding when stage s must have landed -- except on the first
-         * step of a later tile, where the previous tile's stores were issued
-         * after this tile's head stages and vmcnt(63) leaves stage 0
-         * complete.  The barrier then makes every wave's A rows of stage s
-         * visible and frees slot (s - 1) % BT_NS for the stage issued. */
+         * outstanding when stage s must have landed.  On the first step of
+         * a later tile the previous tile's epilogue stores follow this
+         * tile's head stages in issue order; the same count then waits for
+         * them too (the counter completes in order), which keeps stage 0
+         * complete whatever the number of stores.  The barrier then makes
+         * every wave's A rows of stage s visible and frees slot
+         * (s - 1) % BT_NS for the stage issued. */
         auto kloop = [&](auto nri_c) {
             constexpr int NRI = decltype(nri_c)::value;
             auto kstep = [&](int d, int s) {
-                if (!first && s == 0) VMCNT_WAIT(63);
-                else VMCNT_WAIT((BT_P - 1) * BT_LPS);
+                VMCNT_WAIT((BT_P - 1) * BT_LPS);
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
                 const int sn = min(s + BT_P, KB - 1);
@@ -399,7 +399,6 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         t = tn;
         cur = nxt;
         buf ^= 1;
-        first = false;
     }
     VMCNT_WAIT(0);
 }
