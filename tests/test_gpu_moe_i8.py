@@ -236,3 +236,31 @@ def test_i8_empty_batch_is_a_no_op(ctx):
     ctx.moe_forward_dev(0, 0, None, out, flags=mlamoe.MM_FWD_INT8)
     ctx.sync()
     assert np.array_equal(out.download(), before)
+
+
+@pytest.mark.parametrize("T", [3, 6])
+def test_nan_router_scores_route_distinct_experts(ctx, oracle, T):
+    """A NaN logit makes every softmax score of its token NaN.  The
+    reference's strict '>' scan never picks a NaN (its index is then
+    undefined); here a NaN score ranks after every number, so each token
+    still routes to K distinct experts in range -- the GEMMs' per-expert row
+    lists hold at most T rows -- and tokens without NaN route as the
+    oracle's router.  int8 (this fixture's decode or tiled GEMMs; the K-split
+    gate/up at 3 tokens) and bf16 experts."""
+    H, E, K, I, NS = 256, 16, 4, 128, 1
+    print(f"NaN router scores T={T}", flush=True)
+    w = synth.moe_layer(810 + T, H, E, I, NS)
+    ctx.moe_init(H, E, NS, K, I)
+    ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8 | mlamoe.MM_LOAD_BF16)
+    x = synth.activations(811 + T, T, H)
+    logits = np.random.default_rng(812 + T).random((T, E)).astype(np.float32)
+    logits[0, :] = np.nan                  # every logit NaN
+    logits[1, 3] = np.nan                  # one NaN logit
+    cfg = oracle.moe_cfg(H, E, NS, K, I)
+    for flags in (mlamoe.MM_FWD_INT8, mlamoe.MM_FWD_BF16):
+        _, idx, _, _ = ctx.moe_forward(0, x, logits, flags)
+        for t in range(T):
+            row = idx[t].tolist()
+            assert len(set(row)) == K and min(row) >= 0 and max(row) < E, (flags, t, row)
+            if t >= 2:   # the oracle's scan only on NaN-free tokens
+                assert np.array_equal(idx[t], oracle.route(cfg, logits[t])[1]), (flags, t)
