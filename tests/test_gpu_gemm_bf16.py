@@ -34,7 +34,8 @@ def test_matmul_golden(ctx, oracle):
 
 
 @pytest.mark.parametrize("T,d_out,n_in", [(1, 64, 2048), (37, 100, 264), (512, 576, 2048),
-                                          (512, 4096, 512), (70, 3072, 2048),
+                                          (512, 4096, 512), (512, 3072, 2048),
+                                          (512, 2048, 2048), (70, 3072, 2048),
                                           (1024, 3072, 136),    # 128-column tiles
                                           # skinny-M GEMM (5 <= T <= 64, n_in % 64 == 0):
                                           # one split, many splits, ragged columns

@@ -201,6 +201,10 @@ def test_i8_dsv2_prefill_skewed(ctx, oracle):
     lg = ctx.router_logits(0, x, z)
     assert np.array_equal(lg.view(np.uint32), (oracle.matmul(x, w["moe_gate"]) + z).view(np.uint32))
     out, idx, wt, probs, dd = ctx.moe_forward_i8_debug(0, x, lg)
+    # the product GEMM kernel (the debug call runs its twin): the same bits
+    po, pi, pw, _ = ctx.moe_forward(0, x, lg, mlamoe.MM_FWD_INT8)
+    assert np.array_equal(pi, idx) and np.array_equal(pw.view(np.uint32), wt.view(np.uint32))
+    assert np.array_equal(po.view(np.uint32), out.view(np.uint32))
     cfg = oracle.moe_cfg(H, E, NS, K, I)
     qw = oracle.quantize_moe_weights(w)
     ro, ri, *_ = oracle.ffn_i8(cfg, w, qw, x, lg)

@@ -69,7 +69,9 @@ def test_i8_config3_full_size(oracle, layer0):
     times): top-k identical for every token, every accumulator of the
     hottest and of a cold expert bit-exact, all of the shared expert's
     outputs bit-exact, and the layer output on 48 tokens (including tokens
-    routed to the hottest expert) within 2e-3 of the oracle."""
+    routed to the hottest expert) within 2e-3 of the oracle.  The debug call
+    runs the GEMM's accumulator-writing twin; the product kernel then runs on
+    the same inputs and must give the same bits (output, routing, scores)."""
     w, qw = layer0
     T = 2048
     print(f"config 3 full size: T={T}", flush=True)
@@ -81,6 +83,12 @@ def test_i8_config3_full_size(oracle, layer0):
         ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8)
         lg = ctx.router_logits(0, x, z)
         out, idx, wt, probs, dd = ctx.moe_forward_i8_debug(0, x, lg)
+        # the product kernel (the one the bench times; the debug call runs
+        # its accumulator-writing twin) on the same inputs: the same bits
+        po, pi, pw, pp = ctx.moe_forward(0, x, lg, mlamoe.MM_FWD_INT8)
+    assert np.array_equal(pi, idx) and np.array_equal(pw.view(np.uint32), wt.view(np.uint32))
+    assert np.array_equal(po.view(np.uint32), out.view(np.uint32))
+    assert np.array_equal(pp.view(np.uint32), probs.view(np.uint32))
     # router logits: the reference's sequential fp32 order, bit for bit
     assert np.array_equal(lg.view(np.uint32), (oracle.matmul(x, w["moe_gate"]) + z).view(np.uint32))
     # routing of every token identical to the CPU router
