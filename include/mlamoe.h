@@ -3,7 +3,7 @@
  * A drop-in for the reference engine's CPU hot path:
  *   - the MoE FFN, ffn_compute (src/run.c:116-162), batched over T tokens,
  *     with bf16 weights (GEMV, T small) or int8 weights (MFMA, any T);
- *   - (declared as they are implemented) the dense bf16 matmul
+ *   - the dense bf16 matmul
  *     (src/run.c:29-37) and the MLA absorbed-decode chain (src/run.c:430-460).
  *
  * Conventions
@@ -16,8 +16,9 @@
  *     time.  The reference keeps this state in a process-global GpuContext
  *     (src/getp_run.hip:26, src/kernels/getp_state.h:57-96).
  *   - Functions named *_dev take device pointers and are asynchronous on the
- *     context stream; the mm_ffn_compute* mirrors take host pointers and
- *     return with the result in host memory, like the reference functions.
+ *     context stream.  mm_moe_forward / mm_ffn_compute, mm_matmul_bf16 and
+ *     mm_mla_absorbed_decode take host pointers and return with the result
+ *     in host memory, like the reference functions they replace.
  *   - Weights are uploaded (and quantised, for int8) once per layer, outside
  *     any timed region, like the reference's warm_up (src/getp_run.hip:703-880).
  */
@@ -66,6 +67,10 @@ MM_API void *mm_ctx_stream(mm_ctx *ctx);
 MM_API int mm_ctx_set_stream(mm_ctx *ctx, void *stream);
 /* Wait for all work queued on the context stream. */
 MM_API int mm_ctx_sync(mm_ctx *ctx);
+/* Bytes of device workspace the context holds now: the *_dev entry points
+ * grow it on demand (after a stream sync) and keep it until the context is
+ * destroyed; mm_moe_forward_noalloc_dev never touches it. */
+MM_API int mm_ctx_workspace_bytes(mm_ctx *ctx, size_t *bytes);
 
 /* ---- device memory and timing helpers ------------------------------------ */
 MM_API int mm_dev_alloc(mm_ctx *ctx, size_t bytes, void **dptr);
@@ -129,6 +134,19 @@ MM_API int mm_moe_init(mm_ctx *ctx, const mm_moe_config *cfg, int n_layers);
 /* Upload one layer's weights (synchronous). */
 MM_API int mm_moe_load_layer(mm_ctx *ctx, int layer, const mm_moe_layer_weights *w, unsigned flags);
 
+/* Load layer `layer` as a dense SwiGLU layer, the first_k_dense layers of
+ * the reference (ffn_compute's dense branch, src/run.c:119-122: ModelWeights
+ * dense_gate / dense_up [dense_inter, H], dense_down [H, dense_inter], bf16,
+ * include/model.h:79-81); dense_inter % 8 == 0.  The forward calls then
+ * compute out = down . (silu(gate . xn) * (up . xn)) for it, with bf16
+ * weights and fp32 activations whatever the MM_FWD_* format flag, and leave
+ * topk_idx, topk_w and probs untouched (the reference returns before its
+ * router).  Host pointers, or device pointers with MM_LOAD_DEVICE_PTRS (the
+ * weights are copied).  Synchronous. */
+MM_API int mm_moe_load_dense_layer(mm_ctx *ctx, int layer, const uint16_t *gate,
+                                   const uint16_t *up, const uint16_t *down, int dense_inter,
+                                   unsigned flags);
+
 /* ---- the packed int8 expert format (offline quantisation) ------------------ */
 /* One layer's int8 experts as the MFMA kernels read them: a pool of 16-row x
  * 64-byte fragments -- routed gate/up [E][I/16][H/64][gate, up], routed down
@@ -177,10 +195,11 @@ MM_API int mm_moe_forward_dev(mm_ctx *ctx, int layer, int T, const float *xn, fl
  * device array of MM_NOALLOC_SCRATCH_BYTES per device (32 MiB: e.g. up to
  * ~280 tokens of a DeepSeek-V2-Lite int8 layer, 64 for the bench's decode
  * batch) instead of the context's growable buffer.  A call that would need
- * more fails with MM_ERR_UNSUPPORTED before launching anything; so does a
- * call while per-kernel profiling is on.  Every call on a device shares that
+ * more fails with MM_ERR_UNSUPPORTED before launching anything.  Every call
+ * on a device shares that
  * device's array: calls that overlap on one device (two streams, two host
- * threads) race. */
+ * threads) race.  While per-kernel profiling is on (mm_prof_enable) it
+ * returns MM_ERR_STATE: the profiler's records are host allocations. */
 #define MM_NOALLOC_SCRATCH_BYTES (32u << 20)
 MM_API int mm_moe_forward_noalloc_dev(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
                                       const float *logits, int32_t *topk_idx, float *topk_w,
@@ -225,10 +244,23 @@ MM_API int mm_moe_forward_i8_debug_dev(mm_ctx *ctx, int layer, int T, const floa
                                        float *probs, unsigned flags,
                                        const mm_moe_i8_debug *dbg);
 
+/* mm_moe_forward_dev with host pointers (the prefill loop of
+ * src/run.c:291-313 in one call): xn, out [T, H], topk_idx / topk_w [T, K],
+ * probs [T, E] (any of the last three may be NULL).  Routes from the layer's
+ * own router (no logits argument).  Synchronous: returns with the results in
+ * host memory. */
+MM_API int mm_moe_forward(mm_ctx *ctx, int layer, int T, const float *xn, float *out,
+                          int32_t *topk_idx, float *topk_w, float *probs, unsigned flags);
+
 /* Host-pointer mirror of ffn_compute (src/run.c:116-117) for one token:
- * out [H] overwritten; topk_idx/topk_w [K] may be NULL. Synchronous. */
+ * out [H] overwritten (MM_FWD_ACCUMULATE is ignored, as the reference
+ * overwrites); topk_idx / topk_w [K] receive the selected experts and
+ * weights, probs [E] the router's softmax (or sigmoid) scores -- what the
+ * reference leaves in s->moe_logits (src/run.c:124-129) --, each may be
+ * NULL.  A dense layer (mm_moe_load_dense_layer) leaves all three untouched,
+ * as the reference's dense branch does.  Synchronous. */
 MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, int *topk_idx,
-                   float *topk_w, unsigned flags);
+                          float *topk_w, float *probs, unsigned flags);
 
 /* ---- dense bf16 matmul ------------------------------------------------------ */
 
@@ -244,6 +276,22 @@ MM_API int mm_ffn_compute(mm_ctx *ctx, int layer, const float *xn, float *out, i
  * asynchronous. */
 MM_API int mm_matmul_bf16_dev(mm_ctx *ctx, float *y, const float *x, const uint16_t *w,
                               int d_out, int n_in, int T, unsigned flags);
+
+#define MM_MATMUL_W_HOST 4u       /* mm_matmul_bf16: w is host memory (uploaded once, kept) */
+
+/* matmul (src/run.c:29-37) with host x [T, n_in] and y [T, d_out]: the
+ * reference call matmul(y, x, w, d_out, n_in) is mm_matmul_bf16(ctx, y, x,
+ * w, d_out, n_in, 1, MM_MATMUL_W_HOST).  w is a device pointer, or with
+ * MM_MATMUL_W_HOST a host pointer whose matrix is copied to the device on
+ * its first use and looked up by (pointer, size) afterwards -- the
+ * reference's weights are read-only mappings of the checkpoint
+ * (include/model.h:44-46), so a host matrix must not change while the
+ * context holds its copy (mm_host_weights_release drops every copy).
+ * Other flags as mm_matmul_bf16_dev.  Synchronous. */
+MM_API int mm_matmul_bf16(mm_ctx *ctx, float *y, const float *x, const uint16_t *w, int d_out,
+                          int n_in, int T, unsigned flags);
+/* Free the device copies of host weights that mm_matmul_bf16 keeps. */
+MM_API int mm_host_weights_release(mm_ctx *ctx);
 
 /* The same product over T <= 64 rows (the batched decode step's
  * projections) with x given already split: xhl [2, T, n_in] bf16, plane 0
@@ -319,6 +367,21 @@ MM_API int mm_mla_absorbed_decode_dev(mm_ctx *ctx, int layer, int B, const float
                                       const uint16_t *cache, int seq_stride,
                                       const int32_t *kv_lens, int kv_len, float *ctx_out,
                                       float *qabs, float *probs, float *clat);
+
+/* The absorbed chain with host pointers and the reference's own fp32 latent
+ * cache (RunState kv_cache rows c_kv | k_pe, include/model.h:117):
+ * q [B, NH, QKN + QKR], cache [B, seq_stride, KVL + QKR] fp32 (the first
+ * kv_len rows of each sequence are read), kv_lens [B] host or NULL, and the
+ * outputs of mm_mla_absorbed_decode_dev in host memory (qabs, probs, clat
+ * may be NULL).  The cache rows are rounded to bf16 (nearest even) on the
+ * device, the element type the attention kernels read: the results are
+ * those of mm_mla_absorbed_decode_dev on the rounded cache, and differ from
+ * the fp32 reference by what that rounding moves (at most 2^-9 of each
+ * element; normwise below 2^-8).  Synchronous. */
+MM_API int mm_mla_absorbed_decode(mm_ctx *ctx, int layer, int B, const float *q,
+                                  const float *cache, int seq_stride, const int32_t *kv_lens,
+                                  int kv_len, float *ctx_out, float *qabs, float *probs,
+                                  float *clat);
 
 /* ---- MLA decode front: projections, RoPE, latent-cache append -------------- */
 

@@ -81,6 +81,7 @@ static const struct {
     [K_REDUCE_RMSNORM] = {"mm_reduce_rmsnorm", MOD_LM_HEAD},
     [K_ZERO32] = {"mm_zero32", MOD_UTIL},
     [K_GATHER_ROWS] = {"mm_gather_rows", MOD_UTIL},
+    [K_F32_BF16] = {"mm_f32_bf16", MOD_UTIL},
 };
 
 /* ---- errors ------------------------------------------------------------- */
@@ -175,7 +176,9 @@ void mm_ctx_destroy(mm_ctx *c) {
     if (c->own_stream && c->own_stream != c->stream) hipStreamSynchronize(c->own_stream);
     mm_moe_release(c);
     mm_mla_release(c);
+    mm_host_release(c);
     if (c->ws) hipFree(c->ws);
+    if (c->io) hipFree(c->io);
     for (size_t i = 0; i < c->ev_pool_n; i++) hipEventDestroy(c->ev_pool[i]);
     free(c->ev_pool);
     free(c->prof);
@@ -350,6 +353,25 @@ int mm_workspace(mm_ctx *c, size_t bytes, void **out) {
         c->ws_bytes = nb;
     }
     *out = c->ws;
+    return MM_OK;
+}
+
+int mm_io_buffer(mm_ctx *c, size_t bytes, void **out) {
+    if (bytes > c->io_bytes) {
+        MM_HIP(hipStreamSynchronize(c->stream));
+        if (c->io) MM_HIP(hipFree(c->io));
+        c->io = NULL;
+        c->io_bytes = 0;
+        MM_HIP(hipMalloc(&c->io, bytes));
+        c->io_bytes = bytes;
+    }
+    *out = c->io;
+    return MM_OK;
+}
+
+int mm_ctx_workspace_bytes(mm_ctx *c, size_t *bytes) {
+    if (!c || !bytes) return mm_fail(MM_ERR_INVALID, "mm_ctx_workspace_bytes: bad argument");
+    *bytes = c->ws_bytes;
     return MM_OK;
 }
 

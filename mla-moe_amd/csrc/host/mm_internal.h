@@ -58,6 +58,7 @@ typedef enum {
     K_REDUCE_RMSNORM,
     K_ZERO32,
     K_GATHER_ROWS,
+    K_F32_BF16,
     K_COUNT
 } mm_kernel_id;
 
@@ -68,11 +69,13 @@ typedef struct {
 
 typedef struct {
     int loaded;
+    int dense;                  /* a dense SwiGLU layer (l < first_k_dense, src/run.c:119-122) */
+    int dense_inter;            /* its intermediate size */
     unsigned formats;
     uint16_t *wg;               /* [E, H] bf16 router weight */
     float *bias;                /* [E] or NULL */
     uint16_t *bf16_pool;        /* one allocation holding the six bf16 families */
-    uint16_t *eg, *eu, *ed, *sg, *su, *sd;
+    uint16_t *eg, *eu, *ed, *sg, *su, *sd;   /* dense layer: sg, su, sd = gate, up, down */
     int8_t *i8_pool;            /* packed int8 fragments (kernel_params.h) */
     float *i8_scales;
     mm_i8_weights i8;
@@ -106,7 +109,6 @@ struct mm_ctx {
     float *norm_xn;
     uint16_t *norm_xn_hl;
     float norm_eps;
-    float *ffn_io;              /* mm_ffn_compute staging: x [H] | out [H] | idx [K] | w [K] */
 
     /* MLA */
     int mla_ready;
@@ -122,6 +124,12 @@ struct mm_ctx {
     /* growable device workspace */
     void *ws;
     size_t ws_bytes;
+    /* growable device staging of the synchronous host-pointer entry points */
+    void *io;
+    size_t io_bytes;
+    /* device copies of host weights passed to mm_matmul_bf16 (MM_MATMUL_W_HOST) */
+    struct mm_wcache_entry *wcache;
+    size_t wcache_n, wcache_cap;
 
     /* this device's copy of the no-allocation entry point's static scratch
      * array (its device address, from hipGetSymbolAddress at set-up) */
@@ -169,6 +177,10 @@ int mm_launch(mm_ctx *ctx, mm_kernel_id id, unsigned gx, unsigned gy, unsigned g
 /* Device workspace of at least `bytes`, reallocated (after a stream sync)
  * when too small. */
 int mm_workspace(mm_ctx *ctx, size_t bytes, void **out);
+/* Device staging of at least `bytes` for the host-pointer entry points (a
+ * buffer of its own: the forward calls they make use the workspace). */
+int mm_io_buffer(mm_ctx *ctx, size_t bytes, void **out);
+void mm_host_release(mm_ctx *ctx);
 
 /* Dense bf16 GEMM (mm_matmul_bf16_dev) on a caller-provided workspace of at
  * least mm_gemm_bf16_ws_bytes(T, n_in, d_out, flags) bytes. */

@@ -32,8 +32,6 @@ void mm_moe_release(mm_ctx *c) {
     c->layers = NULL;
     if (c->moe_cnt) hipFree(c->moe_cnt);
     c->moe_cnt = NULL;
-    if (c->ffn_io) hipFree(c->ffn_io);
-    c->ffn_io = NULL;
     c->moe_ready = 0;
 }
 
@@ -54,7 +52,6 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     MM_HIP(hipMalloc((void **)&c->moe_cnt, (size_t)E * sizeof(int32_t)));
     MM_HIP(hipMemsetAsync(c->moe_cnt, 0, (size_t)E * sizeof(int32_t), c->stream));
     MM_HIP(hipStreamSynchronize(c->stream));
-    MM_HIP(hipMalloc((void **)&c->ffn_io, (2 * (size_t)H + 2 * (size_t)K) * sizeof(float)));
     c->layers = calloc((size_t)n_layers, sizeof(mm_moe_layer));
     if (!c->layers) return mm_fail(MM_ERR_NOMEM, "mm_moe_init: calloc");
     c->moe = *cfg;
@@ -263,6 +260,45 @@ out:;
     return st;
 }
 
+/* ---- dense layers (l < first_k_dense) --------------------------------------- */
+
+int mm_moe_load_dense_layer(mm_ctx *c, int layer, const uint16_t *gate, const uint16_t *up,
+                            const uint16_t *down, int dense_inter, unsigned flags) {
+    if (!c || !gate || !up || !down)
+        return mm_fail(MM_ERR_INVALID, "mm_moe_load_dense_layer: NULL argument");
+    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_load_dense_layer: call mm_moe_init first");
+    if (layer < 0 || layer >= c->n_layers)
+        return mm_fail(MM_ERR_INVALID, "mm_moe_load_dense_layer: layer %d out of range", layer);
+    if (dense_inter <= 0 || dense_inter % 8)
+        return mm_fail(MM_ERR_UNSUPPORTED,
+                       "mm_moe_load_dense_layer: dense_inter must be a positive multiple of 8");
+    mm_moe_layer *L = &c->layers[layer];
+    if (L->loaded) return mm_fail(MM_ERR_STATE, "mm_moe_load_dense_layer: layer %d already loaded", layer);
+    int st = mm_set_device(c);
+    if (st) return st;
+    const size_t H = c->moe.hidden_size, DI = dense_inter, ne = DI * H;
+    const int dev = (flags & MM_LOAD_DEVICE_PTRS) != 0;
+    if (hipMalloc((void **)&L->bf16_pool, 3 * ne * sizeof(uint16_t)) != hipSuccess)
+        return mm_fail(MM_ERR_NOMEM, "mm_moe_load_dense_layer: %zu bytes", 3 * ne * 2);
+    L->sg = L->bf16_pool;
+    L->su = L->sg + ne;
+    L->sd = L->su + ne;
+    if (!(st = upload(c, L->sg, gate, ne * 2, dev)) && !(st = upload(c, L->su, up, ne * 2, dev)))
+        st = upload(c, L->sd, down, ne * 2, dev);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (!st && e != hipSuccess) st = mm_hip_fail(e, "mm_moe_load_dense_layer");
+    if (st) {
+        hipFree(L->bf16_pool);
+        L->bf16_pool = L->sg = L->su = L->sd = NULL;
+        return st;
+    }
+    L->dense = 1;
+    L->dense_inter = dense_inter;
+    L->formats = MM_LOAD_BF16;
+    L->loaded = 1;
+    return MM_OK;
+}
+
 /* ---- packed int8 layers (the offline expert format) ------------------------ */
 
 static int i8_cfg_ok(const mm_moe_config *g) {
@@ -360,6 +396,45 @@ static int take_ws(mm_ctx *c, const mm_fixed_ws *fx, size_t need, char **ws) {
         return MM_OK;
     }
     return mm_workspace(c, need, (void **)ws);
+}
+
+/* The dense branch of ffn_compute (src/run.c:119-122, swiglu at :86-93):
+ * out = down . (silu(gate . xn) * (up . xn)) over T rows, fp32 activations
+ * and bf16 weights whatever the expert format (the reference's dense MLP
+ * is bf16), out overwritten or accumulated.  Gate and up in one pass (the
+ * fused GEMV up to MM_GEMV_NB rows, the skinny or tiled MFMA GEMM above),
+ * SwiGLU in place over the gate rows, then the down projection. */
+static int forward_dense(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
+                         int acc, const mm_fixed_ws *fx) {
+    const int H = c->moe.hidden_size, DI = L->dense_inter;
+    const int gv_gu = T <= MM_GEMV_NB && H <= MM_LM_HMAX;
+    const int gv_d = T <= MM_GEMV_NB && DI <= MM_LM_HMAX;
+    const unsigned dflags = acc ? MM_MATMUL_ACCUMULATE : 0;
+    size_t wsb = gv_gu ? 0 : mm_gemm_bf16_ws2_bytes(T, H, DI, DI, 0);
+    const size_t wsd = gv_d ? 0 : mm_gemm_bf16_ws_bytes(T, DI, H, dflags);
+    if (wsd > wsb) wsb = wsd;
+    mm_plan p = {0};
+    const size_t o_g = plan_take(&p, (size_t)T * DI * 4), o_u = plan_take(&p, (size_t)T * DI * 4);
+    const size_t o_ws = plan_take(&p, wsb);
+    char *ws;
+    int st = take_ws(c, fx, p.off, &ws);
+    if (st) return st;
+    float *g = (float *)(ws + o_g), *u = (float *)(ws + o_u);
+    if (gv_gu) {
+        mm_gemv_args a = {xn, NULL, 0.0f, L->sg, L->su, g, u, DI, DI, DI, DI, T, H, 0, 0};
+        if ((st = mm_gemv_launch(c, &a))) return st;
+    } else if ((st = mm_gemm_bf16_ws2(c, g, L->sg, DI, u, L->su, DI, xn, H, T, 0, ws + o_ws))) {
+        return st;
+    }
+    const size_t n = (size_t)T * DI;
+    mm_swiglu_args sa = {g, u, g, n};
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    if ((st = mm_launch(c, K_SWIGLU, (unsigned)blocks, 1, 1, 256, 0, &sa))) return st;
+    if (gv_d) {
+        mm_gemv_args a = {g, NULL, 0.0f, L->sd, NULL, out, NULL, H, 0, H, 0, T, DI, acc, 0};
+        return mm_gemv_launch(c, &a);
+    }
+    return mm_gemm_bf16_ws(c, out, g, L->sd, H, DI, T, dflags, ws + o_ws);
 }
 
 /* ---- bf16 forward ------------------------------------------------------------ */
@@ -699,6 +774,12 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
     int st = mm_set_device(c);
     if (st) return st;
     const int acc = (flags & MM_FWD_ACCUMULATE) != 0;
+    if (L->dense) {
+        /* the reference returns before routing: topk_idx, topk_w, probs untouched */
+        if (dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: layer %d is dense (no int8 "
+                                "intermediates)", layer);
+        return forward_dense(c, L, T, xn, out, acc, fx);
+    }
     if (flags & MM_FWD_INT8) {
         if (!(L->formats & MM_LOAD_INT8))
             return mm_fail(MM_ERR_STATE, "mm_moe_forward: layer %d has no int8 weights", layer);
@@ -736,8 +817,9 @@ int mm_moe_router_logits_dev(mm_ctx *c, int layer, int T, const float *xn,
                              const float *logit_bias, float *logits) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_router_logits_dev: NULL context");
     if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_router_logits_dev: call mm_moe_init first");
-    if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded)
-        return mm_fail(MM_ERR_STATE, "mm_moe_router_logits_dev: layer %d not loaded", layer);
+    if (layer < 0 || layer >= c->n_layers || !c->layers[layer].loaded || c->layers[layer].dense)
+        return mm_fail(MM_ERR_STATE, "mm_moe_router_logits_dev: layer %d is not a loaded MoE layer",
+                       layer);
     if (T < 0 || (T > 0 && (!xn || !logits)))
         return mm_fail(MM_ERR_INVALID, "mm_moe_router_logits_dev: bad arguments");
     if (T == 0) return MM_OK;
@@ -775,24 +857,4 @@ int mm_moe_forward_i8_debug_dev(mm_ctx *c, int layer, int T, const float *xn, fl
     if (!dbg) return mm_fail(MM_ERR_INVALID, "mm_moe_forward_i8_debug_dev: NULL debug block");
     return forward(c, layer, T, xn, out, logits, topk_idx, topk_w, probs, flags | MM_FWD_INT8,
                    dbg, NULL);
-}
-
-int mm_ffn_compute(mm_ctx *c, int layer, const float *xn, float *out, int *topk_idx,
-                   float *topk_w, unsigned flags) {
-    if (!c || !xn || !out) return mm_fail(MM_ERR_INVALID, "mm_ffn_compute: NULL argument");
-    if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_ffn_compute: call mm_moe_init first");
-    const int H = c->moe.hidden_size, K = c->moe.n_experts_per_tok;
-    int st = mm_set_device(c);
-    if (st) return st;
-    /* the context's staging (allocated by mm_moe_init): [x | out | idx | w] */
-    float *dx = c->ffn_io, *dout = dx + H;
-    int32_t *didx = (int32_t *)(dout + H);
-    float *dw = (float *)(didx + K);
-    if (!(st = mm_h2d(c, dx, xn, (size_t)H * sizeof(float))))
-        st = mm_moe_forward_dev(c, layer, 1, dx, dout, NULL, didx, dw, NULL,
-                                flags & ~(unsigned)MM_FWD_ACCUMULATE);
-    if (!st) st = mm_d2h(c, out, dout, (size_t)H * sizeof(float));
-    if (!st && topk_idx) st = mm_d2h(c, topk_idx, didx, (size_t)K * sizeof(int32_t));
-    if (!st && topk_w) st = mm_d2h(c, topk_w, dw, (size_t)K * sizeof(float));
-    return st;
 }

@@ -113,6 +113,14 @@ typedef struct {
     size_t n;
 } mm_swiglu_args;
 
+/* y = bf16(x), round to nearest even, over n values (the host-pointer
+ * absorbed-decode entry point's fp32 cache rows). */
+typedef struct {
+    const float *x;
+    uint16_t *y;
+    uint64_t n;
+} mm_f32_bf16_args;
+
 /* ---- int8 MoE path ------------------------------------------------------ */
 
 /* Per-layer int8 weights in MFMA fragment order.  A "fragment" is the

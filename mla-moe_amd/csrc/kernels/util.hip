@@ -94,3 +94,10 @@ extern "C" __global__ __launch_bounds__(256) void mm_swiglu(mm_swiglu_args a) {
         a.h[i] = g / (1.0f + expf(-g)) * a.u[i];
     }
 }
+
+/* y = bf16(x) rounded to nearest even (the latent cache's element type). */
+extern "C" __global__ __launch_bounds__(256) void mm_f32_bf16(mm_f32_bf16_args a) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        a.y[i] = rne16(a.x[i]);
+}

@@ -22,7 +22,7 @@ HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "mlamoe.h")
 MM_LOAD_BF16, MM_LOAD_INT8, MM_LOAD_DEVICE_PTRS = 1, 2, 4
 MM_FWD_BF16, MM_FWD_INT8, MM_FWD_ACCUMULATE = 0, 1, 2
 MM_FILL_BF16_NORMAL, MM_FILL_F32_NORMAL, MM_FILL_F32_UNIFORM = 0, 1, 2
-MM_MATMUL_X_BF16, MM_MATMUL_ACCUMULATE = 1, 2
+MM_MATMUL_X_BF16, MM_MATMUL_ACCUMULATE, MM_MATMUL_W_HOST = 1, 2, 4
 
 _vp = C.c_void_p
 
@@ -129,7 +129,14 @@ def lib():
         L.mm_moe_load_layer.argtypes = [_vp, C.c_int, C.POINTER(MoeLayerWeights), C.c_uint]
         L.mm_moe_forward_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_uint]
-        L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_ffn_compute.argtypes = [_vp, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_moe_forward.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_uint]
+        L.mm_moe_load_dense_layer.argtypes = [_vp, C.c_int, _vp, _vp, _vp, C.c_int, C.c_uint]
+        L.mm_matmul_bf16.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
+        L.mm_host_weights_release.argtypes = [_vp]
+        L.mm_mla_absorbed_decode.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
+                                             C.c_int, _vp, _vp, _vp, _vp]
+        L.mm_ctx_workspace_bytes.argtypes = [_vp, C.POINTER(C.c_size_t)]
         L.mm_moe_forward_noalloc_dev.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                                  _vp, C.c_uint]
         L.mm_matmul_bf16_dev.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint]
@@ -266,6 +273,12 @@ class Context:
     def stream(self):
         return lib().mm_ctx_stream(self.h)
 
+    def workspace_bytes(self):
+        """Device workspace the context holds now (mm_ctx_workspace_bytes)."""
+        n = C.c_size_t()
+        _check(lib().mm_ctx_workspace_bytes(self.h, C.byref(n)))
+        return n.value
+
     # timing --------------------------------------------------------------
     def timer_start(self):
         _check(lib().mm_timer_start(self.h))
@@ -319,6 +332,35 @@ class Context:
         lw = MoeLayerWeights(base(w["moe_gate"]), base(w.get("moe_gate_bias")), eg, eu, ed,
                              base(w["sg"]), base(w["su"]), base(w["sd"]))
         _check(lib().mm_moe_load_layer(self.h, layer, C.byref(lw), flags))
+
+    def moe_load_dense_layer(self, layer, gate, up, down, flags=0):
+        """A dense SwiGLU layer (the reference's first_k_dense layers):
+        gate/up [DI, H], down [H, DI] bf16 host arrays (or DevBufs with
+        MM_LOAD_DEVICE_PTRS)."""
+        if flags & MM_LOAD_DEVICE_PTRS:
+            ptrs, di = (gate.ptr, up.ptr, down.ptr), gate.shape[0]
+        else:
+            gate, up, down = (np.ascontiguousarray(a, np.uint16) for a in (gate, up, down))
+            ptrs, di = (gate.ctypes.data, up.ctypes.data, down.ctypes.data), gate.shape[0]
+        _check(lib().mm_moe_load_dense_layer(self.h, layer, *ptrs, int(di), flags))
+
+    def moe_forward_host(self, layer, xn, flags=MM_FWD_BF16, out=None, want=True):
+        """mm_moe_forward: host arrays in and out through the synchronous
+        host-pointer entry point.  Returns out, topk_idx, topk_w, probs (the
+        last three preset to -1 / NaN so a dense layer shows them untouched)."""
+        cfg = self._moe_cfg
+        xn = np.ascontiguousarray(xn, np.float32)
+        T = xn.shape[0]
+        E, K, H = cfg.n_routed_experts, cfg.n_experts_per_tok, cfg.hidden_size
+        o = np.zeros((T, H), np.float32) if out is None else \
+            np.array(out, np.float32, copy=True, order="C")
+        idx = np.full((T, K), -1, np.int32)
+        w = np.full((T, K), np.nan, np.float32)
+        p = np.full((T, E), np.nan, np.float32)
+        q = (lambda a: a.ctypes.data) if want else (lambda a: None)
+        _check(lib().mm_moe_forward(self.h, layer, T, xn.ctypes.data, o.ctypes.data, q(idx), q(w),
+                                    q(p), flags))
+        return o, idx, w, p
 
     def moe_forward_dev(self, layer, T, xn, out, logits=None, topk_idx=None, topk_w=None,
                         probs=None, flags=MM_FWD_BF16):
@@ -420,6 +462,23 @@ class Context:
             b.free()
             self._bufs.remove(b)
         return y
+
+    def matmul_host(self, x, w, flags=MM_MATMUL_W_HOST, y0=None):
+        """mm_matmul_bf16: host x (and y), w a host bf16 array (kept by the
+        context, MM_MATMUL_W_HOST) or a DevBuf."""
+        dev = isinstance(w, DevBuf)
+        wa = w if dev else np.ascontiguousarray(w, np.uint16)
+        d_out, n_in = w.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, n_in)
+        y = np.zeros((x.shape[0], d_out), np.float32) if y0 is None else \
+            np.array(y0, np.float32, copy=True, order="C")
+        _check(lib().mm_matmul_bf16(self.h, y.ctypes.data, x.ctypes.data,
+                                    wa.ptr if dev else wa.ctypes.data, d_out, n_in, x.shape[0],
+                                    flags))
+        return y
+
+    def host_weights_release(self):
+        _check(lib().mm_host_weights_release(self.h))
 
     def matmul(self, x, w, flags=0, y0=None):
         """Mirror of the reference matmul (src/run.c:30) over the rows of x."""
@@ -531,6 +590,23 @@ class Context:
             self._bufs.remove(b)
         return out
 
+    def mla_absorbed_decode_host(self, layer, q, cache, kv_len, kv_lens=None, want=True):
+        """mm_mla_absorbed_decode: host q [B, NH, QKN+QKR] and the fp32 cache
+        [B, L, KVL+QKR]; returns ctx, qabs, probs, clat (None without want)."""
+        cfg = self._mla_cfg
+        q = np.ascontiguousarray(q, np.float32)
+        cache = np.ascontiguousarray(cache, np.float32)
+        B, L = cache.shape[0], cache.shape[1]
+        NH, KVL, VHD = cfg.n_heads, cfg.kv_lora_rank, cfg.v_head_dim
+        ctx = np.empty((B, NH * VHD), np.float32)
+        outs = [np.empty((B, NH, KVL), np.float32), np.empty((B, NH, kv_len), np.float32),
+                np.empty((B, NH, KVL), np.float32)] if want else [None] * 3
+        lens = np.ascontiguousarray(kv_lens, np.int32) if kv_lens is not None else None
+        p = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+        _check(lib().mm_mla_absorbed_decode(self.h, layer, B, q.ctypes.data, cache.ctypes.data, L,
+                                            p(lens), kv_len, ctx.ctypes.data, *[p(a) for a in outs]))
+        return (ctx, *outs)
+
     # MLA decode front -----------------------------------------------------------
     def mla_front_init(self, H, inv_freq, q_lora=0, rms_eps=1e-6, mla_eps=1e-6, interleaved=0):
         inv = np.ascontiguousarray(inv_freq, np.float32)
@@ -574,12 +650,16 @@ class Context:
         return out
 
     def ffn_compute(self, layer, xn, flags=MM_FWD_BF16):
-        """Mirror of the reference ffn_compute (src/run.c:116) for one token."""
+        """Mirror of the reference ffn_compute (src/run.c:116) for one token:
+        returns out, topk_idx, topk_w and the router scores (what the
+        reference leaves in s->moe_logits); the last three keep their preset
+        -1 / NaN on a dense layer, which the reference does not route."""
         cfg = self._moe_cfg
         xn = np.ascontiguousarray(xn, np.float32)
         out = np.empty(cfg.hidden_size, np.float32)
-        idx = np.empty(cfg.n_experts_per_tok, np.int32)
-        w = np.empty(cfg.n_experts_per_tok, np.float32)
+        idx = np.full(cfg.n_experts_per_tok, -1, np.int32)
+        w = np.full(cfg.n_experts_per_tok, np.nan, np.float32)
+        p = np.full(cfg.n_routed_experts, np.nan, np.float32)
         _check(lib().mm_ffn_compute(self.h, layer, xn.ctypes.data, out.ctypes.data,
-                                    idx.ctypes.data, w.ctypes.data, flags))
-        return out, idx, w
+                                    idx.ctypes.data, w.ctypes.data, p.ctypes.data, flags))
+        return out, idx, w, p

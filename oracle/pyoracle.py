@@ -245,6 +245,22 @@ def route(cfg, logits, bias=None):
     return s, idx, w
 
 
+def swiglu_rows(xn, gate, up, down):
+    """run.c:86-93 swiglu (the dense branch of ffn_compute, run.c:119-122)
+    for each row of xn: down . (silu(gate . x) * (up . x))."""
+    x2 = c32(xn).reshape(-1, np.shape(gate)[1])
+    gate, up, down = (np.ascontiguousarray(a, dtype=np.uint16) for a in (gate, up, down))
+    inter, H = gate.shape
+    out = np.empty((x2.shape[0], H), np.float32)
+    hb = np.empty(inter, np.float32)
+    hb2 = np.empty(inter, np.float32)
+    for t in range(x2.shape[0]):
+        row = np.ascontiguousarray(x2[t])
+        lib().or_swiglu(_p(out[t], _f32p), _p(row, _f32p), _p(gate, _u16p), _p(up, _u16p),
+                        _p(down, _u16p), inter, H, _p(hb, _f32p), _p(hb2, _f32p))
+    return out
+
+
 def ffn_compute_rows(cfg, w, xn, logits=None):
     """T tokens through the reference MoE FFN; returns out, idx, w, probs."""
     xn = c32(xn)

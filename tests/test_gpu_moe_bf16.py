@@ -110,8 +110,9 @@ def test_ffn_dsv2_golden(ctx, dsv2_layer):
     assert ulp_diff(probs, g["probs"]).max() <= 2
     assert max_abs_rel(out, g["out"]) < TOL
     # the host-pointer mirror of ffn_compute gives the same result
-    o1, i1, w1 = ctx.ffn_compute(0, x[0])
+    o1, i1, w1, p1 = ctx.ffn_compute(0, x[0])
     assert np.array_equal(i1, g["idx"][0]) and max_abs_rel(o1, g["out"][0]) < TOL
+    assert ulp_diff(p1, g["probs"][0]).max() <= 2     # s->moe_logits after ffn_compute
 
 
 def test_ffn_multi_token_and_accumulate(ctx, oracle):

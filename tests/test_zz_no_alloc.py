@@ -2,8 +2,9 @@
 nothing: its workspace is a static per-device scratch array) against
 mm_moe_forward_dev: identical outputs, routing and scores on two calls in a
 row, the second with fewer tokens, for the int8 decode-shaped path at the
-bench's B = 64 DeepSeek-V2-Lite shape, the int8 tiled path and the bf16 GEMV
-path; a call needing more than the array holds, and a call while per-kernel
+bench's B = 64 DeepSeek-V2-Lite shape, the int8 tiled path, the bf16 GEMV
+path and a dense SwiGLU layer; on a fresh context the no-allocation calls
+leave the context's workspace unallocated; a call needing more than the array holds, and a call while per-kernel
 profiling is on, fail with a message before launching anything."""
 import numpy as np
 import pytest
@@ -20,6 +21,10 @@ def _call(ctx, fn, layer, T, x, lg, flags, E, K, H):
     idx = ctx.empty((T, K), np.int32)
     wt = ctx.empty((T, K), np.float32)
     pr = ctx.empty((T, E), np.float32)
+    # the same preset contents for both entry points (a dense layer leaves
+    # the routing outputs as they were)
+    for b, n in ((idx, T * K), (wt, T * K), (pr, T * E)):
+        ctx.fill(b, n, mlamoe.MM_FILL_F32_UNIFORM, 7)
     mlamoe._check(getattr(L, fn)(ctx.h, layer, T, x.ptr, out.ptr, lg.ptr if lg is not None else None,
                                  idx.ptr, wt.ptr, pr.ptr, flags))
     res = (out.download(), idx.download(), wt.download(), pr.download())
@@ -28,19 +33,28 @@ def _call(ctx, fn, layer, T, x, lg, flags, E, K, H):
 
 
 def _compare(ctx, layer, xs, lgs, flags, E, K, H):
-    """Both entry points on each (x, logits) in turn; the no-allocation one
-    is called back to back, the regular one between (it may grow its own
-    workspace, the scratch array is untouched by it)."""
+    """Both entry points on each (x, logits) in turn, the no-allocation one
+    first: on a fresh context it must leave the context's growable
+    workspace unallocated (the property itself, not only equal results),
+    and it never changes the workspace's size; the regular one then runs
+    (it may grow its workspace; the scratch array is untouched by it)."""
     for x, lg in zip(xs, lgs):
         T = x.shape[0]
         print(f"noalloc T={T} flags={flags}", flush=True)
         dx = ctx.to_device(x)
         dl = ctx.to_device(lg) if lg is not None else None
-        a = _call(ctx, "mm_moe_forward_dev", layer, T, dx, dl, flags, E, K, H)
+        ws0 = ctx.workspace_bytes()
         b = _call(ctx, "mm_moe_forward_noalloc_dev", layer, T, dx, dl, flags, E, K, H)
+        assert ctx.workspace_bytes() == ws0
+        a = _call(ctx, "mm_moe_forward_dev", layer, T, dx, dl, flags, E, K, H)
         for u, v in zip(a, b):
             assert np.array_equal(u, v)
         ctx._tmp((dx,) + ((dl,) if dl is not None else ()))
+
+
+def _fresh(ctx):
+    """A context that has not run a forward call holds no workspace."""
+    assert ctx.workspace_bytes() == 0
 
 
 def test_noalloc_int8_decode_dsv2():
@@ -50,6 +64,7 @@ def test_noalloc_int8_decode_dsv2():
     with mlamoe.Context(0) as ctx:
         ctx.moe_init(H, E, NS, K, I)
         ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8)
+        _fresh(ctx)
         xs = [synth.activations(401, 64, H), synth.activations(402, 9, H)]
         lgs = [synth.uniform_logits(403, 64, E), synth.uniform_logits(404, 9, E)]
         _compare(ctx, 0, xs, lgs, mlamoe.MM_FWD_INT8, E, K, H)
@@ -77,6 +92,7 @@ def test_noalloc_int8_tiled(monkeypatch):
     with mlamoe.Context(0) as ctx:
         ctx.moe_init(H, E, NS, K, I)
         ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8)
+        _fresh(ctx)
         xs = [synth.activations(411, 300, H), synth.activations(412, 7, H)]
         _compare(ctx, 0, xs, [None, None], mlamoe.MM_FWD_INT8, E, K, H)
 
@@ -87,5 +103,21 @@ def test_noalloc_bf16():
     with mlamoe.Context(0) as ctx:
         ctx.moe_init(H, E, NS, K, I)
         ctx.moe_load_layer(0, w, mlamoe.MM_LOAD_BF16)
+        _fresh(ctx)
         xs = [synth.activations(421, 11, H), synth.activations(422, 2, H)]
+        _compare(ctx, 0, xs, [None, None], mlamoe.MM_FWD_BF16, E, K, H)
+
+
+def test_noalloc_dense_layer():
+    """A dense SwiGLU layer (the reference's first_k_dense layers) through
+    the no-allocation entry point: the GEMV (2 rows) and the skinny GEMM
+    (40 rows) with their split partials in the scratch array."""
+    H, E, K, I, NS, DI = 256, 16, 4, 128, 2, 512
+    r = np.random.default_rng(430)
+    with mlamoe.Context(0) as ctx:
+        ctx.moe_init(H, E, NS, K, I)
+        ctx.moe_load_dense_layer(0, synth.normal_bf16(r, (DI, H)), synth.normal_bf16(r, (DI, H)),
+                                 synth.normal_bf16(r, (H, DI)))
+        _fresh(ctx)
+        xs = [synth.activations(431, 40, H), synth.activations(432, 2, H)]
         _compare(ctx, 0, xs, [None, None], mlamoe.MM_FWD_BF16, E, K, H)
