@@ -197,17 +197,17 @@ def bench_prefill_i8(ctx, steps, warmup, T=2048):
     ms, wall = timed(ctx, step, steps, warmup)
     ii = idx.download()
     counts = np.bincount(ii.ravel(), minlength=E)
-    names = ["mm_router", "mm_i8_route", "mm_i8_gemm_bt", "mm_i8_quant_h", "mm_i8_combine"]
+    names = ["mm_router", "mm_i8_route", "mm_i8_gemm_gu", "mm_i8_quant_h", "mm_i8_gemm_dn",
+             "mm_i8_combine"]
     psteps = max(2, steps // 4)
     prof = profile_kernels(ctx, step, psteps, names)
-    gk = "mm_i8_gemm_bt"
+    gk = "mm_i8_gemm_gu"
     R = T * K
     gu_ops = 2.0 * R * 2 * I * H + 2.0 * T * 2 * S * H
     dn_ops = 2.0 * R * H * I + 2.0 * T * H * S
-    # grouped GEMM time per layer: mm_i8_gemm_bt runs twice (gate/up, down;
-    # routed and shared experts in one launch each)
-    launches = prof[gk][1] / psteps
-    gemm_ms = prof[gk][0] * launches
+    # grouped GEMM time per layer: one gate/up and one down launch (routed
+    # and shared experts in one launch each)
+    gemm_ms = prof["mm_i8_gemm_gu"][0] + prof["mm_i8_gemm_dn"][0]
     res = dict(
         ms_per_step=ms, wall_ms_per_step=wall, tok_s=T / (ms * 1e-3),
         layer_tops=(gu_ops + dn_ops) / (ms * 1e-3) / 1e12,
@@ -215,12 +215,15 @@ def bench_prefill_i8(ctx, steps, warmup, T=2048):
         expert_rows_max=int(counts.max()), expert_rows_min=int(counts.min()),
         experts_touched=int((counts > 0).sum()),
         kernels_us={n: round(v[0] * 1e3, 2) for n, v in prof.items()},
-        roofline=dict(bound="mfma", kernel=f"{gk} ({launches:.0f} launches per layer)",
+        gemm_tops_gu=gu_ops / (prof["mm_i8_gemm_gu"][0] * 1e-3) / 1e12,
+        gemm_tops_dn=dn_ops / (prof["mm_i8_gemm_dn"][0] * 1e-3) / 1e12,
+        roofline=dict(bound="mfma", kernel="mm_i8_gemm_gu + mm_i8_gemm_dn (one launch each "
+                      "per layer)",
                       achieved=(gu_ops + dn_ops) / (gemm_ms * 1e-3) / 1e12,
                       peak=INT8_PEAK_TOPS, unit="TOPS", ops_per_layer=gu_ops + dn_ops,
-                      avg_launch_us=prof[gk][0] * 1e3))
+                      avg_launch_us=gemm_ms * 1e3 / 2))
     res["roofline"]["frac"] = res["roofline"]["achieved"] / INT8_PEAK_TOPS
-    res["roofline"]["traffic"] = traffic_from_profiles(gk, "prefill_i8")
+    res["roofline"]["traffic"] = traffic_from_profiles("mm_i8_gemm", "prefill_i8")
     return res
 
 

@@ -50,8 +50,10 @@ static const struct {
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},
     [K_I8_COMBINE_NORM] = {"mm_i8_combine_norm", MOD_MOE_I8},
     [K_PACK_I8] = {"mm_pack_i8", MOD_MOE_I8},
-    [K_I8_BT] = {"mm_i8_gemm_bt", MOD_GEMM_I8},
-    [K_I8_BT_DBG] = {"mm_i8_gemm_bt_dbg", MOD_GEMM_I8},
+    [K_I8_BT_GU] = {"mm_i8_gemm_gu", MOD_GEMM_I8},
+    [K_I8_BT_DN] = {"mm_i8_gemm_dn", MOD_GEMM_I8},
+    [K_I8_BT_GU_DBG] = {"mm_i8_gemm_gu_dbg", MOD_GEMM_I8},
+    [K_I8_BT_DN_DBG] = {"mm_i8_gemm_dn_dbg", MOD_GEMM_I8},
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ROPE_QPREP] = {"mm_mla_rope_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},

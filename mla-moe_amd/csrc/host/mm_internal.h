@@ -27,8 +27,10 @@ typedef enum {
     K_I8_COMBINE,
     K_I8_COMBINE_NORM,
     K_PACK_I8,
-    K_I8_BT,
-    K_I8_BT_DBG,
+    K_I8_BT_GU,
+    K_I8_BT_DN,
+    K_I8_BT_GU_DBG,
+    K_I8_BT_DN_DBG,
     K_MLA_QPREP,
     K_MLA_ROPE_QPREP,
     K_MLA_ATTN,

@@ -565,7 +565,9 @@ static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled
     ba.seg[0] = *ta;
     if (ts) ba.seg[1] = *ts;
     ba.nseg = ts ? 2 : 1;
-    return mm_launch(c, ta->dbg_acc ? K_I8_BT_DBG : K_I8_BT, MM_I8B_GRID, 1, 1, 256, 0, &ba);
+    const mm_kernel_id k = ta->gu ? (ta->dbg_acc ? K_I8_BT_GU_DBG : K_I8_BT_GU)
+                                  : (ta->dbg_acc ? K_I8_BT_DN_DBG : K_I8_BT_DN);
+    return mm_launch(c, k, MM_I8B_GRID, 1, 1, 256, 0, &ba);
 }
 
 /* A tiled call that fails after its routing launch leaves rows counted in

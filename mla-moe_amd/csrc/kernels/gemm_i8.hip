@@ -52,21 +52,56 @@ __device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-#define BT_A_BYTES (MM_I8B_BM * 64)
-#define BT_P 2                   /* stages issued ahead of the one consumed */
-#define BT_NS (BT_P + 1)         /* ring slots: A rows in LDS, B operands in registers */
-#define BT_LPS 6                 /* loads per wave per stage: 2 of A, 4 of B */
+#define BT_KB 128                /* K bytes per A stage: whole 128-byte lines of every A row */
+#define BT_A_BYTES (MM_I8B_BM * BT_KB)
+#define BT_NSA 2                 /* A ring (LDS): one stage in flight, one consumed */
+#define BT_NSB 3                 /* B ring (registers): 64-byte K steps, two in flight */
+#define BT_LB 4                  /* B loads per wave per 64-byte K step */
+#define BT_NST_GU 16             /* epilogue stores per wave: gate/up, plain */
+#define BT_NST_PLAIN 32
 static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
-static_assert(BT_P >= 1 && BT_P <= 3, "the vmcnt waits of the K loop count up to two later stages");
+
+/* s_waitcnt vmcnt(n) for a wave-uniform n, a multiple of 4 below 64 (the
+ * instruction takes the count as an immediate) */
+__device__ __forceinline__ void vmcnt_wait_rt(int n) {
+    switch (__builtin_amdgcn_readfirstlane(n) >> 2) {
+    case 0: VMCNT_WAIT(0); break;
+    case 1: VMCNT_WAIT(4); break;
+    case 2: VMCNT_WAIT(8); break;
+    case 3: VMCNT_WAIT(12); break;
+    case 4: VMCNT_WAIT(16); break;
+    case 5: VMCNT_WAIT(20); break;
+    case 6: VMCNT_WAIT(24); break;
+    case 7: VMCNT_WAIT(28); break;
+    case 8: VMCNT_WAIT(32); break;
+    case 9: VMCNT_WAIT(36); break;
+    case 10: VMCNT_WAIT(40); break;
+    case 11: VMCNT_WAIT(44); break;
+    default: VMCNT_WAIT(0); break;
+    }
+}
+
+/* Epilogue staging: per wave one 32 x 32 fp32 tile, rows of BT_EP_LD floats */
+#define BT_EP_LD 36
+
+/* ds_write_b128 of an f32x4 at an LDS byte address, and the wait for the
+ * wave's outstanding LDS operations (the staging round trip is one wave's
+ * own rows: no barrier) */
+__device__ __forceinline__ void ds_write16(uint32_t addr, f32x4 v) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 
 /* registers 4 g .. 4 g + 3 of an accumulator */
 __device__ __forceinline__ i32x4 acc4(const v16i &c, int g) {
     return (i32x4){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
 }
 
-/* position of 16-byte chunk q of staged A row R (64 bytes per row): q ^ swz64(R);
- * any 16 consecutive rows then cover all 64 banks once for a fixed q */
-__device__ __forceinline__ int swz64(int R) { return (R >> 2) & 3; }
+/* position of 16-byte chunk q of staged A row R (128 bytes per row): q ^ swz128(R).
+ * A ds_read_b128 serves 16 lanes per cycle: rows R .. R + 15 at one chunk q
+ * then fall on 16 distinct 16-byte bank groups (the row's parity picks the
+ * half of the 256-byte bank space, swz128 the group within it). */
+__device__ __forceinline__ int swz128(int R) { return (R >> 1) & 7; }
 
 /* s_waitcnt lgkmcnt(0), tied to the operand registers it makes valid */
 template <int N>
@@ -150,7 +185,7 @@ struct bt_xcd_list {
 };
 
 template <bool GU, bool DBG>
-__device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_shared &sh,
+__device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, float *ep, bt_shared &sh,
                                        const bt_xcd_list &xl, int t, int t_step) {
     const int t_end = xl.len;
     const int tid = threadIdx.x, lane = tid & (MM_WAVE - 1);
@@ -160,18 +195,23 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
     constexpr int NT = GU ? 1 : 2;          /* output column tiles of 32 per wave */
 
     /* ---- load parameters of the tile whose stages are being issued ----
-     * A (DMA into LDS): wave w issues instructions 2 w, 2 w + 1 of a stage
-     * (16 rows x 64 B each); lane l carries row R = 16 i + l / 4 and stores
-     * at position l % 4 of the row's 64 B the chunk (l % 4) ^ swz64(R).
-     * B (into registers): column tile cj, K step ks of the stage: lane l
-     * reads column l % 32 of the tile, K chunk 2 ks + l / 32: the 16 bytes at
-     * (16 (2 ks + l / 32) + l % 16) * 16 of the tile's fragment (l % 32) / 16.
-     * gate/up: the wave's column blocks are 2 w, 2 w + 1 of the slab; tile 0
-     * is their gate fragments, tile 1 their up fragments.  plain: column
-     * blocks 4 w .. 4 w + 3, tile cj = blocks 4 w + 2 cj, + 1.  Column
-     * blocks past the last are clamped (results not stored). */
-    uint32_t arow_off[2];
-    int aq[2];
+     * K advances in 64-byte steps h (one packed fragment of every column
+     * block); A is staged 128 bytes of K at a time (stage s = steps 2 s,
+     * 2 s + 1), so that every A load covers whole 128-byte cache lines.
+     * A (DMA into LDS): wave w issues instructions 4 w .. 4 w + 3 of a stage
+     * (8 rows x 128 B each); lane l carries row R = 8 i + l / 8 and stores at
+     * position l % 8 of the row's 128 B the chunk (l % 8) ^ swz128(R).  With
+     * an odd number of steps the last stage is half a stage: its A loads
+     * re-read the row's first 64 bytes (within the row; never multiplied).
+     * B (into registers): column tile cj, K half ks of step h: lane l reads
+     * column l % 32 of the tile, K chunk 2 ks + l / 32: the 16 bytes at
+     * (16 (2 ks + l / 32) + l % 16) * 16 of the tile's fragment (l % 32) / 16
+     * for K block h.  gate/up: the wave's column blocks are 2 w, 2 w + 1 of
+     * the slab; tile 0 is their gate fragments, tile 1 their up fragments.
+     * plain: column blocks 4 w .. 4 w + 3, tile cj = blocks 4 w + 2 cj, + 1.
+     * Column blocks past the last are clamped (results not stored). */
+    uint32_t arow_off[4];
+    int aq[4];
     __amdgpu_buffer_rsrc_t brs;
     const int8_t *aptr;
     uint32_t boff[2];
@@ -181,10 +221,10 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         lkb = g.Kd / 64;
         aptr = g.a;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int R = 16 * (2 * wave + h) + (lane >> 2);
+        for (int h = 0; h < 4; h++) {
+            const int R = 8 * (4 * wave + h) + (lane >> 3);
             arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd;
-            aq[h] = 16 * ((lane & 3) ^ swz64(R));
+            aq[h] = (lane & 7) ^ swz128(R);
         }
         const int ncb = g.N / 16;
         const uint32_t in_frag = (uint32_t)((16 * hi + (lane & 15)) * 16);
@@ -203,17 +243,18 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
                                                 (int)((uint32_t)((GU ? 2 : 1) * ncb * lkb) * 1024u),
                                                 0x00020000);
     };
-    /* B operands of the ring slots: [slot][column tile][K step] */
-    i32x4 bq[BT_NS][2][2];
+    /* B operands of the ring slots: [slot][column tile][K half] */
+    i32x4 bq[BT_NSB][2][2];
     auto issue_a = [&](int s, int slot) {
         const uint32_t st = (uint32_t)(slot * BT_A_BYTES);
+        const bool full = 2 * s + 1 < lkb;
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            lds_dma16(aptr + (arow_off[h] + (uint32_t)(s * 64 + aq[h])),
-                      lds + st + (2 * wave + h) * 1024);
+        for (int h = 0; h < 4; h++)
+            lds_dma16(aptr + (arow_off[h] + (uint32_t)(s * BT_KB + 16 * (full ? aq[h] : aq[h] & 3))),
+                      lds + st + (4 * wave + h) * 1024);
     };
-    auto issue_b = [&](int slot, int s) {
-        const int so = __builtin_amdgcn_readfirstlane(s * bstep);
+    auto issue_b = [&](int slot, int h) {
+        const int so = __builtin_amdgcn_readfirstlane(h * bstep);
 #pragma unroll
         for (int cj = 0; cj < 2; cj++)
 #pragma unroll
@@ -222,25 +263,27 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
                     i32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, boff[cj] + 512 * ks, so, 0));
     };
 
-    /* a tile's first BT_P stages (its last one again where it has fewer),
-     * into slots 0 .. BT_P - 1 */
+    /* a tile's head: its first two A stages and first two B steps, issued
+     * before the previous tile's epilogue stores so that the tile's first
+     * two steps wait for none of those stores */
     auto issue_head = [&]() {
-#pragma unroll
-        for (int d = 0; d < BT_P; d++) {
-            issue_a(min(d, lkb - 1), d);
-            issue_b(d, min(d, lkb - 1));
-        }
+        issue_a(0, 0);
+        issue_b(0, 0);
+        if (lkb > 1) issue_b(1, 1);
+        if (lkb > 2) issue_a(1, 1);
     };
 
-    /* A operand of row block ri, K step ks: row 32 ri + l % 32, chunk
-     * 2 ks + l / 32 (the swizzle depends on l % 32 only) */
-    uint32_t rdA[2];
+    /* A operand of row block ri, K step h, half ks: row 32 ri + l % 32,
+     * chunk 4 (h % 2) + 2 ks + l / 32 of the stage (the swizzle depends on
+     * l % 32 only) */
+    uint32_t rdA[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) rdA[ks] = l32 * 64 + 16 * ((2 * ks + hi) ^ swz64(l32));
+    for (int c = 0; c < 4; c++) rdA[c] = l32 * BT_KB + 16 * ((2 * c + hi) ^ swz128(l32));
 
     /* ---- first tile ---- */
     bt_tile_id cur = bt_decode(a, sh, xl(t));
     int buf = 0;
+    bool first = true;
     if (tid < MM_I8B_BM) {
         int rid, arow;
         bt_row(a.seg[cur.si], cur, tid, &rid, &arow);
@@ -253,7 +296,6 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
 
     for (;;) {
         const mm_i8_tiled_args &g = a.seg[cur.si];
-        const int KB = lkb;                 /* this tile's stages (set_tile(cur) was last) */
         const int tn = t + t_step;
         const bool has_next = tn < t_end;
         const bt_tile_id nxt = has_next ? bt_decode(a, sh, xl(tn)) : cur;
@@ -285,53 +327,82 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
          * padding-only blocks skip their reads and MFMAs */
         const int vrows = min(cur.M - cur.m0, MM_I8B_BM);
         const int nri = __builtin_amdgcn_readfirstlane((vrows + 31) >> 5);
-        /* step s, ring slot d = s % BT_NS.  Every step issues one stage
-         * (s + BT_P, or the tile's last one again past the end: results
-         * unused), so the loads of exactly BT_P - 1 later stages are
-         * outstanding when stage s must have landed.  On the first step of
-         * a later tile the previous tile's epilogue stores follow this
-         * tile's head stages in issue order; the same count then waits for
-         * them too (the counter completes in order), which keeps stage 0
-         * complete whatever the number of stores.  The barrier then makes
-         * every wave's A rows of stage s visible and frees slot
-         * (s - 1) % BT_NS for the stage issued. */
+        /* step h (64 bytes of K): A stage s = h / 2 in LDS slot s % 2, B in
+         * register slot h % 3.  Loads are issued in this order: the tile's
+         * head A(0), B(0), B(1), A(1), B(2); then at each even step 2 s >= 2,
+         * after its wait and barrier, A(s + 1) and B(2 s + 2); at each odd
+         * step h, B(h + 2).  The vmcnt counter completes in issue order, so a
+         * step waits until only the operations issued after the loads it
+         * needs are outstanding: even step 2 s >= 2 needs A(s) and B(2 s),
+         * after which only B(2 s + 1) was issued (BT_LB loads); odd step
+         * 2 s + 1 >= 3 needs B(2 s + 1), after which A(s + 1) and B(2 s + 2)
+         * were issued (2 BT_LB).  The tile's head is A(0), B(0), B(1), A(1),
+         * followed on a later tile by the previous tile's epilogue stores
+         * (exactly NST per wave); step 0 issues B(2).  Steps 0 and 1 need
+         * head loads issued before the stores, which may stay outstanding
+         * until step 2.  Near the end of the tile
+         * fewer loads follow, and the counts shrink accordingly (0: wait for
+         * all).  The barrier of an even step makes every wave's A rows of
+         * stage s visible and frees slot (s + 1) % 2, read by every wave
+         * during steps 2 s - 2 and 2 s - 1 (or by the previous tile). */
+        constexpr int NST = GU ? BT_NST_GU : BT_NST_PLAIN;
+        const int nst = first ? 0 : NST;
         auto kloop = [&](auto nri_c) {
             constexpr int NRI = decltype(nri_c)::value;
-            auto kstep = [&](int d, int s) {
-                VMCNT_WAIT((BT_P - 1) * BT_LPS);
-                __builtin_amdgcn_s_barrier();
+            auto kstep = [&](auto d_c, int h) {
+                constexpr int D = decltype(d_c)::value;     /* h % 6 */
+                constexpr int J = D & 1, SB = D % BT_NSB;
+                const int sa_slot = (h >> 1) & 1;
+                const bool more = h + 1 < lkb;
+                if (h == 0) vmcnt_wait_rt(4 * (lkb > 1) + 4 * (lkb > 2) + nst);
+                else if (h == 1) vmcnt_wait_rt(8 * (lkb > 2) + nst);
+                else if (J == 0) {
+                    if (more) VMCNT_WAIT(BT_LB); else VMCNT_WAIT(0);
+                } else {
+                    if (more) VMCNT_WAIT(2 * BT_LB); else VMCNT_WAIT(0);
+                }
+                if (J == 0) __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                const int sn = min(s + BT_P, KB - 1);
-                issue_a(sn, (s + BT_P) % BT_NS);
-                issue_b((d + BT_P) % BT_NS, sn);
+                /* A(1) is part of the head */
+                if (J == 0 && h > 0 && h + 2 < lkb) issue_a((h >> 1) + 1, sa_slot ^ 1);
+                if (h + 2 < lkb) issue_b((D + 2) % BT_NSB, h + 2);
                 __builtin_amdgcn_sched_barrier(0);
-                const uint32_t sb = lds0 + (uint32_t)((s % BT_NS) * BT_A_BYTES);
+                const uint32_t sb = lds0 + (uint32_t)(sa_slot * BT_A_BYTES);
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
                     i32x4 A[NRI];
 #pragma unroll
-                    for (int ri = 0; ri < NRI; ri++) A[ri] = ds_read16(sb + rdA[ks], ri * 2048);
+                    for (int ri = 0; ri < NRI; ri++)
+                        A[ri] = ds_read16(sb + rdA[2 * J + ks], ri * 32 * BT_KB);
                     lds_wait_regs(A);
 #pragma unroll
                     for (int ri = 0; ri < NRI; ri++)
 #pragma unroll
                         for (int cj = 0; cj < 2; cj++)
-                            acc[ri][cj] = mfma32_i8(bq[d][cj][ks], A[ri], acc[ri][cj]);
+                            acc[ri][cj] = mfma32_i8(bq[SB][cj][ks], A[ri], acc[ri][cj]);
                 }
             };
-            int s0 = 0;
-            for (; s0 + BT_NS <= KB; s0 += BT_NS) {
-#pragma unroll
-                for (int d = 0; d < BT_NS; d++) kstep(d, s0 + d);
+            using std::integral_constant;
+            int h0 = 0;
+            for (; h0 + 6 <= lkb; h0 += 6) {
+                kstep(integral_constant<int, 0>(), h0);
+                kstep(integral_constant<int, 1>(), h0 + 1);
+                kstep(integral_constant<int, 2>(), h0 + 2);
+                kstep(integral_constant<int, 3>(), h0 + 3);
+                kstep(integral_constant<int, 4>(), h0 + 4);
+                kstep(integral_constant<int, 5>(), h0 + 5);
             }
-#pragma unroll
-            for (int d = 0; d < BT_NS; d++)
-                if (s0 + d < KB) kstep(d, s0 + d);
+            if (h0 < lkb) kstep(integral_constant<int, 0>(), h0);
+            if (h0 + 1 < lkb) kstep(integral_constant<int, 1>(), h0 + 1);
+            if (h0 + 2 < lkb) kstep(integral_constant<int, 2>(), h0 + 2);
+            if (h0 + 3 < lkb) kstep(integral_constant<int, 3>(), h0 + 3);
+            if (h0 + 4 < lkb) kstep(integral_constant<int, 4>(), h0 + 4);
         };
         if (nri >= 4) kloop(std::integral_constant<int, 4>());
         else if (nri == 3) kloop(std::integral_constant<int, 3>());
         else if (nri == 2) kloop(std::integral_constant<int, 2>());
         else kloop(std::integral_constant<int, 1>());
+        first = false;
         VMCNT_WAIT(0);
 
         /* row tables: this tile's scales, the next tile's rows */
@@ -342,7 +413,8 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
         }
         sh.cs[buf][tid] = cs_r;
         __syncthreads();
-        /* the next tile's head stages go out before this tile's stores */
+        /* the next tile's head goes out before this tile's stores (its third
+         * B step after them) */
         if (has_next) {
             set_tile(nxt, buf ^ 1);
             issue_head();
@@ -350,48 +422,75 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
 
         /* ---- epilogue ----
          * accumulator register 4 g + i of lane l is row 32 ri + l % 32,
-         * column 8 g + 4 (l / 32) + i of the wave's 32-column tile cj
-         * (gate/up: slab columns 32 w .., tile 0 gate, tile 1 up; plain:
-         * slab columns 64 w + 32 cj ..).  One 16-byte store per (ri, tile,
-         * g); stores are unconditional (exactly 16 NT per wave): padded rows
-         * and columns past N go to the spare row of `out`. */
+         * column 8 g + 4 (l / 32) + i of the wave's 32-column tile q
+         * (gate/up: slab columns 32 w .., tile 0 gate, tile 1 up, one output
+         * tile; plain: slab columns 64 w + 32 q ..).  Each 32 x 32 output
+         * tile goes through the wave's own LDS staging rows (row stride 36
+         * floats: both access patterns below are free of bank conflicts
+         * but for one pair of lanes), written as the MFMA left it and read
+         * back row-major, so that each 16-byte store instruction writes 8
+         * whole 128-byte rows instead of 32-byte pieces of 32 rows (L2
+         * requests, not bytes, bound this kernel).  Stores are unconditional
+         * (exactly NST per wave): padded rows and columns past N go to the
+         * spare row of `out`. */
         float *out = g.out;
         const size_t spare = (size_t)g.spare_row * N;
+        float *stg = ep + wave * (32 * BT_EP_LD);
+        const uint32_t stg_w = lds_addr(stg) + (uint32_t)(l32 * BT_EP_LD + 4 * hi) * 4;
+        const int er = lane >> 3, ec = 4 * (lane & 7);      /* read back: row er + 8 k, columns ec .. */
+        const uint32_t stg_r = lds_addr(stg) + (uint32_t)(er * BT_EP_LD + ec) * 4;
         {
             int32_t *dbg = g.dbg_acc;
 #pragma unroll
             for (int ri = 0; ri < 4; ri++) {
-                const int rid = sh.rid[buf][32 * ri + l32];
                 const float sa = sh.sa[buf][32 * ri + l32];
 #pragma unroll
                 for (int q = 0; q < NT; q++) {
+                    const int ct = (GU ? 32 * wave : 64 * wave + 32 * q);   /* tile's first slab column */
 #pragma unroll
                     for (int gq = 0; gq < 4; gq++) {
-                        const int cl = (GU ? 32 * wave : 64 * wave + 32 * q) + 8 * gq + 4 * hi;
-                        const int col = slab_c0 + cl;
-                        const bool ok = rid >= 0 && col < N;
-                        const size_t o = ok ? (size_t)rid * N + col : spare + col;
+                        const int cl = ct + 8 * gq + 4 * hi;
                         const f32x4 c0 = *(const f32x4 *)(&sh.cs[buf][cl]);
                         f32x4 v;
                         if (GU) {
                             const f32x4 c1 = *(const f32x4 *)(&sh.cs[buf][128 + cl]);
 #pragma unroll
                             for (int i = 0; i < 4; i++)
-                                v[i] = silu_mul(((float)acc[ri][0][4 * gq + i] * sa) * c0[i],
-                                                ((float)acc[ri][1][4 * gq + i] * sa) * c1[i]);
-                            if (DBG && dbg && ok) {
-                                int32_t *d = dbg + ((size_t)rid * 2) * N + col;
-                                *(i32x4 *)d = acc4(acc[ri][0], gq);
-                                *(i32x4 *)(d + N) = acc4(acc[ri][1], gq);
+                                v[i] = silu_mul_fast(((float)acc[ri][0][4 * gq + i] * sa) * c0[i],
+                                                     ((float)acc[ri][1][4 * gq + i] * sa) * c1[i]);
+                            if (DBG && dbg) {
+                                const int rid = sh.rid[buf][32 * ri + l32], col = slab_c0 + cl;
+                                if (rid >= 0 && col < N) {
+                                    int32_t *d = dbg + ((size_t)rid * 2) * N + col;
+                                    *(i32x4 *)d = acc4(acc[ri][0], gq);
+                                    *(i32x4 *)(d + N) = acc4(acc[ri][1], gq);
+                                }
                             }
                         } else {
 #pragma unroll
                             for (int i = 0; i < 4; i++) v[i] = ((float)acc[ri][q][4 * gq + i] * sa) * c0[i];
-                            if (DBG && dbg && ok)
-                                *(i32x4 *)(dbg + (size_t)rid * N + col) = acc4(acc[ri][q], gq);
+                            if (DBG && dbg) {
+                                const int rid = sh.rid[buf][32 * ri + l32], col = slab_c0 + cl;
+                                if (rid >= 0 && col < N)
+                                    *(i32x4 *)(dbg + (size_t)rid * N + col) = acc4(acc[ri][q], gq);
+                            }
                         }
-                        *(f32x4 *)(out + o) = v;
+                        ds_write16(stg_w + 32 * gq, v);
                     }
+                    lds_wait();
+                    i32x4 rv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) rv[k] = ds_read16(stg_r, 8 * k * BT_EP_LD * 4);
+                    lds_wait_regs(rv);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const f32x4 v = __builtin_bit_cast(f32x4, rv[k]);
+                        const int rid = sh.rid[buf][32 * ri + 8 * k + er];
+                        const int col = slab_c0 + ct + ec;
+                        const bool ok = rid >= 0 && col < N;
+                        *(f32x4 *)(out + (ok ? (size_t)rid * N + col : spare + col)) = v;
+                    }
+                    lds_wait();
                 }
             }
         }
@@ -409,9 +508,10 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, bt_s
  * those tiles in turn, so the blocks of one XCD work on neighbouring tiles at
  * the same time: row groups of the same expert and slab, whose weights then
  * come from HBM once and from that XCD's L2 for the others. */
-template <bool DBG>
+template <bool GU, bool DBG>
 __device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NS * BT_A_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t lds[BT_NSA * BT_A_BYTES];
+    __shared__ __attribute__((aligned(16))) float ep[4 * 32 * BT_EP_LD];
     __shared__ bt_shared sh;
     const mm_i8_tiled_args &g0 = a.seg[0];
     const int E = g0.cnt ? g0.E : 1;
@@ -450,20 +550,25 @@ __device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
     xl.lo1 = n0 + n1 * xcd / MM_I8S_XCD;
     xl.len = xl.len0 + n0 + n1 * (xcd + 1) / MM_I8S_XCD - xl.lo1;
     if (j >= xl.len) return;
-    if (g0.gu)
-        bt_run<true, DBG>(a, lds, sh, xl, j, nbx);
-    else
-        bt_run<false, DBG>(a, lds, sh, xl, j, nbx);
+    bt_run<GU, DBG>(a, lds, ep, sh, xl, j, nbx);
 }
 
-extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt(mm_i8_bt_args a) {
-    bt_kernel<false>(a);
+/* One kernel per epilogue form, so that each holds only its own code:
+ * gate/up (SwiGLU, segments' gu = 1) and down (plain dequantisation). */
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_gu(mm_i8_bt_args a) {
+    bt_kernel<true, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_dn(mm_i8_bt_args a) {
+    bt_kernel<false, false>(a);
 }
 
-/* As mm_i8_gemm_bt, also writing the raw accumulators of each segment whose
- * dbg_acc is set (the shared segment's is not); debug entry point only: a
- * kernel of its own keeps these stores and their registers out of the
- * product kernel. */
-extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_bt_dbg(mm_i8_bt_args a) {
-    bt_kernel<true>(a);
+/* As mm_i8_gemm_gu / _dn, also writing the raw accumulators of each segment
+ * whose dbg_acc is set (the shared segment's is not); debug entry points
+ * only: kernels of their own keep these stores and their registers out of
+ * the product kernels. */
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_gu_dbg(mm_i8_bt_args a) {
+    bt_kernel<true, true>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 2) void mm_i8_gemm_dn_dbg(mm_i8_bt_args a) {
+    bt_kernel<false, true>(a);
 }

@@ -117,6 +117,13 @@ def test_i8_no_shared_expert(ctx, oracle):
     run_case(ctx, oracle, 128, 8, 2, 64, 0, 9, 62)
 
 
+def test_i8_odd_k_blocks(ctx, oracle):
+    """Reduction lengths of an odd number of 64-byte K blocks (H = 192:
+    three; I = S = 320: five): the tiled GEMM's last 128-byte stage is half
+    a stage."""
+    run_case(ctx, oracle, 192, 16, 4, 320, 1, 37, 63)
+
+
 def test_i8_dsv2_decode_batch(ctx, oracle):
     """DeepSeek-V2-Lite shape, batched decode with given uniform logits
     (config 4's routing), T = 16 (routed and shared accumulators checked on
