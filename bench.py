@@ -519,7 +519,7 @@ def cpu_baseline_decode(B=64, seconds_hint=True):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
     log("[cpu_baseline] generating one host layer")
-    w = synth.moe_layer(9001, H, E, I, NS)
+    w = _host_layer()
     rng = np.random.default_rng(9002)
     x = synth.normal_f32(rng, (B, H))
     lg = synth.uniform_logits(9003, B, E)
@@ -534,6 +534,72 @@ def cpu_baseline_decode(B=64, seconds_hint=True):
                 sample=f"{B} tokens x 1 of 26 layers ({dt:.1f} s single-threaded, "
                        f"x26 for a step); oracle ffn_compute on bf16 experts",
                 cpu=_cpu_name(), nproc=os.cpu_count())
+
+
+_HOST_LAYER = []
+
+
+def _host_layer():
+    """One DeepSeek-V2-Lite-shaped bf16 host layer for the CPU timings
+    (generated once per run)."""
+    if not _HOST_LAYER:
+        _HOST_LAYER.append(synth.moe_layer(9001, H, E, I, NS))
+    return _HOST_LAYER[0]
+
+
+def _median_timed(fn, reps):
+    """run.c:548-608's convention: rep 0 is a warm-up, the median of the rest."""
+    ts = []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        fn()
+        if r:
+            ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baselines_extra():
+    """CPU timings beside configs 1 and 3 and the scalar int8 oracle on its
+    own (BASELINE's plan), single-threaded, bounded samples:
+    config 1: one token through one bf16 layer (oracle ffn_compute);
+    config 3: 16 tokens of the Zipf-routed T = 2048 prefill through the
+    bf16 reference path (what the reference executes for this layer) and
+    through the scalar int8 oracle, each scaled x128 to the 2048 tokens
+    (tokens are independent in ffn_compute); config 4: the int8 oracle on
+    16 of the 64 tokens of one layer, x4 x26 for a step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    log("[cpu_baseline] configs 1 and 3, int8 oracle")
+    w = _host_layer()
+    qw = pyoracle.quantize_moe_weights(w)
+    cfg = pyoracle.moe_cfg(H, E, NS, K, I)
+    common = dict(cores=1, cpu=_cpu_name(), nproc=os.cpu_count())
+    x1 = synth.activations(9102, 1, H)
+    t1 = _median_timed(lambda: pyoracle.ffn_compute_rows(cfg, w, x1), 3)
+    c1 = dict(value=1.0 / t1, unit="tok/s", kind="port", ms_per_token=t1 * 1e3,
+              sample="1 token x 1 layer, median of 3 after a warm-up; oracle ffn_compute "
+                     "on bf16 experts", **common)
+    n3 = 16
+    x3 = synth.activations(9103, n3, H)
+    lg3 = pyoracle.matmul(x3, w["moe_gate"]) + synth.zipf_prior(9104, E, 1.1)[None, :]
+    t3 = _median_timed(lambda: pyoracle.ffn_compute_rows(cfg, w, x3, lg3), 1)
+    t3i = _median_timed(lambda: pyoracle.ffn_i8(cfg, w, qw, x3, lg3), 1)
+    scale = 2048 / n3
+    c3 = dict(value=2048 / (t3 * scale), unit="tok/s", kind="port", ms_per_layer=t3 * scale * 1e3,
+              sample=f"{n3} of the 2048 Zipf-routed tokens x 1 layer, x{scale:.0f}; oracle "
+                     "ffn_compute on bf16 experts (the reference's path)",
+              int8_oracle=dict(value=2048 / (t3i * scale), unit="tok/s",
+                               ms_per_layer=t3i * scale * 1e3,
+                               sample=f"the same {n3} tokens through the scalar int8 oracle "
+                                      "(or_ffn_i8: int8 quantisation, exact int32 dots)"),
+              **common)
+    x4 = synth.activations(9105, 16, H)
+    lg4 = synth.uniform_logits(9106, 16, E)
+    t4i = _median_timed(lambda: pyoracle.ffn_i8(cfg, w, qw, x4, lg4), 1)
+    c4 = dict(value=64 / (t4i * 4 * 26), unit="tok/s", kind="port", cores=1,
+              sample="16 of the 64 tokens x 1 of 26 layers through the scalar int8 oracle, "
+                     "x4 x26 for a step")
+    return c1, c3, c4
 
 
 def _cpu_name():
@@ -610,6 +676,11 @@ def main():
         extra["engine_dsv2"] = bench_engine(args.steps, args.warmup)
     roof = dec.pop("roofline")
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
+    if not args.no_cpu_baseline and not args.no_extra:
+        c1, c3, c4 = cpu_baselines_extra()
+        extra["decode_bf16_config1"]["cpu_baseline"] = c1
+        extra["prefill_i8_config3"]["cpu_baseline"] = c3
+        cpu["int8_oracle"] = c4
     line = {
         "metric": METRIC,
         "value": round(dec["tok_s"], 1),

@@ -45,6 +45,7 @@ static const struct {
     [K_QUANT_W] = {"mm_quant_weight", MOD_UTIL},
     [K_I8_ROUTE] = {"mm_i8_route", MOD_MOE_I8},
     [K_I8_GU] = {"mm_i8_gu", MOD_MOE_I8},
+    [K_I8_GU_KS] = {"mm_i8_gu_ks", MOD_MOE_I8},
     [K_I8_QUANT_H] = {"mm_i8_quant_h", MOD_MOE_I8},
     [K_I8_DOWN] = {"mm_i8_down", MOD_MOE_I8},
     [K_I8_COMBINE] = {"mm_i8_combine", MOD_MOE_I8},

@@ -22,6 +22,7 @@ typedef enum {
     K_QUANT_W,
     K_I8_ROUTE,
     K_I8_GU,
+    K_I8_GU_KS,
     K_I8_QUANT_H,
     K_I8_DOWN,
     K_I8_COMBINE,

@@ -700,7 +700,7 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                                        rrows * ceil_div(I / 16, per_blk));
         /* dynamic LDS: the 16-row A tile (16 * K bytes), the row list, the
          * K split's partials */
-        FAIL_ROUTED(mm_launch(c, K_I8_GU, nb, 1, 1, 64 * MM_I8S_W,
+        FAIL_ROUTED(mm_launch(c, ga.ksplit ? K_I8_GU_KS : K_I8_GU, nb, 1, 1, 64 * MM_I8S_W,
                               16 * H + al16(4 * (size_t)T) + (ga.ksplit ? KSPLIT_RED(2) : 0), &ga));
     }
 

@@ -445,8 +445,9 @@ static_assert(MM_I8S_SEG == 1, "the K split serves one column block per block");
 /* Expert of routed block row u: expert u, or with the K split (grid over
  * route slots, T * K of them) the expert of slot u unless an earlier slot
  * names it too (-1: that block has nothing to do). */
+template <bool KS>
 __device__ __forceinline__ int routed_expert(const mm_i8_gemm_args &a, int u) {
-    if (!a.ksplit) return u;
+    if (!KS) return u;
     const int e = a.topk[u];
     for (int j = 0; j < u; j++)
         if (a.topk[j] == e) return -1;
@@ -459,12 +460,13 @@ __device__ __forceinline__ int routed_expert(const mm_i8_gemm_args &a, int u) {
  * that their work starts early; a routed block of an expert with no rows
  * exits at once.  Dynamic LDS: 16 * H bytes (the A tile), then T ints (the
  * expert's row list). */
-extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
+template <bool KS>
+__device__ __forceinline__ void i8_gu(const mm_i8_gemm_args &a) {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds_a[];
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int KB = a.H / 64;
-    const int gs = units_per_wave_group(a.S / 16, a.ksplit);
+    const int gs = units_per_wave_group(a.S / 16, KS);
     const int n_sh = a.S ? (gs + MM_I8S_XCD - 1) / MM_I8S_XCD * MM_I8S_XCD * MM_I8S_RT : 0;
     const int b = blockIdx.x;
     const int8_t *bbase;
@@ -491,8 +493,8 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
         kdiv = 1;
     } else {
         nbl = a.I / 16;
-        G = units_per_wave_group(nbl, a.ksplit);
-        const int v = b - n_sh, e = routed_expert(a, v / G);
+        G = units_per_wave_group(nbl, KS);
+        const int v = b - n_sh, e = routed_expert<KS>(a, v / G);
         if (e < 0) return;
         g = v % G;
         int *list = (int *)(lds_a + 16 * a.H);
@@ -511,13 +513,13 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
     if (m0 >= M) return;   /* whole block: a shared row tile past T */
     const int ncols = nbl * 16;
     /* this wave's first column block (K split: the block's one) */
-    const int nb0 = a.ksplit ? g : (g + G * wave) * MM_I8S_SEG;
+    const int nb0 = KS ? g : (g + G * wave) * MM_I8S_SEG;
     const int nseg = max(0, min(MM_I8S_SEG, nbl - nb0));
     /* per-column scales: lane l holds column l % 16 of block nb0 + l / 16 */
     const int scol = (min(nb0 + min(lane >> 4, MM_I8S_SEG - 1), nbl - 1)) * 16 + (lane & 15);
     const float cg_all = sg[scol], cu_all = su[scol];
     int kw0 = 0, nkw = KB;                          /* this wave's K steps */
-    if (a.ksplit) ks_range(KB, wave, &kw0, &nkw);
+    if (KS) ks_range(KB, wave, &kw0, &nkw);
     const int8_t *bp = bbase + (size_t)min(nb0, nbl - 1) * 2 * KB * 1024 + (size_t)kw0 * 2048 + lane * 16;
     v4i *red = (v4i *)(lds_a + 16 * a.H + ((4 * a.T + 15) & ~15));   /* K split: [W][2][64] */
     v4i bq[MM_I8S_DEPTH_GU][2];
@@ -560,7 +562,7 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
                     }
                 }
         };
-        if (!a.ksplit) {
+        if (!KS) {
             stream_lds<true, MM_I8S_DEPTH_GU>(bp, KB, nseg, lds_addr(lds_a) + lane * 16, true, bq,
                                               finish);
             continue;
@@ -580,6 +582,17 @@ extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_
             finish(0, ag, au);
         }
     }
+}
+
+/* The gate/up GEMM in two kernels: column groups, and the K split (few
+ * tokens): the K split's partial-sum code and registers would otherwise
+ * hold every launch to fewer resident blocks (94 against 72 VGPRs: two
+ * six-wave blocks per CU instead of three). */
+extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu(mm_i8_gemm_args a) {
+    i8_gu<false>(a);
+}
+extern "C" __global__ __launch_bounds__(MM_I8S_W * MM_WAVE) void mm_i8_gu_ks(mm_i8_gemm_args a) {
+    i8_gu<true>(a);
 }
 
 /* Decode-shaped down projection, same block layout (shared blocks over the
