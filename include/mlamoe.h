@@ -103,7 +103,7 @@ MM_API int mm_prof_query(mm_ctx *ctx, const char *kernel, double *total_ms, long
 /* The MoE fields of the reference Config (include/model.h:12-42). */
 typedef struct {
     int hidden_size;        /* H */
-    int n_routed_experts;   /* E (<= 256) */
+    int n_routed_experts;   /* E (<= 1024, src/run.c:133-134) */
     int n_shared_experts;   /* shared MLP width = n_shared_experts * moe_inter_size */
     int n_experts_per_tok;  /* K (<= 16) */
     int moe_inter_size;     /* I */

@@ -85,6 +85,8 @@ static const struct {
     [K_ZERO32] = {"mm_zero32", MOD_UTIL},
     [K_GATHER_ROWS] = {"mm_gather_rows", MOD_UTIL},
     [K_F32_BF16] = {"mm_f32_bf16", MOD_UTIL},
+    [K_ROUTER_WIDE] = {"mm_router_wide", MOD_MOE_BF16},
+    [K_ROUTE_WIDE] = {"mm_route_wide", MOD_MOE_I8},
 };
 
 /* ---- errors ------------------------------------------------------------- */

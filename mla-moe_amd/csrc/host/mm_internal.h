@@ -62,6 +62,8 @@ typedef enum {
     K_ZERO32,
     K_GATHER_ROWS,
     K_F32_BF16,
+    K_ROUTER_WIDE,
+    K_ROUTE_WIDE,
     K_COUNT
 } mm_kernel_id;
 

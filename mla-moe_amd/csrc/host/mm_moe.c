@@ -42,9 +42,10 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     const int I = cfg->moe_inter_size, NS = cfg->n_shared_experts;
     if (n_layers <= 0 || H <= 0 || E <= 0 || K <= 0 || I <= 0 || NS < 0)
         return mm_fail(MM_ERR_INVALID, "mm_moe_init: non-positive dimension");
-    /* run.c:133-134 limits K <= 16 and E <= 1024; this build routes E <= 256 */
+    /* run.c:133-134 limits K <= 16 and E <= 1024 (above MM_EMAX_FAST experts
+     * the wide routers serve) */
     if (K > 16 || K > E) return mm_fail(MM_ERR_INVALID, "mm_moe_init: need K <= min(16, E)");
-    if (E > 256) return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_init: E > 256 experts");
+    if (E > MM_EMAX) return mm_fail(MM_ERR_INVALID, "mm_moe_init: E > %d experts", MM_EMAX);
     if (H % 8 || I % 8)
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_init: hidden and moe_inter must be multiples of 8");
     int st = mm_set_device(c);
@@ -437,6 +438,56 @@ static int forward_dense(mm_ctx *c, const mm_moe_layer *L, int T, const float *x
     return mm_gemm_bf16_ws(c, out, g, L->sd, H, DI, T, dflags, ws + o_ws);
 }
 
+/* ---- routing for more than MM_EMAX_FAST experts --------------------------------- */
+
+/* Logits (computed from xn into lg_buf unless given) and the wide router
+ * over all T tokens: idx, wts and probs (or NULL); with ra (int8) also the
+ * quantisation of x and the tiled path's row lists.  */
+static int route_wide(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn,
+                      const float *logits, float *lg_buf, int32_t *idx, float *wts, float *probs,
+                      const mm_i8_route_args *ra) {
+    const mm_moe_config *g = &c->moe;
+    int st;
+    if (!logits) {
+        mm_router_args la;
+        memset(&la, 0, sizeof(la));
+        la.x = xn;
+        la.wg = L->wg;
+        la.logits_out = lg_buf;
+        la.T = T;
+        la.H = g->hidden_size;
+        la.E = g->n_routed_experts;
+        la.K = g->n_experts_per_tok;
+        if ((st = mm_launch(c, K_ROUTER_WIDE, (unsigned)((T + 3) / 4),
+                            (unsigned)((la.E + 63) / 64), 1, 256, 0, &la)))
+            return st;
+        logits = lg_buf;
+    }
+    mm_route_wide_args wa;
+    memset(&wa, 0, sizeof(wa));
+    wa.r.x = xn;
+    wa.r.logits_in = logits;
+    wa.r.bias = L->bias;
+    wa.r.probs = probs;
+    wa.r.topk_idx = idx;
+    wa.r.topk_w = wts;
+    wa.r.T = T;
+    wa.r.H = g->hidden_size;
+    wa.r.E = g->n_routed_experts;
+    wa.r.K = g->n_experts_per_tok;
+    wa.r.sigmoid = g->router_sigmoid;
+    wa.r.norm_topk = g->norm_topk;
+    wa.r.scale = g->routed_scaling;
+    if (ra) {
+        wa.cnt = ra->cnt;
+        wa.rows = ra->rows;
+        wa.x = ra->x;
+        wa.qx = ra->qx;
+        wa.sx = ra->sx;
+    }
+    return mm_launch(c, K_ROUTE_WIDE, (unsigned)((T + 3) / 4), 1, 1, 256, 0, &wa);
+}
+
 /* ---- bf16 forward ------------------------------------------------------------ */
 
 /* bf16 weights, GEMV stages (kernels/moe_bf16.hip), BF16_NT_MAX tokens per pass. */
@@ -447,16 +498,24 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const int H = g->hidden_size, E = g->n_routed_experts, K = g->n_experts_per_tok;
     const int I = g->moe_inter_size, S = g->n_shared_experts * I;
     const size_t hw = (size_t)K * I + S;
+    const int wide = E > MM_EMAX_FAST;
     mm_plan p = {0};
     const size_t o_h = plan_take(&p, (size_t)BF16_NT_MAX * hw * sizeof(float));
     const size_t o_i = plan_take(&p, (size_t)T * K * sizeof(int32_t));
     const size_t o_w = plan_take(&p, (size_t)T * K * sizeof(float));
+    const size_t o_lg = plan_take(&p, wide && !logits ? (size_t)T * E * sizeof(float) : 0);
     char *ws;
     int st = take_ws(c, fx, p.off, &ws);
     if (st) return st;
     float *hcat = (float *)(ws + o_h);
     if (!idx) idx = (int32_t *)(ws + o_i);
     if (!wts) wts = (float *)(ws + o_w);
+    if (wide) {
+        /* more than MM_EMAX_FAST experts: every token routed up front by
+         * the wide routers, then the stages below without their router */
+        if ((st = route_wide(c, L, T, xn, logits, (float *)(ws + o_lg), idx, wts, probs, NULL)))
+            return st;
+    }
     for (int t0 = 0; t0 < T; t0 += BF16_NT_MAX) {
         const int Tc = T - t0 < BF16_NT_MAX ? T - t0 : BF16_NT_MAX;
         mm_gu_bf16_args a;
@@ -484,7 +543,19 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
         a.K = K;
         a.rows_per_block = GU2_ROWS_PER_BLOCK;
         a.n_blocks_per_token = (I + GU2_ROWS_PER_BLOCK - 1) / GU2_ROWS_PER_BLOCK;
-        if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
+        if (wide) {
+            a.r.n_router_blocks = 0;   /* routed above: stage 1 runs the shared gate/up only */
+            a.gate = L->sg;
+            a.up = L->su;
+            a.rows_per_block = GU_ROWS_PER_BLOCK;
+            const unsigned nb1 = (unsigned)((S + GU_ROWS_PER_BLOCK - 1) / GU_ROWS_PER_BLOCK);
+            if ((st = mm_launch(c, K_MOE_BF16_S1, nb1, 1, 1, 256, 0, &a))) return st;
+            a.rows_per_block = GU2_ROWS_PER_BLOCK;
+            a.gate = L->eg;
+            a.up = L->eu;
+            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
+                return st;
+        } else if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
             /* small T: the router one token per block (product / chain
              * form); up to RSH_TMAX tokens the shared expert's gate/up runs
              * in the same launch (it does not wait on the routing; one block
@@ -537,6 +608,9 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
  * MM_ROUTER_PC_EB experts per block (the token's products spread over
  * several CUs' LDS). */
 static int launch_router_logits(mm_ctx *c, mm_router_args *a) {
+    if (a->E > MM_EMAX_FAST)
+        return mm_launch(c, K_ROUTER_WIDE, (unsigned)((a->T + 3) / 4), (unsigned)((a->E + 63) / 64), 1,
+                         256, 0, a);
     if (a->E <= 64 && a->H % 8 == 0 && a->T <= MM_ROUTER_PC_TMAX)
         return mm_launch(c, K_ROUTER_PC_SPLIT, (unsigned)a->T,
                          (unsigned)((a->E + MM_ROUTER_PC_EB - 1) / MM_ROUTER_PC_EB), 1, 256, 0, a);
@@ -654,9 +728,12 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
      * cleared at init and by every tiled call's combine); a failure after it
      * clears them itself (FAIL_ROUTED) */
     /* routing waves and as many x-quantising waves per block */
-    if ((st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
-                        2 * 64 * MM_I8_RT_WAVES, 0, &ra)))
-        return tiled ? clear_counters(c, st) : st;
+    if (E > MM_EMAX_FAST)   /* the wide router (logits are given or computed above) */
+        st = route_wide(c, L, T, xn, logits, NULL, idx, wts, probs, &ra);
+    else
+        st = mm_launch(c, K_I8_ROUTE, (T + MM_I8_RT_TOKENS - 1) / MM_I8_RT_TOKENS, 1, 1,
+                       2 * 64 * MM_I8_RT_WAVES, 0, &ra);
+    if (st) return tiled ? clear_counters(c, st) : st;
 #define FAIL_ROUTED(call)                                   \
     do {                                                    \
         if ((st = (call))) return tiled ? clear_counters(c, st) : st; \

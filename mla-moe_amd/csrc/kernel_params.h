@@ -140,7 +140,10 @@ typedef struct {
 /* Routing + per-token activation quantisation (logits given). */
 #define MM_I8_RT_WAVES 4
 #define MM_I8_RT_TOKENS 4        /* tokens per block: one per wave */
-#define MM_EMAX 256
+#define MM_EMAX_FAST 256         /* experts served by the routers below (E / 64 per lane) */
+#define MM_EMAX 1024             /* experts served at all (run.c:133-134's limit): above
+                                    MM_EMAX_FAST by the wide routers (mm_router_wide,
+                                    mm_route_wide) */
 typedef struct {
     mm_router_args r;
     int32_t *cnt;            /* [E] rows per expert (zero on entry), or 0 */
@@ -523,5 +526,21 @@ typedef struct {
     mm_mla_rope_args r;
     mm_mla_qprep_args qp;
 } mm_mla_rope_qprep_args;
+
+/* ---- routing for more than MM_EMAX_FAST experts ------------------------------- */
+/* mm_router_wide: logits [T, E] (mm_router_args' logits mode: logits_out,
+ * logit_bias), grid (ceil(T / 4), ceil(E / 64)).  mm_route_wide: scores,
+ * top-k and weights from logits_in, one wave per token (4 per block), E up
+ * to MM_EMAX; with qx set also the per-token int8 quantisation of x, with
+ * cnt/rows also the tiled path's per-expert row lists. */
+#define MM_RW_EJ (MM_EMAX / 64)  /* experts per lane */
+typedef struct {
+    mm_router_args r;
+    int32_t *cnt;            /* [E] rows per expert (zero on entry), or 0 */
+    int32_t *rows;           /* [E, T] route ids (t*K + r) per expert, or 0 */
+    const float *x;          /* [T, H], with qx */
+    int8_t *qx;              /* [T, H] or 0 */
+    float *sx;               /* [T] */
+} mm_route_wide_args;
 
 #endif /* MLAMOE_KERNEL_PARAMS_H */

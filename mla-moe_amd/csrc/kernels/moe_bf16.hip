@@ -136,6 +136,40 @@ extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_rou
     router_block(a, blockIdx.x, lds);
 }
 
+/* Router logits for any E (the wide path, E > MM_EMAX_FAST): block (token
+ * group tb, expert group eb) of 4 x 64 threads, thread (t, e) owning the
+ * logit of token 4 tb + t, expert 64 eb + e: the sum over ascending hidden
+ * index of the separately rounded products x[i] * W[e, i] (run.c:29-37),
+ * chunks of 64 hidden indices of W (widened to fp32) and of x staged in LDS
+ * (W rows padded to 65 floats: the 64 threads of a token read 64 rows at one
+ * column conflict-free).  Indices past H contribute +0 (exact). */
+#pragma clang fp contract(off)
+extern "C" __global__ __launch_bounds__(256) void mm_router_wide(mm_router_args a) {
+    __shared__ float wsh[64][65];
+    __shared__ float xsh[4][64];
+    const int tt = threadIdx.x >> 6, el = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + tt, e = blockIdx.y * 64 + el;
+    const int H = a.H;
+    float acc = 0.0f;
+    for (int i0 = 0; i0 < H; i0 += 64) {
+        __syncthreads();
+        for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+            const int rr = k >> 6, c = k & 63, ee = blockIdx.y * 64 + rr, ii = i0 + c;
+            wsh[rr][c] = (ee < a.E && ii < H) ? bf16_f32(a.wg[(size_t)ee * H + ii]) : 0.0f;
+        }
+        xsh[tt][el] = (t < a.T && i0 + el < H) ? a.x[(size_t)t * H + i0 + el] : 0.0f;
+        __syncthreads();
+#pragma unroll 8
+        for (int c = 0; c < 64; c++) {
+            const float pr = xsh[tt][c] * wsh[el][c];
+            acc = acc + pr;
+        }
+    }
+    if (t < a.T && e < a.E)
+        a.logits_out[(size_t)t * a.E + e] = a.logit_bias ? acc + a.logit_bias[e] : acc;
+}
+#pragma clang fp contract(on)
+
 /* Router logits, one token per block (E <= 64; router_logits_pc). */
 extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc(mm_router_args a) {
     __shared__ __attribute__((aligned(16))) float lds[RPC_LDS_FLOATS];

@@ -114,15 +114,15 @@ static_assert(RT_TOKENS == MM_I8_RT_TOKENS, "route block size");
  *   weight = raw score, optional normalisation seeded with 1e-20 summed in
  *   slot order, times routed_scaling.
  * On return lanes r < K hold slot r's expert (*e_out) and weight (*w_out).
- * `ws` is this wave's LDS scratch of 2 * MM_EMAX + 2 * MM_KMAX words. */
+ * `ws` is this wave's LDS scratch of 2 * MM_EMAX_FAST + 2 * MM_KMAX words. */
 template <int EJ>
 __device__ __forceinline__ void route_token(const mm_router_args &a, int tok, const float (&lg)[EJ],
                                             float *ws, int *e_out, float *w_out) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int E = a.E, K = a.K;
-    float *sp = ws, *ss = ws + MM_EMAX;
-    int *slot_e = (int *)(ws + 2 * MM_EMAX);
-    float *slot_w = ws + 2 * MM_EMAX + MM_KMAX;
+    float *sp = ws, *ss = ws + MM_EMAX_FAST;
+    int *slot_e = (int *)(ws + 2 * MM_EMAX_FAST);
+    float *slot_w = ws + 2 * MM_EMAX_FAST + MM_KMAX;
     float p[EJ];
     if (a.sigmoid) {
 #pragma unroll
@@ -216,8 +216,8 @@ __device__ __forceinline__ void route_token(const mm_router_args &a, int tok, co
 template <int EJ>
 __device__ __forceinline__ void i8_route(const mm_i8_route_args &a) {
     static_assert(RT_TPW == 1, "one token per routing wave");
-    __shared__ int lcnt[MM_EMAX];
-    __shared__ float wsc[MM_I8_RT_WAVES][2 * MM_EMAX + 2 * MM_KMAX];
+    __shared__ int lcnt[MM_EMAX_FAST];
+    __shared__ float wsc[MM_I8_RT_WAVES][2 * MM_EMAX_FAST + 2 * MM_KMAX];
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const bool router = wave < MM_I8_RT_WAVES;
@@ -275,6 +275,128 @@ extern "C" __global__ __launch_bounds__(2 * MM_I8_RT_WAVES * MM_WAVE) void mm_i8
         i8_route<2>(a);
     else
         i8_route<4>(a);
+}
+
+/* ---- routing for more than MM_EMAX_FAST experts ------------------------------- */
+
+/* One wave per token, lane l holding experts l + 64 j (j < MM_RW_EJ), for
+ * E up to MM_EMAX (run.c:133-134's limit).  Scores as route_token: softmax
+ * (max, e^(x - max) with -inf -> 0, the sum in ascending expert order,
+ * divide) or sigmoid.  Top-k by K passes of a wave-wide argmax over the
+ * unused experts in the order (score + bias descending, index ascending),
+ * NaN ranked as -inf: the experts the CPU's strict '>' scan picks
+ * (run.c:132-143), pass for pass, and the same permutation as the rank form
+ * of the narrower routers.  Weight = raw score, optional normalisation
+ * seeded with 1e-20 summed in slot order, times routed_scaling
+ * (run.c:144-149).  Then, optionally, the token's int8 quantisation and its
+ * places in the per-expert row lists (one atomic per route). */
+extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_route_wide(mm_route_wide_args a) {
+    __shared__ __attribute__((aligned(16))) float sp[4][MM_EMAX];
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const mm_router_args &r = a.r;
+    const int T = r.T, E = r.E, K = r.K;
+    const int tok = blockIdx.x * 4 + wave;
+    if (tok >= T) return;
+    float p[MM_RW_EJ];
+#pragma unroll
+    for (int j = 0; j < MM_RW_EJ; j++) {
+        const int e = lane + MM_WAVE * j;
+        p[j] = e < E ? r.logits_in[(size_t)tok * E + e] : -INFINITY;
+    }
+    if (r.sigmoid) {
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++) p[j] = 1.0f / (1.0f + exp_cr(-p[j]));
+    } else {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++)
+            if (lane + MM_WAVE * j < E) mx = fmaxf(mx, p[j]);
+        mx = wave_max(mx);
+        float *ws = sp[wave];
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++) {
+            const int e = lane + MM_WAVE * j;
+            p[j] = (e < E && p[j] != -INFINITY) ? exp_cr(p[j] - mx) : 0.0f;
+            if (e < E) ws[e] = p[j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        float sum = 0.0f;   /* ascending expert order, as the CPU sums */
+        for (int e = 0; e < E; e += 4) {
+            const f32x4 v = *(const f32x4 *)(ws + e);
+            sum += v.x;
+            if (e + 1 < E) sum += v.y;
+            if (e + 2 < E) sum += v.z;
+            if (e + 3 < E) sum += v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++) p[j] = p[j] / sum;
+    }
+    if (r.probs) {
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++) {
+            const int e = lane + MM_WAVE * j;
+            if (e < E) r.probs[(size_t)tok * E + e] = p[j];
+        }
+    }
+    float sel[MM_RW_EJ];
+#pragma unroll
+    for (int j = 0; j < MM_RW_EJ; j++) {
+        const int e = lane + MM_WAVE * j;
+        sel[j] = e < E ? p[j] + (r.bias ? r.bias[e] : 0.0f) : -INFINITY;
+        if (sel[j] != sel[j]) sel[j] = -INFINITY;
+    }
+    unsigned used = 0;                      /* bit j: expert lane + 64 j taken */
+    int my_e = -1;
+    float my_w = 0.0f;
+    for (int k = 0; k < K; k++) {
+        /* this lane's best unused expert (ascending j: the lowest index
+         * wins a tie), then the wave's */
+        float bv = -INFINITY;
+        int be = 0x7fffffff;
+        float bp = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MM_RW_EJ; j++) {
+            const int e = lane + MM_WAVE * j;
+            if (e < E && !(used & (1u << j)) && (sel[j] > bv || be == 0x7fffffff)) {
+                bv = sel[j];
+                be = e;
+                bp = p[j];
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, MM_WAVE);
+            const int oe = __shfl_xor(be, off, MM_WAVE);
+            const float op = __shfl_xor(bp, off, MM_WAVE);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+                bp = op;
+            }
+        }
+        if ((be & (MM_WAVE - 1)) == lane) used |= 1u << (be / MM_WAVE);
+        if (lane == k) {
+            my_e = be;
+            my_w = bp;
+        }
+    }
+    /* weights in slot order */
+    if (r.norm_topk) {
+        float s = 1e-20f;
+        for (int k = 0; k < K; k++) s += __shfl(my_w, k, MM_WAVE);
+        my_w /= s;
+    }
+    my_w *= r.scale;
+    if (lane < K) {
+        r.topk_idx[(size_t)tok * K + lane] = my_e;
+        r.topk_w[(size_t)tok * K + lane] = my_w;
+        if (a.rows) {
+            const int pos = atomicAdd(&a.cnt[my_e], 1);
+            if (pos < T) a.rows[(size_t)my_e * T + pos] = tok * K + lane;
+        }
+    }
+    if (a.qx) quant_row_wave(a.x + (size_t)tok * r.H, r.H, a.qx + (size_t)tok * r.H, a.sx + tok);
 }
 
 /* ---- streaming grouped GEMM (decode) ------------------------------------------- */
