@@ -107,7 +107,9 @@ struct mm_ctx {
     mm_moe_config moe;
     int n_layers;
     mm_moe_layer *layers;
-    int32_t *moe_cnt;           /* [E] per-expert row counters of the tiled path */
+    int32_t *moe_cnt;           /* [max(E, 4)] per-expert row counters of the tiled int8
+                                   path, per-token counters of the bf16 router + shared
+                                   launch; zero between calls */
     /* set by mm_moe_forward_norm for the duration of one forward: the int8
      * combine also writes rmsnorm(out, norm_w) into norm_xn */
     const uint16_t *norm_w;

@@ -13,7 +13,8 @@
 
 #define BF16_NT_MAX 8         /* tokens per pass of the bf16 GEMV path */
 #define GU_ROWS_PER_BLOCK 4   /* stage 1: one gate/up row pair per wave */
-#define GU2_ROWS_PER_BLOCK 16 /* stage 2: four row pairs per wave, two at a time */
+#define GU2_ROWS_PER_BLOCK 8  /* stage 2: two row pairs per wave (one round of loads) */
+#define RSH_ROWS_PER_BLOCK 16 /* shared gate/up beside the router: four row pairs per wave */
 #define RSH_TMAX 4            /* tokens up to which the shared gate/up joins the router launch */
 #define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
 #define ROUTER_TOKENS_PER_BLOCK (4 * MM_ROUTER_TPW)
@@ -50,8 +51,11 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
         return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_init: hidden and moe_inter must be multiples of 8");
     int st = mm_set_device(c);
     if (st) return st;
-    MM_HIP(hipMalloc((void **)&c->moe_cnt, (size_t)E * sizeof(int32_t)));
-    MM_HIP(hipMemsetAsync(c->moe_cnt, 0, (size_t)E * sizeof(int32_t), c->stream));
+    /* per-expert counters of the tiled int8 path, or per-token counters of
+     * the bf16 router + shared launch (RSH_TMAX tokens): zero between calls */
+    const size_t ncnt = E > RSH_TMAX ? (size_t)E : RSH_TMAX;
+    MM_HIP(hipMalloc((void **)&c->moe_cnt, ncnt * sizeof(int32_t)));
+    MM_HIP(hipMemsetAsync(c->moe_cnt, 0, ncnt * sizeof(int32_t), c->stream));
     MM_HIP(hipStreamSynchronize(c->stream));
     c->layers = calloc((size_t)n_layers, sizeof(mm_moe_layer));
     if (!c->layers) return mm_fail(MM_ERR_NOMEM, "mm_moe_init: calloc");
@@ -503,7 +507,10 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     const size_t o_h = plan_take(&p, (size_t)BF16_NT_MAX * hw * sizeof(float));
     const size_t o_i = plan_take(&p, (size_t)T * K * sizeof(int32_t));
     const size_t o_w = plan_take(&p, (size_t)T * K * sizeof(float));
-    const size_t o_lg = plan_take(&p, wide && !logits ? (size_t)T * E * sizeof(float) : 0);
+    /* router logits scratch: the wide routers', or the split router's of
+     * the router + shared launch (computed logits, T <= RSH_TMAX) */
+    const int rsh = !wide && E <= 64 && H % 8 == 0 && S % I == 0;
+    const size_t o_lg = plan_take(&p, !logits && (wide || rsh) ? (size_t)T * E * sizeof(float) : 0);
     char *ws;
     int st = take_ws(c, fx, p.off, &ws);
     if (st) return st;
@@ -555,11 +562,10 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             a.up = L->eu;
             if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
                 return st;
-        } else if (E <= 64 && H % 8 == 0 && Tc <= MM_ROUTER_PC_TMAX && S % I == 0) {
-            /* small T: the router one token per block (product / chain
-             * form); up to RSH_TMAX tokens the shared expert's gate/up runs
-             * in the same launch (it does not wait on the routing; one block
-             * per CU there, the router's LDS), else with the routed gate/up */
+        } else if (rsh && Tc <= MM_ROUTER_PC_TMAX) {
+            /* small T: the router in product / chain form; up to RSH_TMAX
+             * tokens the shared expert's gate/up runs in the same launch (it
+             * does not wait on the routing), else with the routed gate/up */
             a.r.n_router_blocks = Tc;
             a.gate = L->eg;
             a.up = L->eu;
@@ -568,8 +574,18 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             a.nsh_parts = S / I;
             const unsigned nsh = (unsigned)(Tc * a.nsh_parts);
             if (Tc <= RSH_TMAX) {
-                if ((st = mm_launch(c, K_MOE_BF16_RSH, (unsigned)Tc + a.n_blocks_per_token * nsh, 1, 1,
-                                    256, 0, &a)))
+                /* computed logits: MM_RSH_EB experts per router block */
+                const unsigned ngr = logits ? 1u : (unsigned)((E + MM_RSH_EB - 1) / MM_RSH_EB);
+                a.lg = (float *)(ws + o_lg);
+                a.cnt = c->moe_cnt;
+                /* the shared rows beside the router in blocks of RSH_ROWS_PER_BLOCK
+                 * (measured: fewer, longer blocks there; more, shorter ones for
+                 * the routed gate/up after it) */
+                mm_gu_bf16_args ar = a;
+                ar.rows_per_block = RSH_ROWS_PER_BLOCK;
+                ar.n_blocks_per_token = (I + RSH_ROWS_PER_BLOCK - 1) / RSH_ROWS_PER_BLOCK;
+                if ((st = mm_launch(c, K_MOE_BF16_RSH, (unsigned)Tc * ngr + ar.n_blocks_per_token * nsh,
+                                    1, 1, 256, 0, &ar)))
                     return st;
                 if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, (unsigned)(Tc * K), 1, 256,
                                     0, &a)))

@@ -53,7 +53,14 @@ typedef struct {
      * grid rows T*K .. T*K + T*nsh_parts - 1, S = nsh_parts * I */
     const uint16_t *sgate, *sup;
     int nsh_parts;
+    /* mm_moe_bf16_router_sh with computed logits: MM_RSH_EB experts per
+     * router block, the logits through lg [T, E]; the block that completes
+     * a token's count in cnt [T] (zero on entry, cleared by that block)
+     * selects its experts */
+    float *lg;
+    int32_t *cnt;
 } mm_gu_bf16_args;
+#define MM_RSH_EB 16
 
 /* bf16 GEMV MoE, stage 3: out[t] (=|+=) sum over routed slots and the shared
  * expert of down_seg[d, :] . hcat[t, seg] */

@@ -186,19 +186,60 @@ extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_router_pc_split(mm_
         a.logits_out[(size_t)blockIdx.x * a.E + e] = a.logit_bias ? acc + a.logit_bias[e] : acc;
 }
 
-/* Small T: the router (one token per block, blocks [0, T)) and the shared
- * expert's gate/up (the other blocks, stage 2's shared parts: row block
- * x, then (token, part) v = t nsh_parts + j) in one launch -- the shared
- * weight stream runs on the CUs the router's add chains leave idle.  The
- * router's LDS holds every block of the launch to one per CU, which is
- * enough for a 23 MB stream in the chains' ~11 us. */
+/* Router logits of MM_RSH_EB experts of token tok (expert group eg of
+ * ngr), then the token's selection by the block whose logits complete it:
+ * every block stores its logits to a.lg and arrives on a.cnt[tok] (a
+ * workgroup barrier, then one thread's agent-scope release fence before the
+ * atomic); the last one (agent-scope acquire) reads the token's E logits
+ * back, clears the counter and selects.  No block waits on another. */
+__device__ __forceinline__ void router_split_block(const mm_gu_bf16_args &a, int tok, int eg, int ngr,
+                                                   float *lds) {
+    __shared__ int s_last;
+    const mm_router_args &r = a.r;
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const float acc = router_logits_pc<RPC_HC, MM_RSH_EB>(r, lds, tok, eg);
+    const int e = eg * MM_RSH_EB + lane;
+    if (threadIdx.x < MM_RSH_EB && e < r.E)
+        a.lg[(size_t)tok * r.E + e] = r.logit_bias ? acc + r.logit_bias[e] : acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const int last = atomicAdd(a.cnt + tok, 1) == ngr - 1;
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            a.cnt[tok] = 0;   /* every block of the token has arrived */
+        }
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || threadIdx.x >= MM_WAVE) return;
+    /* the other waves have left: their LDS is this wave's scratch */
+    const float v = lane < r.E ? a.lg[(size_t)tok * r.E + lane] : 0.0f;
+    router_select_one(r, tok, v, lds, router_no_post());
+}
+
+/* Small T: the router and the shared expert's gate/up (stage 2's shared
+ * parts: row block x, then (token, part) v = t nsh_parts + j) in one launch
+ * -- the shared weight stream runs on the CUs the router's add chains leave
+ * idle.  Router blocks [0, T ngr): with computed logits ngr = E / MM_RSH_EB
+ * blocks per token (router_split_block: a quarter of the 64-expert block's
+ * LDS product traffic per block, and LDS for five blocks per CU, so the
+ * shared stream is not held to one block per CU); with given logits one
+ * block per token selects. */
 extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_moe_bf16_router_sh(mm_gu_bf16_args a) {
-    __shared__ __attribute__((aligned(16))) float lds[RPC_LDS_FLOATS];
-    if ((int)blockIdx.x < a.T) {
-        router_block_pc<RPC_HC>(a.r, lds);
+    __shared__ __attribute__((aligned(16))) float lds[rpc_shape<RPC_HC, MM_RSH_EB>::LDS_FLOATS];
+    const int ngr = a.r.logits_in ? 1 : (a.r.E + MM_RSH_EB - 1) / MM_RSH_EB;
+    if ((int)blockIdx.x < a.T * ngr) {
+        if (!a.r.logits_in) {
+            router_split_block(a, (int)blockIdx.x / ngr, (int)blockIdx.x % ngr, ngr, lds);
+        } else if (threadIdx.x < MM_WAVE) {   /* given logits: the selection only */
+            const int tok = blockIdx.x, lane = threadIdx.x;
+            const float v = lane < a.r.E ? a.r.logits_in[(size_t)tok * a.r.E + lane] : 0.0f;
+            router_select_one(a.r, tok, v, lds, router_no_post());
+        }
         return;
     }
-    const int b = blockIdx.x - a.T;
+    const int b = blockIdx.x - a.T * ngr;
     const int row0 = (b % a.n_blocks_per_token) * a.rows_per_block;
     const int nrows = min(a.rows_per_block, a.I - row0);
     const int v = b / a.n_blocks_per_token, t = v / a.nsh_parts, j = v % a.nsh_parts;

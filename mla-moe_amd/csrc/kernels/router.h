@@ -400,8 +400,8 @@ __device__ __forceinline__ void router_block(const mm_router_args &a, int block,
  * contribute +0 (exact, as in router_logits_block).  Returns the logit of
  * expert `lane` in wave 0 (0 elsewhere).
  *
- * EB < 64: the block serves experts EB blockIdx.y .. + EB - 1 of its token
- * only (lane e of the chain wave: expert EB blockIdx.y + e, lanes >= EB
+ * EB < 64: the block serves experts EB eg .. + EB - 1 of its token (eg:
+ * blockIdx.y unless given) only (lane e of the chain wave: expert EB eg + e, lanes >= EB
  * idle), so a token's products -- written to LDS and read back, 2 x 4 B
  * per product -- spread over 64 / EB CUs: with all 64 experts in one block
  * that LDS traffic (1 MB per token), not the add chains, set the pace. */
@@ -422,14 +422,15 @@ struct rpc_shape {
 #define RPC_EB_SPLIT MM_ROUTER_PC_EB                    /* experts per block, logits only */
 
 template <int HC, int EB = MM_WAVE>
-__device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float *lds) {
+__device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float *lds,
+                                                  int tok = blockIdx.x, int eg = blockIdx.y) {
     using S = rpc_shape<HC, EB>;
     static_assert(HC % 8 == 0 && MM_WAVE % S::LPR == 0, "chunk rows of whole 16-byte pieces");
     static_assert(EB <= MM_WAVE && EB % (MM_WAVE / S::LPR) == 0, "whole loads of expert rows");
-    const int e0 = EB < MM_WAVE ? (int)blockIdx.y * EB : 0;
+    const int e0 = EB < MM_WAVE ? eg * EB : 0;
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
-    const int tok = blockIdx.x, H = a.H, E = a.E;
+    const int H = a.H, E = a.E;
     const int nch = (H + HC - 1) / HC;
     const int nph = (nch + RPC_NPROD - 1) / RPC_NPROD;
     float *prod = lds;                                   /* [6][EB][RS] */
