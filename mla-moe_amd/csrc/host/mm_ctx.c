@@ -166,6 +166,11 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->i8_tiled_min_t = 256;
     const char *ev = getenv("MLAMOE_I8_TILED_MIN_T");
     if (ev && *ev) c->i8_tiled_min_t = atoi(ev);
+    /* MLAMOE_MLA_PART_MAX (bytes) overrides the cap on the attention chunk
+     * partials of one launch, above which rows go in groups */
+    c->mla_part_max = MM_MLA_PART_MAX;
+    ev = getenv("MLAMOE_MLA_PART_MAX");
+    if (ev && *ev && atoll(ev) > 0) c->mla_part_max = (size_t)atoll(ev);
     if ((st = mm_noalloc_setup(c))) goto fail;
     *out = c;
     return MM_OK;

@@ -127,6 +127,7 @@ struct mm_ctx {
     float *front_inv;           /* [qk_rope_head_dim / 2] device RoPE table */
 
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
+    size_t mla_part_max;        /* attention chunk partials per launch (bytes) */
 
     /* growable device workspace */
     void *ws;

@@ -72,10 +72,32 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                               qabs, probs, clat, NULL, NULL);
 }
 
+static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
+                       int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
+                       float *ctx_out, float *qabs, float *probs, float *clat,
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in);
+
 int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
                        const mm_mla_rope_args *rope, uint16_t *ctx_hl) {
+    return decode_rows(c, layer, B, q, cache, seq_stride, slots, kv_lens, kv_len, ctx_out, qabs,
+                       probs, clat, rope, ctx_hl, 0, 0);
+}
+
+/* The merge's blocks per (head, sequence): the latent columns over 4 blocks
+ * when the grid would otherwise have fewer than 128 blocks (each block's
+ * chunk groups then meet in group order). */
+static unsigned merge_z(int NH, int B) { return (size_t)NH * B < 128 ? MM_MLA_KVL / 128 : 1; }
+
+/* chunk_in > 0: a group of a larger call's rows, with that call's chunk
+ * length and merge split zc_in (the same partition of every row's keys and
+ * the same order of their sums, so the same results) and no further
+ * grouping. */
+static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
+                       int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
+                       float *ctx_out, float *qabs, float *probs, float *clat,
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
     if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
         return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
@@ -99,6 +121,7 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
      * twice the length instead, whose block writes clat itself (no merge
      * launch) */
     if (chunk < MM_MLA_CHUNK && kv_len > chunk && kv_len <= chunk + chunk / 2) chunk *= 2;
+    if (chunk_in > 0) chunk = chunk_in;
     const int nchunks = (kv_len + chunk - 1) / chunk;
     const int direct = nchunks == 1 && !probs;
     if (kv_len > MM_MAX_KV_LEN || nchunks > MM_MLA_MAXCH)
@@ -110,9 +133,37 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     if (st) return st;
     const mm_mla_config *g = &c->mla;
     const int NH = g->n_heads, HG = (NH + 15) / 16;
+    /* The chunk partials take B HG nchunks (16 x 512 + 32) floats: every row
+     * is sized for the longest context of the step (kv_len).  Above
+     * c->mla_part_max bytes (MM_MLA_PART_MAX) the rows go in groups, one
+     * after another on the stream, each within the cap and with this call's
+     * chunk length (the RoPE / cache append of a front step first, for all
+     * rows).  Not with ctx_hl, whose lo plane sits B rows after the hi plane
+     * (its callers pass at most MM_SKINNY_T rows). */
+    const size_t part_row = direct ? 0 : (size_t)HG * nchunks * (16 * MM_MLA_KVL + 32) * 4;
+    if (!chunk_in && !ctx_hl && (size_t)B * part_row > c->mla_part_max) {
+        if (rope && (st = mm_launch(c, K_MLA_ROPE, (unsigned)B, 1, 1, 256, 0, (void *)rope))) return st;
+        const int G = (int)(c->mla_part_max / part_row) > 0 ? (int)(c->mla_part_max / part_row) : 1;
+        const int QKD = g->qk_nope_head_dim + MM_MLA_QKR;
+        for (int r0 = 0; r0 < B; r0 += G) {
+            const int n = B - r0 < G ? B - r0 : G;
+            const size_t rq = (size_t)r0 * NH;
+            /* without slots row b reads cache sequence b */
+            if ((st = decode_rows(
+                     c, layer, n, q + rq * QKD,
+                     slots ? cache : cache + (size_t)r0 * seq_stride * MM_MLA_KVD, seq_stride,
+                     slots ? slots + r0 : NULL, kv_lens ? kv_lens + r0 : NULL, kv_len,
+                     ctx_out + rq * g->v_head_dim, qabs ? qabs + rq * MM_MLA_KVL : NULL,
+                     probs ? probs + rq * kv_len : NULL, clat ? clat + rq * MM_MLA_KVL : NULL, NULL,
+                     NULL, chunk, merge_z(NH, B))))
+                return st;
+        }
+        return MM_OK;
+    }
     const size_t qa_b = qabs ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
-    const size_t ml_b = (size_t)B * HG * nchunks * 32 * 4;
-    const size_t po_b = (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
+    /* chunk partials (none when one block takes a row's whole context) */
+    const size_t ml_b = direct ? 0 : (size_t)B * HG * nchunks * 32 * 4;
+    const size_t po_b = direct ? 0 : (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
     const size_t cl_b = clat ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
     const size_t qhl_b = (size_t)B * NH * 2 * MM_MLA_KVL * 2;   /* qabs as bf16 hi + lo */
     char *ws;
@@ -150,9 +201,7 @@ int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks,
                               ctx_hl};
-    /* merge: split the latent columns over 4 blocks per (head, sequence)
-     * when the grid would otherwise have fewer than 128 blocks */
-    const unsigned zc = (size_t)NH * B < 128 ? MM_MLA_KVL / 128 : 1;
+    const unsigned zc = chunk_in > 0 ? zc_in : merge_z(NH, B);
     if (!direct && (st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, zc, 256, 0, &ca)))
         return st;
     return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,

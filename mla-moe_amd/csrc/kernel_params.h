@@ -297,6 +297,9 @@ typedef struct {
  * the longest chunk, above the reference's KV_CACHE_CAP of 163,840
  * (src/model_load.c:237). */
 #define MM_MLA_MAXCH 512
+#ifndef MM_MLA_PART_MAX
+#define MM_MLA_PART_MAX ((size_t)512 << 20)   /* bytes of attention chunk partials per launch */
+#endif
 #define MM_MLA_TILE_B (16 * 1056 + 16 * 128)   /* LDS bytes of one 16-key sub-tile */
 
 /* qabs = q_nope . W_UK per head. */

@@ -155,3 +155,23 @@ def test_mla_two_row_tiles_ragged(ctx, oracle):
     lens = [1500 - 37 * b for b in range(40)]
     lens[3], lens[17], lens[39] = 1, 16, 513
     run_case(ctx, oracle, 16, 40, 1500, 1500, 651, kv_lens=lens)
+
+
+def test_mla_rows_in_groups(monkeypatch, oracle):
+    """Chunk partials over the per-launch cap (MLAMOE_MLA_PART_MAX, here
+    three rows' worth): the rows go in groups of 3, 3, 3 and 1, one after
+    another.  Every row against the oracle and bit-identical to the
+    ungrouped call (ragged lengths; B * HG * chunks = 10 x 24)."""
+    B, L, NH = 10, 1500, 16
+    lens = [1500, 7, 900, 64, 1, 1499, 300, 16, 1024, 777]
+    per_row = 24 * (16 * 512 + 32) * 4            # 24 chunks of 64 keys
+    with mlamoe.Context(0) as c0:
+        ref = run_case(c0, oracle, NH, B, L, L, 660, kv_lens=lens)
+    monkeypatch.setenv("MLAMOE_MLA_PART_MAX", str(3 * per_row))
+    with mlamoe.Context(0) as c1:
+        got = run_case(c1, oracle, NH, B, L, L, 660, kv_lens=lens)
+    same = lambda x, y: np.array_equal(np.asarray(x).view(np.uint32), np.asarray(y).view(np.uint32))  # noqa: E731
+    for name, i in (("ctx", 0), ("qabs", 1), ("clat", 3)):
+        assert same(ref[i], got[i]), name
+    for b, n in enumerate(lens):   # the weights of each row's own keys (the rest is not written)
+        assert same(ref[2][b][:, :n], got[2][b][:, :n]), ("probs", b)

@@ -125,3 +125,28 @@ def test_generate_with_chunked_prefill(oracle, max_rows):
         for k, t in enumerate(o):
             row = lg[len(p) - 1 + k]
             assert t == row.argmax() or row[t] >= row.max() - TOL * np.abs(row).max()
+
+
+def test_prefill_rows_in_attention_groups(monkeypatch):
+    """120 prompt rows in one step (past the hi/lo operand rows: the
+    attention's chunk partials sized per row, two 64-key chunks each), with
+    the per-launch cap on the partials (MLAMOE_MLA_PART_MAX) set to 7 rows'
+    worth: the front's RoPE / cache append for all rows, then the rows in
+    groups of 7.  Logits bit-identical to the same step without the cap."""
+    c, m, g = engine_case("dsv2")
+    inv = g["inv"]
+    toks = np.random.default_rng(77).integers(0, c["vocab"], 120).astype(np.int32)
+    n = len(toks)
+    out = []
+    for cap in (None, 7 * 2 * (16 * 512 + 32) * 4):
+        if cap:
+            monkeypatch.setenv("MLAMOE_MLA_PART_MAX", str(cap))
+        with mlamoe.Context(0) as ctx:
+            eng = Engine.from_host(ctx, c, m, inv, max_batch=1, max_seq=128)
+            try:
+                _, lg = eng.step_rows(np.zeros(n), toks, np.arange(n), np.arange(n),
+                                      want_logits=True)
+            finally:
+                eng.close()
+        out.append(lg)
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
