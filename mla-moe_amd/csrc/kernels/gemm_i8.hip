@@ -9,22 +9,27 @@
  *
  * Block tile MM_I8B_BM = 128 rows x MM_I8B_FR = 16 fragments (gate/up: the
  * gate and up fragments of 8 column blocks, 128 output columns; plain: 256
- * output columns), K step (stage) 64 bytes.  The four waves split the
- * columns: wave w owns all 128 rows and fragments 4 w .. 4 w + 3, i.e. four
- * 32-row blocks x two 32-column MFMA tiles (gate/up: the gate and the up
- * tile of one 32-column pair), 8 accumulators of 16 registers.
+ * output columns), K step 64 bytes.  The four waves split the columns: wave
+ * w owns all 128 rows and fragments 4 w .. 4 w + 3, i.e. four 32-row blocks
+ * x two 32-column MFMA tiles (gate/up: the gate and the up tile of one
+ * 32-column pair), 8 accumulators of 16 registers.
  *
  * The 32x32x32 MFMA is used because it keeps the pipe 85-90% busy at one or
  * two waves per SIMD, where the 16x16x64 form is limited by issue to 58-75%
  * (measured on MI355X).  Two blocks share a CU, so one block's set-up, load
  * latency and epilogue overlap the other's MFMAs.
  *
- * Data path per stage: the A rows (8 KB: 64 bytes of each row, 16-byte
- * chunks XOR-swizzled by row) go global -> LDS by direct loads, read by all
- * four waves; each wave loads its own B operands (4 KB) straight into
- * registers, as the decode GEMMs do.  A ring of BT_NS slots (LDS for A,
- * registers for B) runs BT_P stages ahead.  A 32x32x32 B operand (lane l:
- * column l % 32, K bytes 16 (l / 32) .. + 15) is one 16-byte load per lane
+ * Data path: the A rows go global -> LDS by direct loads in stages of
+ * BT_KB = 128 bytes of K per row (16 KB: whole cache lines of every row,
+ * 16-byte chunks XOR-swizzled by row), two LDS slots, read by all four
+ * waves; each wave loads its own B operands (4 KB per 64-byte K step)
+ * straight into registers, as the decode GEMMs do, through a ring of BT_NSB
+ * slots two steps ahead.  A tile's head (its first two A stages and B
+ * steps) goes out before the previous tile's stores; the output tile is
+ * restaged through LDS so that the stores are whole 128-byte lines.
+ *
+ * A 32x32x32 B operand (lane l: column l % 32, K bytes 16 (l / 32) .. + 15)
+ * is one 16-byte load per lane
  * out of two packed 16x64 fragments: the 16 bytes of (column c, K chunk q)
  * sit at byte (16 q + c % 16) * 16 of fragment c / 16.  Measured on MI355X
  * against staging both operands in LDS (which costs each wave 12 LDS reads
@@ -39,8 +44,9 @@
  * activation rows as src1, so the result is the output tile transposed:
  * lane l holds activation row l % 32 and, in registers 4 g .. 4 g + 3, four
  * consecutive output columns 8 g + 4 (l / 32) .. + 3, which the epilogue
- * stores as one 16-byte write (a quarter of the stores of the other operand
- * order, whose lanes hold one column of four rows).
+ * writes to its LDS staging tile as one 16-byte write (a quarter of the
+ * writes of the other operand order, whose lanes hold one column of four
+ * rows).
  */
 #include <type_traits>
 
