@@ -446,56 +446,72 @@ __device__ __forceinline__ float router_logits_pc(const mm_router_args &a, float
         const int o = 8 * (lane % S::LPR);
         u32x4 wr[NSL][S::NLD];
         float xv[NSL];
+        /* loads unconditional (addresses clamped into the matrix; chunks
+         * past the end re-read the last), the values past H or past the
+         * last chunk zeroed where they are used: a load under a condition
+         * becomes a branch, and the compiler then drains every outstanding
+         * load before the next use instead of waiting for the one it needs */
         auto fetch = [&](int slot, int c) {
-            const int i = c * HC + o;
+            const int cc = min(c, nch - 1);
+            const int i = min(cc * HC + o, H - 8);
 #pragma unroll
             for (int j = 0; j < S::NLD; j++) {
                 const int e = min(e0 + RPL * j + lane / S::LPR, E - 1);
-                /* in range: H is a multiple of 8; past H: zeros */
-                wr[slot][j] = (c < nch && i < H) ? *(const u32x4 *)(a.wg + (size_t)e * H + i)
-                                                 : (u32x4){0u, 0u, 0u, 0u};
+                wr[slot][j] = *(const u32x4 *)(a.wg + (size_t)e * H + i);
             }
-            const int ix = c * HC + lane;
-            xv[slot] = (c < nch && lane < HC && ix < H) ? xrow[ix] : 0.0f;
+            xv[slot] = xrow[min(cc * HC + min(lane, HC - 1), H - 1)];
         };
 #pragma unroll
         for (int d = 0; d < RPC_PF; d++) fetch(d, RPC_NPROD * d + p);
-        /* phase k uses slot k % NSL and refills slot (k + RPC_PF) % NSL */
-        for (int k0 = 0; k0 <= nph; k0 += NSL) {
+        /* phase k uses slot k % NSL and refills slot (k + RPC_PF) % NSL;
+         * whole turns of NSL phases first, then the last partial turn */
+        auto phase = [&](int d, int k) {
+#pragma clang fp contract(off)
+            const int b = (k & 1) * RPC_NPROD + p;
+            const int c = RPC_NPROD * k + p;             /* this phase's chunk */
+            float *xb = xs + b * HC;
+            /* this chunk's x to LDS (read back by this wave only: its LDS
+             * accesses complete in order); zeros past H or past the last
+             * chunk, and their weights zeroed too */
+            if (lane < HC) xb[lane] = (c < nch && c * HC + lane < H) ? xv[d] : 0.0f;
+            const bool wok = c < nch && c * HC + o < H;
+            fetch((d + RPC_PF) % NSL, RPC_NPROD * (k + RPC_PF) + p);
+            const f32x4 x0 = *(const f32x4 *)(xb + o);
+            const f32x4 x1 = *(const f32x4 *)(xb + o + 4);
+            float *pb = prod + b * S::BUF + o;
+#pragma unroll
+            for (int j = 0; j < S::NLD; j++) {
+                const u32x4 w = wok ? wr[d][j] : (u32x4){0u, 0u, 0u, 0u};
+                f32x4 lo, hi;
+                lo.x = x0.x * __uint_as_float(w.x << 16);
+                lo.y = x0.y * __uint_as_float(w.x & 0xffff0000u);
+                lo.z = x0.z * __uint_as_float(w.y << 16);
+                lo.w = x0.w * __uint_as_float(w.y & 0xffff0000u);
+                hi.x = x1.x * __uint_as_float(w.z << 16);
+                hi.y = x1.y * __uint_as_float(w.z & 0xffff0000u);
+                hi.z = x1.z * __uint_as_float(w.w << 16);
+                hi.w = x1.w * __uint_as_float(w.w & 0xffff0000u);
+                float *row = pb + (size_t)(RPL * j + lane / S::LPR) * S::RS;
+                *(f32x4 *)row = lo;
+                *(f32x4 *)(row + 4) = hi;
+            }
+        };
+        int k0 = 0;
+        for (; k0 + NSL <= nph; k0 += NSL) {
 #pragma unroll
             for (int d = 0; d < NSL; d++) {
-                const int k = k0 + d;
-                if (k > nph) break;
-                if (k < nph) {
-#pragma clang fp contract(off)
-                    const int b = (k & 1) * RPC_NPROD + p;
-                    float *xb = xs + b * HC;
-                    /* this chunk's x to LDS (read back by this wave only:
-                     * its LDS accesses complete in order) */
-                    if (lane < HC) xb[lane] = xv[d];
-                    fetch((d + RPC_PF) % NSL, RPC_NPROD * (k + RPC_PF) + p);
-                    const f32x4 x0 = *(const f32x4 *)(xb + o);
-                    const f32x4 x1 = *(const f32x4 *)(xb + o + 4);
-                    float *pb = prod + b * S::BUF + o;
-#pragma unroll
-                    for (int j = 0; j < S::NLD; j++) {
-                        const u32x4 w = wr[d][j];
-                        f32x4 lo, hi;
-                        lo.x = x0.x * __uint_as_float(w.x << 16);
-                        lo.y = x0.y * __uint_as_float(w.x & 0xffff0000u);
-                        lo.z = x0.z * __uint_as_float(w.y << 16);
-                        lo.w = x0.w * __uint_as_float(w.y & 0xffff0000u);
-                        hi.x = x1.x * __uint_as_float(w.z << 16);
-                        hi.y = x1.y * __uint_as_float(w.z & 0xffff0000u);
-                        hi.z = x1.z * __uint_as_float(w.w << 16);
-                        hi.w = x1.w * __uint_as_float(w.w & 0xffff0000u);
-                        float *row = pb + (size_t)(RPL * j + lane / S::LPR) * S::RS;
-                        *(f32x4 *)row = lo;
-                        *(f32x4 *)(row + 4) = hi;
-                    }
-                }
+                phase(d, k0 + d);
                 __syncthreads();
             }
+        }
+        /* phases k0 .. nph: the last product phases, then the barrier of
+         * the chain wave's final consumption (nph + 1 barriers in all) */
+#pragma unroll
+        for (int d = 0; d < NSL; d++) {
+            const int k = k0 + d;
+            if (k > nph) break;
+            if (k < nph) phase(d, k);
+            __syncthreads();
         }
     } else {
         for (int k = 0; k <= nph; k++) {
