@@ -189,9 +189,24 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
         if (k0 + j < KB) step(k0 + j, j);
     VMCNT_WAIT(0);
 
-    /* lane holds D[4 (l / 16) + i][l % 16] of each 16 x 16 tile */
+    /* lane holds D[4 (l / 16) + i][l % 16] of each 16 x 16 tile.  With
+     * accumulate, a row block's old outputs are all loaded (clamped
+     * addresses, unconditionally) before any is added: a load under the
+     * row / column conditions would be a branch of its own, each waited
+     * for before the next is issued. */
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < 4; r++) {
+        float prev[GB_NC][4];
+        if (a.accumulate) {   /* uniform */
+#pragma unroll
+            for (int c = 0; c < GB_NC; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = min(n0 + (GB_BN / 2) * wn + 16 * c + (lane & 15), a.d_out - 1);
+                    const int m = min(m0 + 64 * wm + 16 * r + 4 * (lane >> 4) + i, a.T - 1);
+                    prev[c][i] = a.y[(size_t)m * a.d_out + n];
+                }
+        }
 #pragma unroll
         for (int c = 0; c < GB_NC; c++) {
             const int n = n0 + (GB_BN / 2) * wn + 16 * c + (lane & 15);
@@ -200,10 +215,10 @@ __device__ __forceinline__ void gemm_block(const mm_gemm_bf16_args &a, uint8_t *
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + 64 * wm + 16 * r + 4 * (lane >> 4) + i;
                 if (m >= a.T) continue;
-                float *o = a.y + (size_t)m * a.d_out + n;
-                *o = a.accumulate ? *o + acc[r][c][i] : acc[r][c][i];
+                a.y[(size_t)m * a.d_out + n] = a.accumulate ? prev[c][i] + acc[r][c][i] : acc[r][c][i];
             }
         }
+    }
 }
 
 /* 1-D grid of 8 * ceil(ceil(d_out / 128) / 8) * ceil(T / 128) blocks, 256
