@@ -107,9 +107,10 @@ struct mm_ctx {
     mm_moe_config moe;
     int n_layers;
     mm_moe_layer *layers;
-    int32_t *moe_cnt;           /* [max(E, 4)] per-expert row counters of the tiled int8
-                                   path, per-token counters of the bf16 router + shared
-                                   launch; zero between calls */
+    int32_t *moe_cnt;           /* [E * MM_CNT_STRIDE]: per-expert row counters of the
+                                   tiled int8 path (one per 128-byte line), or per-token
+                                   counters (the first RSH_TMAX entries) of the bf16
+                                   router + shared launch; zero between calls */
     /* set by mm_moe_forward_norm for the duration of one forward: the int8
      * combine also writes rmsnorm(out, norm_w) into norm_xn */
     const uint16_t *norm_w;

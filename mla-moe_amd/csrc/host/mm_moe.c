@@ -53,7 +53,7 @@ int mm_moe_init(mm_ctx *c, const mm_moe_config *cfg, int n_layers) {
     if (st) return st;
     /* per-expert counters of the tiled int8 path, or per-token counters of
      * the bf16 router + shared launch (RSH_TMAX tokens): zero between calls */
-    const size_t ncnt = E > RSH_TMAX ? (size_t)E : RSH_TMAX;
+    const size_t ncnt = (size_t)E * MM_CNT_STRIDE;   /* >= RSH_TMAX */
     MM_HIP(hipMalloc((void **)&c->moe_cnt, ncnt * sizeof(int32_t)));
     MM_HIP(hipMemsetAsync(c->moe_cnt, 0, ncnt * sizeof(int32_t), c->stream));
     MM_HIP(hipStreamSynchronize(c->stream));
@@ -664,7 +664,8 @@ static int launch_tiled(mm_ctx *c, const mm_i8_tiled_args *ta, const mm_i8_tiled
  * the per-expert counters that its combine would have cleared: clear them
  * here (best effort: the launch itself may be what fails) and return st. */
 static int clear_counters(mm_ctx *c, int st) {
-    mm_zero32_args za = {(uint32_t *)c->moe_cnt, (uint64_t)c->moe.n_routed_experts};
+    mm_zero32_args za = {(uint32_t *)c->moe_cnt,
+                         (uint64_t)c->moe.n_routed_experts * MM_CNT_STRIDE};
     (void)mm_launch(c, K_ZERO32, 1, 1, 1, 256, 0, &za);
     return st;
 }

@@ -148,12 +148,17 @@ typedef struct {
 #define MM_I8_RT_WAVES 4
 #define MM_I8_RT_TOKENS 4        /* tokens per block: one per wave */
 #define MM_EMAX_FAST 256         /* experts served by the routers below (E / 64 per lane) */
+/* The per-expert row counters of the tiled path sit one per 128-byte line
+ * (counter e at cnt[e * MM_CNT_STRIDE]): every routing block adds to the
+ * counters of the experts it routes to, and counters sharing a line
+ * serialise those atomics. */
+#define MM_CNT_STRIDE 32
 #define MM_EMAX 1024             /* experts served at all (run.c:133-134's limit): above
                                     MM_EMAX_FAST by the wide routers (mm_router_wide,
                                     mm_route_wide) */
 typedef struct {
     mm_router_args r;
-    int32_t *cnt;            /* [E] rows per expert (zero on entry), or 0 */
+    int32_t *cnt;            /* [E * MM_CNT_STRIDE] rows per expert (zero on entry), or 0 */
     int32_t *rows;           /* [E, T] route ids (t*K + r) per expert, or 0 (no lists) */
     const float *x;          /* [T, H] */
     int8_t *qx;              /* [T, H] */
@@ -163,7 +168,7 @@ typedef struct {
 /* Grouped int8 GEMM over experts 0..E-1 (routed) and the shared expert. */
 typedef struct {
     mm_i8_weights w;
-    const int32_t *cnt;      /* [E] (tiled path) */
+    const int32_t *cnt;      /* [E * MM_CNT_STRIDE] (tiled path) */
     const int32_t *rows;     /* [E, T] (tiled path) */
     const int32_t *topk;     /* [T, K] expert ids (decode path builds its row lists) */
     const int8_t *a;         /* gate/up: qx [T, H];  down: qh [T*K, I] */
@@ -193,8 +198,9 @@ typedef struct {
     int rows2, n2;
 } mm_i8_quant_rows_args;
 
-/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]; clears cnt[0..E) when
- * cnt is given (the tiled path's per-expert counters, read by then). */
+/* out[t] (=|+=) sum_r w[t,r] * y[t*K + r] + ys[t]; clears the E counters
+ * cnt[e * MM_CNT_STRIDE] when cnt is given (the tiled path's per-expert
+ * counters, read by then). */
 typedef struct {
     const float *y, *ys;
     const float *topk_w;
@@ -256,7 +262,7 @@ typedef struct {
     size_t b_expert_stride;  /* bytes between experts' fragment sets */
     const float *sb0, *sb1;  /* per-column weight scales (gate, up) of expert 0 */
     int sb_expert_stride;    /* floats between experts' scale vectors */
-    const int32_t *cnt;      /* [E] rows per expert, or 0: one expert with T rows */
+    const int32_t *cnt;      /* [E * MM_CNT_STRIDE] rows per expert, or 0: one expert with T rows */
     const int32_t *rows;     /* [E, T] route ids, or 0: identity rows */
     const int8_t *a;         /* A rows (int8), indexed by token (gate/up) or route id (down) */
     const float *sa;         /* A row scales, same index as a */
@@ -546,7 +552,7 @@ typedef struct {
 #define MM_RW_EJ (MM_EMAX / 64)  /* experts per lane */
 typedef struct {
     mm_router_args r;
-    int32_t *cnt;            /* [E] rows per expert (zero on entry), or 0 */
+    int32_t *cnt;            /* [E * MM_CNT_STRIDE] rows per expert (zero on entry), or 0 */
     int32_t *rows;           /* [E, T] route ids (t*K + r) per expert, or 0 */
     const float *x;          /* [T, H], with qx */
     int8_t *qx;              /* [T, H] or 0 */

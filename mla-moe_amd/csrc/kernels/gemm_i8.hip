@@ -161,7 +161,7 @@ __device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt
         id.e = lo;
         id.slab = loc / ge;
         id.m0 = (loc % ge) * MM_I8B_BM;
-        id.M = g.cnt ? min(g.cnt[lo], g.T) : g.T;
+        id.M = g.cnt ? min(g.cnt[lo * MM_CNT_STRIDE], g.T) : g.T;
     } else {
         const mm_i8_tiled_args &g = a.seg[1];
         const int loc = t - sh.n0;
@@ -527,7 +527,7 @@ __device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
         int base = 0;
         for (int e0 = 0; e0 < E; e0 += MM_WAVE) {
             const int e = e0 + lane;
-            const int M = e < E ? (g0.cnt ? min(g0.cnt[e], g0.T) : g0.T) : 0;
+            const int M = e < E ? (g0.cnt ? min(g0.cnt[e * MM_CNT_STRIDE], g0.T) : g0.T) : 0;
             const int nt = (M + MM_I8B_BM - 1) / MM_I8B_BM;
             int incl = nt;
 #pragma unroll

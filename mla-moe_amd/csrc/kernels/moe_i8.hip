@@ -258,7 +258,7 @@ __device__ __forceinline__ void i8_route(const mm_i8_route_args &a) {
         __syncthreads();
         for (int e = threadIdx.x; e < E; e += MM_I8_RT_WAVES * MM_WAVE) {
             const int n = lcnt[e];
-            lcnt[e] = n ? atomicAdd(&a.cnt[e], n) : 0;   /* now the block's base */
+            lcnt[e] = n ? atomicAdd(&a.cnt[e * MM_CNT_STRIDE], n) : 0;   /* now the block's base */
         }
         __syncthreads();
         if (my_e >= 0) {
@@ -392,7 +392,7 @@ extern "C" __global__ __launch_bounds__(4 * MM_WAVE) void mm_route_wide(mm_route
         r.topk_idx[(size_t)tok * K + lane] = my_e;
         r.topk_w[(size_t)tok * K + lane] = my_w;
         if (a.rows) {
-            const int pos = atomicAdd(&a.cnt[my_e], 1);
+            const int pos = atomicAdd(&a.cnt[my_e * MM_CNT_STRIDE], 1);
             if (pos < T) a.rows[(size_t)my_e * T + pos] = tok * K + lane;
         }
     }
@@ -879,7 +879,7 @@ extern "C" __global__ __launch_bounds__(256) void mm_i8_combine(mm_i8_combine_ar
         *op = a.accumulate ? o + acc : acc;
     }
     if (a.cnt && t == 0 && blockIdx.y == 0)
-        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e * MM_CNT_STRIDE] = 0;
 }
 
 /* ---- weight packing ----------------------------------------------------------- */
@@ -954,7 +954,7 @@ extern "C" __global__ __launch_bounds__(MM_I8_CN_THREADS) void mm_i8_combine_nor
         }
     }
     if (a.cnt && t == 0)
-        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e] = 0;
+        for (int e = threadIdx.x; e < a.E; e += blockDim.x) a.cnt[e * MM_CNT_STRIDE] = 0;
 }
 
 extern "C" __global__ __launch_bounds__(256) void mm_pack_i8(mm_pack_i8_args a) {
