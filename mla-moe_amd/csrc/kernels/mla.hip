@@ -21,6 +21,7 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 #define KVL MM_MLA_KVL
 #define KVD MM_MLA_KVD
@@ -619,42 +620,49 @@ __device__ __forceinline__ void rope_token(const mm_mla_rope_args &a, int b) {
 #pragma clang fp contract(off)
     __shared__ float cs[2][128];
     __shared__ float red[256 / MM_WAVE];
+    static_assert(KVL == 512 && MM_MLA_QKR <= 256, "one c_kv pair per thread, one k_pe pair per thread");
     const int tid = threadIdx.x;
-    const int half = a.qkr / 2, kvd = a.kvl + a.qkr;
-    const int p = a.pos[b];
-    if (tid < half) {
-        const double ang = (double)((float)p * a.inv_freq[tid]);
-        cs[0][tid] = (float)cos(ang);
-        cs[1][tid] = (float)sin(ang);
-    }
-    const float *comp = a.comp + (size_t)b * kvd;
-    float ss = 0.0f;
-    for (int i = tid; i < a.kvl; i += 256) ss += comp[i] * comp[i];
-    ss = wave_sum(ss);
-    if ((tid & (MM_WAVE - 1)) == 0) red[tid / MM_WAVE] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 256 / MM_WAVE; w++) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / (float)a.kvl + a.eps);
-
-    /* q_pe of every head, in place: all pairs are read before any is written
-     * (the split-half layout moves values across pairs) */
-    const int qhd = a.qkn + a.qkr;
-    float *q = a.q + (size_t)b * a.nh * qhd + a.qkn;
-    const int npairs = a.nh * half;
+    const int half = MM_MLA_QKR / 2, kvd = KVL + MM_MLA_QKR;
+    const int qhd = a.qkn + MM_MLA_QKR, npairs = a.nh * half;
     constexpr int QK = MM_ROPE_PAIRS_MAX / 256;
+    /* Every load of the block goes out first, at clamped addresses (no load
+     * under a condition: each would be waited for on its own), so the block
+     * pays one round trip: the position, the cache slot, the frequency, this
+     * thread's c_kv pair with its norm weights, its k_pe pair and its q_pe
+     * pairs.  Thread t owns c_kv values 2t, 2t + 1 and k_pe pair t (t < 32). */
+    const int p = a.pos[b];
+    const int seq = a.slots ? a.slots[b] : b;
+    const float invf = a.inv_freq[min(tid, half - 1)];
+    const float *comp = a.comp + (size_t)b * kvd;
+    const f32x2 cv = *(const f32x2 *)(comp + 2 * tid);
+    const uint32_t nw = *(const uint32_t *)(a.kv_norm + 2 * tid);
+    const f32x2 kp = *(const f32x2 *)(comp + KVL + 2 * min(tid, half - 1));
+    float *q = a.q + (size_t)b * a.nh * qhd + a.qkn;
     float qe[QK], qo[QK];
 #pragma unroll
     for (int k = 0; k < QK; k++) {
-        const int i = tid + 256 * k;
-        if (i < npairs) {
-            const int h = i / half, j = i - h * half;
-            qe[k] = q[(size_t)h * qhd + 2 * j];
-            qo[k] = q[(size_t)h * qhd + 2 * j + 1];
-        }
+        const int i = min(tid + 256 * k, npairs - 1);
+        const int h = i / half, j = i - h * half;
+        const f32x2 v = *(const f32x2 *)(q + (size_t)h * qhd + 2 * j);   /* adjacent pair, both layouts */
+        qe[k] = v.x;
+        qo[k] = v.y;
     }
-    if (a.interleaved) __syncthreads();
+    if (tid < half) {
+        const double ang = (double)((float)p * invf);
+        cs[0][tid] = (float)cos(ang);
+        cs[1][tid] = (float)sin(ang);
+    }
+    float ss = cv.x * cv.x + cv.y * cv.y;
+    ss = wave_sum(ss);
+    if ((tid & (MM_WAVE - 1)) == 0) red[tid / MM_WAVE] = ss;
+    __syncthreads();   /* red and cs; every thread has read its q pairs */
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 256 / MM_WAVE; w++) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)KVL + a.eps);
+
+    /* q_pe of every head, in place (all pairs were read before the barrier:
+     * the split-half layout moves values across pairs) */
 #pragma unroll
     for (int k = 0; k < QK; k++) {
         const int i = tid + 256 * k;
@@ -674,20 +682,21 @@ __device__ __forceinline__ void rope_token(const mm_mla_rope_args &a, int b) {
 
     /* the cache row */
     const bool wr = p >= 0 && p < a.seq_stride;
-    const int seq = a.slots ? a.slots[b] : b;
     uint16_t *dst = a.cache + ((size_t)seq * a.seq_stride + (wr ? p : 0)) * kvd;
     float *ko = a.kv_out ? a.kv_out + (size_t)b * kvd : nullptr;
-    for (int i = 2 * tid; i < a.kvl; i += 512) {
-        const float y0 = comp[i] * inv * bf16_f32(a.kv_norm[i]);
-        const float y1 = comp[i + 1] * inv * bf16_f32(a.kv_norm[i + 1]);
+    {
+        const int i = 2 * tid;
+        const float y0 = cv.x * inv * bf16_lo(nw);
+        const float y1 = cv.y * inv * bf16_hi(nw);
         if (wr) *(uint32_t *)(dst + i) = (uint32_t)bf16_rne_keepnan(y0) | (uint32_t)bf16_rne_keepnan(y1) << 16;
         if (ko) { ko[i] = y0; ko[i + 1] = y1; }
     }
-    for (int j = tid; j < half; j += 256) {
+    if (tid < half) {
+        const int j = tid;
         const float c = cs[0][j], s = cs[1][j];
-        const float x0 = comp[a.kvl + 2 * j], x1 = comp[a.kvl + 2 * j + 1];
-        const int o0 = a.kvl + (a.interleaved ? j : 2 * j);
-        const int o1 = a.kvl + (a.interleaved ? half + j : 2 * j + 1);
+        const float x0 = kp.x, x1 = kp.y;
+        const int o0 = KVL + (a.interleaved ? j : 2 * j);
+        const int o1 = KVL + (a.interleaved ? half + j : 2 * j + 1);
         const float r0 = x0 * c - x1 * s;
         const float r1 = a.interleaved ? x1 * c + x0 * s : x0 * s + x1 * c;
         if (wr) { dst[o0] = bf16_rne_keepnan(r0); dst[o1] = bf16_rne_keepnan(r1); }
