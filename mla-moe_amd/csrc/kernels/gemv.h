@@ -30,13 +30,21 @@ __device__ __forceinline__ void gemv_load_x(f32x4 (&xv)[NB][GV_PPL][2], const fl
 #pragma unroll
     for (int t = 0; t < NB; t++) {
         ss[t] = 0.0f;
+        /* loads at clamped addresses, unconditionally, zeroed after: a load
+         * under a condition becomes a branch around it, each then waited
+         * for on its own */
+#pragma unroll
+        for (int j = 0; j < GV_PPL; j++) {
+            const int p = min(lane + MM_WAVE * j, np - 1);
+            const float *src = x + (size_t)min(t, B - 1) * H + 8 * p;
+            xv[t][j][0] = *(const f32x4 *)src;
+            xv[t][j][1] = *(const f32x4 *)(src + 4);
+        }
 #pragma unroll
         for (int j = 0; j < GV_PPL; j++) {
             const int p = lane + MM_WAVE * j;
-            const bool ok = j < ppl && p < np && t < B;
-            const float *src = x + (size_t)min(t, B - 1) * H + 8 * (ok ? p : 0);
-            xv[t][j][0] = ok ? *(const f32x4 *)src : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-            xv[t][j][1] = ok ? *(const f32x4 *)(src + 4) : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            if (!(j < ppl && p < np && t < B))
+                xv[t][j][0] = xv[t][j][1] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -48,7 +56,8 @@ __device__ __forceinline__ void gemv_load_x(f32x4 (&xv)[NB][GV_PPL][2], const fl
         for (int j = 0; j < GV_PPL; j++) {
             const int p = lane + MM_WAVE * j;
             const bool ok = j < ppl && p < np;
-            const u32x4 nw = ok ? *(const u32x4 *)(norm + 8 * p) : (u32x4){0u, 0u, 0u, 0u};
+            const u32x4 nl = *(const u32x4 *)(norm + 8 * min(p, np - 1));
+            const u32x4 nw = ok ? nl : (u32x4){0u, 0u, 0u, 0u};
             const float wn[8] = {bf16_lo(nw.x), bf16_hi(nw.x), bf16_lo(nw.y), bf16_hi(nw.y),
                                  bf16_lo(nw.z), bf16_hi(nw.z), bf16_lo(nw.w), bf16_hi(nw.w)};
 #pragma unroll
@@ -92,13 +101,14 @@ __device__ __forceinline__ void gemv_rows(const f32x4 (&xv)[NB][GV_PPL][2], int 
         for (int r = 0; r < GV_RPW; r++) {
             const uint16_t *wr = rowptr(min(r0 + r, nrows - 1));
 #pragma unroll
-            for (int j = 0; j < GV_PPL; j++) {
-                const int p = lane + MM_WAVE * j;
-                wv[r][j] = (j < ppl && p < np)
-                               ? __builtin_nontemporal_load((const u32x4 *)wr + p)
-                               : (u32x4){0u, 0u, 0u, 0u};
-            }
+            for (int j = 0; j < GV_PPL; j++)
+                wv[r][j] = __builtin_nontemporal_load((const u32x4 *)wr + min(lane + MM_WAVE * j, np - 1));
         }
+#pragma unroll
+        for (int r = 0; r < GV_RPW; r++)
+#pragma unroll
+            for (int j = 0; j < GV_PPL; j++)
+                if (!(j < ppl && lane + MM_WAVE * j < np)) wv[r][j] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
         for (int r = 0; r < GV_RPW; r++) {
             float acc[NB];
