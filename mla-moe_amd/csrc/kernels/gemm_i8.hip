@@ -355,23 +355,41 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         const int nst = first ? 0 : NST;
         auto kloop = [&](auto nri_c) {
             constexpr int NRI = decltype(nri_c)::value;
-            auto kstep = [&](auto d_c, int h) {
+            /* FULL: a step of a whole turn of 6 (h0 + 6 <= lkb), whose
+             * loads are issued unconditionally.  A load under a condition is
+             * a branch, and the compiler then waits for every outstanding
+             * load (vmcnt(0)) before the next MFMAs, draining the B ring at
+             * each step.  In a whole turn: step 0 of the tile re-issues A(1)
+             * (same bytes into the same slot as the head's, read from step 2
+             * on), and near the tile's end B and A are issued at clamped
+             * indices (a B step into the free register slot, an A stage into
+             * the LDS slot that no later step of the tile reads; the tile ends
+             * with vmcnt(0) before the next head).  Extra later loads only
+             * make a hand-counted wait stricter, except at step 1, whose
+             * count includes the re-issued A(1). */
+            auto kstep = [&](auto d_c, int h, auto full_c) {
                 constexpr int D = decltype(d_c)::value;     /* h % 6 */
+                constexpr bool FULL = decltype(full_c)::value;
                 constexpr int J = D & 1, SB = D % BT_NSB;
                 const int sa_slot = (h >> 1) & 1;
                 const bool more = h + 1 < lkb;
-                if (h == 0) vmcnt_wait_rt(4 * (lkb > 1) + 4 * (lkb > 2) + nst);
-                else if (h == 1) vmcnt_wait_rt(8 * (lkb > 2) + nst);
+                if (D == 0 && h == 0) vmcnt_wait_rt(4 * (lkb > 1) + 4 * (lkb > 2) + nst);
+                else if (D == 1 && h == 1) vmcnt_wait_rt((FULL ? 12 : 8 * (lkb > 2)) + nst);
                 else if (J == 0) {
-                    if (more) VMCNT_WAIT(BT_LB); else VMCNT_WAIT(0);
+                    if (FULL || more) VMCNT_WAIT(BT_LB); else VMCNT_WAIT(0);
                 } else {
-                    if (more) VMCNT_WAIT(2 * BT_LB); else VMCNT_WAIT(0);
+                    if (FULL || more) VMCNT_WAIT(2 * BT_LB); else VMCNT_WAIT(0);
                 }
                 if (J == 0) __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                /* A(1) is part of the head */
-                if (J == 0 && h > 0 && h + 2 < lkb) issue_a((h >> 1) + 1, sa_slot ^ 1);
-                if (h + 2 < lkb) issue_b((D + 2) % BT_NSB, h + 2);
+                if (FULL) {
+                    if (J == 0) issue_a(min((h >> 1) + 1, (lkb - 1) >> 1), sa_slot ^ 1);
+                    issue_b((D + 2) % BT_NSB, min(h + 2, lkb - 1));
+                } else {
+                    /* A(1) is part of the head */
+                    if (J == 0 && h > 0 && h + 2 < lkb) issue_a((h >> 1) + 1, sa_slot ^ 1);
+                    if (h + 2 < lkb) issue_b((D + 2) % BT_NSB, h + 2);
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 const uint32_t sb = lds0 + (uint32_t)(sa_slot * BT_A_BYTES);
 #pragma unroll
@@ -389,20 +407,22 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
                 }
             };
             using std::integral_constant;
+            using T_ = std::true_type;
+            using F_ = std::false_type;
             int h0 = 0;
             for (; h0 + 6 <= lkb; h0 += 6) {
-                kstep(integral_constant<int, 0>(), h0);
-                kstep(integral_constant<int, 1>(), h0 + 1);
-                kstep(integral_constant<int, 2>(), h0 + 2);
-                kstep(integral_constant<int, 3>(), h0 + 3);
-                kstep(integral_constant<int, 4>(), h0 + 4);
-                kstep(integral_constant<int, 5>(), h0 + 5);
+                kstep(integral_constant<int, 0>(), h0, T_());
+                kstep(integral_constant<int, 1>(), h0 + 1, T_());
+                kstep(integral_constant<int, 2>(), h0 + 2, T_());
+                kstep(integral_constant<int, 3>(), h0 + 3, T_());
+                kstep(integral_constant<int, 4>(), h0 + 4, T_());
+                kstep(integral_constant<int, 5>(), h0 + 5, T_());
             }
-            if (h0 < lkb) kstep(integral_constant<int, 0>(), h0);
-            if (h0 + 1 < lkb) kstep(integral_constant<int, 1>(), h0 + 1);
-            if (h0 + 2 < lkb) kstep(integral_constant<int, 2>(), h0 + 2);
-            if (h0 + 3 < lkb) kstep(integral_constant<int, 3>(), h0 + 3);
-            if (h0 + 4 < lkb) kstep(integral_constant<int, 4>(), h0 + 4);
+            if (h0 < lkb) kstep(integral_constant<int, 0>(), h0, F_());
+            if (h0 + 1 < lkb) kstep(integral_constant<int, 1>(), h0 + 1, F_());
+            if (h0 + 2 < lkb) kstep(integral_constant<int, 2>(), h0 + 2, F_());
+            if (h0 + 3 < lkb) kstep(integral_constant<int, 3>(), h0 + 3, F_());
+            if (h0 + 4 < lkb) kstep(integral_constant<int, 4>(), h0 + 4, F_());
         };
         if (nri >= 4) kloop(std::integral_constant<int, 4>());
         else if (nri == 3) kloop(std::integral_constant<int, 3>());
