@@ -81,6 +81,32 @@ __device__ __forceinline__ void lds_dma16(const void *src, void *dst) {
     __builtin_amdgcn_global_load_lds((glb_void_t *)src, (lds_void_t *)dst, 16, 0, 0);
 }
 
+/* Buffer resource of a raw byte range (four scalar registers):
+ * base, no stride, num_records bytes, the raw 32-bit format word. */
+typedef uint32_t rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ rsrc_t raw_rsrc(const void *base, uint32_t num_records) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    rsrc_t r;
+    r.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
+    r.z = num_records;
+    r.w = 0x00020000u;
+    return r;
+}
+
+/* 16 bytes per lane at byte offset `voff` of buffer `r` into LDS at byte
+ * address `dst` (wave-uniform) + 16 * lane, as inline assembly.  An offset
+ * past num_records reads no memory and stages zeros.  The compiler does not
+ * see this LDS write, so it adds no wait for the load before later LDS
+ * accesses (for a direct-to-LDS load it knows of, it waits for every load
+ * and store in flight before any LDS read it cannot tell apart from the
+ * destination); the caller orders every access to the destination itself,
+ * with vmcnt waits and barriers. */
+__device__ __forceinline__ void lds_dma16_buf(uint32_t voff, rsrc_t r, uint32_t dst) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 : : "v"(voff), "s"(r), "{m0}"(__builtin_amdgcn_readfirstlane(dst)) : "memory");
+}
+
 /* LDS byte address of a __shared__ location. */
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const lds_void_t *)p;

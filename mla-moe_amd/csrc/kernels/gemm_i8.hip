@@ -63,6 +63,9 @@ __device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
 #define BT_NSA 2                 /* A ring (LDS): one stage in flight, one consumed */
 #define BT_NSB 3                 /* B ring (registers): 64-byte K steps, two in flight */
 #define BT_LB 4                  /* B loads per wave per 64-byte K step */
+/* A buffer range and the offset of padding rows past it (A offsets are
+ * below 2^31; a K step adds less than 2^16) */
+#define BT_A_OOB 0xFFFF0000u
 #define BT_NST_GU 16             /* epilogue stores per wave: gate/up, plain */
 #define BT_NST_PLAIN 32
 static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
@@ -119,10 +122,21 @@ __device__ __forceinline__ void lds_wait_regs(i32x4 (&A)[N]) {
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]));
 }
 
+/* A wave-uniform pointer held in scalar registers. */
+template <class P>
+__device__ __forceinline__ P *uniform_ptr(P *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (P *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 /* Per-block schedule and row tables in LDS. */
 struct bt_shared {
     int gstart[MM_EMAX + 1];                 /* segment 0: exclusive prefix of 128-row groups */
+    int cnt[MM_EMAX];                        /* segment 0: rows of each expert (<= T) */
     int g1;                                  /* segment 1 (one expert): its row groups */
+    int m1;                                  /* segment 1: its rows */
     int n0, n;                               /* tiles of segment 0, of both */
     int arow[2][MM_I8B_BM];                  /* A row of each tile row (two tiles in flight) */
     __attribute__((aligned(16))) int rid[2][MM_I8B_BM];     /* output row id, -1 = padding */
@@ -143,7 +157,9 @@ __device__ __forceinline__ int bt_nslab(const mm_i8_tiled_args &g) {
 
 /* Tiles are ordered (segment, expert, slab, row group): expert e of
  * segment 0 owns tiles [nslab gstart[e], nslab gstart[e + 1]); segment 1
- * follows.  Uniform over the block. */
+ * follows.  Uniform over the block (made explicit, so that the segment's
+ * fields are scalar loads).  Reads LDS only: no global load here whose
+ * wait would also wait for the stores and loads in flight. */
 __device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt_shared &sh,
                                                 int t) {
     bt_tile_id id;
@@ -161,7 +177,7 @@ __device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt
         id.e = lo;
         id.slab = loc / ge;
         id.m0 = (loc % ge) * MM_I8B_BM;
-        id.M = g.cnt ? min(g.cnt[lo * MM_CNT_STRIDE], g.T) : g.T;
+        id.M = sh.cnt[lo];
     } else {
         const mm_i8_tiled_args &g = a.seg[1];
         const int loc = t - sh.n0;
@@ -169,16 +185,29 @@ __device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt
         id.e = 0;
         id.slab = loc / sh.g1;
         id.m0 = (loc % sh.g1) * MM_I8B_BM;
-        id.M = g.T;
+        id.M = sh.m1;
     }
+    id.si = __builtin_amdgcn_readfirstlane(id.si);
+    id.e = __builtin_amdgcn_readfirstlane(id.e);
+    id.slab = __builtin_amdgcn_readfirstlane(id.slab);
+    id.m0 = __builtin_amdgcn_readfirstlane(id.m0);
+    id.M = __builtin_amdgcn_readfirstlane(id.M);
     return id;
 }
 
-/* Row id and A row of tile row `r` (threads r < 128). */
-__device__ __forceinline__ void bt_row(const mm_i8_tiled_args &g, const bt_tile_id &id, int r,
-                                       int *rid, int *arow) {
+/* Row id and A row of tile row `r` (r < 128) in two parts: the load (always
+ * issued, from the scale array where the segment has no row list, so that
+ * no branch joins a value still in flight) and, where the value is used,
+ * the ids. */
+__device__ __forceinline__ int bt_row_load(const mm_i8_tiled_args &g, const bt_tile_id &id, int r) {
     const int m = id.m0 + r < id.M ? id.m0 + r : id.m0;
-    const int q = g.rows ? g.rows[(size_t)id.e * g.T + m] : m;
+    const int *p = g.rows ? g.rows + (size_t)id.e * g.T + m : (const int *)g.sa;
+    return *p;
+}
+__device__ __forceinline__ void bt_row_ids(const mm_i8_tiled_args &g, const bt_tile_id &id, int r,
+                                           int raw, int *rid, int *arow) {
+    const int m = id.m0 + r < id.M ? id.m0 + r : id.m0;
+    const int q = g.rows ? raw : m;
     *arow = (g.a_by_route || !g.rows) ? q : q / g.K;
     *rid = id.m0 + r < id.M ? q : -1;
 }
@@ -219,17 +248,20 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
     uint32_t arow_off[4];
     int aq[4];
     __amdgpu_buffer_rsrc_t brs;
-    const int8_t *aptr;
+    rsrc_t ars;
     uint32_t boff[2];
     int lkb, bstep;
     auto set_tile = [&](const bt_tile_id &id, int buf) {
         const mm_i8_tiled_args &g = a.seg[id.si];
         lkb = g.Kd / 64;
-        aptr = g.a;
+        /* A rows past the tile's valid rows: an offset past the range (no
+         * memory read, zeros staged; their results are not stored) */
+        ars = raw_rsrc(g.a, BT_A_OOB);
+        const int vrows = min(id.M - id.m0, MM_I8B_BM);
 #pragma unroll
         for (int h = 0; h < 4; h++) {
             const int R = 8 * (4 * wave + h) + (lane >> 3);
-            arow_off[h] = (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd;
+            arow_off[h] = R < vrows ? (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd : BT_A_OOB;
             aq[h] = (lane & 7) ^ swz128(R);
         }
         const int ncb = g.N / 16;
@@ -256,8 +288,8 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         const bool full = 2 * s + 1 < lkb;
 #pragma unroll
         for (int h = 0; h < 4; h++)
-            lds_dma16(aptr + (arow_off[h] + (uint32_t)(s * BT_KB + 16 * (full ? aq[h] : aq[h] & 3))),
-                      lds + st + (4 * wave + h) * 1024);
+            lds_dma16_buf(arow_off[h] + (uint32_t)(s * BT_KB + 16 * (full ? aq[h] : aq[h] & 3)), ars,
+                          lds0 + st + (uint32_t)((4 * wave + h) * 1024));
     };
     auto issue_b = [&](int slot, int h) {
         const int so = __builtin_amdgcn_readfirstlane(h * bstep);
@@ -271,12 +303,16 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
 
     /* a tile's head: its first two A stages and first two B steps, issued
      * before the previous tile's epilogue stores so that the tile's first
-     * two steps wait for none of those stores */
+     * two steps wait for none of those stores.  Always four groups of loads
+     * (a tile of one K step re-reads B(0) into slot 1, one of at most two
+     * steps A(0) into slot 1, neither read by the tile): loads under a
+     * condition would leave the ring registers defined on some paths only,
+     * and the compiler's copies at the join wait for every load in flight. */
     auto issue_head = [&]() {
         issue_a(0, 0);
         issue_b(0, 0);
-        if (lkb > 1) issue_b(1, 1);
-        if (lkb > 2) issue_a(1, 1);
+        issue_b(1, min(1, lkb - 1));
+        issue_a(min(1, (lkb - 1) >> 1), 1);
     };
 
     /* A operand of row block ri, K step h, half ks: row 32 ri + l % 32,
@@ -289,10 +325,9 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
     /* ---- first tile ---- */
     bt_tile_id cur = bt_decode(a, sh, xl(t));
     int buf = 0;
-    bool first = true;
     if (tid < MM_I8B_BM) {
         int rid, arow;
-        bt_row(a.seg[cur.si], cur, tid, &rid, &arow);
+        bt_row_ids(a.seg[cur.si], cur, tid, bt_row_load(a.seg[cur.si], cur, tid), &rid, &arow);
         sh.rid[0][tid] = rid;
         sh.arow[0][tid] = arow;
     }
@@ -300,7 +335,13 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
     set_tile(cur, 0);
     issue_head();
 
-    for (;;) {
+    /* one tile: K loop, then the next tile's head and this tile's epilogue;
+     * false after the last.  The first tile is a copy of its own (FIRST: no
+     * epilogue stores follow its head), so that every entry into the
+     * loop's copy comes after the same loads and stores and the compiler's
+     * own wait counts there stay exact. */
+    auto tile = [&](auto first_c) -> bool {
+        constexpr bool FIRST = decltype(first_c)::value;
         const mm_i8_tiled_args &g = a.seg[cur.si];
         const int tn = t + t_step;
         const bool has_next = tn < t_end;
@@ -308,19 +349,25 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
 
         /* loads whose results are used after the K loop: this tile's row
          * scales and column scales (thread tid: slab column tid, gate/up:
-         * gate column tid or up column tid - 128), the next tile's row ids */
-        float sa_r = 0.0f;
-        int nrid = -1, narow = 0;
-        if (tid < MM_I8B_BM) {
-            sa_r = g.sa[sh.arow[buf][tid]];
-            if (has_next) bt_row(a.seg[nxt.si], nxt, tid, &nrid, &narow);
-        }
+         * gate column tid or up column tid - 128), the next tile's row ids.
+         * Every thread issues them (tile row clamped to 127) and the values
+         * are first used after the K loop: the first use of a load, or a
+         * branch joining its value, is where the compiler waits for it, and
+         * that wait would also take the previous tile's stores and this
+         * tile's head. */
+        const int trow = min(tid, MM_I8B_BM - 1);
+        const float sa_r = g.sa[sh.arow[buf][trow]];
+        const int nraw = bt_row_load(a.seg[nxt.si], nxt, trow);
         const int N = g.N;
         const int slab_c0 = cur.slab * (GU ? 128 : 256);   /* first output column of the slab */
         float cs_r;
         {
-            const float *sb = (GU && tid >= 128 ? g.sb1 : g.sb0) + (size_t)cur.e * g.sb_expert_stride;
-            cs_r = sb[min(slab_c0 + (GU ? (tid & 127) : tid), N - 1)];
+            /* both pointers in scalar registers before the per-thread choice
+             * (else the choice is made on the fields' addresses: a divergent
+             * load of the pointer, then a dependent load) */
+            const float *sb = (GU && tid >= 128 ? uniform_ptr(g.sb1) : uniform_ptr(g.sb0)) +
+                              (size_t)cur.e * g.sb_expert_stride;
+            cs_r = ((const __attribute__((address_space(1))) float *)sb)[min(slab_c0 + (GU ? (tid & 127) : tid), N - 1)];
         }
 
         /* ---- K loop ---- */
@@ -329,10 +376,14 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         for (int ri = 0; ri < 4; ri++)
 #pragma unroll
             for (int cj = 0; cj < 2; cj++) acc[ri][cj] = (v16i){};
-        /* 32-row blocks that hold valid rows (uniform over the block):
-         * padding-only blocks skip their reads and MFMAs */
-        const int vrows = min(cur.M - cur.m0, MM_I8B_BM);
-        const int nri = __builtin_amdgcn_readfirstlane((vrows + 31) >> 5);
+        /* Every tile runs all four 32-row blocks, padding included (its A
+         * rows are staged as zeros without a memory read; its results go to
+         * the spare row): the loop is bound by the operands it takes in, not
+         * by its MFMAs (a tile of one valid row block took as long as a full
+         * one), and one form of the loop keeps the head's ring registers
+         * where the loop reads them (with a form per row-block count the
+         * compiler copies them on entry, and a copy of a register still
+         * being loaded waits for every load and store in flight). */
         /* step h (64 bytes of K): A stage s = h / 2 in LDS slot s % 2, B in
          * register slot h % 3.  Loads are issued in this order: the tile's
          * head A(0), B(0), B(1), A(1), B(2); then at each even step 2 s >= 2,
@@ -344,15 +395,16 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
          * 2 s + 1 >= 3 needs B(2 s + 1), after which A(s + 1) and B(2 s + 2)
          * were issued (2 BT_LB).  The tile's head is A(0), B(0), B(1), A(1),
          * followed on a later tile by the previous tile's epilogue stores
-         * (exactly NST per wave); step 0 issues B(2).  Steps 0 and 1 need
-         * head loads issued before the stores, which may stay outstanding
-         * until step 2.  Near the end of the tile
+         * (exactly NST per wave); step 0 issues B(2) (and, in a whole turn,
+         * A(1) again).  Steps 0 and 1 need head loads issued before the
+         * stores, which may stay outstanding until step 2.  Near the end of
+         * the tile
          * fewer loads follow, and the counts shrink accordingly (0: wait for
          * all).  The barrier of an even step makes every wave's A rows of
          * stage s visible and frees slot (s + 1) % 2, read by every wave
          * during steps 2 s - 2 and 2 s - 1 (or by the previous tile). */
         constexpr int NST = GU ? BT_NST_GU : BT_NST_PLAIN;
-        const int nst = first ? 0 : NST;
+        constexpr int NSTF = FIRST ? 0 : NST;   /* stores issued after the head */
         auto kloop = [&](auto nri_c) {
             constexpr int NRI = decltype(nri_c)::value;
             /* FULL: a step of a whole turn of 6 (h0 + 6 <= lkb), whose
@@ -367,18 +419,26 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
              * with vmcnt(0) before the next head).  Extra later loads only
              * make a hand-counted wait stricter, except at step 1, whose
              * count includes the re-issued A(1). */
-            auto kstep = [&](auto d_c, int h, auto full_c) {
+            auto kstep = [&](auto d_c, int h, auto full_c, auto ft_c) {
                 constexpr int D = decltype(d_c)::value;     /* h % 6 */
                 constexpr bool FULL = decltype(full_c)::value;
+                constexpr bool FT = decltype(ft_c)::value;  /* the tile's first whole turn */
                 constexpr int J = D & 1, SB = D % BT_NSB;
                 const int sa_slot = (h >> 1) & 1;
                 const bool more = h + 1 < lkb;
-                if (D == 0 && h == 0) vmcnt_wait_rt(4 * (lkb > 1) + 4 * (lkb > 2) + nst);
-                else if (D == 1 && h == 1) vmcnt_wait_rt((FULL ? 12 : 8 * (lkb > 2)) + nst);
-                else if (J == 0) {
-                    if (FULL || more) VMCNT_WAIT(BT_LB); else VMCNT_WAIT(0);
+                if (FULL) {
+                    if (FT && D == 0) VMCNT_WAIT(2 * BT_LB + NSTF);
+                    else if (FT && D == 1) VMCNT_WAIT(3 * BT_LB + NSTF);
+                    else if (J == 0) VMCNT_WAIT(BT_LB);
+                    else VMCNT_WAIT(2 * BT_LB);
+                } else if (D == 0 && h == 0) {
+                    VMCNT_WAIT(2 * BT_LB + NSTF);
+                } else if (D == 1 && h == 1) {
+                    vmcnt_wait_rt(BT_LB + BT_LB * (lkb > 2) + NSTF);
+                } else if (J == 0) {
+                    if (more) VMCNT_WAIT(BT_LB); else VMCNT_WAIT(0);
                 } else {
-                    if (FULL || more) VMCNT_WAIT(2 * BT_LB); else VMCNT_WAIT(0);
+                    if (more) VMCNT_WAIT(2 * BT_LB); else VMCNT_WAIT(0);
                 }
                 if (J == 0) __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
@@ -409,30 +469,36 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
             using std::integral_constant;
             using T_ = std::true_type;
             using F_ = std::false_type;
+            /* the first whole turn is a copy of its own (its waits count the
+             * head and the stores after it), so that every entry into the
+             * turn loop follows a whole turn and the compiler's own counts
+             * there stay exact */
+            auto turn = [&](int h0, auto ft_c) {
+                kstep(integral_constant<int, 0>(), h0, T_(), ft_c);
+                kstep(integral_constant<int, 1>(), h0 + 1, T_(), ft_c);
+                kstep(integral_constant<int, 2>(), h0 + 2, T_(), ft_c);
+                kstep(integral_constant<int, 3>(), h0 + 3, T_(), ft_c);
+                kstep(integral_constant<int, 4>(), h0 + 4, T_(), ft_c);
+                kstep(integral_constant<int, 5>(), h0 + 5, T_(), ft_c);
+            };
             int h0 = 0;
-            for (; h0 + 6 <= lkb; h0 += 6) {
-                kstep(integral_constant<int, 0>(), h0, T_());
-                kstep(integral_constant<int, 1>(), h0 + 1, T_());
-                kstep(integral_constant<int, 2>(), h0 + 2, T_());
-                kstep(integral_constant<int, 3>(), h0 + 3, T_());
-                kstep(integral_constant<int, 4>(), h0 + 4, T_());
-                kstep(integral_constant<int, 5>(), h0 + 5, T_());
+            if (lkb >= 6) {
+                turn(0, T_());
+                for (h0 = 6; h0 + 6 <= lkb; h0 += 6) turn(h0, F_());
             }
-            if (h0 < lkb) kstep(integral_constant<int, 0>(), h0, F_());
-            if (h0 + 1 < lkb) kstep(integral_constant<int, 1>(), h0 + 1, F_());
-            if (h0 + 2 < lkb) kstep(integral_constant<int, 2>(), h0 + 2, F_());
-            if (h0 + 3 < lkb) kstep(integral_constant<int, 3>(), h0 + 3, F_());
-            if (h0 + 4 < lkb) kstep(integral_constant<int, 4>(), h0 + 4, F_());
+            if (h0 < lkb) kstep(integral_constant<int, 0>(), h0, F_(), F_());
+            if (h0 + 1 < lkb) kstep(integral_constant<int, 1>(), h0 + 1, F_(), F_());
+            if (h0 + 2 < lkb) kstep(integral_constant<int, 2>(), h0 + 2, F_(), F_());
+            if (h0 + 3 < lkb) kstep(integral_constant<int, 3>(), h0 + 3, F_(), F_());
+            if (h0 + 4 < lkb) kstep(integral_constant<int, 4>(), h0 + 4, F_(), F_());
         };
-        if (nri >= 4) kloop(std::integral_constant<int, 4>());
-        else if (nri == 3) kloop(std::integral_constant<int, 3>());
-        else if (nri == 2) kloop(std::integral_constant<int, 2>());
-        else kloop(std::integral_constant<int, 1>());
-        first = false;
+        kloop(std::integral_constant<int, 4>());
         VMCNT_WAIT(0);
 
         /* row tables: this tile's scales, the next tile's rows */
         if (tid < MM_I8B_BM) {
+            int nrid = -1, narow = 0;
+            if (has_next) bt_row_ids(a.seg[nxt.si], nxt, tid, nraw, &nrid, &narow);
             sh.sa[buf][tid] = sa_r;
             sh.rid[buf ^ 1][tid] = nrid;
             sh.arow[buf ^ 1][tid] = narow;
@@ -440,11 +506,12 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         sh.cs[buf][tid] = cs_r;
         __syncthreads();
         /* the next tile's head goes out before this tile's stores (its third
-         * B step after them) */
-        if (has_next) {
-            set_tile(nxt, buf ^ 1);
-            issue_head();
-        }
+         * B step after them); after the last tile a head of this tile again
+         * (nxt == cur, row 0 of the segment for every row: valid addresses
+         * into LDS slots and registers nothing reads, waited for at the end),
+         * so that the head's loads are never under a condition */
+        set_tile(nxt, buf ^ 1);
+        issue_head();
 
         /* ---- epilogue ----
          * accumulator register 4 g + i of lane l is row 32 ri + l % 32,
@@ -520,11 +587,15 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
                 }
             }
         }
-        if (!has_next) break;
+        if (!has_next) return false;
         t = tn;
         cur = nxt;
         buf ^= 1;
-    }
+        return true;
+    };
+    if (tile(std::true_type{}))
+        while (tile(std::false_type{})) {
+        }
     VMCNT_WAIT(0);
 }
 
@@ -549,6 +620,7 @@ __device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
             const int e = e0 + lane;
             const int M = e < E ? (g0.cnt ? min(g0.cnt[e * MM_CNT_STRIDE], g0.T) : g0.T) : 0;
             const int nt = (M + MM_I8B_BM - 1) / MM_I8B_BM;
+            if (e < E) sh.cnt[e] = M;
             int incl = nt;
 #pragma unroll
             for (int off = 1; off < MM_WAVE; off <<= 1) {
@@ -562,6 +634,7 @@ __device__ __forceinline__ void bt_kernel(const mm_i8_bt_args &a) {
             sh.gstart[E] = base;
             sh.n0 = base * bt_nslab(g0);
             sh.g1 = a.nseg > 1 ? (a.seg[1].T + MM_I8B_BM - 1) / MM_I8B_BM : 0;
+            sh.m1 = a.nseg > 1 ? a.seg[1].T : 0;
             sh.n = sh.n0 + (a.nseg > 1 ? sh.g1 * bt_nslab(a.seg[1]) : 0);
         }
     }
