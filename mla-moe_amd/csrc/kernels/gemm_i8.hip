@@ -376,14 +376,13 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         for (int ri = 0; ri < 4; ri++)
 #pragma unroll
             for (int cj = 0; cj < 2; cj++) acc[ri][cj] = (v16i){};
-        /* Every tile runs all four 32-row blocks, padding included (its A
-         * rows are staged as zeros without a memory read; its results go to
-         * the spare row): the loop is bound by the operands it takes in, not
-         * by its MFMAs (a tile of one valid row block took as long as a full
-         * one), and one form of the loop keeps the head's ring registers
-         * where the loop reads them (with a form per row-block count the
-         * compiler copies them on entry, and a copy of a register still
-         * being loaded waits for every load and store in flight). */
+        /* One form of the loop for every tile: 32-row blocks made only of
+         * padding (A rows staged as zeros without a memory read, results to
+         * the spare row) skip their MFMAs by a uniform branch.  With a form
+         * per row-block count the compiler copies the head's ring registers
+         * on entry, and a copy of a register still being loaded waits for
+         * every load and store in flight. */
+        const int nri = __builtin_amdgcn_readfirstlane((min(cur.M - cur.m0, MM_I8B_BM) + 31) >> 5);
         /* step h (64 bytes of K): A stage s = h / 2 in LDS slot s % 2, B in
          * register slot h % 3.  Loads are issued in this order: the tile's
          * head A(0), B(0), B(1), A(1), B(2); then at each even step 2 s >= 2,
@@ -461,9 +460,10 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
                     lds_wait_regs(A);
 #pragma unroll
                     for (int ri = 0; ri < NRI; ri++)
+                        if (ri == 0 || ri < nri)   /* uniform: padding-only blocks skip */
 #pragma unroll
-                        for (int cj = 0; cj < 2; cj++)
-                            acc[ri][cj] = mfma32_i8(bq[SB][cj][ks], A[ri], acc[ri][cj]);
+                            for (int cj = 0; cj < 2; cj++)
+                                acc[ri][cj] = mfma32_i8(bq[SB][cj][ks], A[ri], acc[ri][cj]);
                 }
             };
             using std::integral_constant;
