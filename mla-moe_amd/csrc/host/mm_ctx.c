@@ -171,6 +171,11 @@ int mm_ctx_create(int device, mm_ctx **out) {
     c->mla_part_max = MM_MLA_PART_MAX;
     ev = getenv("MLAMOE_MLA_PART_MAX");
     if (ev && *ev && atoll(ev) > 0) c->mla_part_max = (size_t)atoll(ev);
+    /* MLAMOE_MOE_T_CHUNK lowers the rows of one MoE forward pass (longer
+     * calls run in chunks of it; for testing that the chunks agree) */
+    c->moe_t_chunk = 0;
+    ev = getenv("MLAMOE_MOE_T_CHUNK");
+    if (ev && *ev && atoi(ev) > 0) c->moe_t_chunk = atoi(ev);
     if ((st = mm_noalloc_setup(c))) goto fail;
     *out = c;
     return MM_OK;

@@ -129,6 +129,7 @@ struct mm_ctx {
 
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
     size_t mla_part_max;        /* attention chunk partials per launch (bytes) */
+    int moe_t_chunk;            /* cap on the rows of one MoE forward pass (0: MM_MOE_T_CHUNK) */
 
     /* growable device workspace */
     void *ws;

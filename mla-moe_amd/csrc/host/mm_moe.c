@@ -197,6 +197,19 @@ out:;
     return st;
 }
 
+/* Shapes the int8 kernels take: K dimensions (hidden, moe_inter and the
+ * shared experts' concatenated inter size) multiples of 64 and below 2^16
+ * (the tiled GEMMs' 32-bit activation offsets leave 2^16 past the matrix
+ * for padding rows). */
+static int i8_cfg_ok(const mm_moe_config *g) {
+    return g->hidden_size > 0 && g->n_routed_experts > 0 && g->moe_inter_size > 0 &&
+           g->n_shared_experts >= 0 && g->hidden_size % 64 == 0 && g->moe_inter_size % 64 == 0 &&
+           g->hidden_size < 65536 && g->moe_inter_size < 65536 &&
+           (size_t)g->n_shared_experts * g->moe_inter_size < 65536;
+}
+#define I8_CFG_MSG "needs hidden and moe_inter multiples of 64, and hidden, moe_inter and " \
+                   "n_shared x moe_inter below 65536"
+
 int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsigned flags) {
     if (!c || !w) return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: NULL argument");
     if (!c->moe_ready) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer: call mm_moe_init first");
@@ -204,10 +217,8 @@ int mm_moe_load_layer(mm_ctx *c, int layer, const mm_moe_layer_weights *w, unsig
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: layer %d out of range", layer);
     if (!(flags & (MM_LOAD_BF16 | MM_LOAD_INT8)))
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: no weight format requested");
-    if ((flags & MM_LOAD_INT8) &&
-        (c->moe.hidden_size % 64 || c->moe.moe_inter_size % 64))
-        return mm_fail(MM_ERR_UNSUPPORTED,
-                       "mm_moe_load_layer: int8 format needs hidden and moe_inter multiples of 64");
+    if ((flags & MM_LOAD_INT8) && !i8_cfg_ok(&c->moe))
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_load_layer: int8 format " I8_CFG_MSG);
     if (!w->moe_gate || !w->expert_gate || !w->expert_up || !w->expert_down)
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer: NULL weight pointer");
     int st = mm_set_device(c);
@@ -306,16 +317,11 @@ int mm_moe_load_dense_layer(mm_ctx *c, int layer, const uint16_t *gate, const ui
 
 /* ---- packed int8 layers (the offline expert format) ------------------------ */
 
-static int i8_cfg_ok(const mm_moe_config *g) {
-    return g->hidden_size > 0 && g->n_routed_experts > 0 && g->moe_inter_size > 0 &&
-           g->n_shared_experts >= 0 && g->hidden_size % 64 == 0 && g->moe_inter_size % 64 == 0;
-}
-
 int mm_moe_i8_layer_size(const mm_moe_config *cfg, size_t *pool_bytes, size_t *n_scales) {
     if (!cfg || !pool_bytes || !n_scales) return mm_fail(MM_ERR_INVALID, "mm_moe_i8_layer_size: NULL argument");
     if (!i8_cfg_ok(cfg))
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_i8_layer_size: int8 format needs positive sizes "
-                       "with hidden and moe_inter multiples of 64");
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_i8_layer_size: int8 format needs positive sizes, "
+                       I8_CFG_MSG);
     i8_sizes(cfg, pool_bytes, n_scales);
     return MM_OK;
 }
@@ -344,8 +350,7 @@ int mm_moe_load_layer_i8_packed(mm_ctx *c, int layer, const uint16_t *moe_gate,
     if (layer < 0 || layer >= c->n_layers)
         return mm_fail(MM_ERR_INVALID, "mm_moe_load_layer_i8_packed: layer %d out of range", layer);
     if (!i8_cfg_ok(&c->moe))
-        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_load_layer_i8_packed: int8 format needs hidden "
-                       "and moe_inter multiples of 64");
+        return mm_fail(MM_ERR_UNSUPPORTED, "mm_moe_load_layer_i8_packed: int8 format " I8_CFG_MSG);
     mm_moe_layer *L = &c->layers[layer];
     if (L->loaded) return mm_fail(MM_ERR_STATE, "mm_moe_load_layer_i8_packed: layer %d already loaded", layer);
     int st = mm_set_device(c);
@@ -854,6 +859,24 @@ static int forward_int8(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
     return MM_OK;
 }
 
+/* Rows of one forward pass.  Every token's routing and expert rows are its
+ * own, so a longer call runs as consecutive chunks with identical results;
+ * the chunk keeps each int8 activation matrix of the tiled GEMMs (T x H,
+ * T K x I and T x S bytes) below the 32-bit range of their row offsets
+ * (MM_I8_TILED_A_MAX) and the workspace to the chunk's rows. */
+#define MM_MOE_T_CHUNK 65536
+static int moe_t_chunk(const mm_ctx *c) {
+    const mm_moe_config *g = &c->moe;
+    size_t w = g->hidden_size;
+    const size_t ki = (size_t)g->n_experts_per_tok * g->moe_inter_size;
+    const size_t s = (size_t)g->n_shared_experts * g->moe_inter_size;
+    if (ki > w) w = ki;
+    if (s > w) w = s;
+    size_t n = c->moe_t_chunk > 0 ? (size_t)c->moe_t_chunk : MM_MOE_T_CHUNK;
+    if (w && n > (MM_I8_TILED_A_MAX - 1) / w) n = (MM_I8_TILED_A_MAX - 1) / w;
+    return n > 0 ? (int)n : 1;
+}
+
 static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, const float *logits,
                    int32_t *topk_idx, float *topk_w, float *probs, unsigned flags,
                    const mm_moe_i8_debug *dbg, const mm_fixed_ws *fx) {
@@ -867,6 +890,26 @@ static int forward(mm_ctx *c, int layer, int T, const float *xn, float *out, con
     if ((uintptr_t)xn % 16 || (uintptr_t)out % 16)
         return mm_fail(MM_ERR_INVALID, "mm_moe_forward: xn/out must be 16-byte aligned");
     const mm_moe_layer *L = &c->layers[layer];
+    const int tc = moe_t_chunk(c);
+    if (T > tc) {
+        /* the debug block and the fused next-layer norm (its lo plane at row
+         * T + t) are laid out for the whole call */
+        if (dbg || c->norm_w)
+            return mm_fail(MM_ERR_INVALID, "mm_moe_forward: %d rows with debug outputs or the "
+                           "fused norm (at most %d)", T, tc);
+        const size_t H = c->moe.hidden_size, E = c->moe.n_routed_experts;
+        const size_t K = c->moe.n_experts_per_tok;
+        for (int t0 = 0; t0 < T; t0 += tc) {
+            const int n = T - t0 < tc ? T - t0 : tc;
+            const int st = forward(c, layer, n, xn + (size_t)t0 * H, out + (size_t)t0 * H,
+                                   logits ? logits + (size_t)t0 * E : NULL,
+                                   topk_idx ? topk_idx + (size_t)t0 * K : NULL,
+                                   topk_w ? topk_w + (size_t)t0 * K : NULL,
+                                   probs ? probs + (size_t)t0 * E : NULL, flags, NULL, fx);
+            if (st) return st;
+        }
+        return MM_OK;
+    }
     int st = mm_set_device(c);
     if (st) return st;
     const int acc = (flags & MM_FWD_ACCUMULATE) != 0;
@@ -894,7 +937,7 @@ int mm_moe_forward_norm(mm_ctx *c, int layer, int T, const float *xn, float *out
     *fused = 0;
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_moe_forward: NULL context");
     const int can = (flags & MM_FWD_INT8) && c->moe.hidden_size <= MM_I8_CN_MAXH &&
-                    c->moe.hidden_size % 4 == 0 && norm_w && xn_next;
+                    c->moe.hidden_size % 4 == 0 && norm_w && xn_next && T <= moe_t_chunk(c);
     if (can) {
         c->norm_w = norm_w;
         c->norm_xn = xn_next;

@@ -255,6 +255,11 @@ typedef struct {
 #define MM_I8B_BM 128
 #define MM_I8B_FR 16
 #define MM_I8B_GRID 512          /* persistent grid: 2 blocks on each of 256 CUs */
+/* The tiled GEMMs address activation rows by 32-bit byte offsets from the
+ * matrix base: matrices below MM_I8_TILED_A_MAX bytes (the host splits
+ * longer calls); offsets from it up read nothing (padding rows, plus less
+ * than 2^16 of K) */
+#define MM_I8_TILED_A_MAX 0xFFFF0000u
 /* One GEMM segment: the routed experts, or the shared expert as one dense
  * GEMM. */
 typedef struct {

@@ -63,9 +63,6 @@ __device__ __forceinline__ v16i mfma32_i8(i32x4 a, i32x4 b, v16i c) {
 #define BT_NSA 2                 /* A ring (LDS): one stage in flight, one consumed */
 #define BT_NSB 3                 /* B ring (registers): 64-byte K steps, two in flight */
 #define BT_LB 4                  /* B loads per wave per 64-byte K step */
-/* A buffer range and the offset of padding rows past it (A offsets are
- * below 2^31; a K step adds less than 2^16) */
-#define BT_A_OOB 0xFFFF0000u
 #define BT_NST_GU 16             /* epilogue stores per wave: gate/up, plain */
 #define BT_NST_PLAIN 32
 static_assert(MM_I8B_BM == 128 && MM_I8B_FR == 16, "block tile shape is fixed by the wave grid");
@@ -256,12 +253,12 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         lkb = g.Kd / 64;
         /* A rows past the tile's valid rows: an offset past the range (no
          * memory read, zeros staged; their results are not stored) */
-        ars = raw_rsrc(g.a, BT_A_OOB);
+        ars = raw_rsrc(g.a, MM_I8_TILED_A_MAX);
         const int vrows = min(id.M - id.m0, MM_I8B_BM);
 #pragma unroll
         for (int h = 0; h < 4; h++) {
             const int R = 8 * (4 * wave + h) + (lane >> 3);
-            arow_off[h] = R < vrows ? (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd : BT_A_OOB;
+            arow_off[h] = R < vrows ? (uint32_t)sh.arow[buf][R] * (uint32_t)g.Kd : MM_I8_TILED_A_MAX;
             aq[h] = (lane & 7) ^ swz128(R);
         }
         const int ncb = g.N / 16;

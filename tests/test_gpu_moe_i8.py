@@ -275,3 +275,30 @@ def test_nan_router_scores_route_distinct_experts(ctx, oracle, T):
             assert len(set(row)) == K and min(row) >= 0 and max(row) < E, (flags, t, row)
             if t >= 2:   # the oracle's scan only on NaN-free tokens
                 assert np.array_equal(idx[t], oracle.route(cfg, logits[t])[1]), (flags, t)
+
+
+def test_i8_rows_in_chunks(ctx, oracle, monkeypatch):
+    """A call longer than the forward pass's row cap runs as consecutive
+    chunks: outputs, routing and scores bit-identical to one pass (the cap
+    lowered to 37 rows through MLAMOE_MOE_T_CHUNK; by default it keeps every
+    int8 activation matrix of the tiled GEMMs below their 32-bit offsets)."""
+    H, E, K, I, NS, T = 256, 16, 4, 128, 2, 100
+    w = synth.moe_layer(120, H, E, I, NS)
+    x = synth.activations(121, T, H)
+    monkeypatch.setenv("MLAMOE_MOE_T_CHUNK", "37")
+    cc = mlamoe.Context(0)
+    try:
+        for c in (ctx, cc):
+            c.moe_init(H, E, NS, K, I)
+            c.moe_load_layer(0, w, mlamoe.MM_LOAD_INT8 | mlamoe.MM_LOAD_BF16)
+        for flags in (mlamoe.MM_FWD_INT8, mlamoe.MM_FWD_BF16):
+            one = ctx.moe_forward(0, x, flags=flags)
+            chunked = cc.moe_forward(0, x, flags=flags)
+            for a, b in zip(one, chunked):
+                assert np.array_equal(a, b), flags
+        ro, ri, *_ = oracle.ffn_i8(oracle.moe_cfg(H, E, NS, K, I), w,
+                                   oracle.quantize_moe_weights(w), x)
+        out, idx, *_ = cc.moe_forward(0, x, flags=mlamoe.MM_FWD_INT8)
+        assert np.array_equal(idx, ri) and max_abs_rel(out, ro) < TOL
+    finally:
+        cc.close()

@@ -76,6 +76,12 @@ def test_pack_layer_pieces(oracle):
     assert weights.layer_size(cfg) == (pool.size, scales.size)
     with pytest.raises(mlamoe.MMError, match="multiples of 64"):
         weights.layer_size(mlamoe.MoeConfig(H, E, NS, 2, 100, 0, 0, 1.0))
+    # K dimensions of the int8 GEMMs stay below 2^16: moe_inter itself, and the
+    # shared experts' concatenated inter size (2 x 32768)
+    for ns, inter in ((0, 65536), (2, 32768)):
+        with pytest.raises(mlamoe.MMError, match="below 65536"):
+            weights.layer_size(mlamoe.MoeConfig(H, E, ns, 2, inter, 0, 0, 1.0))
+    assert weights.layer_size(mlamoe.MoeConfig(H, E, 1, 2, 32704, 0, 0, 1.0))[0] > 0
 
 
 def test_container_roundtrip(tmp_path):
