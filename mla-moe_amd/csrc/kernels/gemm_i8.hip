@@ -92,11 +92,14 @@ __device__ __forceinline__ void vmcnt_wait_rt(int n) {
 
 /* ds_write_b128 of an f32x4 at an LDS byte address, and the wait for the
  * wave's outstanding LDS operations (the staging round trip is one wave's
- * own rows: no barrier) */
+ * own rows: no barrier).  No memory clobber: they serve the epilogue's
+ * staging rows only, which only assembly reads (volatile, so kept in order
+ * with these); with a clobber the compiler would read every LDS value it
+ * uses (scales, row ids) again after each of them. */
 __device__ __forceinline__ void ds_write16(uint32_t addr, f32x4 v) {
-    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v));
 }
-__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"); }
 
 /* registers 4 g .. 4 g + 3 of an accumulator */
 __device__ __forceinline__ i32x4 acc4(const v16i &c, int g) {
@@ -117,6 +120,14 @@ __device__ __forceinline__ void lds_wait_regs(i32x4 (&A)[N]) {
     if constexpr (N == 3) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]));
     if constexpr (N == 4)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]));
+}
+
+/* ds_read_b32 at addr + off (a constant), as inline assembly: the caller
+ * waits (lgkmcnt) before using the result */
+__device__ __forceinline__ int ds_read4(uint32_t addr, int off) {
+    int r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off));
+    return r;
 }
 
 /* A wave-uniform pointer held in scalar registers. */
@@ -531,6 +542,9 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
         const uint32_t stg_r = lds_addr(stg) + (uint32_t)(er * BT_EP_LD + ec) * 4;
         {
             int32_t *dbg = g.dbg_acc;
+            /* the output rows: assembly reads beside the staging reads,
+             * under one wait */
+            const uint32_t rid_r = lds_addr(&sh.rid[buf][er]);
 #pragma unroll
             for (int ri = 0; ri < 4; ri++) {
                 const float sa = sh.sa[buf][32 * ri + l32];
@@ -569,13 +583,18 @@ __device__ __forceinline__ void bt_run(const mm_i8_bt_args &a, int8_t *lds, floa
                     }
                     lds_wait();
                     i32x4 rv[4];
+                    int ridk[4];
 #pragma unroll
                     for (int k = 0; k < 4; k++) rv[k] = ds_read16(stg_r, 8 * k * BT_EP_LD * 4);
-                    lds_wait_regs(rv);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) ridk[k] = ds_read4(rid_r, (32 * ri + 8 * k) * 4);
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(rv[0]), "+v"(rv[1]), "+v"(rv[2]), "+v"(rv[3]), "+v"(ridk[0]),
+                                   "+v"(ridk[1]), "+v"(ridk[2]), "+v"(ridk[3]));
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         const f32x4 v = __builtin_bit_cast(f32x4, rv[k]);
-                        const int rid = sh.rid[buf][32 * ri + 8 * k + er];
+                        const int rid = ridk[k];
                         const int col = slab_c0 + ct + ec;
                         const bool ok = rid >= 0 && col < N;
                         *(f32x4 *)(out + (ok ? (size_t)rid * N + col : spare + col)) = v;
