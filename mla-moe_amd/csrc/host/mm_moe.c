@@ -635,8 +635,9 @@ static int launch_router_logits(mm_ctx *c, mm_router_args *a) {
     if (a->E <= 64 && a->H % 8 == 0 && a->T <= MM_ROUTER_PC_TMAX)
         return mm_launch(c, K_ROUTER_PC_SPLIT, (unsigned)a->T,
                          (unsigned)((a->E + MM_ROUTER_PC_EB - 1) / MM_ROUTER_PC_EB), 1, 256, 0, a);
-    return mm_launch(c, K_ROUTER, (a->T + ROUTER_TOKENS_PER_BLOCK - 1) / ROUTER_TOKENS_PER_BLOCK, 1,
-                     1, 256, 0, a);
+    const int tpb = MM_ROUTER_WAVES_LOGITS * MM_ROUTER_TPW;
+    return mm_launch(c, K_ROUTER, (unsigned)((a->T + tpb - 1) / tpb), 1, 1, 64 * MM_ROUTER_WAVES_LOGITS, 0,
+                     a);
 }
 
 /* ---- int8 forward ----------------------------------------------------------- */

@@ -11,8 +11,13 @@
  * caller-supplied), softmax/sigmoid, greedy top-k with the lowest-index tie
  * rule, optional normalisation and scaling. */
 #ifndef MM_ROUTER_TPW
-#define MM_ROUTER_TPW 1           /* router: tokens per wave (4 waves per block) */
+#define MM_ROUTER_TPW 1           /* router: tokens per wave */
 #endif
+/* waves (tokens) per block of mm_router, the logits of larger T: every block
+ * streams the whole gate weight through LDS, so 8 tokens per block take half
+ * the weight traffic of 4 at the same two waves per SIMD (measured at config
+ * 3: 33 against 39 us; 16 per block leave half the CUs idle, 50 us) */
+#define MM_ROUTER_WAVES_LOGITS 8
 
 /* Logits-only router with one token per block (mm_router_pc): used for
  * E <= 64, H % 8 == 0 and T up to this many tokens. */

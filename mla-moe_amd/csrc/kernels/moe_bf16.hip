@@ -131,9 +131,9 @@ __device__ __forceinline__ void gu_rows_x1(const uint16_t *__restrict__ gate,
     }
 }
 
-extern "C" __global__ __launch_bounds__(MM_ROUTER_THREADS) void mm_router(mm_router_args a) {
-    __shared__ float lds[MM_ROUTER_LDS_FLOATS];
-    router_block(a, blockIdx.x, lds);
+extern "C" __global__ __launch_bounds__(MM_ROUTER_WAVES_LOGITS * MM_WAVE) void mm_router(mm_router_args a) {
+    __shared__ float lds[MM_ROUTER_LDS_FLOATS_NW(MM_ROUTER_WAVES_LOGITS)];
+    router_block<MM_ROUTER_WAVES_LOGITS>(a, blockIdx.x, lds);
 }
 
 /* Router logits for any E (the wide path, E > MM_EMAX_FAST): block (token

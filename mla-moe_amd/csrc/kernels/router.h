@@ -22,15 +22,14 @@
 #include "common.h"
 
 #define MM_KMAX 16
-#define MM_ROUTER_WAVES 4
-#define MM_ROUTER_THREADS (MM_ROUTER_WAVES * MM_WAVE)
+#define MM_ROUTER_WAVES 4             /* waves per router block of the bf16 stage 1 */
 #define MM_ROUTER_CHUNK_FLOATS 8192   /* router-weight chunk: HC rows x E experts */
-#define MM_ROUTER_TOKENS (MM_ROUTER_WAVES * MM_ROUTER_TPW)
-#define MM_ROUTER_XCHUNK_FLOATS (MM_ROUTER_TOKENS * (MM_ROUTER_CHUNK_FLOATS / MM_WAVE))
-/* weight chunk widened to fp32 with 4 pad floats per expert row (at most 256
- * rows), then the token columns */
-#define MM_ROUTER_BUF_FLOATS (MM_ROUTER_CHUNK_FLOATS + 4 * 256 + MM_ROUTER_XCHUNK_FLOATS)
-#define MM_ROUTER_LDS_FLOATS (2 * MM_ROUTER_BUF_FLOATS)
+/* LDS of a router block of nw waves: two buffers, each the weight chunk
+ * widened to fp32 with 4 pad floats per expert row (at most 256 rows), then
+ * the token columns */
+#define MM_ROUTER_LDS_FLOATS_NW(nw) \
+    (2 * (MM_ROUTER_CHUNK_FLOATS + 4 * 256 + (nw) * MM_ROUTER_TPW * (MM_ROUTER_CHUNK_FLOATS / MM_WAVE)))
+#define MM_ROUTER_LDS_FLOATS MM_ROUTER_LDS_FLOATS_NW(MM_ROUTER_WAVES)
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -40,8 +39,8 @@ struct router_no_post {
     __device__ void operator()(int, const int *, const float *) const {}
 };
 
-/* Block-cooperative logits for the block's MM_ROUTER_TOKENS tokens.  Every
- * thread of the block must call this (it synchronises).
+/* Block-cooperative logits for the block's NW * TPW tokens (NW waves).
+ * Every thread of the block must call this (it synchronises).
  *
  * The router weight is used in its checkpoint layout, W [E][H] bf16 (its
  * fp32 values are exact).  It is consumed in chunks of HC hidden indices:
@@ -55,21 +54,22 @@ struct router_no_post {
  * On return lg[t][j] is the logit of token t0 + t, expert lane + 64 j. */
 #define RL_PF 3                                    /* chunks in flight in registers */
 #define RL_WBYTES (MM_ROUTER_CHUNK_FLOATS * 2)      /* bf16 weight bytes per chunk */
-template <int EJ, int TPW>
+template <int EJ, int TPW, int NW = MM_ROUTER_WAVES>
 __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int tb0, int t0,
                                                     float (&lg)[TPW][EJ], float *lds) {
+    constexpr int NTHR = NW * MM_WAVE, NTOK = NW * TPW;
     static_assert(TPW <= 2, "tail handling assumes at most two tokens per wave");
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int E = a.E, H = a.H, T = a.T;
     constexpr int HC = MM_ROUTER_CHUNK_FLOATS / (MM_WAVE * EJ);   /* hidden indices per chunk */
     constexpr int RS = HC + 4;                                    /* padded LDS row, fp32 */
     constexpr int WLDS = MM_WAVE * EJ * RS * 4;                   /* weight bytes in LDS */
-    constexpr int XB = MM_ROUTER_TOKENS * HC * 4;                 /* x bytes per chunk */
+    constexpr int XB = NTOK * HC * 4;                 /* x bytes per chunk */
     constexpr int BUF = WLDS + XB;                                /* LDS bytes per buffer */
-    static_assert(2 * BUF <= MM_ROUTER_LDS_FLOATS * 4, "router LDS");
+    static_assert(2 * BUF <= MM_ROUTER_LDS_FLOATS_NW(NW) * 4, "router LDS");
     constexpr int PPE = HC / 8;                                   /* 16-byte pieces per expert row */
-    constexpr int WP = RL_WBYTES / 16 / MM_ROUTER_THREADS;        /* weight pieces per thread */
-    constexpr int XP = (XB / 16 + MM_ROUTER_THREADS - 1) / MM_ROUTER_THREADS;
+    constexpr int WP = RL_WBYTES / 16 / NTHR;        /* weight pieces per thread */
+    constexpr int XP = (XB / 16 + NTHR - 1) / NTHR;
     const int nch = (H + HC - 1) / HC;
     const bool active = t0 < T;
     const int tw = t0 - tb0;                                       /* wave's first row in x chunk */
@@ -88,7 +88,7 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
          * partial */
 #pragma unroll
         for (int k = 0; k < WP; k++) {
-            const int i = threadIdx.x + k * MM_ROUTER_THREADS;   /* piece: expert i / PPE */
+            const int i = threadIdx.x + k * NTHR;   /* piece: expert i / PPE */
             const int e = i / PPE, o = (i % PPE) * 8;
             const bool ok = c < nch && e < E && c0 + o < H;
             const u32x4 v = *(const u32x4 *)(a.wg + (size_t)min(e, E - 1) * H + min(c0 + o, H - 8));
@@ -96,10 +96,10 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
         }
 #pragma unroll
         for (int k = 0; k < XP; k++) {
-            const int i = threadIdx.x + k * MM_ROUTER_THREADS;   /* float4 index in [tokens][HC] */
+            const int i = threadIdx.x + k * NTHR;   /* float4 index in [tokens][HC] */
             const int row = i / (HC / 4), col = (i % (HC / 4)) * 4;
             const int tok = min(tb0 + row, T - 1);
-            const bool ok = c < nch && row < MM_ROUTER_TOKENS && c0 + col < H;
+            const bool ok = c < nch && row < NTOK && c0 + col < H;
             const u32x4 v = *(const u32x4 *)(a.x + (size_t)tok * H + min(c0 + col, H - 4));
             xr[slot][k] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
         }
@@ -109,7 +109,7 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
         for (int k = 0; k < WP; k++) {
             /* the bf16 weights widened to fp32 once here (exact), so the
              * serial compute below spends no instruction on unpacking */
-            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
+            const int i = threadIdx.x + k * NTHR;
             const int e = i / PPE, o = (i % PPE) * 8;
             const u32x4 d = wr[slot][k];
             const f32x4 lo = {__uint_as_float(d.x << 16), __uint_as_float(d.x & 0xffff0000u),
@@ -121,7 +121,7 @@ __device__ __forceinline__ void router_logits_block(const mm_router_args &a, int
         }
 #pragma unroll
         for (int k = 0; k < XP; k++) {
-            const int i = threadIdx.x + k * MM_ROUTER_THREADS;
+            const int i = threadIdx.x + k * NTHR;
             if (i < XB / 16) *(u32x4 *)(buf + WLDS + (size_t)i * 16) = xr[slot][k];
         }
     };
@@ -329,12 +329,12 @@ __device__ __forceinline__ void router_select_wave(const mm_router_args &a, int 
     }
 }
 
-template <int EJ, class Post>
+template <int EJ, int NW, class Post>
 __device__ __forceinline__ void router_block_t(const mm_router_args &a, int block, float *lds,
                                                Post post) {
     const int lane = threadIdx.x & (MM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
-    const int t0 = (block * MM_ROUTER_WAVES + wave) * MM_ROUTER_TPW;
+    const int t0 = (block * NW + wave) * MM_ROUTER_TPW;
     float lg[MM_ROUTER_TPW][EJ];
     if (a.logits_in) {
 #pragma unroll
@@ -345,7 +345,7 @@ __device__ __forceinline__ void router_block_t(const mm_router_args &a, int bloc
                 lg[t][j] = e < a.E ? a.logits_in[(size_t)tt * a.E + e] : 0.0f;
             }
     } else {
-        router_logits_block<EJ, MM_ROUTER_TPW>(a, block * MM_ROUTER_TOKENS, t0, lg, lds);
+        router_logits_block<EJ, MM_ROUTER_TPW, NW>(a, block * NW * MM_ROUTER_TPW, t0, lg, lds);
         if (a.logit_bias) {
 #pragma unroll
             for (int t = 0; t < MM_ROUTER_TPW; t++)
@@ -369,17 +369,17 @@ __device__ __forceinline__ void router_block_t(const mm_router_args &a, int bloc
     router_select_wave<EJ, MM_ROUTER_TPW>(a, t0, lg, post);
 }
 
-/* One block of MM_ROUTER_WAVES waves routes MM_ROUTER_TOKENS tokens.  All
- * threads of the block must call it; `lds` holds MM_ROUTER_LDS_FLOATS. */
-template <class Post = router_no_post>
+/* One block of NW waves routes NW * MM_ROUTER_TPW tokens.  All threads of
+ * the block must call it; `lds` holds MM_ROUTER_LDS_FLOATS_NW(NW). */
+template <int NW = MM_ROUTER_WAVES, class Post = router_no_post>
 __device__ __forceinline__ void router_block(const mm_router_args &a, int block, float *lds,
                                              Post post = Post()) {
     if (a.E <= 64)
-        router_block_t<1>(a, block, lds, post);
+        router_block_t<1, NW>(a, block, lds, post);
     else if (a.E <= 128)
-        router_block_t<2>(a, block, lds, post);
+        router_block_t<2, NW>(a, block, lds, post);
     else
-        router_block_t<4>(a, block, lds, post);
+        router_block_t<4, NW>(a, block, lds, post);
 }
 
 /* ---- logits of one token per block, products and sums on separate waves ----
