@@ -28,6 +28,16 @@
  * steps) goes out before the previous tile's stores; the output tile is
  * restaged through LDS so that the stores are whole 128-byte lines.
  *
+ * Waits: only the hand-counted partial vmcnt waits order the ring.  The
+ * compiler adds a wait for every load and store in flight wherever a load
+ * was issued under a condition, a branch joins a value still being loaded,
+ * a register still being loaded is copied, or an LDS read follows a
+ * direct-to-LDS load it knows of.  So the loads of whole K turns and of
+ * every head are unconditional (clamped indices past a tile's end), the A
+ * stages are assembly, the tile metadata loads are issued by every thread
+ * and used only after the K loop, and the first tile and first K turn are
+ * copies of their own (their entry follows a different history of loads).
+ *
  * A 32x32x32 B operand (lane l: column l % 32, K bytes 16 (l / 32) .. + 15)
  * is one 16-byte load per lane
  * out of two packed 16x64 fragments: the 16 bytes of (column c, K chunk q)
