@@ -302,3 +302,16 @@ def test_i8_rows_in_chunks(ctx, oracle, monkeypatch):
         assert np.array_equal(idx, ri) and max_abs_rel(out, ro) < TOL
     finally:
         cc.close()
+
+
+@pytest.mark.parametrize("H,I,NS", [(384, 448, 1), (768, 704, 2), (832, 576, 1)])
+def test_i8_k_turn_boundaries(ctx, oracle, H, I, NS):
+    """Reduction lengths around the tiled GEMM's whole turns of 6 K steps:
+    gate/up 6, 12 and 13 steps (one turn, two, two plus one), down 7, 11 and
+    9 (a turn plus a tail of 1, 5 and 3, odd: a half last stage), the shared
+    down 7, 22 and 9.  Every accumulator against the oracle through the
+    debug entry, and the product kernels' output bit-identical to it."""
+    T, E, K = 40, 16, 4
+    out, ro, idx, x, w = run_case(ctx, oracle, H, E, K, I, NS, T, 130 + H // 64)
+    prod, pidx, *_ = ctx.moe_forward(0, x, flags=mlamoe.MM_FWD_INT8)
+    assert np.array_equal(pidx, idx) and np.array_equal(prod, out)
