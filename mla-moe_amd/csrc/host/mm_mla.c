@@ -191,12 +191,13 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     }
     mm_mla_attn_args aa = {qhl, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
                            part_o, probs, kv_len, NH, HG, nchunks, QKN, chunk, slots,
-                           direct ? clat : NULL};
+                           direct ? clat : NULL, B};
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
-    if ((st = mm_launch(c, K_MLA_ATTN, (unsigned)nchunks, (unsigned)B, (unsigned)HG, 64 * MM_MLA_AW, alds,
-                        &aa)))
+    /* a row's chunks on one XCD: see mm_mla_attn_args */
+    const unsigned ntrip = (unsigned)B * (unsigned)HG * (unsigned)nchunks;
+    if ((st = mm_launch(c, K_MLA_ATTN, 8 * ((ntrip + 7) / 8), 1, 1, 64 * MM_MLA_AW, alds, &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks,

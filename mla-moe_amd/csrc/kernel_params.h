@@ -334,7 +334,11 @@ typedef struct {
     int NH, QKN, VHD;
 } mm_mla_wprep_args;
 
-/* Flash-decoding partials: block (chunk, b, head group). */
+/* Flash-decoding partials of (row b, head group, chunk) triples, N = B * HG
+ * * nchunks of them, in that order (row-major): a 1-D grid of 8 * ceil(N / 8)
+ * blocks, block L taking triple (L % 8) * ceil(N / 8) + L / 8 (blocks past N
+ * exit), so that a row's chunks run on one XCD (blocks are dealt to the 8
+ * XCDs in turn) and share its Q in that L2. */
 typedef struct {
     const uint16_t *qhl;      /* [B, NH, 2, KVL] bf16: qabs as hi + lo halves (qprep) */
     const float *q;           /* [B, NH, QKN + QKR] (the q_pe part) */
@@ -352,6 +356,7 @@ typedef struct {
     const int32_t *slots;     /* [B] cache sequence of row b, or 0: sequence b */
     float *clat;              /* one chunk (nchunks == 1, no probabilities): clat [B, NH, KVL]
                                  written here, O / l as the merge computes it; else 0 */
+    int B;
 } mm_mla_attn_args;
 
 /* Merge the chunk partials, normalise (clat); then ctx = W_UV . clat. */

@@ -20,6 +20,7 @@
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -176,7 +177,8 @@ static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
 static_assert((AW * 16 * OROW + AW * 32 + 16) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
 static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
-/* grid (nchunks, B, HG), AW waves; row b attends to the first kv_lens[b]
+/* one block per (row b, head group hg, chunk) triple (the 1-D grid and its
+ * XCD-grouped order: mm_mla_attn_args), AW waves; row b attends to the first kv_lens[b]
  * rows of cache sequence slots[b] (b without slots); with KPW = a.chunk / AW
  * keys per wave,
  * wave w handles keys [chunk * a.chunk + w * KPW, + KPW) in 16-key
@@ -195,12 +197,17 @@ static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
  * Dynamic LDS: AW * 2 * TILE_B bytes (the merge reuses it). */
 extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_attn_args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
-    const int chunk = blockIdx.x, b = blockIdx.y, hg = blockIdx.z;
+    const int ntrip = a.B * a.HG * a.nchunks, per = (ntrip + 7) / 8;
+    const int trip = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (trip >= ntrip) return;
+    const int chunk = trip % a.nchunks, hg = (trip / a.nchunks) % a.HG, b = trip / (a.nchunks * a.HG);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, kl = lane & 15;
     const int L = a.kv_lens ? min(a.kv_lens[b], a.kv_len) : a.kv_len;
-    uint8_t *wt0 = alds + (size_t)w * 2 * TILE_B;     /* this wave's two stages */
+    /* stage st of wave w at (st AW + w) TILE_B: the second stages of all
+     * waves are one region, which holds the block's Q before their loads */
+    auto stage = [&](int st) { return alds + (size_t)(st * AW + w) * TILE_B; };
 
     const int kpw = a.chunk / AW;                     /* keys per wave */
     const int kbeg = chunk * a.chunk + w * kpw;
@@ -210,55 +217,118 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
     /* sub-tile at key k0 -> stage st: row p's c_kv (1 KB, one load per lane
      * of 16 B) at p * CROW_B; the k_pe parts (128 B per row) of rows 0..7 and
      * 8..15 as two 1 KB pieces after the c_kv rows.  Rows past L load row
-     * L - 1 (masked in the softmax). */
+     * L - 1 (masked in the softmax; row 0 when L = 0). */
+    const int klast = max(L - 1, 0);
 #define ISSUE_LOADS 18            /* direct loads per issue(): 16 c_kv rows + 2 k_pe pieces */
     auto issue = [&](int st, int k0) {
-        uint8_t *t = wt0 + st * TILE_B;
+        uint8_t *t = stage(st);
 #pragma unroll
         for (int p = 0; p < 16; p++) {
-            const int key = __builtin_amdgcn_readfirstlane(min(k0 + p, L - 1));
+            const int key = __builtin_amdgcn_readfirstlane(min(k0 + p, klast));
             lds_dma16(cseq + (uint32_t)(key * KVD * 2) + lane * 16, t + p * CROW_B);
         }
 #pragma unroll
         for (int p = 0; p < 2; p++) {
-            const int key = min(k0 + 8 * p + (lane >> 3), L - 1);
+            const int key = min(k0 + 8 * p + (lane >> 3), klast);
             lds_dma16(cseq + (uint32_t)(key * KVD * 2 + KVL * 2 + (lane & 7) * 16),
                       t + 16 * CROW_B + p * 1024);
         }
     };
     /* both stages from the start: the first two sub-tiles' loads are in
      * flight while Q is prepared, and each later sub-tile is issued one
-     * sub-tile of compute before its use */
-    if (kbeg < kend) issue(0, kbeg);
-    if (kbeg + 16 < kend) issue(1, kbeg + 16);
+     * sub-tile of compute before its use.  The Q loads go out first: the
+     * counter completes in issue order, and behind both sub-tiles (every
+     * wave of the launch asking for its first two at once) Q arrived ~8 us
+     * after the block's start, ~5 us after the first sub-tile. */
 
     /* Q operands in registers: lane (head kl, g) holds [qabs | q_pe] of its
      * head, latent 32 c + 8 g .. +7, as bf16 hi + lo; head slots past NH are
      * zero.  qabs comes split by qprep (splitting all 16 heads' 576 values
      * in every wave cost ~3-4 us of VALU per block); the 64 q_pe values
-     * are split here. */
+     * are split here, after the cache loads are issued. */
     bf16x8 qh[KC], ql[KC];
+    f32x4 qpe[KC - KVL / 32][2];
+    static_assert(KC - KVL / 32 == 2, "q_pe: two 32-value K steps");
+    const bool qreal = hg * 16 + kl < a.NH;
+    /* qabs (hi and lo rows of the group's 16 heads, 32 KB) is staged once
+     * per block in the second-stage region, each wave loading 8 of its 32
+     * 1 KB rows (head h, half p at h QROW_B + 1024 p: the 16-byte pad
+     * between heads puts the 16 heads of a ds_read_b128 on distinct banks);
+     * every wave then reads all of it into registers.  Loaded per wave
+     * from global memory, the same 36 KB went out 32 times per row (4
+     * waves x 8 chunks) in 64-byte pieces and took ~5 us to arrive. */
+    constexpr int QROW_B = 2 * KVL * 2 + 16;
+    static_assert(16 * QROW_B <= AW * TILE_B, "Q staging exceeds the second stages");
+    uint8_t *qlds = alds + (size_t)AW * TILE_B;
     {
-        const int qhd = hg * 16 + kl;
-        const bool real = qhd < a.NH;
-        const uint16_t *qa = a.qhl + ((size_t)b * a.NH + (real ? qhd : 0)) * 2 * KVL + 8 * g;
-        const float *qp = a.q + ((size_t)b * a.NH + (real ? qhd : 0)) * (a.QKN + MM_MLA_QKR) + a.QKN;
+        /* q_pe per wave as assembly loads (after a direct-to-LDS load the
+         * compiler waits for every load in flight at the first use of a
+         * loaded register; these waits are counted by hand below) */
+        const int qhd = qreal ? hg * 16 + kl : 0;
+        const float *qp = a.q + ((size_t)b * a.NH + qhd) * (a.QKN + MM_MLA_QKR) + a.QKN + 8 * g;
+#pragma unroll
+        for (int c = 0; c < KC - KVL / 32; c++) {
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qpe[c][0]) : "v"(qp), "i"(128 * c));
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qpe[c][1]) : "v"(qp), "i"(128 * c + 16));
+        }
+        static_assert(AW == 4, "8 qabs rows per wave");
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int row = 8 * w + j, h = row >> 1, p = row & 1;
+            const int qhd2 = hg * 16 + h < a.NH ? hg * 16 + h : 0;   /* head slots past NH: zeroed below */
+            lds_dma16(a.qhl + (((size_t)b * a.NH + qhd2) * 2 + p) * KVL + 8 * lane, qlds + h * QROW_B + p * 1024);
+        }
+    }
+    /* the first stage, then the wait for Q, then the second stage (into
+     * the region Q leaves): Q meets one stage's loads of every wave.  Both
+     * stages whatever the wave's key count (clamped rows of its own LDS,
+     * waited for before the merge), so that the counts hold */
+    __builtin_amdgcn_sched_barrier(0);
+    issue(0, kbeg);
+    __builtin_amdgcn_sched_barrier(0);
+    /* this wave's part of Q has landed once at most the first stage's
+     * loads are outstanding; the barrier waits for the other waves' parts */
+    static_assert(ISSUE_LOADS == 18, "wait count");
+    asm volatile("s_waitcnt vmcnt(18)" : "+v"(qpe[0][0]), "+v"(qpe[0][1]), "+v"(qpe[1][0]), "+v"(qpe[1][1]));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const uint32_t qa = lds_addr(qlds) + (uint32_t)(kl * QROW_B + 16 * g);
+#pragma unroll
+        for (int c = 0; c < KVL / 32; c++) {
+            qh[c] = __builtin_bit_cast(bf16x8, ds_read16(qa, 64 * c));
+            ql[c] = __builtin_bit_cast(bf16x8, ds_read16(qa, 1024 + 64 * c));
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(qh[0]), "+v"(qh[1]), "+v"(qh[2]), "+v"(qh[3]), "+v"(qh[4]), "+v"(qh[5]), "+v"(qh[6]),
+                   "+v"(qh[7]), "+v"(qh[8]), "+v"(qh[9]), "+v"(qh[10]), "+v"(qh[11]), "+v"(qh[12]), "+v"(qh[13]),
+                   "+v"(qh[14]), "+v"(qh[15]));
+    asm volatile(""
+                 : "+v"(ql[0]), "+v"(ql[1]), "+v"(ql[2]), "+v"(ql[3]), "+v"(ql[4]), "+v"(ql[5]), "+v"(ql[6]),
+                   "+v"(ql[7]), "+v"(ql[8]), "+v"(ql[9]), "+v"(ql[10]), "+v"(ql[11]), "+v"(ql[12]), "+v"(ql[13]),
+                   "+v"(ql[14]), "+v"(ql[15]));
+    /* every wave has read Q: the region takes the second stages */
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, kbeg + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    {
         const bf16x8 z8 = __builtin_bit_cast(bf16x8, (u16x8){});
 #pragma unroll
         for (int c = 0; c < KVL / 32; c++) {
-            const bf16x8 h8 = *(const bf16x8 *)(qa + 32 * c), l8 = *(const bf16x8 *)(qa + KVL + 32 * c);
-            qh[c] = real ? h8 : z8;
-            ql[c] = real ? l8 : z8;
+            qh[c] = qreal ? qh[c] : z8;
+            ql[c] = qreal ? ql[c] : z8;
         }
 #pragma unroll
         for (int c = KVL / 32; c < KC; c++) {
-            const float *src = qp + 32 * (c - KVL / 32) + 8 * g;
-            const f32x4 x0 = *(const f32x4 *)src, x1 = *(const f32x4 *)(src + 4);
+            const f32x4 x0 = qpe[c - KVL / 32][0], x1 = qpe[c - KVL / 32][1];
             u16x8 hi, lo;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 uint16_t h16, l16;
-                split_bf16(real ? (j < 4 ? x0[j & 3] : x1[j & 3]) : 0.0f, &h16, &l16);
+                split_bf16(qreal ? (j < 4 ? x0[j & 3] : x1[j & 3]) : 0.0f, &h16, &l16);
                 hi[j] = h16;
                 lo[j] = l16;
             }
@@ -332,6 +402,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             ph[i] = (short)hi;
             pl[i] = (short)lo;
         }
+        const bf16x8 pa = __builtin_bit_cast(bf16x8, (s16x8){ph[0], ph[1], ph[2], ph[3], pl[0], pl[1], pl[2], pl[3]});
 #pragma unroll
         for (int bt = 0; bt < KVL / 128; bt++) {
             asm volatile("s_waitcnt lgkmcnt(0)"
@@ -344,8 +415,11 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int nb = 8 * bt + j;
-                O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, bv[bt & 1][j], O[nb], 0, 0, 0);
-                O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, bv[bt & 1][j], O[nb], 0, 0, 0);
+                /* K = 32 as (key 4g + i, hi) at 8g + i and (key 4g + i, lo)
+                 * at 8g + 4 + i: the hi and lo products in one MFMA */
+                const s16x4 c = bv[bt & 1][j];
+                const bf16x8 bb = __builtin_bit_cast(bf16x8, (s16x8){c[0], c[1], c[2], c[3], c[0], c[1], c[2], c[3]});
+                O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bb, O[nb], 0, 0, 0);
             }
         }
     };
@@ -364,7 +438,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             if (k0 + 16 < kend) VMCNT_WAIT(ISSUE_LOADS);
             else VMCNT_WAIT(0);
             __builtin_amdgcn_sched_barrier(0);
-            const uint32_t t = lds_addr(wt0 + st * TILE_B);
+            const uint32_t t = lds_addr(stage(st));
             score(t, k0, sv);
             const float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
             if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_TAU)) {
@@ -404,7 +478,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             }
         }
         m = mnew;
-        accumulate(lds_addr(wt0 + st * TILE_B), sv);
+        accumulate(lds_addr(stage(st)), sv);
         __builtin_amdgcn_sched_barrier(0);
         if (k0 + 32 < kend) issue(st, k0 + 32);
         __builtin_amdgcn_sched_barrier(0);
