@@ -197,7 +197,6 @@ __device__ __forceinline__ bt_tile_id bt_decode(const mm_i8_bt_args &a, const bt
         id.m0 = (loc % ge) * MM_I8B_BM;
         id.M = sh.cnt[lo];
     } else {
-        const mm_i8_tiled_args &g = a.seg[1];
         const int loc = t - sh.n0;
         id.si = 1;
         id.e = 0;
