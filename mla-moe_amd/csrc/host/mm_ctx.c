@@ -41,6 +41,7 @@ static const struct {
     [K_MOE_BF16_S1] = {"mm_moe_bf16_stage1", MOD_MOE_BF16},
     [K_MOE_BF16_S2] = {"mm_moe_bf16_stage2", MOD_MOE_BF16},
     [K_MOE_BF16_S3] = {"mm_moe_bf16_stage3", MOD_MOE_BF16},
+    [K_MOE_BF16_S3L] = {"mm_moe_bf16_stage3_lds", MOD_MOE_BF16},
     [K_FILL] = {"mm_fill", MOD_UTIL},
     [K_QUANT_W] = {"mm_quant_weight", MOD_UTIL},
     [K_I8_ROUTE] = {"mm_i8_route", MOD_MOE_I8},

@@ -18,6 +18,7 @@ typedef enum {
     K_MOE_BF16_S1,
     K_MOE_BF16_S2,
     K_MOE_BF16_S3,
+    K_MOE_BF16_S3L,
     K_FILL,
     K_QUANT_W,
     K_I8_ROUTE,

@@ -16,7 +16,8 @@
 #define GU2_ROWS_PER_BLOCK 8  /* stage 2: two row pairs per wave (one round of loads) */
 #define RSH_ROWS_PER_BLOCK 16 /* shared gate/up beside the router: four row pairs per wave */
 #define RSH_TMAX 4            /* tokens up to which the shared gate/up joins the router launch */
-#define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave */
+#define DOWN_ROWS_PER_BLOCK 4 /* one output row per wave (the LDS-staged form needs exactly this) */
+#define DN_LDS_MAX 65536      /* stage 3 stages the hidden row in LDS up to this many bytes */
 #define ROUTER_TOKENS_PER_BLOCK (4 * MM_ROUTER_TPW)
 
 void mm_moe_release(mm_ctx *c) {
@@ -617,8 +618,12 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
 
         mm_down_bf16_args d = {hcat, L->ed, L->sd, idx + (size_t)t0 * K, out + (size_t)t0 * H,
                                Tc, H, I, S, K, E, acc, DOWN_ROWS_PER_BLOCK};
-        if ((st = mm_launch(c, K_MOE_BF16_S3, (H + DOWN_ROWS_PER_BLOCK - 1) / DOWN_ROWS_PER_BLOCK,
-                            Tc, 1, 256, 0, &d)))
+        /* the hidden row staged in LDS per block when it fits DN_LDS_MAX */
+        const size_t hl_b = ((size_t)hw * 4 + 1023) / 1024 * 1024;
+        const int staged = hl_b <= DN_LDS_MAX;
+        if ((st = mm_launch(c, staged ? K_MOE_BF16_S3L : K_MOE_BF16_S3,
+                            (H + DOWN_ROWS_PER_BLOCK - 1) / DOWN_ROWS_PER_BLOCK, Tc, 1, 256,
+                            staged ? hl_b : 0, &d)))
             return st;
     }
     return MM_OK;

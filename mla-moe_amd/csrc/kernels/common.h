@@ -26,6 +26,20 @@ __device__ __forceinline__ uint16_t rne16(float x) {
 
 /* 8 bf16 weights (one 128-bit load) dotted with 8 fp32 activations read as
  * two 128-bit loads (x must be 16-byte aligned). */
+/* as dot8_bf16 with x in LDS */
+__device__ __forceinline__ float dot8_bf16_lds(u32x4 w, const __attribute__((address_space(3))) float *x, float acc) {
+    const f32x4 a = *(const __attribute__((address_space(3))) f32x4 *)x;
+    const f32x4 b = *(const __attribute__((address_space(3))) f32x4 *)(x + 4);
+    acc = __builtin_fmaf(bf16_lo(w.x), a.x, acc);
+    acc = __builtin_fmaf(bf16_hi(w.x), a.y, acc);
+    acc = __builtin_fmaf(bf16_lo(w.y), a.z, acc);
+    acc = __builtin_fmaf(bf16_hi(w.y), a.w, acc);
+    acc = __builtin_fmaf(bf16_lo(w.z), b.x, acc);
+    acc = __builtin_fmaf(bf16_hi(w.z), b.y, acc);
+    acc = __builtin_fmaf(bf16_lo(w.w), b.z, acc);
+    acc = __builtin_fmaf(bf16_hi(w.w), b.w, acc);
+    return acc;
+}
 __device__ __forceinline__ float dot8_bf16(u32x4 w, const float *x, float acc) {
     const f32x4 a = *(const f32x4 *)x, b = *(const f32x4 *)(x + 4);
     acc = __builtin_fmaf(bf16_lo(w.x), a.x, acc);

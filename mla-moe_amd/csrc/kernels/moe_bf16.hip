@@ -295,24 +295,50 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_g
  * chunk 0 of it and are skipped), so a row costs ceil(chunks / DN_BATCH)
  * round trips instead of one per segment. */
 #define DN_BATCH 24
-extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_down_bf16_args a) {
+/* STAGE: the token's concatenated hidden row is staged once per block into
+ * LDS (dynamic: 1 KB pieces by direct loads spread over the waves, issued
+ * before the weights; the first batch's weight loads stay in flight across
+ * the barrier) and read from there: read per wave from
+ * global memory it cost every wave the whole row (45 KB at DeepSeek-V2-Lite
+ * shape) from L2, twice the bytes of the wave's weights.  One output row
+ * per wave (rows_per_block == GU_WAVES). */
+template <bool STAGE>
+__device__ __forceinline__ void stage3_body(const mm_down_bf16_args &a) {
+    extern __shared__ __attribute__((aligned(16))) float hl[];
+    const __attribute__((address_space(3))) float *hl3 = (const __attribute__((address_space(3))) float *)hl;
     const int t = blockIdx.y;
-    const float *hs = a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S);
+    const size_t hw = (size_t)a.K * a.I + a.S;
+    const float *hs = a.hcat + (size_t)t * hw;
 
     const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int wave = threadIdx.x / MM_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int d0 = blockIdx.x * a.rows_per_block;
     const int nrows = min(a.rows_per_block, a.H - d0);
     const int nci = a.I >> 3, ncs = a.S >> 3;
     const int cpl = (nci + MM_WAVE - 1) / MM_WAVE;        /* chunk slots per routed segment */
     const int cps = (ncs + MM_WAVE - 1) / MM_WAVE;        /* ... of the shared segment */
     const int nf = a.K * cpl + (a.S > 0 ? cps : 0);
-    for (int rr = wave; rr < nrows; rr += GU_WAVES) {
-        const int d = d0 + rr;
+    /* the routed segments' experts, read once (uniform) */
+    int er[MM_KMAX];
+#pragma unroll
+    for (int r = 0; r < MM_KMAX; r++)
+        er[r] = r < a.K ? min(max(a.topk_idx[(size_t)t * a.K + r], 0), a.E - 1) : 0;
+    if (STAGE) {
+        /* assembly loads: the compiler would wait for every load in flight
+         * at the first use of a weight register after a direct-to-LDS load
+         * it knows of; these are waited for by hand below.  Bytes past the
+         * row read as zeros (past the buffer's range: no memory read). */
+        const rsrc_t hr = raw_rsrc(hs, (uint32_t)(hw * 4));
+        const int np = (int)((hw * 4 + 1023) / 1024);
+        for (int j = __builtin_amdgcn_readfirstlane(wave); j < np; j += GU_WAVES)
+            lds_dma16_buf((uint32_t)(1024 * j + 16 * lane), hr, lds_addr(hl) + 1024u * (uint32_t)j);
+    }
+    for (int rr = wave; rr < (STAGE ? GU_WAVES : nrows); rr += GU_WAVES) {
+        const int d = d0 + min(rr, nrows - 1);   /* STAGE: a wave past the rows loads row nrows - 1 */
         float acc = 0.0f;
         for (int f0 = 0; f0 < nf; f0 += DN_BATCH) {
             u32x4 wv[DN_BATCH];
-            const float *hv[DN_BATCH];
+            int ho[DN_BATCH];
             bool ok[DN_BATCH];
 #pragma unroll
             for (int b = 0; b < DN_BATCH; b++) {
@@ -323,27 +349,44 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_d
                     const int r = f / cpl;
                     c = lane + MM_WAVE * (f % cpl);
                     ok[b] = f0 + b < nf && c < nci;
-                    const int e = min(max(a.topk_idx[(size_t)t * a.K + r], 0), a.E - 1);
+                    int e = er[0];
+#pragma unroll
+                    for (int q = 1; q < MM_KMAX; q++) e = r == q ? er[q] : e;
                     p = (const u32x4 *)(a.down + ((size_t)e * a.H + d) * a.I);
-                    hv[b] = hs + r * a.I;
+                    ho[b] = r * a.I;
                 } else {
                     c = lane + MM_WAVE * (f - a.K * cpl);
                     ok[b] = f0 + b < nf && c < ncs;
                     p = (const u32x4 *)(a.sdown + (size_t)d * a.S);
-                    hv[b] = hs + a.K * a.I;
+                    ho[b] = a.K * a.I;
                 }
                 if (!ok[b]) c = 0;
                 wv[b] = __builtin_nontemporal_load(p + c);
-                hv[b] += 8 * c;
+                ho[b] += 8 * c;
+            }
+            if (STAGE && f0 == 0) {
+                /* this wave's pieces have landed once at most the batch's
+                 * weight loads are outstanding; the barrier waits for the
+                 * other waves' pieces */
+                static_assert(DN_BATCH == 24, "wait count");
+                asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+                __syncthreads();
             }
 #pragma unroll
             for (int b = 0; b < DN_BATCH; b++)
-                if (ok[b]) acc = dot8_bf16(wv[b], hv[b], acc);
+                if (ok[b]) acc = STAGE ? dot8_bf16_lds(wv[b], hl3 + ho[b], acc) : dot8_bf16(wv[b], hs + ho[b], acc);
         }
         acc = wave_sum(acc);
-        if (lane == 0) {
+        if (lane == 0 && rr < nrows) {
             float *o = a.out + (size_t)t * a.H + d;
             *o = a.accumulate ? *o + acc : acc;
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3(mm_down_bf16_args a) {
+    stage3_body<false>(a);
+}
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage3_lds(mm_down_bf16_args a) {
+    stage3_body<true>(a);
 }

@@ -134,6 +134,24 @@ def test_ffn_multi_token_and_accumulate(ctx, oracle):
     assert max_abs_rel(acc - base, ro) < TOL
 
 
+@pytest.mark.parametrize("K,I,NS", [(4, 72, 1), (8, 2304, 1)])
+def test_ffn_down_hidden_row_forms(ctx, oracle, K, I, NS):
+    """The down stage stages a token's concatenated hidden row (K I + NS I
+    floats) in LDS up to 64 KB, in 1 KB pieces (360 floats: the second piece
+    partly past the row), and reads it from global memory beyond (20736
+    floats)."""
+    print(f"ffn down hidden row K={K} I={I}", flush=True)
+    H, E, T = 128, 8, 3
+    w = synth.moe_layer(51 + K, H, E, I, NS)
+    _layer_ctx(ctx, w, H, E, NS, K, I)
+    x = synth.activations(52 + K, T, H)
+    cfg = oracle.moe_cfg(H, E, NS, K, I)
+    ro, ri, rw, rp = oracle.ffn_compute_rows(cfg, w, x)
+    out, idx, wt, probs = ctx.moe_forward(0, x)
+    assert np.array_equal(idx, ri)
+    assert max_abs_rel(out, ro) < TOL
+
+
 def test_rejects_bad_shapes(ctx):
     with pytest.raises(mlamoe.MMError):
         ctx.moe_init(100, 8, 1, 2, 12)          # H not a multiple of 8
