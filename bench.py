@@ -243,7 +243,7 @@ def bench_decode_bf16(ctx, steps, warmup):
         mlamoe._check(lib.mm_moe_forward_dev(h, 0, 1, x.ptr, out.ptr, None, idx.ptr, wts.ptr,
                                              None, mlamoe.MM_FWD_BF16))
     ms, wall = timed(ctx, step, steps * 20, warmup * 5)
-    names = ["mm_moe_bf16_router_sh", "mm_moe_bf16_stage2", "mm_moe_bf16_stage3_lds"]
+    names = ["mm_moe_bf16_router_sh", "mm_moe_bf16_stage2_lds", "mm_moe_bf16_stage3_lds"]
     prof = profile_kernels(ctx, step, 50, names)
     nbytes = 262144 + 103809024 + 34603008      # router + 6 experts + shared (bf16)
     return dict(ms_per_step=ms, tok_s=1.0 / (ms * 1e-3), layer_gbs=nbytes / (ms * 1e-3) / 1e9,

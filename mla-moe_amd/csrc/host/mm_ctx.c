@@ -40,6 +40,7 @@ static const struct {
     [K_MOE_BF16_RSH] = {"mm_moe_bf16_router_sh", MOD_MOE_BF16},
     [K_MOE_BF16_S1] = {"mm_moe_bf16_stage1", MOD_MOE_BF16},
     [K_MOE_BF16_S2] = {"mm_moe_bf16_stage2", MOD_MOE_BF16},
+    [K_MOE_BF16_S2L] = {"mm_moe_bf16_stage2_lds", MOD_MOE_BF16},
     [K_MOE_BF16_S3] = {"mm_moe_bf16_stage3", MOD_MOE_BF16},
     [K_MOE_BF16_S3L] = {"mm_moe_bf16_stage3_lds", MOD_MOE_BF16},
     [K_FILL] = {"mm_fill", MOD_UTIL},

@@ -17,6 +17,7 @@ typedef enum {
     K_MOE_BF16_RSH,
     K_MOE_BF16_S1,
     K_MOE_BF16_S2,
+    K_MOE_BF16_S2L,
     K_MOE_BF16_S3,
     K_MOE_BF16_S3L,
     K_FILL,

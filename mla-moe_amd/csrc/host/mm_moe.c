@@ -500,6 +500,15 @@ static int route_wide(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn,
 
 /* ---- bf16 forward ------------------------------------------------------------ */
 
+/* Stage 2 (routed gate/up, shared parts): blocks of GU2_ROWS_PER_BLOCK rows,
+ * one row group per wave, so the form that stages x once per block in LDS
+ * (H * 4 bytes rounded up to 1 KB) applies whenever x fits 64 KB. */
+static int launch_s2(mm_ctx *c, unsigned gx, unsigned gy, mm_gu_bf16_args *a) {
+    const size_t xl = ((size_t)a->H * 4 + 1023) / 1024 * 1024;
+    const int staged = a->rows_per_block == GU2_ROWS_PER_BLOCK && xl <= 65536;
+    return mm_launch(c, staged ? K_MOE_BF16_S2L : K_MOE_BF16_S2, gx, gy, 1, 256, staged ? xl : 0, a);
+}
+
 /* bf16 weights, GEMV stages (kernels/moe_bf16.hip), BF16_NT_MAX tokens per pass. */
 static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn, float *out,
                         const float *logits, int32_t *idx, float *wts, float *probs, int acc,
@@ -566,7 +575,7 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             a.rows_per_block = GU2_ROWS_PER_BLOCK;
             a.gate = L->eg;
             a.up = L->eu;
-            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
+            if ((st = launch_s2(c, a.n_blocks_per_token, Tc * K, &a)))
                 return st;
         } else if (rsh && Tc <= MM_ROUTER_PC_TMAX) {
             /* small T: the router in product / chain form; up to RSH_TMAX
@@ -593,13 +602,11 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
                 if ((st = mm_launch(c, K_MOE_BF16_RSH, (unsigned)Tc * ngr + ar.n_blocks_per_token * nsh,
                                     1, 1, 256, 0, &ar)))
                     return st;
-                if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, (unsigned)(Tc * K), 1, 256,
-                                    0, &a)))
+                if ((st = launch_s2(c, a.n_blocks_per_token, (unsigned)(Tc * K), &a)))
                     return st;
             } else {
                 if ((st = mm_launch(c, K_ROUTER_PC, (unsigned)Tc, 1, 1, 256, 0, &a.r))) return st;
-                if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, (unsigned)(Tc * K) + nsh, 1,
-                                    256, 0, &a)))
+                if ((st = launch_s2(c, a.n_blocks_per_token, (unsigned)(Tc * K) + nsh, &a)))
                     return st;
             }
         } else {
@@ -612,7 +619,7 @@ static int forward_bf16(mm_ctx *c, const mm_moe_layer *L, int T, const float *xn
             a.rows_per_block = GU2_ROWS_PER_BLOCK;
             a.gate = L->eg;
             a.up = L->eu;
-            if ((st = mm_launch(c, K_MOE_BF16_S2, a.n_blocks_per_token, Tc * K, 1, 256, 0, &a)))
+            if ((st = launch_s2(c, a.n_blocks_per_token, Tc * K, &a)))
                 return st;
         }
 

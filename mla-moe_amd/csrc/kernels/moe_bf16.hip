@@ -72,13 +72,25 @@ __device__ __forceinline__ void gu_rows(const uint16_t *__restrict__ gate, const
  * reads x from global memory again for every row). */
 #define GU_RPW 2
 #define GU_MAXC 4
+template <bool STAGE = false>
 __device__ __forceinline__ void gu_rows_x1(const uint16_t *__restrict__ gate,
                                            const uint16_t *__restrict__ up, const float *x, int H,
                                            int row0, int nrows, float *__restrict__ h, int hoff,
                                            float wt) {
+    extern __shared__ __attribute__((aligned(16))) float xl[];
+    const __attribute__((address_space(3))) float *xl3 = (const __attribute__((address_space(3))) float *)xl;
     const int lane = threadIdx.x & (MM_WAVE - 1);
-    const int wave = threadIdx.x / MM_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
     const int nch = H >> 3;
+    if (STAGE) {
+        /* x staged once per block (1 KB pieces over the waves, before the
+         * weights; assembly, waited for by hand below): read per wave it
+         * was a third of each wave's bytes.  Bytes past x read as zeros. */
+        const rsrc_t xr = raw_rsrc(x, (uint32_t)H * 4u);
+        const int np = (H * 4 + 1023) / 1024;
+        for (int j = wave; j < np; j += GU_WAVES)
+            lds_dma16_buf((uint32_t)(1024 * j + 16 * lane), xr, lds_addr(xl) + 1024u * (uint32_t)j);
+    }
     for (int rb = wave * GU_RPW; rb < nrows; rb += GU_WAVES * GU_RPW) {
         float ag[GU_RPW], au[GU_RPW];
 #pragma unroll
@@ -95,16 +107,31 @@ __device__ __forceinline__ void gu_rows_x1(const uint16_t *__restrict__ gate,
 #pragma unroll
                 for (int k = 0; k < GU_MAXC; k++) {
                     const int c = c0 + lane + MM_WAVE * k;
-                    if (c < nch) {
+                    if (STAGE) {   /* every load issued (clamped), for the count below */
+                        gv[q][k] = __builtin_nontemporal_load(gp + min(c, nch - 1));
+                        uv[q][k] = __builtin_nontemporal_load(upp + min(c, nch - 1));
+                    } else if (c < nch) {
                         gv[q][k] = __builtin_nontemporal_load(gp + c);
                         uv[q][k] = __builtin_nontemporal_load(upp + c);
                     }
                 }
             }
+            if (STAGE && c0 == 0) {
+                /* this wave's pieces have landed once at most the group's
+                 * weight loads are outstanding; the barrier waits for the
+                 * other waves' (every wave takes exactly one row group) */
+                static_assert(2 * GU_RPW * GU_MAXC == 16, "wait count");
+                asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+                __syncthreads();
+            }
 #pragma unroll
             for (int k = 0; k < GU_MAXC; k++) {
                 const int c = c0 + lane + MM_WAVE * k;
-                if (c < nch) {
+                if (STAGE) {
+                    const int cc = min(c, nch - 1);
+                    xa[k] = *(const __attribute__((address_space(3))) f32x4 *)(xl3 + 8 * cc);
+                    xb[k] = *(const __attribute__((address_space(3))) f32x4 *)(xl3 + 8 * cc + 4);
+                } else if (c < nch) {
                     xa[k] = *(const f32x4 *)(x + 8 * c);
                     xb[k] = *(const f32x4 *)(x + 8 * c + 4);
                 }
@@ -265,7 +292,11 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage1(mm_g
             a.K * a.I, one);
 }
 
-extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_gu_bf16_args a) {
+/* STAGE: x staged once per block in LDS (dynamic, H * 4 bytes rounded up
+ * to 1 KB); needs every wave to take exactly one row group
+ * (rows_per_block == GU_WAVES * GU_RPW, a divisor of I). */
+template <bool STAGE>
+__device__ __forceinline__ void stage2_body(const mm_gu_bf16_args &a) {
     const int route = blockIdx.y;               /* t*K + r */
     const int row0 = blockIdx.x * a.rows_per_block;
     const int nrows = min(a.rows_per_block, a.I - row0);
@@ -276,16 +307,23 @@ extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_g
          * K I + j I .. of hcat (weight 1) */
         const int v = route - a.T * a.K, t = v / a.nsh_parts, j = v % a.nsh_parts;
         const size_t off = (size_t)j * a.I * a.H;
-        gu_rows_x1(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
-                   a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), (a.K + j) * a.I, 1.0f);
+        gu_rows_x1<STAGE>(a.sgate + off, a.sup + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
+                          a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), (a.K + j) * a.I, 1.0f);
         return;
     }
     const int t = route / a.K, r = route % a.K;
     const int e = min(max(a.r.topk_idx[route], 0), a.r.E - 1);
     const float wr = a.r.topk_w[route];
     const size_t off = (size_t)e * a.I * a.H;
-    gu_rows_x1(a.gate + off, a.up + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
-               a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), r * a.I, wr);
+    gu_rows_x1<STAGE>(a.gate + off, a.up + off, a.x + (size_t)t * a.H, a.H, row0, nrows,
+                      a.hcat + (size_t)t * ((size_t)a.K * a.I + a.S), r * a.I, wr);
+}
+
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2(mm_gu_bf16_args a) {
+    stage2_body<false>(a);
+}
+extern "C" __global__ __launch_bounds__(GU_THREADS) void mm_moe_bf16_stage2_lds(mm_gu_bf16_args a) {
+    stage2_body<true>(a);
 }
 
 /* Down rows: a wave's row d takes, per lane, chunks c = lane, lane + 64, ...
