@@ -177,6 +177,94 @@ static_assert(TILE_B == MM_MLA_TILE_B, "sub-tile size");
 static_assert((AW * 16 * OROW + AW * 32 + 16) * 4 <= AW * 2 * TILE_B, "merge buffer exceeds the staging LDS");
 static_assert((16 * KVL) % (4 * AW * MM_WAVE) == 0, "merge loop");
 
+/* A operand of the score product: cache row kl of the sub-tile at LDS
+ * address t, latent 32 c + 8 g .. +7 (c_kv, then the k_pe part) */
+__device__ __forceinline__ i32x4 mla_read_a(uint32_t t, int c, int kl, int g) {
+    return c < KVL / 32 ? ds_read16(t + kl * CROW_B + 16 * g, 64 * c)
+                        : ds_read16(t + 16 * CROW_B + kl * 128 + 16 * g, 64 * (c - KVL / 32));
+}
+
+/* S^T[key 4g+i][head kl] for the sub-tile at LDS address t: A = cache
+ * row kl, latent 32 c + 8 g .. +7; LDS reads run one batch of 6 ahead of
+ * the MFMAs.  Returns the scaled scores, -inf past kend. */
+__device__ __forceinline__ void mla_score(const mm_mla_attn_args &a, uint32_t t, int k0, int kend, int b,
+                                          int hg, int kl, int g, const bf16x8 (&qh)[KC],
+                                          const bf16x8 (&ql)[KC], float *sv) {
+    /* the hi and lo products in two independent MFMA chains (one chain
+     * of 36 dependent MFMAs waits out each one's latency), added at the
+     * end */
+    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    i32x4 af[2][6];
+#pragma unroll
+    for (int c = 0; c < 6; c++) af[0][c] = mla_read_a(t, c, kl, g);
+#pragma unroll
+    for (int bt = 0; bt < KC / 6; bt++) {
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[bt & 1][0]), "+v"(af[bt & 1][1]), "+v"(af[bt & 1][2]),
+                     "+v"(af[bt & 1][3]), "+v"(af[bt & 1][4]), "+v"(af[bt & 1][5]));
+        if (bt + 1 < KC / 6) {
+#pragma unroll
+            for (int c = 0; c < 6; c++) af[(bt + 1) & 1][c] = mla_read_a(t, 6 * (bt + 1) + c, kl, g);
+        }
+#pragma unroll
+        for (int c = 0; c < 6; c++) {
+            const bf16x8 ab = __builtin_bit_cast(bf16x8, af[bt & 1][c]);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[6 * bt + c], s, 0, 0, 0);
+            s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[6 * bt + c], s2, 0, 0, 0);
+        }
+    }
+    s += s2;
+    const int head = hg * 16 + kl;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int key = k0 + 4 * g + i;
+        sv[i] = key < kend ? s[i] * a.scale : -INFINITY;
+        if (a.scores && key < kend && head < a.NH)
+            a.scores[((size_t)b * a.NH + head) * a.probs_stride + key] = sv[i];
+    }
+}
+
+/* P = e^(s - m) into the sums and O[head][r] += P . C_kv.  P[head kl][keys
+ * 4g .. 4g+3] is a bf16 hi/lo pair of A operands; the B operands come by
+ * transposing reads (lane 4k + c of group g reads row 4g + k, columns
+ * 16 nb + 4c .. +3), one batch of 8 ahead of the MFMAs. */
+__device__ __forceinline__ void mla_accumulate(uint32_t t, const float *sv, float m, float &l,
+                                               f32x4 (&O)[KVL / 16], int kl, int g) {
+    const uint32_t tb = t + (4 * g + (kl >> 2)) * CROW_B + 8 * (kl & 3);
+    s16x4 bv[2][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) bv[0][j] = ds_read_tr16(tb, 32 * j);
+    s16x4 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float p = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - m);
+        l += p;
+        uint16_t hi, lo;
+        split_bf16(p, &hi, &lo);
+        ph[i] = (short)hi;
+        pl[i] = (short)lo;
+    }
+    const bf16x8 pa = __builtin_bit_cast(bf16x8, (s16x8){ph[0], ph[1], ph[2], ph[3], pl[0], pl[1], pl[2], pl[3]});
+#pragma unroll
+    for (int bt = 0; bt < KVL / 128; bt++) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(bv[bt & 1][0]), "+v"(bv[bt & 1][1]), "+v"(bv[bt & 1][2]), "+v"(bv[bt & 1][3]),
+                       "+v"(bv[bt & 1][4]), "+v"(bv[bt & 1][5]), "+v"(bv[bt & 1][6]), "+v"(bv[bt & 1][7]));
+        if (bt + 1 < KVL / 128) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) bv[(bt + 1) & 1][j] = ds_read_tr16(tb, 32 * (8 * (bt + 1) + j));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int nb = 8 * bt + j;
+            /* K = 32 as (key 4g + i, hi) at 8g + i and (key 4g + i, lo)
+             * at 8g + 4 + i: the hi and lo products in one MFMA */
+            const s16x4 c = bv[bt & 1][j];
+            const bf16x8 bb = __builtin_bit_cast(bf16x8, (s16x8){c[0], c[1], c[2], c[3], c[0], c[1], c[2], c[3]});
+            O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bb, O[nb], 0, 0, 0);
+        }
+    }
+}
+
 /* one block per (row b, head group hg, chunk) triple (the 1-D grid and its
  * XCD-grouped order: mm_mla_attn_args), AW waves; row b attends to the first kv_lens[b]
  * rows of cache sequence slots[b] (b without slots); with KPW = a.chunk / AW
@@ -342,87 +430,6 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
 #pragma unroll
     for (int nb = 0; nb < KVL / 16; nb++) O[nb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto read_a = [&](uint32_t t, int c) -> i32x4 {
-        return c < KVL / 32 ? ds_read16(t + kl * CROW_B + 16 * g, 64 * c)
-                            : ds_read16(t + 16 * CROW_B + kl * 128 + 16 * g, 64 * (c - KVL / 32));
-    };
-
-    /* S^T[key 4g+i][head kl] for the sub-tile at LDS address t: A = cache
-     * row kl, latent 32 c + 8 g .. +7; LDS reads run one batch of 6 ahead of
-     * the MFMAs.  Returns the scaled scores, -inf past kend. */
-    auto score = [&](uint32_t t, int k0, float *sv) {
-        /* the hi and lo products in two independent MFMA chains (one chain
-         * of 36 dependent MFMAs waits out each one's latency), added at the
-         * end */
-        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
-        i32x4 af[2][6];
-#pragma unroll
-        for (int c = 0; c < 6; c++) af[0][c] = read_a(t, c);
-#pragma unroll
-        for (int bt = 0; bt < KC / 6; bt++) {
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[bt & 1][0]), "+v"(af[bt & 1][1]), "+v"(af[bt & 1][2]),
-                         "+v"(af[bt & 1][3]), "+v"(af[bt & 1][4]), "+v"(af[bt & 1][5]));
-            if (bt + 1 < KC / 6) {
-#pragma unroll
-                for (int c = 0; c < 6; c++) af[(bt + 1) & 1][c] = read_a(t, 6 * (bt + 1) + c);
-            }
-#pragma unroll
-            for (int c = 0; c < 6; c++) {
-                const bf16x8 ab = __builtin_bit_cast(bf16x8, af[bt & 1][c]);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, qh[6 * bt + c], s, 0, 0, 0);
-                s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, ql[6 * bt + c], s2, 0, 0, 0);
-            }
-        }
-        s += s2;
-        const int head = hg * 16 + kl;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = k0 + 4 * g + i;
-            sv[i] = key < kend ? s[i] * a.scale : -INFINITY;
-            if (a.scores && key < kend && head < a.NH)
-                a.scores[((size_t)b * a.NH + head) * a.probs_stride + key] = sv[i];
-        }
-    };
-    /* P = e^(s - m) into the sums and O[head][r] += P . C_kv.  P[head kl][keys
-     * 4g .. 4g+3] is a bf16 hi/lo pair of A operands; the B operands come by
-     * transposing reads (lane 4k + c of group g reads row 4g + k, columns
-     * 16 nb + 4c .. +3), one batch of 8 ahead of the MFMAs. */
-    auto accumulate = [&](uint32_t t, const float *sv) {
-        const uint32_t tb = t + (4 * g + (kl >> 2)) * CROW_B + 8 * (kl & 3);
-        s16x4 bv[2][8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) bv[0][j] = ds_read_tr16(tb, 32 * j);
-        s16x4 ph, pl;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float p = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - m);
-            l += p;
-            uint16_t hi, lo;
-            split_bf16(p, &hi, &lo);
-            ph[i] = (short)hi;
-            pl[i] = (short)lo;
-        }
-        const bf16x8 pa = __builtin_bit_cast(bf16x8, (s16x8){ph[0], ph[1], ph[2], ph[3], pl[0], pl[1], pl[2], pl[3]});
-#pragma unroll
-        for (int bt = 0; bt < KVL / 128; bt++) {
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(bv[bt & 1][0]), "+v"(bv[bt & 1][1]), "+v"(bv[bt & 1][2]), "+v"(bv[bt & 1][3]),
-                           "+v"(bv[bt & 1][4]), "+v"(bv[bt & 1][5]), "+v"(bv[bt & 1][6]), "+v"(bv[bt & 1][7]));
-            if (bt + 1 < KVL / 128) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) bv[(bt + 1) & 1][j] = ds_read_tr16(tb, 32 * (8 * (bt + 1) + j));
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int nb = 8 * bt + j;
-                /* K = 32 as (key 4g + i, hi) at 8g + i and (key 4g + i, lo)
-                 * at 8g + 4 + i: the hi and lo products in one MFMA */
-                const s16x4 c = bv[bt & 1][j];
-                const bf16x8 bb = __builtin_bit_cast(bf16x8, (s16x8){c[0], c[1], c[2], c[3], c[0], c[1], c[2], c[3]});
-                O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bb, O[nb], 0, 0, 0);
-            }
-        }
-    };
     /* The inner loop touches O only through MFMAs (it stays in accumulation
      * registers); a sub-tile that needs a rescale leaves it, and the outer
      * loop rescales and accumulates that sub-tile. */
@@ -439,13 +446,13 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             else VMCNT_WAIT(0);
             __builtin_amdgcn_sched_barrier(0);
             const uint32_t t = lds_addr(stage(st));
-            score(t, k0, sv);
+            mla_score(a, t, k0, kend, b, hg, kl, g, qh, ql, sv);
             const float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
             if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_TAU)) {
                 moved = true;
                 break;
             }
-            accumulate(t, sv);
+            mla_accumulate(t, sv, m, l, O, kl, g);
             __builtin_amdgcn_sched_barrier(0);
             /* this stage's LDS reads are complete (accumulate waits for them
              * before its last MFMAs): refill it with the sub-tile after next */
@@ -478,7 +485,7 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
             }
         }
         m = mnew;
-        accumulate(lds_addr(stage(st)), sv);
+        mla_accumulate(lds_addr(stage(st)), sv, m, l, O, kl, g);
         __builtin_amdgcn_sched_barrier(0);
         if (k0 + 32 < kend) issue(st, k0 + 32);
         __builtin_amdgcn_sched_barrier(0);
