@@ -60,6 +60,7 @@ static const struct {
     [K_MLA_QPREP] = {"mm_mla_qprep", MOD_MLA},
     [K_MLA_ROPE_QPREP] = {"mm_mla_rope_qprep", MOD_MLA},
     [K_MLA_ATTN] = {"mm_mla_attn", MOD_MLA},
+    [K_MLA_ATTN_ROWS] = {"mm_mla_attn_rows", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
     [K_MLA_UV] = {"mm_mla_uv", MOD_MLA},
     [K_MLA_WPREP] = {"mm_mla_wprep", MOD_MLA},
@@ -171,6 +172,10 @@ int mm_ctx_create(int device, mm_ctx **out) {
     /* MLAMOE_MLA_PART_MAX (bytes) overrides the cap on the attention chunk
      * partials of one launch, above which rows go in groups */
     c->mla_part_max = MM_MLA_PART_MAX;
+    {
+        const char *r4 = getenv("MLAMOE_MLA_ROWS4");
+        c->mla_rows4 = !(r4 && r4[0] == '0');
+    }
     ev = getenv("MLAMOE_MLA_PART_MAX");
     if (ev && *ev && atoll(ev) > 0) c->mla_part_max = (size_t)atoll(ev);
     /* MLAMOE_MOE_T_CHUNK lowers the rows of one MoE forward pass (longer

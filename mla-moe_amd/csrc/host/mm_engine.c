@@ -317,6 +317,10 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
         if (w < 0 || w >= R || (j > 0 && w <= hio[IO_WANT * MR + j - 1]))
             return mm_fail(MM_ERR_INVALID, "mm_engine_step: want_rows must ascend within [0, %d)", R);
     }
+    /* every group of 4 rows in one slot (a prefill's positions): the
+     * attention reads each group's keys once */
+    int rows4 = R > 1;
+    for (int r = 0; r < R && rows4; r++) rows4 = hio[IO_SLOT * MR + r] == hio[IO_SLOT * MR + (r & ~3)];
     int st = mm_engine_reserve(e, kvmax);
     if (st) return st;
     if ((st = mm_set_device(c))) return st;
@@ -343,7 +347,7 @@ static int engine_run(mm_engine *e, int R, int n_want, int32_t *next, float *log
             return st;
         if ((st = mm_mla_decode_rows(c, l, R, e->q, e->cache[l], e->lcap[l], d_slot, d_len, kvmax,
                                      e->ctxo, NULL, NULL, NULL, fuse ? &ra : NULL,
-                                     hl_rows(e, R) ? e->ctx_hl : NULL)))
+                                     hl_rows(e, R) ? e->ctx_hl : NULL, rows4)))
             return st;
         const int dense = l < f->first_k_dense;
         if ((st = oproj_post_norm(e, L, R, dense))) return st;

@@ -37,6 +37,7 @@ typedef enum {
     K_MLA_QPREP,
     K_MLA_ROPE_QPREP,
     K_MLA_ATTN,
+    K_MLA_ATTN_ROWS,
     K_MLA_COMBINE,
     K_MLA_UV,
     K_MLA_WPREP,
@@ -131,6 +132,8 @@ struct mm_ctx {
 
     int i8_tiled_min_t;         /* token count from which the tiled int8 GEMM is used */
     size_t mla_part_max;        /* attention chunk partials per launch (bytes) */
+    int mla_rows4;              /* row groups sharing a sequence read its keys once
+                                   (MLAMOE_MLA_ROWS4=0: per row, for comparisons) */
     int moe_t_chunk;            /* cap on the rows of one MoE forward pass (0: MM_MOE_T_CHUNK) */
 
     /* growable device workspace */
@@ -245,11 +248,14 @@ int mm_mla_front_rows(mm_ctx *ctx, int B, const float *x, const mm_mla_front_wei
                       int seq_stride, float *kv_rows, const float *xn_pre,
                       const uint16_t *xn_pre_hl, float *comp_buf, mm_mla_rope_args *defer);
 /* rope (or NULL): the deferred RoPE of mm_mla_front_rows, run with qprep;
- * ctx_hl (or NULL): ctx_out also as bf16 hi/lo planes [2, B, NH * VHD]. */
+ * ctx_hl (or NULL): ctx_out also as bf16 hi/lo planes [2, B, NH * VHD].
+ * rows4: slots given and rows 4 j .. 4 j + 3 of every group share a cache
+ * sequence (a prefill's consecutive positions): the attention reads each
+ * group's keys once (mm_mla_attn_rows). */
 int mm_mla_decode_rows(mm_ctx *ctx, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope, uint16_t *ctx_hl);
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int rows4);
 
 void mm_moe_release(mm_ctx *ctx);
 void mm_mla_release(mm_ctx *ctx);

@@ -69,20 +69,21 @@ int mm_mla_absorbed_decode_dev(mm_ctx *c, int layer, int B, const float *q,
                                int kv_len, float *ctx_out, float *qabs, float *probs,
                                float *clat) {
     return mm_mla_decode_rows(c, layer, B, q, cache, seq_stride, NULL, kv_lens, kv_len, ctx_out,
-                              qabs, probs, clat, NULL, NULL);
+                              qabs, probs, clat, NULL, NULL, 0);
 }
 
 static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in);
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in,
+                       int rows4);
 
 int mm_mla_decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope, uint16_t *ctx_hl) {
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int rows4) {
     return decode_rows(c, layer, B, q, cache, seq_stride, slots, kv_lens, kv_len, ctx_out, qabs,
-                       probs, clat, rope, ctx_hl, 0, 0);
+                       probs, clat, rope, ctx_hl, 0, 0, rows4 && slots && c->mla_rows4);
 }
 
 /* The merge's blocks per (head, sequence): the latent columns over 4 blocks
@@ -97,7 +98,8 @@ static unsigned merge_z(int NH, int B) { return (size_t)NH * B < 128 ? MM_MLA_KV
 static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16_t *cache,
                        int seq_stride, const int32_t *slots, const int32_t *kv_lens, int kv_len,
                        float *ctx_out, float *qabs, float *probs, float *clat,
-                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in) {
+                       const mm_mla_rope_args *rope, uint16_t *ctx_hl, int chunk_in, unsigned zc_in,
+                       int rows4) {
     if (!c) return mm_fail(MM_ERR_INVALID, "mm_mla_absorbed_decode_dev: NULL context");
     if (!c->mla_ready || layer < 0 || layer >= c->mla_layers || !c->mla_kvb[layer])
         return mm_fail(MM_ERR_STATE, "mm_mla_absorbed_decode_dev: layer %d not loaded", layer);
@@ -113,8 +115,9 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
      * over more CUs; long contexts keep the longest chunk, up to
      * MM_MLA_MAXCH of them (the merge's limit) */
     int chunk = MM_MLA_CHUNK;
+    const size_t Bblk = rows4 ? (size_t)(B + MM_MLA_AW - 1) / MM_MLA_AW : (size_t)B;   /* blocks per chunk */
     while (chunk > 16 * MM_MLA_AW &&
-           (size_t)B * HG0 * ((kv_len + chunk - 1) / chunk) < MM_MLA_MIN_BLOCKS &&
+           Bblk * HG0 * ((kv_len + chunk - 1) / chunk) < MM_MLA_MIN_BLOCKS &&
            (kv_len + chunk / 2 - 1) / (chunk / 2) <= 64)
         chunk /= 2;
     /* a second chunk of under half a chunk (short contexts): one chunk of
@@ -143,7 +146,8 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const size_t part_row = direct ? 0 : (size_t)HG * nchunks * (16 * MM_MLA_KVL + 32) * 4;
     if (!chunk_in && !ctx_hl && (size_t)B * part_row > c->mla_part_max) {
         if (rope && (st = mm_launch(c, K_MLA_ROPE, (unsigned)B, 1, 1, 256, 0, (void *)rope))) return st;
-        const int G = (int)(c->mla_part_max / part_row) > 0 ? (int)(c->mla_part_max / part_row) : 1;
+        int G = (int)(c->mla_part_max / part_row) > 0 ? (int)(c->mla_part_max / part_row) : 1;
+        if (rows4) G = G >= MM_MLA_AW ? G / MM_MLA_AW * MM_MLA_AW : MM_MLA_AW;   /* whole row groups */
         const int QKD = g->qk_nope_head_dim + MM_MLA_QKR;
         for (int r0 = 0; r0 < B; r0 += G) {
             const int n = B - r0 < G ? B - r0 : G;
@@ -155,7 +159,7 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
                      slots ? slots + r0 : NULL, kv_lens ? kv_lens + r0 : NULL, kv_len,
                      ctx_out + rq * g->v_head_dim, qabs ? qabs + rq * MM_MLA_KVL : NULL,
                      probs ? probs + rq * kv_len : NULL, clat ? clat + rq * MM_MLA_KVL : NULL, NULL,
-                     NULL, chunk, merge_z(NH, B))))
+                     NULL, chunk, merge_z(NH, B), rows4)))
                 return st;
         }
         return MM_OK;
@@ -195,9 +199,11 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     /* dynamic LDS: two 16-key cache tiles per wave (c_kv rows padded to 1056 B,
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
-    /* a row's chunks on one XCD: see mm_mla_attn_args */
-    const unsigned ntrip = (unsigned)B * (unsigned)HG * (unsigned)nchunks;
-    if ((st = mm_launch(c, K_MLA_ATTN, 8 * ((ntrip + 7) / 8), 1, 1, 64 * MM_MLA_AW, alds, &aa)))
+    /* a row's chunks on one XCD: see mm_mla_attn_args; row groups sharing
+     * a sequence: one block per group */
+    const unsigned ntrip = (unsigned)Bblk * (unsigned)HG * (unsigned)nchunks;
+    if ((st = mm_launch(c, rows4 ? K_MLA_ATTN_ROWS : K_MLA_ATTN, 8 * ((ntrip + 7) / 8), 1, 1, 64 * MM_MLA_AW,
+                        rows4 ? (size_t)MM_MLA_ROWS_LDS : alds, &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks,

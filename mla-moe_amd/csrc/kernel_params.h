@@ -317,6 +317,9 @@ typedef struct {
 #define MM_MLA_PART_MAX ((size_t)512 << 20)   /* bytes of attention chunk partials per launch */
 #endif
 #define MM_MLA_TILE_B (16 * 1056 + 16 * 128)   /* LDS bytes of one 16-key sub-tile */
+/* mm_mla_attn_rows' dynamic LDS: each wave's row output, 16 heads of
+ * MM_MLA_KVL + 4 floats (it also holds the shared sub-tile ring) */
+#define MM_MLA_ROWS_LDS (MM_MLA_AW * 16 * (MM_MLA_KVL + 4) * 4)
 
 /* qabs = q_nope . W_UK per head. */
 typedef struct {

@@ -562,6 +562,200 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
     }
 }
 
+/* Rows that read one cache sequence in groups of AW (a prefill's
+ * consecutive positions): one block per (row group, head group, chunk) in
+ * the XCD-grouped 1-D order of mm_mla_attn (triples over ceil(B / AW)
+ * groups); wave w is row AW grp + w and takes every key of the chunk below
+ * its own length.  The chunk's 16-key sub-tiles go through a ring of NSR
+ * stages shared by the block -- each wave loads 5 of a sub-tile's 18
+ * pieces (the two k_pe pieces twice, identical bytes) -- so the group's
+ * rows read their common keys once instead of once per row; one barrier
+ * per sub-tile (every wave's pieces of it landed, every wave done with the
+ * stage the refill takes).  No merge across waves: each wave leaves its
+ * row's partial (or, with one chunk, clat) through its own LDS region.
+ * a.slots is required and the host guarantees that a group's rows share a
+ * sequence.  Dynamic LDS: AW * 16 * OROW * 4 bytes (>= NSR * TILE_B). */
+#define NSR 4                      /* shared sub-tile stages */
+#define RPIECES 5                  /* pieces per wave per sub-tile */
+static_assert(NSR * TILE_B <= AW * 16 * OROW * 4 && AW * 16 * OROW * 4 == MM_MLA_ROWS_LDS, "row-group LDS");
+static_assert(AW == 4, "pieces of a sub-tile over four waves");
+extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn_rows(mm_mla_attn_args a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
+    const int ngrp = (a.B + AW - 1) / AW;
+    const int ntrip = ngrp * a.HG * a.nchunks, per = (ntrip + 7) / 8;
+    const int trip = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (trip >= ntrip) return;
+    const int chunk = trip % a.nchunks, hg = (trip / a.nchunks) % a.HG, grp = trip / (a.nchunks * a.HG);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, kl = lane & 15;
+    const int b = grp * AW + w;                       /* this wave's row */
+    const bool brow = b < a.B;
+    const int bc = min(b, a.B - 1);
+    auto len = [&](int r) { return a.kv_lens ? min(a.kv_lens[r], a.kv_len) : a.kv_len; };
+    int lmax = 0;
+#pragma unroll
+    for (int r = 0; r < AW; r++) lmax = max(lmax, len(min(grp * AW + r, a.B - 1)));
+    const int kbeg = chunk * a.chunk;
+    const int kend = brow ? min(kbeg + a.chunk, len(bc)) : kbeg;   /* this wave's keys */
+    const int nsub = max(min(kbeg + a.chunk, lmax) - kbeg + 15, 0) / 16;   /* the block's sub-tiles */
+    const int klast = max(lmax - 1, 0);
+    const uint8_t *cseq = (const uint8_t *)(a.cache + (size_t)a.slots[grp * AW] * a.seq_stride * KVD);
+    auto stage = [&](int st) { return alds + (size_t)st * TILE_B; };
+    /* pieces w, w + 4, w + 8, w + 12 (c_kv rows) and k_pe piece w & 1 of
+     * the sub-tile at key k0 (rows past the group's longest row load row
+     * lmax - 1, masked in the softmax) */
+    auto issue = [&](int st, int k0) {
+        uint8_t *t = stage(st);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int p = w + 4 * j;
+            const int key = __builtin_amdgcn_readfirstlane(min(k0 + p, klast));
+            lds_dma16(cseq + (uint32_t)(key * KVD * 2) + lane * 16, t + p * CROW_B);
+        }
+        const int q = w & 1;
+        const int key = min(k0 + 8 * q + (lane >> 3), klast);
+        lds_dma16(cseq + (uint32_t)(key * KVD * 2 + KVL * 2 + (lane & 7) * 16), t + 16 * CROW_B + q * 1024);
+    };
+
+    /* Q of this wave's row (as mm_mla_attn, from global memory: a row's Q
+     * is read by its chunks' blocks only), then the ring's first NSR - 1
+     * sub-tiles; assembly loads, waited for by hand (after a direct-to-LDS
+     * load the compiler waits for every load in flight at the first use of
+     * a loaded register) */
+    bf16x8 qh[KC], ql[KC];
+    f32x4 qpe[KC - KVL / 32][2];
+    static_assert(KC - KVL / 32 == 2, "q_pe: two 32-value K steps");
+    const bool qreal = hg * 16 + kl < a.NH;
+    {
+        const int qhd = qreal ? hg * 16 + kl : 0;
+        const uint16_t *qa = a.qhl + ((size_t)bc * a.NH + qhd) * 2 * KVL + 8 * g;
+        const float *qp = a.q + ((size_t)bc * a.NH + qhd) * (a.QKN + MM_MLA_QKR) + a.QKN + 8 * g;
+#pragma unroll
+        for (int c = 0; c < KVL / 32; c++) {
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qh[c]) : "v"(qa), "i"(64 * c));
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(ql[c]) : "v"(qa), "i"(2 * KVL + 64 * c));
+        }
+#pragma unroll
+        for (int c = 0; c < KC - KVL / 32; c++) {
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qpe[c][0]) : "v"(qp), "i"(128 * c));
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(qpe[c][1]) : "v"(qp), "i"(128 * c + 16));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < NSR - 1; st++) issue(st, kbeg + 16 * st);
+    __builtin_amdgcn_sched_barrier(0);
+    static_assert((NSR - 1) * RPIECES == 15, "wait count");
+    asm volatile("s_waitcnt vmcnt(15)"
+                 : "+v"(qh[0]), "+v"(qh[1]), "+v"(qh[2]), "+v"(qh[3]), "+v"(qh[4]), "+v"(qh[5]), "+v"(qh[6]),
+                   "+v"(qh[7]), "+v"(qh[8]), "+v"(qh[9]), "+v"(qh[10]), "+v"(qh[11]), "+v"(qh[12]), "+v"(qh[13]),
+                   "+v"(qh[14]), "+v"(qh[15]), "+v"(qpe[0][0]), "+v"(qpe[0][1]));
+    asm volatile(""
+                 : "+v"(ql[0]), "+v"(ql[1]), "+v"(ql[2]), "+v"(ql[3]), "+v"(ql[4]), "+v"(ql[5]), "+v"(ql[6]),
+                   "+v"(ql[7]), "+v"(ql[8]), "+v"(ql[9]), "+v"(ql[10]), "+v"(ql[11]), "+v"(ql[12]), "+v"(ql[13]),
+                   "+v"(ql[14]), "+v"(ql[15]), "+v"(qpe[1][0]), "+v"(qpe[1][1]));
+    {
+        const bf16x8 z8 = __builtin_bit_cast(bf16x8, (u16x8){});
+#pragma unroll
+        for (int c = 0; c < KVL / 32; c++) {
+            qh[c] = qreal ? qh[c] : z8;
+            ql[c] = qreal ? ql[c] : z8;
+        }
+#pragma unroll
+        for (int c = KVL / 32; c < KC; c++) {
+            const f32x4 x0 = qpe[c - KVL / 32][0], x1 = qpe[c - KVL / 32][1];
+            u16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint16_t h16, l16;
+                split_bf16(qreal ? (j < 4 ? x0[j & 3] : x1[j & 3]) : 0.0f, &h16, &l16);
+                hi[j] = h16;
+                lo[j] = l16;
+            }
+            qh[c] = __builtin_bit_cast(bf16x8, hi);
+            ql[c] = __builtin_bit_cast(bf16x8, lo);
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;        /* head kl: running max; this lane's share of the sum */
+    f32x4 O[KVL / 16];
+#pragma unroll
+    for (int nb = 0; nb < KVL / 16; nb++) O[nb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < nsub; i++) {
+        /* this wave's pieces of sub-tile i have landed once at most those of
+         * the next NSR - 2 sub-tiles are outstanding (every step issues one
+         * sub-tile, past the chunk at clamped keys: the count holds to the
+         * end); the barrier: every wave's pieces, and every wave done with
+         * sub-tile i - 1, whose stage the refill below takes */
+        static_assert((NSR - 2) * RPIECES == 10, "wait count");
+        VMCNT_WAIT(10);
+        /* a bare barrier: __syncthreads() would also wait for every load
+         * in flight (the ring's later sub-tiles) */
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue((i + NSR - 1) % NSR, kbeg + 16 * (i + NSR - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        const int k0 = kbeg + 16 * i;
+        const uint32_t t = lds_addr(stage(i % NSR));
+        float sv[4];
+        mla_score(a, t, k0, kend, bc, hg, kl, g, qh, ql, sv);
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE_TAU)) {
+            /* some head's maximum moved: new m = the head's max over the
+             * sub-tile (across the 4 lane groups); O and l rescaled unless
+             * still empty */
+            mx = fmaxf(mx, __shfl_xor(mx, 16, MM_WAVE));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, MM_WAVE));
+            const float mnew = fmaxf(m, mx);
+            if (__builtin_amdgcn_ballot_w64(m != -INFINITY)) {
+                const float cr = m == -INFINITY ? 0.0f : __expf(m - mnew);
+                l *= cr;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float ci = __shfl(cr, 4 * g + r, MM_WAVE);
+#pragma unroll
+                    for (int nb = 0; nb < KVL / 16; nb++) O[nb][r] *= ci;
+                }
+            }
+            m = mnew;
+        }
+        mla_accumulate(t, sv, m, l, O, kl, g);
+    }
+    VMCNT_WAIT(0);
+    __syncthreads();   /* every stage read: the LDS takes the waves' outputs */
+
+    /* this wave's row: (m, l) per head and O, scaled by 1 / l for clat */
+    l += __shfl_xor(l, 16, MM_WAVE);
+    l += __shfl_xor(l, 32, MM_WAVE);
+    float *ob = (float *)alds + (size_t)w * 16 * OROW;
+    const float fself = a.clat ? (l > 0.0f ? 1.0f / l : 0.0f) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float fr = __shfl(fself, 4 * g + r, MM_WAVE);
+#pragma unroll
+        for (int nb = 0; nb < KVL / 16; nb++) ob[(4 * g + r) * OROW + nb * 16 + kl] = O[nb][r] * fr;
+    }
+    if (!brow) return;
+    const size_t pidx = ((size_t)(b * a.HG + hg) * a.nchunks + chunk);
+    if (!a.clat && g == 0) {
+        a.part_ml[pidx * 32 + kl] = m;
+        a.part_ml[pidx * 32 + 16 + kl] = l;
+    }
+#pragma unroll 4
+    for (int j = 0; j < 16 * KVL / (4 * MM_WAVE); j++) {
+        const int e = 4 * (lane + j * MM_WAVE);
+        const int hh = e / KVL, col = e % KVL;
+        const f32x4 v = *(const f32x4 *)(ob + hh * OROW + col);
+        if (a.clat) {
+            const int head = hg * 16 + hh;
+            if (head < a.NH) *(f32x4 *)(a.clat + ((size_t)b * a.NH + head) * KVL + col) = v;
+        } else {
+            *(f32x4 *)(a.part_o + pidx * 16 * KVL + e) = v;
+        }
+    }
+}
+
 /* Merge the chunk partials of (head h, sequence b): clat = sum_c w_c O_c / l
  * with w_c = e^(m_c - m); also turns the debug scores into probabilities.
  * grid (NH, B, Z) with Z = 1 or KVL / 128, 256 threads: block z owns the
