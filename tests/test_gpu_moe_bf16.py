@@ -152,6 +152,23 @@ def test_ffn_down_hidden_row_forms(ctx, oracle, K, I, NS):
     assert max_abs_rel(out, ro) < TOL
 
 
+@pytest.mark.parametrize("H", [1032, 4096])
+def test_ffn_gate_up_x_forms(ctx, oracle, H):
+    """The gate/up stage stages x in LDS in 1 KB pieces: 1032 values (the
+    last piece partly past x, chunks past the row clamped) and 4096 (two
+    groups of chunks per row pair, the second reading the staged x)."""
+    print(f"ffn gate/up x H={H}", flush=True)
+    E, K, I, NS, T = 8, 2, 64, 1, 2
+    w = synth.moe_layer(61 + H, H, E, I, NS)
+    _layer_ctx(ctx, w, H, E, NS, K, I)
+    x = synth.activations(62 + H, T, H)
+    cfg = oracle.moe_cfg(H, E, NS, K, I)
+    ro, ri, rw, rp = oracle.ffn_compute_rows(cfg, w, x)
+    out, idx, wt, probs = ctx.moe_forward(0, x)
+    assert np.array_equal(idx, ri)
+    assert max_abs_rel(out, ro) < TOL
+
+
 def test_rejects_bad_shapes(ctx):
     with pytest.raises(mlamoe.MMError):
         ctx.moe_init(100, 8, 1, 2, 12)          # H not a multiple of 8
