@@ -200,10 +200,10 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
      * then the k_pe parts); also holds the waves' partial states for the merge */
     const size_t alds = (size_t)MM_MLA_AW * 2 * MM_MLA_TILE_B;   /* two sub-tile stages per wave */
     /* a row's chunks on one XCD: see mm_mla_attn_args; row groups sharing
-     * a sequence: one block per group */
+     * a sequence: one block per group, in index order */
     const unsigned ntrip = (unsigned)Bblk * (unsigned)HG * (unsigned)nchunks;
-    if ((st = mm_launch(c, rows4 ? K_MLA_ATTN_ROWS : K_MLA_ATTN, 8 * ((ntrip + 7) / 8), 1, 1, 64 * MM_MLA_AW,
-                        rows4 ? (size_t)MM_MLA_ROWS_LDS : alds, &aa)))
+    if ((st = mm_launch(c, rows4 ? K_MLA_ATTN_ROWS : K_MLA_ATTN, rows4 ? ntrip : 8 * ((ntrip + 7) / 8), 1, 1,
+                        64 * MM_MLA_AW, rows4 ? (size_t)MM_MLA_ROWS_LDS : alds, &aa)))
         return st;
     mm_mla_combine_args ca = {part_ml, part_o, c->mla_kvb[layer], kv_lens, kv_len, ctx_out, clat,
                               probs, kv_len, B, NH, g->qk_nope_head_dim, g->v_head_dim, HG, nchunks,

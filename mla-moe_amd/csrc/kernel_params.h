@@ -341,7 +341,9 @@ typedef struct {
  * * nchunks of them, in that order (row-major): a 1-D grid of 8 * ceil(N / 8)
  * blocks, block L taking triple (L % 8) * ceil(N / 8) + L / 8 (blocks past N
  * exit), so that a row's chunks run on one XCD (blocks are dealt to the 8
- * XCDs in turn) and share its Q in that L2. */
+ * XCDs in turn) and share its Q in that L2 -- with one length for every
+ * row; with kv_lens, block L takes triple N - 1 - L (rows of unequal
+ * lengths spread over the XCDs, a prefill's longest first). */
 typedef struct {
     const uint16_t *qhl;      /* [B, NH, 2, KVL] bf16: qabs as hi + lo halves (qprep) */
     const float *q;           /* [B, NH, QKN + QKR] (the q_pe part) */

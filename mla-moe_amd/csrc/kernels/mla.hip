@@ -285,9 +285,14 @@ __device__ __forceinline__ void mla_accumulate(uint32_t t, const float *sv, floa
  * Dynamic LDS: AW * 2 * TILE_B bytes (the merge reuses it). */
 extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_attn_args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
+    /* XCD-grouped order for rows of one length; rows of their own lengths
+     * (kv_lens) last row first, in index order over the XCDs in turn, so
+     * that long and short rows spread over the XCDs and a prefill's longest
+     * rows start first */
     const int ntrip = a.B * a.HG * a.nchunks, per = (ntrip + 7) / 8;
-    const int trip = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-    if (trip >= ntrip) return;
+    const int trip = a.kv_lens ? ntrip - 1 - (int)blockIdx.x
+                               : (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (trip < 0 || trip >= ntrip) return;   /* the grid is rounded up to 8 blocks */
     const int chunk = trip % a.nchunks, hg = (trip / a.nchunks) % a.HG, b = trip / (a.nchunks * a.HG);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -563,9 +568,9 @@ extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn(mm_mla_at
 }
 
 /* Rows that read one cache sequence in groups of AW (a prefill's
- * consecutive positions): one block per (row group, head group, chunk) in
- * the XCD-grouped 1-D order of mm_mla_attn (triples over ceil(B / AW)
- * groups); wave w is row AW grp + w and takes every key of the chunk below
+ * consecutive positions): one block per (row group, head group, chunk), a
+ * 1-D grid of ceil(B / AW) HG nchunks blocks, the last group's first;
+ * wave w is row AW grp + w and takes every key of the chunk below
  * its own length.  The chunk's 16-key sub-tiles go through a ring of NSR
  * stages shared by the block -- each wave loads 5 of a sub-tile's 18
  * pieces (the two k_pe pieces twice, identical bytes) -- so the group's
@@ -581,11 +586,16 @@ static_assert(NSR * TILE_B <= AW * 16 * OROW * 4 && AW * 16 * OROW * 4 == MM_MLA
 static_assert(AW == 4, "pieces of a sub-tile over four waves");
 extern "C" __global__ __launch_bounds__(AW * MM_WAVE) void mm_mla_attn_rows(mm_mla_attn_args a) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t alds[];
+    /* last group first (a prefill's longest rows), blocks in index order
+     * over the XCDs in turn: with a prefill's causal lengths, the XCD-grouped
+     * order of mm_mla_attn gave the last XCD every long row (measured: its
+     * blocks ended ~600 us after the first while the others idled) */
     const int ngrp = (a.B + AW - 1) / AW;
-    const int ntrip = ngrp * a.HG * a.nchunks, per = (ntrip + 7) / 8;
-    const int trip = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    const int ntrip = ngrp * a.HG * a.nchunks;
+    const int trip = (int)blockIdx.x;
     if (trip >= ntrip) return;
-    const int chunk = trip % a.nchunks, hg = (trip / a.nchunks) % a.HG, grp = trip / (a.nchunks * a.HG);
+    const int rem = trip % (a.HG * a.nchunks);
+    const int grp = ngrp - 1 - trip / (a.HG * a.nchunks), hg = rem / a.nchunks, chunk = rem % a.nchunks;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, kl = lane & 15;
