@@ -124,6 +124,12 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
      * twice the length instead, whose block writes clat itself (no merge
      * launch) */
     if (chunk < MM_MLA_CHUNK && kv_len > chunk && kv_len <= chunk + chunk / 2) chunk *= 2;
+    /* row groups numerous enough to fill the CUs twice over (a prefill's
+     * causal rows): one block per group takes the whole context and writes
+     * clat itself -- no chunk partials, no merge launch; dealt longest
+     * first, the groups' unequal lengths even out over the CUs */
+    if (rows4 && Bblk * HG0 >= 2 * MM_MLA_MIN_BLOCKS)
+        chunk = (kv_len + 16 * MM_MLA_AW - 1) / (16 * MM_MLA_AW) * (16 * MM_MLA_AW);
     if (chunk_in > 0) chunk = chunk_in;
     const int nchunks = (kv_len + chunk - 1) / chunk;
     const int direct = nchunks == 1 && !probs;

@@ -357,7 +357,8 @@ typedef struct {
     float *scores;            /* [B, NH, probs_stride] scaled scores (debug) or 0 */
     int probs_stride;
     int NH, HG, nchunks, QKN;
-    int chunk;                /* keys per block: a multiple of 16 * MM_MLA_AW, <= MM_MLA_CHUNK */
+    int chunk;                /* keys per block: a multiple of 16 * MM_MLA_AW, <= MM_MLA_CHUNK
+                                 (mm_mla_attn_rows: any length, up to a whole context) */
     const int32_t *slots;     /* [B] cache sequence of row b, or 0: sequence b */
     float *clat;              /* one chunk (nchunks == 1, no probabilities): clat [B, NH, KVL]
                                  written here, O / l as the merge computes it; else 0 */

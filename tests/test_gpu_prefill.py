@@ -152,30 +152,34 @@ def test_prefill_rows_in_attention_groups(monkeypatch):
     assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
 
 
-def test_prefill_row_groups_agree_with_rows(monkeypatch):
+@pytest.mark.parametrize("n", [42, 2048])
+def test_prefill_row_groups_agree_with_rows(monkeypatch, n):
     """A step's rows attend in groups of 4 rows of one slot (the keys read
     once per group) unless MLAMOE_MLA_ROWS4=0; both forms give the same
-    logits to rounding, here with 20 heads (two head groups, the second
-    part empty) and a last group of 2 rows."""
+    logits to rounding.  42 rows: 20 heads (two head groups, the second
+    part empty), a last group of 2 rows, the context in chunks.  2048
+    rows: 512 groups, each group's whole context in one block (no chunk
+    partials, no merge), logits of a sample of rows up to the longest."""
     from mlamoe import synth
     c, _, _ = engine_case("dsv2")
-    c = dict(c, NH=20, n_layers=2)
+    c = dict(c, NH=20 if n < 64 else 16, n_layers=2)
     m = synth.model(971, c["n_layers"], c["first_dense"], c["H"], c["NH"], c["QKN"], c["QKR"],
                     c["KVL"], c["VHD"], c["dense_inter"], c["E"], c["I"], c["n_shared"], c["vocab"])
     inv = np.array([1.0 / 10000.0 ** (2 * j / c["QKR"]) for j in range(c["QKR"] // 2)], np.float32)
-    toks = np.random.default_rng(972).integers(0, c["vocab"], 42).astype(np.int32)
-    n = len(toks)
+    toks = np.random.default_rng(972).integers(0, c["vocab"], n).astype(np.int32)
+    want = np.arange(n) if n < 64 else np.unique(np.r_[np.arange(0, n, 97), n - 5 + np.arange(5)])
     out = []
     for rows4 in ("1", "0"):
         monkeypatch.setenv("MLAMOE_MLA_ROWS4", rows4)
         print(f"row groups {rows4}: {n} rows, NH={c['NH']}", flush=True)
         with mlamoe.Context(0) as ctx:
-            eng = Engine.from_host(ctx, c, m, inv, max_batch=2, max_seq=64)
+            eng = Engine.from_host(ctx, c, m, inv, max_batch=2, max_seq=max(64, n),
+                                   max_rows=n if n > 1024 else 0)
             try:
-                _, lg = eng.step_rows(np.zeros(n), toks, np.arange(n), np.arange(n), want_logits=True)
+                _, lg = eng.step_rows(np.zeros(n), toks, np.arange(n), want, want_logits=True)
             finally:
                 eng.close()
         out.append(lg)
     err = max(max_abs_rel(a, b) for a, b in zip(out[0], out[1]))
-    print(f"worst normwise difference {err:.2e}", flush=True)
-    assert 0.0 < err < 1e-4    # the two forms sum a row's keys in different orders
+    print(f"worst normwise difference {err:.2e} over {len(want)} rows", flush=True)
+    assert 0.0 < err < 1e-4    # the two forms sum a row's keys in different orders    # the two forms sum a row's keys in different orders
