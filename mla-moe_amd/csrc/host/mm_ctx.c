@@ -63,6 +63,8 @@ static const struct {
     [K_MLA_ATTN_ROWS] = {"mm_mla_attn_rows", MOD_MLA},
     [K_MLA_COMBINE] = {"mm_mla_combine", MOD_MLA},
     [K_MLA_UV] = {"mm_mla_uv", MOD_MLA},
+    [K_MLA_QPREP_W] = {"mm_mla_qprep_w", MOD_MLA},
+    [K_MLA_UV_W] = {"mm_mla_uv_w", MOD_MLA},
     [K_MLA_WPREP] = {"mm_mla_wprep", MOD_MLA},
     [K_GEMM_BF16] = {"mm_gemm_bf16", MOD_GEMM_BF16},
     [K_CVT_BF16] = {"mm_cvt_bf16", MOD_GEMM_BF16},

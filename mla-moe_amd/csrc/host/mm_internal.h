@@ -40,6 +40,8 @@ typedef enum {
     K_MLA_ATTN_ROWS,
     K_MLA_COMBINE,
     K_MLA_UV,
+    K_MLA_QPREP_W,
+    K_MLA_UV_W,
     K_MLA_WPREP,
     K_GEMM_BF16,
     K_CVT_BF16,

@@ -170,7 +170,9 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
         }
         return MM_OK;
     }
-    const size_t qa_b = qabs ? 0 : (size_t)B * NH * MM_MLA_KVL * 4;
+    /* qabs in fp32 only for a caller that asks for it (the attention reads
+     * its bf16 hi / lo rows) */
+    const size_t qa_b = 0;
     /* chunk partials (none when one block takes a row's whole context) */
     const size_t ml_b = direct ? 0 : (size_t)B * HG * nchunks * 32 * 4;
     const size_t po_b = direct ? 0 : (size_t)B * HG * nchunks * 16 * MM_MLA_KVL * 4;
@@ -181,7 +183,6 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const size_t a3 = (ml_b + 255) & ~(size_t)255, a4 = (po_b + 255) & ~(size_t)255;
     const size_t a5 = (cl_b + 255) & ~(size_t)255;
     if ((st = mm_workspace(c, a1 + a2 + a3 + a4 + a5 + qhl_b, (void **)&ws))) return st;
-    if (!qabs) qabs = (float *)(ws + a1);
     float *part_ml = (float *)(ws + a1 + a2), *part_o = (float *)(ws + a1 + a2 + a3);
     if (!clat) clat = (float *)(ws + a1 + a2 + a3 + a4);
     uint16_t *qhl = (uint16_t *)(ws + a1 + a2 + a3 + a4 + a5);
@@ -189,14 +190,19 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const int QKN = g->qk_nope_head_dim;
     const size_t nkvb = (size_t)NH * (QKN + g->v_head_dim) * MM_MLA_KVL;
     mm_mla_qprep_args qa = {q, c->mla_kvb[layer] + nkvb, qabs, qhl, B, NH, QKN};
+    /* many rows (a prefill): MM_MLA_WIDE_S column tiles per wave in the W_UK
+     * and W_UV products, a 32-row tile of their fp32 operand read and split
+     * once for all of them */
+    const int wide = B >= MM_MLA_WIDE_B;
     if (rope) {   /* the front's RoPE / cache append in the same launch */
         mm_mla_rope_qprep_args rq;
         rq.r = *rope;
         rq.qp = qa;
         const unsigned nq = (unsigned)(MM_MLA_KVL / 64 * NH * ((B + 31) / 32));
         if ((st = mm_launch(c, K_MLA_ROPE_QPREP, (unsigned)B + nq, 1, 1, 256, 0, &rq))) return st;
-    } else if ((st = mm_launch(c, K_MLA_QPREP, MM_MLA_KVL / 64, (unsigned)NH, (unsigned)((B + 31) / 32),
-                               256, 0, &qa))) {
+    } else if ((st = mm_launch(c, wide ? K_MLA_QPREP_W : K_MLA_QPREP,
+                               MM_MLA_KVL / (wide ? 64 * MM_MLA_WIDE_S : 64), (unsigned)NH,
+                               (unsigned)((B + 31) / 32), 256, 0, &qa))) {
         return st;
     }
     mm_mla_attn_args aa = {qhl, q, cache, kv_lens, kv_len, seq_stride, g->softmax_scale, part_ml,
@@ -217,7 +223,8 @@ static int decode_rows(mm_ctx *c, int layer, int B, const float *q, const uint16
     const unsigned zc = chunk_in > 0 ? zc_in : merge_z(NH, B);
     if (!direct && (st = mm_launch(c, K_MLA_COMBINE, (unsigned)NH, (unsigned)B, zc, 256, 0, &ca)))
         return st;
-    return mm_launch(c, K_MLA_UV, (unsigned)((g->v_head_dim + 15) / 16), (unsigned)NH,
+    const int vt = wide ? 16 * MM_MLA_WIDE_S : 16;
+    return mm_launch(c, wide ? K_MLA_UV_W : K_MLA_UV, (unsigned)((g->v_head_dim + vt - 1) / vt), (unsigned)NH,
                      (unsigned)((B + 31) / 32), 256, 0, &ca);
 }
 

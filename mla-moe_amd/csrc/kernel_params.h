@@ -303,6 +303,12 @@ typedef struct {
 #ifndef MM_MLA_CHUNK
 #define MM_MLA_CHUNK 512          /* keys per attention block (the longest chunk) */
 #endif
+/* From MM_MLA_WIDE_B rows on, the W_UK and W_UV products take
+ * MM_MLA_WIDE_S column tiles per wave (mm_mla_qprep_w, mm_mla_uv_w). */
+#ifndef MM_MLA_WIDE_B
+#define MM_MLA_WIDE_B 512
+#endif
+#define MM_MLA_WIDE_S 4
 #ifndef MM_MLA_MIN_BLOCKS
 #define MM_MLA_MIN_BLOCKS 256     /* chunks shrink (to 16 keys per wave) until the grid has this many blocks */
 #endif
@@ -325,7 +331,7 @@ typedef struct {
 typedef struct {
     const float *q;           /* [B, NH, QKN + QKR] */
     const uint16_t *wukT;     /* [NH, KVL, QKN] bf16: W_UK per head, transposed */
-    float *qabs;              /* [B, NH, KVL] */
+    float *qabs;              /* [B, NH, KVL], or 0: not written */
     uint16_t *qhl;            /* [B, NH, 2, KVL] bf16: qabs split into hi (row 0) + lo (row 1) */
     int B, NH, QKN;
 } mm_mla_qprep_args;

@@ -96,6 +96,64 @@ __device__ __forceinline__ void hl_gemm_32x16(const float *X, size_t xs, int mro
     }
 }
 
+/* hl_gemm_32x16 for S column tiles at once (large batches): lane l's W
+ * row of tile s starts at wr[s] (row l % 16 of the tile, chosen by the
+ * caller); each K step's X fragments are loaded and split into hi + lo once
+ * for the S tiles, so a wave reads its 32 rows of X once per S x 16 columns.
+ * On return acc[s][t][i] = Y[16 t + 4 (l / 16) + i][tile s, column l % 16]. */
+template <int S>
+__device__ __forceinline__ void hl_gemm_32x16s(const float *X, size_t xs, int mrows,
+                                               const uint16_t *const (&wr)[S], int k_begin,
+                                               int k_end, f32x4 (&acc)[S][2]) {
+    constexpr int GB = S >= 4 ? 2 : 4;   /* K steps whose loads are issued together */
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int r16 = lane & 15, kq = 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < S; s++) acc[s][0] = acc[s][1] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const float *xr[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int m = 16 * t + r16;
+        xr[t] = X + (size_t)(m < mrows ? m : 0) * xs + kq;
+    }
+    for (int k0 = k_begin; k0 < k_end; k0 += 32 * GB) {
+        u16x8 bw[GB][S];
+        f32x4 xv[GB][2][2];
+#pragma unroll
+        for (int g = 0; g < GB; g++) {
+            const int k = min(k0 + 32 * g, k_end - 32);   /* steps past the end: not used */
+#pragma unroll
+            for (int s = 0; s < S; s++) bw[g][s] = *(const u16x8 *)(wr[s] + kq + k);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                xv[g][t][0] = *(const f32x4 *)(xr[t] + k);
+                xv[g][t][1] = *(const f32x4 *)(xr[t] + k + 4);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GB; g++) {
+            if (k0 + 32 * g >= k_end) break;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                u16x8 hi, lo;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint16_t h16, l16;
+                    split_bf16(xv[g][t][j >> 2][j & 3], &h16, &l16);
+                    hi[j] = h16;
+                    lo[j] = l16;
+                }
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    const bf16x8 b8 = __builtin_bit_cast(bf16x8, bw[g][s]);
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hi), b8, acc[s][t], 0, 0, 0);
+                    acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lo), b8, acc[s][t], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 /* Absorbed queries, qabs[b, h, r] = sum_d q_nope[b, h, d] W_UK_h[d, r], as a
  * per-head GEMM with W_UK_h kept transposed ([r][d], prepared at load
  * time), also written split into bf16 hi + lo (the attention's Q operands,
@@ -119,7 +177,7 @@ __device__ __forceinline__ void qprep_block(const mm_mla_qprep_args &a, int slab
                 const size_t row = (size_t)(b0 + bb) * a.NH + h;
                 uint16_t hi, lo;
                 split_bf16(acc[t][i], &hi, &lo);
-                a.qabs[row * KVL + e] = acc[t][i];
+                if (a.qabs) a.qabs[row * KVL + e] = acc[t][i];
                 a.qhl[row * 2 * KVL + e] = hi;
                 a.qhl[(row * 2 + 1) * KVL + e] = lo;
             }
@@ -128,6 +186,45 @@ __device__ __forceinline__ void qprep_block(const mm_mla_qprep_args &a, int slab
 
 extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep(mm_mla_qprep_args a) {
     qprep_block(a, blockIdx.x, blockIdx.y, blockIdx.z * 32);
+}
+
+/* mm_mla_qprep for large batches (a prefill's rows): grid (KVL / (64 S),
+ * NH, ceil(B / 32)), wave w taking columns (slab S + s) 64 + 16 w .. +15 of
+ * each tile s < S -- the 32 rows of q are read and split once per S tiles
+ * instead of once per tile. */
+static_assert(KVL % (64 * MM_MLA_WIDE_S) == 0, "qprep column slabs");
+extern "C" __global__ __launch_bounds__(256) void mm_mla_qprep_w(mm_mla_qprep_args a) {
+    constexpr int S = MM_MLA_WIDE_S;
+    const int slab = blockIdx.x, h = blockIdx.y, b0 = blockIdx.z * 32;
+    const int QKR = MM_MLA_QKR, QKN = a.QKN;
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int mrows = min(32, a.B - b0);
+    const uint16_t *wr[S];
+#pragma unroll
+    for (int s = 0; s < S; s++)
+        wr[s] = a.wukT + ((size_t)h * KVL + (slab * S + s) * 64 + 16 * wave + (lane & 15)) * QKN;
+    f32x4 acc[S][2];
+    hl_gemm_32x16s<S>(a.q + ((size_t)b0 * a.NH + h) * (QKN + QKR), (size_t)a.NH * (QKN + QKR), mrows,
+                      wr, 0, QKN, acc);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int e = (slab * S + s) * 64 + 16 * wave + (lane & 15);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int bb = 16 * t + 4 * (lane >> 4) + i;
+                if (bb < mrows) {
+                    const size_t row = (size_t)(b0 + bb) * a.NH + h;
+                    uint16_t hi, lo;
+                    split_bf16(acc[s][t][i], &hi, &lo);
+                    if (a.qabs) a.qabs[row * KVL + e] = acc[s][t][i];
+                    a.qhl[row * 2 * KVL + e] = hi;
+                    a.qhl[(row * 2 + 1) * KVL + e] = lo;
+                }
+            }
+    }
 }
 
 /* Load-time: W_UK_h transposed, wukT[h][r][d] = kv_b[h (QKN + VHD) + d][r]. */
@@ -881,6 +978,58 @@ extern "C" __global__ __launch_bounds__(256) void mm_mla_uv(mm_mla_combine_args 
                 }
             }
         }
+}
+
+/* mm_mla_uv for large batches: grid (ceil(VHD / (16 S)), NH, ceil(B / 32)),
+ * each wave S column tiles of its K quarter (clat read and split once per
+ * S tiles); W_UV rows past VHD read row VHD - 1 (results not stored). */
+extern "C" __global__ __launch_bounds__(256) void mm_mla_uv_w(mm_mla_combine_args a) {
+    constexpr int S = MM_MLA_WIDE_S;
+    __shared__ f32x4 red[3][S][2][MM_WAVE];
+    const int v0 = blockIdx.x * 16 * S, h = blockIdx.y, b0 = blockIdx.z * 32;
+    const int lane = threadIdx.x & (MM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / MM_WAVE);
+    const int mrows = min(32, a.B - b0);
+    const uint16_t *wuv = a.kv_b + ((size_t)h * (a.QKN + a.VHD) + a.QKN) * KVL;
+    const uint16_t *wr[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) wr[s] = wuv + (size_t)min(v0 + 16 * s + (lane & 15), a.VHD - 1) * KVL;
+    f32x4 acc[S][2];
+    hl_gemm_32x16s<S>(a.clat + ((size_t)b0 * a.NH + h) * KVL, (size_t)a.NH * KVL, mrows, wr,
+                      wave * (KVL / 4), (wave + 1) * (KVL / 4), acc);
+    if (wave > 0) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            red[wave - 1][s][0][lane] = acc[s][0];
+            red[wave - 1][s][1][lane] = acc[s][1];
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+#pragma unroll
+        for (int w = 0; w < 3; w++) {
+            acc[s][0] += red[w][s][0][lane];
+            acc[s][1] += red[w][s][1][lane];
+        }
+        const int v = v0 + 16 * s + (lane & 15);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int bb = 16 * t + 4 * (lane >> 4) + i;
+                if (bb < mrows && v < a.VHD) {
+                    const size_t o = ((size_t)(b0 + bb) * a.NH + h) * a.VHD + v;
+                    a.ctx[o] = acc[s][t][i];
+                    if (a.ctx_hl) {
+                        const uint16_t hi = rne16(acc[s][t][i]);
+                        a.ctx_hl[o] = hi;
+                        a.ctx_hl[(size_t)a.B * a.NH * a.VHD + o] = rne16(acc[s][t][i] - bf16_f32(hi));
+                    }
+                }
+            }
+    }
 }
 
 /* ---- decode front: RoPE, kv_a_layernorm, latent-cache append ----------------- */

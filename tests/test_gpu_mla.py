@@ -157,6 +157,16 @@ def test_mla_two_row_tiles_ragged(ctx, oracle):
     run_case(ctx, oracle, 16, 40, 1500, 1500, 651, kv_lens=lens)
 
 
+@pytest.mark.parametrize("NH,B,VHD", [(16, 520, 128), (20, 516, 80)])
+def test_mla_wide_products(ctx, oracle, NH, B, VHD):
+    """From 512 rows on (a prefill's) the W_UK and W_UV products take four
+    column tiles per wave: a partial last row tile, two head groups, and a
+    V head dimension of 80 (the second column block's tiles past it read a
+    clamped W_UV row and store nothing), ragged short contexts."""
+    lens = [1 + (37 * b) % 60 for b in range(B)]
+    run_case(ctx, oracle, NH, B, 60, 60, 655 + NH, kv_lens=lens, VHD=VHD)
+
+
 def test_mla_rows_in_groups(monkeypatch, oracle):
     """Chunk partials over the per-launch cap (MLAMOE_MLA_PART_MAX, here
     three rows' worth): the rows go in groups of 3, 3, 3 and 1, one after
