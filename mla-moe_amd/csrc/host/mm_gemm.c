@@ -50,6 +50,11 @@ size_t mm_gemm_bf16_ws_bytes(int T, int n_in, int d_out, unsigned flags) {
     return mm_gemm_bf16_ws2_bytes(T, n_in, d_out, 0, flags);
 }
 
+static int gemm_bf16_rows(mm_ctx *c, float *y, const uint16_t *xh, const uint16_t *xl,
+                          const uint16_t *w, int d_out, int n_in, int kp, int T, int split, int acc);
+static int cvt_rows(mm_ctx *c, const float *x, int n_in, int T, int split, char *ws,
+                    uint16_t **xh, uint16_t **xl, int *kp);
+
 int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1,
                      const uint16_t *w1, int d1, const float *x, int n_in, int T, unsigned flags,
                      char *ws) {
@@ -75,8 +80,12 @@ int mm_gemm_bf16_ws2(mm_ctx *c, float *y0, const uint16_t *w0, int d0, float *y1
         const size_t blocks = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
         return mm_launch(c, K_SKINNY_REDUCE, (unsigned)blocks, 1, 1, 256, 0, &r);
     }
-    if ((st = mm_gemm_bf16_ws(c, y0, x, w0, d0, n_in, T, flags, ws))) return st;
-    return d1 ? mm_gemm_bf16_ws(c, y1, x, w1, d1, n_in, T, flags, ws) : MM_OK;
+    /* x converted once for both weights */
+    uint16_t *xh, *xl;
+    int kp;
+    if ((st = cvt_rows(c, x, n_in, T, split, ws, &xh, &xl, &kp))) return st;
+    if ((st = gemm_bf16_rows(c, y0, xh, xl, w0, d0, n_in, kp, T, split, acc))) return st;
+    return d1 ? gemm_bf16_rows(c, y1, xh, xl, w1, d1, n_in, kp, T, split, acc) : MM_OK;
 }
 
 size_t mm_gemm_bf16_hl_ws_bytes(int T, int n_in, int d0, int d1) {
@@ -148,19 +157,9 @@ int mm_gemm_bf16_add_rmsnorm_hl(mm_ctx *c, float *x, const uint16_t *ahl, const 
     return mm_launch(c, K_REDUCE_RMSNORM, (unsigned)T, 1, 1, MM_RRN_THREADS, 0, &r);
 }
 
-int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
-                    int T, unsigned flags, char *ws) {
-    if (skinny_ok(T, n_in)) return mm_gemm_bf16_ws2(c, y, w, d_out, NULL, NULL, 0, x, n_in, T, flags, ws);
-    const int split = (flags & MM_MATMUL_X_BF16) == 0;
-    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
-    int st;
-    /* x as bf16 rows of a stride padded to 64 (zeros past n_in) */
-    const int kp = (n_in + 63) / 64 * 64;
-    const size_t xb = (size_t)T * kp * 2;
-    uint16_t *xh = (uint16_t *)ws, *xl = split ? (uint16_t *)(ws + al256(xb)) : NULL;
-    mm_cvt_bf16_args ca = {x, xh, xl, T, n_in, kp, split};
-    const size_t chunks = (size_t)T * kp / 8;
-    if ((st = mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca))) return st;
+/* y = x W^T on x already in bf16 rows of stride kp (xh, and xl with split) */
+static int gemm_bf16_rows(mm_ctx *c, float *y, const uint16_t *xh, const uint16_t *xl,
+                          const uint16_t *w, int d_out, int n_in, int kp, int T, int split, int acc) {
     /* block tile columns: the widest of 128, 64, 32 that still gives 192
      * tiles (most of the 256 CUs), else 32 -- the projections of this path
      * have too few 128 x 128 tiles to fill the machine (measured per width) */
@@ -180,6 +179,30 @@ int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int 
     const size_t stage = (size_t)(split ? 2 : 1) * 16384 + (size_t)bn * 128;
     const size_t lds = (split ? 3 : 4) * stage;
     return mm_launch(c, K_GEMM_BF16, (unsigned)(8 * ((nbx + 7) / 8) * nby), 1, 1, 256, lds, &a);
+}
+
+/* x as bf16 rows of a stride padded to 64 (zeros past n_in) into ws: hi,
+ * then (split) lo */
+static int cvt_rows(mm_ctx *c, const float *x, int n_in, int T, int split, char *ws,
+                    uint16_t **xh, uint16_t **xl, int *kp) {
+    *kp = (n_in + 63) / 64 * 64;
+    const size_t xb = (size_t)T * *kp * 2;
+    *xh = (uint16_t *)ws;
+    *xl = split ? (uint16_t *)(ws + al256(xb)) : NULL;
+    mm_cvt_bf16_args ca = {x, *xh, *xl, T, n_in, *kp, split};
+    const size_t chunks = (size_t)T * *kp / 8;
+    return mm_launch(c, K_CVT_BF16, (unsigned)((chunks + 255) / 256), 1, 1, 256, 0, &ca);
+}
+
+int mm_gemm_bf16_ws(mm_ctx *c, float *y, const float *x, const uint16_t *w, int d_out, int n_in,
+                    int T, unsigned flags, char *ws) {
+    if (skinny_ok(T, n_in)) return mm_gemm_bf16_ws2(c, y, w, d_out, NULL, NULL, 0, x, n_in, T, flags, ws);
+    const int split = (flags & MM_MATMUL_X_BF16) == 0;
+    const int acc = (flags & MM_MATMUL_ACCUMULATE) != 0;
+    uint16_t *xh, *xl;
+    int kp, st;
+    if ((st = cvt_rows(c, x, n_in, T, split, ws, &xh, &xl, &kp))) return st;
+    return gemm_bf16_rows(c, y, xh, xl, w, d_out, n_in, kp, T, split, acc);
 }
 
 unsigned mm_gemv_blocks(int rows) {

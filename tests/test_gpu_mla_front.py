@@ -78,9 +78,10 @@ def test_front_golden(oracle, name):
         ctx.close()
 
 
-CASES = [  # B, q_lora, interleaved, H  (B <= 4: fused GEMVs; more: MFMA GEMMs)
+CASES = [  # B, q_lora, interleaved, H  (B <= 4: fused GEMVs; more: MFMA GEMMs; above
+    #          64 rows the tiled GEMM, x converted to bf16 rows once for q and kv_a)
     (1, 0, 0, 2048), (3, 0, 1, 2048), (4, 96, 1, 512), (5, 0, 0, 2048), (9, 96, 0, 512),
-    (2, 0, 0, 4096),
+    (2, 0, 0, 4096), (70, 0, 0, 2048), (66, 96, 1, 512),
 ]
 
 
